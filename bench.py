@@ -1,0 +1,163 @@
+"""Benchmark of the north-star path: fused masked sample + log-probability at
+[S=1, B=256, T=1, V=128256] bf16 with a u8 grammar mask and temperature 0.7.
+
+One step = one launch of nt_hip_rl_sample over the 256 rows, inputs resident in HBM (the
+per-step uniforms are uploaded before the timed region). The timed region is K back-to-back
+launches bracketed by a stream synchronisation and HIP events recorded on the library's own
+stream. Prints one JSON line (the driver's contract) with a `roofline` object (algorithmic
+bytes per launch / average launch time against the 8 TB/s HBM peak) and a `cpu_baseline`
+object (the reference's Cpu(Reference) op sequence, restated in oracle/, timed on this host).
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "noetic-tensor_amd"))
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
+
+
+def hip_events():
+    """hipEvent* from the HIP runtime the library itself links."""
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+    hip.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+    hip.hipEventSynchronize.argtypes = [C.c_void_p]
+    hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+    hip.hipEventDestroy.argtypes = [C.c_void_p]
+    return hip
+
+
+def cpu_baseline(w, rows_sample, seed, min_seconds=10.0):
+    """The reference's CPU path on a bounded sample of the same rows: tempered_logits, the
+    max_dim check, one Gumbel draw per logit from the ChaCha stream, argmax, log_softmax and
+    gather, single-threaded in f32 (Cpu(Reference), oracle/oracle.c). Also the same unfused
+    sequence with the inverse-CDF draw split over every host core (a Cpu(Fast)-style port)."""
+    import workloads as W
+    from oracle import oracle as O
+    V = w["V"]
+    x = W.bf16_to_f32(W.download_rows(w["logits"], range(rows_sample), V))
+    keep = W.download_rows(w["mask"], range(rows_sample), V)
+    rng = O.Rng(seed, "c4/gumbel")
+    reps, t_ref = 0, 0.0
+    while reps < 1 or (t_ref < min_seconds and reps < 16):
+        t0 = time.perf_counter()
+        O.cpuref_sample_logp(x, w["temperature"], keep, rng)
+        t_ref += time.perf_counter() - t0
+        reps += 1
+    cores = os.cpu_count() or 1
+    u = O.Rng(seed, "c4/uniforms").uniforms(rows_sample)
+    t0 = time.perf_counter()
+    O.cpu_sample_logp_invcdf(x, w["temperature"], keep, u, threads=cores)
+    t_fast = time.perf_counter() - t0
+    return {
+        "value": reps * rows_sample / t_ref, "unit": "rows/s", "cores": 1, "kind": "port",
+        "sample": f"{reps} x {rows_sample} c4 rows (V=128256, bf16 values widened to f32): the reference's "
+                  f"Cpu(Reference) op sequence with Gumbel-max sampling, single thread, {t_ref:.2f} s",
+        "fast_port": {"value": rows_sample / t_fast, "unit": "rows/s", "cores": cores,
+                      "what": "unfused op sequence with the inverse-CDF draw, rows split over threads"},
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--seed", type=int, default=2024)
+    ap.add_argument("--cpu-rows", type=int, default=256, help="rows of the CPU baseline sample (0 = skip)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="repeat the CPU sample up to this long")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": f"--gpus {args.gpus}: this build measures one GPU; the path shards by rows "
+                                   "with no exchange (see DESIGN.md), and multi-GPU runs are not part of it"}))
+        sys.exit(2)
+
+    import noetic_rl as nr
+    import workloads as W
+
+    nr.claim(0)
+    w = W.c4(args.seed)
+    rows, V = w["rows"], w["V"]
+    n_launch = args.warmup + args.steps
+    U = nr.Tensor.from_numpy(nr.Rng(args.seed, "c4/uniforms").uniforms(rows * n_launch), "f64")
+    ids = nr.IntTensor((rows,))
+    logp = nr.Tensor((rows,), "f32")
+    status = nr.Tensor((rows,), "u8")
+    L = nr.lib()
+    argv = []
+    for i in range(n_launch):
+        a = nr.NtRlSampleArgs(w["logits"].ptr, nr.NT_BF16, nr.NT_MASK_U8, rows, V, V, w["mask"].ptr, V,
+                              w["temperature"], U.ptr + 8 * rows * i, ids.ptr, logp.ptr, None, status.ptr)
+        argv.append(a)
+    for i in range(args.warmup):
+        nr._check(L.nt_hip_rl_sample(C.byref(argv[i])), "sample")
+    nr.sync()
+
+    hip = hip_events()
+    stream = C.c_void_p()
+    nr._check(L.nt_hip_stream(C.byref(stream)), "stream")
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    hip.hipEventCreate(C.byref(e0))
+    hip.hipEventCreate(C.byref(e1))
+    nr.sync()
+    t0 = time.perf_counter()
+    hip.hipEventRecord(e0, stream)
+    for i in range(args.warmup, n_launch):
+        L.nt_hip_rl_sample(C.byref(argv[i]))
+    hip.hipEventRecord(e1, stream)
+    hip.hipEventSynchronize(e1)
+    nr.sync()
+    wall = time.perf_counter() - t0
+    ms = C.c_float()
+    hip.hipEventElapsedTime(C.byref(ms), e0, e1)
+    st = status.to_numpy()
+    if np.any(st != 0):
+        raise SystemExit(f"bench: {int(np.sum(st != 0))} rows refused")
+
+    ms_per_step = ms.value / args.steps
+    # Algorithmic bytes per launch: every input read once, every output written once.
+    per_row = 2 * V + V + 8 + 4 + 4 + 1  # bf16 logits, u8 mask, f64 uniform, i32 id, f32 logp, u8 status
+    bytes_launch = per_row * rows
+    gbs = bytes_launch / (ms_per_step * 1e-3) / 1e9
+    out = {
+        "metric": "rows/sec + achieved HBM GB/s, fused masked sample+logprob, V=128256 bf16",
+        "value": rows / (ms_per_step * 1e-3),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "c4 constrained decode: bf16 logits [1,256,1,128256] ~ N(0,2^2), u8 grammar mask "
+                               "[256,V] of contiguous runs (~30% kept), temperature 0.7, fused sample + logp",
+                   "rows": rows, "vocab": V, "parallelism": "none (1 GPU)"},
+        "achieved_gbs": gbs,
+        "wall_s_timed_region": wall,
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": gbs / HBM_PEAK_GBS, "traffic": None,
+                     "algorithmic_bytes_per_launch": bytes_launch},
+        "key": nr.key(),
+    }
+    tr = os.path.join(ROOT, "profiles", "c4_sample_traffic.json")
+    if os.path.exists(tr):
+        with open(tr) as f:
+            out["roofline"]["traffic"] = json.load(f).get("hbm_bytes_per_launch")
+    if args.cpu_rows > 0:
+        out["cpu_baseline"] = cpu_baseline(w, min(args.cpu_rows, rows), args.seed, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

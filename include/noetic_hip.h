@@ -1,0 +1,161 @@
+/*
+ * noetic_hip.h — the C ABI of libnoetic_hip.so, the MI355X (gfx950) backend of noetic-tensor's
+ * `nn::rl` vocabulary-row hot path.
+ *
+ * Conventions (all entry points):
+ *  - Plain pointers and sizes; no framework types cross the boundary.
+ *  - Return 0 on success, else an NT_E_* code or a hipError_t value (> 0); the text of the
+ *    last failure on this thread is nt_hip_last_error().
+ *  - Device pointers come from nt_hip_alloc (or any HIP allocation on the claimed device).
+ *    Every launch goes to the library's one stream (one process-wide non-blocking stream, as
+ *    the reference's CUDA backend keeps, src/tensor/cuda/backend.rs:205-206); results are
+ *    ready after nt_hip_sync() or a download.
+ *  - Every device entry point is serialised by one process-wide mutex (the reference's
+ *    `CTX: OnceLock<Mutex<Ctx>>`, src/tensor/cuda/backend.rs:104,148-159).
+ *  - Kernels use no atomics and reduce in a fixed order, so a rerun on the same inputs is
+ *    bit-identical (the reference's determinism contract, src/nn/tests/gpu/rl.rs:125-128).
+ *
+ * Rust binding: INTEGRATION.md gives the hand-written `extern "C"` block and the
+ * GpuBackend methods that call these.
+ */
+#ifndef NOETIC_HIP_H
+#define NOETIC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- error codes (the library's own; hipError_t values are passed through) ---------- */
+#define NT_OK 0
+#define NT_E_ARG (-1)         /* an invalid argument (shape, dtype, null pointer, ...) */
+#define NT_E_UNCLAIMED (-2)   /* no device claimed in this process */
+#define NT_E_CLAIMED (-3)     /* another device is already claimed by this process */
+#define NT_E_UNSUPPORTED (-4) /* a valid request this build does not implement */
+
+/* ---- dtypes and mask kinds ------------------------------------------------------------ */
+#define NT_F32 0  /* f32 logits */
+#define NT_BF16 1 /* bf16 logits, stored as their bit patterns (src/tensor/half.rs:10-12) */
+
+#define NT_MASK_NONE 0 /* no vocabulary mask */
+#define NT_MASK_U8 1   /* u8 keep-mask: 0 excludes the token (adds -inf), any other value keeps it */
+#define NT_MASK_F32 2  /* additive f32 mask (0, -inf, -1e9, any value), added after the divide
+                          by the temperature: rl.rs:475-486 `logits / temperature + mask` */
+
+/* ---- per-row status ------------------------------------------------------------------- */
+#define NT_ROW_OK 0
+#define NT_ROW_NO_TOKEN 1 /* every logit -inf after the mask: rl.rs:516-519 refuses the row */
+#define NT_ROW_NAN 2      /* a NaN reached the row's sum: rl.rs:516-519 refuses the row */
+#define NT_ROW_BAD_TOKEN 3 /* a scored token outside [0, V): the reference's gather panics
+                            (src/tensor/kernels.rs:224) */
+
+/* ===================================================================== runtime
+ * Replaces the device/context/memory slice of the reference's GpuBackend trait
+ * (src/tensor/gpu/mod.rs:137-207) for a new `Device::Hip(i)` (src/tensor/device.rs:23-27). */
+
+/* Claim HIP device `device` for this process (one device per process, as `claim` in
+ * src/tensor/cuda/backend.rs:115-138): sets it current and creates the library's stream.
+ * Claiming the claimed device again is a no-op. */
+int nt_hip_claim(int device);
+/* Number of visible HIP devices (0 without a GPU; never fails). */
+int nt_hip_device_count(void);
+/* The text of the last failure on the calling thread ("" if none). */
+const char *nt_hip_last_error(void);
+/* Provenance key, e.g. "hip-<gcnArchName>-rocm<ver>-kernels-<sha16>" (cf. `key`,
+ * src/tensor/cuda/backend.rs:962-966); written NUL-terminated into buf. */
+int nt_hip_key(char *buf, size_t cap);
+/* GpuBackend::alloc / upload / download / sync (src/tensor/gpu/mod.rs:139-140,181-184). */
+int nt_hip_alloc(size_t bytes, void **out);
+int nt_hip_free(void *ptr);
+int nt_hip_upload(void *dst, const void *src, size_t bytes);   /* host -> device, synchronous */
+int nt_hip_download(void *dst, const void *src, size_t bytes); /* device -> host, synchronous */
+int nt_hip_memset(void *dst, int value, size_t bytes);          /* device fill, on the stream */
+int nt_hip_sync(void);
+/* The library's stream as a hipStream_t (for callers that record events on it). */
+int nt_hip_stream(void **out);
+/* Launch counter (the reference's `launches()`, src/tensor/cuda/backend.rs:1034-1036). */
+uint64_t nt_hip_launches(void);
+
+/* ===================================================================== nn::rl fused rows
+ * Logits are row-major [rows, V] (rows = S*B*T of `[S, B, T, V]`, rl.rs:8-14) with row stride
+ * `ld` elements (ld >= V). A row is one (s, b, t) position. The float arithmetic is f32 with
+ * bf16 inputs converted exactly (float.rs:61-67); per-row scalars are combined in f64. */
+
+/* Fused masked categorical sample + log-probability (+ entropy) of each row: one pass over
+ * the logits and the mask. Replaces, for a Hip tensor, the op sequence of
+ *   ids  = sample_categorical(logits, temperature, mask, rng)      (rl.rs:510-529)
+ *   logp = token_log_probs(tempered_logits(logits, temperature, mask), ids)  (rl.rs:134-141)
+ *   ent  = categorical_entropy(tempered_logits(...), None, TokenReduction::None) (rl.rs:405-414)
+ * with the inverse-CDF draw of one uniform per row in place of Gumbel-max: with z the
+ * tempered logits, m = max z, w_v = exp(z_v - m) and S = sum w, the token is
+ * min{v : sum_{j<=v} w_j > u*S} (excluded tokens have w = 0 and are never drawn; if rounding
+ * leaves no crossing, the last token with w > 0). temperature 0 is greedy: the first argmax
+ * of the masked logits (rl.rs:510-513), no uniform read; logp/entropy are then those of the
+ * temperature-1 distribution (rl.rs:514). */
+typedef struct NtRlSampleArgs {
+    const void *logits;       /* [rows, ld] f32 or bf16 */
+    int32_t dtype;            /* NT_F32 | NT_BF16 */
+    int32_t mask_kind;        /* NT_MASK_* */
+    int64_t rows, vocab, ld;
+    const void *mask;         /* u8 or f32 [rows or 1, mask_ld]; NULL with NT_MASK_NONE */
+    int64_t mask_ld;          /* mask row stride; 0 = one row shared by every logits row */
+    double temperature;       /* >= 0 and finite; 0 = greedy */
+    const double *uniforms;   /* [rows] device, each in (0,1); unused when greedy */
+    int32_t *ids;             /* [rows] out: the sampled token (-1 on a refused row) */
+    float *logp;              /* [rows] out or NULL */
+    float *entropy;           /* [rows] out or NULL */
+    uint8_t *status;          /* [rows] out: NT_ROW_* (required) */
+} NtRlSampleArgs;
+int nt_hip_rl_sample(const NtRlSampleArgs *a);
+
+/* Fused row scoring: for each row, any of
+ *   logp[r]     = token_log_probs(z, tokens)[r]                 (rl.rs:134-141)
+ *   ref_logp[r] = token_log_probs(zr, tokens)[r]                (rl.rs:134-141, reference)
+ *   kl[r]       = categorical_kl(z, zr) per position (exact)    (rl.rs:327-338)
+ *   entropy[r]  = categorical_entropy(z) per position           (rl.rs:405-414)
+ * with z = tempered_logits(logits, T, mask) and zr = tempered_logits(ref_logits, T, mask)
+ * (`reference_kl`, rl.rs:347-351; T = 1 and no mask give `categorical_kl`). One pass reads
+ * each logit (and the mask) once. A token excluded by the mask gives logp -inf, as the
+ * reference does (rl.rs:136-137). */
+typedef struct NtRlScoreArgs {
+    const void *logits;       /* [rows, ld] policy logits */
+    const void *ref_logits;   /* [rows, ld] reference logits or NULL (no ref_logp / kl) */
+    int32_t dtype;            /* NT_F32 | NT_BF16 (both inputs) */
+    int32_t mask_kind;
+    int64_t rows, vocab, ld;
+    const void *mask;
+    int64_t mask_ld;
+    double temperature;       /* > 0 and finite */
+    const int32_t *tokens;    /* [rows] device, each in [0, V); NULL when no logp is asked */
+    float *logp;              /* [rows] out or NULL */
+    float *ref_logp;          /* [rows] out or NULL */
+    float *kl;                /* [rows] out or NULL */
+    float *entropy;           /* [rows] out or NULL */
+    uint8_t *status;          /* [rows] out or NULL: NT_ROW_* of the policy row */
+} NtRlScoreArgs;
+int nt_hip_rl_score(const NtRlScoreArgs *a);
+
+/* kl_estimate per sampled token (rl.rs:380-400), elementwise over n = S*B*T values:
+ * delta = ref_logp - logp, zeroed where mask == 0 (a select, rl.rs:100-102), clamped to
+ * [-clamp, clamp] when clamp > 0; estimator 1: -delta, 2: delta^2/2, 3: exp(delta)-delta-1;
+ * the result is zero at masked positions. mask (f32 0/1) may be NULL. */
+int nt_hip_rl_kl_estimate(const float *logp, const float *ref_logp, const float *mask, int64_t n,
+                          int32_t estimator, double clamp, float *out);
+
+/* zero_masked (rl.rs:100-102): out = mask != 0 ? x : 0, a select (a non-finite value at a
+ * masked position does not leak). */
+int nt_hip_rl_zero_masked(const float *x, const float *mask, int64_t n, float *out);
+
+/* reduce_tokens (rl.rs:69-92) of per-token values [S,B,T] that are already zero at masked
+ * positions, mask f32 [S,B,T] (NULL = every position scored): reduction 1 Sum [S],
+ * 2 TokenMean [S], 3 PerSequence [S,B], 4 SequenceMean [S]. Each output is summed in a fixed
+ * order by one thread. */
+int nt_hip_rl_reduce_tokens(const float *per, const float *mask, int64_t S, int64_t B, int64_t T,
+                            int32_t reduction, float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

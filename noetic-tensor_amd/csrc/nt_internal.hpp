@@ -1,0 +1,33 @@
+// Internal declarations shared by the translation units of libnoetic_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <mutex>
+#include <string>
+
+namespace nt {
+
+// The process-wide device context: one claimed device, one non-blocking stream at the default
+// priority, one mutex serialising every device entry point, a launch counter.
+struct Ctx {
+    int device = -1;
+    hipStream_t stream = nullptr;
+    std::mutex mu;
+    uint64_t launches = 0;
+};
+
+Ctx &ctx();
+
+// Record the failure text for nt_hip_last_error() and return `code`.
+int fail(int code, const std::string &msg);
+// hipSuccess -> 0, else fail(err, "<what>: <name> (<code>): <desc>").
+int hip_check(hipError_t err, const char *what);
+// Check a kernel launch just issued on the library stream and count it.
+int launched(const char *what);
+
+// Lock the context and require a claimed device; on success `*out` holds the lock.
+int enter(std::unique_lock<std::mutex> *out);
+
+}  // namespace nt

@@ -1,0 +1,935 @@
+// Fused nn::rl vocabulary-row kernels for gfx950 (MI355X), and their C-ABI entry points.
+//
+// A row is one (s, b, t) position of logits [S, B, T, V] (src/nn/rl.rs:8-14). The reference
+// runs every nn::rl function as a chain of generic tensor kernels (log_softmax = max_dim x2,
+// sub, exp, sum_dim, log, sub; src/tensor/activation.rs:30-42), materialising [rows, V] about
+// ten times per call. Here one workgroup streams one row once:
+//
+//  * Data layout: a row is cut into chunks of 512 elements (one wavefront x 8 elements per
+//    lane, 16-byte loads for bf16, 2 x 16-byte loads for f32, 8-byte loads of the u8 mask).
+//    Chunk c of a row is processed by wave c % nwaves, so every wave-wide load is a contiguous
+//    1 KiB (bf16) / 2 KiB (f32) read and each wave keeps several chunks in flight.
+//  * Arithmetic: f32 per element; bf16 is widened exactly by a shift. Exponentials are
+//    exp2 of (v - shift) * c on the hardware v_exp_f32, where c = log2(e) / temperature folds
+//    the temperature divide into the exponent (no per-element divide).
+//  * Determinism: no atomics; every reduction (per lane, across a wave, across waves) has a
+//    fixed order independent of timing, so reruns are bit-identical (the contract of
+//    src/nn/tests/gpu/rl.rs:125-128).
+//
+// Sampler (nt_hip_rl_sample): each chunk's (max, sum of exp) goes to LDS; wave 0 then merges
+// the chunk sums in index order in f64, finds the chunk holding u*S, re-reads only that chunk
+// (512 elements, an L2 hit in practice) and scans it in f64. HBM traffic is one pass over the
+// row plus one chunk.
+//
+// Scorer (nt_hip_rl_score): every lane keeps running (max, sum exp, sum exp*d, sum exp*(z-r))
+// for the policy and (max, sum exp) for the reference, rescaled when its max grows (online
+// log-sum-exp); waves and then the workgroup merge them in a fixed order; per-row scalars are
+// finished in f64.
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/noetic_hip.h"
+#include "nt_internal.hpp"
+
+namespace nt {
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kEpl = 8;                  // elements per lane per chunk
+constexpr int kChunk = kWave * kEpl;     // 512 elements per chunk
+constexpr int kBatch = 4;                // chunks per wave with loads in flight together
+constexpr float kLog2e = 1.44269504088896340736f;
+constexpr double kLn2 = 0.69314718055994530942;
+constexpr int kRowBadToken = NT_ROW_BAD_TOKEN;
+
+// ------------------------------------------------------------------ element access
+
+template <int DT>
+struct Elem;
+template <>
+struct Elem<NT_F32> {
+    static constexpr int kWords = 8;     // 8 f32 per lane per chunk
+    static constexpr uint32_t kNegInf = 0xff800000u;
+    static constexpr int kBytes = 4;
+};
+template <>
+struct Elem<NT_BF16> {
+    static constexpr int kWords = 4;     // 8 bf16 packed two per word
+    static constexpr uint32_t kNegInf = 0xff80ff80u;
+    static constexpr int kBytes = 2;
+};
+
+template <int MK>
+struct MaskWords {
+    static constexpr int kWords = MK == NT_MASK_U8 ? 2 : (MK == NT_MASK_F32 ? 8 : 0);
+    static constexpr int kBytes = MK == NT_MASK_U8 ? 1 : (MK == NT_MASK_F32 ? 4 : 0);
+};
+
+// The raw bits of one lane's 8 elements of one chunk (logits and mask).
+template <int DT, int MK>
+struct Raw {
+    uint32_t x[Elem<DT>::kWords];
+    uint32_t m[MaskWords<MK>::kWords > 0 ? MaskWords<MK>::kWords : 1];
+};
+
+// Load the 8 elements at e0 of a row. AL: the row and mask are 16-/8-byte aligned and V % 8
+// == 0, so a lane's 8 elements are all inside the row or all outside it. Elements outside
+// the row read as -inf logits.
+template <int DT, int MK, bool AL>
+__device__ __forceinline__ void load_raw(Raw<DT, MK> &r, const void *xrow, const void *mrow, int64_t e0,
+                                         int64_t V) {
+    if constexpr (MK == NT_MASK_NONE) r.m[0] = 0;
+    if constexpr (AL) {
+        if (e0 < V) {
+            if constexpr (DT == NT_F32) {
+                const uint4 *q = reinterpret_cast<const uint4 *>(static_cast<const float *>(xrow) + e0);
+                uint4 a = q[0], b = q[1];
+                r.x[0] = a.x; r.x[1] = a.y; r.x[2] = a.z; r.x[3] = a.w;
+                r.x[4] = b.x; r.x[5] = b.y; r.x[6] = b.z; r.x[7] = b.w;
+            } else {
+                uint4 a = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(xrow) + e0);
+                r.x[0] = a.x; r.x[1] = a.y; r.x[2] = a.z; r.x[3] = a.w;
+            }
+            if constexpr (MK == NT_MASK_U8) {
+                uint2 k = *reinterpret_cast<const uint2 *>(static_cast<const uint8_t *>(mrow) + e0);
+                r.m[0] = k.x; r.m[1] = k.y;
+            } else if constexpr (MK == NT_MASK_F32) {
+                const uint4 *q = reinterpret_cast<const uint4 *>(static_cast<const float *>(mrow) + e0);
+                uint4 a = q[0], b = q[1];
+                r.m[0] = a.x; r.m[1] = a.y; r.m[2] = a.z; r.m[3] = a.w;
+                r.m[4] = b.x; r.m[5] = b.y; r.m[6] = b.z; r.m[7] = b.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < Elem<DT>::kWords; i++) r.x[i] = Elem<DT>::kNegInf;
+#pragma unroll
+            for (int i = 0; i < (MaskWords<MK>::kWords > 0 ? MaskWords<MK>::kWords : 1); i++) r.m[i] = 0;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < kEpl; j++) {
+            const int64_t e = e0 + j;
+            const bool in = e < V;
+            if constexpr (DT == NT_F32) {
+                r.x[j] = in ? __float_as_uint(static_cast<const float *>(xrow)[e]) : Elem<DT>::kNegInf;
+            } else {
+                uint32_t h = in ? uint32_t(static_cast<const uint16_t *>(xrow)[e]) : 0xff80u;
+                if (j % 2 == 0) r.x[j / 2] = h;
+                else r.x[j / 2] |= h << 16;
+            }
+            if constexpr (MK == NT_MASK_U8) {
+                uint32_t k = in ? uint32_t(static_cast<const uint8_t *>(mrow)[e]) : 0u;
+                if (j % 4 == 0) r.m[j / 4] = k;
+                else r.m[j / 4] |= k << (8 * (j % 4));
+            } else if constexpr (MK == NT_MASK_F32) {
+                r.m[j] = in ? __float_as_uint(static_cast<const float *>(mrow)[e]) : 0u;
+            }
+        }
+    }
+}
+
+// Logit j of a lane's chunk as f32 (bf16 widened exactly).
+template <int DT>
+__device__ __forceinline__ float logit(const uint32_t *x, int j) {
+    if constexpr (DT == NT_F32) return __uint_as_float(x[j]);
+    else return __uint_as_float((j % 2 == 0) ? (x[j / 2] << 16) : (x[j / 2] & 0xffff0000u));
+}
+
+// The "value" of an element, the quantity the kernels take maxima and exponentials of.
+//  - no mask / u8 mask: v = x (an excluded token -> -inf); the temperature is applied through
+//    the exponent scale c = log2(e)/T, and m_z = max(x)/T is exact because correctly rounded
+//    division by T > 0 is monotonic.
+//  - additive f32 mask: v = z = x / T + mask exactly as tempered_logits computes it
+//    (rl.rs:477-484, float.rs:494-499); c = log2(e).
+template <int DT, int MK>
+__device__ __forceinline__ void decode_words(const uint32_t *xw, const uint32_t *mw, float v[kEpl], float tau,
+                                             bool tau_one) {
+#pragma unroll
+    for (int j = 0; j < kEpl; j++) {
+        float x = logit<DT>(xw, j);
+        if constexpr (MK == NT_MASK_U8) {
+            const uint32_t keep = (mw[j / 4] >> (8 * (j % 4))) & 0xffu;
+            v[j] = keep ? x : -INFINITY;
+        } else if constexpr (MK == NT_MASK_F32) {
+            const float z = tau_one ? x : x / tau;
+            v[j] = z + __uint_as_float(mw[j]);
+        } else {
+            v[j] = x;
+        }
+    }
+}
+
+template <int DT, int MK>
+__device__ __forceinline__ void decode(const Raw<DT, MK> &r, float v[kEpl], float tau, bool tau_one) {
+    decode_words<DT, MK>(r.x, r.m, v, tau, tau_one);
+}
+
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float max8(const float v[kEpl]) {
+    return fmaxf(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])), fmaxf(fmaxf(v[4], v[5]), fmaxf(v[6], v[7])));
+}
+
+__device__ __forceinline__ float tree8(const float w[kEpl]) {
+    return ((w[0] + w[1]) + (w[2] + w[3])) + ((w[4] + w[5]) + (w[6] + w[7]));
+}
+
+// Butterfly reductions over the 64 lanes: every lane ends with the same bits (the operations
+// are commutative), the order is fixed.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+// Inclusive prefix sum over lanes (Hillis-Steele, fixed order).
+__device__ __forceinline__ double wave_scan_d(double v, int lane) {
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        double n = __shfl_up(v, o, kWave);
+        if (lane >= o) v += n;
+    }
+    return v;
+}
+__device__ __forceinline__ int first_lane(uint64_t ballot) { return ballot ? __builtin_ctzll(ballot) : -1; }
+__device__ __forceinline__ int last_lane(uint64_t ballot) { return ballot ? 63 - __builtin_clzll(ballot) : -1; }
+
+// ------------------------------------------------------------------ sampler
+
+struct SampleP {
+    const void *logits;
+    const void *mask;
+    int64_t V, ld, mask_ld;
+    float c;          // exponent scale: log2(e)/T (no/u8 mask) or log2(e) (f32 mask)
+    float tau;        // (float)T, the reference's divisor (float.rs:494-499)
+    int tau_one;      // T == 1 (or greedy): no divide
+    int greedy;
+    int nc;           // chunks per row
+    const double *u;
+    int32_t *ids;
+    float *logp;
+    float *ent;
+    uint8_t *status;
+};
+
+template <int DT, int MK, bool ENT, bool AL>
+__global__ __launch_bounds__(1024) void k_sample(SampleP p) {
+    extern __shared__ float smem[];
+    float *cmax = smem;                 // [nc] chunk max (value space)
+    float *csum = smem + p.nc;          // [nc] chunk sum of exp2((v - cmax) c)
+    float *cent = smem + 2 * p.nc;      // [nc] chunk sum of w * (v - cmax) c   (ENT only)
+    const int64_t row = blockIdx.x;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int nw = blockDim.x / kWave;
+    const bool tau_one = p.tau_one != 0;
+    const void *xrow = static_cast<const char *>(p.logits) + row * p.ld * Elem<DT>::kBytes;
+    const void *mrow = nullptr;
+    if constexpr (MK != NT_MASK_NONE) mrow = static_cast<const char *>(p.mask) + row * p.mask_ld * MaskWords<MK>::kBytes;
+
+    // ---- phase 1: stream the row once, per-chunk (max, sum exp[, sum exp * d]) into LDS.
+    for (int c0 = wave; c0 < p.nc; c0 += nw * kBatch) {
+        Raw<DT, MK> raw[kBatch];
+#pragma unroll
+        for (int b = 0; b < kBatch; b++) {
+            const int c = c0 + b * nw;
+            const int64_t e0 = int64_t(c < p.nc ? c : 0) * kChunk + lane * kEpl;
+            load_raw<DT, MK, AL>(raw[b], xrow, mrow, c < p.nc ? e0 : p.V, p.V);
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; b++) {
+            const int c = c0 + b * nw;
+            if (c < p.nc) {
+            float v[kEpl];
+            decode<DT, MK>(raw[b], v, p.tau, tau_one);
+            const float cm = wave_max(max8(v));
+            const float sh = (cm == -INFINITY) ? 0.0f : cm;
+            float w[kEpl], h[kEpl];
+#pragma unroll
+            for (int j = 0; j < kEpl; j++) {
+                const float d = (v[j] - sh) * p.c;
+                w[j] = exp2_hw(d);
+                if constexpr (ENT) h[j] = w[j] * fmaxf(d, -FLT_MAX);
+            }
+            const float cs = wave_sum(tree8(w));
+            float ce = 0.0f;
+            if constexpr (ENT) ce = wave_sum(tree8(h));
+            if (lane == 0) {
+                cmax[c] = cm;
+                csum[c] = cs;
+                if constexpr (ENT) cent[c] = ce;
+            }
+            }
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+
+    // ---- phase 2 (wave 0): merge the chunks in index order, in f64.
+    const int nc = p.nc;
+    const int q = (nc + kWave - 1) / kWave;
+    const int cb = min(lane * q, nc), ce_ = min(cb + q, nc);
+    float lm = -INFINITY;
+    for (int c = cb; c < ce_; c++) lm = fmaxf(lm, cmax[c]);
+    const float a = wave_max(lm);
+    auto refuse = [&](uint8_t st) {
+        if (lane == 0) {
+            p.ids[row] = -1;
+            if (p.logp) p.logp[row] = NAN;
+            if (p.ent) p.ent[row] = NAN;
+            p.status[row] = st;
+        }
+    };
+    if (a == -INFINITY) {
+        refuse(NT_ROW_NO_TOKEN);
+        return;
+    }
+    double lsum = 0.0, lh = 0.0;
+    for (int c = cb; c < ce_; c++) {
+        const float f = exp2_hw((cmax[c] - a) * p.c);
+        lsum += double(f) * double(csum[c]);
+        if constexpr (ENT) {
+            if (csum[c] > 0.0f) lh += double(f) * (double(cent[c]) + double((cmax[c] - a) * p.c) * double(csum[c]));
+        }
+    }
+    const double incl = wave_scan_d(lsum, lane);
+    const double S = __shfl(incl, kWave - 1, kWave);
+    double H2 = 0.0;
+    if constexpr (ENT) H2 = wave_sum_d(lh);
+    if (!(S == S)) {
+        refuse(NT_ROW_NAN);
+        return;
+    }
+    int cstar = -1;
+    double tloc = 0.0;  // target inside chunk cstar, in the chunk's own scale
+    if (p.greedy) {
+        int mine = -1;
+        for (int c = cb; c < ce_; c++)
+            if (cmax[c] == a) { mine = c; break; }
+        const int l = first_lane(__ballot(mine >= 0));
+        cstar = l >= 0 ? __shfl(mine, l, kWave) : -1;
+    } else {
+        const double t = p.u[row] * S;
+        const double excl = (lane == 0) ? 0.0 : __shfl_up(incl, 1, kWave);
+        // Only a lane that holds weight can contain the crossing (a zero-weight lane's
+        // inclusive sum may round above its neighbour's in the scan tree).
+        int l = first_lane(__ballot(incl > t && lsum > 0.0));
+        int mine = -1;
+        double mt = INFINITY;
+        if (l >= 0) {
+            if (lane == l) {
+                double C = excl;
+                int lastpos = -1;
+                for (int c = cb; c < ce_; c++) {
+                    const float f = exp2_hw((cmax[c] - a) * p.c);
+                    const double wt = double(f) * double(csum[c]);
+                    if (wt > 0.0) lastpos = c;
+                    if (C + wt > t) {
+                        mine = c;
+                        mt = (t - C) / double(f);
+                        break;
+                    }
+                    C += wt;
+                }
+                if (mine < 0) mine = lastpos;  // rounding: no crossing inside the lane
+            }
+        } else {
+            // u*S rounded up to S: the last chunk with weight.
+            int lastpos = -1;
+            for (int c = cb; c < ce_; c++)
+                if (csum[c] > 0.0f && cmax[c] != -INFINITY) lastpos = c;
+            l = last_lane(__ballot(lastpos >= 0));
+            if (lane == l) mine = lastpos;
+        }
+        cstar = l >= 0 ? __shfl(mine, l, kWave) : -1;
+        tloc = l >= 0 ? __shfl(mt, l, kWave) : INFINITY;
+    }
+    if (cstar < 0 || cstar >= nc) {
+        // Unreachable with S > 0 (some chunk holds weight); kept so that no path re-reads
+        // outside the row: take the first chunk holding the maximum.
+        int mine = -1;
+        for (int c = cb; c < ce_; c++)
+            if (cmax[c] == a) { mine = c; break; }
+        const int l = first_lane(__ballot(mine >= 0));
+        cstar = l >= 0 ? __shfl(mine, l, kWave) : 0;
+        tloc = INFINITY;
+    }
+
+    // ---- phase 3 (wave 0): re-read chunk cstar, find the token inside it.
+    Raw<DT, MK> raw;
+    const int64_t e0 = int64_t(cstar) * kChunk + lane * kEpl;
+    load_raw<DT, MK, AL>(raw, xrow, mrow, e0, p.V);
+    float v[kEpl];
+    decode<DT, MK>(raw, v, p.tau, tau_one);
+    int jsel = -1, lsel = -1;
+    if (p.greedy) {
+        int mine = -1;
+#pragma unroll
+        for (int j = kEpl - 1; j >= 0; j--)
+            if (v[j] == a) mine = j;
+        lsel = first_lane(__ballot(mine >= 0));
+        jsel = lsel >= 0 ? __shfl(mine, lsel, kWave) : -1;
+    } else {
+        const float cm = cmax[cstar];
+        const float sh = (cm == -INFINITY) ? 0.0f : cm;
+        float w[kEpl];
+        double ls = 0.0;
+#pragma unroll
+        for (int j = 0; j < kEpl; j++) {
+            w[j] = exp2_hw((v[j] - sh) * p.c);
+            ls += double(w[j]);
+        }
+        const double incl2 = wave_scan_d(ls, lane);
+        const double excl2 = (lane == 0) ? 0.0 : __shfl_up(incl2, 1, kWave);
+        int mine = -1;
+        int lastj = -1;
+#pragma unroll
+        for (int j = 0; j < kEpl; j++)
+            if (w[j] > 0.0f) lastj = j;
+        lsel = first_lane(__ballot(incl2 > tloc && ls > 0.0));
+        if (lsel >= 0) {
+            if (lane == lsel) {
+                double C = excl2;
+                for (int j = 0; j < kEpl; j++) {
+                    C += double(w[j]);
+                    if (C > tloc) { mine = j; break; }
+                }
+                if (mine < 0) mine = lastj;
+            }
+        } else {
+            lsel = last_lane(__ballot(lastj >= 0));
+            if (lane == lsel) mine = lastj;
+        }
+        jsel = lsel >= 0 ? __shfl(mine, lsel, kWave) : -1;
+    }
+    if (lsel < 0 || jsel < 0) {
+        // Unreachable (chunk cstar holds weight, or the maximum when greedy); the first
+        // element equal to the chunk's maximum keeps the result a valid token.
+        int mine = -1;
+#pragma unroll
+        for (int j = kEpl - 1; j >= 0; j--)
+            if (v[j] == cmax[cstar]) mine = j;
+        lsel = first_lane(__ballot(mine >= 0));
+        jsel = lsel >= 0 ? __shfl(mine, lsel, kWave) : 0;
+        if (lsel < 0) lsel = 0;
+    }
+    if (lane == lsel) {
+        // jsel indexes this lane's registers: select it without a dynamic register index.
+        float vz = v[0];
+#pragma unroll
+        for (int j = 1; j < kEpl; j++)
+            if (j == jsel) vz = v[j];
+        const int64_t id = int64_t(cstar) * kChunk + lane * kEpl + jsel;
+        // logp = (z_id - m) - ln S, with z_id - m the reference's f32 subtraction
+        // (activation.rs:32-35).
+        float zid = vz, mz = a;
+        if constexpr (MK != NT_MASK_F32) {
+            if (!tau_one) {
+                zid = vz / p.tau;
+                mz = a / p.tau;
+            }
+        }
+        const double lnS = log(S);
+        p.ids[row] = int32_t(id);
+        if (p.logp) p.logp[row] = float(double(zid - mz) - lnS);
+        if (p.ent) p.ent[row] = float(lnS - kLn2 * H2 / S);
+        p.status[row] = NT_ROW_OK;
+    }
+}
+
+// ------------------------------------------------------------------ scorer
+
+struct ScoreP {
+    const void *logits;
+    const void *ref;
+    const void *mask;
+    int64_t V, ld, mask_ld;
+    float c;
+    float tau;
+    int tau_one;
+    int nc;
+    const int32_t *tokens;
+    float *logp, *ref_logp, *kl, *ent;
+    uint8_t *status;
+};
+
+// Running log-sum-exp state of one lane (value space, exponent scale c).
+struct Lse {
+    float a;  // max so far
+    float S;  // sum exp2((v - a) c)
+    float H;  // sum w (v - a) c            (entropy)
+    float B;  // sum w (v - v_ref)          (exact KL)
+};
+
+__device__ __forceinline__ void lse_rescale(Lse &s, float an, float c, bool ent, bool kl) {
+    const float sh = (an == -INFINITY) ? 0.0f : an;
+    const float dd = (s.a - sh) * c;
+    const float f = exp2_hw(dd);
+    if (ent) s.H = f * (s.H + fmaxf(dd, -FLT_MAX) * s.S);
+    s.S = f * s.S;
+    if (kl) s.B = f * s.B;
+    s.a = an;
+}
+
+// Merge state o into s (the same arithmetic whichever side is s).
+__device__ __forceinline__ void lse_merge(Lse &s, const Lse &o, float c, bool ent, bool kl) {
+    const float an = fmaxf(s.a, o.a);
+    const float sh = (an == -INFINITY) ? 0.0f : an;
+    const float d1 = (s.a - sh) * c, d2 = (o.a - sh) * c;
+    const float f1 = exp2_hw(d1), f2 = exp2_hw(d2);
+    if (ent) s.H = f1 * (s.H + fmaxf(d1, -FLT_MAX) * s.S) + f2 * (o.H + fmaxf(d2, -FLT_MAX) * o.S);
+    s.S = f1 * s.S + f2 * o.S;
+    if (kl) s.B = f1 * s.B + f2 * o.B;
+    s.a = an;
+}
+
+__device__ __forceinline__ Lse shfl_down_lse(const Lse &s, int o) {
+    Lse r;
+    r.a = __shfl_down(s.a, o, kWave);
+    r.S = __shfl_down(s.S, o, kWave);
+    r.H = __shfl_down(s.H, o, kWave);
+    r.B = __shfl_down(s.B, o, kWave);
+    return r;
+}
+
+constexpr int kScoreThreads = 256;
+constexpr int kScoreWaves = kScoreThreads / kWave;
+
+template <int DT, int MK, bool REF, bool KL, bool ENT, bool AL>
+__global__ __launch_bounds__(kScoreThreads) void k_score(ScoreP p) {
+    __shared__ Lse wp[kScoreWaves], wr[kScoreWaves];
+    const int64_t row = blockIdx.x;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int nw = blockDim.x / kWave;
+    const bool tau_one = p.tau_one != 0;
+    const void *xrow = static_cast<const char *>(p.logits) + row * p.ld * Elem<DT>::kBytes;
+    const void *yrow = nullptr;
+    if constexpr (REF) yrow = static_cast<const char *>(p.ref) + row * p.ld * Elem<DT>::kBytes;
+    const void *mrow = nullptr;
+    if constexpr (MK != NT_MASK_NONE) mrow = static_cast<const char *>(p.mask) + row * p.mask_ld * MaskWords<MK>::kBytes;
+
+    Lse sp{-INFINITY, 0.0f, 0.0f, 0.0f}, sr{-INFINITY, 0.0f, 0.0f, 0.0f};
+    for (int c0 = wave; c0 < p.nc; c0 += nw * kBatch) {
+        Raw<DT, MK> rx[kBatch];
+        Raw<DT, NT_MASK_NONE> ry[REF ? kBatch : 1];
+#pragma unroll
+        for (int b = 0; b < kBatch; b++) {
+            const int c = c0 + b * nw;
+            const int64_t e0 = c < p.nc ? int64_t(c) * kChunk + lane * kEpl : p.V;
+            load_raw<DT, MK, AL>(rx[b], xrow, mrow, e0, p.V);
+            if constexpr (REF) load_raw<DT, NT_MASK_NONE, AL>(ry[b], yrow, nullptr, e0, p.V);
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; b++) {
+            const int c = c0 + b * nw;
+            if (c < p.nc) {
+            float v[kEpl];
+            decode<DT, MK>(rx[b], v, p.tau, tau_one);
+            float vr[kEpl];
+            if constexpr (REF) {
+                // The reference logits take the same temperature and vocabulary mask
+                // (reference_kl, rl.rs:347-351).
+                decode_words<DT, MK>(ry[b].x, rx[b].m, vr, p.tau, tau_one);
+            }
+            lse_rescale(sp, fmaxf(sp.a, max8(v)), p.c, ENT, KL);
+            {
+                const float sh = (sp.a == -INFINITY) ? 0.0f : sp.a;
+                float w[kEpl], h[kEpl], bb[kEpl];
+#pragma unroll
+                for (int j = 0; j < kEpl; j++) {
+                    const float d = (v[j] - sh) * p.c;
+                    w[j] = exp2_hw(d);
+                    if constexpr (ENT) h[j] = w[j] * fmaxf(d, -FLT_MAX);
+                    if constexpr (KL) bb[j] = w[j] * fmaxf(v[j] - vr[j], -FLT_MAX);
+                }
+                sp.S += tree8(w);
+                if constexpr (ENT) sp.H += tree8(h);
+                if constexpr (KL) sp.B += tree8(bb);
+            }
+            if constexpr (REF) {
+                lse_rescale(sr, fmaxf(sr.a, max8(vr)), p.c, false, false);
+                const float sh = (sr.a == -INFINITY) ? 0.0f : sr.a;
+                float w[kEpl];
+#pragma unroll
+                for (int j = 0; j < kEpl; j++) w[j] = exp2_hw((vr[j] - sh) * p.c);
+                sr.S += tree8(w);
+            }
+            }
+        }
+    }
+    // Wave tree (lane i takes lane i + o), then the waves in order.
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) {
+        const Lse t = shfl_down_lse(sp, o);
+        if (lane < o) lse_merge(sp, t, p.c, ENT, KL);
+        if constexpr (REF) {
+            const Lse u = shfl_down_lse(sr, o);
+            if (lane < o) lse_merge(sr, u, p.c, false, false);
+        }
+    }
+    if (lane == 0) {
+        wp[wave] = sp;
+        if constexpr (REF) wr[wave] = sr;
+    }
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+
+    // Finish the row in f64.
+    auto finish = [&](const Lse *w, double &a_out, double &S_out, double &H_out, double &B_out) {
+        float a = -INFINITY;
+        for (int i = 0; i < nw; i++) a = fmaxf(a, w[i].a);
+        double S = 0.0, H = 0.0, B = 0.0;
+        for (int i = 0; i < nw; i++) {
+            if (w[i].a == -INFINITY) continue;
+            const double d = double(w[i].a - a) * double(p.c);
+            const double f = exp2(d);
+            S += f * double(w[i].S);
+            if (ENT) H += f * (double(w[i].H) + d * double(w[i].S));
+            if (KL) B += f * double(w[i].B);
+        }
+        a_out = a;
+        S_out = S;
+        H_out = H;
+        B_out = B;
+    };
+    double ap, Sp, Hp, Bp;
+    finish(wp, ap, Sp, Hp, Bp);
+    const float apf = float(ap);
+    int st = NT_ROW_OK;
+    if (apf == -INFINITY) st = NT_ROW_NO_TOKEN;
+    else if (!(Sp == Sp)) st = NT_ROW_NAN;
+    const double lnSp = log(Sp);
+    // The value-space max as the reference's f32 max of the tempered logits.
+    auto zmax = [&](float a) -> float {
+        if constexpr (MK != NT_MASK_F32) return tau_one ? a : a / p.tau;
+        else return a;
+    };
+    // The tempered logit of one token, with the reference's f32 arithmetic.
+    auto ztok = [&](const void *row, int64_t tok) -> float {
+        float x;
+        if constexpr (DT == NT_F32) x = static_cast<const float *>(row)[tok];
+        else x = __uint_as_float(uint32_t(static_cast<const uint16_t *>(row)[tok]) << 16);
+        float z = tau_one ? x : x / p.tau;
+        if constexpr (MK == NT_MASK_U8) {
+            if (static_cast<const uint8_t *>(mrow)[tok] == 0) z = -INFINITY;
+        } else if constexpr (MK == NT_MASK_F32) {
+            z = z + static_cast<const float *>(mrow)[tok];
+        }
+        return z;
+    };
+    int64_t tok = -1;
+    if (p.tokens) {
+        tok = p.tokens[row];
+        if ((tok < 0 || tok >= p.V) && st == NT_ROW_OK) st = kRowBadToken;
+    }
+    if (p.logp) {
+        float lp = NAN;
+        if (st == NT_ROW_OK) lp = float(double(ztok(xrow, tok) - zmax(apf)) - lnSp);
+        p.logp[row] = lp;
+    }
+    if (p.ent) p.ent[row] = (st == NT_ROW_OK || st == kRowBadToken) ? float(lnSp - kLn2 * Hp / Sp) : NAN;
+    if constexpr (REF) {
+        double ar, Sr, Hr, Br;
+        finish(wr, ar, Sr, Hr, Br);
+        const float arf = float(ar);
+        const bool rok = arf != -INFINITY && Sr == Sr;
+        if (p.ref_logp) {
+            float lr = NAN;
+            if (rok && tok >= 0 && tok < p.V) lr = float(double(ztok(yrow, tok) - zmax(arf)) - log(Sr));
+            p.ref_logp[row] = lr;
+        }
+        if constexpr (KL) {
+            if (p.kl) {
+                float k = NAN;
+                if ((st == NT_ROW_OK || st == kRowBadToken) && rok) {
+                    // KL = sum p (z - zr) - (lse_p - lse_r), with the temperature applied in f64:
+                    // z - zr = (v - vr)/T and lse = a/T + ln S in the value space.
+                    const double it = (MK == NT_MASK_F32 || tau_one) ? 1.0 : 1.0 / double(p.tau);
+                    k = float((Bp / Sp - (ap - ar)) * it - log(Sp / Sr));
+                }
+                p.kl[row] = k;
+            }
+        }
+    }
+    if (p.status) p.status[row] = uint8_t(st);
+}
+
+// ------------------------------------------------------------------ per-token kernels
+
+__global__ void k_kl_estimate(const float *lp, const float *lr, const float *mask, int64_t n, int est,
+                              float clamp, int clamped, float *out) {
+    for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
+        const bool scored = mask ? (mask[i] != 0.0f) : true;
+        // zero_masked is a select (rl.rs:100-102); then the optional clamp (rl.rs:389-392).
+        float d = scored ? (lr[i] - lp[i]) : 0.0f;
+        if (clamped) d = fminf(fmaxf(d, -clamp), clamp);
+        float k;
+        if (est == 1) k = -d;
+        else if (est == 2) k = (d * d) / 2.0f;
+        else k = expm1f(d) - d;  // = exp(d) - d - 1 without the cancellation near d = 0
+        out[i] = scored ? k : 0.0f;
+    }
+}
+
+__global__ void k_zero_masked(const float *x, const float *mask, int64_t n, float *out) {
+    for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x)
+        out[i] = mask[i] != 0.0f ? x[i] : 0.0f;
+}
+
+__global__ void k_reduce_tokens(const float *per, const float *mask, int64_t S, int64_t B, int64_t T, int red,
+                                float *out) {
+    const int64_t nout = red == 3 ? S * B : S;
+    const int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+    if (i >= nout) return;
+    if (red == 3) {
+        double v = 0.0, m = 0.0;
+        for (int64_t t = 0; t < T; t++) {
+            v += double(per[i * T + t]);
+            m += mask ? double(mask[i * T + t]) : 1.0;
+        }
+        out[i] = float(v / (m > 1.0 ? m : 1.0));
+        return;
+    }
+    double tot = 0.0, cnt = 0.0, seq = 0.0, nonempty = 0.0;
+    for (int64_t b = 0; b < B; b++) {
+        double v = 0.0, m = 0.0;
+        for (int64_t t = 0; t < T; t++) {
+            const int64_t k = (i * B + b) * T + t;
+            v += double(per[k]);
+            m += mask ? double(mask[k]) : 1.0;
+        }
+        tot += v;
+        cnt += m;
+        seq += v / (m > 1.0 ? m : 1.0);
+        nonempty += (m > 1.0 ? 1.0 : m);
+    }
+    if (red == 1) out[i] = float(tot);
+    else if (red == 2) out[i] = float(tot / (cnt > 1.0 ? cnt : 1.0));
+    else out[i] = float(seq / (nonempty > 1.0 ? nonempty : 1.0));
+}
+
+// ------------------------------------------------------------------ dispatch helpers
+
+int check_rows(int64_t rows, int64_t V, int64_t ld, int32_t dtype, int32_t mk, const void *mask, int64_t mask_ld,
+               const char *who) {
+    char buf[256];
+    if (rows < 0 || V < 1 || ld < V || (dtype != NT_F32 && dtype != NT_BF16) || mk < NT_MASK_NONE ||
+        mk > NT_MASK_F32 || ((mk == NT_MASK_NONE) != (mask == nullptr)) || (mask_ld != 0 && mask_ld < V) ||
+        rows > 0x7fffffffLL) {
+        std::snprintf(buf, sizeof buf,
+                      "%s: invalid rows %lld, V %lld, ld %lld, dtype %d, mask kind %d (mask %s), mask_ld %lld", who,
+                      (long long)rows, (long long)V, (long long)ld, dtype, mk, mask ? "set" : "null",
+                      (long long)mask_ld);
+        return fail(NT_E_ARG, buf);
+    }
+    return 0;
+}
+
+bool aligned_rows(const void *x, int64_t V, int64_t ld, int32_t dtype, int32_t mk, const void *mask, int64_t mask_ld) {
+    if (V % kEpl != 0 || ld % kEpl != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0) return false;
+    (void)dtype;
+    if (mk == NT_MASK_U8) return mask_ld % 8 == 0 && reinterpret_cast<uintptr_t>(mask) % 8 == 0;
+    if (mk == NT_MASK_F32) return mask_ld % 4 == 0 && reinterpret_cast<uintptr_t>(mask) % 16 == 0;
+    return true;
+}
+
+template <int DT, int MK, bool ENT, bool AL>
+void launch_sample(const SampleP &p, int64_t rows, int threads, size_t shm, hipStream_t s) {
+    hipLaunchKernelGGL((k_sample<DT, MK, ENT, AL>), dim3(unsigned(rows)), dim3(threads), shm, s, p);
+}
+
+template <int DT, int MK, bool ENT>
+void pick_al_sample(bool al, const SampleP &p, int64_t rows, int threads, size_t shm, hipStream_t s) {
+    if (al) launch_sample<DT, MK, ENT, true>(p, rows, threads, shm, s);
+    else launch_sample<DT, MK, ENT, false>(p, rows, threads, shm, s);
+}
+
+template <int DT, int MK>
+void pick_ent_sample(bool ent, bool al, const SampleP &p, int64_t rows, int threads, size_t shm, hipStream_t s) {
+    if (ent) pick_al_sample<DT, MK, true>(al, p, rows, threads, shm, s);
+    else pick_al_sample<DT, MK, false>(al, p, rows, threads, shm, s);
+}
+
+template <int DT>
+void pick_mk_sample(int mk, bool ent, bool al, const SampleP &p, int64_t rows, int threads, size_t shm,
+                    hipStream_t s) {
+    if (mk == NT_MASK_U8) pick_ent_sample<DT, NT_MASK_U8>(ent, al, p, rows, threads, shm, s);
+    else if (mk == NT_MASK_F32) pick_ent_sample<DT, NT_MASK_F32>(ent, al, p, rows, threads, shm, s);
+    else pick_ent_sample<DT, NT_MASK_NONE>(ent, al, p, rows, threads, shm, s);
+}
+
+template <int DT, int MK, bool REF, bool KL, bool ENT>
+void pick_al_score(bool al, const ScoreP &p, int64_t rows, hipStream_t s) {
+    if (al) hipLaunchKernelGGL((k_score<DT, MK, REF, KL, ENT, true>), dim3(unsigned(rows)), dim3(kScoreThreads), 0, s, p);
+    else hipLaunchKernelGGL((k_score<DT, MK, REF, KL, ENT, false>), dim3(unsigned(rows)), dim3(kScoreThreads), 0, s, p);
+}
+
+template <int DT, int MK>
+void pick_flags_score(bool ref, bool kl, bool ent, bool al, const ScoreP &p, int64_t rows, hipStream_t s) {
+    if (ref && kl) {
+        if (ent) pick_al_score<DT, MK, true, true, true>(al, p, rows, s);
+        else pick_al_score<DT, MK, true, true, false>(al, p, rows, s);
+    } else if (ref) {
+        if (ent) pick_al_score<DT, MK, true, false, true>(al, p, rows, s);
+        else pick_al_score<DT, MK, true, false, false>(al, p, rows, s);
+    } else {
+        if (ent) pick_al_score<DT, MK, false, false, true>(al, p, rows, s);
+        else pick_al_score<DT, MK, false, false, false>(al, p, rows, s);
+    }
+}
+
+template <int DT>
+void pick_mk_score(int mk, bool ref, bool kl, bool ent, bool al, const ScoreP &p, int64_t rows, hipStream_t s) {
+    if (mk == NT_MASK_U8) pick_flags_score<DT, NT_MASK_U8>(ref, kl, ent, al, p, rows, s);
+    else if (mk == NT_MASK_F32) pick_flags_score<DT, NT_MASK_F32>(ref, kl, ent, al, p, rows, s);
+    else pick_flags_score<DT, NT_MASK_NONE>(ref, kl, ent, al, p, rows, s);
+}
+
+}  // namespace
+}  // namespace nt
+
+using namespace nt;
+
+extern "C" {
+
+int nt_hip_rl_sample(const NtRlSampleArgs *a) {
+    if (!a) return fail(NT_E_ARG, "nt_hip_rl_sample: null args");
+    if (int rc = check_rows(a->rows, a->vocab, a->ld, a->dtype, a->mask_kind, a->mask, a->mask_ld, "nt_hip_rl_sample"))
+        return rc;
+    if (!(a->temperature >= 0.0) || !std::isfinite(a->temperature))
+        return fail(NT_E_ARG, "sample_categorical: temperature " + std::to_string(a->temperature) + " (must be ≥ 0)");
+    const bool greedy = a->temperature == 0.0;
+    if (!a->logits || !a->ids || !a->status || (!greedy && !a->uniforms))
+        return fail(NT_E_ARG, "nt_hip_rl_sample: null logits, ids, status or uniforms");
+    std::unique_lock<std::mutex> lk;
+    if (int rc = enter(&lk)) return rc;
+    if (a->rows == 0) return 0;
+    const int64_t nc = (a->vocab + kChunk - 1) / kChunk;
+    const bool ent = a->entropy != nullptr;
+    const size_t shm = size_t(nc) * sizeof(float) * (ent ? 3 : 2);
+    if (shm > 64 * 1024) return fail(NT_E_UNSUPPORTED, "nt_hip_rl_sample: V " + std::to_string(a->vocab) + " too large");
+    SampleP p;
+    p.logits = a->logits;
+    p.mask = a->mask;
+    p.V = a->vocab;
+    p.ld = a->ld;
+    p.mask_ld = a->mask_ld;
+    const double T = greedy ? 1.0 : a->temperature;
+    p.tau = float(T);
+    p.tau_one = (T == 1.0);
+    p.c = (a->mask_kind == NT_MASK_F32 || T == 1.0) ? kLog2e : float(double(kLog2e) / double(p.tau));
+    p.greedy = greedy;
+    p.nc = int(nc);
+    p.u = a->uniforms;
+    p.ids = a->ids;
+    p.logp = a->logp;
+    p.ent = a->entropy;
+    p.status = a->status;
+    // Waves per row: about four chunks per wave, at most 16; many rows get smaller groups.
+    int nw = int(nc / 4);
+    nw = nw < 1 ? 1 : (nw > 16 ? 16 : nw);
+    if (a->rows >= 2048 && nw > 4) nw = 4;
+    const bool al = aligned_rows(a->logits, a->vocab, a->ld, a->dtype, a->mask_kind, a->mask, a->mask_ld);
+    hipStream_t s = ctx().stream;
+    if (a->dtype == NT_F32) pick_mk_sample<NT_F32>(a->mask_kind, ent, al, p, a->rows, nw * kWave, shm, s);
+    else pick_mk_sample<NT_BF16>(a->mask_kind, ent, al, p, a->rows, nw * kWave, shm, s);
+    return launched("nt_hip_rl_sample");
+}
+
+int nt_hip_rl_score(const NtRlScoreArgs *a) {
+    if (!a) return fail(NT_E_ARG, "nt_hip_rl_score: null args");
+    if (int rc = check_rows(a->rows, a->vocab, a->ld, a->dtype, a->mask_kind, a->mask, a->mask_ld, "nt_hip_rl_score"))
+        return rc;
+    if (!(a->temperature > 0.0) || !std::isfinite(a->temperature))
+        return fail(NT_E_ARG, "tempered_logits: temperature " + std::to_string(a->temperature) + " (must be positive)");
+    if (!a->logits) return fail(NT_E_ARG, "nt_hip_rl_score: null logits");
+    if ((a->logp || a->ref_logp) && !a->tokens) return fail(NT_E_ARG, "nt_hip_rl_score: log-probabilities need tokens");
+    if ((a->ref_logp || a->kl) && !a->ref_logits) return fail(NT_E_ARG, "nt_hip_rl_score: ref_logp/kl need ref_logits");
+    std::unique_lock<std::mutex> lk;
+    if (int rc = enter(&lk)) return rc;
+    if (a->rows == 0) return 0;
+    ScoreP p;
+    p.logits = a->logits;
+    p.ref = a->ref_logits;
+    p.mask = a->mask;
+    p.V = a->vocab;
+    p.ld = a->ld;
+    p.mask_ld = a->mask_ld;
+    p.tau = float(a->temperature);
+    p.tau_one = (a->temperature == 1.0);
+    p.c = (a->mask_kind == NT_MASK_F32 || p.tau_one) ? kLog2e : float(double(kLog2e) / double(p.tau));
+    p.nc = int((a->vocab + kChunk - 1) / kChunk);
+    p.tokens = a->tokens;
+    p.logp = a->logp;
+    p.ref_logp = a->ref_logp;
+    p.kl = a->kl;
+    p.ent = a->entropy;
+    p.status = a->status;
+    const bool ref = a->ref_logits != nullptr && (a->ref_logp || a->kl);
+    const bool kl = a->kl != nullptr;
+    const bool ent = a->entropy != nullptr;
+    bool al = aligned_rows(a->logits, a->vocab, a->ld, a->dtype, a->mask_kind, a->mask, a->mask_ld);
+    if (ref) al = al && reinterpret_cast<uintptr_t>(a->ref_logits) % 16 == 0;
+    hipStream_t s = ctx().stream;
+    if (a->dtype == NT_F32) pick_mk_score<NT_F32>(a->mask_kind, ref, kl, ent, al, p, a->rows, s);
+    else pick_mk_score<NT_BF16>(a->mask_kind, ref, kl, ent, al, p, a->rows, s);
+    return launched("nt_hip_rl_score");
+}
+
+int nt_hip_rl_kl_estimate(const float *logp, const float *ref_logp, const float *mask, int64_t n, int32_t estimator,
+                          double clamp, float *out) {
+    if (n < 0 || !logp || !ref_logp || !out || estimator < 1 || estimator > 3)
+        return fail(NT_E_ARG, "nt_hip_rl_kl_estimate: invalid arguments");
+    if (clamp < 0.0) return fail(NT_E_ARG, "kl_estimate: δ clamp " + std::to_string(clamp) + " (need b > 0)");
+    std::unique_lock<std::mutex> lk;
+    if (int rc = enter(&lk)) return rc;
+    if (n == 0) return 0;
+    const int threads = 256;
+    int64_t blocks = (n + threads - 1) / threads;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(k_kl_estimate, dim3(unsigned(blocks)), dim3(threads), 0, ctx().stream, logp, ref_logp, mask, n,
+                       int(estimator), float(clamp), clamp > 0.0 ? 1 : 0, out);
+    return launched("nt_hip_rl_kl_estimate");
+}
+
+int nt_hip_rl_zero_masked(const float *x, const float *mask, int64_t n, float *out) {
+    if (n < 0 || !x || !mask || !out) return fail(NT_E_ARG, "nt_hip_rl_zero_masked: invalid arguments");
+    std::unique_lock<std::mutex> lk;
+    if (int rc = enter(&lk)) return rc;
+    if (n == 0) return 0;
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(k_zero_masked, dim3(unsigned(blocks)), dim3(256), 0, ctx().stream, x, mask, n, out);
+    return launched("nt_hip_rl_zero_masked");
+}
+
+int nt_hip_rl_reduce_tokens(const float *per, const float *mask, int64_t S, int64_t B, int64_t T, int32_t reduction,
+                            float *out) {
+    if (!per || !out || S < 0 || B < 0 || T < 0 || reduction < 1 || reduction > 4)
+        return fail(NT_E_ARG, "nt_hip_rl_reduce_tokens: invalid arguments");
+    std::unique_lock<std::mutex> lk;
+    if (int rc = enter(&lk)) return rc;
+    const int64_t nout = reduction == 3 ? S * B : S;
+    if (nout == 0) return 0;
+    const int threads = 64;
+    hipLaunchKernelGGL(k_reduce_tokens, dim3(unsigned((nout + threads - 1) / threads)), dim3(threads), 0,
+                       ctx().stream, per, mask, S, B, T, int(reduction), out);
+    return launched("nt_hip_rl_reduce_tokens");
+}
+
+}  // extern "C"

@@ -1,0 +1,183 @@
+// Host runtime of libnoetic_hip.so: device claim, the library stream, memory and copies,
+// errors, the provenance key. It replaces the device/context/memory part of the reference's
+// GpuBackend (src/tensor/gpu/mod.rs:137-207) and CUDA context handling
+// (src/tensor/cuda/backend.rs:104-264) for a `Device::Hip(i)`.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/noetic_hip.h"
+#include "nt_internal.hpp"
+
+#ifndef NT_KERNELS_SHA
+#define NT_KERNELS_SHA "unknown"
+#endif
+
+namespace nt {
+
+Ctx &ctx() {
+    static Ctx c;
+    return c;
+}
+
+static thread_local std::string g_last_error;
+
+int fail(int code, const std::string &msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int hip_check(hipError_t err, const char *what) {
+    if (err == hipSuccess) return 0;
+    char buf[512];
+    std::snprintf(buf, sizeof buf, "HIP %s: %s (%d): %s", what, hipGetErrorName(err), (int)err,
+                  hipGetErrorString(err));
+    return fail((int)err, buf);
+}
+
+int launched(const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_check(e, what);
+    ctx().launches++;
+    return 0;
+}
+
+int enter(std::unique_lock<std::mutex> *out) {
+    Ctx &c = ctx();
+    std::unique_lock<std::mutex> lk(c.mu);
+    if (c.device < 0) return fail(NT_E_UNCLAIMED, "no HIP device claimed in this process (nt_hip_claim)");
+    hipError_t e = hipSetDevice(c.device);
+    if (e != hipSuccess) return hip_check(e, "hipSetDevice");
+    *out = std::move(lk);
+    return 0;
+}
+
+}  // namespace nt
+
+using namespace nt;
+
+extern "C" {
+
+int nt_hip_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return n;
+}
+
+int nt_hip_claim(int device) {
+    Ctx &c = ctx();
+    std::lock_guard<std::mutex> lk(c.mu);
+    if (c.device == device) return 0;
+    if (c.device >= 0) {
+        char buf[160];
+        std::snprintf(buf, sizeof buf, "Hip(%d): this process already uses Hip(%d) (one device per process)",
+                      device, c.device);
+        return fail(NT_E_CLAIMED, buf);
+    }
+    int n = 0;
+    if (int rc = hip_check(hipGetDeviceCount(&n), "hipGetDeviceCount")) return rc;
+    if (device < 0 || device >= n) {
+        char buf[120];
+        std::snprintf(buf, sizeof buf, "Hip(%d): %d HIP device(s) visible", device, n);
+        return fail(NT_E_ARG, buf);
+    }
+    if (int rc = hip_check(hipSetDevice(device), "hipSetDevice")) return rc;
+    hipStream_t s = nullptr;
+    // Default priority only: streams of other priorities are not used by this library.
+    if (int rc = hip_check(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreateWithFlags"))
+        return rc;
+    c.device = device;
+    c.stream = s;
+    return 0;
+}
+
+const char *nt_hip_last_error(void) { return g_last_error.c_str(); }
+
+int nt_hip_key(char *buf, size_t cap) {
+    if (!buf || cap == 0) return fail(NT_E_ARG, "nt_hip_key: empty buffer");
+    std::unique_lock<std::mutex> lk;
+    if (int rc = enter(&lk)) return rc;
+    hipDeviceProp_t prop;
+    if (int rc = hip_check(hipGetDeviceProperties(&prop, ctx().device), "hipGetDeviceProperties")) return rc;
+    int rt = 0;
+    (void)hipRuntimeGetVersion(&rt);
+    std::string arch(prop.gcnArchName);
+    for (char &ch : arch)
+        if (ch == ':') ch = '_';
+    std::string sha(NT_KERNELS_SHA);
+    std::string key = "hip-" + arch + "-hiprt" + std::to_string(rt) + "-kernels-" + sha.substr(0, 16);
+    std::snprintf(buf, cap, "%s", key.c_str());
+    return 0;
+}
+
+int nt_hip_alloc(size_t bytes, void **out) {
+    if (!out) return fail(NT_E_ARG, "nt_hip_alloc: null out");
+    std::unique_lock<std::mutex> lk;
+    if (int rc = enter(&lk)) return rc;
+    *out = nullptr;
+    if (bytes == 0) return 0;
+    return hip_check(hipMalloc(out, bytes), "hipMalloc");
+}
+
+int nt_hip_free(void *ptr) {
+    if (!ptr) return 0;
+    std::unique_lock<std::mutex> lk;
+    if (int rc = enter(&lk)) return rc;
+    // Work queued on the library stream may still read the buffer: drain it first.
+    if (int rc = hip_check(hipStreamSynchronize(ctx().stream), "hipStreamSynchronize")) return rc;
+    return hip_check(hipFree(ptr), "hipFree");
+}
+
+int nt_hip_upload(void *dst, const void *src, size_t bytes) {
+    if (bytes == 0) return 0;
+    if (!dst || !src) return fail(NT_E_ARG, "nt_hip_upload: null pointer");
+    std::unique_lock<std::mutex> lk;
+    if (int rc = enter(&lk)) return rc;
+    if (int rc = hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx().stream), "upload"))
+        return rc;
+    return hip_check(hipStreamSynchronize(ctx().stream), "hipStreamSynchronize");
+}
+
+int nt_hip_download(void *dst, const void *src, size_t bytes) {
+    if (bytes == 0) return 0;
+    if (!dst || !src) return fail(NT_E_ARG, "nt_hip_download: null pointer");
+    std::unique_lock<std::mutex> lk;
+    if (int rc = enter(&lk)) return rc;
+    if (int rc = hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx().stream), "download"))
+        return rc;
+    return hip_check(hipStreamSynchronize(ctx().stream), "hipStreamSynchronize");
+}
+
+int nt_hip_memset(void *dst, int value, size_t bytes) {
+    if (bytes == 0) return 0;
+    if (!dst) return fail(NT_E_ARG, "nt_hip_memset: null pointer");
+    std::unique_lock<std::mutex> lk;
+    if (int rc = enter(&lk)) return rc;
+    return hip_check(hipMemsetAsync(dst, value, bytes, ctx().stream), "hipMemsetAsync");
+}
+
+int nt_hip_sync(void) {
+    std::unique_lock<std::mutex> lk;
+    if (int rc = enter(&lk)) return rc;
+    return hip_check(hipStreamSynchronize(ctx().stream), "hipStreamSynchronize");
+}
+
+int nt_hip_stream(void **out) {
+    if (!out) return fail(NT_E_ARG, "nt_hip_stream: null out");
+    std::unique_lock<std::mutex> lk;
+    if (int rc = enter(&lk)) return rc;
+    *out = (void *)ctx().stream;
+    return 0;
+}
+
+uint64_t nt_hip_launches(void) {
+    std::lock_guard<std::mutex> lk(ctx().mu);
+    return ctx().launches;
+}
+
+}  // extern "C"

@@ -1,0 +1,517 @@
+"""Host-side mirror of noetic-tensor's `nn::rl` for a `Device::Hip(0)` tensor.
+
+The reference (shyble/noetic-tensor 0.7.0) is a Rust crate; its `nn::rl` functions take
+`Tensor`/`IntTensor` values and dispatch every op to the device's backend. This module keeps
+those function names, argument meanings and refusal messages, and runs each call as the fused
+kernels of libnoetic_hip.so through its C ABI (include/noetic_hip.h). There is no CPU fallback:
+without the built library, or without a GPU, every call raises `HipUnavailable`.
+
+Tensors live in device memory owned by this module (`Tensor`, `IntTensor`); `to_numpy()` is the
+reference's `to_vec*` (a synchronising download).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import enum
+import math
+import os
+from typing import Optional, Sequence
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libnoetic_hip.so")
+
+# include/noetic_hip.h
+NT_F32, NT_BF16 = 0, 1
+NT_MASK_NONE, NT_MASK_U8, NT_MASK_F32 = 0, 1, 2
+NT_ROW_OK, NT_ROW_NO_TOKEN, NT_ROW_NAN, NT_ROW_BAD_TOKEN = 0, 1, 2, 3
+
+
+class HipUnavailable(RuntimeError):
+    """libnoetic_hip.so is not built, or no HIP device can be claimed."""
+
+
+class HipError(RuntimeError):
+    """A failed call into libnoetic_hip.so (the reference's TensorError::Device)."""
+
+
+class NtRlSampleArgs(C.Structure):
+    _fields_ = [("logits", C.c_void_p), ("dtype", C.c_int32), ("mask_kind", C.c_int32),
+                ("rows", C.c_int64), ("vocab", C.c_int64), ("ld", C.c_int64),
+                ("mask", C.c_void_p), ("mask_ld", C.c_int64), ("temperature", C.c_double),
+                ("uniforms", C.c_void_p), ("ids", C.c_void_p), ("logp", C.c_void_p),
+                ("entropy", C.c_void_p), ("status", C.c_void_p)]
+
+
+class NtRlScoreArgs(C.Structure):
+    _fields_ = [("logits", C.c_void_p), ("ref_logits", C.c_void_p), ("dtype", C.c_int32),
+                ("mask_kind", C.c_int32), ("rows", C.c_int64), ("vocab", C.c_int64), ("ld", C.c_int64),
+                ("mask", C.c_void_p), ("mask_ld", C.c_int64), ("temperature", C.c_double),
+                ("tokens", C.c_void_p), ("logp", C.c_void_p), ("ref_logp", C.c_void_p),
+                ("kl", C.c_void_p), ("entropy", C.c_void_p), ("status", C.c_void_p)]
+
+
+class NtRng(C.Structure):
+    _fields_ = [("key", C.c_uint32 * 8), ("counter", C.c_uint64), ("buf", C.c_uint32 * 16), ("idx", C.c_int32)]
+
+
+class NtSynthNormal(C.Structure):
+    _fields_ = [("out", C.c_void_p), ("dtype", C.c_int32), ("rows", C.c_int64), ("vocab", C.c_int64),
+                ("key", C.c_uint32 * 8), ("mean", C.c_double), ("std", C.c_double), ("zipf_s", C.c_double),
+                ("rot_key", C.c_uint32 * 8), ("base", C.c_void_p)]
+
+
+# Every function the headers under include/ declare, with its ctypes signature.
+_SIGS = {
+    # noetic_hip.h
+    "nt_hip_claim": (C.c_int, [C.c_int]),
+    "nt_hip_device_count": (C.c_int, []),
+    "nt_hip_last_error": (C.c_char_p, []),
+    "nt_hip_key": (C.c_int, [C.c_char_p, C.c_size_t]),
+    "nt_hip_alloc": (C.c_int, [C.c_size_t, C.POINTER(C.c_void_p)]),
+    "nt_hip_free": (C.c_int, [C.c_void_p]),
+    "nt_hip_upload": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
+    "nt_hip_download": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
+    "nt_hip_memset": (C.c_int, [C.c_void_p, C.c_int, C.c_size_t]),
+    "nt_hip_sync": (C.c_int, []),
+    "nt_hip_stream": (C.c_int, [C.POINTER(C.c_void_p)]),
+    "nt_hip_launches": (C.c_uint64, []),
+    "nt_hip_rl_sample": (C.c_int, [C.POINTER(NtRlSampleArgs)]),
+    "nt_hip_rl_score": (C.c_int, [C.POINTER(NtRlScoreArgs)]),
+    "nt_hip_rl_kl_estimate": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_int32, C.c_double,
+                                        C.c_void_p]),
+    "nt_hip_rl_zero_masked": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p]),
+    "nt_hip_rl_reduce_tokens": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_int32,
+                                          C.c_void_p]),
+    # noetic_rng.h
+    "nt_rng_derive": (C.c_int, [C.POINTER(NtRng), C.c_uint64, C.c_char_p, C.c_size_t]),
+    "nt_rng_from_seed": (C.c_int, [C.POINTER(NtRng), C.c_char_p]),
+    "nt_rng_next_u32": (C.c_uint32, [C.POINTER(NtRng)]),
+    "nt_rng_next_u64": (C.c_uint64, [C.POINTER(NtRng)]),
+    "nt_rng_uniforms": (C.c_int, [C.POINTER(NtRng), C.c_size_t, C.c_void_p]),
+    "nt_sha256": (C.c_int, [C.c_char_p, C.c_size_t, C.c_char_p]),
+    # noetic_synth.h
+    "nt_synth_normal": (C.c_int, [C.POINTER(NtSynthNormal)]),
+    "nt_synth_spikes": (C.c_int, [C.c_void_p, C.c_int32, C.c_int64, C.c_int64, C.c_int32, C.POINTER(C.c_uint32),
+                                  C.c_double]),
+    "nt_synth_bernoulli_mask": (C.c_int, [C.c_void_p, C.c_int64, C.POINTER(C.c_uint32), C.c_double]),
+    "nt_synth_tokens": (C.c_int, [C.c_void_p, C.c_int64, C.POINTER(C.c_uint32), C.c_int64]),
+    "nt_synth_keep_tokens": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_void_p]),
+    "nt_synth_runs_mask_host": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_uint64, C.c_char_p, C.c_size_t,
+                                          C.c_int32, C.c_int32]),
+}
+
+_lib = None
+_claimed = False
+
+
+def lib():
+    """The loaded libnoetic_hip.so (no device claimed yet)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise HipUnavailable(f"{LIB_PATH} is not built (run __graft_entry__.build())")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _check(rc, what):
+    if rc != 0:
+        raise HipError(f"{what}: {lib().nt_hip_last_error().decode(errors='replace')} (code {rc})")
+
+
+def claim(device: int = 0):
+    """Claim Hip(device) for this process (one device per process)."""
+    global _claimed
+    L = lib()
+    if L.nt_hip_device_count() < 1:
+        raise HipUnavailable("no HIP device visible")
+    _check(L.nt_hip_claim(device), f"claim Hip({device})")
+    _claimed = True
+
+
+def _dev():
+    if not _claimed:
+        claim(0)
+    return lib()
+
+
+def sync():
+    _check(_dev().nt_hip_sync(), "sync")
+
+
+def key() -> str:
+    buf = C.create_string_buffer(256)
+    _check(_dev().nt_hip_key(buf, 256), "key")
+    return buf.value.decode()
+
+
+def launches() -> int:
+    return int(lib().nt_hip_launches())
+
+
+# ----------------------------------------------------------------------------------- storage
+
+_NP = {"f32": np.float32, "bf16": np.uint16, "u8": np.uint8, "i32": np.int32, "f64": np.float64}
+
+
+class Buffer:
+    """A device allocation owned by Python (freed on garbage collection)."""
+
+    def __init__(self, nbytes: int):
+        L = _dev()
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        _check(L.nt_hip_alloc(max(self.nbytes, 1), C.byref(p)), f"alloc {nbytes} B")
+        self.ptr = p.value
+
+    def __del__(self):
+        try:
+            if self.ptr and _lib is not None:
+                _lib.nt_hip_free(C.c_void_p(self.ptr))
+        except Exception:
+            pass
+        self.ptr = None
+
+
+class Tensor:
+    """Device storage with a shape and a dtype ("f32", "bf16" bits, "u8", "i32", "f64")."""
+
+    def __init__(self, shape: Sequence[int], dtype: str, buf: Optional[Buffer] = None):
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = dtype
+        self.numel = int(np.prod(self.shape)) if self.shape else 1
+        nbytes = self.numel * np.dtype(_NP[dtype]).itemsize
+        self.buf = buf if buf is not None else Buffer(nbytes)
+        self.nbytes = nbytes
+
+    @property
+    def ptr(self):
+        return self.buf.ptr
+
+    @staticmethod
+    def from_numpy(a: np.ndarray, dtype: Optional[str] = None) -> "Tensor":
+        if dtype is None:
+            dtype = {np.dtype(np.float32): "f32", np.dtype(np.uint16): "bf16", np.dtype(np.uint8): "u8",
+                     np.dtype(np.int32): "i32", np.dtype(np.float64): "f64"}[a.dtype]
+        a = np.ascontiguousarray(a, dtype=_NP[dtype])
+        t = Tensor(a.shape, dtype)
+        _check(_dev().nt_hip_upload(C.c_void_p(t.ptr), a.ctypes.data_as(C.c_void_p), t.nbytes), "upload")
+        return t
+
+    def to_numpy(self) -> np.ndarray:
+        out = np.empty(self.shape, dtype=_NP[self.dtype])
+        _check(_dev().nt_hip_download(out.ctypes.data_as(C.c_void_p), C.c_void_p(self.ptr), self.nbytes), "download")
+        return out
+
+    def to_f64(self) -> np.ndarray:
+        """`to_vec_f64` (a bf16 tensor widens exactly)."""
+        a = self.to_numpy()
+        if self.dtype == "bf16":
+            return (a.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+        return a.astype(np.float64)
+
+    def dims(self):
+        return self.shape
+
+
+def IntTensor(shape, buf=None) -> Tensor:
+    """Device I32 indices (the reference's device index dtype, src/tensor/gpu/mod.rs:355-357)."""
+    return Tensor(shape, "i32", buf)
+
+
+def _dtype_code(t: Tensor) -> int:
+    if t.dtype == "f32":
+        return NT_F32
+    if t.dtype == "bf16":
+        return NT_BF16
+    raise ValueError(f"logits of dtype {t.dtype} (f32 or bf16)")
+
+
+# ----------------------------------------------------------------------------------- rng
+
+class Rng:
+    """rng::derive(root, label) (src/rng.rs:9-17): the engine stream the sampler draws from."""
+
+    def __init__(self, root: int, label: str):
+        self.s = NtRng()
+        b = label.encode()
+        _check(lib().nt_rng_derive(C.byref(self.s), root, b, len(b)), "rng derive")
+
+    def clone(self) -> "Rng":
+        r = Rng.__new__(Rng)
+        r.s = NtRng()
+        C.memmove(C.byref(r.s), C.byref(self.s), C.sizeof(NtRng))
+        return r
+
+    def next_u64(self) -> int:
+        return int(lib().nt_rng_next_u64(C.byref(self.s)))
+
+    def next_u32(self) -> int:
+        return int(lib().nt_rng_next_u32(C.byref(self.s)))
+
+    def uniforms(self, n: int) -> np.ndarray:
+        out = np.empty(n, dtype=np.float64)
+        _check(lib().nt_rng_uniforms(C.byref(self.s), n, out.ctypes.data_as(C.c_void_p)), "uniforms")
+        return out
+
+    def key(self):
+        return (C.c_uint32 * 8)(*self.s.key)
+
+
+# ----------------------------------------------------------------------------------- nn::rl
+
+class TokenReduction(enum.IntEnum):
+    """rl.rs:37-55."""
+    NONE = 0
+    SUM = 1
+    TOKEN_MEAN = 2
+    PER_SEQUENCE = 3
+    SEQUENCE_MEAN = 4
+
+
+class KlEstimator(enum.IntEnum):
+    """rl.rs:356-366."""
+    K1 = 1
+    K2 = 2
+    K3 = 3
+
+
+KL_DELTA_CLAMP = 20.0  # rl.rs:150
+
+
+class Tempered:
+    """`tempered_logits(logits, temperature, mask)` (rl.rs:475-486), kept unmaterialised: the
+    fused kernels apply the divide and the vocabulary mask while streaming the logits.
+    mask: None, a u8 keep-mask (0 excludes) or an additive f32 mask, [rows or 1, V] in the
+    logits' rank (a mask whose leading dims are all 1 is shared by every row)."""
+
+    def __init__(self, logits: Tensor, temperature: float, mask: Optional[Tensor]):
+        if not (temperature > 0.0 and math.isfinite(temperature)):
+            raise ValueError(f"tempered_logits: temperature {temperature} (must be positive)")
+        self.logits, self.temperature, self.mask = logits, float(temperature), mask
+        if mask is not None:
+            if len(mask.shape) != len(logits.shape):
+                raise ValueError("tempered_logits: mask rank")
+            if not all(a == b or a == 1 for a, b in zip(mask.shape, logits.shape)):
+                raise ValueError(f"tempered_logits: mask {list(mask.shape)} does not broadcast to the logits "
+                                 f"{list(logits.shape)}")
+            lead = mask.shape[:-1]
+            if mask.shape[-1] != logits.shape[-1] or not (all(d == 1 for d in lead) or lead == logits.shape[:-1]):
+                raise ValueError("tempered_logits: the vocabulary mask must be [.., V] per row or shared by all rows")
+
+
+def tempered_logits(logits: Tensor, temperature: float, mask: Optional[Tensor] = None) -> Tempered:
+    return Tempered(logits, temperature, mask)
+
+
+def _as_tempered(x) -> Tempered:
+    return x if isinstance(x, Tempered) else Tempered(x, 1.0, None)
+
+
+def _mask_fields(t: Tempered, rows: int, V: int):
+    m = t.mask
+    if m is None:
+        return NT_MASK_NONE, None, 0
+    kind = {"u8": NT_MASK_U8, "f32": NT_MASK_F32}.get(m.dtype)
+    if kind is None:
+        raise ValueError(f"vocabulary mask of dtype {m.dtype} (u8 keep-mask or f32 additive)")
+    shared = all(d == 1 for d in m.shape[:-1])
+    return kind, m.ptr, (0 if shared else V)
+
+
+def _rows(x: Tensor):
+    if len(x.shape) < 1:
+        raise ValueError("logits of rank 0")
+    V = x.shape[-1]
+    return x.numel // V, V
+
+
+def sample_logp(logits: Tensor, temperature: float, mask: Optional[Tensor], rng: Optional[Rng],
+                entropy: bool = False, uniforms: Optional[Tensor] = None, check: bool = True):
+    """The fused path: (ids, logp[, entropy]) of the inverse-CDF sample of each row, drawing one
+    uniform per row from `rng` (none at temperature 0). `uniforms` (device f64 [rows]) may be
+    given instead of `rng`. `check` reads the per-row status and refuses a row with no allowed
+    token, as sample_categorical does (rl.rs:516-519)."""
+    if not (temperature >= 0.0 and math.isfinite(temperature)):
+        raise ValueError(f"sample_categorical: temperature {temperature} (must be ≥ 0)")
+    t = Tempered(logits, 1.0 if temperature == 0.0 else temperature, mask)
+    rows, V = _rows(logits)
+    out_shape = logits.shape[:-1]
+    if temperature != 0.0 and uniforms is None:
+        if rng is None:
+            raise ValueError("sample_categorical: a stream is needed at temperature > 0")
+        uniforms = Tensor.from_numpy(rng.uniforms(rows), "f64")
+    ids = IntTensor(out_shape)
+    lp = Tensor(out_shape, "f32")
+    ent = Tensor(out_shape, "f32") if entropy else None
+    status = Tensor(out_shape, "u8")
+    kind, mptr, mld = _mask_fields(t, rows, V)
+    a = NtRlSampleArgs(logits.ptr, _dtype_code(logits), kind, rows, V, V, mptr, mld, float(temperature),
+                       None if uniforms is None else uniforms.ptr, ids.ptr, lp.ptr,
+                       None if ent is None else ent.ptr, status.ptr)
+    _check(lib().nt_hip_rl_sample(C.byref(a)), "sample")
+    if check:
+        st = status.to_numpy().ravel()
+        bad = np.nonzero(st != NT_ROW_OK)[0]
+        if bad.size:
+            raise ValueError(f"sample_categorical: position {bad[0]} has no allowed token (every logit −∞ or a NaN)")
+    return (ids, lp, ent) if entropy else (ids, lp)
+
+
+def sample_categorical(logits: Tensor, temperature: float, mask: Optional[Tensor], rng: Rng) -> Tensor:
+    """rl.rs:510-529 with the inverse-CDF draw (one uniform per row) in place of Gumbel-max."""
+    return sample_logp(logits, temperature, mask, rng)[0]
+
+
+def _score(policy, ref, tokens, want_logp, want_ref_logp, want_kl, want_ent):
+    p = _as_tempered(policy)
+    rows, V = _rows(p.logits)
+    if ref is not None:
+        r = _as_tempered(ref)
+        if r.logits.shape != p.logits.shape or r.logits.dtype != p.logits.dtype:
+            raise ValueError("categorical_kl: reference logits shape")
+        if r.temperature != p.temperature or r.mask is not p.mask:
+            raise ValueError("the fused scorer takes both sides under one temperature and one vocabulary mask "
+                             "(reference_kl)")
+    out_shape = p.logits.shape[:-1]
+    if tokens is not None and tokens.shape != out_shape:
+        raise ValueError("token_log_probs: tokens shape (the logits' without the vocabulary axis)")
+    mk = lambda want: Tensor(out_shape, "f32") if want else None
+    lp, rlp, kl, ent = mk(want_logp), mk(want_ref_logp), mk(want_kl), mk(want_ent)
+    status = Tensor(out_shape, "u8")
+    kind, mptr, mld = _mask_fields(p, rows, V)
+    ptr = lambda t: None if t is None else t.ptr
+    a = NtRlScoreArgs(p.logits.ptr, None if ref is None else _as_tempered(ref).logits.ptr, _dtype_code(p.logits),
+                      kind, rows, V, V, mptr, mld, p.temperature, ptr(tokens), ptr(lp), ptr(rlp), ptr(kl), ptr(ent),
+                      status.ptr)
+    _check(lib().nt_hip_rl_score(C.byref(a)), "score")
+    if tokens is not None:
+        st = status.to_numpy().ravel()
+        bad = np.nonzero(st == NT_ROW_BAD_TOKEN)[0]
+        if bad.size:
+            raise IndexError(f"gather index out of range {V} at position {bad[0]}")
+    return lp, rlp, kl, ent, status
+
+
+def token_log_probs(logits, tokens: Tensor) -> Tensor:
+    """rl.rs:134-141: log_softmax(logits)[…, tokens[…]]; `logits` may be a `tempered_logits`."""
+    return _score(logits, None, tokens, True, False, False, False)[0]
+
+
+def score(logits, ref_logits, tokens: Optional[Tensor], entropy=True, kl=True):
+    """The fused scoring pass: (logp, ref_logp, exact KL, entropy) per position in one read of
+    both logits (token_log_probs x2, categorical_kl / reference_kl, categorical_entropy)."""
+    lp, rlp, k, ent, _ = _score(logits, ref_logits, tokens, tokens is not None,
+                                tokens is not None and ref_logits is not None, kl and ref_logits is not None, entropy)
+    return lp, rlp, k, ent
+
+
+def _reduce(per: Tensor, mask: Optional[Tensor], reduction: TokenReduction) -> Tensor:
+    if len(per.shape) != 3:
+        raise ValueError("per-token values [S, B, T]")
+    S, B, T = per.shape
+    reduction = TokenReduction(reduction)
+    if reduction == TokenReduction.NONE:
+        return per
+    out = Tensor((S, B) if reduction == TokenReduction.PER_SEQUENCE else (S,), "f32")
+    _check(lib().nt_hip_rl_reduce_tokens(per.ptr, None if mask is None else mask.ptr, S, B, T, int(reduction),
+                                         out.ptr), "reduce_tokens")
+    return out
+
+
+def _zero_masked(per: Tensor, mask: Optional[Tensor]) -> Tensor:
+    """zero_masked (rl.rs:100-102): a select, so a non-finite value at a masked position does
+    not leak."""
+    if mask is None:
+        return per
+    if mask.shape != per.shape:
+        raise AssertionError("rl: mask shape")
+    out = Tensor(per.shape, "f32")
+    _check(lib().nt_hip_rl_zero_masked(per.ptr, mask.ptr, per.numel, out.ptr), "zero_masked")
+    return out
+
+
+def categorical_kl(logits, ref_logits, mask: Optional[Tensor] = None,
+                   reduction: TokenReduction = TokenReduction.TOKEN_MEAN) -> Tensor:
+    """rl.rs:327-338 (exact KL per position, reduced per seed)."""
+    x = _as_tempered(logits)
+    if len(x.logits.shape) != 4:
+        raise ValueError("categorical_kl: logits [S, B, T, V]")
+    kl = _score(logits, ref_logits, None, False, False, True, False)[2]
+    return _reduce(_zero_masked(kl, mask), mask, reduction)
+
+
+def reference_kl(logits: Tensor, ref_logits: Tensor, temperature: float, vocab_mask: Optional[Tensor],
+                 mask: Optional[Tensor] = None, reduction: TokenReduction = TokenReduction.TOKEN_MEAN) -> Tensor:
+    """rl.rs:347-351."""
+    return categorical_kl(Tempered(logits, temperature, vocab_mask), Tempered(ref_logits, temperature, vocab_mask),
+                          mask, reduction)
+
+
+def categorical_entropy(logits, mask: Optional[Tensor] = None,
+                        reduction: TokenReduction = TokenReduction.TOKEN_MEAN) -> Tensor:
+    """rl.rs:405-414."""
+    x = _as_tempered(logits)
+    if len(x.logits.shape) != 4:
+        raise ValueError("categorical_entropy: logits [S, B, T, V]")
+    ent = _score(logits, None, None, False, False, False, True)[3]
+    return _reduce(_zero_masked(ent, mask), mask, reduction)
+
+
+def kl_estimate(logp: Tensor, ref_logp: Tensor, estimator: KlEstimator, delta_clamp: Optional[float] = None,
+                mask: Optional[Tensor] = None, reduction: TokenReduction = TokenReduction.TOKEN_MEAN) -> Tensor:
+    """rl.rs:380-400."""
+    if len(logp.shape) != 3:
+        raise ValueError("kl_estimate: logp [S, B, T]")
+    if logp.shape != ref_logp.shape:
+        raise ValueError("kl_estimate: reference log-probabilities shape")
+    if delta_clamp is not None and not delta_clamp > 0.0:
+        raise ValueError(f"kl_estimate: δ clamp {delta_clamp} (need b > 0)")
+    if mask is not None and mask.shape != logp.shape:
+        raise AssertionError("rl: mask shape")
+    out = Tensor(logp.shape, "f32")
+    _check(lib().nt_hip_rl_kl_estimate(logp.ptr, ref_logp.ptr, None if mask is None else mask.ptr, logp.numel,
+                                       int(estimator), 0.0 if delta_clamp is None else float(delta_clamp), out.ptr),
+           "kl_estimate")
+    return _reduce(out, mask, reduction)
+
+
+def group_advantages(rewards: Sequence[float], n: int, norm: str = "mean", eps: float = 0.0,
+                     unbiased: bool = True) -> np.ndarray:
+    """rl.rs:436-463, on the host in f64 as the reference computes it. norm: "mean" (MeanOnly)
+    or "std" (GroupNorm::Std{eps, unbiased})."""
+    r = np.asarray(rewards, dtype=np.float64).ravel()
+    if not (n >= 1 and r.size % n == 0):
+        raise ValueError(f"group_advantages: {r.size} rewards in groups of {n}")
+    if norm == "std":
+        if not eps >= 0.0:
+            raise ValueError(f"group_advantages: ε {eps} < 0")
+        if unbiased and n < 2:
+            raise ValueError("group_advantages: the sample standard deviation needs groups of at least 2")
+    out = np.empty_like(r)
+    for g in range(0, r.size, n):
+        grp = r[g:g + n]
+        if grp.min() == grp.max():
+            out[g:g + n] = 0.0
+            continue
+        mean = sum(grp.tolist()) / n
+        scale = 1.0
+        if norm == "std":
+            ss = sum((x - mean) * (x - mean) for x in grp.tolist())
+            scale = math.sqrt(ss / ((n - 1) if unbiased else n)) + eps
+        out[g:g + n] = [(x - mean) / scale for x in grp.tolist()]
+    return out
+
+
+def group_advantages_tensor(rewards: Tensor, norm: str = "mean", eps: float = 0.0, unbiased: bool = True) -> Tensor:
+    """rl.rs:465-469: the last axis grouped; read to the host and written back (same shape)."""
+    n = rewards.shape[-1]
+    adv = group_advantages(rewards.to_f64().ravel(), n, norm, eps, unbiased)
+    return Tensor.from_numpy(adv.reshape(rewards.shape).astype(np.float32), "f32")

@@ -1,0 +1,100 @@
+"""CPU tests of the C ABI: libnoetic_hip.so loads, exports every symbol include/*.h declares,
+fails cleanly without a GPU, and its host-side stream (the sampler's uniforms) equals the
+oracle's restatement of rng::derive / ChaCha20Rng."""
+import ctypes as C
+import glob
+import os
+import re
+import struct
+
+import numpy as np
+import pytest
+
+import noetic_rl as nr
+from oracle import oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"^\s*[A-Za-z_][\w\s\*]*?\b(nt_\w+)\s*\(", text, flags=re.M):
+            names.add(m.group(1))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    names = declared_symbols()
+    assert {"nt_hip_claim", "nt_hip_rl_sample", "nt_hip_rl_score", "nt_rng_derive"} <= names
+    L = C.CDLL(nr.LIB_PATH)
+    missing = [n for n in sorted(names) if not hasattr(L, n)]
+    assert not missing, missing
+    # the Python binding declares a signature for each of them
+    assert names <= set(nr._SIGS), sorted(names - set(nr._SIGS))
+
+
+def test_without_a_claimed_device_calls_fail_cleanly():
+    L = nr.lib()
+    if L.nt_hip_device_count() > 0:
+        pytest.skip("a GPU is visible: the no-device path is not reachable here")
+    assert L.nt_hip_claim(0) != 0
+    assert b"device" in L.nt_hip_last_error().lower()
+    p = C.c_void_p()
+    assert L.nt_hip_alloc(16, C.byref(p)) == -2  # NT_E_UNCLAIMED
+    a = nr.NtRlSampleArgs()
+    assert L.nt_hip_rl_sample(C.byref(a)) == -1  # NT_E_ARG: null logits / rows checked first
+    with pytest.raises(nr.HipUnavailable):
+        nr.claim(0)
+
+
+def test_argument_validation_precedes_the_device():
+    L = nr.lib()
+    a = nr.NtRlSampleArgs(None, nr.NT_BF16, nr.NT_MASK_U8, 4, 16, 16, None, 0, 1.0, None, None, None, None, None)
+    assert L.nt_hip_rl_sample(C.byref(a)) == -1  # a u8 mask kind without a mask
+    assert b"mask" in L.nt_hip_last_error()
+    a = nr.NtRlSampleArgs(None, nr.NT_F32, nr.NT_MASK_NONE, 4, 16, 16, None, 0, -1.0, None, None, None, None, None)
+    assert L.nt_hip_rl_sample(C.byref(a)) == -1
+    assert "temperature" in L.nt_hip_last_error().decode()
+
+
+def test_product_stream_equals_the_oracle_stream():
+    for root, label in [(5, "sampler test"), (0, "x"), (2 ** 63 + 11, "device sampler"), (7, "")]:
+        a, b = nr.Rng(root, label), O.Rng(root, label)
+        assert [a.next_u64() for _ in range(100)] == [b.next_u64() for _ in range(100)]
+        a.next_u32()
+        b.next_u32()
+        assert np.array_equal(a.uniforms(1000), b.uniforms(1000))
+    # from_seed(0) is the RFC 8439 A.1 keystream
+    r = nr.NtRng()
+    assert nr.lib().nt_rng_from_seed(C.byref(r), bytes(32)) == 0
+    words = [nr.lib().nt_rng_next_u32(C.byref(r)) for _ in range(16)]
+    assert struct.pack("<16I", *words).hex().startswith("76b8e0ada0f13d90405d6ae55386bd28")
+    out = C.create_string_buffer(32)
+    nr.lib().nt_sha256(b"abc", 3, out)
+    assert out.raw.hex() == "ba7816bf8f01cfea414140de5dae2223b00361a396177a9cb410ff61f20015ad"
+
+
+def test_runs_mask_generator_host():
+    rows, V = 16, 4096
+    out = np.empty(rows * V, dtype=np.uint8)
+    lab = b"c4/mask"
+    rc = nr.lib().nt_synth_runs_mask_host(out.ctypes.data_as(C.c_void_p), rows, V, 2024, lab, len(lab), 96, 224)
+    assert rc == 0
+    m = out.reshape(rows, V)
+    assert set(np.unique(m)) <= {0, 1} and m.sum(1).min() >= 1
+    frac = m.mean()
+    assert 0.2 < frac < 0.4, frac  # kept runs of mean 96 between gaps of mean 224: about 30%
+    out2 = np.empty_like(out)
+    nr.lib().nt_synth_runs_mask_host(out2.ctypes.data_as(C.c_void_p), rows, V, 2024, lab, len(lab), 96, 224)
+    assert np.array_equal(out, out2)
+
+
+def test_python_mirror_refuses_like_the_reference_without_a_device():
+    with pytest.raises(ValueError, match="temperature"):
+        nr.tempered_logits(None, 0.0, None)
+    with pytest.raises(ValueError, match="at least 2"):
+        nr.group_advantages([1.0, 2.0], 1, "std", 1e-6, True)
+    assert nr.group_advantages([1, 0, 0, 1, 2, 2, 2, 2], 4).tolist() == [0.5, -0.5, -0.5, 0.5, 0, 0, 0, 0]

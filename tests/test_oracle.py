@@ -1,0 +1,364 @@
+"""CPU tests that pin the oracle (oracle/oracle.c) before it is trusted as the checker.
+
+Each oracle function is checked against something other than its own formula: the reference's
+known-answer tests (src/hash.rs:33-36, src/nn/tests/rl.rs), textbook vectors (RFC 8439),
+independent library routines (hashlib, scipy, numpy's IEEE f32 arithmetic), closed forms,
+invariants, and brute force on tiny inputs.
+"""
+import hashlib
+import json
+import math
+import os
+import struct
+
+import numpy as np
+import pytest
+from scipy.special import log_softmax
+
+from oracle import oracle as O
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+NINF = float("-inf")
+
+
+def f32(x):
+    return np.asarray(x, dtype=np.float32)
+
+
+def assert_close(what, ours, theirs, tol):
+    """|a - b| <= tol * (1 + |b|) (src/nn/tests/mod.rs:104-109)."""
+    ours, theirs = np.asarray(ours, dtype=np.float64), np.asarray(theirs, dtype=np.float64)
+    assert ours.shape == theirs.shape, what
+    bad = ~(np.abs(ours - theirs) <= tol * (1.0 + np.abs(theirs)))
+    both_inf = np.isinf(ours) & np.isinf(theirs) & (np.sign(ours) == np.sign(theirs))
+    bad &= ~both_inf
+    assert not bad.any(), f"{what}: {ours[bad][:4]} vs {theirs[bad][:4]}"
+
+
+# ------------------------------------------------------------------------ SHA-256, ChaCha20
+
+def test_sha256_known_vectors():
+    # src/hash.rs:33-36
+    assert O.sha256(b"").hex() == "e3b0c44298fc1c149afbf4c8996fb92427ae41e4649b934ca495991b7852b855"
+    assert O.sha256(b"abc").hex() == "ba7816bf8f01cfea414140de5dae2223b00361a396177a9cb410ff61f20015ad"
+    rng = np.random.default_rng(1)
+    for n in (1, 55, 56, 63, 64, 65, 119, 120, 128, 1000):
+        data = rng.integers(0, 256, n, dtype=np.uint8).tobytes()
+        assert O.sha256(data) == hashlib.sha256(data).digest(), n
+
+
+# RFC 8439 Appendix A.1, test vectors #1 (counter 0) and #2 (counter 1): all-zero key and nonce.
+TV1 = bytes.fromhex("76b8e0ada0f13d90405d6ae55386bd28bdd219b8a08ded1aa836efcc8b770dc7"
+                    "da41597c5157488d7724e03fb8d84a376a43b8f41518a11cc387b669b2ee6586")
+TV2_HEAD = bytes.fromhex("9f07e7be5551387a98ba977c732d080d")
+
+
+def test_chacha20_rfc8439_vectors():
+    b0 = struct.pack("<16I", *O.chacha_block([0] * 8, 0))
+    b1 = struct.pack("<16I", *O.chacha_block([0] * 8, 1))
+    assert b0 == TV1
+    assert b1[:16] == TV2_HEAD
+
+
+def test_rng_derive_is_sha256_seeded_chacha():
+    # rng::derive(root, label) = ChaCha20Rng::from_seed(SHA-256(root_le || label)) (src/rng.rs:9-17)
+    root, label = 5, "sampler test"
+    seed = hashlib.sha256(struct.pack("<Q", root) + label.encode()).digest()
+    key = list(struct.unpack("<8I", seed))
+    r = O.Rng(root, label)
+    words = [r.next_u32() for _ in range(40)]
+    blocks = O.chacha_block(key, 0) + O.chacha_block(key, 1) + O.chacha_block(key, 2)
+    assert words == blocks[:40]
+    # next_u64 = lo | hi << 32 of the next two words, also across a block boundary after an odd
+    # number of u32 draws (rand_core BlockRng).
+    r1, r2 = O.Rng(root, label), O.Rng(root, label)
+    r1.next_u32()
+    r2.next_u32()
+    w = [r2.next_u32() for _ in range(40)]
+    u = [r1.next_u64() for _ in range(20)]
+    assert u == [w[2 * i] | (w[2 * i + 1] << 32) for i in range(20)]
+
+
+def test_uniform_mapping_endpoints():
+    # u = ((k >> 11) + 0.5) / 2^53 (rl.rs:490-498). The reference calls it the open interval
+    # (0, 1), but for k >> 11 = 2^53 - 1 the f64 sum 2^53 - 0.5 rounds (ties to even) to 2^53,
+    # so u = 1.0 exactly with probability 2^-53; the inverse-CDF sampler then takes its "no
+    # crossing" branch (the last token with weight).
+    assert O.uniform_open01(0) == 0.5 / 2 ** 53
+    assert O.uniform_open01(2 ** 64 - 1) == 1.0
+    assert O.uniform_open01((2 ** 53 - 2) << 11) == (2 ** 53 - 1.5) / 2 ** 53 < 1.0
+    z = f32([[0.0, 1.0, NINF, 2.0, NINF]])
+    ids, _ = O.sample_invcdf(z, [1.0])
+    assert ids[0] == 3
+    assert O.uniform_open01(1 << 63) == 0.5 + 0.5 / 2 ** 53
+
+
+def test_box_muller_normals_are_standard():
+    z = O.Rng(9, "normals").normals(200_000)
+    assert abs(z.mean()) < 0.01 and abs(z.std() - 1.0) < 0.01
+    # the Box-Muller convention: u1 = gen_f64 (max 1e-300), u2 = gen_f64, cos branch
+    r, s = O.Rng(9, "normals"), O.Rng(9, "normals")
+    g = s.gen_f64(2)
+    assert r.normals(1)[0] == math.sqrt(-2.0 * math.log(max(g[0], 1e-300))) * math.cos(2.0 * math.pi * g[1])
+
+
+# ------------------------------------------------------------------------ bf16
+
+def test_bf16_round_to_nearest_even():
+    rng = np.random.default_rng(3)
+    bits = rng.integers(0, 2 ** 32, 200_000, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    x = x[np.isfinite(x)]
+    h = O.bf16_from_f32(x)
+    # brute force: the nearest of the two bf16 neighbours, ties to the even one
+    lo = (x.view(np.uint32) & 0xFFFF0000).view(np.float32)
+    hi_bits = (x.view(np.uint32).astype(np.uint64) & 0xFFFF0000) + 0x10000
+    for i in range(2000):
+        xi = float(x[i])
+        cands = [int(x[i].view(np.uint32) >> 16), int(hi_bits[i] >> 16) & 0xFFFF]
+        vals = [float(O.bf16_to_f32(np.uint16(c))) for c in cands]
+        d = [abs(v - xi) if math.isfinite(v) else math.inf for v in vals]
+        if d[0] < d[1]:
+            want = cands[0]
+        elif d[1] < d[0]:
+            want = cands[1]
+        else:
+            want = cands[0] if cands[0] % 2 == 0 else cands[1]
+        assert int(h[i]) == want, (xi, h[i], cands)
+    # the vectorised form equals the scalar C restatement (half.rs:16-23), NaN included
+    special = f32([0.0, -0.0, 1.0, -1.0, np.inf, -np.inf, np.nan, 3.4e38, 1e-40, 1.00390625, 1.01171875])
+    for v in list(special) + list(x[:500]):
+        assert int(O.bf16_from_f32(f32([v]))[0]) == O.bf16_from_f32_scalar(float(v))
+    assert np.all(O.bf16_to_f32(O.bf16_from_f32(lo)) == lo)
+
+
+# ------------------------------------------------------------------------ row oracle
+
+def test_tempered_logits_are_f32_divide_then_add():
+    rng = np.random.default_rng(4)
+    x = f32(rng.normal(0, 3, (3, 50)))
+    add = f32(rng.normal(0, 1, (1, 50)))
+    for tau in (0.7, 1.0, 2.5):
+        z = O.tempered(x, tau, addmask=add)
+        want = (x if tau == 1.0 else x / np.float32(tau)) + add  # numpy: IEEE f32 divide and add
+        assert np.array_equal(z, want)
+    keep = np.array([[1, 0] * 25], dtype=np.uint8)
+    z = O.tempered(x, 0.8, keep=keep)
+    assert np.all(np.isneginf(z[:, 1::2])) and np.array_equal(z[:, 0::2], x[:, 0::2] / np.float32(0.8))
+
+
+def test_log_probs_entropy_kl_match_scipy():
+    rng = np.random.default_rng(5)
+    for V in (1, 2, 7, 64, 1000):
+        z = f32(rng.normal(0, 3, (6, V)))
+        r = f32(z + rng.normal(0, 0.5, (6, V)))
+        ls = log_softmax(z.astype(np.float64), axis=1)
+        lr = log_softmax(r.astype(np.float64), axis=1)
+        tok = rng.integers(0, V, 6)
+        assert_close("logp", O.token_logp(z, tok), ls[np.arange(6), tok], 1e-13)
+        assert_close("entropy", O.entropy(z), -(np.exp(ls) * ls).sum(1), 1e-12)
+        assert_close("kl", O.kl(z, r), (np.exp(ls) * (ls - lr)).sum(1), 1e-12)
+        assert np.all(O.kl(z, r) >= -1e-15)
+        assert np.all(np.abs(O.kl(z, z)) < 1e-15)  # KL(π ‖ π) = 0 (tests/rl.rs:363)
+
+
+def test_reference_known_answers_large_and_excluded():
+    # tests/rl.rs:134-150: ±1e4 logits stay finite; a −∞ token gives −∞
+    lp = O.token_logp(f32([[1e4, -1e4, 0.0, 1e3], [-1e4, -1e4, 1e4, 1e4]]), [0, 2])
+    assert abs(lp[0]) < 1e-6 and abs(lp[1] - math.log(0.5)) < 1e-6
+    row = f32([[1.0, NINF, 0.0, 2.0]] * 2)
+    lp = O.token_logp(row, [1, 3])
+    assert lp[0] == NINF
+    assert abs(lp[1] - log_softmax([1.0, 0.0, 2.0])[2]) < 1e-12
+    # tests/rl.rs:392-407: −∞ entries give the KL / entropy of the kept tokens
+    p = f32([[1.0, NINF, 0.5, -1.0], [2.0, 0.0, NINF, NINF]])
+    q = f32([[0.0, NINF, 1.5, 0.5], [-1.0, 1.0, NINF, NINF]])
+    assert_close("kl kept", O.kl(p, q), [O.kl(p[:1, [0, 2, 3]], q[:1, [0, 2, 3]])[0], O.kl(p[1:, :2], q[1:, :2])[0]], 1e-15)
+    assert_close("entropy kept", O.entropy(p), [O.entropy(p[:1, [0, 2, 3]])[0], O.entropy(p[1:, :2])[0]], 1e-15)
+    # uniform entropy = ln V (tests/rl.rs:369-370)
+    assert_close("uniform", O.entropy(f32([[0.3] * 5])), [math.log(5)], 1e-15)
+    # π > 0 where π_ref = 0 gives +∞ (tests/rl.rs:420-421)
+    assert O.kl(f32([[0.0, 0.0]]), f32([[0.0, NINF]]))[0] == math.inf
+    # one-sided −1e9 gives about 1e9 · p₂ (tests/rl.rs:807-811)
+    one = f32([[0.0, 0.5, 1.0]])
+    p2 = math.exp(log_softmax([0.0, 0.5, 1.0])[2])
+    k = O.kl(one, one + f32([[0.0, 0.0, -1e9]]))[0]
+    assert abs(k / (1e9 * p2) - 1.0) < 1e-6
+    # rows refused by the sampler: every entry −∞, or a NaN (rl.rs:516-519)
+    assert O.row_stats(f32([NINF, NINF])).status == 1
+    assert O.row_stats(f32([0.0, np.nan, 1.0])).status == 2
+    # first maximum, NaN-propagating (kernels.rs:184-209)
+    assert O.row_stats(f32([1.0, 3.0, 3.0, 2.0])).argmax == 1
+    assert O.row_stats(f32([1.0, np.nan, 5.0])).argmax == 1
+
+
+# ------------------------------------------------------------------------ inverse-CDF sampler
+
+def _numpy_invcdf(z, u):
+    """The same definition by an independent route: f64 weights, cumsum, searchsorted."""
+    m = np.max(z.astype(np.float64))
+    w = np.exp(z.astype(np.float64) - m)
+    c = np.cumsum(w)
+    i = int(np.searchsorted(c, u * c[-1], side="right"))
+    return i if i < len(z) else int(np.nonzero(w > 0)[0][-1])
+
+
+def test_invcdf_matches_brute_force_on_tiny_rows():
+    with open(os.path.join(HERE, "golden", "tiny_invcdf.json")) as f:
+        fx = json.load(f)
+    grid = np.arange(1, 1000) / 1000.0
+    for case in fx["cases"]:
+        x = np.frombuffer(bytes.fromhex(case["logits_f32_hex"]), dtype=np.float32)
+        keep = np.array(case["keep_u8"], dtype=np.uint8)
+        z = O.tempered(x[None, :], case["temperature"], keep=keep[None, :])
+        ids, edges = O.sample_invcdf(np.repeat(z, grid.size, 0), grid)
+        assert ids.tolist() == case["ids_on_grid"], "oracle drifted from the committed fixture"
+        for u, i, e in zip(grid, ids, edges):
+            if e > 1e-12:  # away from floating ties, cumsum order is the same
+                assert i == _numpy_invcdf(z[0], u)
+            assert keep[i] == 1, "an excluded token was drawn"
+        # the step function: token v is drawn on an interval of length p_v
+        p = np.exp(log_softmax(z[0].astype(np.float64)))
+        counts = np.bincount(ids, minlength=len(x)) / grid.size
+        assert np.all(np.abs(counts - p) <= 2.0 / grid.size + 1e-12)
+
+
+def test_invcdf_frequencies_match_the_distribution():
+    # the reference's frequency test (tests/rl.rs:579-611): 40,000 draws within 4.5 s.e.
+    row = f32([0.4, -1.0, 1.2, 3.0, 0.0, -0.3])
+    maskrow = f32([0.0, 0.0, 0.0, NINF, 0.5, 0.0])
+    n = 40_000
+    for tau in (0.7, 1.0, 2.5):
+        z = O.tempered(row[None, :], tau, addmask=maskrow[None, :])
+        u = O.Rng(5, "sampler test").uniforms(n)
+        ids, _ = O.sample_invcdf(np.repeat(z, n, 0), u)
+        p = np.exp(log_softmax((row.astype(np.float64) / tau) + maskrow))
+        cnt = np.bincount(ids, minlength=6)
+        assert cnt[3] == 0, "excluded token drawn"
+        f = cnt / n
+        se = np.sqrt(p * (1 - p) / n)
+        assert np.all(np.abs(f - p) <= 4.5 * se + 1e-12), (tau, f, p)
+
+
+def test_argmax_is_first_and_greedy_picks_masked_argmax():
+    # tests/rl.rs:617-625: τ = 0 is the argmax of the masked logits (token 4)
+    row = f32([0.4, -1.0, 1.2, 3.0, 0.0, -0.3])
+    z = O.tempered(row[None, :], 1.0, addmask=f32([[0.0, 0.0, 0.0, NINF, 2.0, 0.0]]))
+    assert O.argmax_first(z)[0] == 4
+
+
+# ------------------------------------------------------------------------ estimators, reductions
+
+def test_kl_estimators_closed_forms_and_enumeration():
+    # δ = 100: clamped k3 = exp(20) − 21 (tests/rl.rs:753-768); masked positions give 0
+    k = O.kl_estimate([-100.5, -1.0], [-0.5, -1.2], 3, clamp=20.0)
+    assert abs(k[0] - (math.exp(20.0) - 21.0)) <= 1e-12 * k[0]
+    assert abs(k[1] - (math.exp(-0.2) + 0.2 - 1.0)) < 1e-15
+    assert O.kl_estimate([-1.0], [-3.0], 1, mask=[0.0])[0] == 0.0
+    assert O.kl_estimate([-1.0], [-3.0], 2)[0] == 2.0
+    # E_π[k1] = E_π[k3] = KL(π ‖ π_ref) by enumeration (tests/rl.rs:467-500)
+    rng = np.random.default_rng(6)
+    V = 6
+    pl, rl = f32(rng.uniform(-2, 2, V)), f32(rng.uniform(-2, 2, V))
+    lp, lr = log_softmax(pl.astype(np.float64)), log_softmax(rl.astype(np.float64))
+    pi = np.exp(lp)
+    kl = O.kl(pl[None, :], rl[None, :])[0]
+    for est in (1, 3):
+        assert abs(float((O.kl_estimate(lp, lr, est) * pi).sum()) - kl) < 1e-14
+    assert np.all(O.kl_estimate(lp, lr, 2) >= 0) and np.all(O.kl_estimate(lp, lr, 3) >= 0)
+
+
+def test_reductions_by_hand():
+    # tests/rl.rs:163-179: per-token [1 2 0; 0 −10 0], mask [1 1 0; 0 1 0]
+    per = [1.0, 2.0, 0.0, 0.0, -10.0, 0.0]
+    m = [1.0, 1.0, 0.0, 0.0, 1.0, 0.0]
+    sh = (1, 2, 3)
+    assert O.reduce_tokens(per, m, sh, "sum").tolist() == [-7.0]
+    assert abs(O.reduce_tokens(per, m, sh, "token_mean")[0] + 7.0 / 3.0) < 1e-15
+    assert O.reduce_tokens(per, m, sh, "per_sequence").tolist() == [1.5, -10.0]
+    assert O.reduce_tokens(per, m, sh, "sequence_mean").tolist() == [-4.25]
+    assert O.reduce_tokens(per, m, sh, "none").tolist() == per
+    # every position masked: exact zeros (tests/rl.rs:506-545)
+    z = [0.0] * 6
+    for red in ("sum", "token_mean", "per_sequence", "sequence_mean"):
+        assert np.all(O.reduce_tokens(z, z, sh, red) == 0.0)
+
+
+def test_group_advantages_by_hand():
+    # tests/rl.rs:550-569
+    r = [1.0, 0.0, 0.0, 1.0, 2.0, 2.0, 2.0, 2.0, 0.0, 0.0, 0.0, 3.0]
+    s3 = 0.5 / math.sqrt(1.0 / 3.0)
+    assert_close("unbiased", O.group_advantages(r, 4, "std", 0.0, True),
+                 [s3, -s3, -s3, s3, 0, 0, 0, 0, -0.5, -0.5, -0.5, 1.5], 1e-15)
+    p3 = math.sqrt(1.6875)
+    assert_close("population", O.group_advantages(r, 4, "std", 0.0, False),
+                 [1, -1, -1, 1, 0, 0, 0, 0, -0.75 / p3, -0.75 / p3, -0.75 / p3, 2.25 / p3], 1e-15)
+    assert O.group_advantages(r, 4, "mean").tolist() == [0.5, -0.5, -0.5, 0.5, 0, 0, 0, 0, -0.75, -0.75, -0.75, 2.25]
+    assert_close("eps", O.group_advantages(r, 4, "std", 1e-2, True)[8:], [-0.75 / 1.51] * 3 + [2.25 / 1.51], 1e-15)
+    assert O.group_advantages([3.0, -1.0], 1, "std", 1e-6, False).tolist() == [0.0, 0.0]
+    # equal rewards give exact zeros at ε = 0 (tests/rl.rs:644-653)
+    a = O.group_advantages([0.1, 0.1, 0.1, 1.0, 0.0, 0.0], 3, "std", 0.0, True)
+    assert a[:3].tolist() == [0.0, 0.0, 0.0] and a[3] > 0 > a[4] and a[4] == a[5]
+    with pytest.raises(ValueError):
+        O.group_advantages([1.0, 2.0], 1, "std", 1e-6, True)  # tests/rl.rs:571-575
+
+
+# ------------------------------------------------------------------------ Cpu(Reference) restatement
+
+def test_cpuref_log_softmax_in_f32():
+    rng = np.random.default_rng(8)
+    x = f32(rng.normal(0, 4, (5, 333)))
+    y = O.cpuref_log_softmax(x)
+    assert_close("cpuref log_softmax", y, log_softmax(x.astype(np.float64), axis=1), 1e-6)
+    # the 8-partial order is exact on small integers
+    v = f32(np.arange(1, 20))
+    assert O.unrolled_sum(v) == float(v.sum())
+
+
+def test_cpuref_gumbel_sampler_frequencies_and_consumption():
+    row = f32([0.4, -1.0, 1.2, 3.0, 0.0, -0.3])
+    keep = np.array([[1, 1, 1, 0, 1, 1]], dtype=np.uint8)
+    n, tau = 20_000, 0.7
+    rng = O.Rng(5, "gumbel")
+    ids, lp = O.cpuref_sample_logp(np.repeat(row[None, :], n, 0), tau, keep, rng)
+    # the stream advanced one u64 per logit (tests/rl.rs:596-599)
+    copy = O.Rng(5, "gumbel")
+    for _ in range(n * 6):
+        copy.next_u64()
+    assert rng.next_u64() == copy.next_u64()
+    z = np.where(keep[0] == 1, row.astype(np.float64) / tau, -np.inf)
+    p = np.exp(log_softmax(z))
+    cnt = np.bincount(ids, minlength=6)
+    assert cnt[3] == 0
+    se = np.sqrt(p * (1 - p) / n)
+    assert np.all(np.abs(cnt / n - p) <= 4.5 * se + 1e-12)
+    assert_close("gumbel logp", lp, np.log(p[ids]), 1e-6)
+    with pytest.raises(ValueError, match="no allowed token"):
+        O.cpuref_sample_logp(f32(np.zeros((2, 3))), 1.0, np.array([[1, 1, 1], [0, 0, 0]], dtype=np.uint8),
+                             O.Rng(0, "x"))
+
+
+# ------------------------------------------------------------------------ golden C1 fixture
+
+def test_c1_golden_fixture():
+    with open(os.path.join(HERE, "golden", "c1_readme.json")) as f:
+        fx = json.load(f)
+    S, B, T, V = fx["shape"]
+    x = np.stack([np.frombuffer(bytes.fromhex(h), dtype=np.float32) for h in fx["logits_f32_hex"]])
+    keep = np.array(fx["keep_u8"], dtype=np.uint8)
+    u = np.array(fx["uniforms"])
+    assert x.shape == (S * B * T, V) and keep.min(axis=1).min() >= 0 and keep.sum(axis=1).min() >= 1
+    # the fixture's inputs come from the seeded streams it names
+    from tests.golden.make_golden import c1_inputs
+    _, x2, keep2, u2 = c1_inputs()
+    assert np.array_equal(x, x2) and np.array_equal(keep, keep2) and np.array_equal(u, u2)
+    z = O.tempered(x, 1.0, keep=keep)
+    ids, edges = O.sample_invcdf(z, u)
+    assert ids.tolist() == fx["ids"]
+    # independent check of the expected values: scipy's log_softmax over the kept tokens
+    ls = log_softmax(np.where(keep == 1, x.astype(np.float64), -np.inf), axis=1)
+    assert_close("c1 logp", fx["logp"], ls[np.arange(len(ids)), ids], 1e-13)
+    ent = -np.where(keep == 1, np.exp(ls) * np.where(keep == 1, ls, 0.0), 0.0).sum(1)
+    assert_close("c1 entropy", fx["entropy"], ent, 1e-13)
+    for i, row_id in enumerate(ids):
+        assert row_id == _numpy_invcdf(z[i], u[i])
