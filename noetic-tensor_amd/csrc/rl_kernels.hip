@@ -324,7 +324,9 @@ __global__ __launch_bounds__(1024) void k_sample(SampleP p) {
         cstar = l >= 0 ? __shfl(mine, l, kWave) : -1;
     } else {
         const double t = p.u[row] * S;
-        const double excl = (lane == 0) ? 0.0 : __shfl_up(incl, 1, kWave);
+        // Every lane runs the shuffle: a disabled source lane would read as 0.
+        const double prev = __shfl_up(incl, 1, kWave);
+        const double excl = (lane == 0) ? 0.0 : prev;
         // Only a lane that holds weight can contain the crossing (a zero-weight lane's
         // inclusive sum may round above its neighbour's in the scan tree).
         int l = first_lane(__ballot(incl > t && lsum > 0.0));
@@ -394,7 +396,8 @@ __global__ __launch_bounds__(1024) void k_sample(SampleP p) {
             ls += double(w[j]);
         }
         const double incl2 = wave_scan_d(ls, lane);
-        const double excl2 = (lane == 0) ? 0.0 : __shfl_up(incl2, 1, kWave);
+        const double prev2 = __shfl_up(incl2, 1, kWave);
+        const double excl2 = (lane == 0) ? 0.0 : prev2;
         int mine = -1;
         int lastj = -1;
 #pragma unroll
@@ -467,42 +470,53 @@ struct ScoreP {
     uint8_t *status;
 };
 
-// Running log-sum-exp state of one lane (value space, exponent scale c).
-struct Lse {
-    float a;  // max so far
-    float S;  // sum exp2((v - a) c)
-    float H;  // sum w (v - a) c            (entropy)
-    float B;  // sum w (v - v_ref)          (exact KL)
+// Running state of one lane (value space, exponent scale c). Every sum is relative to the
+// lane's running maxima, so no term cancels against another of size |logit|:
+//   S  = sum w,                 w = exp2((v - a) c)
+//   H  = sum w (v - a) c                                  (entropy)
+//   B  = sum w ((v - a) - (v_ref - a_ref)) c              (exact KL)
+//   Sr = sum exp2((v_ref - a_ref) c)                      (reference normaliser)
+struct RowState {
+    float a, S, H, B;
+    float ar, Sr;
 };
 
-__device__ __forceinline__ void lse_rescale(Lse &s, float an, float c, bool ent, bool kl) {
-    const float sh = (an == -INFINITY) ? 0.0f : an;
-    const float dd = (s.a - sh) * c;
-    const float f = exp2_hw(dd);
-    if (ent) s.H = f * (s.H + fmaxf(dd, -FLT_MAX) * s.S);
-    s.S = f * s.S;
-    if (kl) s.B = f * s.B;
-    s.a = an;
+__device__ __forceinline__ float shift_of(float a) { return a == -INFINITY ? 0.0f : a; }
+
+// The B update when the maxima move by d = (a_old - a_new) c and e = (a_ref_old - a_ref_new) c:
+// B' = f (B + (d - e) S). A state with S == 0 holds no policy term.
+__device__ __forceinline__ float b_rescaled(float B, float S, float f, float d, float e) {
+    return S > 0.0f ? f * (B + (d - e) * S) : 0.0f;
 }
 
 // Merge state o into s (the same arithmetic whichever side is s).
-__device__ __forceinline__ void lse_merge(Lse &s, const Lse &o, float c, bool ent, bool kl) {
-    const float an = fmaxf(s.a, o.a);
-    const float sh = (an == -INFINITY) ? 0.0f : an;
+template <bool REF, bool KL, bool ENT>
+__device__ __forceinline__ void state_merge(RowState &s, const RowState &o, float c) {
+    const float an = fmaxf(s.a, o.a), sh = shift_of(an);
     const float d1 = (s.a - sh) * c, d2 = (o.a - sh) * c;
     const float f1 = exp2_hw(d1), f2 = exp2_hw(d2);
-    if (ent) s.H = f1 * (s.H + fmaxf(d1, -FLT_MAX) * s.S) + f2 * (o.H + fmaxf(d2, -FLT_MAX) * o.S);
+    float e1 = 0.0f, e2 = 0.0f;
+    if constexpr (REF) {
+        const float anr = fmaxf(s.ar, o.ar), shr = shift_of(anr);
+        e1 = (s.ar - shr) * c;
+        e2 = (o.ar - shr) * c;
+        s.Sr = exp2_hw(e1) * s.Sr + exp2_hw(e2) * o.Sr;
+        s.ar = anr;
+    }
+    if constexpr (ENT) s.H = f1 * (s.H + fmaxf(d1, -FLT_MAX) * s.S) + f2 * (o.H + fmaxf(d2, -FLT_MAX) * o.S);
+    if constexpr (KL) s.B = b_rescaled(s.B, s.S, f1, d1, e1) + b_rescaled(o.B, o.S, f2, d2, e2);
     s.S = f1 * s.S + f2 * o.S;
-    if (kl) s.B = f1 * s.B + f2 * o.B;
     s.a = an;
 }
 
-__device__ __forceinline__ Lse shfl_down_lse(const Lse &s, int o) {
-    Lse r;
+__device__ __forceinline__ RowState shfl_down_state(const RowState &s, int o) {
+    RowState r;
     r.a = __shfl_down(s.a, o, kWave);
     r.S = __shfl_down(s.S, o, kWave);
     r.H = __shfl_down(s.H, o, kWave);
     r.B = __shfl_down(s.B, o, kWave);
+    r.ar = __shfl_down(s.ar, o, kWave);
+    r.Sr = __shfl_down(s.Sr, o, kWave);
     return r;
 }
 
@@ -511,119 +525,120 @@ constexpr int kScoreWaves = kScoreThreads / kWave;
 
 template <int DT, int MK, bool REF, bool KL, bool ENT, bool AL>
 __global__ __launch_bounds__(kScoreThreads) void k_score(ScoreP p) {
-    __shared__ Lse wp[kScoreWaves], wr[kScoreWaves];
+    __shared__ RowState ws[kScoreWaves];
     const int64_t row = blockIdx.x;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int nw = blockDim.x / kWave;
     const bool tau_one = p.tau_one != 0;
+    const float c = p.c;
     const void *xrow = static_cast<const char *>(p.logits) + row * p.ld * Elem<DT>::kBytes;
     const void *yrow = nullptr;
     if constexpr (REF) yrow = static_cast<const char *>(p.ref) + row * p.ld * Elem<DT>::kBytes;
     const void *mrow = nullptr;
     if constexpr (MK != NT_MASK_NONE) mrow = static_cast<const char *>(p.mask) + row * p.mask_ld * MaskWords<MK>::kBytes;
 
-    Lse sp{-INFINITY, 0.0f, 0.0f, 0.0f}, sr{-INFINITY, 0.0f, 0.0f, 0.0f};
+    RowState st{-INFINITY, 0.0f, 0.0f, 0.0f, -INFINITY, 0.0f};
     for (int c0 = wave; c0 < p.nc; c0 += nw * kBatch) {
         Raw<DT, MK> rx[kBatch];
         Raw<DT, NT_MASK_NONE> ry[REF ? kBatch : 1];
 #pragma unroll
         for (int b = 0; b < kBatch; b++) {
-            const int c = c0 + b * nw;
-            const int64_t e0 = c < p.nc ? int64_t(c) * kChunk + lane * kEpl : p.V;
+            const int ch = c0 + b * nw;
+            const int64_t e0 = ch < p.nc ? int64_t(ch) * kChunk + lane * kEpl : p.V;
             load_raw<DT, MK, AL>(rx[b], xrow, mrow, e0, p.V);
             if constexpr (REF) load_raw<DT, NT_MASK_NONE, AL>(ry[b], yrow, nullptr, e0, p.V);
         }
 #pragma unroll
         for (int b = 0; b < kBatch; b++) {
-            const int c = c0 + b * nw;
-            if (c < p.nc) {
-            float v[kEpl];
-            decode<DT, MK>(rx[b], v, p.tau, tau_one);
-            float vr[kEpl];
-            if constexpr (REF) {
+            const int ch = c0 + b * nw;
+            if (ch < p.nc) {
+                float v[kEpl], vr[kEpl];
+                decode<DT, MK>(rx[b], v, p.tau, tau_one);
                 // The reference logits take the same temperature and vocabulary mask
                 // (reference_kl, rl.rs:347-351).
-                decode_words<DT, MK>(ry[b].x, rx[b].m, vr, p.tau, tau_one);
-            }
-            lse_rescale(sp, fmaxf(sp.a, max8(v)), p.c, ENT, KL);
-            {
-                const float sh = (sp.a == -INFINITY) ? 0.0f : sp.a;
-                float w[kEpl], h[kEpl], bb[kEpl];
+                if constexpr (REF) decode_words<DT, MK>(ry[b].x, rx[b].m, vr, p.tau, tau_one);
+                // Move the running maxima to this chunk's, rescaling the sums (online LSE).
+                const float an = fmaxf(st.a, max8(v)), sh = shift_of(an);
+                const float dold = (st.a - sh) * c;
+                const float f = exp2_hw(dold);
+                float eold = 0.0f, shr = 0.0f;
+                if constexpr (REF) {
+                    const float anr = fmaxf(st.ar, max8(vr));
+                    shr = shift_of(anr);
+                    eold = (st.ar - shr) * c;
+                    st.Sr = exp2_hw(eold) * st.Sr;
+                    st.ar = anr;
+                }
+                if constexpr (ENT) st.H = f * (st.H + fmaxf(dold, -FLT_MAX) * st.S);
+                if constexpr (KL) st.B = b_rescaled(st.B, st.S, f, dold, eold);
+                st.S = f * st.S;
+                st.a = an;
+                float w[kEpl], h[kEpl], bb[kEpl], wr[kEpl];
 #pragma unroll
                 for (int j = 0; j < kEpl; j++) {
-                    const float d = (v[j] - sh) * p.c;
+                    const float d = (v[j] - sh) * c;
                     w[j] = exp2_hw(d);
                     if constexpr (ENT) h[j] = w[j] * fmaxf(d, -FLT_MAX);
-                    if constexpr (KL) bb[j] = w[j] * fmaxf(v[j] - vr[j], -FLT_MAX);
+                    if constexpr (REF) {
+                        const float e = (vr[j] - shr) * c;
+                        wr[j] = exp2_hw(e);
+                        if constexpr (KL) bb[j] = w[j] * fmaxf(d - e, -FLT_MAX);
+                    }
                 }
-                sp.S += tree8(w);
-                if constexpr (ENT) sp.H += tree8(h);
-                if constexpr (KL) sp.B += tree8(bb);
-            }
-            if constexpr (REF) {
-                lse_rescale(sr, fmaxf(sr.a, max8(vr)), p.c, false, false);
-                const float sh = (sr.a == -INFINITY) ? 0.0f : sr.a;
-                float w[kEpl];
-#pragma unroll
-                for (int j = 0; j < kEpl; j++) w[j] = exp2_hw((vr[j] - sh) * p.c);
-                sr.S += tree8(w);
-            }
+                st.S += tree8(w);
+                if constexpr (ENT) st.H += tree8(h);
+                if constexpr (KL) st.B += tree8(bb);
+                if constexpr (REF) st.Sr += tree8(wr);
             }
         }
     }
     // Wave tree (lane i takes lane i + o), then the waves in order.
 #pragma unroll
     for (int o = kWave / 2; o > 0; o >>= 1) {
-        const Lse t = shfl_down_lse(sp, o);
-        if (lane < o) lse_merge(sp, t, p.c, ENT, KL);
-        if constexpr (REF) {
-            const Lse u = shfl_down_lse(sr, o);
-            if (lane < o) lse_merge(sr, u, p.c, false, false);
-        }
+        const RowState t = shfl_down_state(st, o);
+        if (lane < o) state_merge<REF, KL, ENT>(st, t, c);
     }
-    if (lane == 0) {
-        wp[wave] = sp;
-        if constexpr (REF) wr[wave] = sr;
-    }
+    if (lane == 0) ws[wave] = st;
     __syncthreads();
     if (threadIdx.x != 0) return;
 
     // Finish the row in f64.
-    auto finish = [&](const Lse *w, double &a_out, double &S_out, double &H_out, double &B_out) {
-        float a = -INFINITY;
-        for (int i = 0; i < nw; i++) a = fmaxf(a, w[i].a);
-        double S = 0.0, H = 0.0, B = 0.0;
-        for (int i = 0; i < nw; i++) {
-            if (w[i].a == -INFINITY) continue;
-            const double d = double(w[i].a - a) * double(p.c);
+    float af = -INFINITY, arf = -INFINITY;
+    for (int i = 0; i < nw; i++) {
+        af = fmaxf(af, ws[i].a);
+        arf = fmaxf(arf, ws[i].ar);
+    }
+    double S = 0.0, H = 0.0, B = 0.0, Sr = 0.0;
+    for (int i = 0; i < nw; i++) {
+        if (ws[i].S > 0.0f) {
+            const double d = double(ws[i].a - af) * double(c);
             const double f = exp2(d);
-            S += f * double(w[i].S);
-            if (ENT) H += f * (double(w[i].H) + d * double(w[i].S));
-            if (KL) B += f * double(w[i].B);
+            S += f * double(ws[i].S);
+            if (ENT) H += f * (double(ws[i].H) + d * double(ws[i].S));
+            if (KL) {
+                const double e = ws[i].ar == -INFINITY ? -INFINITY : double(ws[i].ar - arf) * double(c);
+                B += f * (double(ws[i].B) + (d - e) * double(ws[i].S));
+            }
+        } else if (!(ws[i].S == ws[i].S)) {
+            S = NAN;
         }
-        a_out = a;
-        S_out = S;
-        H_out = H;
-        B_out = B;
-    };
-    double ap, Sp, Hp, Bp;
-    finish(wp, ap, Sp, Hp, Bp);
-    const float apf = float(ap);
-    int st = NT_ROW_OK;
-    if (apf == -INFINITY) st = NT_ROW_NO_TOKEN;
-    else if (!(Sp == Sp)) st = NT_ROW_NAN;
-    const double lnSp = log(Sp);
+        if (REF && ws[i].ar != -INFINITY) Sr += exp2(double(ws[i].ar - arf) * double(c)) * double(ws[i].Sr);
+    }
+    int stt = NT_ROW_OK;
+    if (af == -INFINITY) stt = NT_ROW_NO_TOKEN;
+    else if (!(S == S)) stt = NT_ROW_NAN;
+    const double lnS = log(S);
     // The value-space max as the reference's f32 max of the tempered logits.
     auto zmax = [&](float a) -> float {
         if constexpr (MK != NT_MASK_F32) return tau_one ? a : a / p.tau;
         else return a;
     };
     // The tempered logit of one token, with the reference's f32 arithmetic.
-    auto ztok = [&](const void *row, int64_t tok) -> float {
+    auto ztok = [&](const void *rowp, int64_t tok) -> float {
         float x;
-        if constexpr (DT == NT_F32) x = static_cast<const float *>(row)[tok];
-        else x = __uint_as_float(uint32_t(static_cast<const uint16_t *>(row)[tok]) << 16);
+        if constexpr (DT == NT_F32) x = static_cast<const float *>(rowp)[tok];
+        else x = __uint_as_float(uint32_t(static_cast<const uint16_t *>(rowp)[tok]) << 16);
         float z = tau_one ? x : x / p.tau;
         if constexpr (MK == NT_MASK_U8) {
             if (static_cast<const uint8_t *>(mrow)[tok] == 0) z = -INFINITY;
@@ -635,38 +650,22 @@ __global__ __launch_bounds__(kScoreThreads) void k_score(ScoreP p) {
     int64_t tok = -1;
     if (p.tokens) {
         tok = p.tokens[row];
-        if ((tok < 0 || tok >= p.V) && st == NT_ROW_OK) st = kRowBadToken;
+        if ((tok < 0 || tok >= p.V) && stt == NT_ROW_OK) stt = kRowBadToken;
     }
-    if (p.logp) {
-        float lp = NAN;
-        if (st == NT_ROW_OK) lp = float(double(ztok(xrow, tok) - zmax(apf)) - lnSp);
-        p.logp[row] = lp;
-    }
-    if (p.ent) p.ent[row] = (st == NT_ROW_OK || st == kRowBadToken) ? float(lnSp - kLn2 * Hp / Sp) : NAN;
+    const bool rowok = stt == NT_ROW_OK || stt == kRowBadToken;
+    if (p.logp) p.logp[row] = stt == NT_ROW_OK ? float(double(ztok(xrow, tok) - zmax(af)) - lnS) : NAN;
+    if (p.ent) p.ent[row] = rowok ? float(lnS - kLn2 * H / S) : NAN;
     if constexpr (REF) {
-        double ar, Sr, Hr, Br;
-        finish(wr, ar, Sr, Hr, Br);
-        const float arf = float(ar);
         const bool rok = arf != -INFINITY && Sr == Sr;
-        if (p.ref_logp) {
-            float lr = NAN;
-            if (rok && tok >= 0 && tok < p.V) lr = float(double(ztok(yrow, tok) - zmax(arf)) - log(Sr));
-            p.ref_logp[row] = lr;
-        }
+        if (p.ref_logp)
+            p.ref_logp[row] = (rok && tok >= 0 && tok < p.V) ? float(double(ztok(yrow, tok) - zmax(arf)) - log(Sr)) : NAN;
         if constexpr (KL) {
-            if (p.kl) {
-                float k = NAN;
-                if ((st == NT_ROW_OK || st == kRowBadToken) && rok) {
-                    // KL = sum p (z - zr) - (lse_p - lse_r), with the temperature applied in f64:
-                    // z - zr = (v - vr)/T and lse = a/T + ln S in the value space.
-                    const double it = (MK == NT_MASK_F32 || tau_one) ? 1.0 : 1.0 / double(p.tau);
-                    k = float((Bp / Sp - (ap - ar)) * it - log(Sp / Sr));
-                }
-                p.kl[row] = k;
-            }
+            // KL = sum p ((z - m) - (z_ref - m_ref)) - ln S + ln S_ref; the first sum is
+            // ln2 * B / S because c ln2 is the value-to-logit scale (1/T, or 1 with an f32 mask).
+            if (p.kl) p.kl[row] = (rowok && rok) ? float(kLn2 * B / S - log(S / Sr)) : NAN;
         }
     }
-    if (p.status) p.status[row] = uint8_t(st);
+    if (p.status) p.status[row] = uint8_t(stt);
 }
 
 // ------------------------------------------------------------------ per-token kernels
