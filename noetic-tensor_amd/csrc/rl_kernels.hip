@@ -32,6 +32,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <string>
+#include <type_traits>
 
 #include "../../include/noetic_hip.h"
 #include "nt_internal.hpp"
@@ -133,6 +134,32 @@ __device__ __forceinline__ void load_raw(Raw<DT, MK> &r, const void *xrow, const
     }
 }
 
+// Aligned load of the 8 elements at e0 with no bounds test (the caller passes an in-bounds
+// e0), so that a run of these loads is straight-line code the compiler can wait on one by one.
+template <int DT, int MK>
+__device__ __forceinline__ void load_raw_inbounds(Raw<DT, MK> &r, const void *xrow, const void *mrow, int64_t e0) {
+    if constexpr (DT == NT_F32) {
+        const uint4 *q = reinterpret_cast<const uint4 *>(static_cast<const float *>(xrow) + e0);
+        uint4 a = q[0], b = q[1];
+        r.x[0] = a.x; r.x[1] = a.y; r.x[2] = a.z; r.x[3] = a.w;
+        r.x[4] = b.x; r.x[5] = b.y; r.x[6] = b.z; r.x[7] = b.w;
+    } else {
+        uint4 a = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(xrow) + e0);
+        r.x[0] = a.x; r.x[1] = a.y; r.x[2] = a.z; r.x[3] = a.w;
+    }
+    if constexpr (MK == NT_MASK_U8) {
+        uint2 k = *reinterpret_cast<const uint2 *>(static_cast<const uint8_t *>(mrow) + e0);
+        r.m[0] = k.x; r.m[1] = k.y;
+    } else if constexpr (MK == NT_MASK_F32) {
+        const uint4 *q = reinterpret_cast<const uint4 *>(static_cast<const float *>(mrow) + e0);
+        uint4 a = q[0], b = q[1];
+        r.m[0] = a.x; r.m[1] = a.y; r.m[2] = a.z; r.m[3] = a.w;
+        r.m[4] = b.x; r.m[5] = b.y; r.m[6] = b.z; r.m[7] = b.w;
+    } else {
+        r.m[0] = 0;
+    }
+}
+
 // Logit j of a lane's chunk as f32 (bf16 widened exactly).
 template <int DT>
 __device__ __forceinline__ float logit(const uint32_t *x, int j) {
@@ -167,6 +194,40 @@ __device__ __forceinline__ void decode_words(const uint32_t *xw, const uint32_t 
 template <int DT, int MK>
 __device__ __forceinline__ void decode(const Raw<DT, MK> &r, float v[kEpl], float tau, bool tau_one) {
     decode_words<DT, MK>(r.x, r.m, v, tau, tau_one);
+}
+
+template <int MK>
+__device__ __forceinline__ void load_mask_inbounds(uint32_t *m, const void *mrow, int64_t e0) {
+    if constexpr (MK == NT_MASK_U8) {
+        uint2 k = *reinterpret_cast<const uint2 *>(static_cast<const uint8_t *>(mrow) + e0);
+        m[0] = k.x; m[1] = k.y;
+    } else if constexpr (MK == NT_MASK_F32) {
+        const uint4 *q = reinterpret_cast<const uint4 *>(static_cast<const float *>(mrow) + e0);
+        uint4 a = q[0], b = q[1];
+        m[0] = a.x; m[1] = a.y; m[2] = a.z; m[3] = a.w;
+        m[4] = b.x; m[5] = b.y; m[6] = b.z; m[7] = b.w;
+    }
+}
+
+// Write decoded values back into the logit words (exact: each value is the widened logit or
+// -inf, both representable in the storage type), so the mask is no longer needed.
+template <int DT>
+__device__ __forceinline__ void fold_values(uint32_t *x, const float v[kEpl]) {
+#pragma unroll
+    for (int j = 0; j < kEpl; j++) {
+        if constexpr (DT == NT_F32) {
+            x[j] = __float_as_uint(v[j]);
+        } else if (j % 2 == 1) {
+            x[j / 2] = (__float_as_uint(v[j]) & 0xffff0000u) | (__float_as_uint(v[j - 1]) >> 16);
+        }
+    }
+}
+
+// Decode words that were folded (the mask already applied) or, for an f32 mask, not.
+template <int DT, int MK, bool FOLDED>
+__device__ __forceinline__ void decode_folded(const Raw<DT, MK> &r, float v[kEpl], float tau, bool tau_one) {
+    if constexpr (FOLDED) decode_words<DT, NT_MASK_NONE>(r.x, r.m, v, tau, tau_one);
+    else decode_words<DT, MK>(r.x, r.m, v, tau, tau_one);
 }
 
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -451,6 +512,485 @@ __global__ __launch_bounds__(1024) void k_sample(SampleP p) {
         if (p.logp) p.logp[row] = float(double(zid - mz) - lnS);
         if (p.ent) p.ent[row] = float(lnS - kLn2 * H2 / S);
         p.status[row] = NT_ROW_OK;
+    }
+}
+
+// ------------------------------------------------------------------ register-resident sampler
+//
+// For rows of at most 16*K chunks (V <= 131072 for bf16 at K = 16) one 1024-thread workgroup
+// keeps the whole row on chip: each wave's logit words stay in VGPRs (64 registers at K = 16)
+// and the u8 mask is copied by the load unit straight into LDS (global_load_lds, 128 KiB at
+// K = 16). Every wave issues the loads of all its chunks up front, in the order it consumes
+// them, so the whole row is in flight at once and nothing is read twice.
+//
+// Phase 1 (all waves): as each chunk lands, w = 2^(v c - s) with s the wave's exponent
+// reference (its earlier maximum; re-set from the chunk's exact maximum only when an element
+// would exceed it by 2^64, which also covers the first chunk), so no exponential waits on a
+// reduction. The chunk's sum of weights is a fixed-order DPP reduction written to LDS.
+// Phase 2 (wave 0): exact masked maximum, f64 scan over the chunk sums in index order, the
+// chunk that holds u*S. Phase 3 (the owning wave): scan that chunk's registers.
+
+constexpr int kRRWaves = 16;
+constexpr int kRRThreads = kRRWaves * kWave;
+#ifndef NT_RR_WINDOW
+#define NT_RR_WINDOW 2
+#endif
+
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+typedef __attribute__((address_space(1))) void *glb_ptr_t;
+
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+// s_waitcnt with only the vector-memory counter constrained (expcnt and lgkmcnt at their
+// maxima): gfx9 encoding, vmcnt bits [3:0] and [15:14].
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// An LDS read the compiler does not track (it would otherwise wait for every outstanding load
+// because the data came from an LDS DMA); the caller has waited for that DMA.
+__device__ __forceinline__ uint2 lds_read_b64(uint32_t addr) {
+    uint2 r;
+    asm volatile("ds_read_b64 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(addr) : "memory");
+    return r;
+}
+__device__ __forceinline__ uint4 lds_read_b128(uint32_t addr) {
+    uint4 r;
+    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(addr) : "memory");
+    return r;
+}
+
+// v_max3_f32 without the canonicalising moves the compiler puts in front of fmaxf: the inputs
+// are widened logits or -inf, and a NaN among them reaches the row's sum through exp2 anyway.
+__device__ __forceinline__ float max3_hw(float a, float b, float c) {
+    float r;
+    asm volatile("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float max8_hw(const float v[kEpl]) {
+    const float t0 = max3_hw(v[0], v[1], v[2]);
+    const float t1 = max3_hw(v[3], v[4], v[5]);
+    return max3_hw(t0, t1, max3_hw(v[6], v[7], v[7]));
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+// Reductions over the 64 lanes: xor-1 and xor-2 quad permutes, the 8- and 16-lane mirrors,
+// then the four rows in a fixed order. Every lane's partial is the same at each step (the
+// operation is commutative), so the result is uniform and independent of timing.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, dpp_mov<0xB1>(v));
+    v = fmaxf(v, dpp_mov<0x4E>(v));
+    v = fmaxf(v, dpp_mov<0x141>(v));
+    v = fmaxf(v, dpp_mov<0x140>(v));
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v = v + dpp_mov<0xB1>(v);
+    v = v + dpp_mov<0x4E>(v);
+    v = v + dpp_mov<0x141>(v);
+    v = v + dpp_mov<0x140>(v);
+    return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
+}
+// One DPP step on an f64: both 32-bit halves move with the same control; lanes with no
+// source (or in rows the row mask leaves out) read 0, the identity of the sum.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const uint64_t b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(0, int(uint32_t(b)), CTRL, ROWS, 0xf, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, int(uint32_t(b >> 32)), CTRL, ROWS, 0xf, true);
+    return __longlong_as_double(int64_t((uint64_t(uint32_t(hi)) << 32) | uint32_t(lo)));
+}
+// Inclusive prefix sum over the 64 lanes in f64, in a fixed order: shifts by 1, 2, 4 and 8
+// inside each 16-lane row, then the row broadcasts of lanes 15 and 31 (the gfx9 DPP scan).
+__device__ __forceinline__ double wave_scan_dpp(double v) {
+    v += dpp_f64<0x111, 0xf>(v);  // row_shr:1
+    v += dpp_f64<0x112, 0xf>(v);  // row_shr:2
+    v += dpp_f64<0x114, 0xf>(v);  // row_shr:4
+    v += dpp_f64<0x118, 0xf>(v);  // row_shr:8
+    v += dpp_f64<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+    v += dpp_f64<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
+// Sum over each 16-lane row (the first four steps of wave_sum_dpp); every lane of a row holds
+// its row's sum.
+__device__ __forceinline__ float row_sum_dpp(float v) {
+    v = v + dpp_mov<0xB1>(v);
+    v = v + dpp_mov<0x4E>(v);
+    v = v + dpp_mov<0x141>(v);
+    v = v + dpp_mov<0x140>(v);
+    return v;
+}
+__device__ __forceinline__ int wave_min_i(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+// Mask bytes per chunk in LDS, and the LDS DMA instructions that bring one chunk's mask.
+template <int MK>
+struct RRMask {
+    static constexpr int kBytes = MK == NT_MASK_U8 ? kChunk : (MK == NT_MASK_F32 ? 4 * kChunk : 0);
+    static constexpr int kDma = kBytes / (4 * kWave);  // one dword per lane per instruction
+};
+
+template <int DT, int MK, int K, bool ENT>
+__global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
+    constexpr int NCH = K * kRRWaves;
+    constexpr int LX = DT == NT_F32 ? 2 : 1;       // logit load instructions per chunk
+    constexpr int LD = RRMask<MK>::kDma;           // mask DMA instructions per chunk
+    constexpr int L = LX + LD;
+    __shared__ __attribute__((aligned(16))) uint8_t mlds[MK == NT_MASK_NONE ? 16 : NCH * RRMask<MK>::kBytes];
+    __shared__ float csum4[NCH * 4];           // per chunk and 16-lane row: sum of 2^(v c - cref)
+    __shared__ float cent4[ENT ? NCH * 4 : 1];  // per chunk and row: sum of w (v c - cref)
+    __shared__ float cref[NCH];   // per chunk: the exponent reference used
+    __shared__ float wmax[kRRWaves];
+    __shared__ int wpick[kRRWaves];
+    __shared__ int pick_c;
+    __shared__ double pick_t, pick_S, pick_H;
+
+    const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int nc = p.nc;
+    const float c = p.c;
+    const bool tau_one = p.tau_one != 0;
+    const void *xrow = static_cast<const char *>(p.logits) + row * p.ld * Elem<DT>::kBytes;
+    const uint8_t *mrow = nullptr;
+    if constexpr (MK != NT_MASK_NONE)
+        mrow = static_cast<const uint8_t *>(p.mask) + row * p.mask_ld * MaskWords<MK>::kBytes;
+    const uint32_t mbase = uint32_t((uintptr_t)(lds_ptr_t)(mlds));
+
+    // ---- loads: the first W chunks now, chunk k + W as chunk k is consumed, so each wave keeps
+    // W chunks in flight (all of them at W = K).
+    constexpr int W = K < NT_RR_WINDOW ? K : NT_RR_WINDOW;
+    Raw<DT, NT_MASK_NONE> raw[K];
+    auto issue = [&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        const int ch = wave + kRRWaves * k;
+        const int64_t e0 = int64_t(ch) * kChunk + lane * kEpl;
+        // Lanes past the row read element 0 (in bounds); their values become -inf below.
+        const int64_t ea = (ch < nc && e0 < p.V) ? e0 : 0;
+        load_raw_inbounds<DT, NT_MASK_NONE>(raw[k], xrow, nullptr, ea);
+        if constexpr (MK != NT_MASK_NONE) {
+            // The chunk's mask bytes [ch*512, ch*512+512) (x4 for f32), one dword per lane per
+            // instruction, into the chunk's slot of mlds (lane l writes slot + 4 l).
+            const int64_t cb = (ch < nc && int64_t(ch) * kChunk < p.V) ? int64_t(ch) * kChunk : 0;
+#pragma unroll
+            for (int d = 0; d < LD; d++) {
+                int64_t off = cb * MaskWords<MK>::kBytes + int64_t(d) * 4 * kWave + 4 * lane;
+                const int64_t lim = p.V * MaskWords<MK>::kBytes - 4;
+                if (off > lim) off = 0;
+                __builtin_amdgcn_global_load_lds((glb_ptr_t)(mrow + off),
+                                                 (lds_ptr_t)(mlds + ch * RRMask<MK>::kBytes + d * 4 * kWave), 4, 0, 0);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    static_for<0, W>(issue);
+
+    // ---- phase 1: each chunk as it lands.
+    float lmax = -INFINITY;
+    float sref = -INFINITY;  // this wave's exponent reference, uniform
+    static_for<0, K>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        const int ch = wave + kRRWaves * k;
+        if (ch < nc) {
+            const int64_t e0 = int64_t(ch) * kChunk + lane * kEpl;
+            uint32_t mw[MaskWords<MK>::kWords > 0 ? MaskWords<MK>::kWords : 1];
+            if constexpr (MK != NT_MASK_NONE) {
+                // Chunks k+1 .. min(K, k+W)-1 may still be in flight.
+                wait_vmcnt<L * ((K < k + W ? K : k + W) - 1 - k)>();
+                const uint32_t a = mbase + ch * RRMask<MK>::kBytes + lane * kEpl * MaskWords<MK>::kBytes;
+                if constexpr (MK == NT_MASK_U8) {
+                    const uint2 m2 = lds_read_b64(a);
+                    mw[0] = m2.x;
+                    mw[1] = m2.y;
+                } else {
+                    const uint4 m0 = lds_read_b128(a), m1 = lds_read_b128(a + 16);
+                    mw[0] = m0.x; mw[1] = m0.y; mw[2] = m0.z; mw[3] = m0.w;
+                    mw[4] = m1.x; mw[5] = m1.y; mw[6] = m1.z; mw[7] = m1.w;
+                }
+            } else {
+                mw[0] = 0;
+            }
+            float v[kEpl];
+            decode_words<DT, MK>(raw[k].x, mw, v, p.tau, tau_one);
+            if (int64_t(ch + 1) * kChunk > p.V) {  // only the row's last chunk can be partial
+                if (e0 >= p.V) {
+#pragma unroll
+                    for (int j = 0; j < kEpl; j++) v[j] = -INFINITY;
+                }
+            }
+            const float m8 = max8_hw(v);
+            lmax = max3_hw(lmax, m8, m8);
+            const bool over = fmaf(m8, c, -sref) > 64.0f;
+            if (sref == -INFINITY || __ballot(over) != 0) {
+                const float wm = wave_max_dpp(m8);
+                sref = (wm == -INFINITY) ? -INFINITY : wm * c;
+            }
+            float gs = 0.0f, gh = 0.0f;
+            if (sref != -INFINITY) {
+                float w[kEpl], h[kEpl];
+#pragma unroll
+                for (int j = 0; j < kEpl; j++) {
+                    const float d = fmaf(v[j], c, -sref);
+                    w[j] = exp2_hw(d);
+                    if constexpr (ENT) h[j] = w[j] * fmaxf(d, -FLT_MAX);
+                }
+                gs = tree8(w);
+                if constexpr (ENT) gh = tree8(h);
+            }
+            // The chunk's four 16-lane row sums (phase 2 adds them in a fixed order).
+            const float cs = row_sum_dpp(gs);
+            float ce = 0.0f;
+            if constexpr (ENT) ce = row_sum_dpp(gh);
+            if ((lane & 15) == 0) {
+                csum4[ch * 4 + lane / 16] = cs;
+                if constexpr (ENT) cent4[ch * 4 + lane / 16] = ce;
+            }
+            if (lane == 0) cref[ch] = sref;
+        }
+        if constexpr (k + W < K) issue(std::integral_constant<int, k + W>{});
+    });
+    {
+        const float wm = wave_max_dpp(lmax);
+        if (lane == 0) wmax[wave] = wm;
+    }
+    __syncthreads();
+
+    // ---- phase 2 (wave 0): exact masked maximum, f64 scan of the chunk sums in index order.
+    float M = -INFINITY;
+    for (int i = 0; i < kRRWaves; i++) M = fmaxf(M, wmax[i]);
+    auto refuse = [&](uint8_t st) {
+        if (tid == 0) {
+            p.ids[row] = -1;
+            if (p.logp) p.logp[row] = NAN;
+            if (p.ent) p.ent[row] = NAN;
+            p.status[row] = st;
+        }
+    };
+    if (M == -INFINITY) {
+        refuse(NT_ROW_NO_TOKEN);
+        return;
+    }
+    const float A = M * c;  // >= every chunk reference (rounding is monotonic)
+    auto factor = [&](int ch) -> float {
+        const float r = cref[ch];
+        return r == -INFINITY ? 0.0f : exp2_hw(r - A);
+    };
+    auto csum = [&](int ch) -> float {
+        return (csum4[ch * 4] + csum4[ch * 4 + 1]) + (csum4[ch * 4 + 2] + csum4[ch * 4 + 3]);
+    };
+    auto cent = [&](int ch) -> float {
+        return (cent4[ch * 4] + cent4[ch * 4 + 1]) + (cent4[ch * 4 + 2] + cent4[ch * 4 + 3]);
+    };
+    if (wave == 0) {
+        // Lane l takes chunks [4l, 4l + 4) (nc <= 256): their weights f * sum in f64.
+        constexpr int Q = (NCH + kWave - 1) / kWave;
+        double wts[Q];
+        float fac[Q];
+        double ls = 0.0, lh = 0.0;
+#pragma unroll
+        for (int i = 0; i < Q; i++) {
+            const int ch = lane * Q + i;
+            fac[i] = 0.0f;
+            wts[i] = 0.0;
+            if (ch < nc) {
+                fac[i] = factor(ch);
+                const float cs = csum(ch);
+                wts[i] = double(fac[i]) * double(cs);
+                if constexpr (ENT) {
+                    if (cs > 0.0f) lh += double(fac[i]) * (double(cent(ch)) + double(cref[ch] - A) * double(cs));
+                }
+            }
+            ls += wts[i];
+        }
+        const double incl = wave_scan_dpp(ls);
+        // Every lane runs the shuffle (a disabled source lane would read as 0).
+        const double prev = __shfl_up(incl, 1, kWave);
+        const double excl = lane == 0 ? 0.0 : prev;
+        const double S = __shfl(incl, kWave - 1, kWave);
+        double H = 0.0;
+        if constexpr (ENT) H = wave_sum_d(lh);
+        int cstar = -1;
+        double tloc = INFINITY;
+        if (S == S && !p.greedy) {
+            const double t = p.u[row] * S;
+            const int l = first_lane(__ballot(incl > t && ls > 0.0));
+            int mine = -1;
+            double mt = INFINITY;
+            if (l >= 0) {
+                if (lane == l) {
+                    // Walk this lane's chunks from the prefix before them.
+                    double C = excl;
+                    int last = -1;
+#pragma unroll
+                    for (int i = 0; i < Q; i++) {
+                        if (mine < 0 && wts[i] > 0.0) {
+                            last = lane * Q + i;
+                            if (C + wts[i] > t) {
+                                mine = lane * Q + i;
+                                mt = (t - C) / double(fac[i]);
+                            }
+                            C += wts[i];
+                        }
+                    }
+                    if (mine < 0) mine = last;  // rounding between the scan and this walk
+                }
+                cstar = __shfl(mine, l, kWave);
+                tloc = __shfl(mt, l, kWave);
+            } else {
+                // u*S rounded up to S: the last chunk with weight.
+                int last = -1;
+#pragma unroll
+                for (int i = 0; i < Q; i++)
+                    if (wts[i] > 0.0) last = lane * Q + i;
+                const int ll = last_lane(__ballot(last >= 0));
+                cstar = ll >= 0 ? __shfl(last, ll, kWave) : -1;
+            }
+        }
+        if (lane == 0) {
+            pick_c = cstar;
+            pick_t = tloc;
+            pick_S = S;
+            pick_H = H;
+        }
+    }
+    __syncthreads();
+    const double S = pick_S;
+    if (!(S == S)) {
+        refuse(NT_ROW_NAN);
+        return;
+    }
+    // ln sum exp(z - m) and the entropy, from the sums relative to A = M c (computed by the
+    // one lane that writes the row).
+    auto write_row = [&](int64_t id, float vz) {
+        const double shiftA = double(A) - double(M) * double(c);
+        const double lnS = log(S) + shiftA * kLn2;
+        const float mz = (MK == NT_MASK_F32 || tau_one) ? M : M / p.tau;
+        const float zid = (MK == NT_MASK_F32 || tau_one) ? vz : vz / p.tau;
+        p.ids[row] = int32_t(id);
+        if (p.logp) p.logp[row] = float(double(zid - mz) - lnS);
+        if (p.ent) p.ent[row] = float(lnS - kLn2 * (pick_H / S + shiftA));
+        p.status[row] = NT_ROW_OK;
+    };
+    // Decode chunk k of this wave again (the mask from LDS; every DMA has completed).
+    auto chunk_values = [&](const Raw<DT, NT_MASK_NONE> &r, int ch, float v[kEpl]) {
+        uint32_t mw[MaskWords<MK>::kWords > 0 ? MaskWords<MK>::kWords : 1];
+        const uint32_t a = mbase + ch * RRMask<MK>::kBytes + lane * kEpl * MaskWords<MK>::kBytes;
+        if constexpr (MK == NT_MASK_U8) {
+            const uint2 m2 = lds_read_b64(a);
+            mw[0] = m2.x;
+            mw[1] = m2.y;
+        } else if constexpr (MK == NT_MASK_F32) {
+            const uint4 m0 = lds_read_b128(a), m1 = lds_read_b128(a + 16);
+            mw[0] = m0.x; mw[1] = m0.y; mw[2] = m0.z; mw[3] = m0.w;
+            mw[4] = m1.x; mw[5] = m1.y; mw[6] = m1.z; mw[7] = m1.w;
+        } else {
+            mw[0] = 0;
+        }
+        decode_words<DT, MK>(r.x, mw, v, p.tau, tau_one);
+        if (int64_t(ch) * kChunk + lane * kEpl >= p.V) {
+#pragma unroll
+            for (int j = 0; j < kEpl; j++) v[j] = -INFINITY;
+        }
+    };
+
+    if (p.greedy) {
+        // The first element equal to the maximum, in index order.
+        int first = 0x7fffffff;
+        static_for<0, K>([&](auto kc) {
+            constexpr int k = decltype(kc)::value;
+            const int ch = wave + kRRWaves * k;
+            if (ch < nc) {
+                float v[kEpl];
+                chunk_values(raw[k], ch, v);
+#pragma unroll
+                for (int j = kEpl - 1; j >= 0; j--)
+                    if (v[j] == M) first = min(first, ch * kChunk + lane * kEpl + j);
+            }
+        });
+        first = wave_min_i(first);
+        if (lane == 0) wpick[wave] = first;
+        __syncthreads();
+        int best = 0x7fffffff;
+        for (int i = 0; i < kRRWaves; i++) best = min(best, wpick[i]);
+        if (tid == 0) write_row(best, M);
+        return;
+    }
+
+    // ---- phase 3: the wave that owns chunk cstar scans it.
+    const int cstar = pick_c;
+    if (cstar < 0) {  // unreachable with S > 0; never leave stale outputs
+        refuse(NT_ROW_NAN);
+        return;
+    }
+    if (wave != cstar % kRRWaves) return;
+    const int kstar = cstar / kRRWaves;
+    Raw<DT, NT_MASK_NONE> r = raw[0];
+    static_for<1, K>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        if (k == kstar) r = raw[k];
+    });
+    float v[kEpl];
+    chunk_values(r, cstar, v);
+    const float sr = cref[cstar];
+    const double tloc = pick_t;
+    float w[kEpl];
+    double ls = 0.0;
+    int jlast = -1;
+#pragma unroll
+    for (int j = 0; j < kEpl; j++) {
+        w[j] = exp2_hw(fmaf(v[j], c, -sr));
+        ls += double(w[j]);
+        if (w[j] > 0.0f) jlast = j;
+    }
+    const double incl = wave_scan_dpp(ls);
+    const double prev = __shfl_up(incl, 1, kWave);
+    const double excl = lane == 0 ? 0.0 : prev;
+    int lsel = first_lane(__ballot(incl > tloc && ls > 0.0));
+    int jsel = -1;
+    if (lsel >= 0) {
+        if (lane == lsel) {
+            double C = excl;
+#pragma unroll
+            for (int j = 0; j < kEpl; j++) {
+                C += double(w[j]);
+                if (jsel < 0 && C > tloc) jsel = j;
+            }
+            if (jsel < 0) jsel = jlast;
+        }
+    } else {
+        lsel = last_lane(__ballot(jlast >= 0));
+        if (lane == lsel) jsel = jlast;
+    }
+    if (lsel < 0) {  // unreachable: the chunk holds weight
+        if (lane == 0) refuse(NT_ROW_NAN);
+        return;
+    }
+    if (lane == lsel) {
+        if (jsel < 0) jsel = 0;
+        float vz = v[0];
+#pragma unroll
+        for (int j = 1; j < kEpl; j++)
+            if (j == jsel) vz = v[j];
+        write_row(int64_t(cstar) * kChunk + lane * kEpl + jsel, vz);
     }
 }
 
@@ -772,6 +1312,46 @@ void pick_mk_sample(int mk, bool ent, bool al, const SampleP &p, int64_t rows, i
     else pick_ent_sample<DT, NT_MASK_NONE>(ent, al, p, rows, threads, shm, s);
 }
 
+// Largest chunks-per-wave of the register-resident sampler: K chunks of logit words live in
+// VGPRs (bf16 4 per chunk, f32 8) and the mask of every chunk in LDS (u8 512 B, f32 2 KiB).
+int rr_kmax(int dtype, int mk) {
+    if (mk == NT_MASK_F32) return 4;
+    return dtype == NT_BF16 ? 16 : 8;
+}
+
+template <int DT, int MK, int K>
+void launch_rr_k(bool ent, const SampleP &p, int64_t rows, hipStream_t s) {
+    if (ent) hipLaunchKernelGGL((k_sample_rr<DT, MK, K, true>), dim3(unsigned(rows)), dim3(kRRThreads), 0, s, p);
+    else hipLaunchKernelGGL((k_sample_rr<DT, MK, K, false>), dim3(unsigned(rows)), dim3(kRRThreads), 0, s, p);
+}
+
+template <int DT, int MK>
+void launch_rr_mk(int K, bool ent, const SampleP &p, int64_t rows, hipStream_t s) {
+    switch (K) {
+        case 1: launch_rr_k<DT, MK, 1>(ent, p, rows, s); break;
+        case 2: launch_rr_k<DT, MK, 2>(ent, p, rows, s); break;
+        case 4: launch_rr_k<DT, MK, 4>(ent, p, rows, s); break;
+        case 8:
+            if constexpr (MK != NT_MASK_F32) launch_rr_k<DT, MK, 8>(ent, p, rows, s);
+            break;
+        default:
+            if constexpr (DT == NT_BF16 && MK != NT_MASK_F32) launch_rr_k<DT, MK, 16>(ent, p, rows, s);
+            break;
+    }
+}
+
+void launch_rr(int dtype, int mk, int K, bool ent, const SampleP &p, int64_t rows, hipStream_t s) {
+    if (dtype == NT_F32) {
+        if (mk == NT_MASK_U8) launch_rr_mk<NT_F32, NT_MASK_U8>(K, ent, p, rows, s);
+        else if (mk == NT_MASK_F32) launch_rr_mk<NT_F32, NT_MASK_F32>(K, ent, p, rows, s);
+        else launch_rr_mk<NT_F32, NT_MASK_NONE>(K, ent, p, rows, s);
+    } else {
+        if (mk == NT_MASK_U8) launch_rr_mk<NT_BF16, NT_MASK_U8>(K, ent, p, rows, s);
+        else if (mk == NT_MASK_F32) launch_rr_mk<NT_BF16, NT_MASK_F32>(K, ent, p, rows, s);
+        else launch_rr_mk<NT_BF16, NT_MASK_NONE>(K, ent, p, rows, s);
+    }
+}
+
 template <int DT, int MK, bool REF, bool KL, bool ENT>
 void pick_al_score(bool al, const ScoreP &p, int64_t rows, hipStream_t s) {
     if (al) hipLaunchKernelGGL((k_score<DT, MK, REF, KL, ENT, true>), dim3(unsigned(rows)), dim3(kScoreThreads), 0, s, p);
@@ -845,6 +1425,15 @@ int nt_hip_rl_sample(const NtRlSampleArgs *a) {
     if (a->rows >= 2048 && nw > 4) nw = 4;
     const bool al = aligned_rows(a->logits, a->vocab, a->ld, a->dtype, a->mask_kind, a->mask, a->mask_ld);
     hipStream_t s = ctx().stream;
+    // Rows that fit the register-resident kernel take it (chunks per wave K = 1..16); the
+    // streaming kernel takes everything else (entropy, unaligned rows, larger V).
+    const int kmax = rr_kmax(a->dtype, a->mask_kind);
+    if (al && nc <= int64_t(kRRWaves) * kmax) {
+        int K = 1;
+        while (int64_t(kRRWaves) * K < nc) K *= 2;
+        launch_rr(a->dtype, a->mask_kind, K, ent, p, a->rows, s);
+        return launched("nt_hip_rl_sample");
+    }
     if (a->dtype == NT_F32) pick_mk_sample<NT_F32>(a->mask_kind, ent, al, p, a->rows, nw * kWave, shm, s);
     else pick_mk_sample<NT_BF16>(a->mask_kind, ent, al, p, a->rows, nw * kWave, shm, s);
     return launched("nt_hip_rl_sample");
