@@ -74,10 +74,22 @@ def main():
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--cpu-rows", type=int, default=256, help="rows of the CPU baseline sample (0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="repeat the CPU sample up to this long")
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="instead of the benchmark: 20 plain device copies of this many bytes (calibrates the "
+                         "FETCH_SIZE / WRITE_SIZE counters against known traffic)")
     args = ap.parse_args()
+    if args.copy_bytes > 0:
+        import torch
+        src = torch.ones(args.copy_bytes // 4, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": src.numel() * 4, "launches": 20}), flush=True)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": f"--gpus {args.gpus}: this build measures one GPU; the path shards by rows "
-                                   "with no exchange (see DESIGN.md), and multi-GPU runs are not part of it"}))
+                                   "with no exchange, and multi-GPU runs are not part of it"}))
         sys.exit(2)
 
     import noetic_rl as nr
@@ -150,7 +162,7 @@ def main():
                      "algorithmic_bytes_per_launch": bytes_launch},
         "key": nr.key(),
     }
-    tr = os.path.join(ROOT, "profiles", "c4_sample_traffic.json")
+    tr = os.path.join(ROOT, "profiles", "k_sample_rr_c4_traffic.json")
     if os.path.exists(tr):
         with open(tr) as f:
             out["roofline"]["traffic"] = json.load(f).get("hbm_bytes_per_launch")

@@ -15,8 +15,8 @@
  *  - Kernels use no atomics and reduce in a fixed order, so a rerun on the same inputs is
  *    bit-identical (the reference's determinism contract, src/nn/tests/gpu/rl.rs:125-128).
  *
- * Rust binding: INTEGRATION.md gives the hand-written `extern "C"` block and the
- * GpuBackend methods that call these.
+ * A Rust caller binds these with a hand-written `extern "C"` block, the reference's FFI style
+ * (src/tensor/cuda/ffi.rs:30-117), from optional GpuBackend methods.
  */
 #ifndef NOETIC_HIP_H
 #define NOETIC_HIP_H

@@ -36,6 +36,33 @@ def test_library_exports_every_declared_symbol():
     assert names <= set(nr._SIGS), sorted(names - set(nr._SIGS))
 
 
+def test_argument_struct_layouts_match_the_header():
+    """The ctypes mirrors of the argument structs have the C header's sizes and field offsets
+    (the header compiled by gcc on this host; a Rust #[repr(C)] binding asserts the same)."""
+    import subprocess
+    import tempfile
+    fields = {"NtRlSampleArgs": [f[0] for f in nr.NtRlSampleArgs._fields_],
+              "NtRlScoreArgs": [f[0] for f in nr.NtRlScoreArgs._fields_]}
+    body = []
+    for st, fs in fields.items():
+        body.append(f'printf("{st} %zu\\n", sizeof({st}));')
+        body += [f'printf("{st}.{f} %zu\\n", offsetof({st}, {f}));' for f in fs]
+    src = ("#include <stdio.h>\n#include <stddef.h>\n#include \"noetic_hip.h\"\nint main(void) {\n"
+           + "\n".join(body) + "\nreturn 0;\n}\n")
+    with tempfile.TemporaryDirectory() as d:
+        c, exe = os.path.join(d, "layout.c"), os.path.join(d, "layout")
+        open(c, "w").write(src)
+        subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), c, "-o", exe], check=True)
+        out = subprocess.run([exe], check=True, capture_output=True, text=True).stdout.split("\n")
+    got = dict(line.split() for line in out if line)
+    for st, fs in fields.items():
+        cls = getattr(nr, st)
+        assert int(got[st]) == C.sizeof(cls), st
+        for f in fs:
+            assert int(got[f"{st}.{f}"]) == getattr(cls, f).offset, (st, f)
+    assert int(got["NtRlSampleArgs"]) == 104 and int(got["NtRlScoreArgs"]) == 120
+
+
 def test_without_a_claimed_device_calls_fail_cleanly():
     L = nr.lib()
     if L.nt_hip_device_count() > 0:
