@@ -7,6 +7,14 @@ launches bracketed by a stream synchronisation and HIP events recorded on the li
 stream. Prints one JSON line (the driver's contract) with a `roofline` object (algorithmic
 bytes per launch / average launch time against the 8 TB/s HBM peak) and a `cpu_baseline`
 object (the reference's Cpu(Reference) op sequence, restated in oracle/, timed on this host).
+
+`--workload c2|c3|c5` measures the other configurations the same way, one JSON line each:
+  c2  decode step, f32 [1,64,1,32000], no mask, tau 0.8: the fused sample + logp;
+  c3  PPO scoring, bf16 policy + reference [8,16,512,50304]: logp, reference logp, exact KL,
+      entropy (nt_hip_rl_score) and the k3 per-token KL (nt_hip_rl_kl_estimate);
+  c5  rollout scoring, f32 [4,32,1024,151936] + u8 mask: logp and entropy (nt_hip_rl_score),
+      the per-sequence mean log-probability (nt_hip_rl_reduce_tokens) and group-relative
+      advantages over groups of 8 along B (host f64, where the reference computes them).
 """
 import argparse
 import ctypes as C
@@ -35,6 +43,54 @@ def hip_events():
     return hip
 
 
+def timed(nr, steps, warmup, step):
+    """Average milliseconds of `step(i)` over `steps` calls after `warmup` untimed ones, from HIP
+    events on the library's stream (where every kernel runs), plus the wall seconds."""
+    for i in range(warmup):
+        step(i)
+    nr.sync()
+    hip = hip_events()
+    stream = C.c_void_p()
+    nr._check(nr.lib().nt_hip_stream(C.byref(stream)), "stream")
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    hip.hipEventCreate(C.byref(e0))
+    hip.hipEventCreate(C.byref(e1))
+    nr.sync()
+    t0 = time.perf_counter()
+    hip.hipEventRecord(e0, stream)
+    for i in range(warmup, warmup + steps):
+        step(i)
+    hip.hipEventRecord(e1, stream)
+    hip.hipEventSynchronize(e1)
+    nr.sync()
+    wall = time.perf_counter() - t0
+    ms = C.c_float()
+    hip.hipEventElapsedTime(C.byref(ms), e0, e1)
+    hip.hipEventDestroy(e0)
+    hip.hipEventDestroy(e1)
+    return ms.value / steps, wall
+
+
+def roofline(bytes_launch, ms, traffic_file=None):
+    gbs = bytes_launch / (ms * 1e-3) / 1e9
+    r = {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
+         "traffic": None, "algorithmic_bytes_per_launch": bytes_launch}
+    if traffic_file:
+        tr = os.path.join(ROOT, "profiles", traffic_file)
+        if os.path.exists(tr):
+            with open(tr) as f:
+                r["traffic"] = json.load(f).get("hbm_bytes_per_launch")
+    return r
+
+
+def line(metric, value, steps, warmup, ms, dtype, config, roof, **extra):
+    out = {"metric": metric, "value": value, "unit": "rows/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+           "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+           "data": "synthetic", "config": config, "roofline": roof}
+    out.update(extra)
+    return out
+
+
 def cpu_baseline(w, rows_sample, seed, min_seconds=10.0):
     """The reference's CPU path on a bounded sample of the same rows: tempered_logits, the
     max_dim check, one Gumbel draw per logit from the ChaCha stream, argmax, log_softmax and
@@ -43,35 +99,178 @@ def cpu_baseline(w, rows_sample, seed, min_seconds=10.0):
     import workloads as W
     from oracle import oracle as O
     V = w["V"]
-    x = W.bf16_to_f32(W.download_rows(w["logits"], range(rows_sample), V))
-    keep = W.download_rows(w["mask"], range(rows_sample), V)
-    rng = O.Rng(seed, "c4/gumbel")
+    x = W.download_rows(w["logits"], range(rows_sample), V)
+    x = W.bf16_to_f32(x) if w["logits"].dtype == "bf16" else x
+    keep = W.download_rows(w["mask"], range(rows_sample), V) if w["mask"] is not None else None
+    rng = O.Rng(seed, f"{w['name']}/gumbel")
     reps, t_ref = 0, 0.0
-    while reps < 1 or (t_ref < min_seconds and reps < 16):
+    while reps < 1 or (t_ref < min_seconds and reps < 1000):
         t0 = time.perf_counter()
         O.cpuref_sample_logp(x, w["temperature"], keep, rng)
         t_ref += time.perf_counter() - t0
         reps += 1
     cores = os.cpu_count() or 1
-    u = O.Rng(seed, "c4/uniforms").uniforms(rows_sample)
+    u = O.Rng(seed, f"{w['name']}/uniforms").uniforms(rows_sample)
     t0 = time.perf_counter()
     O.cpu_sample_logp_invcdf(x, w["temperature"], keep, u, threads=cores)
     t_fast = time.perf_counter() - t0
     return {
         "value": reps * rows_sample / t_ref, "unit": "rows/s", "cores": 1, "kind": "port",
-        "sample": f"{reps} x {rows_sample} c4 rows (V=128256, bf16 values widened to f32): the reference's "
+        "sample": f"{reps} x {rows_sample} {w['name']} rows (V={V}, values widened to f32): the reference's "
                   f"Cpu(Reference) op sequence with Gumbel-max sampling, single thread, {t_ref:.2f} s",
         "fast_port": {"value": rows_sample / t_fast, "unit": "rows/s", "cores": cores,
                       "what": "unfused op sequence with the inverse-CDF draw, rows split over threads"},
     }
 
 
+def cpu_baseline_scoring(w, rows_sample, min_seconds=10.0):
+    """The oracle's scoring of a bounded row sample on one host core: tempered values, then
+    log-softmax at the token, exact KL and entropy per row (f64 after the f32 inputs)."""
+    import workloads as W
+    from oracle import oracle as O
+    V = w["V"]
+    x = W.download_rows(w["logits"], range(rows_sample), V)
+    x = W.bf16_to_f32(x) if w["logits"].dtype == "bf16" else x
+    keep = W.download_rows(w["mask"], range(rows_sample), V) if w.get("mask") is not None else None
+    y = None
+    if w.get("ref") is not None:
+        y = W.download_rows(w["ref"], range(rows_sample), V)
+        y = W.bf16_to_f32(y) if w["ref"].dtype == "bf16" else y
+    tok = w["tokens"].to_numpy().ravel()[:rows_sample].astype(np.int64)
+    reps, t = 0, 0.0
+    while reps < 1 or (t < min_seconds and reps < 1000):
+        t0 = time.perf_counter()
+        z = O.tempered(x, w["temperature"], keep=keep)
+        O.token_logp(z, tok)
+        O.entropy(z)
+        if y is not None:
+            r = O.tempered(y, w["temperature"], keep=keep)
+            O.token_logp(r, tok)
+            O.kl(z, r)
+        t += time.perf_counter() - t0
+        reps += 1
+    return {"value": reps * rows_sample / t, "unit": "rows/s", "cores": 1, "kind": "port",
+            "sample": f"{reps} x {rows_sample} {w['name']} rows (V={V}): the oracle's f64 scoring restatement "
+                      f"(tempered values, log-softmax gather, {'exact KL, ' if y is not None else ''}entropy), "
+                      f"single thread, {t:.2f} s"}
+
+
+def bench_sample(nr, W, args, name):
+    """c4 (the north star) or c2: one launch of nt_hip_rl_sample per step."""
+    w = W.c4(args.seed) if name == "c4" else W.c2(args.seed)
+    rows, V = w["rows"], w["V"]
+    n_launch = args.warmup + args.steps
+    U = nr.Tensor.from_numpy(nr.Rng(args.seed, f"{name}/uniforms").uniforms(rows * n_launch), "f64")
+    ids = nr.IntTensor((rows,))
+    logp = nr.Tensor((rows,), "f32")
+    status = nr.Tensor((rows,), "u8")
+    L = nr.lib()
+    dt = nr.NT_BF16 if w["logits"].dtype == "bf16" else nr.NT_F32
+    mk = nr.NT_MASK_U8 if w["mask"] is not None else nr.NT_MASK_NONE
+    mptr = w["mask"].ptr if w["mask"] is not None else None
+    argv = [nr.NtRlSampleArgs(w["logits"].ptr, dt, mk, rows, V, V, mptr, V if mptr else 0, w["temperature"],
+                              U.ptr + 8 * rows * i, ids.ptr, logp.ptr, None, status.ptr) for i in range(n_launch)]
+    nr._check(L.nt_hip_rl_sample(C.byref(argv[0])), "sample")
+    ms, wall = timed(nr, args.steps, args.warmup, lambda i: L.nt_hip_rl_sample(C.byref(argv[i])))
+    st = status.to_numpy()
+    if np.any(st != 0):
+        raise SystemExit(f"bench: {int(np.sum(st != 0))} rows refused")
+    # Algorithmic bytes per launch: every input read once, every output written once.
+    esz = 2 if dt == nr.NT_BF16 else 4
+    per_row = esz * V + (V if mk == nr.NT_MASK_U8 else 0) + 8 + 4 + 4 + 1  # logits, mask, uniform, id, logp, status
+    bytes_launch = per_row * rows
+    roof = roofline(bytes_launch, ms, "k_sample_rr_c4_traffic.json" if name == "c4" else None)
+    if name == "c4":
+        metric = "rows/sec + achieved HBM GB/s, fused masked sample+logprob, V=128256 bf16"
+        config = {"workload": "c4 constrained decode: bf16 logits [1,256,1,128256] ~ N(0,2^2), u8 grammar mask "
+                              "[256,V] of contiguous runs (~30% kept), temperature 0.7, fused sample + logp",
+                  "rows": rows, "vocab": V, "parallelism": "none (1 GPU)"}
+    else:
+        metric = "rows/sec + achieved HBM GB/s, fused sample+logprob, V=32000 f32 (decode step)"
+        config = {"workload": "c2 decode step: f32 logits [1,64,1,32000] ~ N(0,1) + 8 spikes of +6 per row, no mask, "
+                              "temperature 0.8, fused sample + logp", "rows": rows, "vocab": V,
+                  "parallelism": "none (1 GPU)"}
+    out = line(metric, rows / (ms * 1e-3), args.steps, args.warmup, ms, "bf16" if esz == 2 else "f32", config, roof,
+               achieved_gbs=roof["achieved"], wall_s_timed_region=wall, key=nr.key())
+    if args.cpu_rows > 0:
+        out["cpu_baseline"] = cpu_baseline(w, min(args.cpu_rows, rows), args.seed, args.cpu_seconds)
+    return out
+
+
+def bench_score(nr, W, args, name):
+    """c3 or c5: one fused scoring launch per step plus the small per-token follow-ups."""
+    w = W.c3(args.seed) if name == "c3" else W.c5(args.seed)
+    rows, V = w["rows"], w["V"]
+    shp = w["logits"].shape[:-1]
+    L = nr.lib()
+    dt = nr.NT_BF16 if w["logits"].dtype == "bf16" else nr.NT_F32
+    esz = 2 if dt == nr.NT_BF16 else 4
+    out_t = lambda: nr.Tensor(shp, "f32")
+    lp, ent, status = out_t(), out_t(), nr.Tensor(shp, "u8")
+    ref = w.get("ref")
+    rlp, kl, k3 = (out_t(), out_t(), out_t()) if ref is not None else (None, None, None)
+    mask = w.get("mask")
+    a = nr.NtRlScoreArgs(w["logits"].ptr, ref.ptr if ref is not None else None, dt,
+                         nr.NT_MASK_U8 if mask is not None else nr.NT_MASK_NONE, rows, V, V,
+                         mask.ptr if mask is not None else None, V if mask is not None else 0, w["temperature"],
+                         w["tokens"].ptr, lp.ptr, rlp.ptr if rlp else None, kl.ptr if kl else None, ent.ptr,
+                         status.ptr)
+    score = lambda i: L.nt_hip_rl_score(C.byref(a))
+    nr._check(score(0), "score")
+    # the dominant kernel alone, for the roofline
+    ms_score, _ = timed(nr, args.steps, args.warmup, score)
+    # logits (x2 with a reference), mask, token, logp, entropy, status (+ reference logp, KL)
+    per_row = (2 if ref is not None else 1) * esz * V + (V if mask is not None else 0) + 4 + 4 + 4 + 1
+    if ref is not None:
+        per_row += 4 + 4
+    bytes_score = per_row * rows
+    if name == "c3":
+        def step(i):
+            score(i)
+            nr._check(L.nt_hip_rl_kl_estimate(lp.ptr, rlp.ptr, None, rows, int(nr.KlEstimator.K3), 0.0, k3.ptr),
+                      "kl_estimate")
+    else:
+        S, B, T = shp
+        seq = nr.Tensor((S, B), "f32")
+
+        def step(i):
+            score(i)
+            nr._check(L.nt_hip_rl_reduce_tokens(lp.ptr, None, S, B, T, int(nr.TokenReduction.PER_SEQUENCE), seq.ptr),
+                      "reduce_tokens")
+            # group-relative advantages over groups of 8 along B: host f64 (rl.rs:416-469)
+            nr.group_advantages(seq.to_f64().ravel(), 8)
+    ms, wall = timed(nr, args.steps, args.warmup, step)
+    st = status.to_numpy()
+    if np.any(st != 0):
+        raise SystemExit(f"bench: {int(np.sum(st != 0))} rows refused")
+    roof = roofline(bytes_score, ms_score)
+    roof["kernel"] = "k_score"
+    roof["kernel_ms"] = ms_score
+    if name == "c3":
+        metric = "rows/sec + achieved HBM GB/s, fused PPO scoring (logp, ref logp, exact KL, k3, entropy), V=50304 bf16"
+        config = {"workload": "c3 PPO scoring: bf16 policy [8,16,512,50304] ~ N(0,1.5^2), reference = policy + "
+                              "N(0,0.1^2) (RNE), tokens uniform; logp, ref logp, exact KL, entropy, k3",
+                  "rows": rows, "vocab": V, "parallelism": "none (1 GPU)"}
+    else:
+        metric = ("rows/sec + achieved HBM GB/s, fused masked scoring (logp, entropy) + group advantages, "
+                  "V=151936 f32")
+        config = {"workload": "c5 rollout scoring: f32 [4,32,1024,151936] ~ N(0,1) + Zipf(1.1) rank bias, u8 mask "
+                              "Bernoulli(0.9); logp, entropy, per-sequence mean logp, group advantages (8 along B)",
+                  "rows": rows, "vocab": V, "parallelism": "none (1 GPU)"}
+    out = line(metric, rows / (ms * 1e-3), args.steps, args.warmup, ms, "bf16" if esz == 2 else "f32", config, roof,
+               achieved_gbs=roof["achieved"], wall_s_timed_region=wall, key=nr.key())
+    if args.cpu_rows > 0:
+        out["cpu_baseline"] = cpu_baseline_scoring(w, min(args.cpu_rows, 64), args.cpu_seconds)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 200; 20 for c3/c5)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 20; 3 for c3/c5)")
     ap.add_argument("--seed", type=int, default=2024)
+    ap.add_argument("--workload", default="c4", choices=["c4", "c2", "c3", "c5"])
     ap.add_argument("--cpu-rows", type=int, default=256, help="rows of the CPU baseline sample (0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="repeat the CPU sample up to this long")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -91,83 +290,20 @@ def main():
         print(json.dumps({"error": f"--gpus {args.gpus}: this build measures one GPU; the path shards by rows "
                                    "with no exchange, and multi-GPU runs are not part of it"}))
         sys.exit(2)
+    big = args.workload in ("c3", "c5")
+    if args.steps is None:
+        args.steps = 20 if big else 200
+    if args.warmup is None:
+        args.warmup = 3 if big else 20
 
     import noetic_rl as nr
     import workloads as W
 
     nr.claim(0)
-    w = W.c4(args.seed)
-    rows, V = w["rows"], w["V"]
-    n_launch = args.warmup + args.steps
-    U = nr.Tensor.from_numpy(nr.Rng(args.seed, "c4/uniforms").uniforms(rows * n_launch), "f64")
-    ids = nr.IntTensor((rows,))
-    logp = nr.Tensor((rows,), "f32")
-    status = nr.Tensor((rows,), "u8")
-    L = nr.lib()
-    argv = []
-    for i in range(n_launch):
-        a = nr.NtRlSampleArgs(w["logits"].ptr, nr.NT_BF16, nr.NT_MASK_U8, rows, V, V, w["mask"].ptr, V,
-                              w["temperature"], U.ptr + 8 * rows * i, ids.ptr, logp.ptr, None, status.ptr)
-        argv.append(a)
-    for i in range(args.warmup):
-        nr._check(L.nt_hip_rl_sample(C.byref(argv[i])), "sample")
-    nr.sync()
-
-    hip = hip_events()
-    stream = C.c_void_p()
-    nr._check(L.nt_hip_stream(C.byref(stream)), "stream")
-    e0, e1 = C.c_void_p(), C.c_void_p()
-    hip.hipEventCreate(C.byref(e0))
-    hip.hipEventCreate(C.byref(e1))
-    nr.sync()
-    t0 = time.perf_counter()
-    hip.hipEventRecord(e0, stream)
-    for i in range(args.warmup, n_launch):
-        L.nt_hip_rl_sample(C.byref(argv[i]))
-    hip.hipEventRecord(e1, stream)
-    hip.hipEventSynchronize(e1)
-    nr.sync()
-    wall = time.perf_counter() - t0
-    ms = C.c_float()
-    hip.hipEventElapsedTime(C.byref(ms), e0, e1)
-    st = status.to_numpy()
-    if np.any(st != 0):
-        raise SystemExit(f"bench: {int(np.sum(st != 0))} rows refused")
-
-    ms_per_step = ms.value / args.steps
-    # Algorithmic bytes per launch: every input read once, every output written once.
-    per_row = 2 * V + V + 8 + 4 + 4 + 1  # bf16 logits, u8 mask, f64 uniform, i32 id, f32 logp, u8 status
-    bytes_launch = per_row * rows
-    gbs = bytes_launch / (ms_per_step * 1e-3) / 1e9
-    out = {
-        "metric": "rows/sec + achieved HBM GB/s, fused masked sample+logprob, V=128256 bf16",
-        "value": rows / (ms_per_step * 1e-3),
-        "unit": "rows/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": ms_per_step,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic",
-        "config": {"workload": "c4 constrained decode: bf16 logits [1,256,1,128256] ~ N(0,2^2), u8 grammar mask "
-                               "[256,V] of contiguous runs (~30% kept), temperature 0.7, fused sample + logp",
-                   "rows": rows, "vocab": V, "parallelism": "none (1 GPU)"},
-        "achieved_gbs": gbs,
-        "wall_s_timed_region": wall,
-        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": gbs / HBM_PEAK_GBS, "traffic": None,
-                     "algorithmic_bytes_per_launch": bytes_launch},
-        "key": nr.key(),
-    }
-    tr = os.path.join(ROOT, "profiles", "k_sample_rr_c4_traffic.json")
-    if os.path.exists(tr):
-        with open(tr) as f:
-            out["roofline"]["traffic"] = json.load(f).get("hbm_bytes_per_launch")
-    if args.cpu_rows > 0:
-        out["cpu_baseline"] = cpu_baseline(w, min(args.cpu_rows, rows), args.seed, args.cpu_seconds)
+    if args.workload in ("c4", "c2"):
+        out = bench_sample(nr, W, args, args.workload)
+    else:
+        out = bench_score(nr, W, args, args.workload)
     print(json.dumps(out), flush=True)
 
 

@@ -312,3 +312,68 @@ def test_reference_losses_body_values():
     assert rel_err(got, want) <= tol
     again = nr.reference_kl(xt, rt, 0.8, vmt, mt, nr.TokenReduction.NONE).to_numpy().ravel()
     assert got.tobytes() == again.tobytes()
+
+
+def _sample_rows(rows, n, seed):
+    """The first, second and last rows plus n - 3 others, sorted."""
+    rng = np.random.default_rng(seed)
+    pick = {0, 1, rows - 1} | set(rng.choice(rows, n - 3, replace=False).tolist())
+    return np.array(sorted(pick))
+
+
+def test_c3_full_size_scoring():
+    # BASELINE config 3 at its real size: 2 x bf16 [8,16,512,50304] (13.2 GB). Rows spread over
+    # the tensor against the oracle; every row through size-independent properties.
+    w = W.c3()
+    rows, V = w["rows"], w["V"]
+    lp, rlp, kl, ent = nr.score(w["logits"], w["ref"], w["tokens"])
+    lp2, rlp2, kl2, ent2 = nr.score(w["logits"], w["ref"], w["tokens"])
+    outs = [t.to_numpy().ravel() for t in (lp, rlp, kl, ent)]
+    for a, b in zip(outs, (lp2, rlp2, kl2, ent2)):
+        assert a.tobytes() == b.to_numpy().ravel().tobytes(), "rerun bits"
+    lpn, rlpn, kln, entn = outs
+    assert np.all(np.isfinite(lpn)) and np.all(lpn <= 0.0) and np.all(rlpn <= 0.0)
+    assert np.all(kln >= -1e-6), f"KL < 0 at {np.nonzero(kln < -1e-6)[0][:4]}"
+    assert np.all(entn >= 0.0) and np.all(entn <= math.log(V) * (1 + 1e-6))
+    sel = _sample_rows(rows, 48, 33)
+    xf = W.bf16_to_f32(W.download_rows(w["logits"], sel, V))
+    yf = W.bf16_to_f32(W.download_rows(w["ref"], sel, V))
+    tok = w["tokens"].to_numpy().ravel()[sel]
+    _score_check("c3 full", xf, yf, tok, lpn[sel], rlpn[sel], kln[sel], entn[sel], close_f32)
+    # k3 per sampled token over the whole batch against the oracle's closed form
+    S, B, T = w["logits"].shape[:-1]
+    k3 = nr.kl_estimate(nr.Tensor((S, B, T), "f32", lp.buf), nr.Tensor((S, B, T), "f32", rlp.buf),
+                        nr.KlEstimator.K3, None, None, nr.TokenReduction.NONE).to_numpy().ravel()
+    want = O.kl_estimate(lpn.astype(np.float64), rlpn.astype(np.float64), 3, None, None)
+    assert np.all(close_f32(k3, want)), rel_err(k3, want)
+
+
+def test_c5_full_size_scoring_and_group_advantages():
+    # BASELINE config 5 at its real size: f32 [4,32,1024,151936] (79.7 GB) + u8 mask (19.9 GB).
+    w = W.c5()
+    rows, V = w["rows"], w["V"]
+    S, B, T = w["logits"].shape[:-1]
+    lp, _, _, ent = nr._score(nr.tempered_logits(w["logits"], 1.0, w["mask"]), None, w["tokens"], True, False, False,
+                              True)[:4]
+    lpn, entn = lp.to_numpy().ravel(), ent.to_numpy().ravel()
+    assert np.all(np.isfinite(lpn)) and np.all(lpn <= 0.0), "every scored token is kept"
+    assert np.all(entn >= 0.0) and np.all(entn <= math.log(V) * (1 + 1e-6))
+    sel = _sample_rows(rows, 32, 55)
+    x = W.download_rows(w["logits"], sel, V)
+    keep = W.download_rows(w["mask"], sel, V)
+    z = O.tempered(x, 1.0, keep=keep)
+    tok = w["tokens"].to_numpy().ravel()[sel]
+    want_lp, want_h = O.token_logp(z, tok), O.entropy(z)
+    assert np.all(close_f32(lpn[sel], want_lp)), rel_err(lpn[sel], want_lp)
+    assert np.all(close_f32(entn[sel], want_h)), rel_err(entn[sel], want_h)
+    print(f"c5 full: logp rel {rel_err(lpn[sel], want_lp):.1e}, entropy rel {rel_err(entn[sel], want_h):.1e}")
+    # rewards = each sequence's mean log-probability (device), advantages over groups of 8 along B
+    rew = nr._reduce(nr.Tensor((S, B, T), "f32", lp.buf), None, nr.TokenReduction.PER_SEQUENCE)
+    rewn = rew.to_numpy().astype(np.float64).ravel()
+    want_rew = O.reduce_tokens(lpn.astype(np.float64), np.ones(S * B * T), (S, B, T), "per_sequence")
+    assert np.all(close_f32(rewn, want_rew)), rel_err(rewn, want_rew)
+    adv = nr.group_advantages_tensor(nr.Tensor.from_numpy(rewn.reshape(S, B // 8, 8).astype(np.float32)), "std",
+                                     1e-6).to_numpy().astype(np.float64)
+    want_adv = O.group_advantages(rewn.astype(np.float32).astype(np.float64), 8, "std", 1e-6)
+    assert np.all(close_f32(adv.ravel(), want_adv)), rel_err(adv.ravel(), want_adv)
+    assert np.all(np.abs(adv.reshape(-1, 8).sum(axis=1)) < 1e-4), "each group's advantages sum to zero"
