@@ -1098,38 +1098,65 @@ __global__ __launch_bounds__(kScoreThreads) void k_score(ScoreP p) {
                 // The reference logits take the same temperature and vocabulary mask
                 // (reference_kl, rl.rs:347-351).
                 if constexpr (REF) decode_words<DT, MK>(ry[b].x, rx[b].m, vr, p.tau, tau_one);
-                // Move the running maxima to this chunk's, rescaling the sums (online LSE).
-                const float an = fmaxf(st.a, max8(v)), sh = shift_of(an);
-                const float dold = (st.a - sh) * c;
-                const float f = exp2_hw(dold);
-                float eold = 0.0f, shr = 0.0f;
-                if constexpr (REF) {
-                    const float anr = fmaxf(st.ar, max8(vr));
-                    shr = shift_of(anr);
-                    eold = (st.ar - shr) * c;
-                    st.Sr = exp2_hw(eold) * st.Sr;
-                    st.ar = anr;
-                }
-                if constexpr (ENT) st.H = f * (st.H + fmaxf(dold, -FLT_MAX) * st.S);
-                if constexpr (KL) st.B = b_rescaled(st.B, st.S, f, dold, eold);
-                st.S = f * st.S;
-                st.a = an;
-                float w[kEpl], h[kEpl], bb[kEpl], wr[kEpl];
-#pragma unroll
-                for (int j = 0; j < kEpl; j++) {
-                    const float d = (v[j] - sh) * c;
-                    w[j] = exp2_hw(d);
-                    if constexpr (ENT) h[j] = w[j] * fmaxf(d, -FLT_MAX);
+                // The chunk's weights against the lane's current references; the references
+                // move (and the sums are rescaled) only before the first chunk with a finite
+                // value, or when a weight or a sum overflows: then to the chunk's maximum, and
+                // at least 64/c above the old reference.
+                auto rescale = [&](bool pol, bool rf) {
+                    float dold = 0.0f, eold = 0.0f, f = 1.0f;
+                    if (pol) {
+                        const float an = fmaxf(max8_hw(v), st.a + 64.0f / c);
+                        dold = (st.a - shift_of(an)) * c;
+                        f = exp2_hw(dold);
+                        st.a = an;
+                    }
                     if constexpr (REF) {
-                        const float e = (vr[j] - shr) * c;
-                        wr[j] = exp2_hw(e);
-                        if constexpr (KL) bb[j] = w[j] * fmaxf(d - e, -FLT_MAX);
+                        if (rf) {
+                            const float anr = fmaxf(max8_hw(vr), st.ar + 64.0f / c);
+                            eold = (st.ar - shift_of(anr)) * c;
+                            st.Sr = exp2_hw(eold) * st.Sr;
+                            st.ar = anr;
+                        }
+                    }
+                    if constexpr (ENT) st.H = f * (st.H + fmaxf(dold, -FLT_MAX) * st.S);
+                    if constexpr (KL) st.B = b_rescaled(st.B, st.S, f, dold, eold);
+                    st.S = f * st.S;
+                };
+                float S, H, Bk, Sr;
+                auto accumulate = [&]() {
+                    const float sh = shift_of(st.a);
+                    float shr = 0.0f;
+                    if constexpr (REF) shr = shift_of(st.ar);
+                    S = st.S, H = st.H, Bk = st.B, Sr = st.Sr;
+#pragma unroll
+                    for (int j = 0; j < kEpl; j++) {
+                        const float d = (v[j] - sh) * c;
+                        const float w = exp2_hw(d);
+                        S += w;
+                        if constexpr (ENT) H = fmaf(w, fmaxf(d, -FLT_MAX), H);
+                        if constexpr (REF) {
+                            const float e = (vr[j] - shr) * c;
+                            Sr += exp2_hw(e);
+                            if constexpr (KL) Bk = fmaf(w, fmaxf(d - e, -FLT_MAX), Bk);
+                        }
+                    }
+                };
+                {
+                    const bool pol = st.a == -INFINITY, rf = REF && st.ar == -INFINITY;
+                    if (pol || rf) rescale(pol, rf);
+                }
+                accumulate();
+                {
+                    const bool pol = !(S < INFINITY), rf = REF && !(Sr < INFINITY);
+                    if (pol || rf) {
+                        rescale(pol, rf);
+                        accumulate();
                     }
                 }
-                st.S += tree8(w);
-                if constexpr (ENT) st.H += tree8(h);
-                if constexpr (KL) st.B += tree8(bb);
-                if constexpr (REF) st.Sr += tree8(wr);
+                st.S = S;
+                if constexpr (ENT) st.H = H;
+                if constexpr (KL) st.B = Bk;
+                if constexpr (REF) st.Sr = Sr;
             }
         }
     }
