@@ -537,6 +537,9 @@ constexpr int kRRThreads = kRRWaves * kWave;
 #endif
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
+// Word 3 of a gfx9-family buffer resource: 32-bit data format, no swizzle; with stride 0 every
+// access is range-checked against the byte count in word 2.
+constexpr int kBufferWord3 = 0x00020000;
 typedef __attribute__((address_space(1))) void *glb_ptr_t;
 
 template <int B, int E, class F>
@@ -680,25 +683,35 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     // W chunks in flight (all of them at W = K).
     constexpr int W = K < NT_RR_WINDOW ? K : NT_RR_WINDOW;
     Raw<DT, NT_MASK_NONE> raw[K];
+    // Buffer resources over the row's logits and mask bytes: a read at or past the end returns
+    // zeros (mask 0 = excluded), so chunks past the row need no address clamping. All of the
+    // offset goes in the per-lane register, which the hardware range-checks.
+    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void *>(xrow), short(0), int(p.V * Elem<DT>::kBytes), kBufferWord3);
+    __amdgpu_buffer_rsrc_t mres;
+    if constexpr (MK != NT_MASK_NONE)
+        mres = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(mrow), short(0),
+                                                 int(p.V * MaskWords<MK>::kBytes), kBufferWord3);
     auto issue = [&](auto kc) {
         constexpr int k = decltype(kc)::value;
         const int ch = wave + kRRWaves * k;
-        const int64_t e0 = int64_t(ch) * kChunk + lane * kEpl;
-        // Lanes past the row read element 0 (in bounds); their values become -inf below.
-        const int64_t ea = (ch < nc && e0 < p.V) ? e0 : 0;
-        load_raw_inbounds<DT, NT_MASK_NONE>(raw[k], xrow, nullptr, ea);
-        if constexpr (MK != NT_MASK_NONE) {
-            // The chunk's mask bytes [ch*512, ch*512+512) (x4 for f32), one dword per lane per
-            // instruction, into the chunk's slot of mlds (lane l writes slot + 4 l).
-            const int64_t cb = (ch < nc && int64_t(ch) * kChunk < p.V) ? int64_t(ch) * kChunk : 0;
+        const int xo = (ch * kChunk + lane * kEpl) * Elem<DT>::kBytes;
 #pragma unroll
-            for (int d = 0; d < LD; d++) {
-                int64_t off = cb * MaskWords<MK>::kBytes + int64_t(d) * 4 * kWave + 4 * lane;
-                const int64_t lim = p.V * MaskWords<MK>::kBytes - 4;
-                if (off > lim) off = 0;
-                __builtin_amdgcn_global_load_lds((glb_ptr_t)(mrow + off),
-                                                 (lds_ptr_t)(mlds + ch * RRMask<MK>::kBytes + d * 4 * kWave), 4, 0, 0);
-            }
+        for (int q = 0; q < LX; q++) {
+            const auto a = __builtin_amdgcn_raw_buffer_load_b128(xres, xo + 16 * q, 0, 0);
+            raw[k].x[4 * q] = a[0];
+            raw[k].x[4 * q + 1] = a[1];
+            raw[k].x[4 * q + 2] = a[2];
+            raw[k].x[4 * q + 3] = a[3];
+        }
+        if constexpr (MK != NT_MASK_NONE) {
+            // The chunk's mask bytes, one dword per lane per instruction, into the chunk's slot
+            // of mlds (lane l writes slot + 4 l).
+#pragma unroll
+            for (int d = 0; d < LD; d++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    mres, (lds_ptr_t)(mlds + ch * RRMask<MK>::kBytes + d * 4 * kWave), 4,
+                    ch * RRMask<MK>::kBytes + d * 4 * kWave + 4 * lane, 0, 0, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
     };
