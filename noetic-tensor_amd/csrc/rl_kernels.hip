@@ -232,6 +232,17 @@ __device__ __forceinline__ void decode_folded(const Raw<DT, MK> &r, float v[kEpl
 
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// ln x for a finite x >= 2^-1021 in f64, within about 1e-7 absolute: the binary exponent exactly,
+// plus v_log_f32 of the mantissa in [0.5, 1) rounded to f32 (2^-24 relative, then the
+// instruction's 1 ulp). A dozen instructions where the f64 library log takes about a hundred
+// on the row's critical path.
+__device__ __forceinline__ double ln_fast(double x) {
+    const uint64_t b = uint64_t(__double_as_longlong(x));
+    const int e = int((b >> 52) & 0x7ff) - 1022;
+    const double m = __longlong_as_double(int64_t((b & 0x000fffffffffffffull) | (1022ull << 52)));
+    return (double(e) + double(__builtin_amdgcn_logf(float(m)))) * 0.69314718055994530942;
+}
+
 __device__ __forceinline__ float max8(const float v[kEpl]) {
     return fmaxf(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])), fmaxf(fmaxf(v[4], v[5]), fmaxf(v[6], v[7])));
 }
@@ -571,6 +582,42 @@ __device__ __forceinline__ uint4 lds_read_b128(uint32_t addr) {
     return r;
 }
 
+// The LDS inputs of the sampler's chunk scan for one lane, in one round trip: Q chunks' four
+// row partials (Q * 16 contiguous bytes at acs), their Q exponent references (Q * 4 bytes at
+// ark) and one wave maximum (at awm). Q is 1, 2 or 4.
+template <int Q>
+__device__ __forceinline__ void lds_read_scan_inputs(uint32_t acs, uint32_t ark, uint32_t awm, uint4 *cs, uint32_t *rk,
+                                                     uint32_t &wm) {
+    if constexpr (Q == 4) {
+        uint4 r4;
+        asm volatile(
+            "ds_read_b128 %0, %6\n\tds_read_b128 %1, %6 offset:16\n\tds_read_b128 %2, %6 offset:32\n\t"
+            "ds_read_b128 %3, %6 offset:48\n\tds_read_b128 %4, %7\n\tds_read_b32 %5, %8\n\ts_waitcnt lgkmcnt(0)"
+            : "=&v"(cs[0]), "=&v"(cs[1]), "=&v"(cs[2]), "=&v"(cs[3]), "=&v"(r4), "=&v"(wm)
+            : "v"(acs), "v"(ark), "v"(awm)
+            : "memory");
+        rk[0] = r4.x;
+        rk[1] = r4.y;
+        rk[2] = r4.z;
+        rk[3] = r4.w;
+    } else if constexpr (Q == 2) {
+        uint2 r2;
+        asm volatile(
+            "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:16\n\tds_read_b64 %2, %5\n\tds_read_b32 %3, %6\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(cs[0]), "=&v"(cs[1]), "=&v"(r2), "=&v"(wm)
+            : "v"(acs), "v"(ark), "v"(awm)
+            : "memory");
+        rk[0] = r2.x;
+        rk[1] = r2.y;
+    } else {
+        asm volatile("ds_read_b128 %0, %3\n\tds_read_b32 %1, %4\n\tds_read_b32 %2, %5\n\ts_waitcnt lgkmcnt(0)"
+                     : "=&v"(cs[0]), "=&v"(rk[0]), "=&v"(wm)
+                     : "v"(acs), "v"(ark), "v"(awm)
+                     : "memory");
+    }
+}
+
 // v_max3_f32 without the canonicalising moves the compiler puts in front of fmaxf: the inputs
 // are widened logits or -inf, and a NaN among them reaches the row's sum through exp2 anyway.
 __device__ __forceinline__ float max3_hw(float a, float b, float c) {
@@ -587,6 +634,12 @@ __device__ __forceinline__ float max8_hw(const float v[kEpl]) {
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+__device__ __forceinline__ double readlane_d(double v, int l) {
+    const uint64_t b = uint64_t(__double_as_longlong(v));
+    const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b)), l));
+    const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b >> 32)), l));
+    return __longlong_as_double(int64_t((uint64_t(hi) << 32) | lo));
 }
 __device__ __forceinline__ float readlane_f(float v, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
@@ -658,9 +711,9 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     constexpr int LD = RRMask<MK>::kDma;           // mask DMA instructions per chunk
     constexpr int L = LX + LD;
     __shared__ __attribute__((aligned(16))) uint8_t mlds[MK == NT_MASK_NONE ? 16 : NCH * RRMask<MK>::kBytes];
-    __shared__ float csum4[NCH * 4];           // per chunk and 16-lane row: sum of 2^(v c - cref)
+    __shared__ __attribute__((aligned(16))) float csum4[NCH * 4];  // per chunk and 16-lane row: sum of 2^(v c - cref)
     __shared__ float cent4[ENT ? NCH * 4 : 1];  // per chunk and row: sum of w (v c - cref)
-    __shared__ float cref[NCH];   // per chunk: the exponent reference used
+    __shared__ __attribute__((aligned(16))) float cref[NCH];  // per chunk: the exponent reference used
     __shared__ float wmax[kRRWaves];
     __shared__ int wpick[kRRWaves];
     __shared__ int pick_c;
@@ -678,6 +731,8 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     if constexpr (MK != NT_MASK_NONE)
         mrow = static_cast<const uint8_t *>(p.mask) + row * p.mask_ld * MaskWords<MK>::kBytes;
     const uint32_t mbase = uint32_t((uintptr_t)(lds_ptr_t)(mlds));
+    // The row's uniform, read now so that its latency hides under the row's loads.
+    const double u_row = p.greedy ? 0.0 : p.u[row];
 
     // ---- loads: the first W chunks now, chunk k + W as chunk k is consumed, so each wave keeps
     // W chunks in flight (all of them at W = K).
@@ -788,10 +843,26 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     __syncthreads();
 
     // ---- phase 2 (wave 0): exact masked maximum, f64 scan of the chunk sums in index order.
-    float M = -INFINITY;
-    for (int i = 0; i < kRRWaves; i++) M = fmaxf(M, wmax[i]);
-    auto refuse = [&](uint8_t st) {
-        if (tid == 0) {
+    // Every LDS read is issued up front and unconditionally (one round trip); cross-lane values
+    // move by DPP and v_readlane only; the walk is branch-free.
+    constexpr int Q = (NCH + kWave - 1) / kWave;  // chunks per lane of wave 0
+    static_assert(Q == 1 || Q == 2 || Q == 4, "chunks per lane");
+    uint4 cs4[Q];
+    uint32_t rkb[Q], wmb;
+    {
+        // lanes past the last chunk slot read the last one (unused)
+        const int c0 = min(lane * Q, NCH - Q);
+        const uint32_t acs = uint32_t((uintptr_t)(lds_ptr_t)(csum4)) + uint32_t(c0) * 16u;
+        const uint32_t ark = uint32_t((uintptr_t)(lds_ptr_t)(cref)) + uint32_t(c0) * 4u;
+        const uint32_t awm = uint32_t((uintptr_t)(lds_ptr_t)(wmax)) + uint32_t(lane & (kRRWaves - 1)) * 4u;
+        lds_read_scan_inputs<Q>(acs, ark, awm, cs4, rkb, wmb);
+    }
+    float rk[Q];
+#pragma unroll
+    for (int i = 0; i < Q; i++) rk[i] = __uint_as_float(rkb[i]);
+    const float M = wave_max_dpp(__uint_as_float(wmb));
+    auto refuse = [&](uint8_t st, bool leader) {
+        if (leader) {
             p.ids[row] = -1;
             if (p.logp) p.logp[row] = NAN;
             if (p.ent) p.ent[row] = NAN;
@@ -799,83 +870,64 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
         }
     };
     if (M == -INFINITY) {
-        refuse(NT_ROW_NO_TOKEN);
+        refuse(NT_ROW_NO_TOKEN, tid == 0);
         return;
     }
     const float A = M * c;  // >= every chunk reference (rounding is monotonic)
-    auto factor = [&](int ch) -> float {
-        const float r = cref[ch];
-        return r == -INFINITY ? 0.0f : exp2_hw(r - A);
-    };
-    auto csum = [&](int ch) -> float {
-        return (csum4[ch * 4] + csum4[ch * 4 + 1]) + (csum4[ch * 4 + 2] + csum4[ch * 4 + 3]);
-    };
     auto cent = [&](int ch) -> float {
         return (cent4[ch * 4] + cent4[ch * 4 + 1]) + (cent4[ch * 4 + 2] + cent4[ch * 4 + 3]);
     };
     if (wave == 0) {
-        // Lane l takes chunks [4l, 4l + 4) (nc <= 256): their weights f * sum in f64.
-        constexpr int Q = (NCH + kWave - 1) / kWave;
+        // Lane l takes chunks [Q l, Q l + Q): their weights f * sum in f64.
         double wts[Q];
-        float fac[Q];
         double ls = 0.0, lh = 0.0;
 #pragma unroll
         for (int i = 0; i < Q; i++) {
             const int ch = lane * Q + i;
-            fac[i] = 0.0f;
-            wts[i] = 0.0;
-            if (ch < nc) {
-                fac[i] = factor(ch);
-                const float cs = csum(ch);
-                wts[i] = double(fac[i]) * double(cs);
-                if constexpr (ENT) {
-                    if (cs > 0.0f) lh += double(fac[i]) * (double(cent(ch)) + double(cref[ch] - A) * double(cs));
-                }
+            const bool live = ch < nc && rk[i] != -INFINITY;
+            const float f = live ? exp2_hw(rk[i] - A) : 0.0f;
+            const float cs = (__uint_as_float(cs4[i].x) + __uint_as_float(cs4[i].y)) +
+                             (__uint_as_float(cs4[i].z) + __uint_as_float(cs4[i].w));
+            wts[i] = live ? double(f) * double(cs) : 0.0;
+            if constexpr (ENT) {
+                if (live && cs > 0.0f) lh += double(f) * (double(cent(ch)) + double(rk[i] - A) * double(cs));
             }
             ls += wts[i];
         }
         const double incl = wave_scan_dpp(ls);
-        // Every lane runs the shuffle (a disabled source lane would read as 0).
-        const double prev = __shfl_up(incl, 1, kWave);
-        const double excl = lane == 0 ? 0.0 : prev;
-        const double S = __shfl(incl, kWave - 1, kWave);
+        const double S = readlane_d(incl, kWave - 1);
         double H = 0.0;
-        if constexpr (ENT) H = wave_sum_d(lh);
+        if constexpr (ENT) H = readlane_d(wave_scan_dpp(lh), kWave - 1);
         int cstar = -1;
         double tloc = INFINITY;
         if (S == S && !p.greedy) {
-            const double t = p.u[row] * S;
+            const double t = u_row * S;
             const int l = first_lane(__ballot(incl > t && ls > 0.0));
-            int mine = -1;
+            // Every lane walks its own chunks from the prefix before them (incl - ls: the
+            // same f64 value the ballot compared against, up to one rounding); lane l's
+            // result is the one kept.
+            double C = incl - ls;
+            int mine = -1, last = -1;
             double mt = INFINITY;
-            if (l >= 0) {
-                if (lane == l) {
-                    // Walk this lane's chunks from the prefix before them.
-                    double C = excl;
-                    int last = -1;
 #pragma unroll
-                    for (int i = 0; i < Q; i++) {
-                        if (mine < 0 && wts[i] > 0.0) {
-                            last = lane * Q + i;
-                            if (C + wts[i] > t) {
-                                mine = lane * Q + i;
-                                mt = (t - C) / double(fac[i]);
-                            }
-                            C += wts[i];
-                        }
-                    }
-                    if (mine < 0) mine = last;  // rounding between the scan and this walk
-                }
-                cstar = __shfl(mine, l, kWave);
-                tloc = __shfl(mt, l, kWave);
+            for (int i = 0; i < Q; i++) {
+                const bool pos = wts[i] > 0.0;
+                const bool cross = pos && mine < 0 && C + wts[i] > t;
+                // the target in the chunk's own scale: divide by 2^(r - A)
+                const double tl = (t - C) * double(exp2_hw(A - rk[i]));
+                mine = cross ? lane * Q + i : mine;
+                mt = cross ? tl : mt;
+                last = pos ? lane * Q + i : last;
+                C += wts[i];
+            }
+            if (mine < 0) mine = last;  // rounding between the scan and this walk
+            if (l >= 0) {
+                cstar = __builtin_amdgcn_readlane(mine, l);
+                tloc = readlane_d(mt, l);
             } else {
                 // u*S rounded up to S: the last chunk with weight.
-                int last = -1;
-#pragma unroll
-                for (int i = 0; i < Q; i++)
-                    if (wts[i] > 0.0) last = lane * Q + i;
                 const int ll = last_lane(__ballot(last >= 0));
-                cstar = ll >= 0 ? __shfl(last, ll, kWave) : -1;
+                cstar = ll >= 0 ? __builtin_amdgcn_readlane(last, ll) : -1;
             }
         }
         if (lane == 0) {
@@ -888,14 +940,14 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     __syncthreads();
     const double S = pick_S;
     if (!(S == S)) {
-        refuse(NT_ROW_NAN);
+        refuse(NT_ROW_NAN, tid == 0);
         return;
     }
     // ln sum exp(z - m) and the entropy, from the sums relative to A = M c (computed by the
     // one lane that writes the row).
     auto write_row = [&](int64_t id, float vz) {
         const double shiftA = double(A) - double(M) * double(c);
-        const double lnS = log(S) + shiftA * kLn2;
+        const double lnS = ln_fast(S) + shiftA * kLn2;
         const float mz = (MK == NT_MASK_F32 || tau_one) ? M : M / p.tau;
         const float zid = (MK == NT_MASK_F32 || tau_one) ? vz : vz / p.tau;
         p.ids[row] = int32_t(id);
@@ -951,7 +1003,7 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     // ---- phase 3: the wave that owns chunk cstar scans it.
     const int cstar = pick_c;
     if (cstar < 0) {  // unreachable with S > 0; never leave stale outputs
-        refuse(NT_ROW_NAN);
+        refuse(NT_ROW_NAN, tid == 0);
         return;
     }
     if (wave != cstar % kRRWaves) return;
@@ -975,27 +1027,23 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
         if (w[j] > 0.0f) jlast = j;
     }
     const double incl = wave_scan_dpp(ls);
-    const double prev = __shfl_up(incl, 1, kWave);
-    const double excl = lane == 0 ? 0.0 : prev;
     int lsel = first_lane(__ballot(incl > tloc && ls > 0.0));
-    int jsel = -1;
-    if (lsel >= 0) {
-        if (lane == lsel) {
-            double C = excl;
-#pragma unroll
-            for (int j = 0; j < kEpl; j++) {
-                C += double(w[j]);
-                if (jsel < 0 && C > tloc) jsel = j;
-            }
-            if (jsel < 0) jsel = jlast;
-        }
-    } else {
-        lsel = last_lane(__ballot(jlast >= 0));
-        if (lane == lsel) jsel = jlast;
-    }
+    const bool none = lsel < 0;
+    if (none) lsel = last_lane(__ballot(jlast >= 0));  // rounding: the last lane with weight
     if (lsel < 0) {  // unreachable: the chunk holds weight
-        if (lane == 0) refuse(NT_ROW_NAN);
+        refuse(NT_ROW_NAN, lane == 0);
         return;
+    }
+    // The crossing lane walks its elements from the prefix before them.
+    int jsel = -1;
+    {
+        double C = incl - ls;
+#pragma unroll
+        for (int j = 0; j < kEpl; j++) {
+            C += double(w[j]);
+            if (jsel < 0 && !none && C > tloc) jsel = j;
+        }
+        if (jsel < 0) jsel = jlast;
     }
     if (lane == lsel) {
         if (jsel < 0) jsel = 0;
