@@ -654,13 +654,6 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
     v = fmaxf(v, dpp_mov<0x140>(v));
     return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
 }
-__device__ __forceinline__ float wave_sum_dpp(float v) {
-    v = v + dpp_mov<0xB1>(v);
-    v = v + dpp_mov<0x4E>(v);
-    v = v + dpp_mov<0x141>(v);
-    v = v + dpp_mov<0x140>(v);
-    return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
-}
 // One DPP step on an f64: both 32-bit halves move with the same control; lanes with no
 // source (or in rows the row mask leaves out) read 0, the identity of the sum.
 template <int CTRL, int ROWS>
@@ -682,8 +675,8 @@ __device__ __forceinline__ double wave_scan_dpp(double v) {
     return v;
 }
 
-// Sum over each 16-lane row (the first four steps of wave_sum_dpp); every lane of a row holds
-// its row's sum.
+// Sum over each 16-lane row in four DPP steps (the two quad permutes, then the 8- and 16-lane
+// mirrors); every lane of a row holds its row's sum.
 __device__ __forceinline__ float row_sum_dpp(float v) {
     v = v + dpp_mov<0xB1>(v);
     v = v + dpp_mov<0x4E>(v);
@@ -697,20 +690,91 @@ __device__ __forceinline__ int wave_min_i(int v) {
     return v;
 }
 
-// Mask bytes per chunk in LDS, and the LDS DMA instructions that bring one chunk's mask.
-template <int MK>
-struct RRMask {
-    static constexpr int kBytes = MK == NT_MASK_U8 ? kChunk : (MK == NT_MASK_F32 ? 4 * kChunk : 0);
-    static constexpr int kDma = kBytes / (4 * kWave);  // one dword per lane per instruction
+// Per-lane data of one chunk of the register-resident sampler: EPL elements (8 or 16), read
+// as 16-byte pieces (8 bf16 or 4 f32 each).
+template <int DT, int EPL>
+struct RRX {
+    static constexpr int kWords = DT == NT_F32 ? EPL : EPL / 2;
+    static constexpr int kPieces = kWords / 4;
+    uint32_t x[kWords];
 };
 
-template <int DT, int MK, int K, bool ENT>
+// Mask bytes per chunk in LDS and the LDS DMA instructions that bring one chunk's mask: lane l
+// of DMA instruction d writes B bytes at slot + d * 64 B + l B (B = 16 when the chunk's mask is
+// a whole number of 1 KiB, else 4).
+template <int MK, int EPL>
+struct RRMask {
+    static constexpr int kBytes = MK == NT_MASK_U8 ? kWave * EPL : (MK == NT_MASK_F32 ? 4 * kWave * EPL : 0);
+    static constexpr int kDmaBytes = kBytes % (16 * kWave) == 0 ? 16 : 4;
+    static constexpr int kDma = kBytes / (kDmaBytes * kWave);
+    static constexpr int kWords = MK == NT_MASK_U8 ? EPL / 4 : (MK == NT_MASK_F32 ? EPL : 1);  // per lane
+};
+
+// Decode EPL elements (logit words + mask words) into the kernel's value space.
+template <int DT, int MK, int EPL>
+__device__ __forceinline__ void decode_e(const uint32_t *xw, const uint32_t *mw, float *v, float tau, bool tau_one) {
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {
+        const float x = logit<DT>(xw, j);
+        if constexpr (MK == NT_MASK_U8) {
+            const uint32_t keep = (mw[j / 4] >> (8 * (j % 4))) & 0xffu;
+            v[j] = keep ? x : -INFINITY;
+        } else if constexpr (MK == NT_MASK_F32) {
+            const float z = tau_one ? x : x / tau;
+            v[j] = z + __uint_as_float(mw[j]);
+        } else {
+            v[j] = x;
+        }
+    }
+}
+
+// The lane's mask words of one chunk, from its LDS slot (the caller has waited for the DMA).
+template <int MK, int EPL>
+__device__ __forceinline__ void lds_mask_words(uint32_t a, uint32_t *mw) {
+    if constexpr (MK == NT_MASK_U8 && EPL == 8) {
+        const uint2 m2 = lds_read_b64(a);
+        mw[0] = m2.x;
+        mw[1] = m2.y;
+    } else if constexpr (MK != NT_MASK_NONE) {
+#pragma unroll
+        for (int q = 0; q < RRMask<MK, EPL>::kWords / 4; q++) {
+            const uint4 m4 = lds_read_b128(a + 16 * q);
+            mw[4 * q] = m4.x;
+            mw[4 * q + 1] = m4.y;
+            mw[4 * q + 2] = m4.z;
+            mw[4 * q + 3] = m4.w;
+        }
+    } else {
+        mw[0] = 0;
+    }
+}
+
+template <int N>
+__device__ __forceinline__ float max_hw(const float *v) {
+    if constexpr (N == 8) {
+        return max8_hw(v);
+    } else {
+        const float a = max8_hw(v), b = max8_hw(v + 8);
+        return max3_hw(a, b, b);
+    }
+}
+
+template <int N>
+__device__ __forceinline__ float tree_sum(const float *w) {
+    if constexpr (N == 8) return tree8(w);
+    else return tree8(w) + tree8(w + 8);
+}
+
+template <int DT, int MK, int K, bool ENT, int EPL>
 __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
+    constexpr int CH = kWave * EPL;                // elements per chunk
     constexpr int NCH = K * kRRWaves;
-    constexpr int LX = DT == NT_F32 ? 2 : 1;       // logit load instructions per chunk
-    constexpr int LD = RRMask<MK>::kDma;           // mask DMA instructions per chunk
+    constexpr int LX = RRX<DT, EPL>::kPieces;      // logit load instructions per chunk
+    constexpr int LD = RRMask<MK, EPL>::kDma;      // mask DMA instructions per chunk
+    constexpr int MB = RRMask<MK, EPL>::kBytes;    // mask bytes per chunk
+    constexpr int DB = RRMask<MK, EPL>::kDmaBytes;
     constexpr int L = LX + LD;
-    __shared__ __attribute__((aligned(16))) uint8_t mlds[MK == NT_MASK_NONE ? 16 : NCH * RRMask<MK>::kBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t mlds[MK == NT_MASK_NONE ? 16 : NCH * MB];
     __shared__ __attribute__((aligned(16))) float csum4[NCH * 4];  // per chunk and 16-lane row: sum of 2^(v c - cref)
     __shared__ float cent4[ENT ? NCH * 4 : 1];  // per chunk and row: sum of w (v c - cref)
     __shared__ __attribute__((aligned(16))) float cref[NCH];  // per chunk: the exponent reference used
@@ -736,8 +800,10 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
 
     // ---- loads: the first W chunks now, chunk k + W as chunk k is consumed, so each wave keeps
     // W chunks in flight (all of them at W = K).
-    constexpr int W = K < NT_RR_WINDOW ? K : NT_RR_WINDOW;
-    Raw<DT, NT_MASK_NONE> raw[K];
+    // (the same bytes per wave in flight at either chunk size)
+    constexpr int WIN = EPL == 16 ? (NT_RR_WINDOW + 1) / 2 : NT_RR_WINDOW;
+    constexpr int W = K < WIN ? K : WIN;
+    RRX<DT, EPL> raw[K];
     // Buffer resources over the row's logits and mask bytes: a read at or past the end returns
     // zeros (mask 0 = excluded), so chunks past the row need no address clamping. All of the
     // offset goes in the per-lane register, which the hardware range-checks.
@@ -750,7 +816,7 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     auto issue = [&](auto kc) {
         constexpr int k = decltype(kc)::value;
         const int ch = wave + kRRWaves * k;
-        const int xo = (ch * kChunk + lane * kEpl) * Elem<DT>::kBytes;
+        const int xo = (ch * CH + lane * EPL) * Elem<DT>::kBytes;
 #pragma unroll
         for (int q = 0; q < LX; q++) {
             const auto a = __builtin_amdgcn_raw_buffer_load_b128(xres, xo + 16 * q, 0, 0);
@@ -760,13 +826,17 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
             raw[k].x[4 * q + 3] = a[3];
         }
         if constexpr (MK != NT_MASK_NONE) {
-            // The chunk's mask bytes, one dword per lane per instruction, into the chunk's slot
-            // of mlds (lane l writes slot + 4 l).
+            // The chunk's mask bytes, DB bytes per lane per instruction, into the chunk's slot
+            // of mlds (lane l writes slot + DB l).
 #pragma unroll
-            for (int d = 0; d < LD; d++)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    mres, (lds_ptr_t)(mlds + ch * RRMask<MK>::kBytes + d * 4 * kWave), 4,
-                    ch * RRMask<MK>::kBytes + d * 4 * kWave + 4 * lane, 0, 0, 0);
+            for (int d = 0; d < LD; d++) {
+                if constexpr (DB == 16)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(mres, (lds_ptr_t)(mlds + ch * MB + d * DB * kWave), 16,
+                                                             ch * MB + d * DB * kWave + DB * lane, 0, 0, 0);
+                else
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(mres, (lds_ptr_t)(mlds + ch * MB + d * DB * kWave), 4,
+                                                             ch * MB + d * DB * kWave + DB * lane, 0, 0, 0);
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -779,33 +849,23 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
         constexpr int k = decltype(kc)::value;
         const int ch = wave + kRRWaves * k;
         if (ch < nc) {
-            const int64_t e0 = int64_t(ch) * kChunk + lane * kEpl;
-            uint32_t mw[MaskWords<MK>::kWords > 0 ? MaskWords<MK>::kWords : 1];
+            const int64_t e0 = int64_t(ch) * CH + lane * EPL;
+            uint32_t mw[RRMask<MK, EPL>::kWords];
             if constexpr (MK != NT_MASK_NONE) {
                 // Chunks k+1 .. min(K, k+W)-1 may still be in flight.
                 wait_vmcnt<L * ((K < k + W ? K : k + W) - 1 - k)>();
-                const uint32_t a = mbase + ch * RRMask<MK>::kBytes + lane * kEpl * MaskWords<MK>::kBytes;
-                if constexpr (MK == NT_MASK_U8) {
-                    const uint2 m2 = lds_read_b64(a);
-                    mw[0] = m2.x;
-                    mw[1] = m2.y;
-                } else {
-                    const uint4 m0 = lds_read_b128(a), m1 = lds_read_b128(a + 16);
-                    mw[0] = m0.x; mw[1] = m0.y; mw[2] = m0.z; mw[3] = m0.w;
-                    mw[4] = m1.x; mw[5] = m1.y; mw[6] = m1.z; mw[7] = m1.w;
-                }
+                lds_mask_words<MK, EPL>(mbase + ch * MB + lane * EPL * MaskWords<MK>::kBytes, mw);
             } else {
                 mw[0] = 0;
             }
-            float v[kEpl];
-            decode_words<DT, MK>(raw[k].x, mw, v, p.tau, tau_one);
-            if (int64_t(ch + 1) * kChunk > p.V) {  // only the row's last chunk can be partial
-                if (e0 >= p.V) {
+            float v[EPL];
+            decode_e<DT, MK, EPL>(raw[k].x, mw, v, p.tau, tau_one);
+            if (int64_t(ch + 1) * CH > p.V) {  // only the row's last chunk can be partial
 #pragma unroll
-                    for (int j = 0; j < kEpl; j++) v[j] = -INFINITY;
-                }
+                for (int j = 0; j < EPL; j++)
+                    if (e0 + j >= p.V) v[j] = -INFINITY;
             }
-            const float m8 = max8_hw(v);
+            const float m8 = max_hw<EPL>(v);
             lmax = max3_hw(lmax, m8, m8);
             const bool over = fmaf(m8, c, -sref) > 64.0f;
             if (sref == -INFINITY || __ballot(over) != 0) {
@@ -814,15 +874,15 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
             }
             float gs = 0.0f, gh = 0.0f;
             if (sref != -INFINITY) {
-                float w[kEpl], h[kEpl];
+                float w[EPL], h[EPL];
 #pragma unroll
-                for (int j = 0; j < kEpl; j++) {
+                for (int j = 0; j < EPL; j++) {
                     const float d = fmaf(v[j], c, -sref);
                     w[j] = exp2_hw(d);
                     if constexpr (ENT) h[j] = w[j] * fmaxf(d, -FLT_MAX);
                 }
-                gs = tree8(w);
-                if constexpr (ENT) gh = tree8(h);
+                gs = tree_sum<EPL>(w);
+                if constexpr (ENT) gh = tree_sum<EPL>(h);
             }
             // The chunk's four 16-lane row sums (phase 2 adds them in a fixed order).
             const float cs = row_sum_dpp(gs);
@@ -956,24 +1016,15 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
         p.status[row] = NT_ROW_OK;
     };
     // Decode chunk k of this wave again (the mask from LDS; every DMA has completed).
-    auto chunk_values = [&](const Raw<DT, NT_MASK_NONE> &r, int ch, float v[kEpl]) {
-        uint32_t mw[MaskWords<MK>::kWords > 0 ? MaskWords<MK>::kWords : 1];
-        const uint32_t a = mbase + ch * RRMask<MK>::kBytes + lane * kEpl * MaskWords<MK>::kBytes;
-        if constexpr (MK == NT_MASK_U8) {
-            const uint2 m2 = lds_read_b64(a);
-            mw[0] = m2.x;
-            mw[1] = m2.y;
-        } else if constexpr (MK == NT_MASK_F32) {
-            const uint4 m0 = lds_read_b128(a), m1 = lds_read_b128(a + 16);
-            mw[0] = m0.x; mw[1] = m0.y; mw[2] = m0.z; mw[3] = m0.w;
-            mw[4] = m1.x; mw[5] = m1.y; mw[6] = m1.z; mw[7] = m1.w;
-        } else {
-            mw[0] = 0;
-        }
-        decode_words<DT, MK>(r.x, mw, v, p.tau, tau_one);
-        if (int64_t(ch) * kChunk + lane * kEpl >= p.V) {
+    auto chunk_values = [&](const RRX<DT, EPL> &r, int ch, float *v) {
+        uint32_t mw[RRMask<MK, EPL>::kWords];
+        lds_mask_words<MK, EPL>(mbase + ch * MB + lane * EPL * MaskWords<MK>::kBytes, mw);
+        decode_e<DT, MK, EPL>(r.x, mw, v, p.tau, tau_one);
+        if (int64_t(ch + 1) * CH > p.V) {
+            const int64_t e0 = int64_t(ch) * CH + lane * EPL;
 #pragma unroll
-            for (int j = 0; j < kEpl; j++) v[j] = -INFINITY;
+            for (int j = 0; j < EPL; j++)
+                if (e0 + j >= p.V) v[j] = -INFINITY;
         }
     };
 
@@ -984,11 +1035,11 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
             constexpr int k = decltype(kc)::value;
             const int ch = wave + kRRWaves * k;
             if (ch < nc) {
-                float v[kEpl];
+                float v[EPL];
                 chunk_values(raw[k], ch, v);
 #pragma unroll
-                for (int j = kEpl - 1; j >= 0; j--)
-                    if (v[j] == M) first = min(first, ch * kChunk + lane * kEpl + j);
+                for (int j = EPL - 1; j >= 0; j--)
+                    if (v[j] == M) first = min(first, ch * CH + lane * EPL + j);
             }
         });
         first = wave_min_i(first);
@@ -1008,20 +1059,20 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     }
     if (wave != cstar % kRRWaves) return;
     const int kstar = cstar / kRRWaves;
-    Raw<DT, NT_MASK_NONE> r = raw[0];
+    RRX<DT, EPL> r = raw[0];
     static_for<1, K>([&](auto kc) {
         constexpr int k = decltype(kc)::value;
         if (k == kstar) r = raw[k];
     });
-    float v[kEpl];
+    float v[EPL];
     chunk_values(r, cstar, v);
     const float sr = cref[cstar];
     const double tloc = pick_t;
-    float w[kEpl];
+    float w[EPL];
     double ls = 0.0;
     int jlast = -1;
 #pragma unroll
-    for (int j = 0; j < kEpl; j++) {
+    for (int j = 0; j < EPL; j++) {
         w[j] = exp2_hw(fmaf(v[j], c, -sr));
         ls += double(w[j]);
         if (w[j] > 0.0f) jlast = j;
@@ -1039,7 +1090,7 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     {
         double C = incl - ls;
 #pragma unroll
-        for (int j = 0; j < kEpl; j++) {
+        for (int j = 0; j < EPL; j++) {
             C += double(w[j]);
             if (jsel < 0 && !none && C > tloc) jsel = j;
         }
@@ -1049,9 +1100,9 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
         if (jsel < 0) jsel = 0;
         float vz = v[0];
 #pragma unroll
-        for (int j = 1; j < kEpl; j++)
+        for (int j = 1; j < EPL; j++)
             if (j == jsel) vz = v[j];
-        write_row(int64_t(cstar) * kChunk + lane * kEpl + jsel, vz);
+        write_row(int64_t(cstar) * CH + lane * EPL + jsel, vz);
     }
 }
 
@@ -1400,43 +1451,46 @@ void pick_mk_sample(int mk, bool ent, bool al, const SampleP &p, int64_t rows, i
     else pick_ent_sample<DT, NT_MASK_NONE>(ent, al, p, rows, threads, shm, s);
 }
 
-// Largest chunks-per-wave of the register-resident sampler: K chunks of logit words live in
-// VGPRs (bf16 4 per chunk, f32 8) and the mask of every chunk in LDS (u8 512 B, f32 2 KiB).
-int rr_kmax(int dtype, int mk) {
-    if (mk == NT_MASK_F32) return 4;
-    return dtype == NT_BF16 ? 16 : 8;
+// Largest chunks-per-wave of the register-resident sampler at EPL elements per lane: K chunks
+// of logit words live in VGPRs (64 registers: bf16 EPL/2 words per chunk, f32 EPL) and the mask
+// of every chunk in LDS (u8 64 EPL bytes, f32 256 EPL bytes; at most 128 KiB).
+int rr_kmax(int dtype, int mk, int epl) {
+    int k = (dtype == NT_BF16 ? 128 : 64) / epl;
+    if (mk == NT_MASK_F32) k = k < 32 / epl ? k : 32 / epl;  // 16 waves * K * 256 EPL bytes <= 128 KiB
+    return k;
 }
 
-template <int DT, int MK, int K>
+template <int DT, int MK, int K, int EPL>
 void launch_rr_k(bool ent, const SampleP &p, int64_t rows, hipStream_t s) {
-    if (ent) hipLaunchKernelGGL((k_sample_rr<DT, MK, K, true>), dim3(unsigned(rows)), dim3(kRRThreads), 0, s, p);
-    else hipLaunchKernelGGL((k_sample_rr<DT, MK, K, false>), dim3(unsigned(rows)), dim3(kRRThreads), 0, s, p);
+    if (ent) hipLaunchKernelGGL((k_sample_rr<DT, MK, K, true, EPL>), dim3(unsigned(rows)), dim3(kRRThreads), 0, s, p);
+    else hipLaunchKernelGGL((k_sample_rr<DT, MK, K, false, EPL>), dim3(unsigned(rows)), dim3(kRRThreads), 0, s, p);
 }
 
-template <int DT, int MK>
+// K is a power of two up to rr_kmax(DT, MK, EPL); the instantiations are exactly those.
+template <int DT, int MK, int EPL>
 void launch_rr_mk(int K, bool ent, const SampleP &p, int64_t rows, hipStream_t s) {
+    constexpr int KREG = (DT == NT_BF16 ? 128 : 64) / EPL;
+    constexpr int KMAX = MK == NT_MASK_F32 && 32 / EPL < KREG ? 32 / EPL : KREG;
     switch (K) {
-        case 1: launch_rr_k<DT, MK, 1>(ent, p, rows, s); break;
-        case 2: launch_rr_k<DT, MK, 2>(ent, p, rows, s); break;
-        case 4: launch_rr_k<DT, MK, 4>(ent, p, rows, s); break;
-        case 8:
-            if constexpr (MK != NT_MASK_F32) launch_rr_k<DT, MK, 8>(ent, p, rows, s);
-            break;
-        default:
-            if constexpr (DT == NT_BF16 && MK != NT_MASK_F32) launch_rr_k<DT, MK, 16>(ent, p, rows, s);
-            break;
+        case 1: launch_rr_k<DT, MK, 1, EPL>(ent, p, rows, s); break;
+        case 2: launch_rr_k<DT, MK, 2, EPL>(ent, p, rows, s); break;
+        case 4: if constexpr (KMAX >= 4) launch_rr_k<DT, MK, 4, EPL>(ent, p, rows, s); break;
+        case 8: if constexpr (KMAX >= 8) launch_rr_k<DT, MK, 8, EPL>(ent, p, rows, s); break;
+        case 16: if constexpr (KMAX >= 16) launch_rr_k<DT, MK, 16, EPL>(ent, p, rows, s); break;
+        default: break;
     }
 }
 
+template <int EPL>
 void launch_rr(int dtype, int mk, int K, bool ent, const SampleP &p, int64_t rows, hipStream_t s) {
     if (dtype == NT_F32) {
-        if (mk == NT_MASK_U8) launch_rr_mk<NT_F32, NT_MASK_U8>(K, ent, p, rows, s);
-        else if (mk == NT_MASK_F32) launch_rr_mk<NT_F32, NT_MASK_F32>(K, ent, p, rows, s);
-        else launch_rr_mk<NT_F32, NT_MASK_NONE>(K, ent, p, rows, s);
+        if (mk == NT_MASK_U8) launch_rr_mk<NT_F32, NT_MASK_U8, EPL>(K, ent, p, rows, s);
+        else if (mk == NT_MASK_F32) launch_rr_mk<NT_F32, NT_MASK_F32, EPL>(K, ent, p, rows, s);
+        else launch_rr_mk<NT_F32, NT_MASK_NONE, EPL>(K, ent, p, rows, s);
     } else {
-        if (mk == NT_MASK_U8) launch_rr_mk<NT_BF16, NT_MASK_U8>(K, ent, p, rows, s);
-        else if (mk == NT_MASK_F32) launch_rr_mk<NT_BF16, NT_MASK_F32>(K, ent, p, rows, s);
-        else launch_rr_mk<NT_BF16, NT_MASK_NONE>(K, ent, p, rows, s);
+        if (mk == NT_MASK_U8) launch_rr_mk<NT_BF16, NT_MASK_U8, EPL>(K, ent, p, rows, s);
+        else if (mk == NT_MASK_F32) launch_rr_mk<NT_BF16, NT_MASK_F32, EPL>(K, ent, p, rows, s);
+        else launch_rr_mk<NT_BF16, NT_MASK_NONE, EPL>(K, ent, p, rows, s);
     }
 }
 
@@ -1514,13 +1568,20 @@ int nt_hip_rl_sample(const NtRlSampleArgs *a) {
     const bool al = aligned_rows(a->logits, a->vocab, a->ld, a->dtype, a->mask_kind, a->mask, a->mask_ld);
     hipStream_t s = ctx().stream;
     // Rows that fit the register-resident kernel take it (chunks per wave K = 1..16); the
-    // streaming kernel takes everything else (entropy, unaligned rows, larger V).
-    const int kmax = rr_kmax(a->dtype, a->mask_kind);
-    if (al && nc <= int64_t(kRRWaves) * kmax) {
-        int K = 1;
-        while (int64_t(kRRWaves) * K < nc) K *= 2;
-        launch_rr(a->dtype, a->mask_kind, K, ent, p, a->rows, s);
-        return launched("nt_hip_rl_sample");
+    // streaming kernel takes everything else (unaligned rows, larger V).
+    if (al) {
+        // 8 elements per lane (512-element chunks): 16 per lane measured slower on MI355X at c4
+        // (19.37 us, or 18.81 with a one-chunk window, against 18.24-18.52 us at 8).
+        constexpr int epl = 8;
+        const int64_t nch = (a->vocab + kWave * epl - 1) / (kWave * epl);
+        const int kmax = rr_kmax(a->dtype, a->mask_kind, epl);
+        if (nch <= int64_t(kRRWaves) * kmax) {
+            int K = 1;
+            while (int64_t(kRRWaves) * K < nch) K *= 2;
+            p.nc = int(nch);
+            launch_rr<8>(a->dtype, a->mask_kind, K, ent, p, a->rows, s);
+            return launched("nt_hip_rl_sample");
+        }
     }
     if (a->dtype == NT_F32) pick_mk_sample<NT_F32>(a->mask_kind, ent, al, p, a->rows, nw * kWave, shm, s);
     else pick_mk_sample<NT_BF16>(a->mask_kind, ent, al, p, a->rows, nw * kWave, shm, s);
