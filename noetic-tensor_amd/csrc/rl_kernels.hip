@@ -576,6 +576,11 @@ __device__ __forceinline__ uint2 lds_read_b64(uint32_t addr) {
     asm volatile("ds_read_b64 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(addr) : "memory");
     return r;
 }
+__device__ __forceinline__ uint32_t lds_read_b32(uint32_t addr) {
+    uint32_t r;
+    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(addr) : "memory");
+    return r;
+}
 __device__ __forceinline__ uint4 lds_read_b128(uint32_t addr) {
     uint4 r;
     asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(addr) : "memory");
@@ -647,6 +652,16 @@ __device__ __forceinline__ float readlane_f(float v, int l) {
 // Reductions over the 64 lanes: xor-1 and xor-2 quad permutes, the 8- and 16-lane mirrors,
 // then the four rows in a fixed order. Every lane's partial is the same at each step (the
 // operation is commutative), so the result is uniform and independent of timing.
+// The same reduction with v_max3_f32 (no canonicalising moves): the inputs are maxima of
+// widened logits or -inf.
+__device__ __forceinline__ float wave_max3_dpp(float v) {
+    v = max3_hw(v, dpp_mov<0xB1>(v), dpp_mov<0xB1>(v));
+    v = max3_hw(v, dpp_mov<0x4E>(v), dpp_mov<0x4E>(v));
+    v = max3_hw(v, dpp_mov<0x141>(v), dpp_mov<0x141>(v));
+    v = max3_hw(v, dpp_mov<0x140>(v), dpp_mov<0x140>(v));
+    return max3_hw(max3_hw(readlane_f(v, 0), readlane_f(v, 16), readlane_f(v, 32)), readlane_f(v, 48),
+                   readlane_f(v, 48));
+}
 __device__ __forceinline__ float wave_max_dpp(float v) {
     v = fmaxf(v, dpp_mov<0xB1>(v));
     v = fmaxf(v, dpp_mov<0x4E>(v));
@@ -780,8 +795,14 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     __shared__ __attribute__((aligned(16))) float cref[NCH];  // per chunk: the exponent reference used
     __shared__ float wmax[kRRWaves];
     __shared__ int wpick[kRRWaves];
-    __shared__ int pick_c;
-    __shared__ double pick_t, pick_S, pick_H;
+    struct Pick {
+        double t;   // the target inside chunk c, in the chunk's own scale
+        double S;   // sum of 2^(v c - A) over the row
+        double H;   // sum of w (v c - A) (entropy)
+        int c;      // the crossing chunk (-1: none)
+        float sr;   // chunk c's exponent reference
+    };
+    __shared__ __attribute__((aligned(16))) Pick pick;
 
     const int64_t row = blockIdx.x;
     const int tid = threadIdx.x;
@@ -910,17 +931,27 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     uint4 cs4[Q];
     uint32_t rkb[Q], wmb;
     {
-        // lanes past the last chunk slot read the last one (unused)
+        // lanes past the last chunk slot read the last one (unused); only wave 0 reads the
+        // chunk partials (the other waves need the maximum alone)
         const int c0 = min(lane * Q, NCH - Q);
         const uint32_t acs = uint32_t((uintptr_t)(lds_ptr_t)(csum4)) + uint32_t(c0) * 16u;
         const uint32_t ark = uint32_t((uintptr_t)(lds_ptr_t)(cref)) + uint32_t(c0) * 4u;
         const uint32_t awm = uint32_t((uintptr_t)(lds_ptr_t)(wmax)) + uint32_t(lane & (kRRWaves - 1)) * 4u;
-        lds_read_scan_inputs<Q>(acs, ark, awm, cs4, rkb, wmb);
+        if (wave == 0) {
+            lds_read_scan_inputs<Q>(acs, ark, awm, cs4, rkb, wmb);
+        } else {
+            wmb = lds_read_b32(awm);
+#pragma unroll
+            for (int i = 0; i < Q; i++) {
+                cs4[i] = make_uint4(0, 0, 0, 0);
+                rkb[i] = 0;
+            }
+        }
     }
     float rk[Q];
 #pragma unroll
     for (int i = 0; i < Q; i++) rk[i] = __uint_as_float(rkb[i]);
-    const float M = wave_max_dpp(__uint_as_float(wmb));
+    const float M = wave_max3_dpp(__uint_as_float(wmb));
     auto refuse = [&](uint8_t st, bool leader) {
         if (leader) {
             p.ids[row] = -1;
@@ -991,14 +1022,26 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
             }
         }
         if (lane == 0) {
-            pick_c = cstar;
-            pick_t = tloc;
-            pick_S = S;
-            pick_H = H;
+            pick.t = tloc;
+            pick.S = S;
+            pick.H = H;
+            pick.c = cstar;
+        }
+        if (cstar >= 0 && lane == cstar / Q) {
+            // the lane that read chunk cstar's reference publishes it
+            float r = rk[0];
+#pragma unroll
+            for (int i = 1; i < Q; i++)
+                if (cstar % Q == i) r = rk[i];
+            pick.sr = r;
         }
     }
+    // The maximum in z units, for the row's logp; the waiting waves compute it now.
+    float mz = 0.0f;
+    if (wave != 0) mz = (MK == NT_MASK_F32 || tau_one) ? M : M / p.tau;
     __syncthreads();
-    const double S = pick_S;
+    const Pick pk = pick;
+    const double S = pk.S;
     if (!(S == S)) {
         refuse(NT_ROW_NAN, tid == 0);
         return;
@@ -1008,11 +1051,10 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     auto write_row = [&](int64_t id, float vz) {
         const double shiftA = double(A) - double(M) * double(c);
         const double lnS = ln_fast(S) + shiftA * kLn2;
-        const float mz = (MK == NT_MASK_F32 || tau_one) ? M : M / p.tau;
         const float zid = (MK == NT_MASK_F32 || tau_one) ? vz : vz / p.tau;
         p.ids[row] = int32_t(id);
         if (p.logp) p.logp[row] = float(double(zid - mz) - lnS);
-        if (p.ent) p.ent[row] = float(lnS - kLn2 * (pick_H / S + shiftA));
+        if (p.ent) p.ent[row] = float(lnS - kLn2 * (pk.H / S + shiftA));
         p.status[row] = NT_ROW_OK;
     };
     // Decode chunk k of this wave again (the mask from LDS; every DMA has completed).
@@ -1047,17 +1089,21 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
         __syncthreads();
         int best = 0x7fffffff;
         for (int i = 0; i < kRRWaves; i++) best = min(best, wpick[i]);
-        if (tid == 0) write_row(best, M);
+        if (tid == 0) {
+            mz = (MK == NT_MASK_F32 || tau_one) ? M : M / p.tau;
+            write_row(best, M);
+        }
         return;
     }
 
     // ---- phase 3: the wave that owns chunk cstar scans it.
-    const int cstar = pick_c;
+    const int cstar = pk.c;
     if (cstar < 0) {  // unreachable with S > 0; never leave stale outputs
         refuse(NT_ROW_NAN, tid == 0);
         return;
     }
     if (wave != cstar % kRRWaves) return;
+    if (wave == 0) mz = (MK == NT_MASK_F32 || tau_one) ? M : M / p.tau;
     const int kstar = cstar / kRRWaves;
     RRX<DT, EPL> r = raw[0];
     static_for<1, K>([&](auto kc) {
@@ -1066,17 +1112,16 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     });
     float v[EPL];
     chunk_values(r, cstar, v);
-    const float sr = cref[cstar];
-    const double tloc = pick_t;
+    const float sr = pk.sr;
+    const double tloc = pk.t;
     float w[EPL];
-    double ls = 0.0;
     int jlast = -1;
 #pragma unroll
     for (int j = 0; j < EPL; j++) {
         w[j] = exp2_hw(fmaf(v[j], c, -sr));
-        ls += double(w[j]);
         if (w[j] > 0.0f) jlast = j;
     }
+    const double ls = double(tree_sum<EPL>(w));
     const double incl = wave_scan_dpp(ls);
     int lsel = first_lane(__ballot(incl > tloc && ls > 0.0));
     const bool none = lsel < 0;
@@ -1085,14 +1130,16 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
         refuse(NT_ROW_NAN, lane == 0);
         return;
     }
-    // The crossing lane walks its elements from the prefix before them.
+    // The crossing lane walks its elements from the prefix before them (f32 partial sums
+    // inside the lane, compared against the f64 target).
     int jsel = -1;
     {
-        double C = incl - ls;
+        const double t0 = tloc - (incl - ls);
+        float C = 0.0f;
 #pragma unroll
         for (int j = 0; j < EPL; j++) {
-            C += double(w[j]);
-            if (jsel < 0 && !none && C > tloc) jsel = j;
+            C += w[j];
+            if (jsel < 0 && !none && double(C) > t0) jsel = j;
         }
         if (jsel < 0) jsel = jlast;
     }
