@@ -790,10 +790,10 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     constexpr int DB = RRMask<MK, EPL>::kDmaBytes;
     constexpr int L = LX + LD;
     __shared__ __attribute__((aligned(16))) uint8_t mlds[MK == NT_MASK_NONE ? 16 : NCH * MB];
-    __shared__ __attribute__((aligned(16))) float csum4[NCH * 4];  // per chunk and 16-lane row: sum of 2^(v c - cref)
-    __shared__ float cent4[ENT ? NCH * 4 : 1];  // per chunk and row: sum of w (v c - cref)
-    __shared__ __attribute__((aligned(16))) float cref[NCH];  // per chunk: the exponent reference used
-    __shared__ float wmax[kRRWaves];
+    __shared__ __attribute__((aligned(16))) float csum4[NCH * 4];  // per chunk and 16-lane row: sum of 2^(v c - wref)
+    __shared__ float cent4[ENT ? NCH * 4 : 1];  // per chunk and row: sum of w (v c - wref)
+    __shared__ __attribute__((aligned(16))) float wref[kRRWaves];  // per wave: its final exponent reference
+    __shared__ float wmax[kRRWaves];  // per wave: its maximum (greedy) or its reference's source
     __shared__ int wpick[kRRWaves];
     struct Pick {
         double t;   // the target inside chunk c, in the chunk's own scale
@@ -863,9 +863,13 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     };
     static_for<0, W>(issue);
 
-    // ---- phase 1: each chunk as it lands.
-    float lmax = -INFINITY;
-    float sref = -INFINITY;  // this wave's exponent reference, uniform
+    // ---- phase 1: each chunk as it lands. The wave's exponent reference is set from its first
+    // chunk holding an allowed value (its exact maximum) and moves only when a chunk's weights
+    // overflow (a weight or a lane sum of at least 2^128), to that chunk's maximum; the partials
+    // already written are then rescaled. No maximum is taken per chunk otherwise.
+    float lmax = -INFINITY;    // the exact maximum, kept when greedy only
+    float sref = -INFINITY;    // RN(sref_v c), uniform
+    float sref_v = -INFINITY;  // the wave maximum the reference was taken from
     static_for<0, K>([&](auto kc) {
         constexpr int k = decltype(kc)::value;
         const int ch = wave + kRRWaves * k;
@@ -886,15 +890,19 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
                 for (int j = 0; j < EPL; j++)
                     if (e0 + j >= p.V) v[j] = -INFINITY;
             }
-            const float m8 = max_hw<EPL>(v);
-            lmax = max3_hw(lmax, m8, m8);
-            const bool over = fmaf(m8, c, -sref) > 64.0f;
-            if (sref == -INFINITY || __ballot(over) != 0) {
-                const float wm = wave_max_dpp(m8);
-                sref = (wm == -INFINITY) ? -INFINITY : wm * c;
+            if (p.greedy) {
+                const float m8 = max_hw<EPL>(v);
+                lmax = max3_hw(lmax, m8, m8);
+            }
+            if (sref == -INFINITY) {
+                const float wm = wave_max3_dpp(max_hw<EPL>(v));
+                if (wm != -INFINITY) {
+                    sref_v = wm;
+                    sref = wm * c;
+                }
             }
             float gs = 0.0f, gh = 0.0f;
-            if (sref != -INFINITY) {
+            auto weigh = [&]() {
                 float w[EPL], h[EPL];
 #pragma unroll
                 for (int j = 0; j < EPL; j++) {
@@ -904,6 +912,30 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
                 }
                 gs = tree_sum<EPL>(w);
                 if constexpr (ENT) gh = tree_sum<EPL>(h);
+            };
+            if (sref != -INFINITY) {
+                weigh();
+                if (__ballot(!(gs < INFINITY)) != 0) {
+                    // An overflow (or a NaN, which compares false below and stays in the sums).
+                    const float wm = wave_max3_dpp(max_hw<EPL>(v));
+                    const float nref = wm * c;
+                    if (nref > sref) {
+                        const float dk = sref - nref, f = exp2_hw(dk);
+                        if ((lane & 15) == 0) {
+                            // this wave's earlier partials, owned by lanes 0, 16, 32, 48
+                            static_for<0, k>([&](auto jc) {
+                                constexpr int kk = decltype(jc)::value;
+                                const int idx = (wave + kRRWaves * kk) * 4 + lane / 16;
+                                const float o = csum4[idx];
+                                csum4[idx] = f * o;
+                                if constexpr (ENT) cent4[idx] = f * (cent4[idx] + dk * o);
+                            });
+                        }
+                        sref = nref;
+                        sref_v = wm;
+                        weigh();
+                    }
+                }
             }
             // The chunk's four 16-lane row sums (phase 2 adds them in a fixed order).
             const float cs = row_sum_dpp(gs);
@@ -913,17 +945,22 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
                 csum4[ch * 4 + lane / 16] = cs;
                 if constexpr (ENT) cent4[ch * 4 + lane / 16] = ce;
             }
-            if (lane == 0) cref[ch] = sref;
         }
         if constexpr (k + W < K) issue(std::integral_constant<int, k + W>{});
     });
     {
-        const float wm = wave_max_dpp(lmax);
-        if (lane == 0) wmax[wave] = wm;
+        // the wave's maximum when greedy; otherwise the value its reference came from (a lower
+        // bound of its maximum: every sum is taken relative to RN(value c))
+        const float wm = p.greedy ? wave_max3_dpp(lmax) : sref_v;
+        if (lane == 0) {
+            wmax[wave] = wm;
+            wref[wave] = sref;
+        }
     }
     __syncthreads();
 
-    // ---- phase 2 (wave 0): exact masked maximum, f64 scan of the chunk sums in index order.
+    // ---- phase 2 (wave 0): the row's reference value M (the largest wave reference; the exact
+    // maximum when greedy), f64 scan of the chunk sums in index order.
     // Every LDS read is issued up front and unconditionally (one round trip); cross-lane values
     // move by DPP and v_readlane only; the walk is branch-free.
     constexpr int Q = (NCH + kWave - 1) / kWave;  // chunks per lane of wave 0
@@ -935,7 +972,8 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
         // chunk partials (the other waves need the maximum alone)
         const int c0 = min(lane * Q, NCH - Q);
         const uint32_t acs = uint32_t((uintptr_t)(lds_ptr_t)(csum4)) + uint32_t(c0) * 16u;
-        const uint32_t ark = uint32_t((uintptr_t)(lds_ptr_t)(cref)) + uint32_t(c0) * 4u;
+        // chunk ch's reference is its wave's: wref[ch % 16], contiguous for the lane's Q chunks
+        const uint32_t ark = uint32_t((uintptr_t)(lds_ptr_t)(wref)) + uint32_t(c0 % kRRWaves) * 4u;
         const uint32_t awm = uint32_t((uintptr_t)(lds_ptr_t)(wmax)) + uint32_t(lane & (kRRWaves - 1)) * 4u;
         if (wave == 0) {
             lds_read_scan_inputs<Q>(acs, ark, awm, cs4, rkb, wmb);
@@ -964,7 +1002,7 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
         refuse(NT_ROW_NO_TOKEN, tid == 0);
         return;
     }
-    const float A = M * c;  // >= every chunk reference (rounding is monotonic)
+    const float A = M * c;  // >= every wave reference (rounding is monotonic)
     auto cent = [&](int ch) -> float {
         return (cent4[ch * 4] + cent4[ch * 4 + 1]) + (cent4[ch * 4 + 2] + cent4[ch * 4 + 3]);
     };
