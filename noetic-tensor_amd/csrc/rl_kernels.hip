@@ -725,6 +725,21 @@ struct RRMask {
     static constexpr int kWords = MK == NT_MASK_U8 ? EPL / 4 : (MK == NT_MASK_F32 ? EPL : 1);  // per lane
 };
 
+// x if byte 1 (B = 1) or 2 (B = 2) of a mask word is nonzero, else -inf: one SDWA compare
+// (the compiler masks these two bytes with a separate AND; bytes 0 and 3 it already compares
+// in one instruction).
+template <int B>
+__device__ __forceinline__ float keep_byte(uint32_t mw, float x, float ninf) {
+    float r;
+    if constexpr (B == 1)
+        asm("v_cmp_ne_u32_sdwa vcc, %1, 0 src0_sel:BYTE_1 src1_sel:DWORD\n\tv_cndmask_b32 %0, %2, %3, vcc"
+            : "=v"(r) : "v"(mw), "v"(ninf), "v"(x) : "vcc");
+    else
+        asm("v_cmp_ne_u32_sdwa vcc, %1, 0 src0_sel:BYTE_2 src1_sel:DWORD\n\tv_cndmask_b32 %0, %2, %3, vcc"
+            : "=v"(r) : "v"(mw), "v"(ninf), "v"(x) : "vcc");
+    return r;
+}
+
 // Decode EPL elements (logit words + mask words) into the kernel's value space.
 template <int DT, int MK, int EPL>
 __device__ __forceinline__ void decode_e(const uint32_t *xw, const uint32_t *mw, float *v, float tau, bool tau_one) {
@@ -732,8 +747,14 @@ __device__ __forceinline__ void decode_e(const uint32_t *xw, const uint32_t *mw,
     for (int j = 0; j < EPL; j++) {
         const float x = logit<DT>(xw, j);
         if constexpr (MK == NT_MASK_U8) {
-            const uint32_t keep = (mw[j / 4] >> (8 * (j % 4))) & 0xffu;
-            v[j] = keep ? x : -INFINITY;
+            if (j % 4 == 1) {
+                v[j] = keep_byte<1>(mw[j / 4], x, -INFINITY);
+            } else if (j % 4 == 2) {
+                v[j] = keep_byte<2>(mw[j / 4], x, -INFINITY);
+            } else {
+                const uint32_t keep = (mw[j / 4] >> (8 * (j % 4))) & 0xffu;
+                v[j] = keep ? x : -INFINITY;
+            }
         } else if constexpr (MK == NT_MASK_F32) {
             const float z = tau_one ? x : x / tau;
             v[j] = z + __uint_as_float(mw[j]);
@@ -867,6 +888,12 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     // chunk holding an allowed value (its exact maximum) and moves only when a chunk's weights
     // overflow (a weight or a lane sum of at least 2^128), to that chunk's maximum; the partials
     // already written are then rescaled. No maximum is taken per chunk otherwise.
+    // Each chunk's row partial goes to csum4[4 ch + lane / 16]: a per-lane base, plus 256 bytes
+    // per k (an immediate offset).
+    float *const cpart = csum4 + 4 * wave + lane / 16;
+    float *const epart = ENT ? cent4 + 4 * wave + lane / 16 : nullptr;
+    const bool row_leader = (lane & 15) == 0;
+    const int Vi = int(p.V);  // < 2^31 (at most 16 K chunks of CH)
     float lmax = -INFINITY;    // the exact maximum, kept when greedy only
     float sref = -INFINITY;    // RN(sref_v c), uniform
     float sref_v = -INFINITY;  // the wave maximum the reference was taken from
@@ -885,7 +912,7 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
             }
             float v[EPL];
             decode_e<DT, MK, EPL>(raw[k].x, mw, v, p.tau, tau_one);
-            if (int64_t(ch + 1) * CH > p.V) {  // only the row's last chunk can be partial
+            if ((ch + 1) * CH > Vi) {  // only the row's last chunk can be partial
 #pragma unroll
                 for (int j = 0; j < EPL; j++)
                     if (e0 + j >= p.V) v[j] = -INFINITY;
@@ -898,7 +925,7 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
                 const float wm = wave_max3_dpp(max_hw<EPL>(v));
                 if (wm != -INFINITY) {
                     sref_v = wm;
-                    sref = wm * c;
+                    sref = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(wm * c)));
                 }
             }
             float gs = 0.0f, gh = 0.0f;
@@ -931,7 +958,7 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
                                 if constexpr (ENT) cent4[idx] = f * (cent4[idx] + dk * o);
                             });
                         }
-                        sref = nref;
+                        sref = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(nref)));
                         sref_v = wm;
                         weigh();
                     }
@@ -941,9 +968,9 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
             const float cs = row_sum_dpp(gs);
             float ce = 0.0f;
             if constexpr (ENT) ce = row_sum_dpp(gh);
-            if ((lane & 15) == 0) {
-                csum4[ch * 4 + lane / 16] = cs;
-                if constexpr (ENT) cent4[ch * 4 + lane / 16] = ce;
+            if (row_leader) {
+                cpart[64 * k] = cs;
+                if constexpr (ENT) epart[64 * k] = ce;
             }
         }
         if constexpr (k + W < K) issue(std::integral_constant<int, k + W>{});
