@@ -576,6 +576,13 @@ __device__ __forceinline__ uint2 lds_read_b64(uint32_t addr) {
     asm volatile("ds_read_b64 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(addr) : "memory");
     return r;
 }
+template <int OFF>
+__device__ __forceinline__ uint2 lds_read_b64_off(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+    uint2 r;
+    asm volatile("ds_read_b64 %0, %1 offset:%2\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
+    return r;
+}
 __device__ __forceinline__ uint32_t lds_read_b32(uint32_t addr) {
     uint32_t r;
     asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(addr) : "memory");
@@ -725,13 +732,16 @@ struct RRMask {
     static constexpr int kWords = MK == NT_MASK_U8 ? EPL / 4 : (MK == NT_MASK_F32 ? EPL : 1);  // per lane
 };
 
-// x if byte 1 (B = 1) or 2 (B = 2) of a mask word is nonzero, else -inf: one SDWA compare
-// (the compiler masks these two bytes with a separate AND; bytes 0 and 3 it already compares
-// in one instruction).
+// x if byte B (0, 1 or 2) of a mask word is nonzero, else -inf: one SDWA compare against the
+// inline 0 (the compiler masks bytes 1 and 2 with a separate AND and keeps a zero register for
+// byte 0; byte 3 it compares in one instruction).
 template <int B>
 __device__ __forceinline__ float keep_byte(uint32_t mw, float x, float ninf) {
     float r;
-    if constexpr (B == 1)
+    if constexpr (B == 0)
+        asm("v_cmp_ne_u32_sdwa vcc, %1, 0 src0_sel:BYTE_0 src1_sel:DWORD\n\tv_cndmask_b32 %0, %2, %3, vcc"
+            : "=v"(r) : "v"(mw), "v"(ninf), "v"(x) : "vcc");
+    else if constexpr (B == 1)
         asm("v_cmp_ne_u32_sdwa vcc, %1, 0 src0_sel:BYTE_1 src1_sel:DWORD\n\tv_cndmask_b32 %0, %2, %3, vcc"
             : "=v"(r) : "v"(mw), "v"(ninf), "v"(x) : "vcc");
     else
@@ -747,7 +757,9 @@ __device__ __forceinline__ void decode_e(const uint32_t *xw, const uint32_t *mw,
     for (int j = 0; j < EPL; j++) {
         const float x = logit<DT>(xw, j);
         if constexpr (MK == NT_MASK_U8) {
-            if (j % 4 == 1) {
+            if (j % 4 == 0) {
+                v[j] = keep_byte<0>(mw[j / 4], x, -INFINITY);
+            } else if (j % 4 == 1) {
                 v[j] = keep_byte<1>(mw[j / 4], x, -INFINITY);
             } else if (j % 4 == 2) {
                 v[j] = keep_byte<2>(mw[j / 4], x, -INFINITY);
@@ -894,6 +906,9 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     float *const epart = ENT ? cent4 + 4 * wave + lane / 16 : nullptr;
     const bool row_leader = (lane & 15) == 0;
     const int Vi = int(p.V);  // < 2^31 (at most 16 K chunks of CH)
+    // This lane's mask bytes of the wave's chunk k: mlw + k * 16 MB.
+    const uint32_t mlw = mbase + wave * MB + lane * EPL * MaskWords<MK>::kBytes;
+    bool have_ref = false;     // sref set (uniform)
     float lmax = -INFINITY;    // the exact maximum, kept when greedy only
     float sref = -INFINITY;    // RN(sref_v c), uniform
     float sref_v = -INFINITY;  // the wave maximum the reference was taken from
@@ -906,7 +921,14 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
             if constexpr (MK != NT_MASK_NONE) {
                 // Chunks k+1 .. min(K, k+W)-1 may still be in flight.
                 wait_vmcnt<L * ((K < k + W ? K : k + W) - 1 - k)>();
-                lds_mask_words<MK, EPL>(mbase + ch * MB + lane * EPL * MaskWords<MK>::kBytes, mw);
+                constexpr int kOff = k * kRRWaves * MB;
+                if constexpr (MK == NT_MASK_U8 && EPL == 8 && kOff < 65536) {
+                    const uint2 m2 = lds_read_b64_off<kOff < 65536 ? kOff : 0>(mlw);
+                    mw[0] = m2.x;
+                    mw[1] = m2.y;
+                } else {
+                    lds_mask_words<MK, EPL>(mlw + kOff, mw);
+                }
             } else {
                 mw[0] = 0;
             }
@@ -921,9 +943,10 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
                 const float m8 = max_hw<EPL>(v);
                 lmax = max3_hw(lmax, m8, m8);
             }
-            if (sref == -INFINITY) {
+            if (!have_ref) {
                 const float wm = wave_max3_dpp(max_hw<EPL>(v));
                 if (wm != -INFINITY) {
+                    have_ref = true;
                     sref_v = wm;
                     sref = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(wm * c)));
                 }
@@ -940,7 +963,7 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
                 gs = tree_sum<EPL>(w);
                 if constexpr (ENT) gh = tree_sum<EPL>(h);
             };
-            if (sref != -INFINITY) {
+            if (have_ref) {
                 weigh();
                 if (__ballot(!(gs < INFINITY)) != 0) {
                     // An overflow (or a NaN, which compares false below and stays in the sums).
