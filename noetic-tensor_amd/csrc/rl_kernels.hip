@@ -530,22 +530,21 @@ __global__ __launch_bounds__(1024) void k_sample(SampleP p) {
 //
 // For rows of at most 16*K chunks (V <= 131072 for bf16 at K = 16) one 1024-thread workgroup
 // keeps the whole row on chip: each wave's logit words stay in VGPRs (64 registers at K = 16)
-// and the u8 mask is copied by the load unit straight into LDS (global_load_lds, 128 KiB at
-// K = 16). Every wave issues the loads of all its chunks up front, in the order it consumes
-// them, so the whole row is in flight at once and nothing is read twice.
+// and the u8 mask is copied by the load unit straight into LDS (buffer_load ... lds, 128 KiB at
+// K = 16), so nothing is read twice. Each wave keeps one chunk's loads in flight ahead of the
+// chunk it consumes (kRRWindow): phase 1 is VALU-bound, and on MI355X one chunk ahead measured
+// faster than two (17.40 against 17.57 us at c4) or three.
 //
 // Phase 1 (all waves): as each chunk lands, w = 2^(v c - s) with s the wave's exponent
-// reference (its earlier maximum; re-set from the chunk's exact maximum only when an element
-// would exceed it by 2^64, which also covers the first chunk), so no exponential waits on a
-// reduction. The chunk's sum of weights is a fixed-order DPP reduction written to LDS.
-// Phase 2 (wave 0): exact masked maximum, f64 scan over the chunk sums in index order, the
-// chunk that holds u*S. Phase 3 (the owning wave): scan that chunk's registers.
+// reference (the maximum of its first chunk holding an allowed value; moved only when a chunk's
+// weights overflow), so no exponential waits on a reduction. The chunk's sum of weights is a
+// fixed-order DPP reduction written to LDS as four 16-lane partials.
+// Phase 2 (wave 0): f64 scan over the chunk sums in index order, the chunk that holds u*S.
+// Phase 3 (the owning wave): scan that chunk's registers.
 
 constexpr int kRRWaves = 16;
 constexpr int kRRThreads = kRRWaves * kWave;
-#ifndef NT_RR_WINDOW
-#define NT_RR_WINDOW 2
-#endif
+constexpr int kRRWindow = 1;  // chunks in flight ahead of the one being consumed
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 // Word 3 of a gfx9-family buffer resource: 32-bit data format, no swizzle; with stride 0 every
@@ -853,10 +852,8 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     const double u_row = p.greedy ? 0.0 : p.u[row];
 
     // ---- loads: the first W chunks now, chunk k + W as chunk k is consumed, so each wave keeps
-    // W chunks in flight (all of them at W = K).
-    // (the same bytes per wave in flight at either chunk size)
-    constexpr int WIN = EPL == 16 ? (NT_RR_WINDOW + 1) / 2 : NT_RR_WINDOW;
-    constexpr int W = K < WIN ? K : WIN;
+    // W chunks in flight.
+    constexpr int W = K < kRRWindow ? K : kRRWindow;
     RRX<DT, EPL> raw[K];
     // Buffer resources over the row's logits and mask bytes: a read at or past the end returns
     // zeros (mask 0 = excluded), so chunks past the row need no address clamping. All of the

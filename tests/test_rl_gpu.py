@@ -114,7 +114,7 @@ def test_c2_decode_parity():
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
-@pytest.mark.parametrize("V", [1, 7, 1001, 4099])
+@pytest.mark.parametrize("V", [1, 7, 1000, 1001, 1008, 4099])
 def test_ragged_and_unaligned_rows(dtype, V):
     rng = np.random.default_rng(V)
     rows = 33
