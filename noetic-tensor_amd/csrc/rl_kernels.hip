@@ -531,9 +531,10 @@ __global__ __launch_bounds__(1024) void k_sample(SampleP p) {
 // For rows of at most 16*K chunks (V <= 131072 for bf16 at K = 16) one 1024-thread workgroup
 // keeps the whole row on chip: each wave's logit words stay in VGPRs (64 registers at K = 16)
 // and the u8 mask is copied by the load unit straight into LDS (buffer_load ... lds, 128 KiB at
-// K = 16), so nothing is read twice. Each wave keeps one chunk's loads in flight ahead of the
-// chunk it consumes (kRRWindow): phase 1 is VALU-bound, and on MI355X one chunk ahead measured
-// faster than two (17.40 against 17.57 us at c4) or three.
+// K = 16), so nothing is read twice. Each wave issues chunk k + 1 while it processes chunk k,
+// after decoding it (kRRWindow = 1): phase 1 is VALU-bound, and on MI355X that measured faster
+// than two or three chunks ahead (17.40 against 17.57 and 18.27 us at c4, before the issue point
+// moved into the chunk).
 //
 // Phase 1 (all waves): as each chunk lands, w = 2^(v c - s) with s the wave's exponent
 // reference (the maximum of its first chunk holding an allowed value; moved only when a chunk's
@@ -851,8 +852,7 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     // The row's uniform, read now so that its latency hides under the row's loads.
     const double u_row = p.greedy ? 0.0 : p.u[row];
 
-    // ---- loads: the first W chunks now, chunk k + W as chunk k is consumed, so each wave keeps
-    // W chunks in flight.
+    // ---- loads: the first W chunks now, chunk k + W while chunk k is consumed.
     constexpr int W = K < kRRWindow ? K : kRRWindow;
     RRX<DT, EPL> raw[K];
     // Buffer resources over the row's logits and mask bytes: a read at or past the end returns
@@ -936,6 +936,10 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
                 for (int j = 0; j < EPL; j++)
                     if (e0 + j >= p.V) v[j] = -INFINITY;
             }
+            // The next chunk's loads go out once this chunk's data is in registers: between one
+            // and two chunks in flight per wave (measured faster than issuing after the chunk,
+            // 17.11 against 17.38 us at c4, and than two whole chunks ahead).
+            if constexpr (k + W < K) issue(std::integral_constant<int, k + W>{});
             if (p.greedy) {
                 const float m8 = max_hw<EPL>(v);
                 lmax = max3_hw(lmax, m8, m8);
@@ -993,7 +997,9 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
                 if constexpr (ENT) epart[64 * k] = ce;
             }
         }
-        if constexpr (k + W < K) issue(std::integral_constant<int, k + W>{});
+        if constexpr (k + W < K) {
+            if (!(ch < nc)) issue(std::integral_constant<int, k + W>{});  // (no chunk here to process)
+        }
     });
     {
         // the wave's maximum when greedy; otherwise the value its reference came from (a lower
