@@ -377,3 +377,42 @@ def test_c5_full_size_scoring_and_group_advantages():
     want_adv = O.group_advantages(rewn.astype(np.float32).astype(np.float64), 8, "std", 1e-6)
     assert np.all(close_f32(adv.ravel(), want_adv)), rel_err(adv.ravel(), want_adv)
     assert np.all(np.abs(adv.reshape(-1, 8).sum(axis=1)) < 1e-4), "each group's advantages sum to zero"
+
+
+@pytest.mark.parametrize("case", [
+    # (dtype, mask kind, broadcast mask, V, temperature, entropy)
+    ("bf16", "u8", True, 128256, 0.7, False),   # c4's shape with one shared [1, V] grammar mask
+    ("bf16", "u8", False, 128256, 0.7, True),   # c4 with the entropy output (register-resident)
+    ("f32", "f32", False, 32768, 0.8, True),    # additive f32 mask at the register-resident limit
+    ("f32", "f32", True, 20000, 1.0, False),    # additive mask shared by every row, temperature 1
+    ("f32", "u8", False, 65536, 1.3, False),    # f32 logits, u8 mask, the largest f32 row kept in VGPRs
+    ("bf16", "none", False, 131072, 0.5, True), # no mask, the largest register-resident bf16 row
+])
+def test_sampler_mask_layouts_against_the_oracle(case):
+    dtype, mk, shared, V, tau, want_ent = case
+    rows = 48
+    rng = np.random.default_rng(V + int(100 * tau))
+    x = rng.normal(0, 2, (rows, V)).astype(np.float32)
+    if dtype == "bf16":
+        xb = O.bf16_from_f32(x)
+        x = O.bf16_to_f32(xb)
+        xt = nr.Tensor.from_numpy(xb, "bf16")
+    else:
+        xt = nr.Tensor.from_numpy(x)
+    mrows = 1 if shared else rows
+    keep = add = mt = None
+    if mk == "u8":
+        keep = (rng.random((mrows, V)) < 0.3).astype(np.uint8)
+        keep[:, rng.integers(0, V)] = 1
+        mt = nr.Tensor.from_numpy(keep)
+    elif mk == "f32":
+        add = np.where(rng.random((mrows, V)) < 0.5, 0.0, -np.inf).astype(np.float32)
+        add[:, ::97] = -1e9
+        add[:, rng.integers(0, V)] = 0.0
+        mt = nr.Tensor.from_numpy(add)
+    u = nr.Rng(V, "mask layouts").uniforms(rows)
+    out = nr.sample_logp(xt, tau, mt, None, entropy=want_ent, uniforms=nr.Tensor.from_numpy(u, "f64"))
+    ids, lp = out[0].to_numpy().ravel(), out[1].to_numpy().ravel()
+    z = O.tempered(x, tau, addmask=add, keep=keep)
+    ent = out[2].to_numpy().ravel() if want_ent else None
+    check_sample(f"{case}", z, u, ids, lp, ent, bf16=False)
