@@ -8,10 +8,12 @@ stream. Prints one JSON line (the driver's contract) with a `roofline` object (a
 bytes per launch / average launch time against the 8 TB/s HBM peak) and a `cpu_baseline`
 object (the reference's Cpu(Reference) op sequence, restated in oracle/, timed on this host).
 
-`--workload c2|c3|c5` measures the other configurations the same way, one JSON line each:
+`--workload c2|c3|c3b|c5` measures the other configurations the same way, one JSON line each:
   c2  decode step, f32 [1,64,1,32000], no mask, tau 0.8: the fused sample + logp;
   c3  PPO scoring, bf16 policy + reference [8,16,512,50304]: logp, reference logp, exact KL,
       entropy (nt_hip_rl_score) and the k3 per-token KL (nt_hip_rl_kl_estimate);
+  c3b the c3 scoring forward plus its fused backward (nt_hip_rl_score_backward): the gradient
+      of g_logp logp + g_kl KL + g_H H with respect to the logits, in bf16;
   c5  rollout scoring, f32 [4,32,1024,151936] + u8 mask: logp and entropy (nt_hip_rl_score),
       the per-sequence mean log-probability (nt_hip_rl_reduce_tokens) and group-relative
       advantages over groups of 8 along B (host f64, where the reference computes them).
@@ -41,6 +43,45 @@ def hip_events():
     hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
     hip.hipEventDestroy.argtypes = [C.c_void_p]
     return hip
+
+
+def cpu_model():
+    """The host CPU's model name (Linux /proc/cpuinfo), for the baseline's record."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def copy_peak(nr, nbytes=1 << 29, reps=10):
+    """A measured streaming-copy rate on this device: device-to-device hipMemcpyAsync of nbytes on
+    the library's stream, read + write bytes over the HIP-event time (GB/s)."""
+    hip = hip_events()
+    hip.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+    src, dst = nr.Buffer(nbytes), nr.Buffer(nbytes)
+    stream = C.c_void_p()
+    nr._check(nr.lib().nt_hip_stream(C.byref(stream)), "stream")
+    d2d = 3  # hipMemcpyDeviceToDevice
+    for _ in range(2):
+        hip.hipMemcpyAsync(C.c_void_p(dst.ptr), C.c_void_p(src.ptr), nbytes, d2d, stream)
+    nr.sync()
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    hip.hipEventCreate(C.byref(e0))
+    hip.hipEventCreate(C.byref(e1))
+    hip.hipEventRecord(e0, stream)
+    for _ in range(reps):
+        hip.hipMemcpyAsync(C.c_void_p(dst.ptr), C.c_void_p(src.ptr), nbytes, d2d, stream)
+    hip.hipEventRecord(e1, stream)
+    hip.hipEventSynchronize(e1)
+    ms = C.c_float()
+    hip.hipEventElapsedTime(C.byref(ms), e0, e1)
+    hip.hipEventDestroy(e0)
+    hip.hipEventDestroy(e1)
+    return 2 * nbytes * reps / (ms.value * 1e-3) / 1e9
 
 
 def timed(nr, steps, warmup, step):
@@ -115,7 +156,7 @@ def cpu_baseline(w, rows_sample, seed, min_seconds=10.0):
     O.cpu_sample_logp_invcdf(x, w["temperature"], keep, u, threads=cores)
     t_fast = time.perf_counter() - t0
     return {
-        "value": reps * rows_sample / t_ref, "unit": "rows/s", "cores": 1, "kind": "port",
+        "value": reps * rows_sample / t_ref, "unit": "rows/s", "cores": 1, "kind": "port", "cpu": cpu_model(),
         "sample": f"{reps} x {rows_sample} {w['name']} rows (V={V}, values widened to f32): the reference's "
                   f"Cpu(Reference) op sequence with Gumbel-max sampling, single thread, {t_ref:.2f} s",
         "fast_port": {"value": rows_sample / t_fast, "unit": "rows/s", "cores": cores,
@@ -149,7 +190,7 @@ def cpu_baseline_scoring(w, rows_sample, min_seconds=10.0):
             O.kl(z, r)
         t += time.perf_counter() - t0
         reps += 1
-    return {"value": reps * rows_sample / t, "unit": "rows/s", "cores": 1, "kind": "port",
+    return {"value": reps * rows_sample / t, "unit": "rows/s", "cores": 1, "kind": "port", "cpu": cpu_model(),
             "sample": f"{reps} x {rows_sample} {w['name']} rows (V={V}): the oracle's f64 scoring restatement "
                       f"(tempered values, log-softmax gather, {'exact KL, ' if y is not None else ''}entropy), "
                       f"single thread, {t:.2f} s"}
@@ -180,6 +221,8 @@ def bench_sample(nr, W, args, name):
     per_row = esz * V + (V if mk == nr.NT_MASK_U8 else 0) + 8 + 4 + 4 + 1  # logits, mask, uniform, id, logp, status
     bytes_launch = per_row * rows
     roof = roofline(bytes_launch, ms, "k_sample_rr_c4_traffic.json" if name == "c4" else None)
+    if name == "c4":
+        roof["measured_copy_gbs"] = copy_peak(nr)  # a device-to-device copy on this box, for scale
     if name == "c4":
         metric = "rows/sec + achieved HBM GB/s, fused masked sample+logprob, V=128256 bf16"
         config = {"workload": "c4 constrained decode: bf16 logits [1,256,1,128256] ~ N(0,2^2), u8 grammar mask "
@@ -264,13 +307,84 @@ def bench_score(nr, W, args, name):
     return out
 
 
+def bench_score_grad(nr, W, args):
+    """c3b: the c3 PPO step's scoring forward (nt_hip_rl_score with the per-row log-sum-exp saved)
+    and its fused backward (nt_hip_rl_score_backward: d(g_logp logp + g_kl KL + g_H H)/d logits,
+    written in the logits' dtype), one of each per step."""
+    w = W.c3(args.seed)
+    rows, V = w["rows"], w["V"]
+    shp = w["logits"].shape[:-1]
+    L = nr.lib()
+    out_t = lambda: nr.Tensor(shp, "f32")
+    lp, rlp, kl, ent, status = out_t(), out_t(), out_t(), out_t(), nr.Tensor(shp, "u8")
+    lb, lr, rlb, rlr = out_t(), out_t(), out_t(), out_t()
+    a = nr.NtRlScoreArgs(w["logits"].ptr, w["ref"].ptr, nr.NT_BF16, nr.NT_MASK_NONE, rows, V, V, None, 0,
+                         w["temperature"], w["tokens"].ptr, lp.ptr, rlp.ptr, kl.ptr, ent.ptr, status.ptr, lb.ptr,
+                         lr.ptr, rlb.ptr, rlr.ptr)
+    # upstream gradients of a GRPO-style loss: advantages on logp, beta = 0.04 on KL, -0.01 on entropy
+    rng = np.random.default_rng(args.seed)
+    g_lp = nr.Tensor.from_numpy(rng.normal(0, 1, shp).astype(np.float32))
+    g_kl = nr.Tensor.from_numpy(np.full(shp, 0.04, np.float32))
+    g_h = nr.Tensor.from_numpy(np.full(shp, -0.01, np.float32))
+    grad = nr.Tensor(w["logits"].shape, "bf16")
+    b = nr.NtRlScoreGradArgs(w["logits"].ptr, w["ref"].ptr, nr.NT_BF16, nr.NT_MASK_NONE, rows, V, V, None, 0,
+                             w["temperature"], w["tokens"].ptr, lb.ptr, lr.ptr, rlb.ptr, rlr.ptr, kl.ptr, ent.ptr,
+                             g_lp.ptr, g_kl.ptr, g_h.ptr, grad.ptr, nr.NT_BF16, 0, V)
+    fwd = lambda i: L.nt_hip_rl_score(C.byref(a))
+    bwd = lambda i: L.nt_hip_rl_score_backward(C.byref(b))
+    nr._check(fwd(0), "score")
+    nr._check(bwd(0), "score backward")
+    if np.any(status.to_numpy() != 0):
+        raise SystemExit("bench: refused rows")
+    ms_bwd, _ = timed(nr, args.steps, args.warmup, bwd)
+    ms, wall = timed(nr, args.steps, args.warmup, lambda i: (fwd(i), bwd(i)))
+    # backward, per row: policy and reference logits read, the gradient written (bf16), and the
+    # token, four log-sum-exp values, KL, entropy and three upstream gradients read
+    bytes_bwd = rows * (2 * 2 * V + 2 * V + 4 + 4 * 4 + 4 + 4 + 3 * 4)
+    roof = roofline(bytes_bwd, ms_bwd)
+    roof["kernel"] = "k_score_grad"
+    roof["kernel_ms"] = ms_bwd
+    metric = "rows/sec + achieved HBM GB/s, fused PPO scoring forward + backward (logp, KL, entropy), V=50304 bf16"
+    config = {"workload": "c3b PPO scoring forward and backward: bf16 policy + reference [8,16,512,50304] as c3; "
+                          "forward logp, ref logp, exact KL, entropy; backward d(g_logp logp + 0.04 KL - 0.01 H)/d "
+                          "logits in bf16, g_logp ~ N(0,1)", "rows": rows, "vocab": V, "parallelism": "none (1 GPU)"}
+    out = line(metric, rows / (ms * 1e-3), args.steps, args.warmup, ms, "bf16", config, roof,
+               achieved_gbs=roof["achieved"], wall_s_timed_region=wall, key=nr.key())
+    if args.cpu_rows > 0:
+        out["cpu_baseline"] = cpu_baseline_score_grad(w, min(args.cpu_rows, 16), args.cpu_seconds)
+    return out
+
+
+def cpu_baseline_score_grad(w, rows_sample, min_seconds=10.0):
+    """The oracle's forward statistics and f64 gradient of a bounded row sample on one host core."""
+    import workloads as W
+    from oracle import oracle as O
+    V = w["V"]
+    x = W.bf16_to_f32(W.download_rows(w["logits"], range(rows_sample), V))
+    y = W.bf16_to_f32(W.download_rows(w["ref"], range(rows_sample), V))
+    tok = w["tokens"].to_numpy().ravel()[:rows_sample].astype(np.int64)
+    g_lp = np.random.default_rng(1).normal(0, 1, rows_sample)
+    reps, t = 0, 0.0
+    while reps < 1 or (t < min_seconds and reps < 1000):
+        t0 = time.perf_counter()
+        O.token_logp(x, tok)
+        O.token_logp(y, tok)
+        O.score_grad(x, tok, y, g_lp, np.full(rows_sample, 0.04), np.full(rows_sample, -0.01))
+        t += time.perf_counter() - t0
+        reps += 1
+    return {"value": reps * rows_sample / t, "unit": "rows/s", "cores": 1, "kind": "port", "cpu": cpu_model(),
+            "sample": f"{reps} x {rows_sample} c3 rows (V={V}): the oracle's f64 forward (logp, ref logp) and "
+                      f"gradient of g_logp logp + 0.04 KL - 0.01 H (row statistics, KL, entropy, then each "
+                      f"element), single thread, {t:.2f} s"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default 200; 20 for c3/c5)")
     ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 20; 3 for c3/c5)")
     ap.add_argument("--seed", type=int, default=2024)
-    ap.add_argument("--workload", default="c4", choices=["c4", "c2", "c3", "c5"])
+    ap.add_argument("--workload", default="c4", choices=["c4", "c2", "c3", "c3b", "c5"])
     ap.add_argument("--cpu-rows", type=int, default=256, help="rows of the CPU baseline sample (0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="repeat the CPU sample up to this long")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -290,7 +404,7 @@ def main():
         print(json.dumps({"error": f"--gpus {args.gpus}: this build measures one GPU; the path shards by rows "
                                    "with no exchange, and multi-GPU runs are not part of it"}))
         sys.exit(2)
-    big = args.workload in ("c3", "c5")
+    big = args.workload in ("c3", "c3b", "c5")
     if args.steps is None:
         args.steps = 20 if big else 200
     if args.warmup is None:
@@ -302,6 +416,8 @@ def main():
     nr.claim(0)
     if args.workload in ("c4", "c2"):
         out = bench_sample(nr, W, args, args.workload)
+    elif args.workload == "c3b":
+        out = bench_score_grad(nr, W, args)
     else:
         out = bench_score(nr, W, args, args.workload)
     print(json.dumps(out), flush=True)

@@ -134,8 +134,56 @@ typedef struct NtRlScoreArgs {
     float *kl;                /* [rows] out or NULL */
     float *entropy;           /* [rows] out or NULL */
     uint8_t *status;          /* [rows] out or NULL: NT_ROW_* of the policy row */
+    /* The row's log-sum-exp, for nt_hip_rl_score_backward: lse = lse_base + lse_rest with
+     * lse_base a finite point at most 128 ln 2 below the maximum of the tempered logits (the
+     * maximum itself for most rows) and lse_rest = ln sum exp(z - lse_base); both NaN on a
+     * refused row. Any of the four may be NULL. */
+    float *lse_base;          /* [rows] out or NULL (policy) */
+    float *lse_rest;          /* [rows] out or NULL (policy) */
+    float *ref_lse_base;      /* [rows] out or NULL (reference; needs ref_logits) */
+    float *ref_lse_rest;      /* [rows] out or NULL (reference) */
 } NtRlScoreArgs;
 int nt_hip_rl_score(const NtRlScoreArgs *a);
+
+/* The fused backward of nt_hip_rl_score: for each row, the gradient with respect to the raw
+ * logits x of
+ *   g_logp[r] * logp[r] + g_kl[r] * kl[r] + g_entropy[r] * entropy[r]
+ * with z = x / T + mask (tempered_logits, rl.rs:475-486), pi = softmax(z), log pi_v =
+ * (z_v - lse_base) - lse_rest:
+ *   dlogp/dz_v    = [v == token] - pi_v                     (log_softmax backward,
+ *                                                            activation.rs:36-41, gathered)
+ *   dkl/dz_v      = pi_v ((log pi_v - log pi_ref,v) - kl)   (categorical_kl, rl.rs:327-338;
+ *                                                            the reference is detached)
+ *   dentropy/dz_v = -pi_v (log pi_v + entropy)              (categorical_entropy, rl.rs:405-414)
+ *   dL/dx_v       = dL/dz_v / T                             (the divide's backward)
+ * An entry with pi_v = 0 (excluded, or -inf) gets only the token term. Inputs are the forward's
+ * outputs for the same logits, temperature and mask (the statistics from nt_hip_rl_score). The
+ * gradient is written in grad_dtype (bf16 by round-to-nearest-even from the f32 value, as the
+ * reference stores a bf16 tensor's gradient), row stride grad_ld. One pass reads each logit
+ * (and reference logit) once and writes each gradient element once. */
+typedef struct NtRlScoreGradArgs {
+    const void *logits;       /* [rows, ld] policy logits (NT_F32 | NT_BF16) */
+    const void *ref_logits;   /* [rows, ld] reference logits; needed when g_kl is given */
+    int32_t dtype;
+    int32_t mask_kind;
+    int64_t rows, vocab, ld;
+    const void *mask;
+    int64_t mask_ld;
+    double temperature;       /* > 0 and finite; the forward's */
+    const int32_t *tokens;    /* [rows]; needed when g_logp is given */
+    const float *lse_base, *lse_rest;          /* [rows] from the forward (policy) */
+    const float *ref_lse_base, *ref_lse_rest;  /* [rows] from the forward (reference) */
+    const float *kl;          /* [rows] the forward's exact KL; needed when g_kl is given */
+    const float *entropy;     /* [rows] the forward's entropy; needed when g_entropy is given */
+    const float *g_logp;      /* [rows] upstream gradients, or NULL (zero) */
+    const float *g_kl;
+    const float *g_entropy;
+    void *grad;               /* [rows, grad_ld] out */
+    int32_t grad_dtype;       /* NT_F32 | NT_BF16 */
+    int32_t pad0;
+    int64_t grad_ld;
+} NtRlScoreGradArgs;
+int nt_hip_rl_score_backward(const NtRlScoreGradArgs *a);
 
 /* kl_estimate per sampled token (rl.rs:380-400), elementwise over n = S*B*T values:
  * delta = ref_logp - logp, zeroed where mask == 0 (a select, rl.rs:100-102), clamped to

@@ -656,11 +656,9 @@ __device__ __forceinline__ double readlane_d(double v, int l) {
 __device__ __forceinline__ float readlane_f(float v, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
-// Reductions over the 64 lanes: xor-1 and xor-2 quad permutes, the 8- and 16-lane mirrors,
-// then the four rows in a fixed order. Every lane's partial is the same at each step (the
-// operation is commutative), so the result is uniform and independent of timing.
-// The same reduction with v_max3_f32 (no canonicalising moves): the inputs are maxima of
-// widened logits or -inf.
+// Maximum over the 64 lanes: xor-1 and xor-2 quad permutes, the 8- and 16-lane mirrors, then
+// the four rows in a fixed order, each step a v_max3_f32 (no canonicalising moves; the inputs
+// are maxima of widened logits or -inf). The result is uniform and independent of timing.
 __device__ __forceinline__ float wave_max3_dpp(float v) {
     v = max3_hw(v, dpp_mov<0xB1>(v), dpp_mov<0xB1>(v));
     v = max3_hw(v, dpp_mov<0x4E>(v), dpp_mov<0x4E>(v));
@@ -668,13 +666,6 @@ __device__ __forceinline__ float wave_max3_dpp(float v) {
     v = max3_hw(v, dpp_mov<0x140>(v), dpp_mov<0x140>(v));
     return max3_hw(max3_hw(readlane_f(v, 0), readlane_f(v, 16), readlane_f(v, 32)), readlane_f(v, 48),
                    readlane_f(v, 48));
-}
-__device__ __forceinline__ float wave_max_dpp(float v) {
-    v = fmaxf(v, dpp_mov<0xB1>(v));
-    v = fmaxf(v, dpp_mov<0x4E>(v));
-    v = fmaxf(v, dpp_mov<0x141>(v));
-    v = fmaxf(v, dpp_mov<0x140>(v));
-    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
 }
 // One DPP step on an f64: both 32-bit halves move with the same control; lanes with no
 // source (or in rows the row mask leaves out) read 0, the identity of the sum.
@@ -1258,6 +1249,7 @@ struct ScoreP {
     const int32_t *tokens;
     float *logp, *ref_logp, *kl, *ent;
     uint8_t *status;
+    float *lse_base, *lse_rest, *ref_lse_base, *ref_lse_rest;
 };
 
 // Running state of one lane (value space, exponent scale c). Every sum is relative to the
@@ -1472,8 +1464,14 @@ __global__ __launch_bounds__(kScoreThreads) void k_score(ScoreP p) {
     const bool rowok = stt == NT_ROW_OK || stt == kRowBadToken;
     if (p.logp) p.logp[row] = stt == NT_ROW_OK ? float(double(ztok(xrow, tok) - zmax(af)) - lnS) : NAN;
     if (p.ent) p.ent[row] = rowok ? float(lnS - kLn2 * H / S) : NAN;
+    // The log-sum-exp as base + rest (z units): the base is the tempered value of the row's
+    // final reference, the rest ln of the sum relative to it.
+    if (p.lse_base) p.lse_base[row] = rowok ? zmax(af) : NAN;
+    if (p.lse_rest) p.lse_rest[row] = rowok ? float(lnS) : NAN;
     if constexpr (REF) {
         const bool rok = arf != -INFINITY && Sr == Sr;
+        if (p.ref_lse_base) p.ref_lse_base[row] = rok ? zmax(arf) : NAN;
+        if (p.ref_lse_rest) p.ref_lse_rest[row] = rok ? float(log(Sr)) : NAN;
         if (p.ref_logp)
             p.ref_logp[row] = (rok && tok >= 0 && tok < p.V) ? float(double(ztok(yrow, tok) - zmax(arf)) - log(Sr)) : NAN;
         if constexpr (KL) {
@@ -1483,6 +1481,132 @@ __global__ __launch_bounds__(kScoreThreads) void k_score(ScoreP p) {
         }
     }
     if (p.status) p.status[row] = uint8_t(stt);
+}
+
+// ------------------------------------------------------------------ fused backward
+//
+// dL/dz_v = [v == token] g_logp - pi_v (A + B log pi_v + C log pi_ref,v) with A = g_logp +
+// g_kl KL + g_H H, B = g_H - g_kl, C = g_kl (the sum of the three row gradients), and
+// dL/dx_v = dL/dz_v / T. One block per row; each lane streams 8 elements per step (16-byte
+// loads of logits, mask and reference logits), two steps in flight, and writes 8 gradient
+// elements (32 bytes f32 or 16 bytes bf16).
+
+struct GradP {
+    const void *logits, *ref, *mask;
+    int64_t V, ld, mask_ld, gld;
+    float tau;
+    int tau_one;
+    const int32_t *tokens;
+    const float *lb, *lr, *rlb, *rlr, *kl, *ent, *glp, *gkl, *gh;
+    void *grad;
+};
+
+constexpr int kGradThreads = 256;
+
+// f32 pair -> packed bf16 pair, round to nearest even (lo from a, hi from b).
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+    uint32_t r;
+    asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
+template <int DT, int MK, bool KL, int GDT, bool AL>
+__global__ __launch_bounds__(kGradThreads) void k_score_grad(GradP p) {
+    const int64_t row = blockIdx.x;
+    const bool tau_one = p.tau_one != 0;
+    const float glp = p.glp ? p.glp[row] : 0.0f;
+    const float gh = p.gh ? p.gh[row] : 0.0f;
+    const float lb = p.lb[row], lr = p.lr[row];
+    float gkl = 0.0f, rlb = 0.0f, rlr = 0.0f, klv = 0.0f;
+    if constexpr (KL) {
+        gkl = p.gkl[row];
+        rlb = p.rlb[row];
+        rlr = p.rlr[row];
+        klv = p.kl[row];
+    }
+    const float hv = p.gh ? p.ent[row] : 0.0f;
+    const int64_t tok = p.glp ? int64_t(p.tokens[row]) : -1;
+    const float A = glp + (KL ? gkl * klv : 0.0f) + (p.gh ? gh * hv : 0.0f);
+    const float B = gh - gkl;
+    const float Cr = gkl;
+    const char *xrow = static_cast<const char *>(p.logits) + row * p.ld * Elem<DT>::kBytes;
+    const char *yrow = nullptr;
+    if constexpr (KL) yrow = static_cast<const char *>(p.ref) + row * p.ld * Elem<DT>::kBytes;
+    const char *mrow = nullptr;
+    if constexpr (MK != NT_MASK_NONE) mrow = static_cast<const char *>(p.mask) + row * p.mask_ld * MaskWords<MK>::kBytes;
+    char *grow = static_cast<char *>(p.grad) + row * p.gld * (GDT == NT_F32 ? 4 : 2);
+
+    // The tempered logit as tempered_logits computes it: x / T (an f32 divide), then + mask.
+    auto tempered = [&](float x, uint32_t mword, int j) -> float {
+        float z = tau_one ? x : x / p.tau;
+        if constexpr (MK == NT_MASK_U8) {
+            if (((mword >> (8 * (j % 4))) & 0xffu) == 0) z = -INFINITY;
+        } else if constexpr (MK == NT_MASK_F32) {
+            z = z + __uint_as_float(mword);
+        }
+        return z;
+    };
+    auto step = [&](const Raw<DT, MK> &rx, const Raw<DT, NT_MASK_NONE> &ry, int64_t e0, float *g) {
+#pragma unroll
+        for (int j = 0; j < kEpl; j++) {
+            const uint32_t mword = MK == NT_MASK_U8 ? rx.m[j / 4] : (MK == NT_MASK_F32 ? rx.m[j] : 0u);
+            const float z = tempered(logit<DT>(rx.x, j), mword, j);
+            const float lp = (z - lb) - lr;
+            const float pi = exp2_hw(lp * kLog2e);
+            float t = fmaf(B, lp, A);
+            if constexpr (KL) {
+                const float lpr = (tempered(logit<DT>(ry.x, j), mword, j) - rlb) - rlr;
+                t = fmaf(Cr, lpr, t);
+            }
+            float gz = (e0 + j == tok) ? glp : 0.0f;
+            // pi = 0: no softmax term, even where t is infinite; a refused row (NaN statistics)
+            // gives NaN everywhere, as the op sequence's log_softmax does.
+            gz = pi == 0.0f ? gz : fmaf(-pi, t, gz);
+            g[j] = tau_one ? gz : gz / p.tau;
+        }
+    };
+    auto store = [&](int64_t e0, const float *g) {
+        if constexpr (GDT == NT_F32) {
+            if constexpr (AL) {
+                float4 *q = reinterpret_cast<float4 *>(grow + e0 * 4);
+                q[0] = make_float4(g[0], g[1], g[2], g[3]);
+                q[1] = make_float4(g[4], g[5], g[6], g[7]);
+            } else {
+                for (int j = 0; j < kEpl; j++)
+                    if (e0 + j < p.V) reinterpret_cast<float *>(grow)[e0 + j] = g[j];
+            }
+        } else {
+            if constexpr (AL) {
+                *reinterpret_cast<uint4 *>(grow + e0 * 2) =
+                    make_uint4(pack_bf16(g[0], g[1]), pack_bf16(g[2], g[3]), pack_bf16(g[4], g[5]), pack_bf16(g[6], g[7]));
+            } else {
+                for (int j = 0; j < kEpl; j += 2) {
+                    const uint32_t w = pack_bf16(g[j], g[j + 1]);
+                    if (e0 + j < p.V) reinterpret_cast<uint16_t *>(grow)[e0 + j] = uint16_t(w);
+                    if (e0 + j + 1 < p.V) reinterpret_cast<uint16_t *>(grow)[e0 + j + 1] = uint16_t(w >> 16);
+                }
+            }
+        }
+    };
+    constexpr int64_t kStep = int64_t(kGradThreads) * kEpl;
+    for (int64_t e0 = int64_t(threadIdx.x) * kEpl; e0 < p.V; e0 += 2 * kStep) {
+        const int64_t e1 = e0 + kStep;
+        Raw<DT, MK> x0, x1;
+        Raw<DT, NT_MASK_NONE> y0, y1;
+        load_raw<DT, MK, AL>(x0, xrow, mrow, e0, p.V);
+        load_raw<DT, MK, AL>(x1, xrow, mrow, e1 < p.V ? e1 : e0, p.V);
+        if constexpr (KL) {
+            load_raw<DT, NT_MASK_NONE, AL>(y0, yrow, nullptr, e0, p.V);
+            load_raw<DT, NT_MASK_NONE, AL>(y1, yrow, nullptr, e1 < p.V ? e1 : e0, p.V);
+        }
+        float g[kEpl];
+        step(x0, y0, e0, g);
+        store(e0, g);
+        if (e1 < p.V) {
+            step(x1, y1, e1, g);
+            store(e1, g);
+        }
+    }
 }
 
 // ------------------------------------------------------------------ per-token kernels
@@ -1735,6 +1859,8 @@ int nt_hip_rl_score(const NtRlScoreArgs *a) {
     if (!a->logits) return fail(NT_E_ARG, "nt_hip_rl_score: null logits");
     if ((a->logp || a->ref_logp) && !a->tokens) return fail(NT_E_ARG, "nt_hip_rl_score: log-probabilities need tokens");
     if ((a->ref_logp || a->kl) && !a->ref_logits) return fail(NT_E_ARG, "nt_hip_rl_score: ref_logp/kl need ref_logits");
+    if ((a->ref_lse_base || a->ref_lse_rest) && !a->ref_logits)
+        return fail(NT_E_ARG, "nt_hip_rl_score: reference statistics need ref_logits");
     std::unique_lock<std::mutex> lk;
     if (int rc = enter(&lk)) return rc;
     if (a->rows == 0) return 0;
@@ -1755,7 +1881,11 @@ int nt_hip_rl_score(const NtRlScoreArgs *a) {
     p.kl = a->kl;
     p.ent = a->entropy;
     p.status = a->status;
-    const bool ref = a->ref_logits != nullptr && (a->ref_logp || a->kl);
+    p.lse_base = a->lse_base;
+    p.lse_rest = a->lse_rest;
+    p.ref_lse_base = a->ref_lse_base;
+    p.ref_lse_rest = a->ref_lse_rest;
+    const bool ref = a->ref_logits != nullptr && (a->ref_logp || a->kl || a->ref_lse_base || a->ref_lse_rest);
     const bool kl = a->kl != nullptr;
     const bool ent = a->entropy != nullptr;
     bool al = aligned_rows(a->logits, a->vocab, a->ld, a->dtype, a->mask_kind, a->mask, a->mask_ld);
@@ -1764,6 +1894,78 @@ int nt_hip_rl_score(const NtRlScoreArgs *a) {
     if (a->dtype == NT_F32) pick_mk_score<NT_F32>(a->mask_kind, ref, kl, ent, al, p, a->rows, s);
     else pick_mk_score<NT_BF16>(a->mask_kind, ref, kl, ent, al, p, a->rows, s);
     return launched("nt_hip_rl_score");
+}
+
+int nt_hip_rl_score_backward(const NtRlScoreGradArgs *a) {
+    if (!a) return fail(NT_E_ARG, "nt_hip_rl_score_backward: null args");
+    if (int rc = check_rows(a->rows, a->vocab, a->ld, a->dtype, a->mask_kind, a->mask, a->mask_ld,
+                            "nt_hip_rl_score_backward"))
+        return rc;
+    if (!(a->temperature > 0.0) || !std::isfinite(a->temperature))
+        return fail(NT_E_ARG, "tempered_logits: temperature " + std::to_string(a->temperature) + " (must be positive)");
+    if (!a->logits || !a->grad || !a->lse_base || !a->lse_rest)
+        return fail(NT_E_ARG, "nt_hip_rl_score_backward: null logits, grad or log-sum-exp statistics");
+    if (a->grad_dtype != NT_F32 && a->grad_dtype != NT_BF16)
+        return fail(NT_E_ARG, "nt_hip_rl_score_backward: grad dtype " + std::to_string(a->grad_dtype));
+    if (a->grad_ld < a->vocab) return fail(NT_E_ARG, "nt_hip_rl_score_backward: grad_ld < vocab");
+    if (a->g_logp && !a->tokens) return fail(NT_E_ARG, "nt_hip_rl_score_backward: g_logp needs tokens");
+    if (a->g_kl && (!a->ref_logits || !a->ref_lse_base || !a->ref_lse_rest || !a->kl))
+        return fail(NT_E_ARG, "nt_hip_rl_score_backward: g_kl needs ref_logits, the reference statistics and kl");
+    if (a->g_entropy && !a->entropy) return fail(NT_E_ARG, "nt_hip_rl_score_backward: g_entropy needs entropy");
+    std::unique_lock<std::mutex> lk;
+    if (int rc = enter(&lk)) return rc;
+    if (a->rows == 0) return 0;
+    GradP p;
+    p.logits = a->logits;
+    p.ref = a->ref_logits;
+    p.mask = a->mask;
+    p.V = a->vocab;
+    p.ld = a->ld;
+    p.mask_ld = a->mask_ld;
+    p.gld = a->grad_ld;
+    p.tau = float(a->temperature);
+    p.tau_one = a->temperature == 1.0;
+    p.tokens = a->tokens;
+    p.lb = a->lse_base;
+    p.lr = a->lse_rest;
+    p.rlb = a->ref_lse_base;
+    p.rlr = a->ref_lse_rest;
+    p.kl = a->kl;
+    p.ent = a->entropy;
+    p.glp = a->g_logp;
+    p.gkl = a->g_kl;
+    p.gh = a->g_entropy;
+    p.grad = a->grad;
+    const bool kl = a->g_kl != nullptr;
+    bool al = aligned_rows(a->logits, a->vocab, a->ld, a->dtype, a->mask_kind, a->mask, a->mask_ld) &&
+              reinterpret_cast<uintptr_t>(a->grad) % 16 == 0 && a->grad_ld % kEpl == 0;
+    if (kl) al = al && reinterpret_cast<uintptr_t>(a->ref_logits) % 16 == 0;
+    hipStream_t s = ctx().stream;
+    auto go = [&](auto dt, auto mk) {
+        constexpr int DT = decltype(dt)::value, MK = decltype(mk)::value;
+        auto launch = [&](auto klc, auto gdt, auto alc) {
+            hipLaunchKernelGGL((k_score_grad<DT, MK, decltype(klc)::value, decltype(gdt)::value, decltype(alc)::value>),
+                               dim3(unsigned(a->rows)), dim3(kGradThreads), 0, s, p);
+        };
+        auto by_al = [&](auto klc, auto gdt) {
+            if (al) launch(klc, gdt, std::true_type{});
+            else launch(klc, gdt, std::false_type{});
+        };
+        auto by_gdt = [&](auto klc) {
+            if (a->grad_dtype == NT_F32) by_al(klc, std::integral_constant<int, NT_F32>{});
+            else by_al(klc, std::integral_constant<int, NT_BF16>{});
+        };
+        if (kl) by_gdt(std::true_type{});
+        else by_gdt(std::false_type{});
+    };
+    auto by_mk = [&](auto dt) {
+        if (a->mask_kind == NT_MASK_U8) go(dt, std::integral_constant<int, NT_MASK_U8>{});
+        else if (a->mask_kind == NT_MASK_F32) go(dt, std::integral_constant<int, NT_MASK_F32>{});
+        else go(dt, std::integral_constant<int, NT_MASK_NONE>{});
+    };
+    if (a->dtype == NT_F32) by_mk(std::integral_constant<int, NT_F32>{});
+    else by_mk(std::integral_constant<int, NT_BF16>{});
+    return launched("nt_hip_rl_score_backward");
 }
 
 int nt_hip_rl_kl_estimate(const float *logp, const float *ref_logp, const float *mask, int64_t n, int32_t estimator,

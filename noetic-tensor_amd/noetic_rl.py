@@ -49,7 +49,19 @@ class NtRlScoreArgs(C.Structure):
                 ("mask_kind", C.c_int32), ("rows", C.c_int64), ("vocab", C.c_int64), ("ld", C.c_int64),
                 ("mask", C.c_void_p), ("mask_ld", C.c_int64), ("temperature", C.c_double),
                 ("tokens", C.c_void_p), ("logp", C.c_void_p), ("ref_logp", C.c_void_p),
-                ("kl", C.c_void_p), ("entropy", C.c_void_p), ("status", C.c_void_p)]
+                ("kl", C.c_void_p), ("entropy", C.c_void_p), ("status", C.c_void_p),
+                ("lse_base", C.c_void_p), ("lse_rest", C.c_void_p), ("ref_lse_base", C.c_void_p),
+                ("ref_lse_rest", C.c_void_p)]
+
+
+class NtRlScoreGradArgs(C.Structure):
+    _fields_ = [("logits", C.c_void_p), ("ref_logits", C.c_void_p), ("dtype", C.c_int32),
+                ("mask_kind", C.c_int32), ("rows", C.c_int64), ("vocab", C.c_int64), ("ld", C.c_int64),
+                ("mask", C.c_void_p), ("mask_ld", C.c_int64), ("temperature", C.c_double),
+                ("tokens", C.c_void_p), ("lse_base", C.c_void_p), ("lse_rest", C.c_void_p),
+                ("ref_lse_base", C.c_void_p), ("ref_lse_rest", C.c_void_p), ("kl", C.c_void_p),
+                ("entropy", C.c_void_p), ("g_logp", C.c_void_p), ("g_kl", C.c_void_p), ("g_entropy", C.c_void_p),
+                ("grad", C.c_void_p), ("grad_dtype", C.c_int32), ("pad0", C.c_int32), ("grad_ld", C.c_int64)]
 
 
 class NtRng(C.Structure):
@@ -79,6 +91,7 @@ _SIGS = {
     "nt_hip_launches": (C.c_uint64, []),
     "nt_hip_rl_sample": (C.c_int, [C.POINTER(NtRlSampleArgs)]),
     "nt_hip_rl_score": (C.c_int, [C.POINTER(NtRlScoreArgs)]),
+    "nt_hip_rl_score_backward": (C.c_int, [C.POINTER(NtRlScoreGradArgs)]),
     "nt_hip_rl_kl_estimate": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_int32, C.c_double,
                                         C.c_void_p]),
     "nt_hip_rl_zero_masked": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p]),
@@ -370,7 +383,7 @@ def sample_categorical(logits: Tensor, temperature: float, mask: Optional[Tensor
     return sample_logp(logits, temperature, mask, rng)[0]
 
 
-def _score(policy, ref, tokens, want_logp, want_ref_logp, want_kl, want_ent):
+def _score(policy, ref, tokens, want_logp, want_ref_logp, want_kl, want_ent, want_stats=False):
     p = _as_tempered(policy)
     rows, V = _rows(p.logits)
     if ref is not None:
@@ -385,19 +398,67 @@ def _score(policy, ref, tokens, want_logp, want_ref_logp, want_kl, want_ent):
         raise ValueError("token_log_probs: tokens shape (the logits' without the vocabulary axis)")
     mk = lambda want: Tensor(out_shape, "f32") if want else None
     lp, rlp, kl, ent = mk(want_logp), mk(want_ref_logp), mk(want_kl), mk(want_ent)
+    stats = None
+    if want_stats:
+        stats = RowStats(mk(True), mk(True), mk(ref is not None), mk(ref is not None))
     status = Tensor(out_shape, "u8")
     kind, mptr, mld = _mask_fields(p, rows, V)
     ptr = lambda t: None if t is None else t.ptr
+    sp = (lambda f: ptr(getattr(stats, f))) if stats is not None else (lambda f: None)
     a = NtRlScoreArgs(p.logits.ptr, None if ref is None else _as_tempered(ref).logits.ptr, _dtype_code(p.logits),
                       kind, rows, V, V, mptr, mld, p.temperature, ptr(tokens), ptr(lp), ptr(rlp), ptr(kl), ptr(ent),
-                      status.ptr)
+                      status.ptr, sp("lse_base"), sp("lse_rest"), sp("ref_lse_base"), sp("ref_lse_rest"))
     _check(lib().nt_hip_rl_score(C.byref(a)), "score")
     if tokens is not None:
         st = status.to_numpy().ravel()
         bad = np.nonzero(st == NT_ROW_BAD_TOKEN)[0]
         if bad.size:
             raise IndexError(f"gather index out of range {V} at position {bad[0]}")
+    if want_stats:
+        return lp, rlp, kl, ent, status, stats
     return lp, rlp, kl, ent, status
+
+
+class RowStats:
+    """A scoring pass's per-row log-sum-exp (lse = base + rest, z units), saved for the backward
+    in place of the reference's materialised log_softmax output (activation.rs:36-41)."""
+
+    def __init__(self, lse_base, lse_rest, ref_lse_base=None, ref_lse_rest=None):
+        self.lse_base, self.lse_rest = lse_base, lse_rest
+        self.ref_lse_base, self.ref_lse_rest = ref_lse_base, ref_lse_rest
+
+
+def score_with_stats(logits, ref_logits, tokens: Optional[Tensor], entropy=True, kl=True):
+    """`score` that also returns the RowStats its backward (`score_grad`) needs."""
+    lp, rlp, k, ent, _, stats = _score(logits, ref_logits, tokens, tokens is not None,
+                                       tokens is not None and ref_logits is not None, kl and ref_logits is not None,
+                                       entropy, want_stats=True)
+    return lp, rlp, k, ent, stats
+
+
+def score_grad(logits, ref_logits, tokens: Optional[Tensor], stats: RowStats, kl: Optional[Tensor] = None,
+               entropy: Optional[Tensor] = None, g_logp: Optional[Tensor] = None, g_kl: Optional[Tensor] = None,
+               g_entropy: Optional[Tensor] = None, grad_dtype: Optional[str] = None) -> Tensor:
+    """The fused backward of `score`: d(sum_r g_logp[r] logp[r] + g_kl[r] kl[r] + g_entropy[r]
+    entropy[r]) / d logits (the raw logits under `tempered_logits`), in one pass. It follows the
+    reference's autograd through log_softmax (activation.rs:36-41), gather, categorical_kl
+    (rl.rs:327-338, the reference detached), categorical_entropy (rl.rs:405-414) and the
+    temperature's divide. `grad_dtype` defaults to the logits' dtype."""
+    p = _as_tempered(logits)
+    rows, V = _rows(p.logits)
+    kind, mptr, mld = _mask_fields(p, rows, V)
+    gdt = grad_dtype or p.logits.dtype
+    if gdt not in ("f32", "bf16"):
+        raise ValueError(f"gradient dtype {gdt}")
+    grad = Tensor(p.logits.shape, gdt)
+    ptr = lambda t: None if t is None else t.ptr
+    ref = None if ref_logits is None else _as_tempered(ref_logits)
+    a = NtRlScoreGradArgs(p.logits.ptr, None if ref is None else ref.logits.ptr, _dtype_code(p.logits), kind, rows,
+                          V, V, mptr, mld, p.temperature, ptr(tokens), ptr(stats.lse_base), ptr(stats.lse_rest),
+                          ptr(stats.ref_lse_base), ptr(stats.ref_lse_rest), ptr(kl), ptr(entropy), ptr(g_logp),
+                          ptr(g_kl), ptr(g_entropy), grad.ptr, NT_F32 if gdt == "f32" else NT_BF16, 0, V)
+    _check(lib().nt_hip_rl_score_backward(C.byref(a)), "score backward")
+    return grad
 
 
 def token_log_probs(logits, tokens: Tensor) -> Tensor:

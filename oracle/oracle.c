@@ -240,6 +240,46 @@ double or_kl(const float *z, const float *r, int64_t V) {
     return kl;
 }
 
+int or_score_grad_row(const float *z, const float *r, int64_t V, int64_t tok, double g_lp, double g_kl, double g_h,
+                      double *out) {
+    or_rowstats sp = or_row_stats(z, V);
+    if (sp.status != 0 || (g_kl != 0.0 && !r)) {
+        for (int64_t v = 0; v < V; v++) out[v] = NAN;
+        return -1;
+    }
+    const double lsp = log(sp.S);
+    double kl = 0.0, h = 0.0, lsr = 0.0;
+    or_rowstats sr = {0};
+    if (g_kl != 0.0) {
+        sr = or_row_stats(r, V);
+        if (sr.status != 0) {
+            for (int64_t v = 0; v < V; v++) out[v] = NAN;
+            return -1;
+        }
+        lsr = log(sr.S);
+        kl = or_kl(z, r, V);
+    }
+    if (g_h != 0.0) h = or_entropy(z, V);
+    for (int64_t v = 0; v < V; v++) {
+        double g = (v == tok) ? g_lp : 0.0;
+        if (z[v] != -INFINITY) {
+            const double lp = ((double)z[v] - sp.m) - lsp;
+            const double pi = exp(lp);
+            if (pi > 0.0) {
+                double t = g_lp;
+                if (g_kl != 0.0) {
+                    const double lr = (r[v] == -INFINITY) ? -INFINITY : ((double)r[v] - sr.m) - lsr;
+                    t += g_kl * (kl - (lp - lr));
+                }
+                if (g_h != 0.0) t += g_h * (lp + h);
+                g -= pi * t;
+            }
+        }
+        out[v] = g;
+    }
+    return 0;
+}
+
 int64_t or_sample_invcdf(const float *z, int64_t V, double u, double *edge) {
     or_rowstats s = or_row_stats(z, V);
     if (s.status != 0) {

@@ -88,6 +88,14 @@ double or_entropy(const float *z, int64_t V);
 /* KL(softmax z || softmax r) = sum p (log p - log r), terms with log p == -inf give 0
  * (rl.rs:327-338). */
 double or_kl(const float *z, const float *r, int64_t V);
+/* The gradient with respect to z of g_lp * logp(tok) + g_kl * KL(softmax z || softmax r) +
+ * g_h * H(softmax z) for one row, in f64 (the reference's autograd through log_softmax
+ * activation.rs:36-41, gather, categorical_kl rl.rs:327-338 with r detached, and
+ * categorical_entropy rl.rs:405-414): out_v = [v == tok] g_lp - pi_v (g_lp + g_kl (KL -
+ * (log pi_v - log pi_r,v)) + g_h (log pi_v + H)), 0 softmax term where pi_v = 0. r may be NULL
+ * when g_kl is 0; tok < 0 means no token term. Returns 0, or -1 for a refused row (out NaN). */
+int or_score_grad_row(const float *z, const float *r, int64_t V, int64_t tok, double g_lp, double g_kl, double g_h,
+                      double *out);
 
 /* The inverse-CDF sampler (the build's definition; the reference's sampler is Gumbel-max):
  * with w_v = exp(z_v - m) and S = sum w, return min{v : sum_{j<=v} w_j > u*S}; if rounding

@@ -70,6 +70,9 @@ def lib():
         L.or_entropy.restype = C.c_double
         L.or_kl.argtypes = [_c_float_p, _c_float_p, C.c_int64]
         L.or_kl.restype = C.c_double
+        L.or_score_grad_row.argtypes = [_c_float_p, _c_float_p, C.c_int64, C.c_int64, C.c_double, C.c_double,
+                                        C.c_double, _c_double_p]
+        L.or_score_grad_row.restype = C.c_int
         L.or_sample_invcdf.argtypes = [_c_float_p, C.c_int64, C.c_double, _c_double_p]
         L.or_sample_invcdf.restype = C.c_int64
         L.or_kl_estimate.argtypes = [_c_double_p, _c_double_p, _c_double_p, C.c_int64, C.c_int, C.c_double, _c_double_p]
@@ -202,6 +205,21 @@ def kl(z, r):
     r = _f32(np.atleast_2d(r))
     return np.array([lib().or_kl(_ptr(z[i], _c_float_p), _ptr(r[i], _c_float_p), z.shape[1])
                      for i in range(z.shape[0])])
+
+
+def score_grad(z, tokens=None, r=None, g_lp=None, g_kl=None, g_h=None, tau=1.0):
+    """d(g_lp logp + g_kl KL + g_h H)/dx per row, in f64, for rows of tempered logits z (f32)
+    with z = x / tau + mask: the z gradient (or_score_grad_row) divided by tau."""
+    z = _f32(np.atleast_2d(z))
+    R, V = z.shape
+    rr = None if r is None else _f32(np.atleast_2d(r))
+    out = np.empty((R, V), dtype=np.float64)
+    col = lambda a, i: 0.0 if a is None else float(np.ravel(a)[i])
+    for i in range(R):
+        tok = -1 if tokens is None else int(np.ravel(tokens)[i])
+        lib().or_score_grad_row(_ptr(z[i], _c_float_p), None if rr is None else _ptr(rr[i], _c_float_p), V, tok,
+                                col(g_lp, i), col(g_kl, i), col(g_h, i), _ptr(out[i], _c_double_p))
+    return out / tau
 
 
 def sample_invcdf(z, u):

@@ -42,7 +42,8 @@ def test_argument_struct_layouts_match_the_header():
     import subprocess
     import tempfile
     fields = {"NtRlSampleArgs": [f[0] for f in nr.NtRlSampleArgs._fields_],
-              "NtRlScoreArgs": [f[0] for f in nr.NtRlScoreArgs._fields_]}
+              "NtRlScoreArgs": [f[0] for f in nr.NtRlScoreArgs._fields_],
+              "NtRlScoreGradArgs": [f[0] for f in nr.NtRlScoreGradArgs._fields_]}
     body = []
     for st, fs in fields.items():
         body.append(f'printf("{st} %zu\\n", sizeof({st}));')
@@ -60,7 +61,8 @@ def test_argument_struct_layouts_match_the_header():
         assert int(got[st]) == C.sizeof(cls), st
         for f in fs:
             assert int(got[f"{st}.{f}"]) == getattr(cls, f).offset, (st, f)
-    assert int(got["NtRlSampleArgs"]) == 104 and int(got["NtRlScoreArgs"]) == 120
+    assert int(got["NtRlSampleArgs"]) == 104 and int(got["NtRlScoreArgs"]) == 152
+    assert int(got["NtRlScoreGradArgs"]) == 176
 
 
 def test_without_a_claimed_device_calls_fail_cleanly():
@@ -85,6 +87,23 @@ def test_argument_validation_precedes_the_device():
     a = nr.NtRlSampleArgs(None, nr.NT_F32, nr.NT_MASK_NONE, 4, 16, 16, None, 0, -1.0, None, None, None, None, None)
     assert L.nt_hip_rl_sample(C.byref(a)) == -1
     assert "temperature" in L.nt_hip_last_error().decode()
+    # the backward: each upstream gradient needs the forward outputs it multiplies
+    buf = np.zeros(64, np.float32)
+    h = buf.ctypes.data
+    g = nr.NtRlScoreGradArgs(logits=h, dtype=nr.NT_F32, mask_kind=nr.NT_MASK_NONE, rows=4, vocab=16, ld=16,
+                             temperature=1.0, lse_base=h, lse_rest=h, g_logp=h, grad=h, grad_dtype=nr.NT_F32,
+                             grad_ld=16)
+    assert L.nt_hip_rl_score_backward(C.byref(g)) == -1
+    assert "g_logp needs tokens" in L.nt_hip_last_error().decode()
+    g.g_logp, g.g_kl, g.kl = None, h, h
+    assert L.nt_hip_rl_score_backward(C.byref(g)) == -1
+    assert "g_kl needs ref_logits" in L.nt_hip_last_error().decode()
+    g.g_kl, g.grad_dtype = None, 7
+    assert L.nt_hip_rl_score_backward(C.byref(g)) == -1
+    assert "grad dtype" in L.nt_hip_last_error().decode()
+    g.grad_dtype, g.grad_ld = nr.NT_BF16, 8
+    assert L.nt_hip_rl_score_backward(C.byref(g)) == -1
+    assert "grad_ld" in L.nt_hip_last_error().decode()
 
 
 def test_product_stream_equals_the_oracle_stream():

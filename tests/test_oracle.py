@@ -362,3 +362,68 @@ def test_c1_golden_fixture():
     assert_close("c1 entropy", fx["entropy"], ent, 1e-13)
     for i, row_id in enumerate(ids):
         assert row_id == _numpy_invcdf(z[i], u[i])
+
+
+# ------------------------------------------------------------------------ fused backward
+
+def _fd_objective(z, zr, tok, g_lp, g_kl, g_h):
+    """The forward objective in f64 from scipy (independent of the oracle's restatement)."""
+    lp = log_softmax(z)
+    val = g_lp * lp[tok] if tok >= 0 else 0.0
+    pi = np.exp(lp)
+    if g_kl:
+        lr = log_softmax(zr)
+        val += g_kl * float(np.sum(np.where(pi > 0, pi * (lp - lr), 0.0)))
+    if g_h:
+        val += g_h * float(-np.sum(np.where(pi > 0, pi * lp, 0.0)))
+    return val
+
+
+def test_score_grad_matches_finite_differences():
+    # the reference checks its gradients by central differences (fd_input, eps 1e-6, tol 1e-7;
+    # src/nn/tests/joint_embed.rs:19-33, used at tests/rl.rs:125-129 and 283-314); here against
+    # scipy's log_softmax as the forward, for each term alone and all three together
+    rng = np.random.default_rng(71)
+    V = 12
+    z = rng.uniform(-3, 3, V).astype(np.float32).astype(np.float64)
+    zr = (z + rng.normal(0, 0.5, V)).astype(np.float32).astype(np.float64)
+    tok = 5
+    for g in [(1.0, 0.0, 0.0), (0.0, 1.0, 0.0), (0.0, 0.0, 1.0), (-0.7, 1.3, 0.4)]:
+        got = O.score_grad(z.astype(np.float32), [tok], zr.astype(np.float32), [g[0]], [g[1]], [g[2]])[0]
+        fd = np.empty(V)
+        for j in range(V):
+            zp, zm = z.copy(), z.copy()
+            zp[j] += 1e-6
+            zm[j] -= 1e-6
+            fd[j] = (_fd_objective(zp, zr, tok, *g) - _fd_objective(zm, zr, tok, *g)) / 2e-6
+        assert np.all(np.abs(fd - got) <= 1e-7 * (1 + np.abs(fd))), (g, np.max(np.abs(fd - got)))
+
+
+def test_score_grad_of_token_log_probs_is_onehot_minus_softmax():
+    # tests/rl.rs:116-121: d sum(token_log_probs)/dx = onehot - softmax (to 1e-14 in f64)
+    rng = np.random.default_rng(72)
+    x = rng.uniform(-6, 6, (5, 9)).astype(np.float32)
+    tok = rng.integers(0, 9, 5)
+    got = O.score_grad(x, tok, g_lp=np.ones(5))
+    sm = np.exp(log_softmax(x.astype(np.float64), axis=1))
+    want = np.eye(9)[tok] - sm
+    assert np.max(np.abs(got - want)) <= 1e-14
+    # the temperature's divide: z = x / T, dL/dx = dL/dz / T
+    tau = 0.7
+    z = O.tempered(x, tau)
+    got = O.score_grad(z, tok, g_lp=np.ones(5), tau=tau)
+    want = (np.eye(9)[tok] - np.exp(log_softmax(z.astype(np.float64), axis=1))) / tau
+    assert np.max(np.abs(got - want)) <= 1e-14
+
+
+def test_score_grad_large_and_excluded_logits():
+    # tests/rl.rs:131-150: logits of +-1e4 stay finite; an entry excluded by -inf has gradient 0
+    # (only the token term where the token itself is excluded)
+    x = np.array([[1e4, -1e4, 0.0, 1e3], [-1e4, -1e4, 1e4, 1e4]], np.float32)
+    got = O.score_grad(x, [0, 2], g_lp=[1.0, 1.0])
+    assert np.all(np.isfinite(got))
+    assert got[0, 0] == 0.0 and abs(got[1, 2] - 0.5) < 1e-15 and abs(got[1, 3] + 0.5) < 1e-15
+    z = np.array([[0.5, -np.inf, 1.0, -np.inf]], np.float32)
+    zr = np.array([[0.2, -np.inf, 0.9, 3.0]], np.float32)
+    got = O.score_grad(z, [1], zr, [1.0], [0.3], [0.2])
+    assert got[0, 3] == 0.0 and got[0, 1] == 1.0 and np.all(np.isfinite(got))
