@@ -551,6 +551,8 @@ typedef __attribute__((address_space(3))) void *lds_ptr_t;
 // Word 3 of a gfx9-family buffer resource: 32-bit data format, no swizzle; with stride 0 every
 // access is range-checked against the byte count in word 2.
 constexpr int kBufferWord3 = 0x00020000;
+// Four dwords as the buffer load/store builtins take them.
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) void *glb_ptr_t;
 
 template <int B, int E, class F>
@@ -1487,9 +1489,13 @@ __global__ __launch_bounds__(kScoreThreads) void k_score(ScoreP p) {
 //
 // dL/dz_v = [v == token] g_logp - pi_v (A + B log pi_v + C log pi_ref,v) with A = g_logp +
 // g_kl KL + g_H H, B = g_H - g_kl, C = g_kl (the sum of the three row gradients), and
-// dL/dx_v = dL/dz_v / T. One block per row; each lane streams 8 elements per step (16-byte
-// loads of logits, mask and reference logits), two steps in flight, and writes 8 gradient
-// elements (32 bytes f32 or 16 bytes bf16).
+// dL/dx_v = dL/dz_v / T. The kernel works in base 2: with l_v = log2 pi_v and r_v = log2 pi_ref,v,
+// dL/dx_v = [v == token] g_logp / T - pi_v (A' + B' l_v + C' r_v), where A' = A / T,
+// B' = B ln2 / T and C' = C ln2 / T are per-row constants. l_v is clamped at -256: an excluded
+// (-inf) logit then has pi_v = 0 and a finite sum, so its gradient is exactly zero without a
+// select. A refused row (NaN statistics) sets A' to NaN, which makes the whole row NaN, as the
+// op sequence's log_softmax does. One block per row; each lane streams 8 elements per step,
+// two steps in flight.
 
 struct GradP {
     const void *logits, *ref, *mask;
@@ -1502,6 +1508,8 @@ struct GradP {
 };
 
 constexpr int kGradThreads = 256;
+constexpr int kGradStep = kGradThreads * kEpl;  // elements a block covers per step
+constexpr int kCachePolicyNT = 2;               // buffer access cache policy: non-temporal (streamed once)
 
 // f32 pair -> packed bf16 pair, round to nearest even (lo from a, hi from b).
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
@@ -1510,102 +1518,254 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
     return r;
 }
 
-template <int DT, int MK, bool KL, int GDT, bool AL>
-__global__ __launch_bounds__(kGradThreads) void k_score_grad(GradP p) {
-    const int64_t row = blockIdx.x;
-    const bool tau_one = p.tau_one != 0;
+// The per-row constants of the backward (see above).
+struct GradRow {
+    float lb, l2, rlb, r2, A, B, C, gtok;
+    int64_t tok;
+};
+
+template <bool KL>
+__device__ __forceinline__ GradRow grad_row(const GradP &p, int64_t row) {
+    GradRow g;
+    const float inv_tau = p.tau_one ? 1.0f : 1.0f / p.tau;
     const float glp = p.glp ? p.glp[row] : 0.0f;
     const float gh = p.gh ? p.gh[row] : 0.0f;
-    const float lb = p.lb[row], lr = p.lr[row];
-    float gkl = 0.0f, rlb = 0.0f, rlr = 0.0f, klv = 0.0f;
+    const float hv = p.gh ? p.ent[row] : 0.0f;
+    float gkl = 0.0f, klv = 0.0f;
+    g.lb = p.lb[row];
+    const float lr = p.lr[row];
+    g.l2 = lr * kLog2e;
+    g.rlb = 0.0f;
+    g.r2 = 0.0f;
+    bool refused = !(g.lb == g.lb) || !(lr == lr);
     if constexpr (KL) {
         gkl = p.gkl[row];
-        rlb = p.rlb[row];
-        rlr = p.rlr[row];
         klv = p.kl[row];
+        g.rlb = p.rlb[row];
+        const float rlr = p.rlr[row];
+        g.r2 = rlr * kLog2e;
+        refused = refused || !(g.rlb == g.rlb) || !(rlr == rlr);
     }
-    const float hv = p.gh ? p.ent[row] : 0.0f;
-    const int64_t tok = p.glp ? int64_t(p.tokens[row]) : -1;
     const float A = glp + (KL ? gkl * klv : 0.0f) + (p.gh ? gh * hv : 0.0f);
-    const float B = gh - gkl;
-    const float Cr = gkl;
-    const char *xrow = static_cast<const char *>(p.logits) + row * p.ld * Elem<DT>::kBytes;
-    const char *yrow = nullptr;
-    if constexpr (KL) yrow = static_cast<const char *>(p.ref) + row * p.ld * Elem<DT>::kBytes;
-    const char *mrow = nullptr;
-    if constexpr (MK != NT_MASK_NONE) mrow = static_cast<const char *>(p.mask) + row * p.mask_ld * MaskWords<MK>::kBytes;
-    char *grow = static_cast<char *>(p.grad) + row * p.gld * (GDT == NT_F32 ? 4 : 2);
+    g.A = refused ? __builtin_nanf("") : A * inv_tau;
+    g.B = (gh - gkl) * float(kLn2) * inv_tau;
+    g.C = gkl * float(kLn2) * inv_tau;
+    g.gtok = glp * inv_tau;
+    g.tok = p.glp ? int64_t(p.tokens[row]) : -1;
+    return g;
+}
 
-    // The tempered logit as tempered_logits computes it: x / T (an f32 divide), then + mask.
-    auto tempered = [&](float x, uint32_t mword, int j) -> float {
-        float z = tau_one ? x : x / p.tau;
-        if constexpr (MK == NT_MASK_U8) {
-            if (((mword >> (8 * (j % 4))) & 0xffu) == 0) z = -INFINITY;
-        } else if constexpr (MK == NT_MASK_F32) {
-            z = z + __uint_as_float(mword);
-        }
-        return z;
-    };
-    auto step = [&](const Raw<DT, MK> &rx, const Raw<DT, NT_MASK_NONE> &ry, int64_t e0, float *g) {
+// One element's gradient from its tempered logit z (and reference zr).
+template <bool KL>
+__device__ __forceinline__ float grad_elem(const GradRow &g, float z, float zr) {
+    const float l = fmaxf(fmaf(z - g.lb, kLog2e, -g.l2), -256.0f);
+    const float pi = exp2_hw(l);
+    float t = fmaf(g.B, l, g.A);
+    if constexpr (KL) {
+        const float r = fmaxf(fmaf(zr - g.rlb, kLog2e, -g.r2), -256.0f);
+        t = fmaf(g.C, r, t);
+    }
+    return fmaf(-pi, t, 0.0f);
+}
+
+// The tempered logit as tempered_logits computes it: x / T (an f32 divide), then the mask.
+template <int MK, bool TAU1>
+__device__ __forceinline__ float grad_tempered(float x, float tau, uint32_t mword, int j) {
+    float z = TAU1 ? x : x / tau;
+    if constexpr (MK == NT_MASK_U8) {
+        if (((mword >> (8 * (j % 4))) & 0xffu) == 0) z = -INFINITY;
+    } else if constexpr (MK == NT_MASK_F32) {
+        z = z + __uint_as_float(mword);
+    }
+    return z;
+}
+
+// The token's own term, in the one lane (of one step) that holds it. A lane's 8 elements are
+// e0 + j, or with SPLIT two groups of 4: e0 + j (j < 4) and e1 + j - 4 (j >= 4).
+template <bool SPLIT>
+__device__ __forceinline__ void add_token_term(const GradRow &g, int64_t e0, int64_t e1, float *out) {
+    const int64_t d = g.tok - e0;
+    if (static_cast<uint64_t>(d) < uint64_t(SPLIT ? 4 : kEpl)) {
 #pragma unroll
-        for (int j = 0; j < kEpl; j++) {
-            const uint32_t mword = MK == NT_MASK_U8 ? rx.m[j / 4] : (MK == NT_MASK_F32 ? rx.m[j] : 0u);
-            const float z = tempered(logit<DT>(rx.x, j), mword, j);
-            const float lp = (z - lb) - lr;
-            const float pi = exp2_hw(lp * kLog2e);
-            float t = fmaf(B, lp, A);
-            if constexpr (KL) {
-                const float lpr = (tempered(logit<DT>(ry.x, j), mword, j) - rlb) - rlr;
-                t = fmaf(Cr, lpr, t);
-            }
-            float gz = (e0 + j == tok) ? glp : 0.0f;
-            // pi = 0: no softmax term, even where t is infinite; a refused row (NaN statistics)
-            // gives NaN everywhere, as the op sequence's log_softmax does.
-            gz = pi == 0.0f ? gz : fmaf(-pi, t, gz);
-            g[j] = tau_one ? gz : gz / p.tau;
+        for (int j = 0; j < (SPLIT ? 4 : kEpl); j++) out[j] += (j == int(d)) ? g.gtok : 0.0f;
+    }
+    if constexpr (SPLIT) {
+        const int64_t d1 = g.tok - e1;
+        if (static_cast<uint64_t>(d1) < 4u) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) out[4 + j] += (j == int(d1)) ? g.gtok : 0.0f;
+        }
+    }
+}
+
+template <int DT, int MK, bool KL, bool TAU1, bool SPLIT = false>
+__device__ __forceinline__ void grad_step(const GradRow &g, float tau, const Raw<DT, MK> &rx,
+                                          const Raw<DT, NT_MASK_NONE> &ry, int64_t e0, int64_t e1, float *out) {
+#pragma unroll
+    for (int j = 0; j < kEpl; j++) {
+        const uint32_t mword = MK == NT_MASK_U8 ? rx.m[j / 4] : (MK == NT_MASK_F32 ? rx.m[j] : 0u);
+        const float z = grad_tempered<MK, TAU1>(logit<DT>(rx.x, j), tau, mword, j);
+        const float zr = KL ? grad_tempered<MK, TAU1>(logit<DT>(ry.x, j), tau, mword, j) : 0.0f;
+        out[j] = grad_elem<KL>(g, z, zr);
+    }
+    add_token_term<SPLIT>(g, e0, e1, out);
+}
+
+// Aligned rows (V % 8 == 0, 16-byte rows, row bytes below 2^31): every access goes through a
+// per-row buffer resource. Past the end of the row loads return zeros and stores are dropped by
+// the hardware range check, so the loop needs no bounds tests: every lane runs the same number
+// of steps. A step covers 2048 elements. With a bf16 gradient lane t owns elements 8t..8t+7 (one
+// 16-byte load per input, one 16-byte store). With an f32 gradient (32 bytes per lane) it owns
+// 4t..4t+3 and 1024+4t..1024+4t+3 instead, so that each store instruction writes one contiguous
+// stretch of whole cache lines rather than every other 16 bytes of them. Either way a group of
+// a lane's elements lies wholly inside the row or wholly past it (V % 8 == 0). Every input is
+// read once and the gradient written once, so all of them are accessed non-temporally.
+template <int DT, int MK, bool KL, int GDT, bool TAU1>
+__device__ __forceinline__ void grad_row_aligned(const GradP &p, const GradRow &g, int64_t row) {
+    constexpr int XB = Elem<DT>::kBytes, MB = MaskWords<MK>::kBytes, GB = GDT == NT_F32 ? 4 : 2;
+    constexpr bool SPLIT = GDT == NT_F32;
+    constexpr int kHalf = kGradStep / 2;
+    const int V = int(p.V);
+    const auto xres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char *>(static_cast<const char *>(p.logits) + row * p.ld * XB), short(0), V * XB, kBufferWord3);
+    __amdgpu_buffer_rsrc_t yres = xres, mres = xres;
+    if constexpr (KL)
+        yres = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<char *>(static_cast<const char *>(p.ref) + row * p.ld * XB), short(0), V * XB, kBufferWord3);
+    if constexpr (MK != NT_MASK_NONE)
+        mres = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<char *>(static_cast<const char *>(p.mask) + row * p.mask_ld * MB), short(0), V * MB,
+            kBufferWord3);
+    const auto gres = __builtin_amdgcn_make_buffer_rsrc(static_cast<char *>(p.grad) + row * p.gld * GB, short(0),
+                                                        V * GB, kBufferWord3);
+    // 4 elements of one input at element e into words w0.. of dst (f32: 4 words, bf16: 2)
+    auto load4 = [&](uint32_t *dst, __amdgpu_buffer_rsrc_t rs, int e) {
+        if constexpr (DT == NT_F32) {
+            const auto a = __builtin_amdgcn_raw_buffer_load_b128(rs, e * 4, 0, kCachePolicyNT);
+            for (int i = 0; i < 4; i++) dst[i] = a[i];
+        } else {
+            const auto a = __builtin_amdgcn_raw_buffer_load_b64(rs, e * 2, 0, kCachePolicyNT);
+            dst[0] = a[0];
+            dst[1] = a[1];
         }
     };
-    auto store = [&](int64_t e0, const float *g) {
-        if constexpr (GDT == NT_F32) {
-            if constexpr (AL) {
-                float4 *q = reinterpret_cast<float4 *>(grow + e0 * 4);
-                q[0] = make_float4(g[0], g[1], g[2], g[3]);
-                q[1] = make_float4(g[4], g[5], g[6], g[7]);
-            } else {
-                for (int j = 0; j < kEpl; j++)
-                    if (e0 + j < p.V) reinterpret_cast<float *>(grow)[e0 + j] = g[j];
+    auto load = [&](auto &rx, auto &ry, int e0, int e1) {
+        if constexpr (SPLIT) {
+            constexpr int H = Elem<DT>::kWords / 2;
+            load4(rx.x, xres, e0);
+            load4(rx.x + H, xres, e1);
+            if constexpr (KL) {
+                load4(ry.x, yres, e0);
+                load4(ry.x + H, yres, e1);
+            }
+            if constexpr (MK == NT_MASK_U8) {
+                rx.m[0] = __builtin_amdgcn_raw_buffer_load_b32(mres, e0, 0, kCachePolicyNT);
+                rx.m[1] = __builtin_amdgcn_raw_buffer_load_b32(mres, e1, 0, kCachePolicyNT);
+            } else if constexpr (MK == NT_MASK_F32) {
+                const auto a = __builtin_amdgcn_raw_buffer_load_b128(mres, e0 * 4, 0, kCachePolicyNT);
+                const auto b = __builtin_amdgcn_raw_buffer_load_b128(mres, e1 * 4, 0, kCachePolicyNT);
+                for (int i = 0; i < 4; i++) {
+                    rx.m[i] = a[i];
+                    rx.m[4 + i] = b[i];
+                }
             }
         } else {
-            if constexpr (AL) {
-                *reinterpret_cast<uint4 *>(grow + e0 * 2) =
-                    make_uint4(pack_bf16(g[0], g[1]), pack_bf16(g[2], g[3]), pack_bf16(g[4], g[5]), pack_bf16(g[6], g[7]));
+            if constexpr (DT == NT_F32) {
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    const auto a = __builtin_amdgcn_raw_buffer_load_b128(xres, e0 * 4 + 16 * q, 0, kCachePolicyNT);
+                    for (int i = 0; i < 4; i++) rx.x[4 * q + i] = a[i];
+                    if constexpr (KL) {
+                        const auto b = __builtin_amdgcn_raw_buffer_load_b128(yres, e0 * 4 + 16 * q, 0, kCachePolicyNT);
+                        for (int i = 0; i < 4; i++) ry.x[4 * q + i] = b[i];
+                    }
+                }
             } else {
-                for (int j = 0; j < kEpl; j += 2) {
-                    const uint32_t w = pack_bf16(g[j], g[j + 1]);
-                    if (e0 + j < p.V) reinterpret_cast<uint16_t *>(grow)[e0 + j] = uint16_t(w);
-                    if (e0 + j + 1 < p.V) reinterpret_cast<uint16_t *>(grow)[e0 + j + 1] = uint16_t(w >> 16);
+                const auto a = __builtin_amdgcn_raw_buffer_load_b128(xres, e0 * 2, 0, kCachePolicyNT);
+                for (int i = 0; i < 4; i++) rx.x[i] = a[i];
+                if constexpr (KL) {
+                    const auto b = __builtin_amdgcn_raw_buffer_load_b128(yres, e0 * 2, 0, kCachePolicyNT);
+                    for (int i = 0; i < 4; i++) ry.x[i] = b[i];
+                }
+            }
+            if constexpr (MK == NT_MASK_U8) {
+                const auto k = __builtin_amdgcn_raw_buffer_load_b64(mres, e0, 0, kCachePolicyNT);
+                rx.m[0] = k[0];
+                rx.m[1] = k[1];
+            } else if constexpr (MK == NT_MASK_F32) {
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    const auto a = __builtin_amdgcn_raw_buffer_load_b128(mres, e0 * 4 + 16 * q, 0, kCachePolicyNT);
+                    for (int i = 0; i < 4; i++) rx.m[4 * q + i] = a[i];
                 }
             }
         }
     };
-    constexpr int64_t kStep = int64_t(kGradThreads) * kEpl;
-    for (int64_t e0 = int64_t(threadIdx.x) * kEpl; e0 < p.V; e0 += 2 * kStep) {
-        const int64_t e1 = e0 + kStep;
+    auto store = [&](int e0, int e1, const float *o) {
+        if constexpr (GDT == NT_F32) {
+            const v4u a = {__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]), __float_as_uint(o[3])};
+            const v4u b = {__float_as_uint(o[4]), __float_as_uint(o[5]), __float_as_uint(o[6]), __float_as_uint(o[7])};
+            __builtin_amdgcn_raw_buffer_store_b128(a, gres, e0 * 4, 0, kCachePolicyNT);
+            __builtin_amdgcn_raw_buffer_store_b128(b, gres, e1 * 4, 0, kCachePolicyNT);
+        } else {
+            const v4u w = {pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]), pack_bf16(o[4], o[5]), pack_bf16(o[6], o[7])};
+            __builtin_amdgcn_raw_buffer_store_b128(w, gres, e0 * 2, 0, kCachePolicyNT);
+        }
+    };
+    const int t = int(threadIdx.x);
+    const int first = SPLIT ? 4 * t : kEpl * t;  // the lane's first element in step 0
+    for (int s0 = 0; s0 < V; s0 += 2 * kGradStep) {
         Raw<DT, MK> x0, x1;
         Raw<DT, NT_MASK_NONE> y0, y1;
-        load_raw<DT, MK, AL>(x0, xrow, mrow, e0, p.V);
-        load_raw<DT, MK, AL>(x1, xrow, mrow, e1 < p.V ? e1 : e0, p.V);
-        if constexpr (KL) {
-            load_raw<DT, NT_MASK_NONE, AL>(y0, yrow, nullptr, e0, p.V);
-            load_raw<DT, NT_MASK_NONE, AL>(y1, yrow, nullptr, e1 < p.V ? e1 : e0, p.V);
+        const int a0 = s0 + first, a1 = a0 + kGradStep;
+        load(x0, y0, a0, a0 + kHalf);
+        load(x1, y1, a1, a1 + kHalf);
+        float o[kEpl];
+        grad_step<DT, MK, KL, TAU1, SPLIT>(g, p.tau, x0, y0, a0, a0 + kHalf, o);
+        store(a0, a0 + kHalf, o);
+        grad_step<DT, MK, KL, TAU1, SPLIT>(g, p.tau, x1, y1, a1, a1 + kHalf, o);
+        store(a1, a1 + kHalf, o);
+    }
+}
+
+// Any other row layout: element-wise bounds and plain stores.
+template <int DT, int MK, bool KL, int GDT, bool TAU1>
+__device__ __forceinline__ void grad_row_general(const GradP &p, const GradRow &g, int64_t row) {
+    const char *xrow = static_cast<const char *>(p.logits) + row * p.ld * Elem<DT>::kBytes;
+    const char *yrow = KL ? static_cast<const char *>(p.ref) + row * p.ld * Elem<DT>::kBytes : nullptr;
+    const char *mrow = MK != NT_MASK_NONE ? static_cast<const char *>(p.mask) + row * p.mask_ld * MaskWords<MK>::kBytes
+                                          : nullptr;
+    char *grow = static_cast<char *>(p.grad) + row * p.gld * (GDT == NT_F32 ? 4 : 2);
+    for (int64_t e0 = int64_t(threadIdx.x) * kEpl; e0 < p.V; e0 += kGradStep) {
+        Raw<DT, MK> rx;
+        Raw<DT, NT_MASK_NONE> ry;
+        load_raw<DT, MK, false>(rx, xrow, mrow, e0, p.V);
+        if constexpr (KL) load_raw<DT, NT_MASK_NONE, false>(ry, yrow, nullptr, e0, p.V);
+        float o[kEpl];
+        grad_step<DT, MK, KL, TAU1>(g, p.tau, rx, ry, e0, 0, o);
+        for (int j = 0; j < kEpl; j += 2) {
+            if constexpr (GDT == NT_F32) {
+                if (e0 + j < p.V) reinterpret_cast<float *>(grow)[e0 + j] = o[j];
+                if (e0 + j + 1 < p.V) reinterpret_cast<float *>(grow)[e0 + j + 1] = o[j + 1];
+            } else {
+                const uint32_t w = pack_bf16(o[j], o[j + 1]);
+                if (e0 + j < p.V) reinterpret_cast<uint16_t *>(grow)[e0 + j] = uint16_t(w);
+                if (e0 + j + 1 < p.V) reinterpret_cast<uint16_t *>(grow)[e0 + j + 1] = uint16_t(w >> 16);
+            }
         }
-        float g[kEpl];
-        step(x0, y0, e0, g);
-        store(e0, g);
-        if (e1 < p.V) {
-            step(x1, y1, e1, g);
-            store(e1, g);
-        }
+    }
+}
+
+template <int DT, int MK, bool KL, int GDT, bool AL>
+__global__ __launch_bounds__(kGradThreads) void k_score_grad(GradP p) {
+    const int64_t row = blockIdx.x;
+    const GradRow g = grad_row<KL>(p, row);
+    if (p.tau_one) {
+        if constexpr (AL) grad_row_aligned<DT, MK, KL, GDT, true>(p, g, row);
+        else grad_row_general<DT, MK, KL, GDT, true>(p, g, row);
+    } else {
+        if constexpr (AL) grad_row_aligned<DT, MK, KL, GDT, false>(p, g, row);
+        else grad_row_general<DT, MK, KL, GDT, false>(p, g, row);
     }
 }
 
@@ -1937,8 +2097,10 @@ int nt_hip_rl_score_backward(const NtRlScoreGradArgs *a) {
     p.gh = a->g_entropy;
     p.grad = a->grad;
     const bool kl = a->g_kl != nullptr;
+    // the buffer-resource path addresses a row's bytes with 32-bit offsets
     bool al = aligned_rows(a->logits, a->vocab, a->ld, a->dtype, a->mask_kind, a->mask, a->mask_ld) &&
-              reinterpret_cast<uintptr_t>(a->grad) % 16 == 0 && a->grad_ld % kEpl == 0;
+              reinterpret_cast<uintptr_t>(a->grad) % 16 == 0 && a->grad_ld % kEpl == 0 &&
+              a->vocab * 4 <= int64_t(0x7fffffff);
     if (kl) al = al && reinterpret_cast<uintptr_t>(a->ref_logits) % 16 == 0;
     hipStream_t s = ctx().stream;
     auto go = [&](auto dt, auto mk) {
