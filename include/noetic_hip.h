@@ -203,6 +203,57 @@ int nt_hip_rl_zero_masked(const float *x, const float *mask, int64_t n, float *o
 int nt_hip_rl_reduce_tokens(const float *per, const float *mask, int64_t S, int64_t B, int64_t T,
                             int32_t reduction, float *out);
 
+/* The backward of reduce_tokens after zero_masked (rl.rs:69-102): for each position of
+ * [S,B,T], out = mask != 0 ? scale * upstream[o] * dR/dper * local : 0, where o is the reduced
+ * output the position feeds and dR/dper is 1 (None, Sum), 1/max(sum_s m, 1) (TokenMean),
+ * 1/max(sum_t m, 1) (PerSequence) or 1/(max(sum_t m, 1) * max(sequences of the seed with a
+ * scored position, 1)) (SequenceMean). upstream has the reduced shape ([S,B,T] for None, [S,B]
+ * for PerSequence, [S] otherwise); NULL means ones. local ([S,B,T], NULL = ones) is the
+ * per-token derivative of the loss being reduced (nt_hip_rl_policy_loss's dloss), so that out is
+ * that loss's gradient with respect to logp. mask NULL scores every position. */
+int nt_hip_rl_reduce_tokens_backward(const float *mask, int64_t S, int64_t B, int64_t T, int32_t reduction,
+                                     const float *upstream, double scale, const float *local, float *out);
+
+/* kl_estimate's derivative with respect to logp per sampled token (rl.rs:380-400), with the
+ * same arguments as nt_hip_rl_kl_estimate: with delta = ref_logp - logp, 1 (k1), -delta (k2),
+ * 1 - exp(delta) (k3); zero where the clamp is active (|delta| > clamp) and at masked
+ * positions. */
+int nt_hip_rl_kl_estimate_backward(const float *logp, const float *ref_logp, const float *mask, int64_t n,
+                                   int32_t estimator, double clamp, float *out);
+
+enum { NT_LOSS_PG = 0, NT_LOSS_PPO = 1 };
+
+/* The policy losses per token (rl.rs:228-317), before reduce_tokens.
+ *   kind NT_LOSS_PG:  policy_gradient_loss (rl.rs:228-235), loss = -(w * logp);
+ *   kind NT_LOSS_PPO: clipped_policy_loss (rl.rs:265-287): d = logp - old_logp (0 at masked
+ *     positions), clamped to [-log_ratio_clamp, log_ratio_clamp] when log_ratio_clamp > 0;
+ *     r = exp(d); loss = max(-r A, -clip(r, 1 - clip_low, 1 + clip_high) A) by a select; with a
+ *     dual clip c (dual > 0, c > 1) a token with A < 0 has min(loss, -c A).
+ * weights are the weights (PG) or advantages (PPO), per token [S,B,T] or per sequence [S,B]
+ * (weights_per_sequence = 1). mask f32 [S,B,T], NULL = every position scored. Outputs, each
+ * [S,B,T] and optional:
+ *   loss   the per-token loss, 0 at masked positions (TokenReduction::None's values);
+ *   dloss  d loss / d logp per token (0 at masked positions and where a bound is active; the
+ *          op sequence's autograd, including its NaN for an overflowed ratio without the clamp);
+ *   hit    clip_fraction's numerator (rl.rs:293-317): 1 where the token gets no gradient
+ *          through a bound (A > 0, r > 1 + high; A < 0, r < 1 - low; A < 0, r > c under a dual
+ *          clip; |d| beyond the clamp), times the mask; its TokenMean is clip_fraction.
+ * Arguments follow Clip::check (rl.rs:189-200): 0 <= clip_low < 1, 0 <= clip_high, dual 0 or
+ * c > 1, log_ratio_clamp 0 (unbounded) or b > 0. */
+typedef struct NtRlPolicyLossArgs {
+    const float *logp;
+    const float *old_logp; /* PPO only */
+    const float *weights;
+    const float *mask;
+    int64_t S, B, T;
+    int32_t kind;
+    int32_t weights_per_sequence;
+    double clip_low, clip_high, dual, log_ratio_clamp;
+    float *loss, *dloss, *hit;
+} NtRlPolicyLossArgs;
+
+int nt_hip_rl_policy_loss(const NtRlPolicyLossArgs *a);
+
 #ifdef __cplusplus
 }
 #endif

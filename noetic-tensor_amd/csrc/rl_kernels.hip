@@ -1823,6 +1823,153 @@ __global__ void k_reduce_tokens(const float *per, const float *mask, int64_t S, 
     else out[i] = float(seq / (nonempty > 1.0 ? nonempty : 1.0));
 }
 
+// ------------------------------------------------------------------ reductions per seed
+//
+// One 1024-thread block per seed s: wave w sums sequences w, w+16, ... over T (lane-strided, f64,
+// then a fixed DPP tree), keeping each sequence's value sum and mask sum in LDS; thread 0 folds
+// them in sequence order. The forward writes reduce_tokens' outputs (rl.rs:69-92); the backward
+// writes each position's share of the reduced outputs' upstream gradient.
+
+constexpr int kSeedThreads = 1024;
+constexpr int64_t kSeedMaxB = 4096;  // sequences per seed the LDS of one block holds (2 x f64 each)
+
+template <bool BWD>
+__global__ __launch_bounds__(kSeedThreads) void k_reduce_seed(const float *per, const float *mask, int64_t B,
+                                                               int64_t T, int red, float *out, const float *up,
+                                                               float scale, const float *local) {
+    extern __shared__ double seqs[];  // [B] value sums, then [B] mask sums
+    __shared__ double seed[4];        // total, scored count, sum of sequence means, non-empty sequences
+    double *sv = seqs, *sm = seqs + B;
+    const int64_t s = blockIdx.x;
+    const int tid = int(threadIdx.x), wave = tid / kWave, lane = tid % kWave;
+    const int64_t base = s * B * T;
+    for (int64_t b = wave; b < B; b += kSeedThreads / kWave) {
+        double v = 0.0, m = 0.0;
+        for (int64_t t = lane; t < T; t += kWave) {
+            const int64_t k = base + b * T + t;
+            if constexpr (!BWD) v += double(per[k]);
+            m += mask ? double(mask[k]) : 1.0;
+        }
+        if constexpr (!BWD) v = readlane_d(wave_scan_dpp(v), kWave - 1);
+        m = readlane_d(wave_scan_dpp(m), kWave - 1);
+        if (lane == 0) {
+            sv[b] = v;
+            sm[b] = m;
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        double tot = 0.0, cnt = 0.0, seq = 0.0, nonempty = 0.0;
+        for (int64_t b = 0; b < B; b++) {
+            tot += sv[b];
+            cnt += sm[b];
+            seq += sv[b] / (sm[b] > 1.0 ? sm[b] : 1.0);
+            nonempty += sm[b] > 1.0 ? 1.0 : sm[b];  // clamp_max(1) of the sequence's count
+        }
+        seed[0] = tot;
+        seed[1] = cnt > 1.0 ? cnt : 1.0;
+        seed[2] = seq;
+        seed[3] = nonempty > 1.0 ? nonempty : 1.0;
+    }
+    __syncthreads();
+    if constexpr (!BWD) {
+        if (red == 3) {
+            for (int64_t b = tid; b < B; b += kSeedThreads) out[s * B + b] = float(sv[b] / (sm[b] > 1.0 ? sm[b] : 1.0));
+        } else if (tid == 0) {
+            out[s] = float(red == 1 ? seed[0] : (red == 2 ? seed[0] / seed[1] : seed[2] / seed[3]));
+        }
+    } else {
+        const double gs = red == 0 || red == 3 ? 0.0 : (up ? double(up[s]) : 1.0);
+        for (int64_t j = tid; j < B * T; j += kSeedThreads) {
+            const int64_t k = base + j, b = j / T;
+            const float m = mask ? mask[k] : 1.0f;
+            double g;
+            if (red == 0) g = up ? double(up[k]) : 1.0;
+            else if (red == 1) g = gs;
+            else if (red == 2) g = gs / seed[1];
+            else if (red == 3) g = (up ? double(up[s * B + b]) : 1.0) / (sm[b] > 1.0 ? sm[b] : 1.0);
+            else g = gs / (seed[3] * (sm[b] > 1.0 ? sm[b] : 1.0));
+            const float gl = float(double(scale) * g);
+            out[k] = m != 0.0f ? (local ? gl * local[k] : gl) : 0.0f;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ policy losses per token
+
+struct LossP {
+    const float *lp, *old, *w, *mask;
+    int64_t n, T;
+    int kind, per_seq;
+    float lo, hi;          // 1 - low, 1 + high (f32, as the op sequence's scalar clamp)
+    float neg_c, c;        // -c, c (dual clip)
+    float b;               // the log-ratio clamp
+    int dual, clamped;
+    float *loss, *dloss, *hit;
+};
+
+__global__ void k_policy_loss(LossP p) {
+    for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < p.n; i += int64_t(gridDim.x) * blockDim.x) {
+        const float m = p.mask ? p.mask[i] : 1.0f;
+        const bool scored = m != 0.0f;
+        const float a = p.per_seq ? p.w[i / p.T] : p.w[i];
+        float per, dper, hit = 0.0f;
+        if (p.kind == NT_LOSS_PG) {
+            per = -(p.lp[i] * a);
+            dper = -a;
+        } else {
+            // log_ratio (rl.rs:237-245): zero_masked, then the clamp (its gradient passes inside)
+            const float d = scored ? p.lp[i] - p.old[i] : 0.0f;
+            const float dc = p.clamped ? fminf(fmaxf(d, -p.b), p.b) : d;
+            const float gate = p.clamped ? ((d >= -p.b && d <= p.b) ? 1.0f : 0.0f) : 1.0f;
+            const float r = expf(dc);
+            const float un = -(r * a);
+            const float rc = fminf(fmaxf(r, p.lo), p.hi);
+            const float cl = -(rc * a);
+            // select_max(unclipped, clipped) (rl.rs:124-129): the unclipped branch wins only on a
+            // positive difference; the gradient goes to the selected branch (the clipped one's is
+            // zero outside [1 - low, 1 + high])
+            const bool un_wins = (un - cl) > 0.0f;
+            float v = un_wins ? un : cl;
+            float gr = (un_wins || (r >= p.lo && r <= p.hi)) ? -a : 0.0f;
+            if (p.dual && a < 0.0f) {
+                // min(v, -c A) as -select_max(-v, -cap) with cap = A (-c)
+                const float cap = a * p.neg_c;
+                const bool keep = ((-v) - (-cap)) > 0.0f;
+                v = keep ? v : cap;
+                gr = keep ? gr : 0.0f;
+            }
+            per = v;
+            dper = (gr * r) * gate;  // exp's derivative is r (0 * inf = NaN, as the op sequence)
+            // clip_fraction (rl.rs:293-317) uses the unclamped ratio
+            const float r0 = expf(d);
+            float h = ((a > 0.0f && r0 > p.hi) ? 1.0f : 0.0f) + ((a < 0.0f && r0 < p.lo) ? 1.0f : 0.0f);
+            if (p.dual) h += (r0 > p.c && a < 0.0f) ? 1.0f : 0.0f;
+            if (p.clamped) h += fabsf(d) > p.b ? 1.0f : 0.0f;
+            hit = fminf(h, 1.0f) * m;
+        }
+        if (p.loss) p.loss[i] = scored ? per : 0.0f;
+        if (p.dloss) p.dloss[i] = scored ? dper : 0.0f;
+        if (p.hit) p.hit[i] = scored ? hit : 0.0f;
+    }
+}
+
+__global__ void k_kl_estimate_grad(const float *lp, const float *lr, const float *mask, int64_t n, int est,
+                                   float clamp, int clamped, float *out) {
+    for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
+        const bool scored = mask ? (mask[i] != 0.0f) : true;
+        const float d = scored ? (lr[i] - lp[i]) : 0.0f;
+        const bool active = clamped && !(d >= -clamp && d <= clamp);
+        const float dc = clamped ? fminf(fmaxf(d, -clamp), clamp) : d;
+        // dk/dlogp = -dk/d(delta)
+        float g;
+        if (est == 1) g = 1.0f;
+        else if (est == 2) g = -dc;
+        else g = -expm1f(dc);
+        out[i] = (scored && !active) ? g : 0.0f;
+    }
+}
+
 // ------------------------------------------------------------------ dispatch helpers
 
 int check_rows(int64_t rows, int64_t V, int64_t ld, int32_t dtype, int32_t mk, const void *mask, int64_t mask_ld,
@@ -2165,10 +2312,96 @@ int nt_hip_rl_reduce_tokens(const float *per, const float *mask, int64_t S, int6
     if (int rc = enter(&lk)) return rc;
     const int64_t nout = reduction == 3 ? S * B : S;
     if (nout == 0) return 0;
-    const int threads = 64;
-    hipLaunchKernelGGL(k_reduce_tokens, dim3(unsigned((nout + threads - 1) / threads)), dim3(threads), 0,
-                       ctx().stream, per, mask, S, B, T, int(reduction), out);
+    if (B <= kSeedMaxB && S <= 0x7fffffffLL) {
+        hipLaunchKernelGGL(k_reduce_seed<false>, dim3(unsigned(S)), dim3(kSeedThreads), size_t(2 * B) * sizeof(double),
+                           ctx().stream, per, mask, B, T, int(reduction), out, nullptr, 1.0f, nullptr);
+    } else {
+        const int threads = 64;
+        hipLaunchKernelGGL(k_reduce_tokens, dim3(unsigned((nout + threads - 1) / threads)), dim3(threads), 0,
+                           ctx().stream, per, mask, S, B, T, int(reduction), out);
+    }
     return launched("nt_hip_rl_reduce_tokens");
+}
+
+int nt_hip_rl_reduce_tokens_backward(const float *mask, int64_t S, int64_t B, int64_t T, int32_t reduction,
+                                     const float *upstream, double scale, const float *local, float *out) {
+    if (!out || S < 0 || B < 0 || T < 0 || reduction < 0 || reduction > 4 || !std::isfinite(scale))
+        return fail(NT_E_ARG, "nt_hip_rl_reduce_tokens_backward: invalid arguments");
+    if (B > kSeedMaxB || S > 0x7fffffffLL)
+        return fail(NT_E_UNSUPPORTED, "nt_hip_rl_reduce_tokens_backward: more than 4096 sequences per seed");
+    std::unique_lock<std::mutex> lk;
+    if (int rc = enter(&lk)) return rc;
+    if (S == 0 || B == 0 || T == 0) return 0;
+    hipLaunchKernelGGL(k_reduce_seed<true>, dim3(unsigned(S)), dim3(kSeedThreads), size_t(2 * B) * sizeof(double),
+                       ctx().stream, nullptr, mask, B, T, int(reduction), out, upstream, float(scale), local);
+    return launched("nt_hip_rl_reduce_tokens_backward");
+}
+
+int nt_hip_rl_kl_estimate_backward(const float *logp, const float *ref_logp, const float *mask, int64_t n,
+                                   int32_t estimator, double clamp, float *out) {
+    if (n < 0 || !logp || !ref_logp || !out || estimator < 1 || estimator > 3)
+        return fail(NT_E_ARG, "nt_hip_rl_kl_estimate_backward: invalid arguments");
+    if (clamp < 0.0) return fail(NT_E_ARG, "kl_estimate: δ clamp " + std::to_string(clamp) + " (need b > 0)");
+    std::unique_lock<std::mutex> lk;
+    if (int rc = enter(&lk)) return rc;
+    if (n == 0) return 0;
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(k_kl_estimate_grad, dim3(unsigned(blocks)), dim3(256), 0, ctx().stream, logp, ref_logp, mask, n,
+                       int(estimator), float(clamp), clamp > 0.0 ? 1 : 0, out);
+    return launched("nt_hip_rl_kl_estimate_backward");
+}
+
+int nt_hip_rl_policy_loss(const NtRlPolicyLossArgs *a) {
+    if (!a) return fail(NT_E_ARG, "nt_hip_rl_policy_loss: null args");
+    if (!a->logp || !a->weights || a->S < 0 || a->B < 0 || a->T < 0 ||
+        (a->kind != NT_LOSS_PG && a->kind != NT_LOSS_PPO) || (a->kind == NT_LOSS_PPO && !a->old_logp))
+        return fail(NT_E_ARG, "nt_hip_rl_policy_loss: invalid arguments");
+    if (a->kind == NT_LOSS_PPO) {
+        char buf[200];
+        // Clip::check (rl.rs:189-200)
+        if (!(a->clip_low >= 0.0 && a->clip_low < 1.0 && a->clip_high >= 0.0 && std::isfinite(a->clip_low) &&
+              std::isfinite(a->clip_high))) {
+            std::snprintf(buf, sizeof buf, "clip range [1 − %g, 1 + %g] (need 0 ≤ low < 1, 0 ≤ high)", a->clip_low,
+                          a->clip_high);
+            return fail(NT_E_ARG, buf);
+        }
+        if (a->dual != 0.0 && !(a->dual > 1.0 && std::isfinite(a->dual))) {
+            std::snprintf(buf, sizeof buf, "dual clip %g (need c > 1)", a->dual);
+            return fail(NT_E_ARG, buf);
+        }
+        if (!(a->log_ratio_clamp >= 0.0)) {
+            std::snprintf(buf, sizeof buf, "log-ratio clamp %g (need b > 0)", a->log_ratio_clamp);
+            return fail(NT_E_ARG, buf);
+        }
+    }
+    std::unique_lock<std::mutex> lk;
+    if (int rc = enter(&lk)) return rc;
+    const int64_t n = a->S * a->B * a->T;
+    if (n == 0) return 0;
+    LossP p;
+    p.lp = a->logp;
+    p.old = a->old_logp;
+    p.w = a->weights;
+    p.mask = a->mask;
+    p.n = n;
+    p.T = a->T;
+    p.kind = a->kind;
+    p.per_seq = a->weights_per_sequence != 0;
+    p.lo = float(1.0 - a->clip_low);
+    p.hi = float(1.0 + a->clip_high);
+    p.neg_c = float(-a->dual);
+    p.c = float(a->dual);
+    p.b = float(a->log_ratio_clamp);
+    p.dual = a->dual != 0.0;
+    p.clamped = a->log_ratio_clamp > 0.0;
+    p.loss = a->loss;
+    p.dloss = a->dloss;
+    p.hit = a->hit;
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(k_policy_loss, dim3(unsigned(blocks)), dim3(256), 0, ctx().stream, p);
+    return launched("nt_hip_rl_policy_loss");
 }
 
 }  // extern "C"

@@ -64,6 +64,17 @@ class NtRlScoreGradArgs(C.Structure):
                 ("grad", C.c_void_p), ("grad_dtype", C.c_int32), ("pad0", C.c_int32), ("grad_ld", C.c_int64)]
 
 
+class NtRlPolicyLossArgs(C.Structure):
+    _fields_ = [("logp", C.c_void_p), ("old_logp", C.c_void_p), ("weights", C.c_void_p), ("mask", C.c_void_p),
+                ("S", C.c_int64), ("B", C.c_int64), ("T", C.c_int64), ("kind", C.c_int32),
+                ("weights_per_sequence", C.c_int32), ("clip_low", C.c_double), ("clip_high", C.c_double),
+                ("dual", C.c_double), ("log_ratio_clamp", C.c_double), ("loss", C.c_void_p), ("dloss", C.c_void_p),
+                ("hit", C.c_void_p)]
+
+
+NT_LOSS_PG, NT_LOSS_PPO = 0, 1
+
+
 class NtRng(C.Structure):
     _fields_ = [("key", C.c_uint32 * 8), ("counter", C.c_uint64), ("buf", C.c_uint32 * 16), ("idx", C.c_int32)]
 
@@ -97,6 +108,11 @@ _SIGS = {
     "nt_hip_rl_zero_masked": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p]),
     "nt_hip_rl_reduce_tokens": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_int32,
                                           C.c_void_p]),
+    "nt_hip_rl_reduce_tokens_backward": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_int32,
+                                                   C.c_void_p, C.c_double, C.c_void_p, C.c_void_p]),
+    "nt_hip_rl_kl_estimate_backward": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_int32,
+                                                 C.c_double, C.c_void_p]),
+    "nt_hip_rl_policy_loss": (C.c_int, [C.POINTER(NtRlPolicyLossArgs)]),
     # noetic_rng.h
     "nt_rng_derive": (C.c_int, [C.POINTER(NtRng), C.c_uint64, C.c_char_p, C.c_size_t]),
     "nt_rng_from_seed": (C.c_int, [C.POINTER(NtRng), C.c_char_p]),
@@ -542,6 +558,150 @@ def kl_estimate(logp: Tensor, ref_logp: Tensor, estimator: KlEstimator, delta_cl
                                        int(estimator), 0.0 if delta_clamp is None else float(delta_clamp), out.ptr),
            "kl_estimate")
     return _reduce(out, mask, reduction)
+
+
+def _reduced_shape(shape, reduction: TokenReduction):
+    S, B, _ = shape
+    return {TokenReduction.NONE: tuple(shape), TokenReduction.PER_SEQUENCE: (S, B)}.get(TokenReduction(reduction), (S,))
+
+
+def reduce_tokens_backward(mask: Optional[Tensor], shape, reduction: TokenReduction, upstream: Optional[Tensor] = None,
+                           scale: float = 1.0, local: Optional[Tensor] = None) -> Tensor:
+    """The gradient of reduce_tokens(zero_masked(per)) (rl.rs:69-102) with respect to per, times
+    `scale` and the per-token derivative `local` (a loss's d per / d logp): [S, B, T], 0 at
+    masked positions. `upstream` is the reduced output's gradient (None: ones)."""
+    S, B, T = shape
+    reduction = TokenReduction(reduction)
+    if upstream is not None and tuple(upstream.shape) != _reduced_shape(shape, reduction):
+        raise ValueError(f"reduce_tokens backward: upstream shape {upstream.shape} for {reduction.name}")
+    out = Tensor((S, B, T), "f32")
+    _check(lib().nt_hip_rl_reduce_tokens_backward(None if mask is None else mask.ptr, S, B, T, int(reduction),
+                                                  None if upstream is None else upstream.ptr, float(scale),
+                                                  None if local is None else local.ptr, out.ptr),
+           "reduce_tokens backward")
+    return out
+
+
+def kl_estimate_backward(logp: Tensor, ref_logp: Tensor, estimator: KlEstimator, delta_clamp: Optional[float] = None,
+                         mask: Optional[Tensor] = None, reduction: TokenReduction = TokenReduction.TOKEN_MEAN,
+                         upstream: Optional[Tensor] = None, scale: float = 1.0) -> Tensor:
+    """d (scale * kl_estimate(...)) / d logp (rl.rs:380-400), [S, B, T]; the reference logp is
+    detached."""
+    if logp.shape != ref_logp.shape or len(logp.shape) != 3:
+        raise ValueError("kl_estimate: logp and reference log-probabilities [S, B, T]")
+    if delta_clamp is not None and not delta_clamp > 0.0:
+        raise ValueError(f"kl_estimate: δ clamp {delta_clamp} (need b > 0)")
+    local = Tensor(logp.shape, "f32")
+    _check(lib().nt_hip_rl_kl_estimate_backward(logp.ptr, ref_logp.ptr, None if mask is None else mask.ptr,
+                                                logp.numel, int(estimator),
+                                                0.0 if delta_clamp is None else float(delta_clamp), local.ptr),
+           "kl_estimate backward")
+    return reduce_tokens_backward(mask, logp.shape, reduction, upstream, scale, local)
+
+
+LOG_RATIO_CLAMP = 20.0  # rl.rs:146
+
+
+class Clip:
+    """clipped_policy_loss's settings (rl.rs:161-201): the ratio clipped to [1 - low, 1 + high];
+    `dual` (c > 1) caps a negative-advantage token's loss at -c A; `log_ratio_clamp` bounds
+    logp - old_logp (None: unbounded)."""
+
+    def __init__(self, low: float, high: float, dual: Optional[float] = None,
+                 log_ratio_clamp: Optional[float] = LOG_RATIO_CLAMP):
+        self.low, self.high, self.dual, self.log_ratio_clamp = float(low), float(high), dual, log_ratio_clamp
+
+    @staticmethod
+    def new(low: float, high: float) -> "Clip":
+        return Clip(low, high)
+
+    @staticmethod
+    def symmetric(eps: float) -> "Clip":
+        return Clip(eps, eps)
+
+    def with_dual(self, c: float) -> "Clip":
+        return Clip(self.low, self.high, c, self.log_ratio_clamp)
+
+    def with_log_ratio_clamp(self, b: Optional[float]) -> "Clip":
+        return Clip(self.low, self.high, self.dual, b)
+
+    def check(self):
+        if not (0.0 <= self.low < 1.0 and self.high >= 0.0 and math.isfinite(self.low) and math.isfinite(self.high)):
+            raise ValueError(f"clip range [1 − {self.low}, 1 + {self.high}] (need 0 ≤ low < 1, 0 ≤ high)")
+        if self.dual is not None and not (self.dual > 1.0 and math.isfinite(self.dual)):
+            raise ValueError(f"dual clip {self.dual} (need c > 1)")
+        if self.log_ratio_clamp is not None and not self.log_ratio_clamp > 0.0:
+            raise ValueError(f"log-ratio clamp {self.log_ratio_clamp} (need b > 0)")
+
+
+def _policy_loss(kind: int, what: str, logp: Tensor, old_logp: Optional[Tensor], weights: Tensor,
+                 mask: Optional[Tensor], clip: Optional[Clip]):
+    """(loss, dloss, hit) per token from nt_hip_rl_policy_loss, with the reference's shape checks
+    (token_weights rl.rs:106-122, mask_or_ones 58-66)."""
+    if len(logp.shape) != 3:
+        raise ValueError(f"{what}: logp [S, B, T]")
+    S, B, T = logp.shape
+    if len(weights.shape) == 2:
+        if tuple(weights.shape) != (S, B):
+            raise ValueError(f"{what}: per-sequence weights [S, B]")
+        per_seq = 1
+    elif len(weights.shape) == 3:
+        if tuple(weights.shape) != (S, B, T):
+            raise ValueError(f"{what}: per-token weights [S, B, T]")
+        per_seq = 0
+    else:
+        raise ValueError(f"{what}: weights of rank {len(weights.shape)} (per-sequence [S, B] or per-token [S, B, T])")
+    if mask is not None and mask.shape != logp.shape:
+        raise ValueError("rl: mask shape")
+    if old_logp is not None and old_logp.shape != logp.shape:
+        raise ValueError("rl: old log-probabilities shape")
+    if clip is not None:
+        clip.check()
+    loss, dloss, hit = Tensor(logp.shape, "f32"), Tensor(logp.shape, "f32"), Tensor(logp.shape, "f32")
+    a = NtRlPolicyLossArgs(logp.ptr, None if old_logp is None else old_logp.ptr, weights.ptr,
+                           None if mask is None else mask.ptr, S, B, T, kind, per_seq,
+                           clip.low if clip else 0.0, clip.high if clip else 0.0,
+                           (clip.dual or 0.0) if clip else 0.0,
+                           (clip.log_ratio_clamp or 0.0) if clip else 0.0, loss.ptr, dloss.ptr, hit.ptr)
+    _check(lib().nt_hip_rl_policy_loss(C.byref(a)), what)
+    return loss, dloss, hit
+
+
+def policy_gradient_loss(logp: Tensor, weights: Tensor, mask: Optional[Tensor] = None,
+                         reduction: TokenReduction = TokenReduction.TOKEN_MEAN) -> Tensor:
+    """rl.rs:228-235: -w logp per scored token, reduced per seed."""
+    loss, _, _ = _policy_loss(NT_LOSS_PG, "policy_gradient_loss", logp, None, weights, mask, None)
+    return _reduce(loss, mask, reduction)
+
+
+def policy_gradient_loss_backward(logp: Tensor, weights: Tensor, mask: Optional[Tensor] = None,
+                                  reduction: TokenReduction = TokenReduction.TOKEN_MEAN,
+                                  upstream: Optional[Tensor] = None, scale: float = 1.0) -> Tensor:
+    """d (scale * policy_gradient_loss(...)) / d logp, [S, B, T] (the weights are detached)."""
+    _, dloss, _ = _policy_loss(NT_LOSS_PG, "policy_gradient_loss", logp, None, weights, mask, None)
+    return reduce_tokens_backward(mask, logp.shape, reduction, upstream, scale, dloss)
+
+
+def clipped_policy_loss(logp: Tensor, old_logp: Tensor, advantages: Tensor, mask: Optional[Tensor], clip: Clip,
+                        reduction: TokenReduction = TokenReduction.TOKEN_MEAN) -> Tensor:
+    """rl.rs:265-287: PPO's clipped surrogate as a loss, reduced per seed."""
+    loss, _, _ = _policy_loss(NT_LOSS_PPO, "clipped_policy_loss", logp, old_logp, advantages, mask, clip)
+    return _reduce(loss, mask, reduction)
+
+
+def clipped_policy_loss_backward(logp: Tensor, old_logp: Tensor, advantages: Tensor, mask: Optional[Tensor],
+                                 clip: Clip, reduction: TokenReduction = TokenReduction.TOKEN_MEAN,
+                                 upstream: Optional[Tensor] = None, scale: float = 1.0) -> Tensor:
+    """d (scale * clipped_policy_loss(...)) / d logp, [S, B, T] (old_logp and the advantages are
+    detached)."""
+    _, dloss, _ = _policy_loss(NT_LOSS_PPO, "clipped_policy_loss", logp, old_logp, advantages, mask, clip)
+    return reduce_tokens_backward(mask, logp.shape, reduction, upstream, scale, dloss)
+
+
+def clip_fraction(logp: Tensor, old_logp: Tensor, advantages: Tensor, mask: Optional[Tensor], clip: Clip) -> Tensor:
+    """rl.rs:293-317: per seed [S], the fraction of scored tokens a bound gives no gradient."""
+    _, _, hit = _policy_loss(NT_LOSS_PPO, "clip_fraction", logp, old_logp, advantages, mask, clip)
+    return _reduce(hit, mask, TokenReduction.TOKEN_MEAN)
 
 
 def group_advantages(rewards: Sequence[float], n: int, norm: str = "mean", eps: float = 0.0,

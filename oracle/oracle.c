@@ -567,3 +567,107 @@ int64_t or_cpu_sample_logp_invcdf(const float *x, int64_t rows, int64_t V, doubl
     free(th);
     return refused;
 }
+
+/* ------------------------------------------------------------------ policy losses per token */
+
+/* policy_gradient_loss (rl.rs:228-235, kind 0) and clipped_policy_loss (rl.rs:265-287, kind 1)
+ * per token in f64, before reduce_tokens: the loss (0 at masked positions), its derivative with
+ * respect to logp as the op sequence's autograd propagates it (the select gives the gradient to
+ * the chosen branch, the clamps pass it inside their range only, exp's derivative is its value),
+ * and clip_fraction's per-token indicator (rl.rs:293-317) times the mask. w holds per-token
+ * weights, or per-sequence ones (per_seq: index i / T). dual <= 0: no dual clip; clamp <= 0: no
+ * log-ratio clamp. Any output may be NULL. */
+void or_policy_loss(int kind, int64_t n, int64_t T, const double *lp, const double *old, const double *w,
+                    int per_seq, const double *mask, double low, double high, double dual, double clamp,
+                    double *loss, double *dloss, double *hit) {
+    const double lo = 1.0 - low, hi = 1.0 + high;
+    for (int64_t i = 0; i < n; i++) {
+        const double m = mask ? mask[i] : 1.0;
+        const int scored = m != 0.0;
+        const double a = per_seq ? w[i / T] : w[i];
+        double per, dper, h = 0.0;
+        if (kind == 0) {
+            per = -(lp[i] * a);
+            dper = -a;
+        } else {
+            const double d = scored ? lp[i] - old[i] : 0.0;
+            double dc = d, gate = 1.0;
+            if (clamp > 0.0) {
+                dc = d < -clamp ? -clamp : (d > clamp ? clamp : d);
+                gate = (d >= -clamp && d <= clamp) ? 1.0 : 0.0;
+            }
+            const double r = exp(dc);
+            const double rc = r < lo ? lo : (r > hi ? hi : r);
+            const double un = -(r * a), cl = -(rc * a);
+            const int un_wins = (un - cl) > 0.0;
+            double v = un_wins ? un : cl;
+            double gr = (un_wins || (r >= lo && r <= hi)) ? -a : 0.0;
+            if (dual > 0.0 && a < 0.0) {
+                const double cap = -dual * a;
+                const int keep = (cap - v) > 0.0; /* min(v, -c A): v where v < -c A */
+                v = keep ? v : cap;
+                gr = keep ? gr : 0.0;
+            }
+            per = v;
+            dper = gr * r * gate;
+            const double r0 = exp(d);
+            h = ((a > 0.0 && r0 > hi) ? 1.0 : 0.0) + ((a < 0.0 && r0 < lo) ? 1.0 : 0.0);
+            if (dual > 0.0 && a < 0.0 && r0 > dual) h += 1.0;
+            if (clamp > 0.0 && fabs(d) > clamp) h += 1.0;
+            h = (h > 1.0 ? 1.0 : h) * m;
+        }
+        if (loss) loss[i] = scored ? per : 0.0;
+        if (dloss) dloss[i] = scored ? dper : 0.0;
+        if (hit) hit[i] = scored ? h : 0.0;
+    }
+}
+
+/* The backward of reduce_tokens after zero_masked (rl.rs:69-102): the derivative of each
+ * reduced output with respect to each position's value, times the output's upstream gradient
+ * (up NULL: ones), times scale and local[i] (NULL: ones); 0 at masked positions. */
+void or_reduce_tokens_backward(const double *mask, int64_t S, int64_t B, int64_t T, int reduction, const double *up,
+                               double scale, const double *local, double *out) {
+    for (int64_t s = 0; s < S; s++) {
+        double cnt = 0.0, nonempty = 0.0;
+        for (int64_t b = 0; b < B; b++) {
+            double m = 0.0;
+            for (int64_t t = 0; t < T; t++) m += mask ? mask[(s * B + b) * T + t] : 1.0;
+            cnt += m;
+            nonempty += m > 1.0 ? 1.0 : m;
+        }
+        cnt = cnt > 1.0 ? cnt : 1.0;
+        nonempty = nonempty > 1.0 ? nonempty : 1.0;
+        for (int64_t b = 0; b < B; b++) {
+            double m_seq = 0.0;
+            for (int64_t t = 0; t < T; t++) m_seq += mask ? mask[(s * B + b) * T + t] : 1.0;
+            m_seq = m_seq > 1.0 ? m_seq : 1.0;
+            for (int64_t t = 0; t < T; t++) {
+                const int64_t i = (s * B + b) * T + t;
+                const double m = mask ? mask[i] : 1.0;
+                double g;
+                if (reduction == 0) g = up ? up[i] : 1.0;
+                else if (reduction == 1) g = up ? up[s] : 1.0;
+                else if (reduction == 2) g = (up ? up[s] : 1.0) / cnt;
+                else if (reduction == 3) g = (up ? up[s * B + b] : 1.0) / m_seq;
+                else g = (up ? up[s] : 1.0) / (nonempty * m_seq);
+                out[i] = m != 0.0 ? scale * g * (local ? local[i] : 1.0) : 0.0;
+            }
+        }
+    }
+}
+
+/* d kl_estimate / d logp per token (rl.rs:380-400): with delta = lr - lp, 1 (k1), -delta (k2),
+ * 1 - exp(delta) (k3); 0 at masked positions and where the clamp is active. */
+void or_kl_estimate_grad(const double *lp, const double *lr, const double *mask, int64_t n, int est, double clamp,
+                         double *out) {
+    for (int64_t i = 0; i < n; i++) {
+        const int scored = mask ? (mask[i] != 0.0) : 1;
+        const double d = scored ? (lr[i] - lp[i]) : 0.0;
+        const int active = clamp > 0.0 && !(d >= -clamp && d <= clamp);
+        double g;
+        if (est == 1) g = 1.0;
+        else if (est == 2) g = -d;
+        else g = -expm1(d);
+        out[i] = (scored && !active) ? g : 0.0;
+    }
+}

@@ -116,6 +116,13 @@ int64_t or_reduce_tokens(const double *per, const double *mask, int64_t S, int64
 
 /* group_advantages (rl.rs:436-463): norm 0 MeanOnly, 1 Std. Returns 0, or -1 for an invalid
  * call (groups of n must divide len; eps >= 0; unbiased needs n >= 2). */
+void or_policy_loss(int kind, int64_t n, int64_t T, const double *lp, const double *old, const double *w,
+                    int per_seq, const double *mask, double low, double high, double dual, double clamp,
+                    double *loss, double *dloss, double *hit);
+void or_reduce_tokens_backward(const double *mask, int64_t S, int64_t B, int64_t T, int reduction, const double *up,
+                               double scale, const double *local, double *out);
+void or_kl_estimate_grad(const double *lp, const double *lr, const double *mask, int64_t n, int est, double clamp,
+                         double *out);
 int or_group_advantages(const double *rewards, int64_t len, int64_t n, int norm, double eps,
                         int unbiased, double *out);
 

@@ -78,6 +78,13 @@ def lib():
         L.or_kl_estimate.argtypes = [_c_double_p, _c_double_p, _c_double_p, C.c_int64, C.c_int, C.c_double, _c_double_p]
         L.or_reduce_tokens.argtypes = [_c_double_p, _c_double_p, C.c_int64, C.c_int64, C.c_int64, C.c_int, _c_double_p]
         L.or_reduce_tokens.restype = C.c_int64
+        L.or_policy_loss.argtypes = [C.c_int, C.c_int64, C.c_int64, _c_double_p, _c_double_p, _c_double_p, C.c_int,
+                                     _c_double_p, C.c_double, C.c_double, C.c_double, C.c_double, _c_double_p,
+                                     _c_double_p, _c_double_p]
+        L.or_reduce_tokens_backward.argtypes = [_c_double_p, C.c_int64, C.c_int64, C.c_int64, C.c_int, _c_double_p,
+                                                C.c_double, _c_double_p, _c_double_p]
+        L.or_kl_estimate_grad.argtypes = [_c_double_p, _c_double_p, _c_double_p, C.c_int64, C.c_int, C.c_double,
+                                          _c_double_p]
         L.or_group_advantages.argtypes = [_c_double_p, C.c_int64, C.c_int64, C.c_int, C.c_double, C.c_int, _c_double_p]
         L.or_group_advantages.restype = C.c_int
         L.or_unrolled_sum_f32.argtypes = [_c_float_p, C.c_int64]
@@ -261,6 +268,42 @@ def reduce_tokens(per, mask, shape, reduction):
     n = lib().or_reduce_tokens(_ptr(per, _c_double_p), None if m is None else _ptr(m, _c_double_p),
                                S, B, T, REDUCTIONS[reduction], _ptr(out, _c_double_p))
     return out[:n]
+
+
+def _d(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=np.float64).ravel()
+
+
+def _dp(a):
+    return None if a is None else _ptr(a, _c_double_p)
+
+
+def policy_loss(kind, lp, old, w, mask, T, per_seq=False, low=0.2, high=0.2, dual=None, clamp=20.0):
+    """(loss, dloss, hit) per token, f64 (or_policy_loss): kind "pg" or "ppo"; dual/clamp None
+    for none."""
+    lp, old, w, m = _d(lp), _d(old), _d(w), _d(mask)
+    n = lp.size
+    loss, dloss, hit = np.empty(n), np.empty(n), np.empty(n)
+    lib().or_policy_loss(0 if kind == "pg" else 1, n, T, _dp(lp), _dp(old), _dp(w), 1 if per_seq else 0, _dp(m),
+                         low, high, 0.0 if dual is None else float(dual), 0.0 if clamp is None else float(clamp),
+                         _dp(loss), _dp(dloss), _dp(hit))
+    return loss, dloss, hit
+
+
+def reduce_tokens_backward(mask, shape, reduction, up=None, scale=1.0, local=None):
+    S, B, T = shape
+    m, u, loc = _d(mask), _d(up), _d(local)
+    out = np.empty(S * B * T)
+    lib().or_reduce_tokens_backward(_dp(m), S, B, T, REDUCTIONS[reduction], _dp(u), scale, _dp(loc), _dp(out))
+    return out
+
+
+def kl_estimate_grad(lp, lr, est, clamp=None, mask=None):
+    lp, lr, m = _d(lp), _d(lr), _d(mask)
+    out = np.empty_like(lp)
+    lib().or_kl_estimate_grad(_dp(lp), _dp(lr), _dp(m), lp.size, est, 0.0 if clamp is None else float(clamp),
+                              _dp(out))
+    return out
 
 
 def group_advantages(rewards, n, norm="mean", eps=0.0, unbiased=True):

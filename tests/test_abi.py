@@ -43,7 +43,8 @@ def test_argument_struct_layouts_match_the_header():
     import tempfile
     fields = {"NtRlSampleArgs": [f[0] for f in nr.NtRlSampleArgs._fields_],
               "NtRlScoreArgs": [f[0] for f in nr.NtRlScoreArgs._fields_],
-              "NtRlScoreGradArgs": [f[0] for f in nr.NtRlScoreGradArgs._fields_]}
+              "NtRlScoreGradArgs": [f[0] for f in nr.NtRlScoreGradArgs._fields_],
+              "NtRlPolicyLossArgs": [f[0] for f in nr.NtRlPolicyLossArgs._fields_]}
     body = []
     for st, fs in fields.items():
         body.append(f'printf("{st} %zu\\n", sizeof({st}));')
@@ -62,7 +63,7 @@ def test_argument_struct_layouts_match_the_header():
         for f in fs:
             assert int(got[f"{st}.{f}"]) == getattr(cls, f).offset, (st, f)
     assert int(got["NtRlSampleArgs"]) == 104 and int(got["NtRlScoreArgs"]) == 152
-    assert int(got["NtRlScoreGradArgs"]) == 176
+    assert int(got["NtRlScoreGradArgs"]) == 176 and int(got["NtRlPolicyLossArgs"]) == 120
 
 
 def test_without_a_claimed_device_calls_fail_cleanly():
@@ -104,6 +105,21 @@ def test_argument_validation_precedes_the_device():
     g.grad_dtype, g.grad_ld = nr.NT_BF16, 8
     assert L.nt_hip_rl_score_backward(C.byref(g)) == -1
     assert "grad_ld" in L.nt_hip_last_error().decode()
+    # the policy losses check Clip::check's ranges (rl.rs:189-200) before the device
+    pl = nr.NtRlPolicyLossArgs(logp=h, old_logp=h, weights=h, S=1, B=1, T=4, kind=nr.NT_LOSS_PPO, clip_low=1.0,
+                               clip_high=0.2, log_ratio_clamp=20.0)
+    assert L.nt_hip_rl_policy_loss(C.byref(pl)) == -1
+    assert "need 0 ≤ low < 1" in L.nt_hip_last_error().decode()
+    pl.clip_low, pl.dual = 0.2, 0.5
+    assert L.nt_hip_rl_policy_loss(C.byref(pl)) == -1
+    assert "dual clip 0.5 (need c > 1)" in L.nt_hip_last_error().decode()
+    pl.dual, pl.log_ratio_clamp = 0.0, -1.0
+    assert L.nt_hip_rl_policy_loss(C.byref(pl)) == -1
+    assert "log-ratio clamp" in L.nt_hip_last_error().decode()
+    pl.log_ratio_clamp, pl.old_logp = 20.0, None
+    assert L.nt_hip_rl_policy_loss(C.byref(pl)) == -1
+    with pytest.raises(ValueError, match="need c > 1"):
+        nr.Clip.symmetric(0.2).with_dual(1.0).check()
 
 
 def test_product_stream_equals_the_oracle_stream():

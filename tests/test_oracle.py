@@ -427,3 +427,126 @@ def test_score_grad_large_and_excluded_logits():
     zr = np.array([[0.2, -np.inf, 0.9, 3.0]], np.float32)
     got = O.score_grad(z, [1], zr, [1.0], [0.3], [0.2])
     assert got[0, 3] == 0.0 and got[0, 1] == 1.0 and np.all(np.isfinite(got))
+
+
+# ----------------------------------------------------------------------------- policy losses
+
+def test_policy_gradient_reductions_by_hand():
+    # tests/rl.rs:160-179: logp [-1..-6] as [1,2,3], per-sequence weights [1,-2], mask [1 1 0; 0 1 0]
+    lp = np.array([-1.0, -2.0, -3.0, -4.0, -5.0, -6.0])
+    w = np.array([1.0, -2.0])
+    m = np.array([1.0, 1.0, 0.0, 0.0, 1.0, 0.0])
+    per, dper, _ = O.policy_loss("pg", lp, None, w, m, 3, per_seq=True)
+    assert per.tolist() == [1.0, 2.0, 0.0, 0.0, -10.0, 0.0]
+    assert dper.tolist() == [-1.0, -1.0, 0.0, 0.0, 2.0, 0.0]
+    red = lambda r: O.reduce_tokens(per, m, (1, 2, 3), r).tolist()
+    assert red("sum") == [-7.0]
+    assert abs(red("token_mean")[0] + 7.0 / 3.0) < 1e-15
+    assert red("per_sequence") == [1.5, -10.0]
+    assert red("sequence_mean") == [-4.25]
+    per_all, _, _ = O.policy_loss("pg", lp, None, w, None, 3, per_seq=True)
+    assert O.reduce_tokens(per_all, None, (1, 2, 3), "sum").tolist() == [6.0 - 30.0]
+
+
+def test_clipped_policy_loss_overflow_guard_known_answers():
+    # tests/rl.rs:725-750 in f64: A = -1 with a log-ratio of 100; an on-policy token with A = 1
+    lp, old, adv = np.array([-0.5, -1.0]), np.array([-100.5, -1.0]), np.array([-1.0, 1.0])
+    loss, dloss, hit = O.policy_loss("ppo", lp, old, adv, None, 2, low=0.2, high=0.2, clamp=20.0)
+    assert abs(loss[0] - math.exp(20.0)) <= 1e-9 * math.exp(20.0) and dloss[0] == 0.0
+    assert loss[1] == -1.0 and dloss[1] == -1.0
+    loss, dloss, _ = O.policy_loss("ppo", lp, old, adv, None, 2, dual=3.0, clamp=20.0)
+    assert (loss[0], dloss[0]) == (3.0, 0.0)
+    loss, _, _ = O.policy_loss("ppo", lp, old, adv, None, 2, clamp=None)
+    assert loss[0] == math.exp(100.0)  # f64 holds it; f32 overflows to +inf (tested on the device)
+    assert O.reduce_tokens(hit, None, (1, 1, 2), "token_mean").tolist() == [0.5]
+
+
+def _ppo_case(seed, n=60, T=5):
+    # tests/rl.rs:228-235's construction: old = logp + offsets so every ratio exp(-o) is away from
+    # the clip edges (1.65, 1.105, 0.95, 0.67, and 4.48 for a dual clip), advantages of both signs
+    rng = np.random.default_rng(seed)
+    lp = -rng.uniform(0.1, 4.0, n)
+    offs = np.array([-1.5, -0.5, -0.1, 0.05, 0.4])
+    old = lp + offs[(np.arange(n) * 7 + np.arange(n) // 3) % 5]
+    adv = rng.uniform(-2.0, 2.0, n)
+    adv = np.where(np.abs(adv) < 0.1, -0.5, adv)
+    mask = (rng.random(n) < 0.8).astype(np.float64)
+    return lp, old, adv, mask, T
+
+
+@pytest.mark.parametrize("clip", [dict(low=0.2, high=0.2), dict(low=0.2, high=0.28),
+                                  dict(low=0.2, high=0.2, dual=3.0), dict(low=0.1, high=0.3, clamp=None)])
+def test_policy_loss_derivatives_match_finite_differences(clip):
+    lp, old, adv, mask, T = _ppo_case(840)
+    _, dloss, _ = O.policy_loss("ppo", lp, old, adv, mask, T, **clip)
+    h = 1e-6
+    for i in range(lp.size):
+        e = np.zeros_like(lp)
+        e[i] = h
+        fd = (O.policy_loss("ppo", lp + e, old, adv, mask, T, **clip)[0][i] -
+              O.policy_loss("ppo", lp - e, old, adv, mask, T, **clip)[0][i]) / (2 * h)
+        assert abs(fd - dloss[i]) <= 1e-7 * (1 + abs(fd)), (i, fd, dloss[i])
+    # PG: the derivative is -w, per token and per sequence
+    w = np.random.default_rng(1).uniform(-2, 2, lp.size // T)
+    _, d, _ = O.policy_loss("pg", lp, None, w, mask, T, per_seq=True)
+    assert np.array_equal(d, np.where(mask != 0, -np.repeat(w, T), 0.0))
+
+
+def test_ppo_on_policy_gradient_equals_pg_and_bounds_give_zero():
+    # tests/rl.rs:297-313: at old = logp the PPO derivative is the PG one with the advantages as
+    # weights; a clipped-and-active token (A > 0, r > 1.2 or A < 0, r < 0.8) gets zero, others -A r
+    lp, old, adv, mask, T = _ppo_case(850)
+    _, d_ppo, _ = O.policy_loss("ppo", lp, lp, adv, mask, T)
+    _, d_pg, _ = O.policy_loss("pg", lp, None, adv, mask, T)
+    assert np.array_equal(d_ppo, d_pg)
+    _, d, hit = O.policy_loss("ppo", lp, old, adv, mask, T)
+    r = np.exp(lp - old)
+    clipped = ((adv > 0) & (r > 1.2)) | ((adv < 0) & (r < 0.8))
+    want = np.where((mask == 0) | clipped, 0.0, -adv * r)
+    assert np.allclose(d, want, rtol=1e-14, atol=0)
+    assert np.array_equal(hit, np.where(mask != 0, clipped.astype(float), 0.0))
+    # a dual clip c = 3 caps A < 0 tokens with r > 3 at -3A, with zero derivative
+    loss, d, hit = O.policy_loss("ppo", lp, old, adv, mask, T, dual=3.0)
+    capped = (mask != 0) & (adv < 0) & (r > 3.0)
+    assert capped.any()
+    assert np.array_equal(loss[capped], -3.0 * adv[capped]) and np.all(d[capped] == 0.0)
+    assert np.all(hit[capped] == 1.0)
+
+
+@pytest.mark.parametrize("reduction", ["none", "sum", "token_mean", "per_sequence", "sequence_mean"])
+def test_reduce_tokens_backward_matches_finite_differences(reduction):
+    S, B, T = 2, 3, 4
+    rng = np.random.default_rng(7)
+    per = rng.normal(0, 1, S * B * T)
+    mask = (rng.random(S * B * T) < 0.6).astype(np.float64)
+    mask[(0 * B + 1) * T:(0 * B + 2) * T] = 0.0  # an empty sequence
+    mask[S * B * T // 2:] = 0.0                  # an empty seed
+    per = np.where(mask != 0, per, 0.0)
+    n_out = O.reduce_tokens(per, mask, (S, B, T), reduction).size
+    up = rng.normal(0, 1, n_out)
+    local = rng.normal(0, 1, S * B * T)
+    got = O.reduce_tokens_backward(mask, (S, B, T), reduction, up, 0.5, local)
+    h = 1e-6
+    for i in range(S * B * T):
+        e = np.zeros_like(per)
+        e[i] = h
+        f = lambda x: float(up @ O.reduce_tokens(np.where(mask != 0, x, 0.0), mask, (S, B, T), reduction))
+        fd = 0.5 * local[i] * (f(per + e) - f(per - e)) / (2 * h)
+        assert abs(fd - got[i]) <= 1e-8 * (1 + abs(fd)), (reduction, i, fd, got[i])
+
+
+def test_kl_estimate_derivatives_match_finite_differences():
+    rng = np.random.default_rng(9)
+    lp = -rng.uniform(0.1, 5, 40)
+    lr = lp + rng.normal(0, 1.5, 40)
+    lr[3] = lp[3] + 30.0  # beyond a clamp of 20
+    mask = (rng.random(40) < 0.8).astype(np.float64)
+    h = 1e-6
+    for est in (1, 2, 3):
+        for clamp in (None, 20.0):
+            g = O.kl_estimate_grad(lp, lr, est, clamp, mask)
+            for i in range(40):
+                e = np.zeros(40)
+                e[i] = h
+                fd = (O.kl_estimate(lp + e, lr, est, clamp, mask)[i] - O.kl_estimate(lp - e, lr, est, clamp, mask)[i]) / (2 * h)
+                assert abs(fd - g[i]) <= 1e-6 * (1 + abs(fd)), (est, clamp, i, fd, g[i])
