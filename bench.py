@@ -17,7 +17,7 @@ object (the reference's Cpu(Reference) op sequence, restated in oracle/, timed o
       of g_logp logp + g_kl KL + g_H H with respect to the logits, in bf16;
   c5  rollout scoring, f32 [4,32,1024,151936] + u8 mask: logp and entropy (nt_hip_rl_score),
       the per-sequence mean log-probability (nt_hip_rl_reduce_tokens) and group-relative
-      advantages over groups of 8 along B (host f64, where the reference computes them).
+      advantages over groups of 8 along B (nt_hip_rl_group_advantages, f64 on the device).
 """
 import argparse
 import ctypes as C
@@ -308,12 +308,14 @@ def bench_score(nr, W, args, name):
         S, B, T = shp
         seq = nr.Tensor((S, B), "f32")
 
+        adv = nr.Tensor((S, B), "f32")
+
         def step(i):
             score(i)
             nr._check(L.nt_hip_rl_reduce_tokens(lp.ptr, None, S, B, T, int(nr.TokenReduction.PER_SEQUENCE), seq.ptr),
                       "reduce_tokens")
-            # group-relative advantages over groups of 8 along B: host f64 (rl.rs:416-469)
-            nr.group_advantages(seq.to_f64().ravel(), 8)
+            # group-relative advantages over groups of 8 along B (rl.rs:416-469), on the device
+            nr._check(L.nt_hip_rl_group_advantages(seq.ptr, S * B // 8, 8, 1, 1e-6, 1, adv.ptr), "group_advantages")
     ms, wall = timed(nr, args.steps, args.warmup, step)
     st = status.to_numpy()
     if np.any(st != 0):

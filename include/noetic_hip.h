@@ -221,6 +221,15 @@ int nt_hip_rl_reduce_tokens_backward(const float *mask, int64_t S, int64_t B, in
 int nt_hip_rl_kl_estimate_backward(const float *logp, const float *ref_logp, const float *mask, int64_t n,
                                    int32_t estimator, double clamp, float *out);
 
+/* group_advantages_tensor (rl.rs:416-469) on the device: rewards [groups, n] (f32, row-major),
+ * each reward minus its group's mean, divided by the group's standard deviation plus eps when
+ * norm is 1 (GroupNorm::Std; unbiased 1: the sample standard deviation, n - 1, which needs
+ * n >= 2; 0: the population one) or by 1 when norm is 0 (MeanOnly); a group whose rewards are all
+ * equal gives exact zeros. In f64, with the group's sums taken left to right as the reference's
+ * host loop takes them, then rounded to f32. */
+int nt_hip_rl_group_advantages(const float *rewards, int64_t groups, int64_t n, int32_t norm, double eps,
+                               int32_t unbiased, float *out);
+
 enum { NT_LOSS_PG = 0, NT_LOSS_PPO = 1 };
 
 /* The policy losses per token (rl.rs:228-317), before reduce_tokens.

@@ -1954,6 +1954,37 @@ __global__ void k_policy_loss(LossP p) {
     }
 }
 
+// group_advantages (rl.rs:436-463): one thread per group, f64, sums left to right.
+__global__ void k_group_advantages(const float *r, int64_t groups, int64_t n, int std_norm, double eps, int unbiased,
+                                   float *out) {
+    const int64_t g = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+    if (g >= groups) return;
+    const float *x = r + g * n;
+    float *y = out + g * n;
+    double lo = INFINITY, hi = -INFINITY, sum = 0.0;
+    for (int64_t i = 0; i < n; i++) {
+        const double v = double(x[i]);
+        lo = v < lo ? v : lo;
+        hi = v > hi ? v : hi;
+    }
+    if (lo == hi) {
+        for (int64_t i = 0; i < n; i++) y[i] = 0.0f;
+        return;
+    }
+    for (int64_t i = 0; i < n; i++) sum += double(x[i]);
+    const double mean = sum / double(n);
+    double scale = 1.0;
+    if (std_norm) {
+        double ss = 0.0;
+        for (int64_t i = 0; i < n; i++) {
+            const double d = double(x[i]) - mean;
+            ss += d * d;
+        }
+        scale = sqrt(ss / (unbiased ? double(n - 1) : double(n))) + eps;
+    }
+    for (int64_t i = 0; i < n; i++) y[i] = float((double(x[i]) - mean) / scale);
+}
+
 __global__ void k_kl_estimate_grad(const float *lp, const float *lr, const float *mask, int64_t n, int est,
                                    float clamp, int clamped, float *out) {
     for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
@@ -2350,6 +2381,23 @@ int nt_hip_rl_kl_estimate_backward(const float *logp, const float *ref_logp, con
     hipLaunchKernelGGL(k_kl_estimate_grad, dim3(unsigned(blocks)), dim3(256), 0, ctx().stream, logp, ref_logp, mask, n,
                        int(estimator), float(clamp), clamp > 0.0 ? 1 : 0, out);
     return launched("nt_hip_rl_kl_estimate_backward");
+}
+
+int nt_hip_rl_group_advantages(const float *rewards, int64_t groups, int64_t n, int32_t norm, double eps,
+                               int32_t unbiased, float *out) {
+    if (!rewards || !out || groups < 0 || (norm != 0 && norm != 1))
+        return fail(NT_E_ARG, "nt_hip_rl_group_advantages: invalid arguments");
+    if (n < 1) return fail(NT_E_ARG, "group_advantages: rewards in groups of " + std::to_string(n));
+    if (norm == 1 && !(eps >= 0.0)) return fail(NT_E_ARG, "group_advantages: ε " + std::to_string(eps) + " < 0");
+    if (norm == 1 && unbiased && n < 2)
+        return fail(NT_E_ARG, "group_advantages: the sample standard deviation needs groups of at least 2");
+    std::unique_lock<std::mutex> lk;
+    if (int rc = enter(&lk)) return rc;
+    if (groups == 0) return 0;
+    const int threads = 64;
+    hipLaunchKernelGGL(k_group_advantages, dim3(unsigned((groups + threads - 1) / threads)), dim3(threads), 0,
+                       ctx().stream, rewards, groups, n, int(norm), eps, int(unbiased != 0), out);
+    return launched("nt_hip_rl_group_advantages");
 }
 
 int nt_hip_rl_policy_loss(const NtRlPolicyLossArgs *a) {

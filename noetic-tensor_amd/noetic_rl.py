@@ -113,6 +113,8 @@ _SIGS = {
     "nt_hip_rl_kl_estimate_backward": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_int32,
                                                  C.c_double, C.c_void_p]),
     "nt_hip_rl_policy_loss": (C.c_int, [C.POINTER(NtRlPolicyLossArgs)]),
+    "nt_hip_rl_group_advantages": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_int32, C.c_double, C.c_int32,
+                                             C.c_void_p]),
     # noetic_rng.h
     "nt_rng_derive": (C.c_int, [C.POINTER(NtRng), C.c_uint64, C.c_char_p, C.c_size_t]),
     "nt_rng_from_seed": (C.c_int, [C.POINTER(NtRng), C.c_char_p]),
@@ -732,7 +734,16 @@ def group_advantages(rewards: Sequence[float], n: int, norm: str = "mean", eps: 
 
 
 def group_advantages_tensor(rewards: Tensor, norm: str = "mean", eps: float = 0.0, unbiased: bool = True) -> Tensor:
-    """rl.rs:465-469: the last axis grouped; read to the host and written back (same shape)."""
+    """rl.rs:465-469: the last axis grouped, computed on the device (f64 per group, the
+    reference's host arithmetic) with no host round trip; same shape, f32."""
+    if len(rewards.shape) == 0:
+        raise ValueError("group_advantages_tensor: rewards of rank 0")
+    if rewards.dtype != "f32":
+        raise ValueError(f"group_advantages_tensor: rewards of dtype {rewards.dtype} (f32)")
+    if norm not in ("mean", "std"):
+        raise ValueError(f"group_advantages: norm {norm!r} (mean or std)")
     n = rewards.shape[-1]
-    adv = group_advantages(rewards.to_f64().ravel(), n, norm, eps, unbiased)
-    return Tensor.from_numpy(adv.reshape(rewards.shape).astype(np.float32), "f32")
+    out = Tensor(rewards.shape, "f32")
+    _check(lib().nt_hip_rl_group_advantages(rewards.ptr, rewards.numel // max(n, 1), n, 1 if norm == "std" else 0,
+                                            float(eps), 1 if unbiased else 0, out.ptr), "group_advantages")
+    return out

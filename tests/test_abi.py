@@ -120,6 +120,11 @@ def test_argument_validation_precedes_the_device():
     assert L.nt_hip_rl_policy_loss(C.byref(pl)) == -1
     with pytest.raises(ValueError, match="need c > 1"):
         nr.Clip.symmetric(0.2).with_dual(1.0).check()
+    # group_advantages' refusals (rl.rs:437-441)
+    assert L.nt_hip_rl_group_advantages(h, 2, 1, 1, 1e-6, 1, h) == -1
+    assert "needs groups of at least 2" in L.nt_hip_last_error().decode()
+    assert L.nt_hip_rl_group_advantages(h, 2, 2, 1, -1.0, 0, h) == -1
+    assert "< 0" in L.nt_hip_last_error().decode()
 
 
 def test_product_stream_equals_the_oracle_stream():

@@ -251,3 +251,37 @@ def test_ppo_objective_gradient_through_the_logits_matches_finite_differences():
     assert np.all(err <= 1e-6 + 1e-4 * np.abs(fd)), f"worst {err.max():.2e} at {np.unravel_index(err.argmax(), x.shape)}"
     assert np.all(grad[mask == 0] == 0.0), "masked positions get no gradient"
     print(f"PPO objective gradient: {x.size} logits, worst |Δ| {err.max():.2e}, max |grad| {np.abs(fd).max():.3e}")
+
+
+def test_group_advantages_on_the_device():
+    # tests/rl.rs:551-575 and 645-653 on the device: hand values, equal rewards give exact zeros
+    # whatever the normalisation, groups of one; then many groups against the oracle to the bit
+    # (f64 per group, rounded to f32)
+    r = np.array([1.0, 0.0, 0.0, 1.0, 2.0, 2.0, 2.0, 2.0, 0.0, 0.0, 0.0, 3.0], np.float32)
+    rt = t(r, (3, 4))
+    s3 = 0.5 / math.sqrt(1.0 / 3.0)
+    got = nr.group_advantages_tensor(rt, "std", 0.0, True).to_numpy().ravel()
+    assert np.array_equal(got, np.float32([s3, -s3, -s3, s3, 0, 0, 0, 0, -0.5, -0.5, -0.5, 1.5]))
+    p3 = math.sqrt(1.6875)
+    got = nr.group_advantages_tensor(rt, "std", 0.0, False).to_numpy().ravel()
+    assert np.array_equal(got, np.float32([1, -1, -1, 1, 0, 0, 0, 0, -0.75 / p3, -0.75 / p3, -0.75 / p3, 2.25 / p3]))
+    got = nr.group_advantages_tensor(rt, "mean").to_numpy().ravel()
+    assert got.tolist() == [0.5, -0.5, -0.5, 0.5, 0.0, 0.0, 0.0, 0.0, -0.75, -0.75, -0.75, 2.25]
+    got = nr.group_advantages_tensor(rt, "std", 1e-2, True).to_numpy().ravel()
+    assert np.array_equal(got[8:], np.float32([-0.75 / 1.51, -0.75 / 1.51, -0.75 / 1.51, 2.25 / 1.51]))
+    assert nr.group_advantages_tensor(t([3.0, -1.0], (2, 1)), "std", 1e-6, False).to_numpy().ravel().tolist() == [0, 0]
+    eq = t([0.1, 0.1, 0.1, 1.0, 0.0, 0.0], (2, 3))
+    for norm, unb in (("std", True), ("std", False), ("mean", True)):
+        a = nr.group_advantages_tensor(eq, norm, 0.0, unb).to_numpy().ravel()
+        assert a[:3].tolist() == [0.0, 0.0, 0.0] and a[3] > 0 and a[4] < 0 and a[4] == a[5], (norm, unb)
+    with pytest.raises(nr.HipError, match="at least 2"):
+        nr.group_advantages_tensor(t([1.0, 2.0], (2, 1)), "std", 1e-6, True)
+    rng = np.random.default_rng(465)
+    for G, n in ((65536, 8), (1000, 1000), (4096, 2)):
+        rw = rng.normal(0, 1, (G, n)).astype(np.float32)
+        rw[::7] = rw[::7, :1]                       # equal-reward groups
+        rw[1::5] = np.round(rw[1::5])               # binary-ish verifier rewards
+        for norm, eps, unb in (("std", 1e-6, True), ("std", 0.0, False), ("mean", 0.0, True)):
+            got = nr.group_advantages_tensor(t(rw, (G, n)), norm, eps, unb).to_numpy().ravel()
+            want = O.group_advantages(rw.astype(np.float64).ravel(), n, norm, eps, unb).astype(np.float32)
+            assert np.array_equal(got, want), (G, n, norm, int((got != want).sum()))
