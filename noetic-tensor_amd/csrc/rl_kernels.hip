@@ -44,6 +44,10 @@ constexpr int kWave = 64;
 constexpr int kEpl = 8;                  // elements per lane per chunk
 constexpr int kChunk = kWave * kEpl;     // 512 elements per chunk
 constexpr int kBatch = 4;                // chunks per wave with loads in flight together
+// The most a lane's 8 weights of one chunk may sum to before its exponent reference moves to the
+// chunk's maximum, where a finishing difference of two log-sums must stay small (entropy, KL):
+// the reference then trails the maximum by at most log2 32 = 5 (log2 units).
+constexpr float kChunkSumCap = 32.0f;
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr double kLn2 = 0.69314718055994530942;
 constexpr int kRowBadToken = NT_ROW_BAD_TOKEN;
@@ -520,7 +524,7 @@ __global__ __launch_bounds__(1024) void k_sample(SampleP p) {
         }
         const double lnS = log(S);
         p.ids[row] = int32_t(id);
-        if (p.logp) p.logp[row] = float(double(zid - mz) - lnS);
+        if (p.logp) p.logp[row] = float((double(zid) - double(mz)) - lnS);
         if (p.ent) p.ent[row] = float(lnS - kLn2 * H2 / S);
         p.status[row] = NT_ROW_OK;
     }
@@ -553,6 +557,8 @@ typedef __attribute__((address_space(3))) void *lds_ptr_t;
 constexpr int kBufferWord3 = 0x00020000;
 // Four dwords as the buffer load/store builtins take them.
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+// Buffer access cache policy for data read or written once: non-temporal.
+constexpr int kCachePolicyNT = 2;
 typedef __attribute__((address_space(1))) void *glb_ptr_t;
 
 template <int B, int E, class F>
@@ -959,8 +965,13 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
             };
             if (have_ref) {
                 weigh();
-                if (__ballot(!(gs < INFINITY)) != 0) {
-                    // An overflow (or a NaN, which compares false below and stays in the sums).
+                // An overflow (or a NaN, which compares false below and stays in the sums) moves
+                // the wave's reference to the chunk's maximum. With the entropy wanted, so does a
+                // lane's 8 weights summing to more than kChunkSumCap: the entropy is ln S - ln2 H / S,
+                // and a reference far below the maximum would make both terms large and cancelling.
+                bool move = !(gs < INFINITY);
+                if constexpr (ENT) move = !(gs <= kChunkSumCap);
+                if (__ballot(move) != 0) {
                     const float wm = wave_max3_dpp(max_hw<EPL>(v));
                     const float nref = wm * c;
                     if (nref > sref) {
@@ -1137,7 +1148,7 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
         const double lnS = ln_fast(S) + shiftA * kLn2;
         const float zid = (MK == NT_MASK_F32 || tau_one) ? vz : vz / p.tau;
         p.ids[row] = int32_t(id);
-        if (p.logp) p.logp[row] = float(double(zid - mz) - lnS);
+        if (p.logp) p.logp[row] = float((double(zid) - double(mz)) - lnS);
         if (p.ent) p.ent[row] = float(lnS - kLn2 * (pk.H / S + shiftA));
         p.status[row] = NT_ROW_OK;
     };
@@ -1307,6 +1318,61 @@ __device__ __forceinline__ RowState shfl_down_state(const RowState &s, int o) {
 constexpr int kScoreThreads = 256;
 constexpr int kScoreWaves = kScoreThreads / kWave;
 
+// load_raw for aligned rows through per-row buffer resources (row bytes below 2^31), no bounds
+// branch, 32-bit offsets, non-temporal (every input is read once). Past the row's end the
+// hardware range check returns zeros (the caller excludes those lanes). A lane's elements in a
+// 512-element chunk at c: bf16 c + 8l .. c + 8l + 7 (one 16-byte load per input); f32 two groups,
+// c + 4l .. c + 4l + 3 and c + 256 + 4l .. c + 256 + 4l + 3, so that each 16-byte load
+// instruction reads one contiguous kilobyte rather than every other 16 bytes of two (measured
+// faster with non-temporal loads). e0 is the lane's first element; each group lies wholly inside
+// the row or wholly past its end (V % 8 == 0).
+template <int DT>
+__device__ __forceinline__ int buf_lane_first(int chunk, int lane) {
+    return chunk * kChunk + lane * (DT == NT_F32 ? 4 : kEpl);
+}
+
+template <int DT, int MK>
+__device__ __forceinline__ void load_raw_buf(Raw<DT, MK> &r, __amdgpu_buffer_rsrc_t xres,
+                                             __amdgpu_buffer_rsrc_t mres, int e0) {
+    constexpr int kHalf = kChunk / 2;
+    if constexpr (DT == NT_F32) {
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const auto a = __builtin_amdgcn_raw_buffer_load_b128(xres, (e0 + q * kHalf) * 4, 0, kCachePolicyNT);
+            for (int i = 0; i < 4; i++) r.x[4 * q + i] = a[i];
+        }
+        if constexpr (MK == NT_MASK_U8) {
+            r.m[0] = __builtin_amdgcn_raw_buffer_load_b32(mres, e0, 0, kCachePolicyNT);
+            r.m[1] = __builtin_amdgcn_raw_buffer_load_b32(mres, e0 + kHalf, 0, kCachePolicyNT);
+        } else if constexpr (MK == NT_MASK_F32) {
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                const auto a = __builtin_amdgcn_raw_buffer_load_b128(mres, (e0 + q * kHalf) * 4, 0, kCachePolicyNT);
+                for (int i = 0; i < 4; i++) r.m[4 * q + i] = a[i];
+            }
+        } else {
+            r.m[0] = 0;
+        }
+    } else {
+        const auto a = __builtin_amdgcn_raw_buffer_load_b128(xres, e0 * 2, 0, kCachePolicyNT);
+        for (int i = 0; i < 4; i++) r.x[i] = a[i];
+        if constexpr (MK == NT_MASK_U8) {
+            const auto k = __builtin_amdgcn_raw_buffer_load_b64(mres, e0, 0, kCachePolicyNT);
+            r.m[0] = k[0];
+            r.m[1] = k[1];
+        } else if constexpr (MK == NT_MASK_F32) {
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                const auto a = __builtin_amdgcn_raw_buffer_load_b128(mres, e0 * 4 + 16 * q, 0, kCachePolicyNT);
+                for (int i = 0; i < 4; i++) r.m[4 * q + i] = a[i];
+            }
+        } else {
+            r.m[0] = 0;
+        }
+    }
+}
+
+
 template <int DT, int MK, bool REF, bool KL, bool ENT, bool AL>
 __global__ __launch_bounds__(kScoreThreads) void k_score(ScoreP p) {
     __shared__ RowState ws[kScoreWaves];
@@ -1322,6 +1388,18 @@ __global__ __launch_bounds__(kScoreThreads) void k_score(ScoreP p) {
     const void *mrow = nullptr;
     if constexpr (MK != NT_MASK_NONE) mrow = static_cast<const char *>(p.mask) + row * p.mask_ld * MaskWords<MK>::kBytes;
 
+    // (used by the aligned path only, whose rows are below 2^31 bytes)
+    const int Vb = AL ? int(p.V) : 0;
+    const __amdgpu_buffer_rsrc_t xres =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(xrow), short(0), Vb * Elem<DT>::kBytes, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t yres =
+        REF ? __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(yrow), short(0), Vb * Elem<DT>::kBytes, kBufferWord3)
+            : xres;
+    const __amdgpu_buffer_rsrc_t mres =
+        MK != NT_MASK_NONE ? __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(mrow), short(0),
+                                                               Vb * MaskWords<MK>::kBytes, kBufferWord3)
+                           : xres;
+
     RowState st{-INFINITY, 0.0f, 0.0f, 0.0f, -INFINITY, 0.0f};
     for (int c0 = wave; c0 < p.nc; c0 += nw * kBatch) {
         Raw<DT, MK> rx[kBatch];
@@ -1329,9 +1407,15 @@ __global__ __launch_bounds__(kScoreThreads) void k_score(ScoreP p) {
 #pragma unroll
         for (int b = 0; b < kBatch; b++) {
             const int ch = c0 + b * nw;
-            const int64_t e0 = ch < p.nc ? int64_t(ch) * kChunk + lane * kEpl : p.V;
-            load_raw<DT, MK, AL>(rx[b], xrow, mrow, e0, p.V);
-            if constexpr (REF) load_raw<DT, NT_MASK_NONE, AL>(ry[b], yrow, nullptr, e0, p.V);
+            if constexpr (AL) {
+                const int e0 = ch < p.nc ? buf_lane_first<DT>(ch, lane) : int(p.V);
+                load_raw_buf<DT, MK>(rx[b], xres, mres, e0);
+                if constexpr (REF) load_raw_buf<DT, NT_MASK_NONE>(ry[b], yres, mres, e0);
+            } else {
+                const int64_t e0 = ch < p.nc ? int64_t(ch) * kChunk + lane * kEpl : p.V;
+                load_raw<DT, MK, AL>(rx[b], xrow, mrow, e0, p.V);
+                if constexpr (REF) load_raw<DT, NT_MASK_NONE, AL>(ry[b], yrow, nullptr, e0, p.V);
+            }
         }
 #pragma unroll
         for (int b = 0; b < kBatch; b++) {
@@ -1342,21 +1426,40 @@ __global__ __launch_bounds__(kScoreThreads) void k_score(ScoreP p) {
                 // The reference logits take the same temperature and vocabulary mask
                 // (reference_kl, rl.rs:347-351).
                 if constexpr (REF) decode_words<DT, MK>(ry[b].x, rx[b].m, vr, p.tau, tau_one);
-                // The chunk's weights against the lane's current references; the references
-                // move (and the sums are rescaled) only before the first chunk with a finite
-                // value, or when a weight or a sum overflows: then to the chunk's maximum, and
-                // at least 64/c above the old reference.
-                auto rescale = [&](bool pol, bool rf) {
+                if constexpr (AL) {
+                    // buffer loads past the row's end read zeros: only the last chunk can hold such
+                    // element groups, which take no part in the sums
+                    if (ch == p.nc - 1) {
+                        const int e0 = buf_lane_first<DT>(ch, lane);
+#pragma unroll
+                        for (int j = 0; j < kEpl; j++) {
+                            const int e = DT == NT_F32 ? e0 + (j < 4 ? j : kChunk / 2 + j - 4) : e0 + j;
+                            if (e >= int(p.V)) {
+                                v[j] = -INFINITY;
+                                vr[j] = -INFINITY;
+                            }
+                        }
+                    }
+                }
+                // The chunk's weights against the lane's current references. A reference is set
+                // at the first chunk with a finite value and moves (the sums are rescaled and
+                // the chunk weighed again) to the chunk's maximum whenever the lane's 8 weights
+                // of one chunk sum to more than kChunkSumCap: then no weight exceeds kChunkSumCap,
+                // so the reference trails the lane's maximum by at most log2 kChunkSumCap, the
+                // sums cannot overflow, and the finishing differences (ln S - ln2 H / S for the
+                // entropy, ln S - ln S_ref for the KL) stay small: no two terms of the size of the
+                // logits cancel. (A NaN fails the test too, and stays in the sums.)
+                auto rescale = [&](bool pol, bool rf, float an, float anr) {
                     float dold = 0.0f, eold = 0.0f, f = 1.0f;
                     if (pol) {
-                        const float an = fmaxf(max8_hw(v), st.a + 64.0f / c);
+                        an = fmaxf(an, st.a);
                         dold = (st.a - shift_of(an)) * c;
                         f = exp2_hw(dold);
                         st.a = an;
                     }
                     if constexpr (REF) {
                         if (rf) {
-                            const float anr = fmaxf(max8_hw(vr), st.ar + 64.0f / c);
+                            anr = fmaxf(anr, st.ar);
                             eold = (st.ar - shift_of(anr)) * c;
                             st.Sr = exp2_hw(eold) * st.Sr;
                             st.ar = anr;
@@ -1385,15 +1488,22 @@ __global__ __launch_bounds__(kScoreThreads) void k_score(ScoreP p) {
                         }
                     }
                 };
-                {
+                // A lane's first reference is the maximum of the wave's whole chunk (512 values),
+                // which makes later moves rare. (A wave-uniform branch: every lane takes part in
+                // the DPP maxima.)
+                if (__ballot(st.a == -INFINITY || (REF && st.ar == -INFINITY)) != 0) {
+                    const float wm = wave_max3_dpp(max8_hw(v));
+                    float wmr = -INFINITY;
+                    if constexpr (REF) wmr = wave_max3_dpp(max8_hw(vr));
                     const bool pol = st.a == -INFINITY, rf = REF && st.ar == -INFINITY;
-                    if (pol || rf) rescale(pol, rf);
+                    if (pol || rf) rescale(pol, rf, wm, wmr);
                 }
                 accumulate();
                 {
-                    const bool pol = !(S < INFINITY), rf = REF && !(Sr < INFINITY);
+                    // the chunk's weight sums (to within rounding, enough for the test)
+                    const bool pol = !(S - st.S <= kChunkSumCap), rf = REF && !(Sr - st.Sr <= kChunkSumCap);
                     if (pol || rf) {
-                        rescale(pol, rf);
+                        rescale(pol, rf, max8_hw(v), REF ? max8_hw(vr) : -INFINITY);
                         accumulate();
                     }
                 }
@@ -1464,7 +1574,7 @@ __global__ __launch_bounds__(kScoreThreads) void k_score(ScoreP p) {
         if ((tok < 0 || tok >= p.V) && stt == NT_ROW_OK) stt = kRowBadToken;
     }
     const bool rowok = stt == NT_ROW_OK || stt == kRowBadToken;
-    if (p.logp) p.logp[row] = stt == NT_ROW_OK ? float(double(ztok(xrow, tok) - zmax(af)) - lnS) : NAN;
+    if (p.logp) p.logp[row] = stt == NT_ROW_OK ? float((double(ztok(xrow, tok)) - double(zmax(af))) - lnS) : NAN;
     if (p.ent) p.ent[row] = rowok ? float(lnS - kLn2 * H / S) : NAN;
     // The log-sum-exp as base + rest (z units): the base is the tempered value of the row's
     // final reference, the rest ln of the sum relative to it.
@@ -1475,7 +1585,7 @@ __global__ __launch_bounds__(kScoreThreads) void k_score(ScoreP p) {
         if (p.ref_lse_base) p.ref_lse_base[row] = rok ? zmax(arf) : NAN;
         if (p.ref_lse_rest) p.ref_lse_rest[row] = rok ? float(log(Sr)) : NAN;
         if (p.ref_logp)
-            p.ref_logp[row] = (rok && tok >= 0 && tok < p.V) ? float(double(ztok(yrow, tok) - zmax(arf)) - log(Sr)) : NAN;
+            p.ref_logp[row] = (rok && tok >= 0 && tok < p.V) ? float((double(ztok(yrow, tok)) - double(zmax(arf))) - log(Sr)) : NAN;
         if constexpr (KL) {
             // KL = sum p ((z - m) - (z_ref - m_ref)) - ln S + ln S_ref; the first sum is
             // ln2 * B / S because c ln2 is the value-to-logit scale (1/T, or 1 with an f32 mask).
@@ -1509,7 +1619,6 @@ struct GradP {
 
 constexpr int kGradThreads = 256;
 constexpr int kGradStep = kGradThreads * kEpl;  // elements a block covers per step
-constexpr int kCachePolicyNT = 2;               // buffer access cache policy: non-temporal (streamed once)
 
 // f32 pair -> packed bf16 pair, round to nearest even (lo from a, hi from b).
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
@@ -2226,7 +2335,9 @@ int nt_hip_rl_score(const NtRlScoreArgs *a) {
     const bool ref = a->ref_logits != nullptr && (a->ref_logp || a->kl || a->ref_lse_base || a->ref_lse_rest);
     const bool kl = a->kl != nullptr;
     const bool ent = a->entropy != nullptr;
-    bool al = aligned_rows(a->logits, a->vocab, a->ld, a->dtype, a->mask_kind, a->mask, a->mask_ld);
+    // the aligned path addresses a row's bytes with 32-bit buffer offsets
+    bool al = aligned_rows(a->logits, a->vocab, a->ld, a->dtype, a->mask_kind, a->mask, a->mask_ld) &&
+              a->vocab * 4 <= int64_t(0x7fffffff);
     if (ref) al = al && reinterpret_cast<uintptr_t>(a->ref_logits) % 16 == 0;
     hipStream_t s = ctx().stream;
     if (a->dtype == NT_F32) pick_mk_score<NT_F32>(a->mask_kind, ref, kl, ent, al, p, a->rows, s);

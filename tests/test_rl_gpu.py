@@ -335,7 +335,7 @@ def test_c3_full_size_scoring():
     assert np.all(np.isfinite(lpn)) and np.all(lpn <= 0.0) and np.all(rlpn <= 0.0)
     assert np.all(kln >= -1e-6), f"KL < 0 at {np.nonzero(kln < -1e-6)[0][:4]}"
     assert np.all(entn >= 0.0) and np.all(entn <= math.log(V) * (1 + 1e-6))
-    sel = _sample_rows(rows, 48, 33)
+    sel = np.union1d(_sample_rows(rows, 48, 33), np.argsort(entn)[:16])
     xf = W.bf16_to_f32(W.download_rows(w["logits"], sel, V))
     yf = W.bf16_to_f32(W.download_rows(w["ref"], sel, V))
     tok = w["tokens"].to_numpy().ravel()[sel]
@@ -358,7 +358,8 @@ def test_c5_full_size_scoring_and_group_advantages():
     lpn, entn = lp.to_numpy().ravel(), ent.to_numpy().ravel()
     assert np.all(np.isfinite(lpn)) and np.all(lpn <= 0.0), "every scored token is kept"
     assert np.all(entn >= 0.0) and np.all(entn <= math.log(V) * (1 + 1e-6))
-    sel = _sample_rows(rows, 32, 55)
+    # random rows, and the 16 of lowest entropy (where the 1e-6 absolute floor is what holds)
+    sel = np.union1d(_sample_rows(rows, 32, 55), np.argsort(entn)[:16])
     x = W.download_rows(w["logits"], sel, V)
     keep = W.download_rows(w["mask"], sel, V)
     z = O.tempered(x, 1.0, keep=keep)
@@ -416,3 +417,42 @@ def test_sampler_mask_layouts_against_the_oracle(case):
     z = O.tempered(x, tau, addmask=add, keep=keep)
     ent = out[2].to_numpy().ravel() if want_ent else None
     check_sample(f"{case}", z, u, ids, lp, ent, bf16=False)
+
+
+def _peaked_rows(rows, V, seed, bf16):
+    """N(0,1) rows with one dominant logit (+20 .. +60) placed late in the row (after every
+    early reference has been set), at an index that differs per row; the tokens are the peaks,
+    whose logp is near 0 (where only the 1e-6 absolute floor holds)."""
+    rng = np.random.default_rng(seed)
+    x = rng.normal(0, 1, (rows, V)).astype(np.float32)
+    peak = (V - 1 - rng.integers(0, V // 3, rows)).astype(np.int64)
+    x[np.arange(rows), peak] = rng.uniform(20, 60, rows).astype(np.float32)
+    y = (x + rng.normal(0, 0.3, x.shape)).astype(np.float32)
+    if bf16:
+        xb, yb = O.bf16_from_f32(x), O.bf16_from_f32(y)
+        return O.bf16_to_f32(xb), O.bf16_to_f32(yb), nr.Tensor.from_numpy(xb, "bf16"), nr.Tensor.from_numpy(yb, "bf16"), peak
+    return x, y, nr.Tensor.from_numpy(x), nr.Tensor.from_numpy(y), peak
+
+
+@pytest.mark.parametrize("dtype,V", [("f32", 151936), ("bf16", 50304), ("f32", 4099)])
+def test_peaked_rows_scoring_keeps_the_tolerance(dtype, V):
+    # A late dominant logit: entropy and KL near 0 and logp near 0, computed as differences of
+    # log-sums (ln S - ln2 H / S, ln S - ln S_ref, (z - m) - ln S) that must not cancel.
+    rows = 48
+    x, y, xt, yt, peak = _peaked_rows(rows, V, V, dtype == "bf16")
+    tok = peak.astype(np.int32)
+    lp, rlp, kl, ent = nr.score(xt, yt, nr.Tensor.from_numpy(tok))
+    _score_check(f"peaked {dtype} V{V}", x, y, tok, lp.to_numpy(), rlp.to_numpy(), kl.to_numpy(), ent.to_numpy(),
+                 close_f32)
+    assert np.max(ent.to_numpy()) < 1e-2, "the rows are peaked"
+
+
+@pytest.mark.parametrize("dtype,V", [("bf16", 128256), ("f32", 32000), ("bf16", 1000), ("bf16", 151936)])
+def test_peaked_rows_sampling_keeps_the_tolerance(dtype, V):
+    # The sampler's logp of the (almost always drawn) peak, and its entropy, on the same rows.
+    rows = 64
+    x, _, xt, _, peak = _peaked_rows(rows, V, V + 1, dtype == "bf16")
+    u = np.random.default_rng(V).random(rows)
+    ids, lp, ent = nr.sample_logp(xt, 1.0, None, None, entropy=True, uniforms=nr.Tensor.from_numpy(u, "f64"))
+    check_sample(f"peaked {dtype} V{V}", x, u, ids.to_numpy().ravel(), lp.to_numpy().ravel(), ent.to_numpy().ravel())
+    assert np.mean(ids.to_numpy().ravel() == peak) > 0.9
