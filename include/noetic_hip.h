@@ -135,8 +135,9 @@ typedef struct NtRlScoreArgs {
     float *entropy;           /* [rows] out or NULL */
     uint8_t *status;          /* [rows] out or NULL: NT_ROW_* of the policy row */
     /* The row's log-sum-exp, for nt_hip_rl_score_backward: lse = lse_base + lse_rest with
-     * lse_base a finite point at most 5 ln 2 below the maximum of the tempered logits and lse_rest = ln sum exp(z - lse_base); both NaN on a
-     * refused row. Any of the four may be NULL. */
+     * lse_base a finite point at most 5 ln 2 below the maximum of the tempered logits and
+     * lse_rest = ln sum exp(z - lse_base); both NaN on a refused row. Any of the four may be
+     * NULL. */
     float *lse_base;          /* [rows] out or NULL (policy) */
     float *lse_rest;          /* [rows] out or NULL (policy) */
     float *ref_lse_base;      /* [rows] out or NULL (reference; needs ref_logits) */
