@@ -80,7 +80,8 @@ void or_sha256(const uint8_t *data, size_t len, uint8_t out[32]) {
     a += b; d ^= a; d = (d << 8) | (d >> 24);                                              \
     c += d; b ^= c; b = (b << 7) | (b >> 25);
 
-void or_chacha_block(const uint32_t key[8], uint64_t counter, uint64_t stream, uint32_t out[16]) {
+/* The block function with `rounds` rounds (20 for ChaCha20Rng, 8 for ChaCha8Rng). */
+void or_chacha_block_rounds(const uint32_t key[8], uint64_t counter, uint64_t stream, int rounds, uint32_t out[16]) {
     uint32_t s[16] = {0x61707865u, 0x3320646eu, 0x79622d32u, 0x6b206574u};
     for (int i = 0; i < 8; i++) s[4 + i] = key[i];
     s[12] = (uint32_t)counter;
@@ -89,7 +90,7 @@ void or_chacha_block(const uint32_t key[8], uint64_t counter, uint64_t stream, u
     s[15] = (uint32_t)(stream >> 32);
     uint32_t x[16];
     memcpy(x, s, sizeof x);
-    for (int r = 0; r < 10; r++) {
+    for (int r = 0; r < rounds / 2; r++) {
         QR(x[0], x[4], x[8], x[12]);
         QR(x[1], x[5], x[9], x[13]);
         QR(x[2], x[6], x[10], x[14]);
@@ -100,6 +101,10 @@ void or_chacha_block(const uint32_t key[8], uint64_t counter, uint64_t stream, u
         QR(x[3], x[4], x[9], x[14]);
     }
     for (int i = 0; i < 16; i++) out[i] = x[i] + s[i];
+}
+
+void or_chacha_block(const uint32_t key[8], uint64_t counter, uint64_t stream, uint32_t out[16]) {
+    or_chacha_block_rounds(key, counter, stream, 20, out);
 }
 
 void or_chacha_seed(or_chacha *r, const uint8_t seed[32]) {
@@ -669,5 +674,53 @@ void or_kl_estimate_grad(const double *lp, const double *lr, const double *mask,
         else if (est == 2) g = -d;
         else g = -expm1(d);
         out[i] = (scored && !active) ? g : 0.0;
+    }
+}
+
+
+/* ------------------------------------------------------------------ the reference's test inputs */
+
+/* rand_core 0.6.4's SeedableRng::seed_from_u64: PCG32 steps (state = state * mul + inc, then the
+ * XSH-RR output: ((state >> 18) ^ state) >> 27 rotated right by state >> 59) fill the 32-byte
+ * seed four little-endian bytes at a time. */
+void or_seed_from_u64(uint64_t state, uint64_t inc, uint8_t seed[32]) {
+    for (int i = 0; i < 8; i++) {
+        state = state * 6364136223846793005ull + inc;
+        const uint32_t xs = (uint32_t)(((state >> 18) ^ state) >> 27);
+        const uint32_t rot = (uint32_t)(state >> 59);
+        const uint32_t x = (xs >> rot) | (xs << ((32u - rot) & 31u));
+        for (int b = 0; b < 4; b++) seed[4 * i + b] = (uint8_t)(x >> (8 * b));
+    }
+}
+
+/* The reference's test helper rnd (src/tensor/tests/mod.rs:28-31): ChaCha8Rng::seed_from_u64(seed),
+ * then n draws of rand 0.8's gen_range(lo..hi) for f32: a u32 from the stream, its top 23 bits as
+ * the mantissa of a value in [1, 2), minus 1, times (hi - lo), plus lo (f32 arithmetic, no fused
+ * multiply-add), drawn again in the rare case the result reaches hi. The stream is consumed one
+ * 16-word block after another, each block's words in order (counter in words 12-13, stream 0). */
+void or_reference_rnd_f32(uint64_t seed, uint64_t inc, int64_t n, float lo, float hi, float *out) {
+    uint8_t sd[32];
+    or_seed_from_u64(seed, inc, sd);
+    or_chacha r;
+    or_chacha_seed(&r, sd);
+    const float scale = hi - lo;
+    for (int64_t i = 0; i < n; i++) {
+        for (;;) {
+            if (r.idx >= 16) {
+                or_chacha_block_rounds(r.key, r.counter, 0, 8, r.buf);
+                r.counter++;
+                r.idx = 0;
+            }
+            const uint32_t u = r.buf[r.idx++];
+            union { uint32_t b; float f; } v;
+            v.b = (u >> 9) | 0x3f800000u;
+            volatile float v01 = v.f - 1.0f;
+            volatile float prod = v01 * scale;
+            const float res = prod + lo;
+            if (res < hi) {
+                out[i] = res;
+                break;
+            }
+        }
     }
 }

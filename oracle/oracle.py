@@ -78,6 +78,7 @@ def lib():
         L.or_kl_estimate.argtypes = [_c_double_p, _c_double_p, _c_double_p, C.c_int64, C.c_int, C.c_double, _c_double_p]
         L.or_reduce_tokens.argtypes = [_c_double_p, _c_double_p, C.c_int64, C.c_int64, C.c_int64, C.c_int, _c_double_p]
         L.or_reduce_tokens.restype = C.c_int64
+        L.or_reference_rnd_f32.argtypes = [C.c_uint64, C.c_uint64, C.c_int64, C.c_float, C.c_float, _c_float_p]
         L.or_policy_loss.argtypes = [C.c_int, C.c_int64, C.c_int64, _c_double_p, _c_double_p, _c_double_p, C.c_int,
                                      _c_double_p, C.c_double, C.c_double, C.c_double, C.c_double, _c_double_p,
                                      _c_double_p, _c_double_p]
@@ -268,6 +269,18 @@ def reduce_tokens(per, mask, shape, reduction):
     n = lib().or_reduce_tokens(_ptr(per, _c_double_p), None if m is None else _ptr(m, _c_double_p),
                                S, B, T, REDUCTIONS[reduction], _ptr(out, _c_double_p))
     return out[:n]
+
+
+# rand_core 0.6.4's seed_from_u64 increment for its PCG32 steps
+PCG32_INC = 11634580027462260723
+
+
+def reference_rnd_f32(seed, n, lo, hi):
+    """The reference's test helper rnd (src/tensor/tests/mod.rs:28-31): ChaCha8Rng::seed_from_u64
+    then gen_range(lo..hi) as f32 (or_reference_rnd_f32)."""
+    out = np.empty(n, dtype=np.float32)
+    lib().or_reference_rnd_f32(seed, PCG32_INC, n, lo, hi, _ptr(out, _c_float_p))
+    return out
 
 
 def _d(a):

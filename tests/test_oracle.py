@@ -550,3 +550,27 @@ def test_kl_estimate_derivatives_match_finite_differences():
                 e[i] = h
                 fd = (O.kl_estimate(lp + e, lr, est, clamp, mask)[i] - O.kl_estimate(lp - e, lr, est, clamp, mask)[i]) / (2 * h)
                 assert abs(fd - g[i]) <= 1e-6 * (1 + abs(fd)), (est, clamp, i, fd, g[i])
+
+
+def test_chacha_stream_layout_matches_the_reference_fixtures():
+    # The reference's recorded burn fixtures (src/tensor/tests/fixtures/burn021-windows-x86_64.txt
+    # and burn021-macos-aarch64.txt, the same records on both platforms: add_scalar, mul_scalar,
+    # sum_dim2 of src/tensor/tests/f64ops.rs:12-24) hash the bits of outputs whose inputs come from
+    # ChaCha8Rng::seed_from_u64 and gen_range (src/tensor/tests/mod.rs:28-31). Reproducing them pins
+    # the ChaCha block layout and word order the oracle's ChaCha20 stream shares (with RFC 8439
+    # pinning the 20-round core), rand_core's seed expansion and rand's f32 range mapping.
+    records = {"add_scalar": "cbe9c8a9adc29c2d425c260f055b10adbd6444714471aa97519b2a7e9b72ccdb",
+               "mul_scalar": "19c77c93a882e0421e1e07d82a202d6f1633c7dce42085119519d85adf9ceef8",
+               "sum_dim2": "9de56d8c8dae0c91245cd23e063c8bb7d5ddc74ca56c9e4b1100e05647cb8425"}
+    x = O.reference_rnd_f32(1, 130, -3.0, 3.0)
+    v = (x.astype(np.float64) * 1.37).astype(np.float32).astype(np.float64)  # `ours` (f64ops.rs:7)
+    sha = lambda a: hashlib.sha256(np.ascontiguousarray(a, "<f8").tobytes()).hexdigest()
+    assert sha(v + 1e-6) == records["add_scalar"]
+    assert sha(v * 0.3) == records["mul_scalar"]
+    s = v.reshape(2, 5, 13)
+    assert sha([sum(list(s[i, j]), 0.0) for i in range(2) for j in range(5)]) == records["sum_dim2"]
+    # the check discriminates: the textbook PCG increment (a plausible mix-up) misses every record
+    bad = np.empty(130, dtype=np.float32)
+    O.lib().or_reference_rnd_f32(1, 1442695040888963407, 130, -3.0, 3.0, bad.ctypes.data_as(O._c_float_p))
+    vb = (bad.astype(np.float64) * 1.37).astype(np.float32).astype(np.float64)
+    assert sha(vb + 1e-6) != records["add_scalar"]
