@@ -401,6 +401,38 @@ float or_unrolled_sum_f32(const float *x, int64_t n) {
     return acc;
 }
 
+/* The same unrolled fold in f64 (kernels.rs:120-151 is generic over the element type). */
+double or_unrolled_sum_f64(const double *x, int64_t n) {
+    double p0 = 0, p1 = 0, p2 = 0, p3 = 0, p4 = 0, p5 = 0, p6 = 0, p7 = 0, acc = 0;
+    int64_t i = 0;
+    for (; i + 8 <= n; i += 8) {
+        p0 = p0 + x[i]; p1 = p1 + x[i + 1]; p2 = p2 + x[i + 2]; p3 = p3 + x[i + 3];
+        p4 = p4 + x[i + 4]; p5 = p5 + x[i + 5]; p6 = p6 + x[i + 6]; p7 = p7 + x[i + 7];
+    }
+    acc = acc + (p0 + p4);
+    acc = acc + (p1 + p5);
+    acc = acc + (p2 + p6);
+    acc = acc + (p3 + p7);
+    for (; i < n; i++) acc = acc + x[i];
+    return acc;
+}
+
+/* log_softmax along rows in the reference's operation order (activation.rs:30-42) in f64:
+ * shifted = x - max, lse = log(unrolled_sum(exp(shifted))), y = shifted - lse. The f32 form is
+ * or_cpuref_log_softmax. */
+void or_cpuref_log_softmax_f64(const double *x, int64_t rows, int64_t V, double *y) {
+    double *e = (double *)malloc((size_t)V * sizeof(double));
+    for (int64_t r = 0; r < rows; r++) {
+        const double *xr = x + r * V;
+        double m = xr[0];
+        for (int64_t k = 1; k < V; k++) m = xr[k] > m ? xr[k] : m;
+        for (int64_t k = 0; k < V; k++) e[k] = exp(xr[k] - m);
+        const double lse = log(or_unrolled_sum_f64(e, V));
+        for (int64_t k = 0; k < V; k++) y[r * V + k] = (xr[k] - m) - lse;
+    }
+    free(e);
+}
+
 static float first_max_f32(const float *x, int64_t V, int64_t *idx_out) {
     float best = x[0];
     int64_t idx = 0;

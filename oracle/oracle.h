@@ -131,6 +131,8 @@ int or_group_advantages(const double *rewards, int64_t len, int64_t n, int norm,
 
 /* ---- Cpu(Reference) op sequence in f32 (the timed CPU baseline) ---------------------- */
 /* ndarray's 8-partial unrolled sum (kernels.rs:122-148). */
+double or_unrolled_sum_f64(const double *x, int64_t n);
+void or_cpuref_log_softmax_f64(const double *x, int64_t rows, int64_t V, double *y);
 float or_unrolled_sum_f32(const float *x, int64_t n);
 /* log_softmax along the last axis, in the reference's op order with materialised
  * intermediates: max_dim, x - max, exp, sum_dim, log, shifted - lse (activation.rs:30-42). */

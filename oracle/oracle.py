@@ -88,6 +88,7 @@ def lib():
                                           _c_double_p]
         L.or_group_advantages.argtypes = [_c_double_p, C.c_int64, C.c_int64, C.c_int, C.c_double, C.c_int, _c_double_p]
         L.or_group_advantages.restype = C.c_int
+        L.or_cpuref_log_softmax_f64.argtypes = [_c_double_p, C.c_int64, C.c_int64, _c_double_p]
         L.or_unrolled_sum_f32.argtypes = [_c_float_p, C.c_int64]
         L.or_unrolled_sum_f32.restype = C.c_float
         L.or_cpuref_log_softmax.argtypes = [_c_float_p, C.c_int64, C.c_int64, _c_float_p]
@@ -330,6 +331,13 @@ def group_advantages(rewards, n, norm="mean", eps=0.0, unbiased=True):
 
 
 # ----------------------------------------------------------------------------- Cpu(Reference)
+
+def cpuref_log_softmax_f64(x):
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float64)
+    y = np.empty_like(x)
+    lib().or_cpuref_log_softmax_f64(_ptr(x, _c_double_p), x.shape[0], x.shape[1], _ptr(y, _c_double_p))
+    return y
+
 
 def unrolled_sum(x):
     x = _f32(x)

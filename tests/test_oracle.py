@@ -574,3 +574,17 @@ def test_chacha_stream_layout_matches_the_reference_fixtures():
     O.lib().or_reference_rnd_f32(1, 1442695040888963407, 130, -3.0, 3.0, bad.ctypes.data_as(O._c_float_p))
     vb = (bad.astype(np.float64) * 1.37).astype(np.float32).astype(np.float64)
     assert sha(vb + 1e-6) != records["add_scalar"]
+
+
+def test_cpuref_log_softmax_order_matches_the_reference_fixture():
+    # src/tensor/tests/f64ops.rs:21 records the reference's log_softmax (activation.rs:30-42) of
+    # [2,5,13] inputs along the last axis in f64; the record (same on both platforms) fixes its
+    # operation order, the unrolled lane sum of kernels.rs:120-151 included. A left-to-right sum
+    # (a plausible restatement) misses it.
+    record = "934eb3edd7b1924449a0c2b3f72727493eaee084a744c77a6dc69f820d8d36d9"
+    x = O.reference_rnd_f32(1, 130, -3.0, 3.0)
+    v = (x.astype(np.float64) * 1.37).astype(np.float32).astype(np.float64).reshape(10, 13)
+    sha = lambda a: hashlib.sha256(np.ascontiguousarray(a, "<f8").tobytes()).hexdigest()
+    assert sha(O.cpuref_log_softmax_f64(v)) == record
+    seq = [[(t - r.max()) - math.log(sum((math.exp(u - r.max()) for u in r), 0.0)) for t in r] for r in v]
+    assert sha(seq) != record
