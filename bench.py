@@ -320,7 +320,7 @@ def bench_score(nr, W, args, name):
     st = status.to_numpy()
     if np.any(st != 0):
         raise SystemExit(f"bench: {int(np.sum(st != 0))} rows refused")
-    roof = roofline(bytes_score, ms_score)
+    roof = roofline(bytes_score, ms_score, f"k_score_{name}_traffic.json")
     roof["kernel"] = "k_score"
     roof["kernel_ms"] = ms_score
     if name == "c3":
@@ -375,7 +375,7 @@ def bench_score_grad(nr, W, args):
     # backward, per row: policy and reference logits read, the gradient written (bf16), and the
     # token, four log-sum-exp values, KL, entropy and three upstream gradients read
     bytes_bwd = rows * (2 * 2 * V + 2 * V + 4 + 4 * 4 + 4 + 4 + 3 * 4)
-    roof = roofline(bytes_bwd, ms_bwd)
+    roof = roofline(bytes_bwd, ms_bwd, "k_score_grad_c3b_traffic.json")
     roof["kernel"] = "k_score_grad"
     roof["kernel_ms"] = ms_bwd
     metric = "rows/sec + achieved HBM GB/s, fused PPO scoring forward + backward (logp, KL, entropy), V=50304 bf16"
