@@ -636,6 +636,32 @@ class Clip:
             raise ValueError(f"log-ratio clamp {self.log_ratio_clamp} (need b > 0)")
 
 
+def check_scored_finite(what: str, logp: Tensor, mask: Optional[Tensor] = None) -> Optional[str]:
+    """rl.rs:200-212: None when every scored log-probability (mask != 0) is finite, else the
+    reference's message naming the first position that is not (a host read)."""
+    v = logp.to_f64().ravel()
+    m = None if mask is None else mask.to_f64().ravel()
+    bad = ~np.isfinite(v) if m is None else (~np.isfinite(v)) & (m != 0.0)
+    idx = np.nonzero(bad)[0]
+    if idx.size == 0:
+        return None
+    i = int(idx[0])
+    val = "inf" if v[i] == np.inf else ("-inf" if v[i] == -np.inf else "NaN")
+    return f"{what}: the scored log-probability at flat position {i} is {val} (not finite)"
+
+
+# The reference runs check_scored_finite in the losses in debug builds (rl.rs:214-221). Here it is
+# opt-in, since it reads the log-probabilities back to the host: NOETIC_RL_DEBUG_CHECKS=1.
+DEBUG_CHECKS = os.environ.get("NOETIC_RL_DEBUG_CHECKS") == "1"
+
+
+def _debug_check(what: str, logp: Tensor, mask: Optional[Tensor]):
+    if DEBUG_CHECKS:
+        e = check_scored_finite(what, logp, mask)
+        if e is not None:
+            raise AssertionError(e)
+
+
 def _policy_loss(kind: int, what: str, logp: Tensor, old_logp: Optional[Tensor], weights: Tensor,
                  mask: Optional[Tensor], clip: Optional[Clip]):
     """(loss, dloss, hit) per token from nt_hip_rl_policy_loss, with the reference's shape checks
@@ -659,6 +685,10 @@ def _policy_loss(kind: int, what: str, logp: Tensor, old_logp: Optional[Tensor],
         raise ValueError("rl: old log-probabilities shape")
     if clip is not None:
         clip.check()
+    if what != "clip_fraction":
+        _debug_check(what, logp, mask)
+        if old_logp is not None:
+            _debug_check(f"{what} (old log-probabilities)", old_logp, mask)
     loss, dloss, hit = Tensor(logp.shape, "f32"), Tensor(logp.shape, "f32"), Tensor(logp.shape, "f32")
     a = NtRlPolicyLossArgs(logp.ptr, None if old_logp is None else old_logp.ptr, weights.ptr,
                            None if mask is None else mask.ptr, S, B, T, kind, per_seq,
@@ -706,10 +736,32 @@ def clip_fraction(logp: Tensor, old_logp: Tensor, advantages: Tensor, mask: Opti
     return _reduce(hit, mask, TokenReduction.TOKEN_MEAN)
 
 
-def group_advantages(rewards: Sequence[float], n: int, norm: str = "mean", eps: float = 0.0,
+class GroupNorm:
+    """rl.rs:417-424: `GroupNorm.MEAN_ONLY` (r - mean) or `GroupNorm.std(eps, unbiased)`
+    ((r - mean) / (std + eps)). The functions also take the strings "mean" and "std"."""
+
+    def __init__(self, kind: str, eps: float = 0.0, unbiased: bool = True):
+        self.kind, self.eps, self.unbiased = kind, float(eps), bool(unbiased)
+
+    @staticmethod
+    def std(eps: float, unbiased: bool) -> "GroupNorm":
+        return GroupNorm("std", eps, unbiased)
+
+
+GroupNorm.MEAN_ONLY = GroupNorm("mean")
+
+
+def _norm(norm, eps, unbiased):
+    if isinstance(norm, GroupNorm):
+        return norm.kind, norm.eps, norm.unbiased
+    return norm, eps, unbiased
+
+
+def group_advantages(rewards: Sequence[float], n: int, norm="mean", eps: float = 0.0,
                      unbiased: bool = True) -> np.ndarray:
-    """rl.rs:436-463, on the host in f64 as the reference computes it. norm: "mean" (MeanOnly)
-    or "std" (GroupNorm::Std{eps, unbiased})."""
+    """rl.rs:436-463, on the host in f64 as the reference computes it. norm: a GroupNorm, or
+    "mean" (MeanOnly) / "std" (Std{eps, unbiased})."""
+    norm, eps, unbiased = _norm(norm, eps, unbiased)
     r = np.asarray(rewards, dtype=np.float64).ravel()
     if not (n >= 1 and r.size % n == 0):
         raise ValueError(f"group_advantages: {r.size} rewards in groups of {n}")
@@ -733,9 +785,10 @@ def group_advantages(rewards: Sequence[float], n: int, norm: str = "mean", eps: 
     return out
 
 
-def group_advantages_tensor(rewards: Tensor, norm: str = "mean", eps: float = 0.0, unbiased: bool = True) -> Tensor:
+def group_advantages_tensor(rewards: Tensor, norm="mean", eps: float = 0.0, unbiased: bool = True) -> Tensor:
     """rl.rs:465-469: the last axis grouped, computed on the device (f64 per group, the
     reference's host arithmetic) with no host round trip; same shape, f32."""
+    norm, eps, unbiased = _norm(norm, eps, unbiased)
     if len(rewards.shape) == 0:
         raise ValueError("group_advantages_tensor: rewards of rank 0")
     if rewards.dtype != "f32":

@@ -165,3 +165,12 @@ def test_python_mirror_refuses_like_the_reference_without_a_device():
     with pytest.raises(ValueError, match="at least 2"):
         nr.group_advantages([1.0, 2.0], 1, "std", 1e-6, True)
     assert nr.group_advantages([1, 0, 0, 1, 2, 2, 2, 2], 4).tolist() == [0.5, -0.5, -0.5, 0.5, 0, 0, 0, 0]
+
+
+def test_group_norm_forms_agree():
+    r = [1.0, 0.0, 0.0, 1.0, 2.0, 2.0, 2.0, 2.0, 0.0, 0.0, 0.0, 3.0]
+    assert nr.group_advantages(r, 4, nr.GroupNorm.MEAN_ONLY).tolist() == nr.group_advantages(r, 4, "mean").tolist()
+    a = nr.group_advantages(r, 4, nr.GroupNorm.std(1e-2, True))
+    assert a.tolist() == nr.group_advantages(r, 4, "std", 1e-2, True).tolist()
+    with pytest.raises(ValueError, match="at least 2"):
+        nr.group_advantages([1.0, 2.0], 1, nr.GroupNorm.std(1e-6, True))

@@ -285,3 +285,19 @@ def test_group_advantages_on_the_device():
             got = nr.group_advantages_tensor(t(rw, (G, n)), norm, eps, unb).to_numpy().ravel()
             want = O.group_advantages(rw.astype(np.float64).ravel(), n, norm, eps, unb).astype(np.float32)
             assert np.array_equal(got, want), (G, n, norm, int((got != want).sum()))
+
+
+def test_check_scored_finite_and_the_debug_refusal():
+    # tests/rl.rs:836-855: a -inf at a scored position is named; at a masked position it passes
+    lp = t([-1.0, -np.inf, -2.0], (1, 1, 3))
+    e = nr.check_scored_finite("test", lp, None)
+    assert e is not None and "position 1" in e and "not finite" in e
+    assert nr.check_scored_finite("test", lp, t([1.0, 0.0, 1.0], (1, 1, 3))) is None
+    assert nr.check_scored_finite("test", t([-1.0, -3.0, -2.0], (1, 1, 3)), None) is None
+    saved = nr.DEBUG_CHECKS
+    try:
+        nr.DEBUG_CHECKS = True
+        with pytest.raises(AssertionError, match="not finite"):
+            nr.policy_gradient_loss(t([-1.0, -np.inf], (1, 1, 2)), t([1.0], (1, 1)), None, nr.TokenReduction.SUM)
+    finally:
+        nr.DEBUG_CHECKS = saved
