@@ -174,3 +174,16 @@ def test_group_norm_forms_agree():
     assert a.tolist() == nr.group_advantages(r, 4, "std", 1e-2, True).tolist()
     with pytest.raises(ValueError, match="at least 2"):
         nr.group_advantages([1.0, 2.0], 1, nr.GroupNorm.std(1e-6, True))
+
+
+def test_bench_refuses_more_than_one_gpu_before_touching_a_device():
+    import json
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    p = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert p.returncode == 2
+    msg = json.loads(p.stdout.strip().splitlines()[-1])
+    assert "one GPU" in msg["error"]
