@@ -540,12 +540,18 @@ __global__ __launch_bounds__(1024) void k_sample(SampleP p) {
 // than two or three chunks ahead (17.40 against 17.57 and 18.27 us at c4, before the issue point
 // moved into the chunk).
 //
+// Wave w owns the K consecutive chunks [w K, w K + K) of the row, so the index order of the
+// row is the order of the waves, then of each wave's chunks.
 // Phase 1 (all waves): as each chunk lands, w = 2^(v c - s) with s the wave's exponent
 // reference (the maximum of its first chunk holding an allowed value; moved only when a chunk's
 // weights overflow), so no exponential waits on a reduction. The chunk's sum of weights is a
-// fixed-order DPP reduction written to LDS as four 16-lane partials.
-// Phase 2 (wave 0): f64 scan over the chunk sums in index order, the chunk that holds u*S.
-// Phase 3 (the owning wave): scan that chunk's registers.
+// fixed-order DPP reduction written to LDS as four 16-lane partials. Each wave then takes the
+// f64 prefix over its own chunks (kept in registers) and publishes its total.
+// Phase 2 (every wave, after the one barrier): f64 scan over the 16 wave totals in index order,
+// the wave whose chunks hold u*S. That wave alone goes on (no second barrier).
+// Phase 3 (that wave): the crossing chunk from its prefix, then a scan of that chunk's registers.
+// Measured at c4 against one 256-chunk scan by wave 0 and a second barrier: 20.2 against 20.6 us
+// HBM-cold, 17.0-17.2 against 17.2-17.4 us cache-warm.
 
 constexpr int kRRWaves = 16;
 constexpr int kRRThreads = kRRWaves * kWave;
@@ -591,51 +597,10 @@ __device__ __forceinline__ uint2 lds_read_b64_off(uint32_t addr) {
     asm volatile("ds_read_b64 %0, %1 offset:%2\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
     return r;
 }
-__device__ __forceinline__ uint32_t lds_read_b32(uint32_t addr) {
-    uint32_t r;
-    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(addr) : "memory");
-    return r;
-}
 __device__ __forceinline__ uint4 lds_read_b128(uint32_t addr) {
     uint4 r;
     asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(addr) : "memory");
     return r;
-}
-
-// The LDS inputs of the sampler's chunk scan for one lane, in one round trip: Q chunks' four
-// row partials (Q * 16 contiguous bytes at acs), their Q exponent references (Q * 4 bytes at
-// ark) and one wave maximum (at awm). Q is 1, 2 or 4.
-template <int Q>
-__device__ __forceinline__ void lds_read_scan_inputs(uint32_t acs, uint32_t ark, uint32_t awm, uint4 *cs, uint32_t *rk,
-                                                     uint32_t &wm) {
-    if constexpr (Q == 4) {
-        uint4 r4;
-        asm volatile(
-            "ds_read_b128 %0, %6\n\tds_read_b128 %1, %6 offset:16\n\tds_read_b128 %2, %6 offset:32\n\t"
-            "ds_read_b128 %3, %6 offset:48\n\tds_read_b128 %4, %7\n\tds_read_b32 %5, %8\n\ts_waitcnt lgkmcnt(0)"
-            : "=&v"(cs[0]), "=&v"(cs[1]), "=&v"(cs[2]), "=&v"(cs[3]), "=&v"(r4), "=&v"(wm)
-            : "v"(acs), "v"(ark), "v"(awm)
-            : "memory");
-        rk[0] = r4.x;
-        rk[1] = r4.y;
-        rk[2] = r4.z;
-        rk[3] = r4.w;
-    } else if constexpr (Q == 2) {
-        uint2 r2;
-        asm volatile(
-            "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:16\n\tds_read_b64 %2, %5\n\tds_read_b32 %3, %6\n\t"
-            "s_waitcnt lgkmcnt(0)"
-            : "=&v"(cs[0]), "=&v"(cs[1]), "=&v"(r2), "=&v"(wm)
-            : "v"(acs), "v"(ark), "v"(awm)
-            : "memory");
-        rk[0] = r2.x;
-        rk[1] = r2.y;
-    } else {
-        asm volatile("ds_read_b128 %0, %3\n\tds_read_b32 %1, %4\n\tds_read_b32 %2, %5\n\ts_waitcnt lgkmcnt(0)"
-                     : "=&v"(cs[0]), "=&v"(rk[0]), "=&v"(wm)
-                     : "v"(acs), "v"(ark), "v"(awm)
-                     : "memory");
-    }
 }
 
 // v_max3_f32 without the canonicalising moves the compiler puts in front of fmaxf: the inputs
@@ -667,11 +632,16 @@ __device__ __forceinline__ float readlane_f(float v, int l) {
 // Maximum over the 64 lanes: xor-1 and xor-2 quad permutes, the 8- and 16-lane mirrors, then
 // the four rows in a fixed order, each step a v_max3_f32 (no canonicalising moves; the inputs
 // are maxima of widened logits or -inf). The result is uniform and independent of timing.
-__device__ __forceinline__ float wave_max3_dpp(float v) {
+// Maximum inside each 16-lane row (the first four steps of wave_max3_dpp): every lane of a row
+// holds its row's maximum.
+__device__ __forceinline__ float row_max3_dpp(float v) {
     v = max3_hw(v, dpp_mov<0xB1>(v), dpp_mov<0xB1>(v));
     v = max3_hw(v, dpp_mov<0x4E>(v), dpp_mov<0x4E>(v));
     v = max3_hw(v, dpp_mov<0x141>(v), dpp_mov<0x141>(v));
-    v = max3_hw(v, dpp_mov<0x140>(v), dpp_mov<0x140>(v));
+    return max3_hw(v, dpp_mov<0x140>(v), dpp_mov<0x140>(v));
+}
+__device__ __forceinline__ float wave_max3_dpp(float v) {
+    v = row_max3_dpp(v);
     return max3_hw(max3_hw(readlane_f(v, 0), readlane_f(v, 16), readlane_f(v, 32)), readlane_f(v, 48),
                    readlane_f(v, 48));
 }
@@ -686,11 +656,16 @@ __device__ __forceinline__ double dpp_f64(double v) {
 }
 // Inclusive prefix sum over the 64 lanes in f64, in a fixed order: shifts by 1, 2, 4 and 8
 // inside each 16-lane row, then the row broadcasts of lanes 15 and 31 (the gfx9 DPP scan).
-__device__ __forceinline__ double wave_scan_dpp(double v) {
+// Inclusive prefix sum inside each 16-lane row in f64 (the first four steps of wave_scan_dpp).
+__device__ __forceinline__ double row_scan_dpp(double v) {
     v += dpp_f64<0x111, 0xf>(v);  // row_shr:1
     v += dpp_f64<0x112, 0xf>(v);  // row_shr:2
     v += dpp_f64<0x114, 0xf>(v);  // row_shr:4
     v += dpp_f64<0x118, 0xf>(v);  // row_shr:8
+    return v;
+}
+__device__ __forceinline__ double wave_scan_dpp(double v) {
+    v = row_scan_dpp(v);
     v += dpp_f64<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
     v += dpp_f64<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
     return v;
@@ -823,18 +798,12 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     constexpr int L = LX + LD;
     __shared__ __attribute__((aligned(16))) uint8_t mlds[MK == NT_MASK_NONE ? 16 : NCH * MB];
     __shared__ __attribute__((aligned(16))) float csum4[NCH * 4];  // per chunk and 16-lane row: sum of 2^(v c - wref)
-    __shared__ float cent4[ENT ? NCH * 4 : 1];  // per chunk and row: sum of w (v c - wref)
-    __shared__ __attribute__((aligned(16))) float wref[kRRWaves];  // per wave: its final exponent reference
-    __shared__ float wmax[kRRWaves];  // per wave: its maximum (greedy) or its reference's source
+    __shared__ __attribute__((aligned(16))) float cent4[ENT ? NCH * 4 : 4];  // per chunk and row: sum of w (v c - wref)
+    __shared__ float wref[kRRWaves];    // per wave: its final exponent reference
+    __shared__ float wmax[kRRWaves];    // per wave: its maximum (greedy) or its reference's source
+    __shared__ double wtot[kRRWaves];   // per wave: its sum of weights, relative to its reference
+    __shared__ double went[ENT ? kRRWaves : 1];  // per wave: its sum of w (v c - wref)
     __shared__ int wpick[kRRWaves];
-    struct Pick {
-        double t;   // the target inside chunk c, in the chunk's own scale
-        double S;   // sum of 2^(v c - A) over the row
-        double H;   // sum of w (v c - A) (entropy)
-        int c;      // the crossing chunk (-1: none)
-        float sr;   // chunk c's exponent reference
-    };
-    __shared__ __attribute__((aligned(16))) Pick pick;
 
     const int64_t row = blockIdx.x;
     const int tid = threadIdx.x;
@@ -865,7 +834,7 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
                                                  int(p.V * MaskWords<MK>::kBytes), kBufferWord3);
     auto issue = [&](auto kc) {
         constexpr int k = decltype(kc)::value;
-        const int ch = wave + kRRWaves * k;
+        const int ch = wave * K + k;
         const int xo = (ch * CH + lane * EPL) * Elem<DT>::kBytes;
 #pragma unroll
         for (int q = 0; q < LX; q++) {
@@ -901,26 +870,26 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     // already written are then rescaled. No maximum is taken per chunk otherwise.
     // Each chunk's row partial goes to csum4[4 ch + lane / 16]: a per-lane base, plus 256 bytes
     // per k (an immediate offset).
-    float *const cpart = csum4 + 4 * wave + lane / 16;
-    float *const epart = ENT ? cent4 + 4 * wave + lane / 16 : nullptr;
+    float *const cpart = csum4 + 4 * K * wave + lane / 16;
+    float *const epart = ENT ? cent4 + 4 * K * wave + lane / 16 : nullptr;
     const bool row_leader = (lane & 15) == 0;
     const int Vi = int(p.V);  // < 2^31 (at most 16 K chunks of CH)
-    // This lane's mask bytes of the wave's chunk k: mlw + k * 16 MB.
-    const uint32_t mlw = mbase + wave * MB + lane * EPL * MaskWords<MK>::kBytes;
+    // This lane's mask bytes of the wave's chunk k: mlw + k MB.
+    const uint32_t mlw = mbase + wave * K * MB + lane * EPL * MaskWords<MK>::kBytes;
     bool have_ref = false;     // sref set (uniform)
     float lmax = -INFINITY;    // the exact maximum, kept when greedy only
     float sref = -INFINITY;    // RN(sref_v c), uniform
     float sref_v = -INFINITY;  // the wave maximum the reference was taken from
     static_for<0, K>([&](auto kc) {
         constexpr int k = decltype(kc)::value;
-        const int ch = wave + kRRWaves * k;
+        const int ch = wave * K + k;
         if (ch < nc) {
             const int64_t e0 = int64_t(ch) * CH + lane * EPL;
             uint32_t mw[RRMask<MK, EPL>::kWords];
             if constexpr (MK != NT_MASK_NONE) {
                 // Chunks k+1 .. min(K, k+W)-1 may still be in flight.
                 wait_vmcnt<L * ((K < k + W ? K : k + W) - 1 - k)>();
-                constexpr int kOff = k * kRRWaves * MB;
+                constexpr int kOff = k * MB;
                 if constexpr (MK == NT_MASK_U8 && EPL == 8 && kOff < 65536) {
                     const uint2 m2 = lds_read_b64_off<kOff < 65536 ? kOff : 0>(mlw);
                     mw[0] = m2.x;
@@ -983,7 +952,7 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
                             // this wave's earlier partials, owned by lanes 0, 16, 32, 48
                             static_for<0, k>([&](auto jc) {
                                 constexpr int kk = decltype(jc)::value;
-                                const int idx = (wave + kRRWaves * kk) * 4 + lane / 16;
+                                const int idx = (wave * K + kk) * 4 + lane / 16;
                                 const float o = csum4[idx];
                                 csum4[idx] = f * o;
                                 if constexpr (ENT) cent4[idx] = f * (cent4[idx] + dk * o);
@@ -1000,18 +969,41 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
             float ce = 0.0f;
             if constexpr (ENT) ce = row_sum_dpp(gh);
             if (row_leader) {
-                cpart[64 * k] = cs;
-                if constexpr (ENT) epart[64 * k] = ce;
+                cpart[4 * k] = cs;
+                if constexpr (ENT) epart[4 * k] = ce;
             }
         }
         if constexpr (k + W < K) {
             if (!(ch < nc)) issue(std::integral_constant<int, k + W>{});  // (no chunk here to process)
         }
     });
+    // ---- end of phase 1 (each wave on its own, while the others still stream): lane k < K
+    // takes chunk k's sum (its four 16-lane partials, in a fixed order) in f64, in the wave's
+    // scale; the f64 prefix over the wave's chunks stays in registers and the wave's totals go
+    // to LDS.
+    double wcs = 0.0, wce = 0.0;
+    {
+        const int ch = wave * K + lane;
+        if (lane < K && ch < nc) {
+            const float4 q = *reinterpret_cast<const float4 *>(csum4 + 4 * ch);
+            wcs = double((q.x + q.y) + (q.z + q.w));
+            if constexpr (ENT) {
+                const float4 e = *reinterpret_cast<const float4 *>(cent4 + 4 * ch);
+                wce = double((e.x + e.y) + (e.z + e.w));
+            }
+        }
+    }
+    const double wincl = row_scan_dpp(wcs);  // lane k < 16: the wave's sum through its chunk k
     {
         // the wave's maximum when greedy; otherwise the value its reference came from (a lower
         // bound of its maximum: every sum is taken relative to RN(value c))
         const float wm = p.greedy ? wave_max3_dpp(lmax) : sref_v;
+        double wh = 0.0;
+        if constexpr (ENT) wh = row_scan_dpp(wce);
+        if (lane == kRRWaves - 1) {
+            wtot[wave] = wincl;
+            if constexpr (ENT) went[wave] = wh;
+        }
         if (lane == 0) {
             wmax[wave] = wm;
             wref[wave] = sref;
@@ -1019,37 +1011,16 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     }
     __syncthreads();
 
-    // ---- phase 2 (wave 0): the row's reference value M (the largest wave reference; the exact
-    // maximum when greedy), f64 scan of the chunk sums in index order.
-    // Every LDS read is issued up front and unconditionally (one round trip); cross-lane values
-    // move by DPP and v_readlane only; the walk is branch-free.
-    constexpr int Q = (NCH + kWave - 1) / kWave;  // chunks per lane of wave 0
-    static_assert(Q == 1 || Q == 2 || Q == 4, "chunks per lane");
-    uint4 cs4[Q];
-    uint32_t rkb[Q], wmb;
-    {
-        // lanes past the last chunk slot read the last one (unused); only wave 0 reads the
-        // chunk partials (the other waves need the maximum alone)
-        const int c0 = min(lane * Q, NCH - Q);
-        const uint32_t acs = uint32_t((uintptr_t)(lds_ptr_t)(csum4)) + uint32_t(c0) * 16u;
-        // chunk ch's reference is its wave's: wref[ch % 16], contiguous for the lane's Q chunks
-        const uint32_t ark = uint32_t((uintptr_t)(lds_ptr_t)(wref)) + uint32_t(c0 % kRRWaves) * 4u;
-        const uint32_t awm = uint32_t((uintptr_t)(lds_ptr_t)(wmax)) + uint32_t(lane & (kRRWaves - 1)) * 4u;
-        if (wave == 0) {
-            lds_read_scan_inputs<Q>(acs, ark, awm, cs4, rkb, wmb);
-        } else {
-            wmb = lds_read_b32(awm);
-#pragma unroll
-            for (int i = 0; i < Q; i++) {
-                cs4[i] = make_uint4(0, 0, 0, 0);
-                rkb[i] = 0;
-            }
-        }
-    }
-    float rk[Q];
-#pragma unroll
-    for (int i = 0; i < Q; i++) rk[i] = __uint_as_float(rkb[i]);
-    const float M = wave_max3_dpp(__uint_as_float(wmb));
+    // ---- phase 2 (every wave, to the same bits): lane w of each 16-lane row takes wave w's
+    // totals. The row's reference value M (the largest wave reference; the exact maximum when
+    // greedy), the row's sums relative to A = M c by an f64 scan over the waves in index order,
+    // and the wave whose chunks hold u S. No second barrier: that wave goes on alone.
+    const int lw = lane & (kRRWaves - 1);
+    const float rw = wref[lw];
+    const double tw = wtot[lw];
+    double hw = 0.0;
+    if constexpr (ENT) hw = went[lw];
+    const float M = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(row_max3_dpp(wmax[lw]))));
     auto refuse = [&](uint8_t st, bool leader) {
         if (leader) {
             p.ids[row] = -1;
@@ -1063,96 +1034,33 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
         return;
     }
     const float A = M * c;  // >= every wave reference (rounding is monotonic)
-    auto cent = [&](int ch) -> float {
-        return (cent4[ch * 4] + cent4[ch * 4 + 1]) + (cent4[ch * 4 + 2] + cent4[ch * 4 + 3]);
-    };
-    if (wave == 0) {
-        // Lane l takes chunks [Q l, Q l + Q): their weights f * sum in f64.
-        double wts[Q];
-        double ls = 0.0, lh = 0.0;
-#pragma unroll
-        for (int i = 0; i < Q; i++) {
-            const int ch = lane * Q + i;
-            const bool live = ch < nc && rk[i] != -INFINITY;
-            const float f = live ? exp2_hw(rk[i] - A) : 0.0f;
-            const float cs = (__uint_as_float(cs4[i].x) + __uint_as_float(cs4[i].y)) +
-                             (__uint_as_float(cs4[i].z) + __uint_as_float(cs4[i].w));
-            wts[i] = live ? double(f) * double(cs) : 0.0;
-            if constexpr (ENT) {
-                if (live && cs > 0.0f) lh += double(f) * (double(cent(ch)) + double(rk[i] - A) * double(cs));
-            }
-            ls += wts[i];
-        }
-        const double incl = wave_scan_dpp(ls);
-        const double S = readlane_d(incl, kWave - 1);
-        double H = 0.0;
-        if constexpr (ENT) H = readlane_d(wave_scan_dpp(lh), kWave - 1);
-        int cstar = -1;
-        double tloc = INFINITY;
-        if (S == S && !p.greedy) {
-            const double t = u_row * S;
-            const int l = first_lane(__ballot(incl > t && ls > 0.0));
-            // Every lane walks its own chunks from the prefix before them (incl - ls: the
-            // same f64 value the ballot compared against, up to one rounding); lane l's
-            // result is the one kept.
-            double C = incl - ls;
-            int mine = -1, last = -1;
-            double mt = INFINITY;
-#pragma unroll
-            for (int i = 0; i < Q; i++) {
-                const bool pos = wts[i] > 0.0;
-                const bool cross = pos && mine < 0 && C + wts[i] > t;
-                // the target in the chunk's own scale: divide by 2^(r - A)
-                const double tl = (t - C) * double(exp2_hw(A - rk[i]));
-                mine = cross ? lane * Q + i : mine;
-                mt = cross ? tl : mt;
-                last = pos ? lane * Q + i : last;
-                C += wts[i];
-            }
-            if (mine < 0) mine = last;  // rounding between the scan and this walk
-            if (l >= 0) {
-                cstar = __builtin_amdgcn_readlane(mine, l);
-                tloc = readlane_d(mt, l);
-            } else {
-                // u*S rounded up to S: the last chunk with weight.
-                const int ll = last_lane(__ballot(last >= 0));
-                cstar = ll >= 0 ? __builtin_amdgcn_readlane(last, ll) : -1;
-            }
-        }
-        if (lane == 0) {
-            pick.t = tloc;
-            pick.S = S;
-            pick.H = H;
-            pick.c = cstar;
-        }
-        if (cstar >= 0 && lane == cstar / Q) {
-            // the lane that read chunk cstar's reference publishes it
-            float r = rk[0];
-#pragma unroll
-            for (int i = 1; i < Q; i++)
-                if (cstar % Q == i) r = rk[i];
-            pick.sr = r;
-        }
-    }
-    // The maximum in z units, for the row's logp; the waiting waves compute it now.
-    float mz = 0.0f;
-    if (wave != 0) mz = (MK == NT_MASK_F32 || tau_one) ? M : M / p.tau;
-    __syncthreads();
-    const Pick pk = pick;
-    const double S = pk.S;
+    const bool wlive = rw != -INFINITY;
+    const float wf = wlive ? exp2_hw(rw - A) : 0.0f;
+    const double wt = wlive ? double(wf) * tw : 0.0;
+    const double incl = row_scan_dpp(wt);
+    const double S = readlane_d(incl, kRRWaves - 1);
     if (!(S == S)) {
         refuse(NT_ROW_NAN, tid == 0);
         return;
     }
+    // The entropy sum relative to A, taken only by the wave that writes the row (every wave
+    // works this phase on the same values, four to a SIMD, so it holds no more than it needs).
+    auto entropy_sum = [&]() -> double {
+        if constexpr (!ENT) return 0.0;
+        const double lh = (wlive && tw > 0.0) ? double(wf) * (hw + double(rw - A) * tw) : 0.0;
+        return readlane_d(row_scan_dpp(lh), kRRWaves - 1);
+    };
     // ln sum exp(z - m) and the entropy, from the sums relative to A = M c (computed by the
     // one lane that writes the row).
-    auto write_row = [&](int64_t id, float vz) {
+    auto write_row = [&](int64_t id, float vz, double H) {
         const double shiftA = double(A) - double(M) * double(c);
         const double lnS = ln_fast(S) + shiftA * kLn2;
-        const float zid = (MK == NT_MASK_F32 || tau_one) ? vz : vz / p.tau;
+        const bool zv = MK == NT_MASK_F32 || tau_one;
+        const float zid = zv ? vz : vz / p.tau;
+        const float mz = zv ? M : M / p.tau;  // the maximum in z units
         p.ids[row] = int32_t(id);
         if (p.logp) p.logp[row] = float((double(zid) - double(mz)) - lnS);
-        if (p.ent) p.ent[row] = float(lnS - kLn2 * (pk.H / S + shiftA));
+        if (p.ent) p.ent[row] = float(lnS - kLn2 * (H / S + shiftA));
         p.status[row] = NT_ROW_OK;
     };
     // Decode chunk k of this wave again (the mask from LDS; every DMA has completed).
@@ -1173,7 +1081,7 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
         int first = 0x7fffffff;
         static_for<0, K>([&](auto kc) {
             constexpr int k = decltype(kc)::value;
-            const int ch = wave + kRRWaves * k;
+            const int ch = wave * K + k;
             if (ch < nc) {
                 float v[EPL];
                 chunk_values(raw[k], ch, v);
@@ -1187,22 +1095,35 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
         __syncthreads();
         int best = 0x7fffffff;
         for (int i = 0; i < kRRWaves; i++) best = min(best, wpick[i]);
-        if (tid == 0) {
-            mz = (MK == NT_MASK_F32 || tau_one) ? M : M / p.tau;
-            write_row(best, M);
-        }
+        const double H = entropy_sum();
+        if (tid == 0) write_row(best, M, H);
         return;
     }
 
-    // ---- phase 3: the wave that owns chunk cstar scans it.
-    const int cstar = pk.c;
-    if (cstar < 0) {  // unreachable with S > 0; never leave stale outputs
+    // The wave whose chunks hold t = u S: the first with its inclusive sum past t.
+    const double t = u_row * S;
+    const bool wl = lane < kRRWaves;
+    int wsel = first_lane(__ballot(wl && incl > t && wt > 0.0));
+    if (wsel < 0) wsel = last_lane(__ballot(wl && wt > 0.0));  // u S rounded up to S
+    if (wsel < 0) {  // unreachable: M's wave has weight; never leave stale outputs
         refuse(NT_ROW_NAN, tid == 0);
         return;
     }
-    if (wave != cstar % kRRWaves) return;
-    if (wave == 0) mz = (MK == NT_MASK_F32 || tau_one) ? M : M / p.tau;
-    const int kstar = cstar / kRRWaves;
+    if (wave != wsel) return;
+    // ---- phase 3 (that wave alone): the target in its own scale (the part of t past the waves
+    // before it, divided by 2^(s - A)), the crossing chunk from the prefix held since phase 1,
+    // then that chunk's registers.
+    const double tl = readlane_d((t - (incl - wt)) * double(exp2_hw(A - rw)), wsel);
+    const bool lk = lane < K;
+    int kstar = first_lane(__ballot(lk && wincl > tl && wcs > 0.0));
+    if (kstar < 0) kstar = last_lane(__ballot(lk && wcs > 0.0));  // rounding between the two scans
+    if (kstar < 0) {  // unreachable: the wave has weight
+        refuse(NT_ROW_NAN, lane == 0);
+        return;
+    }
+    const double tloc = readlane_d(tl - (wincl - wcs), kstar);
+    const int cstar = wave * K + kstar;
+    const double H = entropy_sum();
     RRX<DT, EPL> r = raw[0];
     static_for<1, K>([&](auto kc) {
         constexpr int k = decltype(kc)::value;
@@ -1210,8 +1131,7 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     });
     float v[EPL];
     chunk_values(r, cstar, v);
-    const float sr = pk.sr;
-    const double tloc = pk.t;
+    const float sr = sref;
     float w[EPL];
     int jlast = -1;
 #pragma unroll
@@ -1220,8 +1140,8 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
         if (w[j] > 0.0f) jlast = j;
     }
     const double ls = double(tree_sum<EPL>(w));
-    const double incl = wave_scan_dpp(ls);
-    int lsel = first_lane(__ballot(incl > tloc && ls > 0.0));
+    const double cincl = wave_scan_dpp(ls);
+    int lsel = first_lane(__ballot(cincl > tloc && ls > 0.0));
     const bool none = lsel < 0;
     if (none) lsel = last_lane(__ballot(jlast >= 0));  // rounding: the last lane with weight
     if (lsel < 0) {  // unreachable: the chunk holds weight
@@ -1232,7 +1152,7 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     // inside the lane, compared against the f64 target).
     int jsel = -1;
     {
-        const double t0 = tloc - (incl - ls);
+        const double t0 = tloc - (cincl - ls);
         float C = 0.0f;
 #pragma unroll
         for (int j = 0; j < EPL; j++) {
@@ -1247,7 +1167,7 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
 #pragma unroll
         for (int j = 1; j < EPL; j++)
             if (j == jsel) vz = v[j];
-        write_row(int64_t(cstar) * CH + lane * EPL + jsel, vz);
+        write_row(int64_t(cstar) * CH + lane * EPL + jsel, vz, H);
     }
 }
 
