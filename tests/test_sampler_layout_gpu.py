@@ -1,0 +1,126 @@
+"""The register-resident sampler at every chunks-per-wave K it is built for, against the oracle.
+
+The kernel cuts a row into 512-element chunks and gives wave w (of 16) the K consecutive chunks
+[w K, w K + K), K the smallest power of two with 16 K chunks covering the row (bf16 up to 16,
+f32 up to 8, f32 additive mask up to 4). The crossing of u S is found in three levels: the wave
+(an f64 scan over the 16 wave totals), the chunk (the wave's own prefix), the lane and element.
+These cases put the crossing and the row's weight where those levels meet:
+- V just past a K boundary (waves 9..15 hold no chunk at all, wave 8 one partial chunk) and V
+  just below the next one (every wave full, the last chunk ragged);
+- rows whose allowed tokens all lie in one wave's range, or in the row's last element only, or
+  in its first element only (every other wave has no weight, so its reference is -inf);
+- a row whose maximum sits in the last wave with every other wave far below it (their weights
+  relative to the row's maximum underflow);
+- temperature 1, 0.7 and 0 (greedy, the first maximum in index order).
+ids must equal the oracle's except for draws within 1e-6 of a CDF edge; logp and entropy hold
+the dtype's tolerance (1e-5 relative / 1e-6 absolute for f32, 2e-3 relative for bf16).
+"""
+import numpy as np
+import pytest
+
+import noetic_rl as nr
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+EDGE = 1e-6
+CHUNK = 512
+WAVES = 16
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    nr.claim(0)
+    yield
+
+
+def close(ours, want, bf16):
+    ours, want = np.asarray(ours, np.float64), np.asarray(want, np.float64)
+    tol = (1e-6 + 2e-3 * np.abs(want)) if bf16 else (1e-6 + 1e-5 * np.abs(want))
+    return np.abs(ours - want) <= tol
+
+
+def rows_for(V, rng, K):
+    """16 rows of V logits in [-6, 6] (N(0, 2)) and their u8 keep-masks, with the special rows."""
+    rows = 16
+    x = rng.normal(0, 2, (rows, V)).astype(np.float32)
+    keep = (rng.random((rows, V)) < 0.7).astype(np.uint8)
+    keep[:, 0] = 1
+    span = K * CHUNK  # elements per wave
+    # row 1: only wave 3's range allowed (or the last wave holding elements)
+    w = min(3, (V - 1) // span)
+    keep[1] = 0
+    keep[1, w * span:min(V, (w + 1) * span)] = 1
+    # row 2: only the last element; row 3: only the first
+    keep[2] = 0
+    keep[2, V - 1] = 1
+    keep[3] = 0
+    keep[3, 0] = 1
+    # row 4: the maximum in the row's last element, every other logit 200 below it
+    x[4] -= 200.0
+    x[4, V - 1] = 5.0
+    keep[4, V - 1] = 1
+    # row 5: a peaked row, the mass in one element of the middle wave's range
+    mid = min(V - 1, (V // span // 2) * span + 7)
+    x[5, mid] = 40.0
+    keep[5, mid] = 1
+    return x, keep
+
+
+def cases():
+    out = []
+    for dtype, kmax in (("bf16", 16), ("f32", 8)):
+        K = 1
+        while K <= kmax:
+            # (V a multiple of 8: rows the register-resident kernel takes)
+            lo = WAVES * (K // 2) * CHUNK + 8 if K > 1 else 2 * CHUNK + 8
+            hi = WAVES * K * CHUNK - 40
+            out += [(dtype, "u8", K, lo), (dtype, "u8", K, hi)]
+            K *= 2
+    # the f32 additive mask (K at most 4 there) and no mask
+    out += [("f32", "f32add", 4, WAVES * 4 * CHUNK - 8), ("bf16", "f32add", 2, WAVES * 2 * CHUNK),
+            ("bf16", "none", 16, WAVES * 16 * CHUNK - 8), ("f32", "none", 1, 704)]
+    return out
+
+
+@pytest.mark.parametrize("dtype,mask,K,V", cases())
+def test_register_resident_sampler_levels(dtype, mask, K, V):
+    rng = np.random.default_rng(V * 7 + K)
+    x, keep = rows_for(V, rng, K)
+    rows = x.shape[0]
+    bf16 = dtype == "bf16"
+    if bf16:
+        xb = O.bf16_from_f32(x)
+        x = O.bf16_to_f32(xb)
+        xt = nr.Tensor.from_numpy(xb, "bf16")
+    else:
+        xt = nr.Tensor.from_numpy(x)
+    if mask == "u8":
+        mt, kw = nr.Tensor.from_numpy(keep), dict(keep=keep)
+    elif mask == "f32add":
+        add = np.where(keep == 1, 0.0, -np.inf).astype(np.float32)
+        add[:, 1::3] = np.where(keep[:, 1::3] == 1, -1.5, -np.inf)  # finite offsets too
+        mt, kw = nr.Tensor.from_numpy(add), dict(addmask=add)
+    else:
+        mt, kw = None, {}
+    u = np.random.default_rng(V + K).random(rows)
+    u[0], u[6] = 0.0, np.nextafter(1.0, 0.0)  # the first and the last weight
+    ut = nr.Tensor.from_numpy(u, "f64")
+    for tau in (1.0, 0.7, 0.0):
+        ids, lp, ent = nr.sample_logp(xt, tau, mt, None, entropy=True, uniforms=None if tau == 0.0 else ut)
+        ids, lp, ent = ids.to_numpy(), lp.to_numpy(), ent.to_numpy()
+        z = O.tempered(x, 1.0 if tau == 0.0 else tau, **kw)
+        if tau == 0.0:
+            zz = np.where(np.isfinite(z), z, -np.inf)
+            assert np.array_equal(ids, np.argmax(zz, axis=1)), f"{dtype} {mask} K={K} V={V}: greedy ids"
+        else:
+            want, edges = O.sample_invcdf(z, u)
+            differ = np.nonzero(ids != want)[0]
+            assert np.all(edges[differ] < EDGE), f"{dtype} {mask} K={K} V={V} tau={tau}: rows {differ} differ"
+        allowed = np.isfinite(z[np.arange(rows), ids])
+        assert allowed.all(), f"{dtype} {mask} K={K} V={V} tau={tau}: an excluded token was drawn"
+        assert np.all(close(lp, O.token_logp(z, ids), bf16)), f"{dtype} {mask} K={K} V={V} tau={tau}: logp"
+        assert np.all(close(ent, O.entropy(z), bf16)), f"{dtype} {mask} K={K} V={V} tau={tau}: entropy"
+        assert ids[4] == V - 1
+        if mask != "none":
+            assert ids[2] == V - 1 and ids[3] == 0
