@@ -40,7 +40,11 @@ extern "C" {
 #define NT_BF16 1 /* bf16 logits, stored as their bit patterns (src/tensor/half.rs:10-12) */
 
 #define NT_MASK_NONE 0 /* no vocabulary mask */
-#define NT_MASK_U8 1   /* u8 keep-mask: 0 excludes the token (adds -inf), any other value keeps it */
+#define NT_MASK_U8 1   /* u8 keep-mask: 0 excludes the token, any other value keeps it. An excluded
+                          token's logit is replaced by -inf, whatever it holds, so a NaN or +inf
+                          there does not reach the row (a -inf entry of an f32 mask is added
+                          instead, and NaN + -inf or inf + -inf refuses the row, as the
+                          reference's additive masks do) */
 #define NT_MASK_F32 2  /* additive f32 mask (0, -inf, -1e9, any value), added after the divide
                           by the temperature: rl.rs:475-486 `logits / temperature + mask` */
 

@@ -124,3 +124,69 @@ def test_register_resident_sampler_levels(dtype, mask, K, V):
         assert ids[4] == V - 1
         if mask != "none":
             assert ids[2] == V - 1 and ids[3] == 0
+
+
+@pytest.mark.parametrize("dtype,mask,V", [("bf16", "u8", WAVES * 16 * CHUNK - 8), ("f32", "u8", WAVES * 4 * CHUNK - 8),
+                                          ("f32", "f32add", WAVES * 2 * CHUNK), ("bf16", "none", 4096)])
+def test_register_resident_sampler_refusals(dtype, mask, V):
+    """Each row is refused on its own: a NaN in the first wave's range, in a middle wave's, in the
+    row's last element, or a +inf logit (its weight is inf - inf) gives NT_ROW_NAN; a row with
+    every token excluded gives NT_ROW_NO_TOKEN; the rows between them sample as the oracle does.
+    A NaN at a token the u8 mask excludes does not reach the row; under an f32 mask's -inf it
+    does (NaN + -inf), as in the reference's tempered_logits."""
+    import ctypes as C
+    rows = 10
+    rng = np.random.default_rng(V)
+    x = rng.normal(0, 2, (rows, V)).astype(np.float32)
+    keep = (rng.random((rows, V)) < 0.6).astype(np.uint8)
+    keep[:, 0] = 1
+    span = V // WAVES
+    for r, pos in ((0, 5), (1, 9 * span + 3), (2, V - 1)):
+        x[r, pos] = np.nan
+        keep[r, pos] = 1
+    x[4, 7] = np.inf
+    keep[4, 7] = 1
+    keep[5] = 0
+    x[6, 11] = np.nan  # excluded below
+    keep[6, 11] = 0
+    if mask == "none":
+        keep[:] = 1
+        keep[6, 11] = 1  # no mask: the NaN stays in the row
+        keep[5] = 1
+    nan_rows = {0, 1, 2, 4} | ({6} if mask != "u8" else set())
+    none_rows = {5} if mask != "none" else set()
+    bf16 = dtype == "bf16"
+    if bf16:
+        xs = O.bf16_from_f32(x)
+        x = O.bf16_to_f32(xs)
+        xt = nr.Tensor.from_numpy(xs, "bf16")
+    else:
+        xt = nr.Tensor.from_numpy(x)
+    if mask == "u8":
+        mt, kind, kw = nr.Tensor.from_numpy(keep), nr.NT_MASK_U8, dict(keep=keep)
+    elif mask == "f32add":
+        add = np.where(keep == 1, 0.0, -np.inf).astype(np.float32)
+        mt, kind, kw = nr.Tensor.from_numpy(add), nr.NT_MASK_F32, dict(addmask=add)
+    else:
+        mt, kind, kw = None, nr.NT_MASK_NONE, {}
+    u = np.random.default_rng(1).random(rows)
+    ut = nr.Tensor.from_numpy(u, "f64")
+    ids, lp, ent, st = nr.IntTensor((rows,)), nr.Tensor((rows,), "f32"), nr.Tensor((rows,), "f32"), nr.Tensor((rows,), "u8")
+    a = nr.NtRlSampleArgs(xt.ptr, nr.NT_BF16 if bf16 else nr.NT_F32, kind, rows, V, V, None if mt is None else mt.ptr,
+                          0 if mt is None else V, 0.9, ut.ptr, ids.ptr, lp.ptr, ent.ptr, st.ptr)
+    nr._check(nr.lib().nt_hip_rl_sample(C.byref(a)), "sample")
+    ids, lp, ent, st = ids.to_numpy(), lp.to_numpy(), ent.to_numpy(), st.to_numpy()
+    for r in range(rows):
+        if r in nan_rows:
+            assert st[r] == nr.NT_ROW_NAN and ids[r] == -1 and np.isnan(lp[r]), f"row {r}: {st[r]} {ids[r]}"
+        elif r in none_rows:
+            assert st[r] == nr.NT_ROW_NO_TOKEN and ids[r] == -1, f"row {r}: {st[r]}"
+        else:
+            assert st[r] == nr.NT_ROW_OK, f"row {r}: status {st[r]}"
+    ok = np.array([r for r in range(rows) if r not in nan_rows | none_rows])
+    z = O.tempered(x[ok], 0.9, **({k: v[ok] for k, v in kw.items()}))
+    want, edges = O.sample_invcdf(z, u[ok])
+    differ = np.nonzero(ids[ok] != want)[0]
+    assert np.all(edges[differ] < EDGE), f"rows {ok[differ]} differ"
+    assert np.all(close(lp[ok], O.token_logp(z, ids[ok]), bf16))
+    assert np.all(close(ent[ok], O.entropy(z), bf16))
