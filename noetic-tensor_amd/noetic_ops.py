@@ -1,0 +1,360 @@
+"""Host mirror of the reference's general GPU ops (the `GpuBackend` trait, src/tensor/gpu/mod.rs:137-207)
+for a `Device::Hip(0)` tensor, over libnoetic_hip.so's include/noetic_ops.h entry points.
+
+These are the ops the nn::rl chain runs around the fused entry points: `tempered_logits`' divide
+and mask add, casts of bf16 logits, comparisons and `mask_fill` for clamps and masks, lane
+reductions, `gather` and its scatter. Each function keeps the trait method's name and argument
+meaning (a `Layout` is a view read in place; outputs are fresh, contiguous and row-major), and
+`Layout` keeps src/tensor/layout.rs's view operations. There is no CPU fallback: without the built
+library every call raises `HipUnavailable`, as in `noetic_rl`.
+
+`matmul` (and `matmul_half`, `sort_desc`) are off this path and raise `Unsupported`, as the
+reference's trait lets a first slice do.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import enum
+from typing import List, Optional, Sequence
+
+import numpy as np
+
+import noetic_rl as nr
+from noetic_rl import NtLayout, Tensor, _check, _dev
+
+MAX_RANK = 8
+_DT = {"f32": 0, "bf16": 1, "f16": 2, "bool": 3, "u8": 4, "i32": 5, "i64": 6}
+
+
+class Unsupported(NotImplementedError):
+    """TensorError::Unsupported: a valid request this backend does not implement."""
+
+
+class UnaryOp(enum.IntEnum):
+    """gpu/mod.rs:68-103 (`UnaryOp::code`)."""
+    NEG = 0
+    EXP = 1
+    LOG = 2
+    SQRT = 3
+    RECIP = 4
+    ABS = 5
+    SIGN = 6
+    SIGMOID = 7
+    ADD_SCALAR = 8
+    SUB_SCALAR = 9
+    MUL_SCALAR = 10
+    DIV_SCALAR = 11
+    POW_SCALAR = 12
+
+
+class CmpOp(enum.IntEnum):
+    """gpu/mod.rs:107-114."""
+    GT = 0
+    GE = 1
+    LT = 2
+    LE = 3
+    EQ = 4
+
+
+class BinaryOp(enum.IntEnum):
+    """gpu/mod.rs:116-122."""
+    ADD = 0
+    SUB = 1
+    MUL = 2
+    DIV = 3
+
+
+class ReduceOp(enum.IntEnum):
+    """gpu/mod.rs:124-133."""
+    SUM = 0
+    MAX = 1
+    ARGMAX = 2
+
+
+def _row_major(shape: Sequence[int]) -> List[int]:
+    st, s = [0] * len(shape), 1
+    for d in range(len(shape) - 1, -1, -1):
+        st[d] = s
+        s *= shape[d]
+    return st
+
+
+class Layout:
+    """src/tensor/layout.rs:8-81: shape, element strides and element offset of a view."""
+
+    def __init__(self, shape: Sequence[int], strides: Optional[Sequence[int]] = None, offset: int = 0):
+        self.shape = [int(d) for d in shape]
+        self.strides = [int(s) for s in (strides if strides is not None else _row_major(self.shape))]
+        self.offset = int(offset)
+        if len(self.shape) > MAX_RANK:
+            raise ValueError(f"rank {len(self.shape)} (at most {MAX_RANK} on the device)")
+
+    @staticmethod
+    def contiguous(shape: Sequence[int]) -> "Layout":
+        return Layout(shape)
+
+    def numel(self) -> int:
+        return int(np.prod(self.shape)) if self.shape else 1
+
+    def is_contiguous(self) -> bool:
+        return self.strides == _row_major(self.shape)
+
+    def reshaped(self, shape: Sequence[int]) -> Optional["Layout"]:
+        return Layout(shape, None, self.offset) if self.is_contiguous() else None
+
+    def swapped(self, a: int, b: int) -> "Layout":
+        sh, st = list(self.shape), list(self.strides)
+        sh[a], sh[b] = sh[b], sh[a]
+        st[a], st[b] = st[b], st[a]
+        return Layout(sh, st, self.offset)
+
+    def narrowed(self, ranges: Sequence[range]) -> "Layout":
+        off = self.offset + sum(r.start * s for r, s in zip(ranges, self.strides))
+        return Layout([r.stop - r.start for r in ranges], self.strides, off)
+
+    def broadcast(self, out: Sequence[int]) -> "Layout":
+        """Right-aligned, stride 0 on every expanded dimension (layout.rs:71-80)."""
+        ni, no = len(self.shape), len(out)
+        st = [0] * no
+        for i in range(ni):
+            o = no - ni + i
+            st[o] = self.strides[i] if self.shape[i] == out[o] else 0
+        return Layout(out, st, self.offset)
+
+    def c(self) -> NtLayout:
+        lay = NtLayout()
+        lay.rank = len(self.shape)
+        lay.offset = self.offset
+        for d, (n, s) in enumerate(zip(self.shape, self.strides)):
+            lay.shape[d] = n
+            lay.strides[d] = s
+        return lay
+
+
+def broadcast_shape(a: Sequence[int], b: Sequence[int]) -> List[int]:
+    """shape::broadcast: right-aligned, each pair equal or one of them 1."""
+    n = max(len(a), len(b))
+    a, b = [1] * (n - len(a)) + list(a), [1] * (n - len(b)) + list(b)
+    out = []
+    for x, y in zip(a, b):
+        if x != y and 1 not in (x, y):
+            raise ValueError(f"shapes {a} and {b} do not broadcast")
+        out.append(max(x, y))
+    return out
+
+
+def _esize(dtype: str) -> int:
+    return np.dtype(nr._NP[dtype]).itemsize
+
+
+def _f32(x: Tensor, what: str):
+    if x.dtype != "f32":
+        raise TypeError(f"{what}: {x.dtype} storage in a float kernel (cast to f32 first)")
+
+
+def _inside(t: Tensor, l: Layout, what: str):
+    """The device reads a view in place with no bounds of its own: every element the view selects
+    must lie in the tensor's buffer (the reference's Layout guarantees this by construction)."""
+    if l.numel() == 0:
+        return
+    last = l.offset + sum((n - 1) * s for n, s in zip(l.shape, l.strides))
+    if l.offset < 0 or min(l.strides, default=0) < 0 or last >= t.numel:
+        raise IndexError(f"{what}: the view {l.shape} strides {l.strides} offset {l.offset} leaves the buffer "
+                         f"of {t.numel} elements")
+
+
+# ----------------------------------------------------------------------------------- trait methods
+
+def alloc(dtype: str, shape: Sequence[int]) -> Tensor:
+    """GpuBackend::alloc: uninitialised storage."""
+    return Tensor(shape, dtype)
+
+
+def copy(x: Tensor, xl: Layout) -> Tensor:
+    """GpuBackend::copy: the elements the view selects, contiguous (any dtype)."""
+    _inside(x, xl, "copy")
+    y = Tensor(xl.shape, x.dtype)
+    _check(_dev().nt_hip_copy(C.c_void_p(x.ptr), C.byref(xl.c()), _esize(x.dtype), C.c_void_p(y.ptr)), "copy")
+    return y
+
+
+def write(dst: Tensor, dl: Layout, src: Tensor, sl: Layout) -> None:
+    """GpuBackend::write: the view sl of src into the view dl of dst (slice_assign, cat)."""
+    if dst.dtype != src.dtype or dl.shape != sl.shape:
+        raise ValueError(f"write of {src.dtype} {sl.shape} into {dst.dtype} {dl.shape}")
+    _inside(dst, dl, "write")
+    _inside(src, sl, "write")
+    _check(_dev().nt_hip_write(C.c_void_p(dst.ptr), C.byref(dl.c()), C.c_void_p(src.ptr), C.byref(sl.c()),
+                               _esize(src.dtype)), "write")
+
+
+def cast(x: Tensor, xl: Layout, to: str) -> Tensor:
+    """GpuBackend::cast: f16/bf16/bool -> f32, f32 -> f16/bf16 (RNE), f16 <-> bf16, same = copy."""
+    if to not in ("f32", "f16", "bf16") and to != x.dtype:
+        raise Unsupported(f"cast {x.dtype} → {to}")
+    _inside(x, xl, "cast")
+    y = Tensor(xl.shape, to)
+    _check(_dev().nt_hip_cast(C.c_void_p(x.ptr), C.byref(xl.c()), _DT[x.dtype], _DT[to], C.c_void_p(y.ptr)), "cast")
+    return y
+
+
+def unary(op: UnaryOp, x: Tensor, xl: Layout, s: float = 0.0) -> Tensor:
+    """GpuBackend::unary (f32): the op with its scalar (AddScalar .. PowScalar)."""
+    _f32(x, "unary")
+    _inside(x, xl, "unary")
+    y = Tensor(xl.shape, "f32")
+    _check(_dev().nt_hip_unary(int(op), s, C.c_void_p(x.ptr), C.byref(xl.c()), C.c_void_p(y.ptr)), "unary")
+    return y
+
+
+def compare(op: CmpOp, x: Tensor, xl: Layout, s: float) -> Tensor:
+    """GpuBackend::compare: bool storage of x op s."""
+    _f32(x, "compare")
+    _inside(x, xl, "compare")
+    y = Tensor(xl.shape, "bool")
+    _check(_dev().nt_hip_compare(int(op), s, C.c_void_p(x.ptr), C.byref(xl.c()), C.c_void_p(y.ptr)), "compare")
+    return y
+
+
+def binary(op: BinaryOp, a: Tensor, al: Layout, b: Tensor, bl: Layout) -> Tensor:
+    """GpuBackend::binary over the broadcast shape (al and bl already broadcast to it)."""
+    _f32(a, "binary")
+    _f32(b, "binary")
+    _inside(a, al, "binary")
+    _inside(b, bl, "binary")
+    y = Tensor(al.shape, "f32")
+    _check(_dev().nt_hip_binary(int(op), C.c_void_p(a.ptr), C.byref(al.c()), C.c_void_p(b.ptr), C.byref(bl.c()),
+                                C.c_void_p(y.ptr)), "binary")
+    return y
+
+
+def mask_fill(x: Tensor, xl: Layout, mask: Tensor, ml: Layout, value: float) -> Tensor:
+    """GpuBackend::mask_fill: value where the (bool) mask, broadcast by its layout, is true."""
+    _f32(x, "mask_fill")
+    if mask.dtype != "bool":
+        raise TypeError(f"a mask of {mask.dtype} storage")
+    _inside(x, xl, "mask_fill")
+    _inside(mask, ml, "mask_fill")
+    y = Tensor(xl.shape, "f32")
+    _check(_dev().nt_hip_mask_fill(C.c_void_p(x.ptr), C.byref(xl.c()), C.c_void_p(mask.ptr), C.byref(ml.c()), value,
+                                   C.c_void_p(y.ptr)), "mask_fill")
+    return y
+
+
+def reduce_dim(op: ReduceOp, x: Tensor, shape: Sequence[int], dim: int) -> Tensor:
+    """GpuBackend::reduce_dim along `dim` of contiguous f32 x (the dimension kept, size 1): f32 values
+    for Sum and Max, I32 indices for ArgMax."""
+    _f32(x, "reduce_dim")
+    shape = list(shape)
+    outer, n, inner = int(np.prod(shape[:dim])), shape[dim], int(np.prod(shape[dim + 1:]))
+    out_shape = shape[:dim] + [1] + shape[dim + 1:]
+    if outer * n * inner != x.numel:
+        raise ValueError(f"reduce_dim: shape {shape} against {x.numel} elements")
+    y = Tensor(out_shape, "i32" if op == ReduceOp.ARGMAX else "f32")
+    _check(_dev().nt_hip_reduce_dim(int(op), C.c_void_p(x.ptr), outer, n, inner, int(dim + 1 == len(shape)),
+                                    C.c_void_p(y.ptr)), "reduce_dim")
+    return y
+
+
+def reduce_all(op: ReduceOp, x: Tensor, n: int) -> Tensor:
+    """GpuBackend::reduce_all: Sum or Max of every element, one f32."""
+    _f32(x, "reduce_all")
+    if n > x.numel:
+        raise ValueError(f"reduce_all: {n} elements of {x.numel}")
+    y = Tensor((1,), "f32")
+    _check(_dev().nt_hip_reduce_all(int(op), C.c_void_p(x.ptr), n, C.c_void_p(y.ptr)), "reduce_all")
+    return y
+
+
+def _lanes_fit(x: Optional[Tensor], nx: int, idx: Tensor, ni: int, what: str):
+    if x is not None and (x.dtype != "f32" or x.numel < nx):
+        raise ValueError(f"{what}: f32 storage of at least {nx} elements")
+    if idx.dtype != "i32" or idx.numel < ni:
+        raise ValueError(f"{what}: I32 indices of at least {ni} elements")
+
+
+def gather(x: Tensor, lanes: Sequence[int], idx: Tensor) -> Tensor:
+    """GpuBackend::gather of contiguous x [outer, n, inner] at I32 indices [outer, m, inner]."""
+    outer, n, inner, m = (int(v) for v in lanes)
+    _lanes_fit(x, outer * n * inner, idx, outer * m * inner, "gather")
+    y = Tensor((outer, m, inner), "f32")
+    _check(_dev().nt_hip_gather(C.c_void_p(x.ptr), outer, n, inner, C.c_void_p(idx.ptr), m, C.c_void_p(y.ptr)),
+           "gather")
+    return y
+
+
+def index_select(x: Tensor, lanes: Sequence[int], idx: Tensor) -> Tensor:
+    """GpuBackend::index_select of contiguous x [outer, n, inner] at m I32 indices."""
+    outer, n, inner, m = (int(v) for v in lanes)
+    _lanes_fit(x, outer * n * inner, idx, m, "index_select")
+    y = Tensor((outer, m, inner), "f32")
+    _check(_dev().nt_hip_index_select(C.c_void_p(x.ptr), outer, n, inner, C.c_void_p(idx.ptr), m,
+                                      C.c_void_p(y.ptr)), "index_select")
+    return y
+
+
+def one_hot(idx: Tensor, count: int, n: int) -> Tensor:
+    """GpuBackend::one_hot: f32 rows of width n for count I32 indices."""
+    _lanes_fit(None, 0, idx, count, "one_hot")
+    y = Tensor((count, n), "f32")
+    _check(_dev().nt_hip_one_hot(C.c_void_p(idx.ptr), count, n, C.c_void_p(y.ptr)), "one_hot")
+    return y
+
+
+def scatter_add(idx: Tensor, vals: Tensor, lanes: Sequence[int]) -> Tensor:
+    """GpuBackend::scatter_add of values [outer, m, inner] into zeros [outer, n, inner]."""
+    outer, n, inner, m = (int(v) for v in lanes)
+    _lanes_fit(vals, outer * m * inner, idx, outer * m * inner, "scatter_add")
+    y = Tensor((outer, n, inner), "f32")
+    _check(_dev().nt_hip_scatter_add(C.c_void_p(idx.ptr), C.c_void_p(vals.ptr), outer, n, inner, m,
+                                     C.c_void_p(y.ptr)), "scatter_add")
+    return y
+
+
+def index_add(idx: Tensor, vals: Tensor, lanes: Sequence[int]) -> Tensor:
+    """GpuBackend::index_add of value slices [outer, m, inner] into zeros [outer, n, inner]."""
+    outer, n, inner, m = (int(v) for v in lanes)
+    _lanes_fit(vals, outer * m * inner, idx, m, "index_add")
+    y = Tensor((outer, n, inner), "f32")
+    _check(_dev().nt_hip_index_add(C.c_void_p(idx.ptr), C.c_void_p(vals.ptr), outer, n, inner, m,
+                                   C.c_void_p(y.ptr)), "index_add")
+    return y
+
+
+def fill(shape: Sequence[int], value: float) -> Tensor:
+    """GpuBackend::fill: f32 elements equal to value, written on the device."""
+    y = Tensor(shape, "f32")
+    _check(_dev().nt_hip_fill(C.c_void_p(y.ptr), y.numel, value), "fill")
+    return y
+
+
+def matmul(*_args):
+    raise Unsupported("matmul is off the rl path on this backend")
+
+
+# ----------------------------------------------------------------------------------- tensor level
+
+def tempered_logits(logits: Tensor, temperature: float, mask: Optional[Tensor] = None) -> Tensor:
+    """`tempered_logits` (rl.rs:475-486) materialised on the device with the general ops: bf16 is
+    cast to f32, `div_scalar(τ)` unless τ == 1, then `add(mask)` broadcast at rank (an f32
+    additive mask). The fused entry points take the tempered logits without materialising them;
+    this is the op sequence a caller gets when it asks for the tensor itself."""
+    if not (temperature > 0.0 and np.isfinite(temperature)):
+        raise ValueError(f"tempered_logits: temperature {temperature} (must be positive)")
+    if temperature == 1.0 and mask is None:
+        return logits  # rl.rs:476: no divide, no add
+    lay = Layout.contiguous(logits.shape)
+    z = cast(logits, lay, "f32") if logits.dtype != "f32" else logits
+    if temperature != 1.0:
+        z = unary(UnaryOp.DIV_SCALAR, z, lay, float(np.float32(temperature)))
+    if mask is not None:
+        if mask.dtype != "f32":
+            raise TypeError("tempered_logits: an additive f32 mask")
+        if len(mask.shape) != len(logits.shape):
+            raise ValueError("tempered_logits: mask rank")
+        if not all(a == b or a == 1 for a, b in zip(mask.shape, logits.shape)):
+            raise ValueError(f"tempered_logits: mask {list(mask.shape)} does not broadcast to the logits "
+                             f"{list(logits.shape)}")
+        out = broadcast_shape(logits.shape, mask.shape)
+        z = binary(BinaryOp.ADD, z, lay.broadcast(out), mask, Layout.contiguous(mask.shape).broadcast(out))
+    return z

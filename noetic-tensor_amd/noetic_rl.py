@@ -75,6 +75,12 @@ class NtRlPolicyLossArgs(C.Structure):
 NT_LOSS_PG, NT_LOSS_PPO = 0, 1
 
 
+class NtLayout(C.Structure):
+    """include/noetic_ops.h NtLayout: a view (element offset, shape, element strides)."""
+    _fields_ = [("rank", C.c_int32), ("pad_", C.c_int32), ("offset", C.c_int64), ("shape", C.c_int64 * 8),
+                ("strides", C.c_int64 * 8)]
+
+
 class NtRng(C.Structure):
     _fields_ = [("key", C.c_uint32 * 8), ("counter", C.c_uint64), ("buf", C.c_uint32 * 16), ("idx", C.c_int32)]
 
@@ -115,6 +121,26 @@ _SIGS = {
     "nt_hip_rl_policy_loss": (C.c_int, [C.POINTER(NtRlPolicyLossArgs)]),
     "nt_hip_rl_group_advantages": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_int32, C.c_double, C.c_int32,
                                              C.c_void_p]),
+    # noetic_ops.h
+    "nt_hip_copy": (C.c_int, [C.c_void_p, C.POINTER(NtLayout), C.c_int32, C.c_void_p]),
+    "nt_hip_write": (C.c_int, [C.c_void_p, C.POINTER(NtLayout), C.c_void_p, C.POINTER(NtLayout), C.c_int32]),
+    "nt_hip_cast": (C.c_int, [C.c_void_p, C.POINTER(NtLayout), C.c_int32, C.c_int32, C.c_void_p]),
+    "nt_hip_unary": (C.c_int, [C.c_int32, C.c_float, C.c_void_p, C.POINTER(NtLayout), C.c_void_p]),
+    "nt_hip_compare": (C.c_int, [C.c_int32, C.c_float, C.c_void_p, C.POINTER(NtLayout), C.c_void_p]),
+    "nt_hip_binary": (C.c_int, [C.c_int32, C.c_void_p, C.POINTER(NtLayout), C.c_void_p, C.POINTER(NtLayout),
+                                C.c_void_p]),
+    "nt_hip_mask_fill": (C.c_int, [C.c_void_p, C.POINTER(NtLayout), C.c_void_p, C.POINTER(NtLayout), C.c_float,
+                                   C.c_void_p]),
+    "nt_hip_reduce_dim": (C.c_int, [C.c_int32, C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_int32, C.c_void_p]),
+    "nt_hip_reduce_all": (C.c_int, [C.c_int32, C.c_void_p, C.c_int64, C.c_void_p]),
+    "nt_hip_gather": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_int64, C.c_void_p]),
+    "nt_hip_index_select": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_int64,
+                                      C.c_void_p]),
+    "nt_hip_one_hot": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_void_p]),
+    "nt_hip_scatter_add": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_int64,
+                                     C.c_void_p]),
+    "nt_hip_index_add": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_void_p]),
+    "nt_hip_fill": (C.c_int, [C.c_void_p, C.c_int64, C.c_float]),
     # noetic_rng.h
     "nt_rng_derive": (C.c_int, [C.POINTER(NtRng), C.c_uint64, C.c_char_p, C.c_size_t]),
     "nt_rng_from_seed": (C.c_int, [C.POINTER(NtRng), C.c_char_p]),
@@ -189,7 +215,8 @@ def launches() -> int:
 
 # ----------------------------------------------------------------------------------- storage
 
-_NP = {"f32": np.float32, "bf16": np.uint16, "u8": np.uint8, "i32": np.int32, "f64": np.float64}
+_NP = {"f32": np.float32, "bf16": np.uint16, "f16": np.uint16, "u8": np.uint8, "bool": np.uint8, "i32": np.int32,
+       "i64": np.int64, "f64": np.float64}
 
 
 class Buffer:
@@ -212,7 +239,8 @@ class Buffer:
 
 
 class Tensor:
-    """Device storage with a shape and a dtype ("f32", "bf16" bits, "u8", "i32", "f64")."""
+    """Device storage with a shape and a dtype ("f32", "bf16" or "f16" bits, "u8", "bool" bytes, "i32",
+    "i64", "f64")."""
 
     def __init__(self, shape: Sequence[int], dtype: str, buf: Optional[Buffer] = None):
         self.shape = tuple(int(s) for s in shape)
