@@ -412,13 +412,65 @@ def cpu_baseline_score_grad(w, rows_sample, min_seconds=10.0):
                       f"element), single thread, {t:.2f} s"}
 
 
+def bench_ops(nr, args):
+    """The general device ops (include/noetic_ops.h) at C4's shape, [256, 128256]: each op's
+    HIP-event time per call through the C ABI (outputs allocated before timing) and its
+    algorithmic bytes (every input element read once, every output element written once) against
+    the HBM peak. Rows are f32 unless named."""
+    from noetic_ops import BinaryOp, Layout, ReduceOp, UnaryOp
+
+    rows, V = 256, 128256
+    L = nr.lib()
+    rng = np.random.default_rng(args.seed)
+    xf = rng.normal(0, 2, (rows, V)).astype(np.float32)
+    x = nr.Tensor.from_numpy(xf)
+    xb = nr.Tensor.from_numpy((xf.view(np.uint32) >> 16).astype(np.uint16), "bf16")
+    mask = nr.Tensor.from_numpy(np.where(rng.random((1, V)) < 0.3, 0.0, -np.inf).astype(np.float32))
+    idx = nr.Tensor.from_numpy(rng.integers(0, V, (rows, 1)).astype(np.int32))
+    y = nr.Tensor((rows, V), "f32")
+    yr = nr.Tensor((rows,), "f32")
+    n = rows * V
+    lay = Layout([rows, V]).c()
+    mlay = Layout([1, V]).broadcast([rows, V]).c()
+    tlay = Layout([V, rows], [1, V]).c()
+    P = lambda t: C.c_void_p(t.ptr)
+    ck = lambda rc: nr._check(rc, "op")
+    cases = {
+        "cast bf16->f32": (lambda: ck(L.nt_hip_cast(P(xb), C.byref(lay), 1, 0, P(y))), 6 * n),
+        "unary div_scalar": (lambda: ck(L.nt_hip_unary(int(UnaryOp.DIV_SCALAR), 0.7, P(x), C.byref(lay), P(y))), 8 * n),
+        "unary exp": (lambda: ck(L.nt_hip_unary(int(UnaryOp.EXP), 0.0, P(x), C.byref(lay), P(y))), 8 * n),
+        "binary add [1,V] mask": (lambda: ck(L.nt_hip_binary(int(BinaryOp.ADD), P(x), C.byref(lay), P(mask),
+                                                             C.byref(mlay), P(y))), 8 * n + 4 * V),
+        "copy transposed [V,rows]": (lambda: ck(L.nt_hip_copy(P(x), C.byref(tlay), 4, P(y))), 8 * n),
+        "reduce_dim sum last axis (CpuRef order)": (lambda: ck(L.nt_hip_reduce_dim(int(ReduceOp.SUM), P(x), rows, V, 1,
+                                                                                   1, P(yr))), 4 * n + 4 * rows),
+        "reduce_dim argmax last axis": (lambda: ck(L.nt_hip_reduce_dim(int(ReduceOp.ARGMAX), P(x), rows, V, 1, 1,
+                                                                       P(yr))), 4 * n + 4 * rows),
+        "gather token logits": (lambda: ck(L.nt_hip_gather(P(x), rows, V, 1, P(idx), 1, P(yr))), 12 * rows),
+    }
+    res = {}
+    steps, warmup = min(args.steps, 50), min(args.warmup, 5)
+    for name, (fn, nbytes) in cases.items():
+        ms, _ = timed(nr, steps, warmup, lambda i: fn())
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[name] = {"us": round(ms * 1e3, 2), "bytes": nbytes, "gbs": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    top = res["unary div_scalar"]
+    return {"metric": "general device ops at [256,128256]: HIP-event time and achieved HBM GB/s per op",
+            "value": top["gbs"], "unit": "GB/s (unary div_scalar)", "n_gpus": 1, "steps": steps, "warmup": warmup,
+            "ms_per_step": top["us"] / 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "ops: the GpuBackend general ops on C4's shape, f32 rows unless named"},
+            "ops": res}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default 200; 20 for c3/c5)")
     ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 20; 3 for c3/c5)")
     ap.add_argument("--seed", type=int, default=2024)
-    ap.add_argument("--workload", default="c4", choices=["c4", "c2", "c3", "c3b", "c5"])
+    ap.add_argument("--workload", default="c4", choices=["c4", "c2", "c3", "c3b", "c5", "ops"])
     ap.add_argument("--cpu-rows", type=int, default=256, help="rows of the CPU baseline sample (0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="repeat the CPU sample up to this long")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -452,6 +504,8 @@ def main():
         out = bench_sample(nr, W, args, args.workload)
     elif args.workload == "c3b":
         out = bench_score_grad(nr, W, args)
+    elif args.workload == "ops":
+        out = bench_ops(nr, args)
     else:
         out = bench_score(nr, W, args, args.workload)
     print(json.dumps(out), flush=True)

@@ -37,6 +37,17 @@ __device__ __forceinline__ int64_t at(int64_t i, const View &v) {
     int64_t o = v.off;
     if constexpr (R == 1) {
         o += i * v.st[0];
+    } else if (i <= int64_t(0xffffffff)) {
+        // coordinates by 32-bit division (a third of the 64-bit sequence's instructions)
+        uint32_t u = uint32_t(i);
+#pragma unroll
+        for (int d = R - 1; d >= 1; d--) {
+            const uint32_t s = uint32_t(v.shape[d]);
+            const uint32_t q = u / s;
+            o += int64_t(u - q * s) * v.st[d];
+            u = q;
+        }
+        o += int64_t(u) * v.st[0];
     } else {
 #pragma unroll
         for (int d = R - 1; d >= 1; d--) {
@@ -146,6 +157,26 @@ __global__ __launch_bounds__(kOpsThreads) void k_copy(const T *__restrict__ x, V
     GRID_STRIDE(i, n) { y[at<R>(i, yv)] = x[at<R>(i, xv)]; }
 }
 
+// A transposed view into a contiguous output, out[a, b] = x[off + a + b ld]: 64 x 64 tiles
+// through LDS, read along a and written along b, so both sides are coalesced (the element loop
+// above would read with stride ld).
+template <typename T>
+__global__ __launch_bounds__(kOpsThreads) void k_transpose(const T *__restrict__ x, int64_t off, int64_t ld,
+                                                           T *__restrict__ y, int64_t A, int64_t B) {
+    __shared__ T tile[64][65];
+    const int64_t ta_n = (A + 63) / 64, tiles = ta_n * ((B + 63) / 64);
+    const int c = threadIdx.x & 63, r0 = threadIdx.x >> 6;
+    for (int64_t t = blockIdx.x; t < tiles; t += gridDim.x) {
+        const int64_t a0 = (t % ta_n) * 64, b0 = (t / ta_n) * 64;
+        for (int k = r0; k < 64; k += kOpsThreads / 64)
+            if (a0 + c < A && b0 + k < B) tile[k][c] = x[off + (b0 + k) * ld + a0 + c];
+        __syncthreads();
+        for (int k = r0; k < 64; k += kOpsThreads / 64)
+            if (a0 + k < A && b0 + c < B) y[(a0 + k) * B + b0 + c] = tile[c][k];
+        __syncthreads();
+    }
+}
+
 template <typename T>
 int launch_copy(const void *x, const NtLayout *xl, void *y, const NtLayout *yl) {
     const NtLayout *ls[2] = {xl, yl};
@@ -154,6 +185,14 @@ int launch_copy(const void *x, const NtLayout *xl, void *y, const NtLayout *yl) 
     const int64_t n = numel_of(xl);
     if (n == 0) return 0;
     hipStream_t s = ctx().stream;
+    if (R == 2 && v[1].off == 0 && v[1].st[1] == 1 && v[1].st[0] == v[1].shape[1] && v[0].st[0] == 1 &&
+        v[0].st[1] > 1) {
+        const int64_t A = v[0].shape[0], B = v[0].shape[1];
+        const int64_t tiles = ((A + 63) / 64) * ((B + 63) / 64);
+        hipLaunchKernelGGL((k_transpose<T>), dim3(unsigned(tiles < kMaxBlocks ? tiles : kMaxBlocks)), dim3(kOpsThreads),
+                           0, s, static_cast<const T *>(x), v[0].off, v[0].st[1], static_cast<T *>(y), A, B);
+        return launched("copy (transpose)");
+    }
     RANK_SWITCH(R, hipLaunchKernelGGL((k_copy<T, RR>), dim3(blocks_for(n)), dim3(kOpsThreads), 0, s,
                                       static_cast<const T *>(x), v[0], static_cast<T *>(y), v[1], n));
     return launched("copy");
@@ -265,11 +304,11 @@ int launch_cast(const void *x, const NtLayout *xl, void *y) {
 __device__ __forceinline__ float exp_f(float a) { return float(exp(double(a))); }
 __device__ __forceinline__ float log_f(float a) { return float(log(double(a))); }
 __device__ __forceinline__ float pow_f(float a, float s) { return float(pow(double(a), double(s))); }
-// The correctly rounded f32 quotient and square root: taken in f64 from f32 operands and rounded
-// once more to f32. For these operations f64 carries more than 2 x 24 + 2 bits, so the second
-// rounding never differs from rounding the exact value (and no compiler option can change it).
-__device__ __forceinline__ float div_f(float a, float b) { return float(double(a) / double(b)); }
-__device__ __forceinline__ float sqrt_f(float a) { return float(sqrt(double(a))); }
+// The correctly rounded f32 quotient and square root: the division operator and sqrtf compile to
+// the IEEE sequences (v_div_scale / v_div_fmas / v_div_fixup; v_sqrt_f32 with its residual
+// correction). __fsqrt_rn is not used: on this target it is v_sqrt_f32 alone, 1 ulp.
+__device__ __forceinline__ float div_f(float a, float b) { return a / b; }
+__device__ __forceinline__ float sqrt_f(float a) { return sqrtf(a); }
 
 __device__ __forceinline__ float unary_op(int op, float a, float s) {
     switch (op) {
@@ -298,6 +337,24 @@ template <int R>
 __global__ __launch_bounds__(kOpsThreads) void k_unary(int op, float s, const float *__restrict__ x, View xv,
                                                        float *__restrict__ y, int64_t n) {
     GRID_STRIDE(i, n) { y[i] = unary_op(op, x[at<R>(i, xv)], s); }
+}
+
+// The contiguous case, 16-byte aligned: four elements per thread through one 16-byte load and
+// store (the element loop moves 4 bytes per instruction).
+__global__ __launch_bounds__(kOpsThreads) void k_unary_vec(int op, float s, const float *__restrict__ x,
+                                                           float *__restrict__ y, int64_t n) {
+    const int64_t n4 = n / 4;
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    float4 *y4 = reinterpret_cast<float4 *>(y);
+    GRID_STRIDE(i, n4) {
+        float4 a = x4[i];
+        a.x = unary_op(op, a.x, s);
+        a.y = unary_op(op, a.y, s);
+        a.z = unary_op(op, a.z, s);
+        a.w = unary_op(op, a.w, s);
+        y4[i] = a;
+    }
+    GRID_STRIDE(i, n - 4 * n4) { y[4 * n4 + i] = unary_op(op, x[4 * n4 + i], s); }
 }
 
 template <int R>
@@ -356,7 +413,18 @@ __global__ __launch_bounds__(kOpsThreads) void k_sum_last(const float *__restric
         const float *r = x + row * n;
         const int64_t n8 = n - n % 8;
         float p = 0.0f;
-        for (int64_t j = g; j < n8; j += 8) p = p + r[j];
+        // The fold is one dependent chain per lane, so its loads go out 64 at a time ahead of
+        // the adds (the order of the adds is unchanged).
+        constexpr int kB = 64;
+        int64_t j = g;
+        for (; j + 8 * (kB - 1) < n8; j += 8 * kB) {
+            float v[kB];
+#pragma unroll
+            for (int t = 0; t < kB; t++) v[t] = r[j + 8 * t];
+#pragma unroll
+            for (int t = 0; t < kB; t++) p = p + v[t];
+        }
+        for (; j < n8; j += 8) p = p + r[j];
         // the group's partials to its lane 0 (widths of 8)
         const float p0 = __shfl(p, 0, 8), p1 = __shfl(p, 1, 8), p2 = __shfl(p, 2, 8), p3 = __shfl(p, 3, 8);
         const float p4 = __shfl(p, 4, 8), p5 = __shfl(p, 5, 8), p6 = __shfl(p, 6, 8), p7 = __shfl(p, 7, 8);
@@ -409,15 +477,33 @@ __device__ __forceinline__ Best shfl_best(Best b, int src_lane_delta) {
     return o;
 }
 
-// One block per lane of the last axis (or per lane of everything, outer = 1): each thread picks
-// over its strided subsequence, then the block combines.
-__global__ __launch_bounds__(kOpsThreads) void k_best_last(const float *__restrict__ x, int64_t outer, int64_t n,
-                                                           float *__restrict__ val, int32_t *__restrict__ idx) {
-    __shared__ Best wb[kOpsThreads / kWave];
+// One 1024-thread block per lane of the last axis (or per lane of everything, outer = 1): each
+// thread picks over its strided subsequence, then the block combines.
+constexpr int kBestThreads = 1024;
+__global__ __launch_bounds__(kBestThreads) void k_best_last(const float *__restrict__ x, int64_t outer, int64_t n,
+                                                            float *__restrict__ val, int32_t *__restrict__ idx) {
+    __shared__ Best wb[kBestThreads / kWave];
     for (int64_t row = blockIdx.x; row < outer; row += gridDim.x) {
         const float *r = x + row * n;
         Best b{r[0], 0};
-        for (int64_t k = threadIdx.x; k < n; k += blockDim.x) b = pick(b, Best{r[k], k});
+        if (n <= int64_t(0x7fffffff)) {
+            // 32-bit positions in the loop (the pick compares indices only on ties)
+            float bv = r[0];
+            int32_t bk = 0;
+            for (int32_t k = int32_t(threadIdx.x); k < int32_t(n); k += kBestThreads) {
+                const float e = r[k];
+                const bool en = e != e, bn = bv != bv;
+                // k > bk always here, so the earlier index wins ties: take e only if it is a NaN
+                // over a number, or a larger number
+                if (!bn && (en || e > bv)) {
+                    bv = e;
+                    bk = k;
+                }
+            }
+            b = Best{bv, bk};
+        } else {
+            for (int64_t k = threadIdx.x; k < n; k += kBestThreads) b = pick(b, Best{r[k], k});
+        }
         for (int o = kWave / 2; o > 0; o >>= 1) {
             const Best other = shfl_best(b, o);
             b = pick(b, other);
@@ -426,7 +512,7 @@ __global__ __launch_bounds__(kOpsThreads) void k_best_last(const float *__restri
         __syncthreads();
         if (threadIdx.x == 0) {
             Best t = wb[0];
-            for (int w = 1; w < kOpsThreads / kWave; w++) t = pick(t, wb[w]);
+            for (int w = 1; w < kBestThreads / kWave; w++) t = pick(t, wb[w]);
             if (val) val[row] = t.v;
             if (idx) idx[row] = int32_t(t.k);
         }
@@ -576,6 +662,12 @@ int nt_hip_unary(int32_t op, float scalar, const float *x, const NtLayout *xl, f
     View v[1];
     const int R = simplify(ls, 1, v);
     hipStream_t s = ctx().stream;
+    if (R == 1 && v[0].st[0] == 1 && reinterpret_cast<uintptr_t>(x + v[0].off) % 16 == 0 &&
+        reinterpret_cast<uintptr_t>(out) % 16 == 0) {
+        hipLaunchKernelGGL(k_unary_vec, dim3(blocks_for((n + 3) / 4)), dim3(kOpsThreads), 0, s, int(op), scalar,
+                           x + v[0].off, out, n);
+        return launched("unary");
+    }
     RANK_SWITCH(R, hipLaunchKernelGGL((k_unary<RR>), dim3(blocks_for(n)), dim3(kOpsThreads), 0, s, int(op), scalar, x,
                                       v[0], out, n));
     return launched("unary");
@@ -663,7 +755,7 @@ int nt_hip_reduce_dim(int32_t op, const float *x, int64_t outer, int64_t n, int6
     }
     if (inner == 1) {
         const int64_t b = outer > kMaxBlocks ? kMaxBlocks : outer;
-        hipLaunchKernelGGL(k_best_last, dim3(unsigned(b)), dim3(kOpsThreads), 0, s, x, outer, n, val, idx);
+        hipLaunchKernelGGL(k_best_last, dim3(unsigned(b)), dim3(kBestThreads), 0, s, x, outer, n, val, idx);
     } else {
         hipLaunchKernelGGL(k_best_mid, dim3(blocks_for(lanes)), dim3(kOpsThreads), 0, s, x, outer, n, inner, val, idx);
     }
@@ -680,7 +772,7 @@ int nt_hip_reduce_all(int32_t op, const float *x, int64_t n, float *out) {
     if (int rc = enter(&lk)) return rc;
     hipStream_t s = ctx().stream;
     if (op == NT_RED_SUM) hipLaunchKernelGGL(k_sum_last, dim3(1), dim3(kOpsThreads), 0, s, x, int64_t(1), n, out);
-    else hipLaunchKernelGGL(k_best_last, dim3(1), dim3(kOpsThreads), 0, s, x, int64_t(1), n, out, (int32_t *)nullptr);
+    else hipLaunchKernelGGL(k_best_last, dim3(1), dim3(kBestThreads), 0, s, x, int64_t(1), n, out, (int32_t *)nullptr);
     return launched("reduce_all");
 }
 

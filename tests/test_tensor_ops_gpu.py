@@ -54,6 +54,9 @@ VIEWS = [
     ((6, 7), (4, 6, 7), (0, 7, 1), 0),
     ((2, 3, 4, 5, 6), (2, 3, 4, 5, 6), (360, 120, 30, 6, 1), 0),
     ((2, 3, 4, 5, 6), (6, 5, 2, 4, 3), (1, 6, 360, 30, 120), 0),
+    # transposes of several 64 x 64 tiles (ragged at both edges), one from an offset
+    ((300, 130), (130, 300), (1, 130), 0),
+    ((10, 9), (8, 9), (1, 9), 1),
 ]
 
 
