@@ -358,3 +358,261 @@ def tempered_logits(logits: Tensor, temperature: float, mask: Optional[Tensor] =
         out = broadcast_shape(logits.shape, mask.shape)
         z = binary(BinaryOp.ADD, z, lay.broadcast(out), mask, Layout.contiguous(mask.shape).broadcast(out))
     return z
+
+
+# ----------------------------------------------------------------------------------- dispatch
+
+class DTensor:
+    """A tensor on the device: storage and the Layout it is read through. The methods are the
+    reference's tensor-level dispatch onto the trait (src/tensor/gpu/mod.rs:327-700, the `gpu_*`
+    functions) for the ops the rl chain uses: 16-bit operands are cast to f32 first
+    (`f32_operand`), reductions and indexing read a contiguous f32 copy (`f32_contiguous`), binary
+    ops broadcast both layouts to the output shape, and views (swap_dims, slice, expand, reshape of
+    a row-major layout) are new layouts over the same storage (layout.rs)."""
+
+    def __init__(self, storage: Tensor, layout: Optional[Layout] = None):
+        self.storage = storage
+        self.layout = layout if layout is not None else Layout.contiguous(storage.shape)
+        self.dtype = storage.dtype
+
+    @staticmethod
+    def from_numpy(a, dtype: Optional[str] = None) -> "DTensor":
+        return DTensor(Tensor.from_numpy(np.ascontiguousarray(a), dtype))
+
+    @property
+    def shape(self) -> List[int]:
+        return list(self.layout.shape)
+
+    def numel(self) -> int:
+        return self.layout.numel()
+
+    def contiguous(self) -> "DTensor":
+        """gpu_copy: the view's elements, row-major (the same storage when already so)."""
+        l = self.layout
+        if l.is_contiguous() and l.offset == 0 and self.storage.numel == l.numel():
+            return self
+        return DTensor(copy(self.storage, l))
+
+    def to_numpy(self) -> np.ndarray:
+        return self.contiguous().storage.to_numpy().reshape(self.shape)
+
+    # -- views (layout.rs)
+    def swap_dims(self, a: int, b: int) -> "DTensor":
+        return DTensor(self.storage, self.layout.swapped(a, b))
+
+    def slice(self, ranges: Sequence[range]) -> "DTensor":
+        return DTensor(self.storage, self.layout.narrowed(ranges))
+
+    def expand(self, shape: Sequence[int]) -> "DTensor":
+        return DTensor(self.storage, self.layout.broadcast(shape))
+
+    def unsqueeze(self, d: int) -> "DTensor":
+        sh, st = list(self.layout.shape), list(self.layout.strides)
+        sh.insert(d, 1)
+        st.insert(d, st[d] * sh[d + 1] if d < len(st) else 1)
+        return DTensor(self.storage, Layout(sh, st, self.layout.offset))
+
+    def reshape(self, shape: Sequence[int]) -> "DTensor":
+        c = self.contiguous()
+        return DTensor(c.storage, c.layout.reshaped(shape))
+
+    # -- operands
+    def _f32(self) -> "DTensor":
+        """f32_operand (gpu/mod.rs:336-342): f16 and bf16 are cast to f32 first."""
+        if self.dtype == "f32":
+            return self
+        if self.dtype in ("f16", "bf16"):
+            return DTensor(cast(self.storage, self.layout, "f32"))
+        raise TypeError(f"{self.dtype} storage in a float GPU kernel")
+
+    def _f32_contiguous(self) -> "DTensor":
+        return self._f32().contiguous()
+
+    # -- elementwise
+    def unary(self, op: UnaryOp, s: float = 0.0) -> "DTensor":
+        x = self._f32()
+        return DTensor(unary(op, x.storage, x.layout, float(np.float32(s))))
+
+    def neg(self):
+        return self.unary(UnaryOp.NEG)
+
+    def exp(self):
+        return self.unary(UnaryOp.EXP)
+
+    def log(self):
+        return self.unary(UnaryOp.LOG)
+
+    def sqrt(self):
+        return self.unary(UnaryOp.SQRT)
+
+    def recip(self):
+        return self.unary(UnaryOp.RECIP)
+
+    def abs(self):
+        return self.unary(UnaryOp.ABS)
+
+    def sign(self):
+        return self.unary(UnaryOp.SIGN)
+
+    def sigmoid(self):
+        return self.unary(UnaryOp.SIGMOID)
+
+    def add_scalar(self, s):
+        return self.unary(UnaryOp.ADD_SCALAR, s)
+
+    def sub_scalar(self, s):
+        return self.unary(UnaryOp.SUB_SCALAR, s)
+
+    def mul_scalar(self, s):
+        return self.unary(UnaryOp.MUL_SCALAR, s)
+
+    def div_scalar(self, s):
+        return self.unary(UnaryOp.DIV_SCALAR, s)
+
+    def powf_scalar(self, p: float) -> "DTensor":
+        """float.rs:543-570: an integer exponent goes through powi (0 ones, 1 itself, 2 x·x, −1 recip,
+        −2 recip(x·x)), any other through PowScalar(p as f32)."""
+        if float(p).is_integer():
+            k = int(p)
+            if k == 0:
+                return DTensor(fill(self.shape, 1.0))
+            if k == 1:
+                return self
+            if k == 2:
+                return self.mul(self)
+            if k == -1:
+                return self.recip()
+            if k == -2:
+                return self.mul(self).recip()
+        return self.unary(UnaryOp.POW_SCALAR, p)
+
+    def _binary(self, op: BinaryOp, other: "DTensor") -> "DTensor":
+        out = broadcast_shape(self.shape, other.shape)
+        a, b = self._f32(), other._f32()
+        return DTensor(binary(op, a.storage, a.layout.broadcast(out), b.storage, b.layout.broadcast(out)))
+
+    def add(self, o):
+        return self._binary(BinaryOp.ADD, o)
+
+    def sub(self, o):
+        return self._binary(BinaryOp.SUB, o)
+
+    def mul(self, o):
+        return self._binary(BinaryOp.MUL, o)
+
+    def div(self, o):
+        return self._binary(BinaryOp.DIV, o)
+
+    def compare(self, op: CmpOp, s: float) -> "DTensor":
+        x = self._f32()
+        return DTensor(compare(op, x.storage, x.layout, float(np.float32(s))))
+
+    def greater_elem(self, s):
+        return self.compare(CmpOp.GT, s)
+
+    def lower_elem(self, s):
+        return self.compare(CmpOp.LT, s)
+
+    def mask_fill(self, mask: "DTensor", value: float) -> "DTensor":
+        x = self._f32()
+        return DTensor(mask_fill(x.storage, x.layout, mask.storage, mask.layout.broadcast(self.shape),
+                                 float(np.float32(value))))
+
+    def clamp(self, lo: float, hi: float) -> "DTensor":
+        """float.rs:576-595: clamp_min(clamp_max(x, hi), lo), each a mask_fill of a comparison."""
+        x = self.mask_fill(self.greater_elem(hi), hi)
+        return x.mask_fill(x.lower_elem(lo), lo)
+
+    # -- reductions
+    def sum(self) -> "DTensor":
+        x = self._f32_contiguous()
+        return DTensor(reduce_all(ReduceOp.SUM, x.storage, x.numel()))
+
+    def mean(self) -> "DTensor":
+        return self.sum().div_scalar(float(self.numel()))
+
+    def max(self) -> "DTensor":
+        x = self._f32_contiguous()
+        return DTensor(reduce_all(ReduceOp.MAX, x.storage, x.numel()))
+
+    def sum_dim(self, d: int) -> "DTensor":
+        x = self._f32_contiguous()
+        return DTensor(reduce_dim(ReduceOp.SUM, x.storage, self.shape, d))
+
+    def mean_dim(self, d: int) -> "DTensor":
+        return self.sum_dim(d).div_scalar(float(self.shape[d]))
+
+    def max_dim(self, d: int) -> "DTensor":
+        x = self._f32_contiguous()
+        return DTensor(reduce_dim(ReduceOp.MAX, x.storage, self.shape, d))
+
+    def argmax(self, d: int) -> np.ndarray:
+        """gpu_argmax: I32 device indices read back as host i64 (int tensors live on the host)."""
+        x = self._f32_contiguous()
+        return reduce_dim(ReduceOp.ARGMAX, x.storage, self.shape, d).to_numpy().astype(np.int64)
+
+    # -- indexing and casts
+    def gather(self, d: int, idx: np.ndarray) -> "DTensor":
+        x = self._f32_contiguous()
+        sh = self.shape
+        outer, n, inner = int(np.prod(sh[:d])), sh[d], int(np.prod(sh[d + 1:]))
+        m = idx.shape[d]
+        i = Tensor.from_numpy(np.ascontiguousarray(idx, np.int64).astype(np.int32))
+        y = gather(x.storage, (outer, n, inner, m), i)
+        return DTensor(y, Layout.contiguous(list(idx.shape)))
+
+    def select(self, d: int, indices: Sequence[int]) -> "DTensor":
+        x = self._f32_contiguous()
+        sh = self.shape
+        outer, n, inner = int(np.prod(sh[:d])), sh[d], int(np.prod(sh[d + 1:]))
+        i = Tensor.from_numpy(np.asarray(indices, np.int32))
+        y = index_select(x.storage, (outer, n, inner, len(indices)), i)
+        out = list(sh)
+        out[d] = len(indices)
+        return DTensor(y, Layout.contiguous(out))
+
+    def cast(self, to: str) -> "DTensor":
+        """gpu_cast: 16-bit through f32 (f32_operand), f32 to 16-bit by the cast kernel."""
+        if to == "f32":
+            return self._f32().contiguous()
+        x = self._f32()
+        return DTensor(cast(x.storage, x.layout, to))
+
+    def float(self) -> "DTensor":
+        """A bool tensor as f32 1.0 / 0.0 (gpu_bool_float)."""
+        return DTensor(cast(self.storage, self.layout, "f32"))
+
+    def slice_assign(self, ranges: Sequence[range], value: "DTensor") -> "DTensor":
+        """gpu_slice_assign: a fresh copy of self with value written into ranges."""
+        out = DTensor(copy(self._f32().storage, self._f32().layout))
+        v = value._f32()
+        write(out.storage, Layout.contiguous(self.shape).narrowed(ranges), v.storage, v.layout)
+        return out
+
+    @staticmethod
+    def cat(parts: Sequence["DTensor"], d: int) -> "DTensor":
+        """gpu_cat: each part written into its slice of one fresh f32 buffer."""
+        out_sh = list(parts[0].shape)
+        out_sh[d] = sum(p.shape[d] for p in parts)
+        out = alloc("f32", out_sh)
+        base = Layout.contiguous(out_sh)
+        at = 0
+        for p in parts:
+            v = p._f32()
+            r = [range(0, s) for s in out_sh]
+            r[d] = range(at, at + p.shape[d])
+            at += p.shape[d]
+            write(out, base.narrowed(r), v.storage, v.layout)
+        return DTensor(out)
+
+
+def softmax(x: DTensor, d: int) -> DTensor:
+    """activation.rs:13-25: exp(x − max) / Σ exp(x − max) along d."""
+    e = x.sub(x.max_dim(d)).exp()
+    return e.div(e.sum_dim(d))
+
+
+def log_softmax(x: DTensor, d: int) -> DTensor:
+    """activation.rs:27-42: (x − max) − log Σ exp(x − max) along d."""
+    shifted = x.sub(x.max_dim(d))
+    return shifted.sub(shifted.exp().sum_dim(d).log())
