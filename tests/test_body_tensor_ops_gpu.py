@@ -3,7 +3,9 @@ ops, through the tensor-level dispatch mirror (noetic_ops.DTensor):
 - `body_exact_ops_match_cpu_ref_bit_for_bit`: every case but the three matmuls (matmul is off the
   rl path here), bit for bit against CpuRef;
 - `body_transcendentals_within_4_ulp`: exp, log, sqrt, powf 0.5 and 3, sigmoid within 4 ulp, and
-  softmax / log_softmax within 1e-6 relative.
+  softmax / log_softmax within 1e-6 relative;
+- `body_nan_max_argmax_and_stable_sort_match_cpu_ref` without its sort (off this path) and
+  `body_deterministic_twice` without its matmul (ops.rs:183-234).
 Inputs are the reference's own: `t(shape, seed)` = rnd(numel, seed, -2, 2) (ChaCha8 seeded from
 the u64, rand 0.8's f32 gen_range; tests/mod.rs:28-31), restated by the oracle and pinned there
 against the reference's fixture records. CpuRef's values are the checker's: IEEE f32 elementwise
@@ -181,3 +183,29 @@ def test_body_transcendentals_within_4_ulp():
         report.append(f"{name} max rel {d:.1e}")
         assert d <= 1e-6, f"{name}: {d}"
     print("; ".join(report))
+
+
+def test_body_nan_max_argmax_match_cpu_ref():
+    """ops.rs:219-234 (the sort half is off this path): NaN-propagating max and argmax."""
+    nan = np.nan
+    v = np.array([1.0, nan, 5.0, 2.0, nan, 3.0, 9.0, 0.0, 4.0, nan, nan, 1.0, 1.0, 7.0, 7.0, 2.0], F).reshape(4, 4)
+    x = DTensor.from_numpy(v)
+    for d in (0, 1):
+        idx, val = T.argmax_dim(v, [4, 4], d)
+        assert np.array_equal(x.argmax(d), idx), f"argmax {d}"
+        assert ulps(x.max_dim(d).to_numpy(), val).max() == 0, f"max_dim {d}"
+    for w in ([1.0, nan, 2.0], [nan, 1.0, 2.0], [1.0, 2.0, nan], [1.0, 3.0, 2.0]):
+        w = np.array(w, F)
+        assert ulps(DTensor.from_numpy(w).max().to_numpy(), np.array([T.max_all(w)], F)).max() == 0, "max"
+
+
+def test_body_deterministic_twice():
+    """ops.rs:183-196 without its matmul (off this path): a softmax's lane sums and a sigmoid's
+    means, computed twice, are the same bits."""
+    def run():
+        a = DTensor.from_numpy(t([8, 64, 96], 11))
+        y = ops.softmax(a, 2).sum_dim(1).log()
+        z = a.sigmoid().mean_dim(2)
+        return y.to_numpy(), z.to_numpy()
+    (y1, z1), (y2, z2) = run(), run()
+    assert y1.tobytes() == y2.tobytes() and z1.tobytes() == z2.tobytes()
