@@ -464,13 +464,76 @@ def bench_ops(nr, args):
             "ops": res}
 
 
+def bench_readout(nr, W, args):
+    """What fusing the sampler into the decoder readout could save at C4's decode shape: the readout
+    GEMM logits[256, 128256] = h[256, 4096] · W[4096, 128256] in bf16 (torch.matmul, hipBLASLt,
+    as the baseline a fused kernel would have to match), then nt_hip_rl_sample on the logits it
+    just wrote, both on the library's stream. The sampler's share of the step is the most a
+    readout-fused epilogue could remove; the GEMM itself reads the 1.05 GB weight matrix."""
+    import torch
+
+    rows, d, V = 256, 4096, 128256
+    stream = C.c_void_p()
+    nr._check(nr.lib().nt_hip_stream(C.byref(stream)), "stream")
+    ts = torch.cuda.ExternalStream(stream.value, device="cuda:0")
+    g = torch.Generator(device="cuda:0").manual_seed(args.seed)
+    w = W.c4(args.seed)
+    with torch.cuda.stream(ts):
+        h = torch.randn(rows, d, device="cuda:0", dtype=torch.bfloat16, generator=g)
+        wt = (torch.randn(d, V, device="cuda:0", dtype=torch.bfloat16, generator=g) * (2.0 / 64.0)).to(torch.bfloat16)
+        logits = torch.empty(rows, V, device="cuda:0", dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    U = nr.Tensor.from_numpy(nr.Rng(args.seed, "readout/uniforms").uniforms(rows), "f64")
+    ids, logp, st = nr.IntTensor((rows,)), nr.Tensor((rows,), "f32"), nr.Tensor((rows,), "u8")
+    a = nr.NtRlSampleArgs(logits.data_ptr(), nr.NT_BF16, nr.NT_MASK_U8, rows, V, V, w["mask"].ptr, V, 0.7, U.ptr,
+                          ids.ptr, logp.ptr, None, st.ptr)
+    L = nr.lib()
+
+    def gemm(i):
+        with torch.cuda.stream(ts):
+            torch.matmul(h, wt, out=logits)
+
+    def sample(i):
+        nr._check(L.nt_hip_rl_sample(C.byref(a)), "sample")
+
+    def step(i):
+        gemm(i)
+        sample(i)
+
+    steps, warmup = min(args.steps, 50), min(args.warmup, 5)
+    # three interleaved rounds of each; medians (the GEMM's own time varies by a few us)
+    res = {"gemm": [], "sample": [], "step": []}
+    for _ in range(3):
+        res["gemm"].append(timed(nr, steps, warmup, gemm)[0])
+        gemm(0)
+        res["sample"].append(timed(nr, steps, warmup, sample)[0])
+        res["step"].append(timed(nr, steps, warmup, step)[0])
+    ms_gemm, ms_sample, ms_step = (float(np.median(res[k])) for k in ("gemm", "sample", "step"))
+    stn = st.to_numpy()
+    if np.any(stn != 0):
+        raise RuntimeError("readout: refused rows")
+    gemm_bytes = 2 * (rows * d + d * V + rows * V)
+    return {"metric": "decode step at C4's shape: bf16 readout GEMM + fused sample, and the sampler's share",
+            "value": rows / (ms_step * 1e-3), "unit": "rows/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+            "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": "readout: h[256,4096] @ W[4096,128256] bf16 (torch.matmul) then nt_hip_rl_sample "
+                                   "(u8 c4 mask, tau 0.7) on the logits just written"},
+            "readout": {"gemm_us": round(ms_gemm * 1e3, 2), "step_us": round(ms_step * 1e3, 2),
+                        "sampler_alone_us": round(ms_sample * 1e3, 2),
+                        "step_minus_gemm_us": round((ms_step - ms_gemm) * 1e3, 2),
+                        "sampler_share_of_gemm_plus_sampler": round(ms_sample / (ms_gemm + ms_sample), 4),
+                        "gemm_gbs": round(gemm_bytes / (ms_gemm * 1e-3) / 1e9, 1),
+                        "gemm_tflops": round(2 * rows * d * V / (ms_gemm * 1e-3) / 1e12, 1)}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default 200; 20 for c3/c5)")
     ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 20; 3 for c3/c5)")
     ap.add_argument("--seed", type=int, default=2024)
-    ap.add_argument("--workload", default="c4", choices=["c4", "c2", "c3", "c3b", "c5", "ops"])
+    ap.add_argument("--workload", default="c4", choices=["c4", "c2", "c3", "c3b", "c5", "ops", "readout"])
     ap.add_argument("--cpu-rows", type=int, default=256, help="rows of the CPU baseline sample (0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="repeat the CPU sample up to this long")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -499,6 +562,10 @@ def main():
     import noetic_rl as nr
     import workloads as W
 
+    if args.workload == "readout":
+        # torch's own HIP runtime must find the device before the library claims it
+        import torch
+        torch.zeros(1, device="cuda:0")
     nr.claim(0)
     if args.workload in ("c4", "c2"):
         out = bench_sample(nr, W, args, args.workload)
@@ -506,6 +573,8 @@ def main():
         out = bench_score_grad(nr, W, args)
     elif args.workload == "ops":
         out = bench_ops(nr, args)
+    elif args.workload == "readout":
+        out = bench_readout(nr, W, args)
     else:
         out = bench_score(nr, W, args, args.workload)
     print(json.dumps(out), flush=True)
