@@ -70,7 +70,11 @@ const char *nt_hip_last_error(void);
 /* Provenance key, e.g. "hip-<gcnArchName>-rocm<ver>-kernels-<sha16>" (cf. `key`,
  * src/tensor/cuda/backend.rs:962-966); written NUL-terminated into buf. */
 int nt_hip_key(char *buf, size_t cap);
-/* GpuBackend::alloc / upload / download / sync (src/tensor/gpu/mod.rs:139-140,181-184). */
+/* GpuBackend::alloc / upload / download / sync (src/tensor/gpu/mod.rs:139-140,181-184).
+ * nt_hip_alloc takes memory from the device's stream-ordered pool when it has one: it is valid for
+ * work queued on the library stream after the call. nt_hip_free only records the pointer and
+ * returns at once (the reference's Mem drop, src/tensor/cuda/backend.rs:35-45); the next entry
+ * point frees it on the stream, after the work queued before the release. */
 int nt_hip_alloc(size_t bytes, void **out);
 int nt_hip_free(void *ptr);
 int nt_hip_upload(void *dst, const void *src, size_t bytes);   /* host -> device, synchronous */

@@ -14,6 +14,7 @@ namespace nt {
 struct Ctx {
     int device = -1;
     hipStream_t stream = nullptr;
+    bool pools = false;  // stream-ordered allocation (hipMallocAsync / hipFreeAsync) on the device
     std::mutex mu;
     uint64_t launches = 0;
 };
@@ -27,7 +28,8 @@ int hip_check(hipError_t err, const char *what);
 // Check a kernel launch just issued on the library stream and count it.
 int launched(const char *what);
 
-// Lock the context and require a claimed device; on success `*out` holds the lock.
+// Lock the context, require a claimed device, make it current and free (stream-ordered) what
+// nt_hip_free recorded since; on success `*out` holds the lock.
 int enter(std::unique_lock<std::mutex> *out);
 
 }  // namespace nt

@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "../../include/noetic_hip.h"
 #include "nt_internal.hpp"
@@ -44,12 +45,32 @@ int launched(const char *what) {
     return 0;
 }
 
+// Pointers released by nt_hip_free since the last entry, freed on the stream by the next one
+// (the reference's PENDING_FREE, src/tensor/cuda/backend.rs:35-45 and 222-243: a release only
+// records the pointer, so it never waits for the device or for the context's lock).
+static std::mutex g_pending_mu;
+static std::vector<void *> g_pending;
+
 int enter(std::unique_lock<std::mutex> *out) {
     Ctx &c = ctx();
     std::unique_lock<std::mutex> lk(c.mu);
     if (c.device < 0) return fail(NT_E_UNCLAIMED, "no HIP device claimed in this process (nt_hip_claim)");
     hipError_t e = hipSetDevice(c.device);
     if (e != hipSuccess) return hip_check(e, "hipSetDevice");
+    std::vector<void *> freed;
+    {
+        std::lock_guard<std::mutex> pl(g_pending_mu);
+        freed.swap(g_pending);
+    }
+    for (void *p : freed) {
+        // the work queued before the release still runs first: the free is ordered after it
+        if (c.pools) {
+            if (int rc = hip_check(hipFreeAsync(p, c.stream), "hipFreeAsync")) return rc;
+        } else {
+            if (int rc = hip_check(hipStreamSynchronize(c.stream), "hipStreamSynchronize")) return rc;
+            if (int rc = hip_check(hipFree(p), "hipFree")) return rc;
+        }
+    }
     *out = std::move(lk);
     return 0;
 }
@@ -91,8 +112,14 @@ int nt_hip_claim(int device) {
     // Default priority only: streams of other priorities are not used by this library.
     if (int rc = hip_check(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreateWithFlags"))
         return rc;
+    int pools = 0;
+    if (hipDeviceGetAttribute(&pools, hipDeviceAttributeMemoryPoolsSupported, device) != hipSuccess) {
+        (void)hipGetLastError();
+        pools = 0;
+    }
     c.device = device;
     c.stream = s;
+    c.pools = pools != 0;
     return 0;
 }
 
@@ -121,16 +148,17 @@ int nt_hip_alloc(size_t bytes, void **out) {
     if (int rc = enter(&lk)) return rc;
     *out = nullptr;
     if (bytes == 0) return 0;
+    // From the device's stream-ordered pool when it has one (cuMemAllocAsync in the reference,
+    // src/tensor/cuda/backend.rs:245-264): usable by work queued on the library stream after it.
+    if (ctx().pools) return hip_check(hipMallocAsync(out, bytes, ctx().stream), "hipMallocAsync");
     return hip_check(hipMalloc(out, bytes), "hipMalloc");
 }
 
 int nt_hip_free(void *ptr) {
     if (!ptr) return 0;
-    std::unique_lock<std::mutex> lk;
-    if (int rc = enter(&lk)) return rc;
-    // Work queued on the library stream may still read the buffer: drain it first.
-    if (int rc = hip_check(hipStreamSynchronize(ctx().stream), "hipStreamSynchronize")) return rc;
-    return hip_check(hipFree(ptr), "hipFree");
+    std::lock_guard<std::mutex> pl(g_pending_mu);
+    g_pending.push_back(ptr);
+    return 0;
 }
 
 int nt_hip_upload(void *dst, const void *src, size_t bytes) {

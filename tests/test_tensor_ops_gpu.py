@@ -282,3 +282,24 @@ def test_tempered_logits_from_the_general_ops(dtype):
         want = O.tempered(x.reshape(-1, 257), tau, addmask=mask.reshape(1, 257))
         assert np.array_equal(bits(z), bits(want))
     assert ops.tempered_logits(xt, 1.0, None) is xt
+
+
+def test_release_is_stream_ordered():
+    """nt_hip_free only records the pointer; the next entry frees it on the stream after the work
+    queued before it (the reference's deferred, stream-ordered free). A buffer released while a
+    kernel that reads it is still queued, then memory taken again and filled, leaves that kernel's
+    result intact."""
+    import ctypes as C
+    L = nr.lib()
+    n = 1 << 24
+    x = np.random.default_rng(10).normal(0, 1, n).astype(np.float32)
+    for _ in range(3):
+        xt = dev(x)
+        y = nr.Tensor((n,), "f32")
+        nr._check(L.nt_hip_unary(int(UnaryOp.EXP), 0.0, C.c_void_p(xt.ptr), C.byref(Layout([n]).c()), C.c_void_p(y.ptr)),
+                  "exp")
+        del xt  # released with the exp still queued
+        z = ops.fill((n,), 7.0)  # new memory, possibly the same block, written on the stream
+        got = y.to_numpy()
+        assert np.array_equal(got, ops.unary(UnaryOp.EXP, dev(x), Layout([n])).to_numpy())
+        assert np.all(z.to_numpy() == np.float32(7.0))
