@@ -2,7 +2,8 @@
 passes them: every kernel must read only the first V elements of each row and write only the first
 V gradient elements. The pads hold NaN (inputs) or a sentinel (gradient), so a read or write of a
 pad shows. With aligned strides the results equal the dense call's bit for bit; with unaligned
-strides (the element-wise path) they hold the oracle's tolerances.
+strides (the element-wise path) they hold the oracle's tolerances. Several host threads calling
+the entry points at once get the results of calling them one after another.
 """
 import ctypes as C
 
@@ -133,3 +134,37 @@ def test_scoring_and_backward_read_and_write_only_the_first_V(case):
         for s, d in zip(s_out, d_out):
             assert s.tobytes() == d.tobytes(), "aligned strides: the dense call's bits"
         assert s_grad[:, :V].tobytes() == d_grad.tobytes()
+
+
+def test_entry_points_from_several_threads():
+    """Every device entry point takes the one process-wide lock (the reference's Mutex<Ctx>), so
+    host threads calling the sampler and the scorer at once get the results of calling them one
+    after another."""
+    import threading
+    rng = np.random.default_rng(77)
+    rows, V = 40, 5000
+    jobs = []
+    for k in range(6):
+        x = rng.normal(0, 2, (rows, V)).astype(np.float32)
+        tok = rng.integers(0, V, rows).astype(np.int32)
+        jobs.append((dev(x), dev(tok), dev(rng.random(rows), "f64")))
+
+    def run(job):
+        xt, tt, ut = job
+        ids, lp, ent = nr.sample_logp(xt, 0.9, None, None, entropy=True, uniforms=ut)
+        slp, _, _, sent = nr.score(xt, None, tt)
+        return [a.to_numpy().tobytes() for a in (ids, lp, ent, slp, sent)]
+
+    want = [run(j) for j in jobs]
+    got = [None] * len(jobs)
+
+    def worker(i):
+        for _ in range(5):
+            got[i] = run(jobs[i])
+
+    th = [threading.Thread(target=worker, args=(i,)) for i in range(len(jobs))]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join()
+    assert got == want
