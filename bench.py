@@ -9,7 +9,8 @@ library's own stream; the same launches re-reading one input are reported as `wa
 bytes per launch / average launch time against the 8 TB/s HBM peak) and a `cpu_baseline`
 object (the reference's Cpu(Reference) op sequence, restated in oracle/, timed on this host).
 
-`--workload c2|c3|c3b|c5` measures the other configurations the same way, one JSON line each:
+`--workload c4s|c2|c3|c3b|c5` measures the other configurations the same way, one JSON line each:
+  c4s C4 with one u8 grammar mask [1,V] shared by every row (mask_ld 0);
   c2  decode step, f32 [1,64,1,32000], no mask, tau 0.8: the fused sample + logp;
   c3  PPO scoring, bf16 policy + reference [8,16,512,50304]: logp, reference logp, exact KL,
       entropy (nt_hip_rl_score) and the k3 per-token KL (nt_hip_rl_kl_estimate);
@@ -143,7 +144,8 @@ def cpu_baseline(w, rows_sample, seed, min_seconds=10.0):
     V = w["V"]
     x = W.download_rows(w["logits"], range(rows_sample), V)
     x = W.bf16_to_f32(x) if w["logits"].dtype == "bf16" else x
-    keep = W.download_rows(w["mask"], range(rows_sample), V) if w["mask"] is not None else None
+    mrows = [0] * rows_sample if w.get("mask_shared") else range(rows_sample)
+    keep = W.download_rows(w["mask"], mrows, V) if w["mask"] is not None else None
     rng = O.Rng(seed, f"{w['name']}/gumbel")
     reps, t_ref = 0, 0.0
     while reps < 1 or (t_ref < min_seconds and reps < 1000):
@@ -209,15 +211,20 @@ def bench_sample(nr, W, args, name):
     input was last touched a GiB of traffic earlier: `value` and `roofline` are HBM-cold. The
     same launches on one input, re-read every time (cache-warm, as when the logits were just
     written by the readout), are reported beside them as `warm_cache`."""
-    mk_w = (lambda sd: W.c4(sd)) if name == "c4" else (lambda sd: W.c2(sd))
+    shared = name == "c4s"  # C4 with one grammar mask [1, V] shared by every row (mask_ld 0)
+
+    def mk_w(sd):
+        return W.c2(sd) if name == "c2" else W.c4(sd, shared_mask=shared)
+
     w = mk_w(args.seed)
     rows, V = w["rows"], w["V"]
     dt = nr.NT_BF16 if w["logits"].dtype == "bf16" else nr.NT_F32
     mk = nr.NT_MASK_U8 if w["mask"] is not None else nr.NT_MASK_NONE
     esz = 2 if dt == nr.NT_BF16 else 4
     # Algorithmic bytes per launch: every input read once, every output written once.
-    per_row = esz * V + (V if mk == nr.NT_MASK_U8 else 0) + 8 + 4 + 4 + 1  # logits, mask, uniform, id, logp, status
-    bytes_launch = per_row * rows
+    mask_row = V if (mk == nr.NT_MASK_U8 and not shared) else 0
+    per_row = esz * V + mask_row + 8 + 4 + 4 + 1  # logits, mask, uniform, id, logp, status
+    bytes_launch = per_row * rows + (V if shared else 0)
     copies = max(2, -(-CACHE_BYTES // bytes_launch))
     ws = [w] + [mk_w(args.seed + 1 + k) for k in range(copies - 1)]
     n_launch = args.warmup + args.steps
@@ -233,7 +240,8 @@ def bench_sample(nr, W, args, name):
             x = pick(i)
             out.append(nr.NtRlSampleArgs(x["logits"].ptr, dt, mk, rows, V, V,
                                          x["mask"].ptr if x["mask"] is not None else None,
-                                         V if x["mask"] is not None else 0, w["temperature"], U.ptr + 8 * rows * i,
+                                         V if (x["mask"] is not None and not shared) else 0, w["temperature"],
+                                         U.ptr + 8 * rows * i,
                                          ids.ptr, logp.ptr, None, status.ptr))
         return out
 
@@ -253,7 +261,13 @@ def bench_sample(nr, W, args, name):
                           "inputs": "one input re-read every launch (served partly by the Infinity Cache)"}
     if name == "c4":
         roof["measured_copy_gbs"] = copy_peak(nr)  # a device-to-device copy on this box, for scale
-    if name == "c4":
+    if name == "c4s":
+        metric = "rows/sec + achieved HBM GB/s, fused masked sample+logprob, V=128256 bf16, one shared mask"
+        config = {"workload": "c4 with one u8 grammar mask [1,V] shared by the 256 rows (mask_ld 0): bf16 logits "
+                              "[1,256,1,128256] ~ N(0,2^2), temperature 0.7, fused sample + logp; launches cycle over "
+                              "independent input copies (1 GiB in all)", "rows": rows, "vocab": V,
+                  "parallelism": "none (1 GPU)"}
+    elif name == "c4":
         metric = "rows/sec + achieved HBM GB/s, fused masked sample+logprob, V=128256 bf16"
         config = {"workload": "c4 constrained decode: bf16 logits [1,256,1,128256] ~ N(0,2^2), u8 grammar mask "
                               "[256,V] of contiguous runs (~30% kept), temperature 0.7, fused sample + logp; launches cycle over "
@@ -533,7 +547,7 @@ def main():
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default 200; 20 for c3/c5)")
     ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 20; 3 for c3/c5)")
     ap.add_argument("--seed", type=int, default=2024)
-    ap.add_argument("--workload", default="c4", choices=["c4", "c2", "c3", "c3b", "c5", "ops", "readout"])
+    ap.add_argument("--workload", default="c4", choices=["c4", "c4s", "c2", "c3", "c3b", "c5", "ops", "readout"])
     ap.add_argument("--cpu-rows", type=int, default=256, help="rows of the CPU baseline sample (0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="repeat the CPU sample up to this long")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -567,7 +581,7 @@ def main():
         import torch
         torch.zeros(1, device="cuda:0")
     nr.claim(0)
-    if args.workload in ("c4", "c2"):
+    if args.workload in ("c4", "c4s", "c2"):
         out = bench_sample(nr, W, args, args.workload)
     elif args.workload == "c3b":
         out = bench_score_grad(nr, W, args)

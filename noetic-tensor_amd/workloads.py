@@ -51,14 +51,17 @@ def c2(seed=2024, rows=64):
     return {"name": "c2", "logits": x, "mask": None, "temperature": 0.8, "rows": rows, "V": V}
 
 
-def c4(seed=2024, rows=256):
+def c4(seed=2024, rows=256, shared_mask=False):
+    """C4's decode rows; with shared_mask, one grammar mask [1, V] that every row reads (mask_ld 0)."""
     V = 128256
     x = normal((1, rows, 1, V), "bf16", seed, "c4/logits", std=2.0)
-    m = np.empty((1, rows, 1, V), dtype=np.uint8)
+    mrows = 1 if shared_mask else rows
+    m = np.empty((1, mrows, 1, V), dtype=np.uint8)
     lab = b"c4/mask"
-    nr._check(nr.lib().nt_synth_runs_mask_host(m.ctypes.data_as(C.c_void_p), rows, V, seed, lab, len(lab), 96, 224),
+    nr._check(nr.lib().nt_synth_runs_mask_host(m.ctypes.data_as(C.c_void_p), mrows, V, seed, lab, len(lab), 96, 224),
               "runs mask")
-    return {"name": "c4", "logits": x, "mask": nr.Tensor.from_numpy(m, "u8"), "temperature": 0.7, "rows": rows, "V": V}
+    return {"name": "c4s" if shared_mask else "c4", "logits": x, "mask": nr.Tensor.from_numpy(m, "u8"),
+            "mask_shared": shared_mask, "temperature": 0.7, "rows": rows, "V": V}
 
 
 def c3(seed=2024, rows=8 * 16 * 512):
