@@ -67,9 +67,15 @@ int nt_hip_claim(int device);
 int nt_hip_device_count(void);
 /* The text of the last failure on the calling thread ("" if none). */
 const char *nt_hip_last_error(void);
-/* Provenance key, e.g. "hip-<gcnArchName>-rocm<ver>-kernels-<sha16>" (cf. `key`,
- * src/tensor/cuda/backend.rs:962-966); written NUL-terminated into buf. */
+/* Provenance key, "hip-<gcnArchName>-hiprt<runtime version>-kernels-<sha16 of the device
+ * sources>" (cf. `key`, src/tensor/cuda/backend.rs:962-966); written NUL-terminated into buf. */
 int nt_hip_key(char *buf, size_t cap);
+/* What the device's results depend on outside the library's sources (cf. `platform_details`,
+ * src/tensor/gpu/mod.rs:199, src/tensor/cuda/backend.rs:968-974, used by `gpu_platform_key`,
+ * gpu/mod.rs:699-700): "hipdriver<version>-amdgpu-<kernel driver release or inbox>-clang-<the
+ * compiler version and release that built the code objects>", NUL-terminated into buf; an
+ * error when cap cannot hold it. */
+int nt_hip_platform_details(char *buf, size_t cap);
 /* GpuBackend::alloc / upload / download / sync (src/tensor/gpu/mod.rs:139-140,181-184).
  * nt_hip_alloc takes memory from the device's stream-ordered pool when it has one: it is valid for
  * work queued on the library stream after the call. nt_hip_free only records the pointer and

@@ -62,13 +62,21 @@ int enter(std::unique_lock<std::mutex> *out) {
         std::lock_guard<std::mutex> pl(g_pending_mu);
         freed.swap(g_pending);
     }
-    for (void *p : freed) {
+    for (size_t i = 0; i < freed.size(); ++i) {
         // the work queued before the release still runs first: the free is ordered after it
+        void *p = freed[i];
+        int rc = 0;
         if (c.pools) {
-            if (int rc = hip_check(hipFreeAsync(p, c.stream), "hipFreeAsync")) return rc;
+            rc = hip_check(hipFreeAsync(p, c.stream), "hipFreeAsync");
         } else {
-            if (int rc = hip_check(hipStreamSynchronize(c.stream), "hipStreamSynchronize")) return rc;
-            if (int rc = hip_check(hipFree(p), "hipFree")) return rc;
+            rc = hip_check(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
+            if (!rc) rc = hip_check(hipFree(p), "hipFree");
+        }
+        if (rc) {
+            // keep what is not freed yet for the next entry
+            std::lock_guard<std::mutex> pl(g_pending_mu);
+            g_pending.insert(g_pending.end(), freed.begin() + (ptrdiff_t)i + 1, freed.end());
+            return rc;
         }
     }
     *out = std::move(lk);
@@ -139,6 +147,49 @@ int nt_hip_key(char *buf, size_t cap) {
     std::string sha(NT_KERNELS_SHA);
     std::string key = "hip-" + arch + "-hiprt" + std::to_string(rt) + "-kernels-" + sha.substr(0, 16);
     std::snprintf(buf, cap, "%s", key.c_str());
+    return 0;
+}
+
+int nt_hip_platform_details(char *buf, size_t cap) {
+    if (!buf || cap == 0) return fail(NT_E_ARG, "nt_hip_platform_details: empty buffer");
+    std::unique_lock<std::mutex> lk;
+    if (int rc = enter(&lk)) return rc;
+    int drv = 0;
+    if (int rc = hip_check(hipDriverGetVersion(&drv), "hipDriverGetVersion")) return rc;
+    // The kernel driver's release, when the amdgpu module reports one (a packaged driver does;
+    // the one built into the kernel does not).
+    std::string kmd = "inbox";
+    if (std::FILE *f = std::fopen("/sys/module/amdgpu/version", "r")) {
+        char v[64] = {0};
+        if (std::fgets(v, sizeof v, f)) {
+            std::string t(v);
+            while (!t.empty() && (t.back() == '\n' || t.back() == ' ')) t.pop_back();
+            if (!t.empty()) kmd = t;
+        }
+        std::fclose(f);
+    }
+    // The compiler that built the code objects: its version and release tag, without the
+    // repository URL and commit.
+    std::string cc;
+    {
+        std::string word;
+        const std::string text = std::string(__clang_version__) + " ";
+        for (char ch : text) {
+            if (ch != ' ' && ch != '(' && ch != ')') {
+                word += ch;
+                continue;
+            }
+            bool url = word.rfind("http", 0) == 0;
+            bool commit = word.size() >= 32 && word.find_first_not_of("0123456789abcdef") == std::string::npos;
+            if (!word.empty() && !url && !commit) cc += (cc.empty() ? "" : "-") + word;
+            word.clear();
+        }
+    }
+    std::string d = "hipdriver" + std::to_string(drv) + "-amdgpu-" + kmd + "-clang-" + cc;
+    for (char &ch : d)
+        if (ch == ' ' || ch == ':') ch = '_';
+    if (d.size() + 1 > cap) return fail(NT_E_ARG, "nt_hip_platform_details: buffer too small");
+    std::snprintf(buf, cap, "%s", d.c_str());
     return 0;
 }
 

@@ -98,6 +98,7 @@ _SIGS = {
     "nt_hip_device_count": (C.c_int, []),
     "nt_hip_last_error": (C.c_char_p, []),
     "nt_hip_key": (C.c_int, [C.c_char_p, C.c_size_t]),
+    "nt_hip_platform_details": (C.c_int, [C.c_char_p, C.c_size_t]),
     "nt_hip_alloc": (C.c_int, [C.c_size_t, C.POINTER(C.c_void_p)]),
     "nt_hip_free": (C.c_int, [C.c_void_p]),
     "nt_hip_upload": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
@@ -207,6 +208,20 @@ def key() -> str:
     buf = C.create_string_buffer(256)
     _check(_dev().nt_hip_key(buf, 256), "key")
     return buf.value.decode()
+
+
+def platform_details() -> str:
+    """`GpuBackend::platform_details` (gpu/mod.rs:199): the HIP driver, the amdgpu kernel driver
+    release and the compiler that built the code objects."""
+    buf = C.create_string_buffer(512)
+    _check(_dev().nt_hip_platform_details(buf, 512), "platform_details")
+    return buf.value.decode()
+
+
+def platform_key() -> str:
+    """`gpu_platform_key` (gpu/mod.rs:699-704) at the default f32 matmul precision:
+    `key()` followed by `platform_details()`."""
+    return f"{key()}-{platform_details()}"
 
 
 def launches() -> int:

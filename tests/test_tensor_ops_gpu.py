@@ -303,3 +303,20 @@ def test_release_is_stream_ordered():
         got = y.to_numpy()
         assert np.array_equal(got, ops.unary(UnaryOp.EXP, dev(x), Layout([n])).to_numpy())
         assert np.all(z.to_numpy() == np.float32(7.0))
+
+
+def test_key_and_platform_details():
+    """`key` and `platform_details` (gpu/mod.rs:197-199), joined as `gpu_platform_key`
+    (gpu/mod.rs:699-704): stable across calls, no spaces, and a buffer too small is an error."""
+    import ctypes as C
+    import re
+
+    k, d = nr.key(), nr.platform_details()
+    assert re.fullmatch(r"hip-gfx950[^ ]*-hiprt\d+-kernels-[0-9a-f]{16}", k), k
+    assert re.fullmatch(r"hipdriver\d+-amdgpu-[^ ]+-clang-[^ ]+", d), d
+    assert nr.platform_key() == f"{k}-{d}"
+    assert (nr.key(), nr.platform_details()) == (k, d)
+    small = C.create_string_buffer(8)
+    assert nr.lib().nt_hip_platform_details(small, 8) != 0
+    assert "too small" in nr.lib().nt_hip_last_error().decode()
+    print("platform key:", nr.platform_key())
