@@ -9,7 +9,7 @@ library's own stream; the same launches re-reading one input are reported as `wa
 bytes per launch / average launch time against the 8 TB/s HBM peak) and a `cpu_baseline`
 object (the reference's Cpu(Reference) op sequence, restated in oracle/, timed on this host).
 
-`--workload c4s|c2|c3|c3b|c5` measures the other configurations the same way, one JSON line each:
+`--workload c4s|c2|c3|c3b|c5|matmul` measures the other configurations the same way, one JSON line each:
   c4s C4 with one u8 grammar mask [1,V] shared by every row (mask_ld 0);
   c2  decode step, f32 [1,64,1,32000], no mask, tau 0.8: the fused sample + logp;
   c3  PPO scoring, bf16 policy + reference [8,16,512,50304]: logp, reference logp, exact KL,
@@ -18,7 +18,9 @@ object (the reference's Cpu(Reference) op sequence, restated in oracle/, timed o
       of g_logp logp + g_kl KL + g_H H with respect to the logits, in bf16;
   c5  rollout scoring, f32 [4,32,1024,151936] + u8 mask: logp and entropy (nt_hip_rl_score),
       the per-sequence mean log-probability (nt_hip_rl_reduce_tokens) and group-relative
-      advantages over groups of 8 along B (nt_hip_rl_group_advantages, f64 on the device).
+      advantages over groups of 8 along B (nt_hip_rl_group_advantages, f64 on the device);
+  matmul  the general ops' f32 matmul (CpuRef's arithmetic) at the reference's throughput
+      shapes and 4096^3.
 """
 import argparse
 import ctypes as C
@@ -478,6 +480,64 @@ def bench_ops(nr, args):
             "ops": res}
 
 
+VALU_F32_PEAK_TFLOPS = 78.6  # 256 CUs x 4 SIMDs x 16 lanes x 2 flops x 2.4 GHz, one v_fma_f32 per lane
+
+
+def bench_matmul(nr, args):
+    """nt_hip_matmul (GpuBackend::matmul, CpuRef's fma-chain order bit for bit) at the reference's
+    matmul_throughput shapes (src/tensor/tests/gpu/kernels.rs:262-291: A.B 1024^3, A.B 512x512x2048,
+    A.B^T 512x2048x512, A^T.B 512x512x2048) and at 4096^3, on resident f32 operands. The order
+    rules out the matrix cores, so the roofline is the VALU's f32 fma rate without packed
+    instructions (78.6 TFLOP/s)."""
+    from noetic_ops import Layout
+    L = nr.lib()
+    P = lambda t: C.c_void_p(t.ptr)  # noqa: E731
+    rng = np.random.default_rng(args.seed)
+    cases = [("A.B 1024^3", 1024, 1024, 1024, False, False), ("A.B 512x512x2048", 512, 2048, 512, False, False),
+             ("A.B^T 512x2048x512", 512, 512, 2048, False, True), ("A^T.B 512x512x2048", 512, 2048, 512, True, False),
+             ("A.B 4096^3", 4096, 4096, 4096, False, False)]
+    res = {}
+    steps, warmup = min(args.steps, 20), min(args.warmup, 3)
+    for name, m, k, n, ta, tb in cases:
+        a = nr.Tensor.from_numpy(rng.uniform(-2, 2, (k, m) if ta else (m, k)).astype(np.float32))
+        b = nr.Tensor.from_numpy(rng.uniform(-2, 2, (n, k) if tb else (k, n)).astype(np.float32))
+        al = Layout([k, m]).swapped(0, 1) if ta else Layout([m, k])
+        bl = Layout([n, k]).swapped(0, 1) if tb else Layout([k, n])
+        y = nr.Tensor((m, n), "f32")
+        ca, cb = al.c(), bl.c()
+        ck = lambda rc: nr._check(rc, "matmul")  # noqa: E731
+        ms, _ = timed(nr, steps, warmup, lambda i: ck(L.nt_hip_matmul(P(a), C.byref(ca), P(b), C.byref(cb), P(y))))
+        tf = 2.0 * m * k * n / (ms * 1e-3) / 1e12
+        res[name] = {"ms": round(ms, 4), "tflops": round(tf, 2), "frac_of_valu_peak": round(tf / VALU_F32_PEAK_TFLOPS, 4)}
+    top = res["A.B 4096^3"]
+    out = {"metric": "f32 matmul (CpuRef's arithmetic bit for bit) TFLOP/s", "value": top["tflops"],
+           "unit": "TFLOP/s (A.B 4096^3)", "n_gpus": 1, "steps": steps, "warmup": warmup,
+           "ms_per_step": top["ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "f32", "data": "synthetic",
+           "config": {"workload": "matmul: uniform(-2, 2) f32 operands resident on the device, fresh-output-free "
+                                  "(one preallocated output per shape)"},
+           "roofline": {"bound": "valu", "achieved": top["tflops"], "peak": VALU_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": top["frac_of_valu_peak"], "traffic": None,
+                        "note": "the published 157.3 TFLOP/s f32 figure counts matrix-core or packed-f32 "
+                                "instructions; neither keeps the reference's per-output fma chain"},
+           "shapes": res}
+    if args.cpu_rows > 0:
+        import time as _t
+        from oracle import oracle as O
+        a = rng.uniform(-2, 2, (64, 1024)).astype(np.float32)
+        b = rng.uniform(-2, 2, (1024, 1024)).astype(np.float32)
+        reps, t_ref = 0, 0.0
+        while reps < 1 or (t_ref < args.cpu_seconds and reps < 100):
+            t0 = _t.perf_counter()
+            O.matmul(a, b)
+            t_ref += _t.perf_counter() - t0
+            reps += 1
+        out["cpu_baseline"] = {"value": reps * 2.0 * 64 * 1024 * 1024 / t_ref / 1e12, "unit": "TFLOP/s", "cores": 1,
+                               "kind": "port", "cpu": cpu_model(),
+                               "sample": f"{reps} x [64,1024]x[1024,1024] through oracle.c's fmaf chains, one thread"}
+    return out
+
+
 def bench_readout(nr, W, args):
     """What fusing the sampler into the decoder readout could save at C4's decode shape: the readout
     GEMM logits[256, 128256] = h[256, 4096] · W[4096, 128256] in bf16 (torch.matmul, hipBLASLt,
@@ -547,7 +607,8 @@ def main():
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default 200; 20 for c3/c5)")
     ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 20; 3 for c3/c5)")
     ap.add_argument("--seed", type=int, default=2024)
-    ap.add_argument("--workload", default="c4", choices=["c4", "c4s", "c2", "c3", "c3b", "c5", "ops", "readout"])
+    ap.add_argument("--workload", default="c4",
+                    choices=["c4", "c4s", "c2", "c3", "c3b", "c5", "ops", "readout", "matmul"])
     ap.add_argument("--cpu-rows", type=int, default=256, help="rows of the CPU baseline sample (0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="repeat the CPU sample up to this long")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -587,6 +648,8 @@ def main():
         out = bench_score_grad(nr, W, args)
     elif args.workload == "ops":
         out = bench_ops(nr, args)
+    elif args.workload == "matmul":
+        out = bench_matmul(nr, args)
     elif args.workload == "readout":
         out = bench_readout(nr, W, args)
     else:

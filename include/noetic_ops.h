@@ -149,6 +149,14 @@ int nt_hip_index_add(const int32_t *idx, const float *v, int64_t outer, int64_t 
 /* GpuBackend::fill (gpu/mod.rs:190-193): n f32 elements equal to value. */
 int nt_hip_fill(float *out, int64_t n, float value);
 
+/* GpuBackend::matmul (gpu/mod.rs:155-156; the CUDA backend's matmul, cuda/backend.rs:784-830):
+ * the batched product of two f32 views a [..., m, k] and b [..., k, n] of equal rank >= 2, batch
+ * dimensions broadcast where one side is 1, into contiguous out [batch..., m, n]. Every output is
+ * the reference's arithmetic (cuda/kernels.rs:14-20, CpuRef's matrixmultiply order): an fma chain
+ * from zero over k in order, closed every 256 k, the first block's chain the total and each later
+ * block's chain added to it; so the result equals CpuRef's bit for bit. k = 0 gives zeros. */
+int nt_hip_matmul(const float *a, const NtLayout *al, const float *b, const NtLayout *bl, float *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,277 @@
+// Batched f32 matmul of a Device::Hip tensor (GpuBackend::matmul, src/tensor/gpu/mod.rs:155-156),
+// bit for bit the reference's product. The reference fixes the arithmetic of every output
+// (src/tensor/cuda/kernels.rs:14-20, the order of matrixmultiply 0.3.11's sgemm that CpuRef calls
+// per batch, src/tensor/kernels.rs:415-420): an fma chain from zero over k in order, closed every
+// 256 k; the first block's chain is the total and each later block's chain is added to it. That
+// order allows no split of one output's chain over lanes and no matrix-core instruction (an MFMA
+// sums several products before it rounds), so this is a VALU kernel: each of a block's 256
+// threads owns an 8x8 (or 4x4) register tile of outputs and runs their 64 (16) chains side by
+// side, one v_fma_f32 per product, on A and B panels staged through LDS.
+//
+// Layout of a 128x128 block tile: thread (tx, ty) = (tid % 16, tid / 16) owns rows
+// {ty*4 + i, 64 + ty*4 + i} and columns {tx*4 + j, 64 + tx*4 + j} (i, j < 4), so each k step
+// reads its 8 A values and 8 B values as four 16-byte LDS reads (A's are broadcast: a wave spans
+// four ty). The panels are double-buffered (one barrier per 16 k). Workgroups are renumbered so
+// that each of the 8 XCDs (which the hardware deals consecutive workgroups to in turn) works on a
+// contiguous run of tiles, whose A panels then stay in that XCD's L2.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "../../include/noetic_hip.h"
+#include "../../include/noetic_ops.h"
+#include "nt_internal.hpp"
+
+namespace nt {
+namespace {
+
+constexpr int kMmThreads = 256;
+constexpr int kBK = 16;    // k per LDS stage
+constexpr int kKC = 256;   // the chain is closed every kKC k
+constexpr int kMaxBatchDims = NT_MAX_RANK - 2;
+constexpr int kPad = 4;    // LDS row padding (keeps 16-byte alignment, spreads the stores' banks)
+
+struct MatmulP {
+    const float *a, *b;
+    float *c;
+    int64_t a_off, b_off;          // element offsets of batch 0
+    int64_t a_rs, a_cs, b_rs, b_cs;
+    int64_t bshape[kMaxBatchDims]; // the output's batch dimensions
+    int64_t a_bs[kMaxBatchDims];   // per batch dimension: A's stride (0 where A broadcasts)
+    int64_t b_bs[kMaxBatchDims];
+    int64_t blocks;                // batches * tiles_m * tiles_n
+    int32_t m, n, k;
+    int32_t tm, tn;                // tiles along m and n
+    int32_t nbd;                   // batch dimensions
+};
+
+// H = 2: 128x128 tile, 8x8 outputs per thread; H = 1: 64x64 tile, 4x4 per thread.
+// AK: A is read along k (a_cs == 1); otherwise along m. BN: B is read along n (b_cs == 1);
+// otherwise along k. Either way consecutive lanes read consecutive addresses when the view is
+// contiguous along that dimension.
+template <int H, bool AK, bool BN>
+__global__ __launch_bounds__(kMmThreads) void k_matmul(MatmulP p) {
+    constexpr int T = 64 * H;             // tile edge
+    constexpr int LPT = T * kBK / kMmThreads;  // elements of each panel a thread loads per stage
+    __shared__ __attribute__((aligned(16))) float As[2][kBK][T + kPad];
+    __shared__ __attribute__((aligned(16))) float Bs[2][kBK][T + kPad];
+
+    const int tid = threadIdx.x;
+    const int tx = tid % 16, ty = tid / 16;
+    int64_t wg = blockIdx.x;
+    const int64_t full = p.blocks / 8 * 8;
+    if (wg < full) wg = (wg % 8) * (full / 8) + wg / 8;
+    const int64_t per_batch = int64_t(p.tm) * p.tn;
+    const int64_t z = wg / per_batch;
+    const int64_t rem = wg - z * per_batch;
+    const int row0 = int(rem / p.tn) * T, col0 = int(rem % p.tn) * T;
+    int64_t ao = p.a_off, bo = p.b_off;
+    {
+        int64_t q = z;
+        for (int d = p.nbd - 1; d >= 0; --d) {
+            const int64_t i = q % p.bshape[d];
+            q /= p.bshape[d];
+            ao += i * p.a_bs[d];
+            bo += i * p.b_bs[d];
+        }
+    }
+    const float *a = p.a + ao;
+    const float *b = p.b + bo;
+    const int M = p.m, N = p.n, K = p.k;
+
+    float ra[LPT], rb[LPT];
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < LPT; i++) {
+            const int e = tid + kMmThreads * i;
+            int r, kk;
+            if constexpr (AK) {
+                kk = e % kBK;
+                r = e / kBK;
+            } else {
+                r = e % T;
+                kk = e / T;
+            }
+            const int gr = row0 + r, gk = k0 + kk;
+            ra[i] = (gr < M && gk < K) ? a[int64_t(gr) * p.a_rs + int64_t(gk) * p.a_cs] : 0.0f;
+            int cc;
+            if constexpr (BN) {
+                cc = e % T;
+                kk = e / T;
+            } else {
+                kk = e % kBK;
+                cc = e / kBK;
+            }
+            const int gc = col0 + cc, gk2 = k0 + kk;
+            rb[i] = (gc < N && gk2 < K) ? b[int64_t(gk2) * p.b_rs + int64_t(gc) * p.b_cs] : 0.0f;
+        }
+    };
+    auto stash = [&](int s) {
+#pragma unroll
+        for (int i = 0; i < LPT; i++) {
+            const int e = tid + kMmThreads * i;
+            if constexpr (AK) As[s][e % kBK][e / kBK] = ra[i];
+            else As[s][e / T][e % T] = ra[i];
+            if constexpr (BN) Bs[s][e / T][e % T] = rb[i];
+            else Bs[s][e % kBK][e / kBK] = rb[i];
+        }
+    };
+
+    float acc[4 * H][4 * H], tot[4 * H][4 * H];
+#pragma unroll
+    for (int i = 0; i < 4 * H; i++)
+#pragma unroll
+        for (int j = 0; j < 4 * H; j++) {
+            acc[i][j] = 0.0f;
+            tot[i][j] = 0.0f;
+        }
+
+    auto step = [&](int s, int kk) {
+        float av[4 * H], bv[4 * H];
+#pragma unroll
+        for (int h = 0; h < H; h++) {
+            const float4 x = *reinterpret_cast<const float4 *>(&As[s][kk][h * 64 + ty * 4]);
+            const float4 y = *reinterpret_cast<const float4 *>(&Bs[s][kk][h * 64 + tx * 4]);
+            av[4 * h] = x.x;
+            av[4 * h + 1] = x.y;
+            av[4 * h + 2] = x.z;
+            av[4 * h + 3] = x.w;
+            bv[4 * h] = y.x;
+            bv[4 * h + 1] = y.y;
+            bv[4 * h + 2] = y.z;
+            bv[4 * h + 3] = y.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 4 * H; i++)
+#pragma unroll
+            for (int j = 0; j < 4 * H; j++) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+    };
+
+    load(0);
+    stash(0);
+    __syncthreads();
+    int s = 0;
+    for (int k0 = 0; k0 < K; k0 += kBK) {
+        const bool more = k0 + kBK < K;
+        if (more) load(k0 + kBK);  // the next panels' loads are in flight during this stage
+        if (k0 + kBK <= K) {
+#pragma unroll
+            for (int kk = 0; kk < kBK; kk++) step(s, kk);
+        } else {
+            const int kmax = K - k0;
+            for (int kk = 0; kk < kmax; kk++) step(s, kk);
+        }
+        if ((k0 + kBK) % kKC == 0 || !more) {
+            const bool first = k0 < kKC;
+#pragma unroll
+            for (int i = 0; i < 4 * H; i++)
+#pragma unroll
+                for (int j = 0; j < 4 * H; j++) {
+                    tot[i][j] = first ? acc[i][j] : acc[i][j] + tot[i][j];
+                    acc[i][j] = 0.0f;
+                }
+        }
+        if (more) stash(s ^ 1);  // the other buffer was last read before the previous barrier
+        __syncthreads();
+        s ^= 1;
+    }
+
+    float *c = p.c + z * int64_t(M) * N;
+    const bool vec = (N % 4) == 0;
+#pragma unroll
+    for (int hr = 0; hr < H; hr++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = row0 + hr * 64 + ty * 4 + i;
+            if (r >= M) continue;
+            float *crow = c + int64_t(r) * N;
+#pragma unroll
+            for (int hc = 0; hc < H; hc++) {
+                const int c0 = col0 + hc * 64 + tx * 4;
+                const int ri = hr * 4 + i, cj = hc * 4;
+                if (vec && c0 + 3 < N) {
+                    *reinterpret_cast<float4 *>(crow + c0) =
+                        make_float4(tot[ri][cj], tot[ri][cj + 1], tot[ri][cj + 2], tot[ri][cj + 3]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        if (c0 + j < N) crow[c0 + j] = tot[ri][cj + j];
+                }
+            }
+        }
+}
+
+template <int H>
+int launch_matmul(const MatmulP &p, bool ak, bool bn, hipStream_t s) {
+    const dim3 grid(unsigned(p.blocks)), block(kMmThreads);
+    if (ak && bn) hipLaunchKernelGGL((k_matmul<H, true, true>), grid, block, 0, s, p);
+    else if (ak) hipLaunchKernelGGL((k_matmul<H, true, false>), grid, block, 0, s, p);
+    else if (bn) hipLaunchKernelGGL((k_matmul<H, false, true>), grid, block, 0, s, p);
+    else hipLaunchKernelGGL((k_matmul<H, false, false>), grid, block, 0, s, p);
+    return launched("k_matmul");
+}
+
+}  // namespace
+}  // namespace nt
+
+using namespace nt;
+
+extern "C" {
+
+int nt_hip_matmul(const float *a, const NtLayout *al, const float *b, const NtLayout *bl, float *out) {
+    if (!al || !bl) return fail(NT_E_ARG, "matmul: null layout");
+    const int r = al->rank;
+    if (r < 2 || r > NT_MAX_RANK || bl->rank != r || al->shape[r - 1] != bl->shape[r - 2])
+        return fail(NT_E_ARG, "matmul: shapes [" + std::to_string(r) + "-d] do not multiply (rank >= 2, equal "
+                              "ranks, a's last dimension equal to b's second last)");
+    for (int d = 0; d < r; d++)
+        if (al->shape[d] < 0 || bl->shape[d] < 0 || al->strides[d] < 0 || bl->strides[d] < 0 || al->offset < 0 ||
+            bl->offset < 0)
+            return fail(NT_E_ARG, "matmul: negative shape, stride or offset");
+    MatmulP p{};
+    p.nbd = r - 2;
+    int64_t nb = 1;
+    for (int d = 0; d < r - 2; d++) {
+        const int64_t x = al->shape[d], y = bl->shape[d];
+        if (x != y && x != 1 && y != 1)
+            return fail(NT_E_ARG, "matmul: batch dimension " + std::to_string(d) + " does not broadcast (" +
+                                      std::to_string(x) + " against " + std::to_string(y) + ")");
+        p.bshape[d] = x == 1 ? y : x;
+        p.a_bs[d] = x == 1 ? 0 : al->strides[d];
+        p.b_bs[d] = y == 1 ? 0 : bl->strides[d];
+        nb *= p.bshape[d];
+    }
+    const int64_t m = al->shape[r - 2], k = al->shape[r - 1], n = bl->shape[r - 1];
+    if (m >= (int64_t(1) << 31) - 256 || n >= (int64_t(1) << 31) - 256 || k >= (int64_t(1) << 31) - 256)
+        return fail(NT_E_ARG, "matmul: m, k and n must each be below 2^31 - 256");
+    if (nb == 0 || m == 0 || n == 0) return 0;
+    if (!a || !b || !out) return fail(NT_E_ARG, "matmul: null buffer");
+    p.a = a;
+    p.b = b;
+    p.c = out;
+    p.a_off = al->offset;
+    p.b_off = bl->offset;
+    p.a_rs = al->strides[r - 2];
+    p.a_cs = al->strides[r - 1];
+    p.b_rs = bl->strides[r - 2];
+    p.b_cs = bl->strides[r - 1];
+    p.m = int32_t(m);
+    p.n = int32_t(n);
+    p.k = int32_t(k);
+    // 128x128 tiles when they give at least two workgroups per CU of the 256, else 64x64.
+    const int64_t big = nb * ((m + 127) / 128) * ((n + 127) / 128);
+    const int H = big >= 512 ? 2 : 1;
+    const int T = 64 * H;
+    p.tm = int32_t((m + T - 1) / T);
+    p.tn = int32_t((n + T - 1) / T);
+    p.blocks = nb * p.tm * p.tn;
+    if (p.blocks > int64_t(0x7fffffff)) return fail(NT_E_ARG, "matmul: too many output tiles");
+    const bool ak = k == 1 || p.a_cs == 1;
+    const bool bn = n == 1 || p.b_cs == 1;
+    std::unique_lock<std::mutex> lk;
+    if (int rc = enter(&lk)) return rc;
+    return H == 2 ? launch_matmul<2>(p, ak, bn, ctx().stream) : launch_matmul<1>(p, ak, bn, ctx().stream);
+}
+
+}  // extern "C"

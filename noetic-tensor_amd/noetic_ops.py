@@ -8,14 +8,15 @@ meaning (a `Layout` is a view read in place; outputs are fresh, contiguous and r
 `Layout` keeps src/tensor/layout.rs's view operations. There is no CPU fallback: without the built
 library every call raises `HipUnavailable`, as in `noetic_rl`.
 
-`matmul` (and `matmul_half`, `sort_desc`) are off this path and raise `Unsupported`, as the
-reference's trait lets a first slice do.
+`matmul` is the reference's f32 product bit for bit (a VALU kernel: the reference's order of fma
+chains rules out the matrix cores). `matmul_half` is off this path and raises `Unsupported`, as
+the reference's trait lets a backend do.
 """
 from __future__ import annotations
 
 import ctypes as C
 import enum
-from typing import List, Optional, Sequence
+from typing import List, Optional, Sequence, Tuple
 
 import numpy as np
 
@@ -328,8 +329,23 @@ def fill(shape: Sequence[int], value: float) -> Tensor:
     return y
 
 
-def matmul(*_args):
-    raise Unsupported("matmul is off the rl path on this backend")
+def matmul(a: Tensor, al: Layout, b: Tensor, bl: Layout) -> Tuple[Tensor, List[int]]:
+    """GpuBackend::matmul: the batched product of two f32 views (batch dimensions broadcast when
+    1) and the output shape; CpuRef's arithmetic bit for bit (nt_hip_matmul)."""
+    if a.dtype != "f32" or b.dtype != "f32":
+        raise ValueError(f"matmul of {a.dtype} and {b.dtype} storage (f32 operands only)")
+    ash, bsh = list(al.shape), list(bl.shape)
+    r = len(ash)
+    if r < 2 or len(bsh) != r or ash[r - 1] != bsh[r - 2]:
+        raise ValueError(f"matmul {ash} × {bsh}")
+    batch = list(broadcast_shape(ash[:-2], bsh[:-2]))
+    _inside(a, al, "matmul")
+    _inside(b, bl, "matmul")
+    shape = batch + [ash[r - 2], bsh[r - 1]]
+    y = Tensor(shape, "f32")
+    _check(_dev().nt_hip_matmul(C.c_void_p(a.ptr), C.byref(al.c()), C.c_void_p(b.ptr), C.byref(bl.c()),
+                                C.c_void_p(y.ptr)), "matmul")
+    return y, shape
 
 
 # ----------------------------------------------------------------------------------- tensor level
@@ -427,6 +443,16 @@ class DTensor:
 
     def _f32_contiguous(self) -> "DTensor":
         return self._f32().contiguous()
+
+    # -- products
+    def matmul(self, rhs: "DTensor") -> "DTensor":
+        """Tensor::matmul on the device (float.rs:926-960 -> gpu_matmul, gpu/mod.rs:458-470):
+        both operands as f32 views (16-bit ones cast first), batch dimensions broadcast."""
+        if self.dtype != rhs.dtype:
+            raise TypeError(f"matmul of {self.dtype} and {rhs.dtype}")
+        x, y = self._f32(), rhs._f32()
+        st, shape = matmul(x.storage, x.layout, y.storage, y.layout)
+        return DTensor(st, Layout.contiguous(shape))
 
     # -- elementwise
     def unary(self, op: UnaryOp, s: float = 0.0) -> "DTensor":

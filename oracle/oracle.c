@@ -756,3 +756,31 @@ void or_reference_rnd_f32(uint64_t seed, uint64_t inc, int64_t n, float lo, floa
         }
     }
 }
+
+/* ===================================================================== matmul and sort */
+/* One [m, k] x [k, n] product in the reference's arithmetic (src/tensor/cuda/kernels.rs:14-20,
+ * the order of matrixmultiply 0.3.11's sgemm that CpuRef calls per batch,
+ * src/tensor/kernels.rs:415-420): each output is an fmaf chain from zero over k in order, closed
+ * every 256 k; the first block's chain is the total and each later block's chain is added to it.
+ * Element strides a_rs/a_cs and b_rs/b_cs; c is contiguous [m, n]. */
+void or_matmul_f32(const float *a, int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs, int64_t b_cs,
+                   int64_t m, int64_t k, int64_t n, float *c) {
+    /* a row of outputs at a time, each output's chain still in k order (the loops over j only
+     * interleave independent chains) */
+    float *acc = (float *)malloc((size_t)(n > 0 ? n : 1) * sizeof(float));
+    for (int64_t i = 0; i < m; i++) {
+        float *tot = c + i * n;
+        for (int64_t j = 0; j < n; j++) tot[j] = 0.0f;
+        for (int64_t k0 = 0; k0 < k; k0 += 256) {
+            const int64_t k1 = k0 + 256 < k ? k0 + 256 : k;
+            for (int64_t j = 0; j < n; j++) acc[j] = 0.0f;
+            for (int64_t l = k0; l < k1; l++) {
+                const float x = a[i * a_rs + l * a_cs];
+                const float *brow = b + l * b_rs;
+                for (int64_t j = 0; j < n; j++) acc[j] = fmaf(x, brow[j * b_cs], acc[j]);
+            }
+            for (int64_t j = 0; j < n; j++) tot[j] = k0 == 0 ? acc[j] : acc[j] + tot[j];
+        }
+    }
+    free(acc);
+}

@@ -47,6 +47,9 @@ void or_chacha_block(const uint32_t key[8], uint64_t counter, uint64_t stream, u
 void or_chacha_block_rounds(const uint32_t key[8], uint64_t counter, uint64_t stream, int rounds, uint32_t out[16]);
 void or_seed_from_u64(uint64_t state, uint64_t inc, uint8_t seed[32]);
 void or_reference_rnd_f32(uint64_t seed, uint64_t inc, int64_t n, float lo, float hi, float *out);
+/* One f32 product in the reference's matmul order: fmaf chains over k closed every 256. */
+void or_matmul_f32(const float *a, int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs, int64_t b_cs,
+                   int64_t m, int64_t k, int64_t n, float *c);
 void or_chacha_seed(or_chacha *r, const uint8_t seed[32]);
 /* rng::derive(root, label): ChaCha20Rng::from_seed(SHA-256(root.to_le_bytes() || label))
  * (src/rng.rs:9-17). */

@@ -98,6 +98,8 @@ def lib():
         L.or_cpu_sample_logp_invcdf.argtypes = [_c_float_p, C.c_int64, C.c_int64, C.c_double, _c_u8_p, C.c_int64,
                                                 _c_double_p, _c_int64_p, _c_float_p, C.c_int]
         L.or_cpu_sample_logp_invcdf.restype = C.c_int64
+        L.or_matmul_f32.argtypes = [_c_float_p, C.c_int64, C.c_int64, _c_float_p, C.c_int64, C.c_int64, C.c_int64,
+                                    C.c_int64, C.c_int64, _c_float_p]
         _lib = L
     return _lib
 
@@ -342,6 +344,32 @@ def cpuref_log_softmax_f64(x):
 def unrolled_sum(x):
     x = _f32(x)
     return lib().or_unrolled_sum_f32(_ptr(x, _c_float_p), x.size)
+
+
+def matmul(a, b):
+    """Tensor::matmul on Cpu(Reference) (float.rs:926-960, kernels.rs:415-450): a [..., m, k] and
+    b [..., k, n] f32 of equal rank, batch dimensions broadcast where one side is 1; each batch
+    is oracle.c `or_matmul_f32` (fmaf chains over k in order, closed every 256). Views are read
+    through their strides."""
+    a, b = np.asarray(a), np.asarray(b)
+    assert a.dtype == np.float32 and b.dtype == np.float32 and a.ndim == b.ndim >= 2
+    assert a.shape[-1] == b.shape[-2]
+    batch = np.broadcast_shapes(a.shape[:-2], b.shape[:-2])
+    m, k, n = a.shape[-2], a.shape[-1], b.shape[-1]
+    ab = np.broadcast_to(a, batch + (m, k))
+    bb = np.broadcast_to(b, batch + (k, n))
+    out = np.empty(batch + (m, n), np.float32)
+    L = lib()
+    for z in np.ndindex(*batch):
+        x, y = ab[z], bb[z]
+        # the base of each view, with element strides (numpy strides are in bytes; a broadcast
+        # batch has stride 0 and is already folded into the view's base)
+        xs, ys = (s // 4 for s in x.strides), (s // 4 for s in y.strides)
+        (ars, acs), (brs, bcs) = xs, ys
+        xp = C.cast(x.__array_interface__["data"][0], _c_float_p)
+        yp = C.cast(y.__array_interface__["data"][0], _c_float_p)
+        L.or_matmul_f32(xp, ars, acs, yp, brs, bcs, m, k, n, _ptr(out[z], _c_float_p))
+    return out
 
 
 def cpuref_log_softmax(x):

@@ -1,16 +1,16 @@
 """The reference's device op bodies (src/tensor/tests/gpu/ops.rs:52-148) on this build's general
 ops, through the tensor-level dispatch mirror (noetic_ops.DTensor):
-- `body_exact_ops_match_cpu_ref_bit_for_bit`: every case but the three matmuls (matmul is off the
-  rl path here), bit for bit against CpuRef;
+- `body_exact_ops_match_cpu_ref_bit_for_bit`: every case, the three matmuls included, bit for bit
+  against CpuRef;
 - `body_transcendentals_within_4_ulp`: exp, log, sqrt, powf 0.5 and 3, sigmoid within 4 ulp, and
   softmax / log_softmax within 1e-6 relative;
 - `body_nan_max_argmax_and_stable_sort_match_cpu_ref` without its sort (off this path) and
-  `body_deterministic_twice` without its matmul (ops.rs:183-234).
+  `body_deterministic_twice` (ops.rs:183-234).
 Inputs are the reference's own: `t(shape, seed)` = rnd(numel, seed, -2, 2) (ChaCha8 seeded from
 the u64, rand 0.8's f32 gen_range; tests/mod.rs:28-31), restated by the oracle and pinned there
 against the reference's fixture records. CpuRef's values are the checker's: IEEE f32 elementwise
 arithmetic, the eight-partial sum along the last axis and in-order sums along others, the first
-maximum, the binary16 / bfloat16 conversions.
+maximum, the binary16 / bfloat16 conversions, matmul's fma chains closed every 256 k.
 """
 import numpy as np
 import pytest
@@ -118,6 +118,13 @@ def exact_cases(a, b, c):
          lambda x: np.concatenate([x[0], x[2], x[0]], axis=1)),
         ("expand", lambda x: x[1].expand([3, 4, 7]).mul_scalar(2.0),
          lambda x: np.broadcast_to(x[1], (3, 4, 7)) * F(2.0)),
+        ("matmul batched", lambda x: x[0].matmul(x[2].swap_dims(1, 2)),
+         lambda x: O.matmul(x[0], np.swapaxes(x[2], 1, 2))),
+        ("matmul broadcast batch",
+         lambda x: x[0].matmul(x[2].slice([range(0, 1), range(0, 5), range(0, 7)]).swap_dims(1, 2)),
+         lambda x: O.matmul(x[0], np.swapaxes(x[2][0:1, 0:5, 0:7], 1, 2))),
+        ("matmul rank 4 swapped", lambda x: x[0].reshape([3, 5, 1, 7]).matmul(x[2].reshape([3, 1, 7, 5])),
+         lambda x: O.matmul(x[0].reshape(3, 5, 1, 7), x[2].reshape(3, 1, 7, 5))),
         ("gather", lambda x: x[0].gather(2, g_idx), lambda x: np.take_along_axis(x[0], g_idx, axis=2)),
         ("select", lambda x: x[0].select(1, [4, 0, 0, 2]), lambda x: x[0][:, [4, 0, 0, 2], :]),
         ("cast f16 round trip", lambda x: x[0].cast("f16").cast("f32"),
@@ -145,7 +152,7 @@ def test_body_exact_ops_match_cpu_ref_bit_for_bit():
         want = np.asarray(on_cpu(arrays), F).reshape(got.shape) if np.asarray(on_cpu(arrays)).size == got.size \
             else np.asarray(on_cpu(arrays), F)
         assert bits_equal(got, want), f"{name}: {np.count_nonzero(got.ravel() != np.asarray(want).ravel())} differ"
-    print(f"{len(cases)} op cases bit for bit against CpuRef (the reference's three matmul cases are off this path)")
+    print(f"{len(cases)} op cases bit for bit against CpuRef")
 
 
 def ulps(a, b):
@@ -200,11 +207,12 @@ def test_body_nan_max_argmax_match_cpu_ref():
 
 
 def test_body_deterministic_twice():
-    """ops.rs:183-196 without its matmul (off this path): a softmax's lane sums and a sigmoid's
-    means, computed twice, are the same bits."""
+    """ops.rs:183-196: a softmax's lane sums over a matmul and a sigmoid's means, computed twice,
+    are the same bits."""
     def run():
         a = DTensor.from_numpy(t([8, 64, 96], 11))
-        y = ops.softmax(a, 2).sum_dim(1).log()
+        b = DTensor.from_numpy(t([8, 96, 64], 12))
+        y = ops.softmax(a.matmul(b), 2).sum_dim(1).log()
         z = a.sigmoid().mean_dim(2)
         return y.to_numpy(), z.to_numpy()
     (y1, z1), (y2, z2) = run(), run()

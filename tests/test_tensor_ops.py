@@ -113,3 +113,61 @@ def test_op_refusals_before_the_device():
     assert L.nt_hip_reduce_dim(1, p, 1, 0, 1, 1, p) == -1
     assert "empty dimension" in L.nt_hip_last_error().decode()
     assert L.nt_hip_reduce_all(2, p, 4, p) == -4  # NT_E_UNSUPPORTED: argmax over all elements
+    # matmul: shapes that do not multiply, and batches that do not broadcast
+    la, lb = ops.Layout([2, 3]).c(), ops.Layout([4, 2]).c()
+    assert L.nt_hip_matmul(p, C.byref(la), p, C.byref(lb), p) == -1
+    assert "multiply" in L.nt_hip_last_error().decode()
+    la, lb = ops.Layout([2, 1, 2]).c(), ops.Layout([3, 2, 1]).c()
+    assert L.nt_hip_matmul(p, C.byref(la), p, C.byref(lb), p) == -1
+    assert "broadcast" in L.nt_hip_last_error().decode()
+
+
+# ----------------------------------------------------------------------------------- matmul checker
+
+def test_matmul_checker_small_integers_are_exact():
+    """With small integer operands every partial sum is exact in f32, so any order gives the
+    integer product: the checker equals numpy's int64 matmul, with and without chain closures
+    (k up to 600), broadcast batches and transposed views."""
+    rng = np.random.default_rng(3)
+    for (ba, bb, m, k, n) in [((1,), (1,), 7, 5, 3), ((2,), (2,), 13, 256, 9), ((3,), (1,), 17, 600, 11),
+                              ((2, 1), (1, 3), 5, 300, 4)]:
+        a = rng.integers(-8, 9, ba + (m, k)).astype(np.float32)
+        bt = rng.integers(-8, 9, bb + (n, k)).astype(np.float32)
+        b = np.swapaxes(bt, -1, -2)  # a transposed view, read through its strides
+        want = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
+        assert np.array_equal(O.matmul(a, b), want)
+
+
+def test_matmul_checker_closes_the_chain_every_256():
+    """k = 512: A's row is [2^24, 1 x 511] and B's column all ones. The first 256-long chain stays
+    at 2^24 (each +1 rounds back to even), the second chain is 256, and the closure adds them:
+    2^24 + 256. A single 512-long chain would stay at 2^24."""
+    a = np.ones((1, 1, 512), np.float32)
+    a[0, 0, 0] = 2.0 ** 24
+    b = np.ones((1, 512, 1), np.float32)
+    assert O.matmul(a, b)[0, 0, 0] == np.float32(2.0 ** 24 + 256)
+    a[0, 0, 0], a[0, 0, 256] = 1.0, 2.0 ** 24  # 2^24 leads the second chain instead: 255 + 1 then 2^24
+    assert O.matmul(a, b)[0, 0, 0] == np.float32(2.0 ** 24 + 256)
+
+
+def test_matmul_checker_fuses_each_product_in_k_order():
+    """[-1, 1 + 2^-12] . [1, 1 + 2^-12]: the chain is -1, then fma(1 + 2^-12, 1 + 2^-12, -1) =
+    2^-11 + 2^-24 exactly. A rounded product (1 + 2^-11) or the reversed order (round the square
+    first, then add -1) gives 2^-11."""
+    e = np.float32(1 + 2.0 ** -12)
+    a = np.array([[[-1.0, e]]], np.float32)
+    b = np.array([[[1.0], [e]]], np.float32)
+    assert O.matmul(a, b)[0, 0, 0] == np.float32(2.0 ** -11 + 2.0 ** -24)
+    assert O.matmul(a[:, :, ::-1].copy(), b[:, ::-1, :].copy())[0, 0, 0] == np.float32(2.0 ** -11)
+
+
+def test_matmul_checker_within_the_reference_error_bound():
+    """Random [-1, 1] operands: within the reference's bound 2 k eps sum|a||b| of the f64 product
+    (src/tensor/tests/gpu/cuda_only.rs:40-50), for k past several chain closures."""
+    rng = np.random.default_rng(4)
+    a = rng.uniform(-1, 1, (2, 33, 1000)).astype(np.float32)
+    b = rng.uniform(-1, 1, (2, 1000, 17)).astype(np.float32)
+    got = O.matmul(a, b).astype(np.float64)
+    exact = a.astype(np.float64) @ b.astype(np.float64)
+    bound = 2 * 1000 * np.finfo(np.float32).eps * (np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64))
+    assert np.all(np.abs(got - exact) <= bound)
