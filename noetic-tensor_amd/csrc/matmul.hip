@@ -16,6 +16,7 @@
 // contiguous run of tiles, whose A panels then stay in that XCD's L2.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <string>
 
@@ -40,17 +41,23 @@ struct MatmulP {
     int64_t bshape[kMaxBatchDims]; // the output's batch dimensions
     int64_t a_bs[kMaxBatchDims];   // per batch dimension: A's stride (0 where A broadcasts)
     int64_t b_bs[kMaxBatchDims];
-    int64_t blocks;                // batches * tiles_m * tiles_n
+    int64_t blocks;                // splits * batches * tiles_m * tiles_n
+    float *slices;                 // split-k: [ceil(k / 256)][batches * m * n], one per 256-k block
+    int64_t outputs;               // batches * m * n
     int32_t m, n, k;
     int32_t tm, tn;                // tiles along m and n
     int32_t nbd;                   // batch dimensions
+    int32_t kc_per;                // split-k: 256-k blocks per split
 };
 
 // H = 2: 128x128 tile, 8x8 outputs per thread; H = 1: 64x64 tile, 4x4 per thread.
 // AK: A is read along k (a_cs == 1); otherwise along m. BN: B is read along n (b_cs == 1);
 // otherwise along k. Either way consecutive lanes read consecutive addresses when the view is
 // contiguous along that dimension.
-template <int H, bool AK, bool BN>
+// SPLIT: the workgroup covers kc_per 256-k blocks of its tile and writes each block's chain to
+// that block's slice; k_fold then closes the chains in order (the same arithmetic, more
+// workgroups for outputs too few to fill the chip).
+template <int H, bool AK, bool BN, bool SPLIT>
 __global__ __launch_bounds__(kMmThreads) void k_matmul(MatmulP p) {
     constexpr int T = 64 * H;             // tile edge
     constexpr int LPT = T * kBK / kMmThreads;  // elements of each panel a thread loads per stage
@@ -63,8 +70,18 @@ __global__ __launch_bounds__(kMmThreads) void k_matmul(MatmulP p) {
     const int64_t full = p.blocks / 8 * 8;
     if (wg < full) wg = (wg % 8) * (full / 8) + wg / 8;
     const int64_t per_batch = int64_t(p.tm) * p.tn;
-    const int64_t z = wg / per_batch;
-    const int64_t rem = wg - z * per_batch;
+    int64_t zs = wg / per_batch;  // split * batches + batch
+    const int64_t rem = wg - zs * per_batch;
+    int kbeg = 0, kend = p.k;
+    if constexpr (SPLIT) {
+        int64_t nbat = 1;
+        for (int d = 0; d < p.nbd; d++) nbat *= p.bshape[d];
+        const int sp = int(zs / nbat);
+        zs -= int64_t(sp) * nbat;
+        kbeg = sp * p.kc_per * kKC;
+        kend = min(p.k, kbeg + p.kc_per * kKC);
+    }
+    const int64_t z = zs;
     const int row0 = int(rem / p.tn) * T, col0 = int(rem % p.tn) * T;
     int64_t ao = p.a_off, bo = p.b_off;
     {
@@ -118,14 +135,35 @@ __global__ __launch_bounds__(kMmThreads) void k_matmul(MatmulP p) {
         }
     };
 
-    float acc[4 * H][4 * H], tot[4 * H][4 * H];
+    float acc[4 * H][4 * H], tot[SPLIT ? 1 : 4 * H][SPLIT ? 1 : 4 * H];
 #pragma unroll
     for (int i = 0; i < 4 * H; i++)
 #pragma unroll
-        for (int j = 0; j < 4 * H; j++) {
-            acc[i][j] = 0.0f;
-            tot[i][j] = 0.0f;
-        }
+        for (int j = 0; j < 4 * H; j++) acc[i][j] = 0.0f;
+    if constexpr (!SPLIT) {
+#pragma unroll
+        for (int i = 0; i < 4 * H; i++)
+#pragma unroll
+            for (int j = 0; j < 4 * H; j++) tot[i][j] = 0.0f;
+    }
+    // split-k: a closed chain goes to its 256-k block's slice, at the tile's outputs
+    auto put_slice = [&](int kc) {
+        float *sl = p.slices + int64_t(kc) * p.outputs + z * int64_t(p.m) * p.n;
+#pragma unroll
+        for (int hr = 0; hr < H; hr++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int r = row0 + hr * 64 + ty * 4 + i;
+                if (r >= p.m) continue;
+#pragma unroll
+                for (int hc = 0; hc < H; hc++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int cc = col0 + hc * 64 + tx * 4 + j;
+                        if (cc < p.n) sl[int64_t(r) * p.n + cc] = acc[hr * 4 + i][hc * 4 + j];
+                    }
+            }
+    };
 
     auto step = [&](int s, int kk) {
         float av[4 * H], bv[4 * H];
@@ -148,12 +186,12 @@ __global__ __launch_bounds__(kMmThreads) void k_matmul(MatmulP p) {
             for (int j = 0; j < 4 * H; j++) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
     };
 
-    load(0);
+    load(kbeg);
     stash(0);
     __syncthreads();
     int s = 0;
-    for (int k0 = 0; k0 < K; k0 += kBK) {
-        const bool more = k0 + kBK < K;
+    for (int k0 = kbeg; k0 < kend; k0 += kBK) {
+        const bool more = k0 + kBK < kend;
         if (more) load(k0 + kBK);  // the next panels' loads are in flight during this stage
         if (k0 + kBK <= K) {
 #pragma unroll
@@ -163,19 +201,28 @@ __global__ __launch_bounds__(kMmThreads) void k_matmul(MatmulP p) {
             for (int kk = 0; kk < kmax; kk++) step(s, kk);
         }
         if ((k0 + kBK) % kKC == 0 || !more) {
-            const bool first = k0 < kKC;
+            if constexpr (SPLIT) {
+                put_slice(k0 / kKC);
 #pragma unroll
-            for (int i = 0; i < 4 * H; i++)
+                for (int i = 0; i < 4 * H; i++)
 #pragma unroll
-                for (int j = 0; j < 4 * H; j++) {
-                    tot[i][j] = first ? acc[i][j] : acc[i][j] + tot[i][j];
-                    acc[i][j] = 0.0f;
-                }
+                    for (int j = 0; j < 4 * H; j++) acc[i][j] = 0.0f;
+            } else {
+                const bool first = k0 < kKC;
+#pragma unroll
+                for (int i = 0; i < 4 * H; i++)
+#pragma unroll
+                    for (int j = 0; j < 4 * H; j++) {
+                        tot[i][j] = first ? acc[i][j] : acc[i][j] + tot[i][j];
+                        acc[i][j] = 0.0f;
+                    }
+            }
         }
         if (more) stash(s ^ 1);  // the other buffer was last read before the previous barrier
         __syncthreads();
         s ^= 1;
     }
+    if constexpr (SPLIT) return;
 
     float *c = p.c + z * int64_t(M) * N;
     const bool vec = (N % 4) == 0;
@@ -189,26 +236,38 @@ __global__ __launch_bounds__(kMmThreads) void k_matmul(MatmulP p) {
 #pragma unroll
             for (int hc = 0; hc < H; hc++) {
                 const int c0 = col0 + hc * 64 + tx * 4;
-                const int ri = hr * 4 + i, cj = hc * 4;
+                const int ri = SPLIT ? 0 : hr * 4 + i, cj = SPLIT ? 0 : hc * 4;
                 if (vec && c0 + 3 < N) {
                     *reinterpret_cast<float4 *>(crow + c0) =
-                        make_float4(tot[ri][cj], tot[ri][cj + 1], tot[ri][cj + 2], tot[ri][cj + 3]);
+                        make_float4(tot[ri][SPLIT ? 0 : cj], tot[ri][SPLIT ? 0 : cj + 1], tot[ri][SPLIT ? 0 : cj + 2],
+                                    tot[ri][SPLIT ? 0 : cj + 3]);
                 } else {
 #pragma unroll
                     for (int j = 0; j < 4; j++)
-                        if (c0 + j < N) crow[c0 + j] = tot[ri][cj + j];
+                        if (c0 + j < N) crow[c0 + j] = tot[ri][SPLIT ? 0 : cj + j];
                 }
             }
         }
 }
 
-template <int H>
+// Split-k's closing pass: per output, the first 256-k block's chain is the total and each later
+// block's chain is added to it, in order (the unsplit kernel's closure, element for element).
+__global__ void k_fold(const float *slices, int64_t outputs, int nkc, float *out) {
+    for (int64_t o = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; o < outputs;
+         o += int64_t(gridDim.x) * blockDim.x) {
+        float t = slices[o];
+        for (int j = 1; j < nkc; j++) t = slices[int64_t(j) * outputs + o] + t;
+        out[o] = t;
+    }
+}
+
+template <int H, bool SPLIT>
 int launch_matmul(const MatmulP &p, bool ak, bool bn, hipStream_t s) {
     const dim3 grid(unsigned(p.blocks)), block(kMmThreads);
-    if (ak && bn) hipLaunchKernelGGL((k_matmul<H, true, true>), grid, block, 0, s, p);
-    else if (ak) hipLaunchKernelGGL((k_matmul<H, true, false>), grid, block, 0, s, p);
-    else if (bn) hipLaunchKernelGGL((k_matmul<H, false, true>), grid, block, 0, s, p);
-    else hipLaunchKernelGGL((k_matmul<H, false, false>), grid, block, 0, s, p);
+    if (ak && bn) hipLaunchKernelGGL((k_matmul<H, true, true, SPLIT>), grid, block, 0, s, p);
+    else if (ak) hipLaunchKernelGGL((k_matmul<H, true, false, SPLIT>), grid, block, 0, s, p);
+    else if (bn) hipLaunchKernelGGL((k_matmul<H, false, true, SPLIT>), grid, block, 0, s, p);
+    else hipLaunchKernelGGL((k_matmul<H, false, false, SPLIT>), grid, block, 0, s, p);
     return launched("k_matmul");
 }
 
@@ -265,13 +324,38 @@ int nt_hip_matmul(const float *a, const NtLayout *al, const float *b, const NtLa
     const int T = 64 * H;
     p.tm = int32_t((m + T - 1) / T);
     p.tn = int32_t((n + T - 1) / T);
-    p.blocks = nb * p.tm * p.tn;
+    const int64_t tiles = nb * p.tm * p.tn;
+    p.outputs = nb * m * n;
+    // Split k over more workgroups when the tiles alone leave CUs idle: each workgroup takes
+    // kc_per of the ceil(k / 256) chains, so that about 1024 workgroups run in all.
+    const int64_t nkc = (k + kKC - 1) / kKC;
+    int64_t splits = 1;
+    // (the slices take 4 bytes per output and 256-k block; past 1 GiB the tiles run unsplit)
+    if (tiles < 1024 && nkc > 1 && nkc * p.outputs <= (int64_t(1) << 28)) {
+        const int64_t want = (1024 + tiles - 1) / tiles;
+        const int64_t per = (nkc + std::min(want, nkc) - 1) / std::min(want, nkc);
+        p.kc_per = int32_t(per);
+        splits = (nkc + per - 1) / per;
+    }
+    p.blocks = tiles * splits;
     if (p.blocks > int64_t(0x7fffffff)) return fail(NT_E_ARG, "matmul: too many output tiles");
     const bool ak = k == 1 || p.a_cs == 1;
     const bool bn = n == 1 || p.b_cs == 1;
     std::unique_lock<std::mutex> lk;
     if (int rc = enter(&lk)) return rc;
-    return H == 2 ? launch_matmul<2>(p, ak, bn, ctx().stream) : launch_matmul<1>(p, ak, bn, ctx().stream);
+    hipStream_t st = ctx().stream;
+    if (splits == 1) return H == 2 ? launch_matmul<2, false>(p, ak, bn, st) : launch_matmul<1, false>(p, ak, bn, st);
+    void *sl = nullptr;
+    if (int rc = scratch_alloc(size_t(nkc) * size_t(p.outputs) * sizeof(float), &sl)) return rc;
+    p.slices = static_cast<float *>(sl);
+    int rc = H == 2 ? launch_matmul<2, true>(p, ak, bn, st) : launch_matmul<1, true>(p, ak, bn, st);
+    if (!rc) {
+        const int64_t fb = std::min<int64_t>((p.outputs + kMmThreads - 1) / kMmThreads, 4096);
+        hipLaunchKernelGGL(k_fold, dim3(unsigned(fb)), dim3(kMmThreads), 0, st, p.slices, p.outputs, int(nkc), out);
+        rc = launched("k_fold");
+    }
+    const int rf = scratch_release(sl);
+    return rc ? rc : rf;
 }
 
 }  // extern "C"

@@ -32,4 +32,10 @@ int launched(const char *what);
 // nt_hip_free recorded since; on success `*out` holds the lock.
 int enter(std::unique_lock<std::mutex> *out);
 
+// Device scratch for work queued on the library stream, with the context lock held: from the
+// stream-ordered pool when the device has one. scratch_release orders the free after the work
+// queued so far (hipFreeAsync), or, without a pool, records it for the next entry to free.
+int scratch_alloc(size_t bytes, void **out);
+int scratch_release(void *ptr);
+
 }  // namespace nt

@@ -83,6 +83,21 @@ int enter(std::unique_lock<std::mutex> *out) {
     return 0;
 }
 
+int scratch_alloc(size_t bytes, void **out) {
+    *out = nullptr;
+    if (bytes == 0) return 0;
+    if (ctx().pools) return hip_check(hipMallocAsync(out, bytes, ctx().stream), "hipMallocAsync");
+    return hip_check(hipMalloc(out, bytes), "hipMalloc");
+}
+
+int scratch_release(void *ptr) {
+    if (!ptr) return 0;
+    if (ctx().pools) return hip_check(hipFreeAsync(ptr, ctx().stream), "hipFreeAsync");
+    std::lock_guard<std::mutex> pl(g_pending_mu);
+    g_pending.push_back(ptr);
+    return 0;
+}
+
 }  // namespace nt
 
 using namespace nt;

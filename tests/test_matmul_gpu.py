@@ -77,9 +77,20 @@ def test_body_matmul_large_tiles_and_split_k_bit_exact(i, case):
           lambda x, y: O.matmul(SWAP(x) if ta else x, SWAP(y) if tb else y))
 
 
+def test_unsplit_chains_closed_in_registers():
+    """With 1024 tiles or more the workgroups close the 256-k chains themselves (no split-k):
+    both tile sizes, k past one closure."""
+    rng = np.random.default_rng(8)
+    a, b = rng.uniform(-2, 2, (4, 1024, 300)).astype(F), rng.uniform(-2, 2, (4, 300, 1024)).astype(F)
+    check("unsplit 64 tiles [4,1024,300]x[4,300,1024]", a, b, lambda x, y: x.matmul(y), O.matmul)
+    a, b = rng.uniform(-2, 2, (1, 4096, 260)).astype(F), rng.uniform(-2, 2, (1, 260, 4096)).astype(F)
+    check("unsplit 128 tiles [1,4096,260]x[1,260,4096]", a, b, lambda x, y: x.matmul(y), O.matmul)
+
+
 def test_both_tiles_every_orientation_and_offsets():
     """The 128x128 tile (at least 512 tiles) and the 64x64 one, with A read along k and along m and
-    B along n and along k, chains closed inside both; views at odd offsets and strides."""
+    B along n and along k, chains closed inside both (split over workgroups, then folded in
+    order); views at odd offsets and strides."""
     rng = np.random.default_rng(7)
     big_a = rng.uniform(-2, 2, (2, 2048, 264)).astype(F)
     big_b = rng.uniform(-2, 2, (2, 264, 2048)).astype(F)
