@@ -445,6 +445,7 @@ def bench_ops(nr, args):
     idx = nr.Tensor.from_numpy(rng.integers(0, V, (rows, 1)).astype(np.int32))
     y = nr.Tensor((rows, V), "f32")
     yr = nr.Tensor((rows,), "f32")
+    yi = nr.Tensor((rows, V), "i32")
     n = rows * V
     lay = Layout([rows, V]).c()
     mlay = Layout([1, V]).broadcast([rows, V]).c()
@@ -463,6 +464,10 @@ def bench_ops(nr, args):
         "reduce_dim argmax last axis": (lambda: ck(L.nt_hip_reduce_dim(int(ReduceOp.ARGMAX), P(x), rows, V, 1, 1,
                                                                        P(yr))), 4 * n + 4 * rows),
         "gather token logits": (lambda: ck(L.nt_hip_gather(P(x), rows, V, 1, P(idx), 1, P(yr))), 12 * rows),
+        # read each value once, write each value and its I32 position once (the runs and merge
+        # passes in between are the sort's own traffic)
+        "sort_desc of every row (top-p's sort)": (lambda: ck(L.nt_hip_sort_desc(P(x), rows, V, 1, P(y), P(yi))),
+                                                  12 * n),
     }
     res = {}
     steps, warmup = min(args.steps, 50), min(args.warmup, 5)

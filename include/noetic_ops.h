@@ -157,6 +157,14 @@ int nt_hip_fill(float *out, int64_t n, float value);
  * block's chain added to it; so the result equals CpuRef's bit for bit. k = 0 gives zeros. */
 int nt_hip_matmul(const float *a, const NtLayout *al, const float *b, const NtLayout *bl, float *out);
 
+/* GpuBackend::sort_desc (gpu/mod.rs:186-191; CpuRef's order, kernels.rs:374-413): along the
+ * middle of contiguous f32 x [outer, n, inner], descending: every NaN first (all NaNs equal),
+ * then total_cmp (+0 before -0), ties in ascending source position. vals gets the source values
+ * (NaN payloads kept), idx their I32 positions along the lane, both [outer, n, inner]. Every
+ * lane length runs on the device (the CUDA backend sends lanes past 4096 through the host,
+ * cuda/backend.rs:919-937); lanes past 8192 take 16 bytes of scratch per element. */
+int nt_hip_sort_desc(const float *x, int64_t outer, int64_t n, int64_t inner, float *vals, int32_t *idx);
+
 #ifdef __cplusplus
 }
 #endif

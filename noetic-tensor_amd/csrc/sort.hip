@@ -1,0 +1,210 @@
+// Descending sort along the middle of a contiguous f32 [outer, n, inner] of a Device::Hip tensor
+// (GpuBackend::sort_desc, src/tensor/gpu/mod.rs:186-191): the values and their I32 source
+// positions, in CpuRef's order (src/tensor/kernels.rs:374-413, `sort_order`): every NaN above
+// +inf and equal to every other NaN, otherwise total_cmp (+0 above -0), stable (ties keep
+// ascending source position). The CUDA backend sorts lanes of up to 4096 on the device and sends
+// longer ones through the host (cuda/backend.rs:919-937); here every lane length stays on the
+// device.
+//
+// Each element becomes one 64-bit key, (order key << 32) | ~position, so that a plain descending
+// comparison of keys is CpuRef's order with ties broken by position, and no two keys are equal.
+// A lane of up to kSortCap elements is sorted by one workgroup in LDS (bitonic). A longer lane is
+// cut into kSortCap-long runs, each sorted that way into a scratch buffer, and the runs are
+// merged pairwise in global memory (merge path: every thread finds where its kMergeItems outputs
+// start by a binary search along its diagonal, then merges them sequentially) until one run
+// remains. The last step writes each position's source value (NaN payloads kept) and index.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <string>
+
+#include "../../include/noetic_hip.h"
+#include "../../include/noetic_ops.h"
+#include "nt_internal.hpp"
+
+namespace nt {
+namespace {
+
+constexpr int kSortThreads = 1024;
+constexpr int kSortCap = 8192;   // elements one workgroup sorts in LDS (64 KB of keys)
+constexpr int kMergeThreads = 256;
+constexpr int kMergeItems = 8;   // outputs per thread of a merge pass
+
+__device__ __forceinline__ uint64_t sort_key(float v, uint32_t pos) {
+    uint32_t k;
+    if (v != v) {
+        k = 0xffffffffu;  // every NaN, whatever its sign and payload, above +inf
+    } else {
+        const uint32_t b = __float_as_uint(v);
+        k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);  // total_cmp's order as an unsigned key
+    }
+    return (uint64_t(k) << 32) | uint64_t(~pos);
+}
+
+__device__ __forceinline__ uint32_t key_pos(uint64_t c) { return ~uint32_t(c); }
+
+struct SortP {
+    const float *x;
+    float *vals;
+    int32_t *idx;
+    uint64_t *runs;   // [lanes][n] sorted runs (multi-run lanes)
+    int64_t outer, n, inner;
+    int32_t chunks;   // runs per lane
+    int32_t pw;       // power of two >= the longest run (<= kSortCap)
+};
+
+// Sort run `chunk` of lane `lane` in LDS; a lane of one run is written out directly.
+__global__ __launch_bounds__(kSortThreads) void k_sort_runs(SortP p) {
+    __shared__ uint64_t s[kSortCap];
+    const int64_t lane = blockIdx.x / p.chunks;
+    const int chunk = int(blockIdx.x - lane * p.chunks);
+    const int64_t o = lane / p.inner, i = lane - o * p.inner;
+    const int64_t beg = int64_t(chunk) * kSortCap;
+    const int len = int(std::min<int64_t>(kSortCap, p.n - beg));
+    const int P = p.pw;
+    for (int t = threadIdx.x; t < P; t += kSortThreads) {
+        uint64_t c = 0;  // padding: below every real key (the smallest real order key is 0x007fffff)
+        if (t < len) {
+            const int64_t d = beg + t;
+            c = sort_key(p.x[(o * p.n + d) * p.inner + i], uint32_t(d));
+        }
+        s[t] = c;
+    }
+    __syncthreads();
+    for (int k = 2; k <= P; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int t = threadIdx.x; t < P; t += kSortThreads) {
+                const int l = t ^ j;
+                if (l > t) {
+                    const uint64_t a = s[t], b = s[l];
+                    const bool desc = (t & k) == 0;
+                    if (desc ? a < b : a > b) {
+                        s[t] = b;
+                        s[l] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    if (p.chunks == 1) {
+        for (int t = threadIdx.x; t < len; t += kSortThreads) {
+            const uint32_t src = key_pos(s[t]);
+            const int64_t at = (o * p.n + t) * p.inner + i;
+            p.vals[at] = p.x[(o * p.n + src) * p.inner + i];
+            p.idx[at] = int32_t(src);
+        }
+    } else {
+        uint64_t *r = p.runs + lane * p.n + beg;
+        for (int t = threadIdx.x; t < len; t += kSortThreads) r[t] = s[t];
+    }
+}
+
+// One merge pass: in every lane, runs [base, base + w) and [base + w, base + 2w) (clipped to n)
+// into one run of `dst`. If LAST, the merged positions go straight to the outputs.
+template <bool LAST>
+__global__ __launch_bounds__(kMergeThreads) void k_merge(SortP p, const uint64_t *src, uint64_t *dst, int64_t w,
+                                                         int64_t per_lane) {
+    const int64_t g = int64_t(blockIdx.x) * kMergeThreads + threadIdx.x;
+    const int64_t lane = g / per_lane;
+    if (lane >= p.outer * p.inner) return;
+    const int64_t pos = (g - lane * per_lane) * kMergeItems;
+    if (pos >= p.n) return;
+    const int64_t n = p.n;
+    const int64_t base = pos / (2 * w) * (2 * w);
+    const int64_t la = std::min<int64_t>(w, n - base);
+    const int64_t lb = std::max<int64_t>(0, std::min<int64_t>(w, n - base - la));
+    const uint64_t *A = src + lane * n + base;
+    const uint64_t *B = A + la;
+    const int64_t d = pos - base;
+    // co-rank: how many of the first d outputs come from A (keys are distinct: no ties)
+    int64_t lo = std::max<int64_t>(0, d - lb), hi = std::min<int64_t>(d, la);
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (A[mid] > B[d - mid - 1]) lo = mid + 1;
+        else hi = mid;
+    }
+    int64_t ia = lo, ib = d - lo;
+    const int64_t o = lane / p.inner, i = lane - o * p.inner;
+    const int64_t end = std::min<int64_t>(kMergeItems, la + lb - d);
+    for (int64_t q = 0; q < end; q++) {
+        uint64_t c;
+        if (ib >= lb || (ia < la && A[ia] > B[ib])) c = A[ia++];
+        else c = B[ib++];
+        if constexpr (LAST) {
+            const uint32_t s = key_pos(c);
+            const int64_t at = (o * n + pos + q) * p.inner + i;
+            p.vals[at] = p.x[(o * n + s) * p.inner + i];
+            p.idx[at] = int32_t(s);
+        } else {
+            dst[lane * n + pos + q] = c;
+        }
+    }
+}
+
+}  // namespace
+}  // namespace nt
+
+using namespace nt;
+
+extern "C" {
+
+int nt_hip_sort_desc(const float *x, int64_t outer, int64_t n, int64_t inner, float *vals, int32_t *idx) {
+    if (outer < 0 || n < 0 || inner < 0) return fail(NT_E_ARG, "sort_desc: negative lanes");
+    if (n > int64_t(0x7fffffff)) return fail(NT_E_ARG, "sort_desc: a lane longer than 2^31 - 1 (I32 positions)");
+    const int64_t lanes = outer * inner;
+    if (lanes == 0 || n == 0) return 0;
+    if (!x || !vals || !idx) return fail(NT_E_ARG, "sort_desc: null buffer");
+    SortP p{};
+    p.x = x;
+    p.vals = vals;
+    p.idx = idx;
+    p.outer = outer;
+    p.n = n;
+    p.inner = inner;
+    const int64_t chunks = (n + kSortCap - 1) / kSortCap;
+    if (lanes * chunks > int64_t(0x7fffffff)) return fail(NT_E_ARG, "sort_desc: too many lanes");
+    p.chunks = int32_t(chunks);
+    int pw = 1;
+    while (pw < std::min<int64_t>(n, kSortCap)) pw <<= 1;
+    p.pw = pw;
+    std::unique_lock<std::mutex> lk;
+    if (int rc = enter(&lk)) return rc;
+    hipStream_t st = ctx().stream;
+    if (chunks == 1) {
+        hipLaunchKernelGGL(k_sort_runs, dim3(unsigned(lanes)), dim3(kSortThreads), 0, st, p);
+        return launched("k_sort_runs");
+    }
+    void *buf[2] = {nullptr, nullptr};
+    const size_t bytes = size_t(lanes) * size_t(n) * sizeof(uint64_t);
+    if (int rc = scratch_alloc(bytes, &buf[0])) return rc;
+    if (int rc = scratch_alloc(bytes, &buf[1])) {
+        scratch_release(buf[0]);
+        return rc;
+    }
+    p.runs = static_cast<uint64_t *>(buf[0]);
+    hipLaunchKernelGGL(k_sort_runs, dim3(unsigned(lanes * chunks)), dim3(kSortThreads), 0, st, p);
+    int rc = launched("k_sort_runs");
+    const int64_t per_lane = (n + kMergeItems - 1) / kMergeItems;
+    const int64_t blocks = (lanes * per_lane + kMergeThreads - 1) / kMergeThreads;
+    int cur = 0;
+    for (int64_t w = kSortCap; !rc && w < n; w *= 2) {
+        const uint64_t *src = static_cast<const uint64_t *>(buf[cur]);
+        uint64_t *dst = static_cast<uint64_t *>(buf[cur ^ 1]);
+        if (2 * w >= n) {
+            hipLaunchKernelGGL((k_merge<true>), dim3(unsigned(blocks)), dim3(kMergeThreads), 0, st, p, src, dst, w,
+                               per_lane);
+        } else {
+            hipLaunchKernelGGL((k_merge<false>), dim3(unsigned(blocks)), dim3(kMergeThreads), 0, st, p, src, dst, w,
+                               per_lane);
+        }
+        rc = launched("k_merge");
+        cur ^= 1;
+    }
+    const int r0 = scratch_release(buf[0]);
+    const int r1 = scratch_release(buf[1]);
+    return rc ? rc : (r0 ? r0 : r1);
+}
+
+}  // extern "C"

@@ -9,8 +9,9 @@ meaning (a `Layout` is a view read in place; outputs are fresh, contiguous and r
 library every call raises `HipUnavailable`, as in `noetic_rl`.
 
 `matmul` is the reference's f32 product bit for bit (a VALU kernel: the reference's order of fma
-chains rules out the matrix cores). `matmul_half` is off this path and raises `Unsupported`, as
-the reference's trait lets a backend do.
+chains rules out the matrix cores) and `sort_desc` CpuRef's stable descending order on the device
+for every lane length. `matmul_half` is off this path and raises `Unsupported`, as the reference's
+trait lets a backend do.
 """
 from __future__ import annotations
 
@@ -329,6 +330,18 @@ def fill(shape: Sequence[int], value: float) -> Tensor:
     return y
 
 
+def sort_desc(x: Tensor, lanes: Sequence[int]) -> Tuple[Tensor, Tensor]:
+    """GpuBackend::sort_desc: along the middle of contiguous f32 x [outer, n, inner], descending in
+    CpuRef's order (NaN first, total_cmp, stable); the values and their I32 positions."""
+    outer, n, inner = (int(v) for v in lanes)
+    if x.dtype != "f32" or outer * n * inner > x.numel:
+        raise ValueError(f"sort_desc of {x.dtype} storage of {x.numel} elements as {[outer, n, inner]}")
+    vals, idx = Tensor((outer, n, inner), "f32"), Tensor((outer, n, inner), "i32")
+    _check(_dev().nt_hip_sort_desc(C.c_void_p(x.ptr), outer, n, inner, C.c_void_p(vals.ptr), C.c_void_p(idx.ptr)),
+           "sort_desc")
+    return vals, idx
+
+
 def matmul(a: Tensor, al: Layout, b: Tensor, bl: Layout) -> Tuple[Tensor, List[int]]:
     """GpuBackend::matmul: the batched product of two f32 views (batch dimensions broadcast when
     1) and the output shape; CpuRef's arithmetic bit for bit (nt_hip_matmul)."""
@@ -596,6 +609,26 @@ class DTensor:
         out = list(sh)
         out[d] = len(indices)
         return DTensor(y, Layout.contiguous(out))
+
+    def sort_descending_with_indices(self, d: int) -> Tuple["DTensor", np.ndarray]:
+        """Tensor::sort_descending_with_indices on the device (float.rs:1032-1040 ->
+        gpu_sort_desc, gpu/mod.rs:549-561): rank >= 2, a contiguous f32 copy sorted along d; the
+        values and the positions (read back here as int64, as IntTensor::to_vec does)."""
+        if len(self.shape) < 2:
+            raise ValueError("sort needs rank 2 or more")
+        x = self._f32_contiguous()
+        sh = self.shape
+        lanes = (int(np.prod(sh[:d])), sh[d], int(np.prod(sh[d + 1:])))
+        vals, idx = sort_desc(x.storage, lanes)
+        return DTensor(vals, Layout.contiguous(sh)), idx.to_numpy().reshape(sh).astype(np.int64)
+
+    def topk_with_indices(self, k: int, d: int) -> Tuple["DTensor", np.ndarray]:
+        """Tensor::topk_with_indices (float.rs:1070-1080): the first k of the descending sort
+        along d."""
+        v, i = self.sort_descending_with_indices(d)
+        r = [range(0, s) for s in self.shape]
+        r[d] = range(0, k)
+        return DTensor(v.storage, v.layout.narrowed(r)).contiguous(), i[tuple(slice(q.start, q.stop) for q in r)]
 
     def cast(self, to: str) -> "DTensor":
         """gpu_cast: 16-bit through f32 (f32_operand), f32 to 16-bit by the cast kernel."""

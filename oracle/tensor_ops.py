@@ -143,3 +143,20 @@ def correctly_rounded(fn: str, x: float, s: float = 0.0) -> np.float32:
     else:
         r = d ** Decimal(float(s))
     return _nearest_f32(Fraction(r))
+
+
+def sort_order_key(x):
+    """CpuRef's sort_order (kernels.rs:374-388) as an unsigned key per element: every NaN
+    (whatever its sign and payload) one key above +inf, otherwise total_cmp's order, -0 below +0."""
+    b = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    k = np.where(b & 0x80000000, (~b) & 0xFFFFFFFF, b | 0x80000000)
+    return np.where(np.isnan(np.asarray(x, np.float32)), np.uint64(0xFFFFFFFF), k).astype(np.uint64)
+
+
+def sort_desc(x, shape, dim):
+    """sort_desc_with_indices (kernels.rs:390-413): per lane a stable descending sort in
+    sort_order; the values (the source elements, NaN payloads kept) and their int64 positions."""
+    x = np.asarray(x, np.float32).reshape(shape)
+    keys = sort_order_key(x).astype(np.int64)
+    order = np.argsort(-keys, axis=dim, kind="stable")  # ascending -key = descending key, ties by position
+    return np.take_along_axis(x, order, axis=dim), order.astype(np.int64)

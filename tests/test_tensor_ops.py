@@ -171,3 +171,32 @@ def test_matmul_checker_within_the_reference_error_bound():
     exact = a.astype(np.float64) @ b.astype(np.float64)
     bound = 2 * 1000 * np.finfo(np.float32).eps * (np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64))
     assert np.all(np.abs(got - exact) <= bound)
+
+
+# ----------------------------------------------------------------------------------- sort checker
+
+def _sort_order(a, b):
+    """sort_order (kernels.rs:379-388) from the IEEE definitions: NaNs equal and above everything,
+    else by value, and for equal values (only +-0 can differ) -0 below +0."""
+    an, bn = math.isnan(a), math.isnan(b)
+    if an or bn:
+        return 0 if (an and bn) else (1 if an else -1)
+    if a != b:
+        return -1 if a < b else 1
+    sa, sb = math.copysign(1.0, a) < 0, math.copysign(1.0, b) < 0
+    return 0 if sa == sb else (-1 if sa else 1)
+
+
+def test_sort_checker_is_the_stable_sort_order():
+    """The checker's keyed numpy sort equals Python's stable sorted() under sort_order on lanes
+    with ties, +-0, infinities and NaNs of both signs and several payloads."""
+    import functools
+    levels = np.array([-1e9, -0.5, 0.0, -0.0, 0.25, 1.0, np.nan, -1e-45, np.inf, -np.inf, 2.5], np.float32)
+    nans = np.array([0xFFC00000, 0x7F800001, 0x7FC00001], np.uint32).view(np.float32)
+    rng = np.random.default_rng(5)
+    for n in (1, 2, 17, 300):
+        lane = np.concatenate([levels, nans])[rng.integers(0, 14, n)]
+        vals, pos = T.sort_desc(lane[None, :], [1, n], 1)
+        want = sorted(range(n), key=functools.cmp_to_key(lambda i, j: -_sort_order(float(lane[i]), float(lane[j]))))
+        assert list(pos[0]) == want
+        assert np.array_equal(vals[0].view(np.uint32), lane[want].view(np.uint32))
