@@ -4,6 +4,7 @@
 // (src/tensor/cuda/backend.rs:104-264) for a `Device::Hip(i)`.
 #include <hip/hip_runtime.h>
 
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -139,6 +140,17 @@ int nt_hip_claim(int device) {
     if (hipDeviceGetAttribute(&pools, hipDeviceAttributeMemoryPoolsSupported, device) != hipSuccess) {
         (void)hipGetLastError();
         pools = 0;
+    }
+    if (pools) {
+        // Keep freed memory in the pool across synchronisations instead of returning it to the
+        // driver, as the reference does (src/tensor/cuda/backend.rs:207-213): otherwise the first
+        // allocation after every sync maps its memory again.
+        hipMemPool_t pool = nullptr;
+        if (int rc = hip_check(hipDeviceGetDefaultMemPool(&pool, device), "hipDeviceGetDefaultMemPool")) return rc;
+        uint64_t threshold = UINT64_MAX;
+        if (int rc = hip_check(hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &threshold),
+                               "hipMemPoolSetAttribute"))
+            return rc;
     }
     c.device = device;
     c.stream = s;

@@ -12,7 +12,8 @@
 // cut into kSortCap-long runs, each sorted that way into a scratch buffer, and the runs are
 // merged pairwise in global memory (merge path: every thread finds where its kMergeItems outputs
 // start by a binary search along its diagonal, then merges them sequentially) until one run
-// remains. The last step writes each position's source value (NaN payloads kept) and index.
+// remains. The last step writes each position's value, decoded from its key (a NaN is read back
+// from its source to keep the payload), and its index.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -43,6 +44,14 @@ __device__ __forceinline__ uint64_t sort_key(float v, uint32_t pos) {
 }
 
 __device__ __forceinline__ uint32_t key_pos(uint64_t c) { return ~uint32_t(c); }
+
+// The element a key came from: the order key is a bijection of the value's bits except for NaN
+// (every NaN has one key), so only a NaN is read back from x to keep its payload.
+__device__ __forceinline__ float key_value(uint64_t c, const float *x, int64_t at_src) {
+    const uint32_t k = uint32_t(c >> 32);
+    if (k == 0xffffffffu) return x[at_src];
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
 
 struct SortP {
     const float *x;
@@ -90,9 +99,10 @@ __global__ __launch_bounds__(kSortThreads) void k_sort_runs(SortP p) {
     }
     if (p.chunks == 1) {
         for (int t = threadIdx.x; t < len; t += kSortThreads) {
-            const uint32_t src = key_pos(s[t]);
+            const uint64_t c = s[t];
+            const uint32_t src = key_pos(c);
             const int64_t at = (o * p.n + t) * p.inner + i;
-            p.vals[at] = p.x[(o * p.n + src) * p.inner + i];
+            p.vals[at] = key_value(c, p.x, (o * p.n + src) * p.inner + i);
             p.idx[at] = int32_t(src);
         }
     } else {
@@ -135,7 +145,7 @@ __global__ __launch_bounds__(kMergeThreads) void k_merge(SortP p, const uint64_t
         if constexpr (LAST) {
             const uint32_t s = key_pos(c);
             const int64_t at = (o * n + pos + q) * p.inner + i;
-            p.vals[at] = p.x[(o * n + s) * p.inner + i];
+            p.vals[at] = key_value(c, p.x, (o * n + s) * p.inner + i);
             p.idx[at] = int32_t(s);
         } else {
             dst[lane * n + pos + q] = c;
