@@ -4,8 +4,8 @@ ops, through the tensor-level dispatch mirror (noetic_ops.DTensor):
   against CpuRef;
 - `body_transcendentals_within_4_ulp`: exp, log, sqrt, powf 0.5 and 3, sigmoid within 4 ulp, and
   softmax / log_softmax within 1e-6 relative;
-- `body_nan_max_argmax_and_stable_sort_match_cpu_ref` without its sort (off this path) and
-  `body_deterministic_twice` (ops.rs:183-234).
+- `body_nan_max_argmax_and_stable_sort_match_cpu_ref` (its sort half is in tests/test_sort_gpu.py)
+  and `body_deterministic_twice` (ops.rs:183-234).
 Inputs are the reference's own: `t(shape, seed)` = rnd(numel, seed, -2, 2) (ChaCha8 seeded from
 the u64, rand 0.8's f32 gen_range; tests/mod.rs:28-31), restated by the oracle and pinned there
 against the reference's fixture records. CpuRef's values are the checker's: IEEE f32 elementwise
@@ -193,7 +193,7 @@ def test_body_transcendentals_within_4_ulp():
 
 
 def test_body_nan_max_argmax_match_cpu_ref():
-    """ops.rs:219-234 (the sort half is off this path): NaN-propagating max and argmax."""
+    """ops.rs:219-234 (the sort half is tests/test_sort_gpu.py's): NaN-propagating max and argmax."""
     nan = np.nan
     v = np.array([1.0, nan, 5.0, 2.0, nan, 3.0, 9.0, 0.0, 4.0, nan, nan, 1.0, 1.0, 7.0, 7.0, 2.0], F).reshape(4, 4)
     x = DTensor.from_numpy(v)
