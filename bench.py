@@ -514,6 +514,12 @@ def bench_matmul(nr, args):
         ms, _ = timed(nr, steps, warmup, lambda i: ck(L.nt_hip_matmul(P(a), C.byref(ca), P(b), C.byref(cb), P(y))))
         tf = 2.0 * m * k * n / (ms * 1e-3) / 1e12
         res[name] = {"ms": round(ms, 4), "tflops": round(tf, 2), "frac_of_valu_peak": round(tf / VALU_F32_PEAK_TFLOPS, 4)}
+        if name in ("A.B 1024^3", "A.B 4096^3"):
+            ms, _ = timed(nr, steps, warmup,
+                          lambda i: ck(L.nt_hip_matmul_half(P(a), C.byref(ca), P(b), C.byref(cb), P(y))))
+            tf = 2.0 * m * k * n / (ms * 1e-3) / 1e12
+            res["half " + name] = {"ms": round(ms, 4), "tflops": round(tf, 2),
+                                   "frac_of_bf16_mfma_peak": round(tf / 2500.0, 4)}
     top = res["A.B 4096^3"]
     out = {"metric": "f32 matmul (CpuRef's arithmetic bit for bit) TFLOP/s", "value": top["tflops"],
            "unit": "TFLOP/s (A.B 4096^3)", "n_gpus": 1, "steps": steps, "warmup": warmup,

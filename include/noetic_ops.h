@@ -157,6 +157,18 @@ int nt_hip_fill(float *out, int64_t n, float value);
  * block's chain added to it; so the result equals CpuRef's bit for bit. k = 0 gives zeros. */
 int nt_hip_matmul(const float *a, const NtLayout *al, const float *b, const NtLayout *bl, float *out);
 
+/* GpuBackend::matmul_half (gpu/mod.rs:157-162; the CUDA backend's hgemm_bf16_f32acc,
+ * cuda/half_gemm.rs:32-..., backend.rs:750-773): the same batched product of two f32 views with
+ * each operand rounded to bf16 (nearest even) and the products summed in f32 on the matrix cores
+ * (v_mfma_f32_32x32x16_bf16). Compared with a stated tolerance, not byte for byte: within
+ * 2^-21 k sum|a||b| of the rounded operands' exact product (src/tensor/tests/gpu/half_gemm.rs:73-104);
+ * the same bits run to run. */
+int nt_hip_matmul_half(const float *a, const NtLayout *al, const float *b, const NtLayout *bl, float *out);
+/* GpuBackend::half_gemm_key (gpu/mod.rs:163-167; cuda/backend.rs:775-783): the reduced-precision
+ * product's key part, "gemm-bf16-mfma32x32x16-f32acc-kernels-<sha16 of the device sources>",
+ * NUL-terminated into buf. */
+int nt_hip_half_gemm_key(char *buf, size_t cap);
+
 /* GpuBackend::sort_desc (gpu/mod.rs:186-191; CpuRef's order, kernels.rs:374-413): along the
  * middle of contiguous f32 x [outer, n, inner], descending: every NaN first (all NaNs equal),
  * then total_cmp (+0 before -0), ties in ascending source position. vals gets the source values

@@ -18,11 +18,16 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdio>
 #include <string>
 
 #include "../../include/noetic_hip.h"
 #include "../../include/noetic_ops.h"
 #include "nt_internal.hpp"
+
+#ifndef NT_KERNELS_SHA
+#define NT_KERNELS_SHA "unknown"
+#endif
 
 namespace nt {
 namespace {
@@ -261,6 +266,137 @@ __global__ void k_fold(const float *slices, int64_t outputs, int nkc, float *out
     }
 }
 
+// ---------------------------------------------------------------------------- matmul_half
+// The reduced-precision product (GpuBackend::matmul_half, gpu/mod.rs:157-162; the CUDA backend's
+// hgemm_bf16_f32acc, cuda/half_gemm.rs:32-...): f32 operands rounded to bf16 (nearest even) as
+// they are staged, products summed in f32 on the matrix cores. A 256-thread workgroup computes a
+// 128x128 tile: each wave a 64x64 quarter as 2x2 v_mfma_f32_32x32x16_bf16 tiles, over k panels of
+// 32 staged through LDS as bf16 ([row][k] for A, [column][k] for B, so that every MFMA operand
+// is one 16-byte LDS read: lane l takes row or column l % 32 and k 8 (l / 32) .. 8 (l / 32) + 7).
+// The next panel's f32 loads are issued before the current panel's MFMAs.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+constexpr int kHT = 128;  // tile edge
+constexpr int kHK = 32;   // k per panel
+constexpr int kHPad = 8;  // bf16 padding per LDS row (rows stay 16-byte aligned)
+constexpr int kHLoads = kHT * kHK / kMmThreads;  // f32 loads per operand and thread per panel
+
+__device__ __forceinline__ uint16_t bf16_bits(float x) {
+    uint32_t r;
+    asm("v_cvt_pk_bf16_f32 %0, %1, %1" : "=v"(r) : "v"(x));
+    return uint16_t(r);
+}
+
+template <bool AK, bool BN>
+__global__ __launch_bounds__(kMmThreads) void k_matmul_half(MatmulP p) {
+    __shared__ __attribute__((aligned(16))) uint16_t As[kHT][kHK + kHPad];
+    __shared__ __attribute__((aligned(16))) uint16_t Bs[kHT][kHK + kHPad];
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+    int64_t wg = blockIdx.x;
+    const int64_t full = p.blocks / 8 * 8;
+    if (wg < full) wg = (wg % 8) * (full / 8) + wg / 8;
+    const int64_t per_batch = int64_t(p.tm) * p.tn;
+    const int64_t z = wg / per_batch;
+    const int64_t rem = wg - z * per_batch;
+    const int row0 = int(rem / p.tn) * kHT, col0 = int(rem % p.tn) * kHT;
+    int64_t ao = p.a_off, bo = p.b_off;
+    {
+        int64_t q = z;
+        for (int d = p.nbd - 1; d >= 0; --d) {
+            const int64_t i = q % p.bshape[d];
+            q /= p.bshape[d];
+            ao += i * p.a_bs[d];
+            bo += i * p.b_bs[d];
+        }
+    }
+    const float *a = p.a + ao;
+    const float *b = p.b + bo;
+    const int M = p.m, N = p.n, K = p.k;
+
+    float ra[kHLoads], rb[kHLoads];
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < kHLoads; i++) {
+            const int e = tid + kMmThreads * i;
+            int r, kk;
+            if constexpr (AK) {
+                kk = e % kHK;
+                r = e / kHK;
+            } else {
+                r = e % kHT;
+                kk = e / kHT;
+            }
+            const int gr = row0 + r, gk = k0 + kk;
+            ra[i] = (gr < M && gk < K) ? a[int64_t(gr) * p.a_rs + int64_t(gk) * p.a_cs] : 0.0f;
+            int cc;
+            if constexpr (BN) {
+                cc = e % kHT;
+                kk = e / kHT;
+            } else {
+                kk = e % kHK;
+                cc = e / kHK;
+            }
+            const int gc = col0 + cc, gk2 = k0 + kk;
+            rb[i] = (gc < N && gk2 < K) ? b[int64_t(gk2) * p.b_rs + int64_t(gc) * p.b_cs] : 0.0f;
+        }
+    };
+    auto stash = [&]() {
+#pragma unroll
+        for (int i = 0; i < kHLoads; i++) {
+            const int e = tid + kMmThreads * i;
+            if constexpr (AK) As[e / kHK][e % kHK] = bf16_bits(ra[i]);
+            else As[e % kHT][e / kHT] = bf16_bits(ra[i]);
+            if constexpr (BN) Bs[e % kHT][e / kHT] = bf16_bits(rb[i]);
+            else Bs[e / kHK][e % kHK] = bf16_bits(rb[i]);
+        }
+    };
+
+    f32x16_t acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[i][j][v] = 0.0f;
+    const int wm = (wave / 2) * 64, wn = (wave % 2) * 64;
+    const int fr = lane % 32, fk = 8 * (lane / 32);
+
+    load(0);
+    for (int k0 = 0; k0 < K; k0 += kHK) {
+        stash();
+        __syncthreads();
+        if (k0 + kHK < K) load(k0 + kHK);  // in flight during this panel's MFMAs
+#pragma unroll
+        for (int ks = 0; ks < kHK; ks += 16) {
+            bf16x8_t af[2], bf[2];
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                af[t] = *reinterpret_cast<const bf16x8_t *>(&As[wm + t * 32 + fr][ks + fk]);
+                bf[t] = *reinterpret_cast<const bf16x8_t *>(&Bs[wn + t * 32 + fr][ks + fk]);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+
+    float *c = p.c + z * int64_t(M) * N;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int col = col0 + wn + j * 32 + fr;
+            if (col >= N) continue;
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int row = row0 + wm + i * 32 + 8 * (v / 4) + 4 * (lane / 32) + (v % 4);
+                if (row < M) c[int64_t(row) * N + col] = acc[i][j][v];
+            }
+        }
+}
+
 template <int H, bool SPLIT>
 int launch_matmul(const MatmulP &p, bool ak, bool bn, hipStream_t s) {
     const dim3 grid(unsigned(p.blocks)), block(kMmThreads);
@@ -356,6 +492,72 @@ int nt_hip_matmul(const float *a, const NtLayout *al, const float *b, const NtLa
     }
     const int rf = scratch_release(sl);
     return rc ? rc : rf;
+}
+
+int nt_hip_matmul_half(const float *a, const NtLayout *al, const float *b, const NtLayout *bl, float *out) {
+    if (!al || !bl) return fail(NT_E_ARG, "matmul_half: null layout");
+    const int r = al->rank;
+    if (r < 2 || r > NT_MAX_RANK || bl->rank != r || al->shape[r - 1] != bl->shape[r - 2])
+        return fail(NT_E_ARG, "matmul_half: shapes [" + std::to_string(r) + "-d] do not multiply (rank >= 2, equal "
+                              "ranks, a's last dimension equal to b's second last)");
+    for (int d = 0; d < r; d++)
+        if (al->shape[d] < 0 || bl->shape[d] < 0 || al->strides[d] < 0 || bl->strides[d] < 0 || al->offset < 0 ||
+            bl->offset < 0)
+            return fail(NT_E_ARG, "matmul_half: negative shape, stride or offset");
+    MatmulP p{};
+    p.nbd = r - 2;
+    int64_t nb = 1;
+    for (int d = 0; d < r - 2; d++) {
+        const int64_t x = al->shape[d], y = bl->shape[d];
+        if (x != y && x != 1 && y != 1)
+            return fail(NT_E_ARG, "matmul_half: batch dimension " + std::to_string(d) + " does not broadcast (" +
+                                      std::to_string(x) + " against " + std::to_string(y) + ")");
+        p.bshape[d] = x == 1 ? y : x;
+        p.a_bs[d] = x == 1 ? 0 : al->strides[d];
+        p.b_bs[d] = y == 1 ? 0 : bl->strides[d];
+        nb *= p.bshape[d];
+    }
+    const int64_t m = al->shape[r - 2], k = al->shape[r - 1], n = bl->shape[r - 1];
+    if (m >= (int64_t(1) << 31) - 256 || n >= (int64_t(1) << 31) - 256 || k >= (int64_t(1) << 31) - 256)
+        return fail(NT_E_ARG, "matmul_half: m, k and n must each be below 2^31 - 256");
+    if (nb == 0 || m == 0 || n == 0) return 0;
+    if (!a || !b || !out) return fail(NT_E_ARG, "matmul_half: null buffer");
+    p.a = a;
+    p.b = b;
+    p.c = out;
+    p.a_off = al->offset;
+    p.b_off = bl->offset;
+    p.a_rs = al->strides[r - 2];
+    p.a_cs = al->strides[r - 1];
+    p.b_rs = bl->strides[r - 2];
+    p.b_cs = bl->strides[r - 1];
+    p.m = int32_t(m);
+    p.n = int32_t(n);
+    p.k = int32_t(k);
+    p.tm = int32_t((m + kHT - 1) / kHT);
+    p.tn = int32_t((n + kHT - 1) / kHT);
+    p.blocks = nb * p.tm * p.tn;
+    if (p.blocks > int64_t(0x7fffffff)) return fail(NT_E_ARG, "matmul_half: too many output tiles");
+    const bool ak = k == 1 || p.a_cs == 1;
+    const bool bn = n == 1 || p.b_cs == 1;
+    std::unique_lock<std::mutex> lk;
+    if (int rc = enter(&lk)) return rc;
+    hipStream_t st = ctx().stream;
+    const dim3 grid(unsigned(p.blocks)), block(kMmThreads);
+    if (ak && bn) hipLaunchKernelGGL((k_matmul_half<true, true>), grid, block, 0, st, p);
+    else if (ak) hipLaunchKernelGGL((k_matmul_half<true, false>), grid, block, 0, st, p);
+    else if (bn) hipLaunchKernelGGL((k_matmul_half<false, true>), grid, block, 0, st, p);
+    else hipLaunchKernelGGL((k_matmul_half<false, false>), grid, block, 0, st, p);
+    return launched("k_matmul_half");
+}
+
+int nt_hip_half_gemm_key(char *buf, size_t cap) {
+    if (!buf || cap == 0) return fail(NT_E_ARG, "nt_hip_half_gemm_key: empty buffer");
+    std::string sha(NT_KERNELS_SHA);
+    const std::string key = "gemm-bf16-mfma32x32x16-f32acc-kernels-" + sha.substr(0, 16);
+    if (key.size() + 1 > cap) return fail(NT_E_ARG, "nt_hip_half_gemm_key: buffer too small");
+    std::snprintf(buf, cap, "%s", key.c_str());
+    return 0;
 }
 
 }  // extern "C"

@@ -9,9 +9,9 @@ meaning (a `Layout` is a view read in place; outputs are fresh, contiguous and r
 library every call raises `HipUnavailable`, as in `noetic_rl`.
 
 `matmul` is the reference's f32 product bit for bit (a VALU kernel: the reference's order of fma
-chains rules out the matrix cores) and `sort_desc` CpuRef's stable descending order on the device
-for every lane length. `matmul_half` is off this path and raises `Unsupported`, as the reference's
-trait lets a backend do.
+chains rules out the matrix cores), `matmul_half` its reduced-precision product on the matrix cores
+(bf16 operands, f32 accumulation), and `sort_desc` CpuRef's stable descending order on the device
+for every lane length.
 """
 from __future__ import annotations
 
@@ -342,9 +342,18 @@ def sort_desc(x: Tensor, lanes: Sequence[int]) -> Tuple[Tensor, Tensor]:
     return vals, idx
 
 
-def matmul(a: Tensor, al: Layout, b: Tensor, bl: Layout) -> Tuple[Tensor, List[int]]:
-    """GpuBackend::matmul: the batched product of two f32 views (batch dimensions broadcast when
-    1) and the output shape; CpuRef's arithmetic bit for bit (nt_hip_matmul)."""
+class MatmulPrecision(enum.Enum):
+    """precision::MatmulPrecision: F32 (CpuRef's bits) or Half (bf16 operands on the matrix cores,
+    f32 accumulation)."""
+    F32 = "f32"
+    HALF = "half"
+
+
+def matmul(a: Tensor, al: Layout, b: Tensor, bl: Layout,
+           precision: MatmulPrecision = MatmulPrecision.F32) -> Tuple[Tensor, List[int]]:
+    """GpuBackend::matmul (or matmul_half with MatmulPrecision.HALF): the batched product of two f32
+    views (batch dimensions broadcast when 1) and the output shape; at F32 CpuRef's arithmetic bit
+    for bit (nt_hip_matmul), at HALF bf16 operands with f32 accumulation (nt_hip_matmul_half)."""
     if a.dtype != "f32" or b.dtype != "f32":
         raise ValueError(f"matmul of {a.dtype} and {b.dtype} storage (f32 operands only)")
     ash, bsh = list(al.shape), list(bl.shape)
@@ -356,9 +365,16 @@ def matmul(a: Tensor, al: Layout, b: Tensor, bl: Layout) -> Tuple[Tensor, List[i
     _inside(b, bl, "matmul")
     shape = batch + [ash[r - 2], bsh[r - 1]]
     y = Tensor(shape, "f32")
-    _check(_dev().nt_hip_matmul(C.c_void_p(a.ptr), C.byref(al.c()), C.c_void_p(b.ptr), C.byref(bl.c()),
-                                C.c_void_p(y.ptr)), "matmul")
+    fn = _dev().nt_hip_matmul_half if precision == MatmulPrecision.HALF else _dev().nt_hip_matmul
+    _check(fn(C.c_void_p(a.ptr), C.byref(al.c()), C.c_void_p(b.ptr), C.byref(bl.c()), C.c_void_p(y.ptr)), "matmul")
     return y, shape
+
+
+def half_gemm_key() -> str:
+    """GpuBackend::half_gemm_key: the reduced-precision product's key part."""
+    buf = C.create_string_buffer(256)
+    _check(_dev().nt_hip_half_gemm_key(buf, 256), "half_gemm_key")
+    return buf.value.decode()
 
 
 # ----------------------------------------------------------------------------------- tensor level
@@ -461,10 +477,14 @@ class DTensor:
     def matmul(self, rhs: "DTensor") -> "DTensor":
         """Tensor::matmul on the device (float.rs:926-960 -> gpu_matmul, gpu/mod.rs:458-470):
         both operands as f32 views (16-bit ones cast first), batch dimensions broadcast."""
+        return self.matmul_with(rhs, MatmulPrecision.F32)
+
+    def matmul_with(self, rhs: "DTensor", precision: MatmulPrecision) -> "DTensor":
+        """Tensor::matmul_with (float.rs:934-944): the product at a named precision."""
         if self.dtype != rhs.dtype:
             raise TypeError(f"matmul of {self.dtype} and {rhs.dtype}")
         x, y = self._f32(), rhs._f32()
-        st, shape = matmul(x.storage, x.layout, y.storage, y.layout)
+        st, shape = matmul(x.storage, x.layout, y.storage, y.layout, precision)
         return DTensor(st, Layout.contiguous(shape))
 
     # -- elementwise

@@ -143,6 +143,8 @@ _SIGS = {
     "nt_hip_index_add": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_void_p]),
     "nt_hip_fill": (C.c_int, [C.c_void_p, C.c_int64, C.c_float]),
     "nt_hip_matmul": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "nt_hip_matmul_half": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "nt_hip_half_gemm_key": (C.c_int, [C.c_char_p, C.c_size_t]),
     "nt_hip_sort_desc": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p]),
     # noetic_rng.h
     "nt_rng_derive": (C.c_int, [C.POINTER(NtRng), C.c_uint64, C.c_char_p, C.c_size_t]),
