@@ -53,6 +53,7 @@ struct MatmulP {
     int32_t tm, tn;                // tiles along m and n
     int32_t nbd;                   // batch dimensions
     int32_t kc_per;                // split-k: 256-k blocks per split
+    int32_t avec, bvec;            // matmul_half: the operand may be staged with 16-byte loads
 };
 
 // H = 2: 128x128 tile, 8x8 outputs per thread; H = 1: 64x64 tile, 4x4 per thread.
@@ -273,7 +274,10 @@ __global__ void k_fold(const float *slices, int64_t outputs, int nkc, float *out
 // 128x128 tile: each wave a 64x64 quarter as 2x2 v_mfma_f32_32x32x16_bf16 tiles, over k panels of
 // 32 staged through LDS as bf16 ([row][k] for A, [column][k] for B, so that every MFMA operand
 // is one 16-byte LDS read: lane l takes row or column l % 32 and k 8 (l / 32) .. 8 (l / 32) + 7).
-// The next panel's f32 loads are issued before the current panel's MFMAs.
+// The next panel's f32 loads are issued before the current panel's MFMAs. Interior panels of an
+// operand whose view is contiguous along one axis (16-byte aligned) are staged four values per
+// load: along k they go to LDS as they are, along m or n each thread loads a 4x4 block and
+// transposes it in registers, so that every LDS store writes four bf16 of one row.
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 constexpr int kHT = 128;  // tile edge
@@ -314,7 +318,45 @@ __global__ __launch_bounds__(kMmThreads) void k_matmul_half(MatmulP p) {
     const int M = p.m, N = p.n, K = p.k;
 
     float ra[kHLoads], rb[kHLoads];
+    // 16-byte staging for this panel? (an interior panel of a vector-eligible view)
+    auto vec_a = [&](int k0) { return p.avec && row0 + kHT <= M && k0 + kHK <= K; };
+    auto vec_b = [&](int k0) { return p.bvec && col0 + kHT <= N && k0 + kHK <= K; };
     auto load = [&](int k0) {
+        if (vec_a(k0)) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                float4 v;
+                if constexpr (AK) {  // along k: group g covers row g / 8, k (g % 8) * 4 .. + 3
+                    const int g = tid + kMmThreads * q;
+                    v = *reinterpret_cast<const float4 *>(a + int64_t(row0 + g / 8) * p.a_rs + k0 + (g % 8) * 4);
+                } else {  // along m: rows (tid % 32) * 4 .. + 3 at k (tid / 32) * 4 + q
+                    v = *reinterpret_cast<const float4 *>(a + row0 + (tid % 32) * 4 +
+                                                          int64_t(k0 + (tid / 32) * 4 + q) * p.a_cs);
+                }
+                ra[4 * q] = v.x;
+                ra[4 * q + 1] = v.y;
+                ra[4 * q + 2] = v.z;
+                ra[4 * q + 3] = v.w;
+            }
+        }
+        if (vec_b(k0)) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                float4 v;
+                if constexpr (BN) {  // along n: columns (tid % 32) * 4 .. + 3 at k (tid / 32) * 4 + q
+                    v = *reinterpret_cast<const float4 *>(b + int64_t(k0 + (tid / 32) * 4 + q) * p.b_rs + col0 +
+                                                          (tid % 32) * 4);
+                } else {  // along k: group g covers column g / 8, k (g % 8) * 4 .. + 3
+                    const int g = tid + kMmThreads * q;
+                    v = *reinterpret_cast<const float4 *>(b + int64_t(col0 + g / 8) * p.b_cs + k0 + (g % 8) * 4);
+                }
+                rb[4 * q] = v.x;
+                rb[4 * q + 1] = v.y;
+                rb[4 * q + 2] = v.z;
+                rb[4 * q + 3] = v.w;
+            }
+        }
+        const bool sa = !vec_a(k0), sb = !vec_b(k0);
 #pragma unroll
         for (int i = 0; i < kHLoads; i++) {
             const int e = tid + kMmThreads * i;
@@ -327,7 +369,7 @@ __global__ __launch_bounds__(kMmThreads) void k_matmul_half(MatmulP p) {
                 kk = e / kHT;
             }
             const int gr = row0 + r, gk = k0 + kk;
-            ra[i] = (gr < M && gk < K) ? a[int64_t(gr) * p.a_rs + int64_t(gk) * p.a_cs] : 0.0f;
+            if (sa) ra[i] = (gr < M && gk < K) ? a[int64_t(gr) * p.a_rs + int64_t(gk) * p.a_cs] : 0.0f;
             int cc;
             if constexpr (BN) {
                 cc = e % kHT;
@@ -337,17 +379,56 @@ __global__ __launch_bounds__(kMmThreads) void k_matmul_half(MatmulP p) {
                 cc = e / kHK;
             }
             const int gc = col0 + cc, gk2 = k0 + kk;
-            rb[i] = (gc < N && gk2 < K) ? b[int64_t(gk2) * p.b_rs + int64_t(gc) * p.b_cs] : 0.0f;
+            if (sb) rb[i] = (gc < N && gk2 < K) ? b[int64_t(gk2) * p.b_rs + int64_t(gc) * p.b_cs] : 0.0f;
         }
     };
-    auto stash = [&]() {
+    // four bf16 of one LDS row (k .. k + 3) in one 8-byte store
+    auto put4 = [](uint16_t *dst, float x0, float x1, float x2, float x3) {
+        uint32_t lo, hi;
+        asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(lo) : "v"(x0), "v"(x1));
+        asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(hi) : "v"(x2), "v"(x3));
+        *reinterpret_cast<uint2 *>(dst) = make_uint2(lo, hi);
+    };
+    auto stash = [&](int k0) {
+        if (vec_a(k0)) {
+            if constexpr (AK) {
 #pragma unroll
-        for (int i = 0; i < kHLoads; i++) {
-            const int e = tid + kMmThreads * i;
-            if constexpr (AK) As[e / kHK][e % kHK] = bf16_bits(ra[i]);
-            else As[e % kHT][e / kHT] = bf16_bits(ra[i]);
-            if constexpr (BN) Bs[e % kHT][e / kHT] = bf16_bits(rb[i]);
-            else Bs[e / kHK][e % kHK] = bf16_bits(rb[i]);
+                for (int q = 0; q < 4; q++) {
+                    const int g = tid + kMmThreads * q;
+                    put4(&As[g / 8][(g % 8) * 4], ra[4 * q], ra[4 * q + 1], ra[4 * q + 2], ra[4 * q + 3]);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++)  // row (tid % 32) * 4 + j, k (tid / 32) * 4 .. + 3
+                    put4(&As[(tid % 32) * 4 + j][(tid / 32) * 4], ra[j], ra[4 + j], ra[8 + j], ra[12 + j]);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kHLoads; i++) {
+                const int e = tid + kMmThreads * i;
+                if constexpr (AK) As[e / kHK][e % kHK] = bf16_bits(ra[i]);
+                else As[e % kHT][e / kHT] = bf16_bits(ra[i]);
+            }
+        }
+        if (vec_b(k0)) {
+            if constexpr (BN) {
+#pragma unroll
+                for (int j = 0; j < 4; j++)  // column (tid % 32) * 4 + j, k (tid / 32) * 4 .. + 3
+                    put4(&Bs[(tid % 32) * 4 + j][(tid / 32) * 4], rb[j], rb[4 + j], rb[8 + j], rb[12 + j]);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int g = tid + kMmThreads * q;
+                    put4(&Bs[g / 8][(g % 8) * 4], rb[4 * q], rb[4 * q + 1], rb[4 * q + 2], rb[4 * q + 3]);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kHLoads; i++) {
+                const int e = tid + kMmThreads * i;
+                if constexpr (BN) Bs[e % kHT][e / kHT] = bf16_bits(rb[i]);
+                else Bs[e / kHK][e % kHK] = bf16_bits(rb[i]);
+            }
         }
     };
 
@@ -363,7 +444,7 @@ __global__ __launch_bounds__(kMmThreads) void k_matmul_half(MatmulP p) {
 
     load(0);
     for (int k0 = 0; k0 < K; k0 += kHK) {
-        stash();
+        stash(k0);
         __syncthreads();
         if (k0 + kHK < K) load(k0 + kHK);  // in flight during this panel's MFMAs
 #pragma unroll
@@ -540,6 +621,18 @@ int nt_hip_matmul_half(const float *a, const NtLayout *al, const float *b, const
     if (p.blocks > int64_t(0x7fffffff)) return fail(NT_E_ARG, "matmul_half: too many output tiles");
     const bool ak = k == 1 || p.a_cs == 1;
     const bool bn = n == 1 || p.b_cs == 1;
+    // 16-byte staging: the view contiguous along its read axis, the other stride, the offsets of
+    // every batch and the base address all multiples of 4 elements / 16 bytes
+    auto batch_aligned = [&](const int64_t *bs, int64_t off, const float *base) {
+        if (off % 4 != 0 || (reinterpret_cast<uintptr_t>(base) & 15) != 0) return false;
+        for (int d = 0; d < r - 2; d++)
+            if (bs[d] % 4 != 0) return false;
+        return true;
+    };
+    const bool a_ok = batch_aligned(p.a_bs, p.a_off, a);
+    const bool b_ok = batch_aligned(p.b_bs, p.b_off, b);
+    p.avec = a_ok && (ak ? (p.a_cs == 1 && p.a_rs % 4 == 0) : (p.a_rs == 1 && p.a_cs % 4 == 0));
+    p.bvec = b_ok && (bn ? (p.b_cs == 1 && p.b_rs % 4 == 0) : (p.b_rs == 1 && p.b_cs % 4 == 0));
     std::unique_lock<std::mutex> lk;
     if (int rc = enter(&lk)) return rc;
     hipStream_t st = ctx().stream;
