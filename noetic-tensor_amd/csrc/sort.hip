@@ -8,7 +8,8 @@
 //
 // Each element becomes one 64-bit key, (order key << 32) | ~position, so that a plain descending
 // comparison of keys is CpuRef's order with ties broken by position, and no two keys are equal.
-// A lane of up to kSortCap elements is sorted by one workgroup in LDS (bitonic). A longer lane is
+// A lane of up to kSortCap elements is sorted by one workgroup (bitonic, the keys in registers,
+// LDS only for exchanges between waves). A longer lane is
 // cut into kSortCap-long runs, each sorted that way into a scratch buffer, and the runs are
 // merged pairwise in global memory (merge path: every thread finds where its kMergeItems outputs
 // start by a binary search along its diagonal, then merges them sequentially) until one run
@@ -31,6 +32,7 @@ constexpr int kSortThreads = 1024;
 constexpr int kSortCap = 8192;   // elements one workgroup sorts in LDS (64 KB of keys)
 constexpr int kMergeThreads = 256;
 constexpr int kMergeItems = 8;   // outputs per thread of a merge pass
+constexpr int kWaveSize = 64;
 
 __device__ __forceinline__ uint64_t sort_key(float v, uint32_t pos) {
     uint32_t k;
@@ -63,51 +65,89 @@ struct SortP {
     int32_t pw;       // power of two >= the longest run (<= kSortCap)
 };
 
-// Sort run `chunk` of lane `lane` in LDS; a lane of one run is written out directly.
+// Sort run `chunk` of lane `lane`; a lane of one run is written out directly. Thread tid holds
+// positions tid + 1024 q (q < 8) in registers through the whole bitonic network, so a stage's
+// partner t ^ j is in the same thread when j >= 1024 (a register swap), in the same wave when
+// j < 64 (a lane shuffle), and only for 64 <= j < 1024 in another wave (an exchange through LDS
+// between two barriers): 22 of the 91 stages of 8192 keys touch LDS.
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int j) {
+    const uint32_t lo = uint32_t(v), hi = uint32_t(v >> 32);
+    return (uint64_t(uint32_t(__shfl_xor(int(hi), j))) << 32) | uint32_t(__shfl_xor(int(lo), j));
+}
+
+// The value position t keeps at stage (k, j) given its partner's: the lower position of a pair
+// takes the larger key in a descending block ((t & k) == 0), the smaller in an ascending one.
+__device__ __forceinline__ uint64_t cmp_keep(uint64_t mine, uint64_t other, int t, int j, int k) {
+    const bool lower = (t & j) == 0;
+    const bool desc = (t & k) == 0;
+    const bool take_max = lower == desc;
+    const bool mine_bigger = mine > other;
+    return (take_max == mine_bigger) ? mine : other;
+}
+
 __global__ __launch_bounds__(kSortThreads) void k_sort_runs(SortP p) {
     __shared__ uint64_t s[kSortCap];
+    constexpr int Q = kSortCap / kSortThreads;  // keys per thread
     const int64_t lane = blockIdx.x / p.chunks;
     const int chunk = int(blockIdx.x - lane * p.chunks);
     const int64_t o = lane / p.inner, i = lane - o * p.inner;
     const int64_t beg = int64_t(chunk) * kSortCap;
     const int len = int(std::min<int64_t>(kSortCap, p.n - beg));
     const int P = p.pw;
-    for (int t = threadIdx.x; t < P; t += kSortThreads) {
+    const int tid = threadIdx.x;
+    uint64_t v[Q];
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+        const int t = tid + kSortThreads * q;
         uint64_t c = 0;  // padding: below every real key (the smallest real order key is 0x007fffff)
-        if (t < len) {
-            const int64_t d = beg + t;
-            c = sort_key(p.x[(o * p.n + d) * p.inner + i], uint32_t(d));
-        }
-        s[t] = c;
+        if (t < len) c = sort_key(p.x[(o * p.n + beg + t) * p.inner + i], uint32_t(beg + t));
+        v[q] = c;
     }
-    __syncthreads();
+    // Positions at or past P only meet each other (t ^ j >= P for t >= P, j < P): zeros stay there.
     for (int k = 2; k <= P; k <<= 1) {
         for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int t = threadIdx.x; t < P; t += kSortThreads) {
-                const int l = t ^ j;
-                if (l > t) {
-                    const uint64_t a = s[t], b = s[l];
-                    const bool desc = (t & k) == 0;
-                    if (desc ? a < b : a > b) {
-                        s[t] = b;
-                        s[l] = a;
-                    }
+            if (j >= kSortThreads) {
+                const int jq = j / kSortThreads;
+#pragma unroll
+                for (int q = 0; q < Q; q++) {
+                    if (q & jq) continue;
+                    const int t = tid + kSortThreads * q;
+                    const uint64_t a = v[q], b = v[q | jq];
+                    v[q] = cmp_keep(a, b, t, j, k);
+                    v[q | jq] = cmp_keep(b, a, t + j, j, k);
+                }
+            } else if (j >= kWaveSize) {
+#pragma unroll
+                for (int q = 0; q < Q; q++) s[tid + kSortThreads * q] = v[q];
+                __syncthreads();
+#pragma unroll
+                for (int q = 0; q < Q; q++) {
+                    const int t = tid + kSortThreads * q;
+                    v[q] = cmp_keep(v[q], s[t ^ j], t, j, k);
+                }
+                __syncthreads();
+            } else {
+#pragma unroll
+                for (int q = 0; q < Q; q++) {
+                    const int t = tid + kSortThreads * q;
+                    v[q] = cmp_keep(v[q], shfl_xor_u64(v[q], j), t, j, k);
                 }
             }
-            __syncthreads();
         }
     }
-    if (p.chunks == 1) {
-        for (int t = threadIdx.x; t < len; t += kSortThreads) {
-            const uint64_t c = s[t];
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+        const int t = tid + kSortThreads * q;
+        if (t >= len) continue;
+        const uint64_t c = v[q];
+        if (p.chunks == 1) {
             const uint32_t src = key_pos(c);
             const int64_t at = (o * p.n + t) * p.inner + i;
             p.vals[at] = key_value(c, p.x, (o * p.n + src) * p.inner + i);
             p.idx[at] = int32_t(src);
+        } else {
+            p.runs[lane * p.n + beg + t] = c;
         }
-    } else {
-        uint64_t *r = p.runs + lane * p.n + beg;
-        for (int t = threadIdx.x; t < len; t += kSortThreads) r[t] = s[t];
     }
 }
 
