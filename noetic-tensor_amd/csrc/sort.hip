@@ -11,9 +11,8 @@
 // A lane of up to kSortCap elements is sorted by one workgroup (bitonic, the keys in registers,
 // LDS only for exchanges between waves). A longer lane is
 // cut into kSortCap-long runs, each sorted that way into a scratch buffer, and the runs are
-// merged pairwise in global memory (merge path: every thread finds where its kMergeItems outputs
-// start by a binary search along its diagonal, then merges them sequentially) until one run
-// remains. The last step writes each position's value, decoded from its key (a NaN is read back
+// merged pairwise (merge path: each workgroup stages the two input windows that feed its tile of
+// outputs into LDS and merges them there) until one run remains. The last step writes each position's value, decoded from its key (a NaN is read back
 // from its source to keep the payload), and its index.
 #include <hip/hip_runtime.h>
 
@@ -32,6 +31,7 @@ constexpr int kSortThreads = 1024;
 constexpr int kSortCap = 8192;   // elements one workgroup sorts in LDS (64 KB of keys)
 constexpr int kMergeThreads = 256;
 constexpr int kMergeItems = 8;   // outputs per thread of a merge pass
+constexpr int kMergeTile = kMergeThreads * kMergeItems;  // outputs per workgroup (divides 2 kSortCap)
 constexpr int kWaveSize = 64;
 
 __device__ __forceinline__ uint64_t sort_key(float v, uint32_t pos) {
@@ -151,44 +151,74 @@ __global__ __launch_bounds__(kSortThreads) void k_sort_runs(SortP p) {
     }
 }
 
-// One merge pass: in every lane, runs [base, base + w) and [base + w, base + 2w) (clipped to n)
-// into one run of `dst`. If LAST, the merged positions go straight to the outputs.
-template <bool LAST>
-__global__ __launch_bounds__(kMergeThreads) void k_merge(SortP p, const uint64_t *src, uint64_t *dst, int64_t w,
-                                                         int64_t per_lane) {
-    const int64_t g = int64_t(blockIdx.x) * kMergeThreads + threadIdx.x;
-    const int64_t lane = g / per_lane;
-    if (lane >= p.outer * p.inner) return;
-    const int64_t pos = (g - lane * per_lane) * kMergeItems;
-    if (pos >= p.n) return;
-    const int64_t n = p.n;
-    const int64_t base = pos / (2 * w) * (2 * w);
-    const int64_t la = std::min<int64_t>(w, n - base);
-    const int64_t lb = std::max<int64_t>(0, std::min<int64_t>(w, n - base - la));
-    const uint64_t *A = src + lane * n + base;
-    const uint64_t *B = A + la;
-    const int64_t d = pos - base;
-    // co-rank: how many of the first d outputs come from A (keys are distinct: no ties)
+// How many of the first d outputs of merging descending runs A (la keys) and B (lb keys) come
+// from A (the merge path's co-rank; keys are distinct, so there are no ties).
+__device__ __forceinline__ int64_t co_rank(const uint64_t *A, int64_t la, const uint64_t *B, int64_t lb, int64_t d) {
     int64_t lo = std::max<int64_t>(0, d - lb), hi = std::min<int64_t>(d, la);
     while (lo < hi) {
         const int64_t mid = (lo + hi) >> 1;
         if (A[mid] > B[d - mid - 1]) lo = mid + 1;
         else hi = mid;
     }
-    int64_t ia = lo, ib = d - lo;
+    return lo;
+}
+
+// One merge pass: in every lane, runs [base, base + w) and [base + w, base + 2w) (clipped to n)
+// into one run of `dst`. A workgroup makes kMergeTile consecutive outputs (kMergeTile divides 2w,
+// so they come from one pair of runs): two co-ranks in global memory bound the A and B windows
+// that feed them, both windows are staged into LDS with coalesced loads, each thread merges its
+// kMergeItems outputs from LDS (its own co-rank by a search in LDS), and the tile is written back
+// coalesced. If LAST, the outputs are the values and positions instead of keys.
+template <bool LAST>
+__global__ __launch_bounds__(kMergeThreads) void k_merge(SortP p, const uint64_t *src, uint64_t *dst, int64_t w,
+                                                         int64_t tiles_per_lane) {
+    __shared__ uint64_t sa[kMergeTile], sb[kMergeTile], so[kMergeTile];
+    __shared__ int64_t cr[2];
+    const int tid = threadIdx.x;
+    const int64_t lane = blockIdx.x / tiles_per_lane;
+    const int64_t n = p.n;
+    const int64_t o0 = (blockIdx.x - lane * tiles_per_lane) * kMergeTile;
+    const int64_t o1 = std::min<int64_t>(n, o0 + kMergeTile);
+    const int64_t base = o0 / (2 * w) * (2 * w);
+    const int64_t la = std::min<int64_t>(w, n - base);
+    const int64_t lb = std::max<int64_t>(0, std::min<int64_t>(w, n - base - la));
+    const uint64_t *A = src + lane * n + base;
+    const uint64_t *B = A + la;
+    const int64_t d0 = o0 - base, d1 = o1 - base;
+    if (tid < 2) cr[tid] = co_rank(A, la, B, lb, tid == 0 ? d0 : d1);
+    __syncthreads();
+    const int64_t a0 = cr[0], b0 = d0 - cr[0];
+    const int na = int(cr[1] - cr[0]), nb = int((d1 - cr[1]) - b0);
+    for (int e = tid; e < na; e += kMergeThreads) sa[e] = A[a0 + e];
+    for (int e = tid; e < nb; e += kMergeThreads) sb[e] = B[b0 + e];
+    __syncthreads();
+    const int dl = tid * kMergeItems;
+    const int total = na + nb;
+    if (dl < total) {
+        int lo = std::max(0, dl - nb), hi = std::min(dl, na);
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (sa[mid] > sb[dl - mid - 1]) lo = mid + 1;
+            else hi = mid;
+        }
+        int ia = lo, ib = dl - lo;
+        const int end = std::min(kMergeItems, total - dl);
+        for (int q = 0; q < end; q++) {
+            const bool from_a = ib >= nb || (ia < na && sa[ia] > sb[ib]);
+            so[dl + q] = from_a ? sa[ia++] : sb[ib++];
+        }
+    }
+    __syncthreads();
     const int64_t o = lane / p.inner, i = lane - o * p.inner;
-    const int64_t end = std::min<int64_t>(kMergeItems, la + lb - d);
-    for (int64_t q = 0; q < end; q++) {
-        uint64_t c;
-        if (ib >= lb || (ia < la && A[ia] > B[ib])) c = A[ia++];
-        else c = B[ib++];
+    for (int e = tid; e < total; e += kMergeThreads) {
+        const uint64_t c = so[e];
         if constexpr (LAST) {
             const uint32_t s = key_pos(c);
-            const int64_t at = (o * n + pos + q) * p.inner + i;
+            const int64_t at = (o * n + o0 + e) * p.inner + i;
             p.vals[at] = key_value(c, p.x, (o * n + s) * p.inner + i);
             p.idx[at] = int32_t(s);
         } else {
-            dst[lane * n + pos + q] = c;
+            dst[lane * n + o0 + e] = c;
         }
     }
 }
@@ -236,18 +266,23 @@ int nt_hip_sort_desc(const float *x, int64_t outer, int64_t n, int64_t inner, fl
     p.runs = static_cast<uint64_t *>(buf[0]);
     hipLaunchKernelGGL(k_sort_runs, dim3(unsigned(lanes * chunks)), dim3(kSortThreads), 0, st, p);
     int rc = launched("k_sort_runs");
-    const int64_t per_lane = (n + kMergeItems - 1) / kMergeItems;
-    const int64_t blocks = (lanes * per_lane + kMergeThreads - 1) / kMergeThreads;
+    const int64_t tiles = (n + kMergeTile - 1) / kMergeTile;
+    const int64_t blocks = lanes * tiles;
+    if (blocks > int64_t(0x7fffffff)) {
+        scratch_release(buf[0]);
+        scratch_release(buf[1]);
+        return fail(NT_E_ARG, "sort_desc: too many merge tiles");
+    }
     int cur = 0;
     for (int64_t w = kSortCap; !rc && w < n; w *= 2) {
         const uint64_t *src = static_cast<const uint64_t *>(buf[cur]);
         uint64_t *dst = static_cast<uint64_t *>(buf[cur ^ 1]);
         if (2 * w >= n) {
             hipLaunchKernelGGL((k_merge<true>), dim3(unsigned(blocks)), dim3(kMergeThreads), 0, st, p, src, dst, w,
-                               per_lane);
+                               tiles);
         } else {
             hipLaunchKernelGGL((k_merge<false>), dim3(unsigned(blocks)), dim3(kMergeThreads), 0, st, p, src, dst, w,
-                               per_lane);
+                               tiles);
         }
         rc = launched("k_merge");
         cur ^= 1;
