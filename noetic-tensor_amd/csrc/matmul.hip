@@ -280,10 +280,8 @@ __global__ void k_fold(const float *slices, int64_t outputs, int nkc, float *out
 // transposes it in registers, so that every LDS store writes four bf16 of one row.
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
-constexpr int kHT = 128;  // tile edge
 constexpr int kHK = 32;   // k per panel
 constexpr int kHPad = 8;  // bf16 padding per LDS row (rows stay 16-byte aligned)
-constexpr int kHLoads = kHT * kHK / kMmThreads;  // f32 loads per operand and thread per panel
 
 __device__ __forceinline__ uint16_t bf16_bits(float x) {
     uint32_t r;
@@ -291,8 +289,15 @@ __device__ __forceinline__ uint16_t bf16_bits(float x) {
     return uint16_t(r);
 }
 
-template <bool AK, bool BN>
+// T = 128: each wave a 64x64 quarter (2x2 MFMA tiles); T = 64 (outputs too few for 512 workgroups
+// of 128): each wave a 32x32 quarter (one MFMA tile).
+template <int T, bool AK, bool BN>
 __global__ __launch_bounds__(kMmThreads) void k_matmul_half(MatmulP p) {
+    constexpr int kHT = T;
+    constexpr int W = T / 64;                         // MFMA tiles per wave along m and along n
+    constexpr int kHLoads = kHT * kHK / kMmThreads;   // scalar f32 loads per operand and thread
+    constexpr int kQuads = kHT * (kHK / 4) / kMmThreads;  // 16-byte loads along k per thread
+    constexpr int kRG = kHT / 4;                      // 4x4 blocks along m or n
     __shared__ __attribute__((aligned(16))) uint16_t As[kHT][kHK + kHPad];
     __shared__ __attribute__((aligned(16))) uint16_t Bs[kHT][kHK + kHPad];
     const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
@@ -317,43 +322,62 @@ __global__ __launch_bounds__(kMmThreads) void k_matmul_half(MatmulP p) {
     const float *b = p.b + bo;
     const int M = p.m, N = p.n, K = p.k;
 
-    float ra[kHLoads], rb[kHLoads];
+    float ra[16], rb[16];
+    // a 4x4 block (4 rows or columns by 4 k) per thread, for threads tid < 2 T
+    const int rg = tid % kRG, kg = tid / kRG;
+    const bool blk = kg < kHK / 4;
     // 16-byte staging for this panel? (an interior panel of a vector-eligible view)
     auto vec_a = [&](int k0) { return p.avec && row0 + kHT <= M && k0 + kHK <= K; };
     auto vec_b = [&](int k0) { return p.bvec && col0 + kHT <= N && k0 + kHK <= K; };
     auto load = [&](int k0) {
         if (vec_a(k0)) {
+            if constexpr (AK) {  // along k: group g covers row g / 8, k (g % 8) * 4 .. + 3
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                float4 v;
-                if constexpr (AK) {  // along k: group g covers row g / 8, k (g % 8) * 4 .. + 3
+                for (int q = 0; q < kQuads; q++) {
                     const int g = tid + kMmThreads * q;
-                    v = *reinterpret_cast<const float4 *>(a + int64_t(row0 + g / 8) * p.a_rs + k0 + (g % 8) * 4);
-                } else {  // along m: rows (tid % 32) * 4 .. + 3 at k (tid / 32) * 4 + q
-                    v = *reinterpret_cast<const float4 *>(a + row0 + (tid % 32) * 4 +
-                                                          int64_t(k0 + (tid / 32) * 4 + q) * p.a_cs);
+                    const float4 v =
+                        *reinterpret_cast<const float4 *>(a + int64_t(row0 + g / 8) * p.a_rs + k0 + (g % 8) * 4);
+                    ra[4 * q] = v.x;
+                    ra[4 * q + 1] = v.y;
+                    ra[4 * q + 2] = v.z;
+                    ra[4 * q + 3] = v.w;
                 }
-                ra[4 * q] = v.x;
-                ra[4 * q + 1] = v.y;
-                ra[4 * q + 2] = v.z;
-                ra[4 * q + 3] = v.w;
+            } else if (blk) {  // along m: rows rg * 4 .. + 3 at k kg * 4 + q
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float4 v =
+                        *reinterpret_cast<const float4 *>(a + row0 + rg * 4 + int64_t(k0 + kg * 4 + q) * p.a_cs);
+                    ra[4 * q] = v.x;
+                    ra[4 * q + 1] = v.y;
+                    ra[4 * q + 2] = v.z;
+                    ra[4 * q + 3] = v.w;
+                }
             }
         }
         if (vec_b(k0)) {
+            if constexpr (BN) {  // along n: columns rg * 4 .. + 3 at k kg * 4 + q
+                if (blk) {
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                float4 v;
-                if constexpr (BN) {  // along n: columns (tid % 32) * 4 .. + 3 at k (tid / 32) * 4 + q
-                    v = *reinterpret_cast<const float4 *>(b + int64_t(k0 + (tid / 32) * 4 + q) * p.b_rs + col0 +
-                                                          (tid % 32) * 4);
-                } else {  // along k: group g covers column g / 8, k (g % 8) * 4 .. + 3
-                    const int g = tid + kMmThreads * q;
-                    v = *reinterpret_cast<const float4 *>(b + int64_t(col0 + g / 8) * p.b_cs + k0 + (g % 8) * 4);
+                    for (int q = 0; q < 4; q++) {
+                        const float4 v =
+                            *reinterpret_cast<const float4 *>(b + int64_t(k0 + kg * 4 + q) * p.b_rs + col0 + rg * 4);
+                        rb[4 * q] = v.x;
+                        rb[4 * q + 1] = v.y;
+                        rb[4 * q + 2] = v.z;
+                        rb[4 * q + 3] = v.w;
+                    }
                 }
-                rb[4 * q] = v.x;
-                rb[4 * q + 1] = v.y;
-                rb[4 * q + 2] = v.z;
-                rb[4 * q + 3] = v.w;
+            } else {  // along k: group g covers column g / 8, k (g % 8) * 4 .. + 3
+#pragma unroll
+                for (int q = 0; q < kQuads; q++) {
+                    const int g = tid + kMmThreads * q;
+                    const float4 v =
+                        *reinterpret_cast<const float4 *>(b + int64_t(col0 + g / 8) * p.b_cs + k0 + (g % 8) * 4);
+                    rb[4 * q] = v.x;
+                    rb[4 * q + 1] = v.y;
+                    rb[4 * q + 2] = v.z;
+                    rb[4 * q + 3] = v.w;
+                }
             }
         }
         const bool sa = !vec_a(k0), sb = !vec_b(k0);
@@ -393,14 +417,14 @@ __global__ __launch_bounds__(kMmThreads) void k_matmul_half(MatmulP p) {
         if (vec_a(k0)) {
             if constexpr (AK) {
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
+                for (int q = 0; q < kQuads; q++) {
                     const int g = tid + kMmThreads * q;
                     put4(&As[g / 8][(g % 8) * 4], ra[4 * q], ra[4 * q + 1], ra[4 * q + 2], ra[4 * q + 3]);
                 }
-            } else {
+            } else if (blk) {
 #pragma unroll
-                for (int j = 0; j < 4; j++)  // row (tid % 32) * 4 + j, k (tid / 32) * 4 .. + 3
-                    put4(&As[(tid % 32) * 4 + j][(tid / 32) * 4], ra[j], ra[4 + j], ra[8 + j], ra[12 + j]);
+                for (int j = 0; j < 4; j++)  // row rg * 4 + j, k kg * 4 .. + 3
+                    put4(&As[rg * 4 + j][kg * 4], ra[j], ra[4 + j], ra[8 + j], ra[12 + j]);
             }
         } else {
 #pragma unroll
@@ -412,12 +436,14 @@ __global__ __launch_bounds__(kMmThreads) void k_matmul_half(MatmulP p) {
         }
         if (vec_b(k0)) {
             if constexpr (BN) {
+                if (blk) {
 #pragma unroll
-                for (int j = 0; j < 4; j++)  // column (tid % 32) * 4 + j, k (tid / 32) * 4 .. + 3
-                    put4(&Bs[(tid % 32) * 4 + j][(tid / 32) * 4], rb[j], rb[4 + j], rb[8 + j], rb[12 + j]);
+                    for (int j = 0; j < 4; j++)  // column rg * 4 + j, k kg * 4 .. + 3
+                        put4(&Bs[rg * 4 + j][kg * 4], rb[j], rb[4 + j], rb[8 + j], rb[12 + j]);
+                }
             } else {
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
+                for (int q = 0; q < kQuads; q++) {
                     const int g = tid + kMmThreads * q;
                     put4(&Bs[g / 8][(g % 8) * 4], rb[4 * q], rb[4 * q + 1], rb[4 * q + 2], rb[4 * q + 3]);
                 }
@@ -432,14 +458,14 @@ __global__ __launch_bounds__(kMmThreads) void k_matmul_half(MatmulP p) {
         }
     };
 
-    f32x16_t acc[2][2];
+    f32x16_t acc[W][W];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < W; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < W; j++)
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[i][j][v] = 0.0f;
-    const int wm = (wave / 2) * 64, wn = (wave % 2) * 64;
+    const int wm = (wave / 2) * 32 * W, wn = (wave % 2) * 32 * W;
     const int fr = lane % 32, fk = 8 * (lane / 32);
 
     load(0);
@@ -449,25 +475,25 @@ __global__ __launch_bounds__(kMmThreads) void k_matmul_half(MatmulP p) {
         if (k0 + kHK < K) load(k0 + kHK);  // in flight during this panel's MFMAs
 #pragma unroll
         for (int ks = 0; ks < kHK; ks += 16) {
-            bf16x8_t af[2], bf[2];
+            bf16x8_t af[W], bf[W];
 #pragma unroll
-            for (int t = 0; t < 2; t++) {
+            for (int t = 0; t < W; t++) {
                 af[t] = *reinterpret_cast<const bf16x8_t *>(&As[wm + t * 32 + fr][ks + fk]);
                 bf[t] = *reinterpret_cast<const bf16x8_t *>(&Bs[wn + t * 32 + fr][ks + fk]);
             }
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+            for (int i = 0; i < W; i++)
 #pragma unroll
-                for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < W; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
         __syncthreads();
     }
 
     float *c = p.c + z * int64_t(M) * N;
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < W; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
+        for (int j = 0; j < W; j++) {
             const int col = col0 + wn + j * 32 + fr;
             if (col >= N) continue;
 #pragma unroll
@@ -615,8 +641,11 @@ int nt_hip_matmul_half(const float *a, const NtLayout *al, const float *b, const
     p.m = int32_t(m);
     p.n = int32_t(n);
     p.k = int32_t(k);
-    p.tm = int32_t((m + kHT - 1) / kHT);
-    p.tn = int32_t((n + kHT - 1) / kHT);
+    // 128x128 tiles when they give at least 512 workgroups, else 64x64
+    const int64_t big = nb * ((m + 127) / 128) * ((n + 127) / 128);
+    const int T = big >= 512 ? 128 : 64;
+    p.tm = int32_t((m + T - 1) / T);
+    p.tn = int32_t((n + T - 1) / T);
     p.blocks = nb * p.tm * p.tn;
     if (p.blocks > int64_t(0x7fffffff)) return fail(NT_E_ARG, "matmul_half: too many output tiles");
     const bool ak = k == 1 || p.a_cs == 1;
@@ -637,10 +666,17 @@ int nt_hip_matmul_half(const float *a, const NtLayout *al, const float *b, const
     if (int rc = enter(&lk)) return rc;
     hipStream_t st = ctx().stream;
     const dim3 grid(unsigned(p.blocks)), block(kMmThreads);
-    if (ak && bn) hipLaunchKernelGGL((k_matmul_half<true, true>), grid, block, 0, st, p);
-    else if (ak) hipLaunchKernelGGL((k_matmul_half<true, false>), grid, block, 0, st, p);
-    else if (bn) hipLaunchKernelGGL((k_matmul_half<false, true>), grid, block, 0, st, p);
-    else hipLaunchKernelGGL((k_matmul_half<false, false>), grid, block, 0, st, p);
+    if (T == 128) {
+        if (ak && bn) hipLaunchKernelGGL((k_matmul_half<128, true, true>), grid, block, 0, st, p);
+        else if (ak) hipLaunchKernelGGL((k_matmul_half<128, true, false>), grid, block, 0, st, p);
+        else if (bn) hipLaunchKernelGGL((k_matmul_half<128, false, true>), grid, block, 0, st, p);
+        else hipLaunchKernelGGL((k_matmul_half<128, false, false>), grid, block, 0, st, p);
+    } else {
+        if (ak && bn) hipLaunchKernelGGL((k_matmul_half<64, true, true>), grid, block, 0, st, p);
+        else if (ak) hipLaunchKernelGGL((k_matmul_half<64, true, false>), grid, block, 0, st, p);
+        else if (bn) hipLaunchKernelGGL((k_matmul_half<64, false, true>), grid, block, 0, st, p);
+        else hipLaunchKernelGGL((k_matmul_half<64, false, false>), grid, block, 0, st, p);
+    }
     return launched("k_matmul_half");
 }
 

@@ -43,7 +43,8 @@ CASES = [("[1,64,64]x[1,64,64]", [1, 64, 64], [1, 64, 64], False),
          ("[1,64,2048]x[1,2048,64] long k", [1, 64, 2048], [1, 2048, 64], False),
          ("[3,100,96]x[1,96,70] broadcast", [3, 100, 96], [1, 96, 70], False),
          ("AT.BT views [2,150,300],[2,260,150]", [2, 150, 300], [2, 260, 150], True),
-         ("[1,512,512]x[1,512,512]", [1, 512, 512], [1, 512, 512], False)]
+         ("[1,512,512]x[1,512,512]", [1, 512, 512], [1, 512, 512], False),
+         ("[2,2048,96]x[2,96,2048] (128 tiles)", [2, 2048, 96], [2, 96, 2048], False)]
 
 
 @pytest.mark.parametrize("i,case", list(enumerate(CASES)))
@@ -68,16 +69,18 @@ def test_body_half_matmul_error_against_f32_on_fixed_shapes(i, case):
     assert e16 <= acc and e32 <= 2 * 2.0 ** -8 + acc and np.all(np.isfinite(got))
 
 
-@pytest.mark.parametrize("shape", [(1, 32, 16, 32), (2, 128, 64, 128), (3, 200, 96, 130), (1, 257, 33, 300)])
+@pytest.mark.parametrize("shape", [(1, 32, 16, 32), (2, 128, 64, 128), (3, 200, 96, 130), (1, 257, 33, 300),
+                                   (2, 2048, 64, 2048)])
 def test_integer_operands_are_exact_and_pin_the_lane_layout(shape):
     """Integers in [-8, 8] are exact in bf16 and every partial sum is exact in f32, so the product
     equals numpy's integer product exactly whatever the summation order: a wrong operand or result
-    lane mapping would show as wrong integers. Both orientations of each operand."""
+    lane mapping would show as wrong integers. Both orientations of each operand; both tile sizes
+    (128x128 from 512 workgroups up, the last shape; 64x64 below)."""
     nb, m, k, n = shape
     rng = np.random.default_rng(m + k)
     a = rng.integers(-8, 9, (nb, m, k)).astype(F)
     b = rng.integers(-8, 9, (nb, k, n)).astype(F)
-    want = (a.astype(np.int64) @ b.astype(np.int64)).astype(F)
+    want = (a.astype(np.float64) @ b.astype(np.float64)).astype(F)  # exact: |sums| <= 64 k
     for ta in (False, True):
         for tb in (False, True):
             da = DTensor.from_numpy(np.ascontiguousarray(SW(a))).swap_dims(1, 2) if ta else DTensor.from_numpy(a)
