@@ -132,10 +132,6 @@ int nt_hip_claim(int device) {
         return fail(NT_E_ARG, buf);
     }
     if (int rc = hip_check(hipSetDevice(device), "hipSetDevice")) return rc;
-    hipStream_t s = nullptr;
-    // Default priority only: streams of other priorities are not used by this library.
-    if (int rc = hip_check(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreateWithFlags"))
-        return rc;
     int pools = 0;
     if (hipDeviceGetAttribute(&pools, hipDeviceAttributeMemoryPoolsSupported, device) != hipSuccess) {
         (void)hipGetLastError();
@@ -152,6 +148,10 @@ int nt_hip_claim(int device) {
                                "hipMemPoolSetAttribute"))
             return rc;
     }
+    hipStream_t s = nullptr;
+    // Default priority only: streams of other priorities are not used by this library.
+    if (int rc = hip_check(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreateWithFlags"))
+        return rc;
     c.device = device;
     c.stream = s;
     c.pools = pools != 0;
