@@ -104,7 +104,37 @@ __device__ __forceinline__ void matmul_body(const MatmulP &p) {
     const int M = p.m, N = p.n, K = p.k;
 
     float ra[LPT], rb[LPT];
+    // Interior panels of a row-major view (A along k, B along n, 16-byte aligned) load four
+    // values per instruction: group g of A is row g / 4, k (g % 4) * 4 .. + 3; of B, k g / (T / 4),
+    // columns (g % (T / 4)) * 4 .. + 3.
+    constexpr int V4 = LPT / 4;
+    auto vec_a = [&](int k0) { return AK && p.avec && row0 + T <= M && k0 + kBK <= K; };
+    auto vec_b = [&](int k0) { return BN && p.bvec && col0 + T <= N && k0 + kBK <= K; };
     auto load = [&](int k0) {
+        const bool va = vec_a(k0), vb = vec_b(k0);
+        if (va) {
+#pragma unroll
+            for (int q = 0; q < V4; q++) {
+                const int g = tid + kMmThreads * q;
+                const float4 v = *reinterpret_cast<const float4 *>(a + int64_t(row0 + g / 4) * p.a_rs + k0 + (g % 4) * 4);
+                ra[4 * q] = v.x;
+                ra[4 * q + 1] = v.y;
+                ra[4 * q + 2] = v.z;
+                ra[4 * q + 3] = v.w;
+            }
+        }
+        if (vb) {
+#pragma unroll
+            for (int q = 0; q < V4; q++) {
+                const int g = tid + kMmThreads * q;
+                const float4 v = *reinterpret_cast<const float4 *>(b + int64_t(k0 + g / (T / 4)) * p.b_rs + col0 +
+                                                                   (g % (T / 4)) * 4);
+                rb[4 * q] = v.x;
+                rb[4 * q + 1] = v.y;
+                rb[4 * q + 2] = v.z;
+                rb[4 * q + 3] = v.w;
+            }
+        }
 #pragma unroll
         for (int i = 0; i < LPT; i++) {
             const int e = tid + kMmThreads * i;
@@ -117,7 +147,7 @@ __device__ __forceinline__ void matmul_body(const MatmulP &p) {
                 kk = e / T;
             }
             const int gr = row0 + r, gk = k0 + kk;
-            ra[i] = (gr < M && gk < K) ? a[int64_t(gr) * p.a_rs + int64_t(gk) * p.a_cs] : 0.0f;
+            if (!va) ra[i] = (gr < M && gk < K) ? a[int64_t(gr) * p.a_rs + int64_t(gk) * p.a_cs] : 0.0f;
             int cc;
             if constexpr (BN) {
                 cc = e % T;
@@ -127,17 +157,39 @@ __device__ __forceinline__ void matmul_body(const MatmulP &p) {
                 cc = e / kBK;
             }
             const int gc = col0 + cc, gk2 = k0 + kk;
-            rb[i] = (gc < N && gk2 < K) ? b[int64_t(gk2) * p.b_rs + int64_t(gc) * p.b_cs] : 0.0f;
+            if (!vb) rb[i] = (gc < N && gk2 < K) ? b[int64_t(gk2) * p.b_rs + int64_t(gc) * p.b_cs] : 0.0f;
         }
     };
-    auto stash = [&](int s) {
+    auto stash = [&](int s, int k0) {
+        if (vec_a(k0)) {
 #pragma unroll
-        for (int i = 0; i < LPT; i++) {
-            const int e = tid + kMmThreads * i;
-            if constexpr (AK) As[s][e % kBK][e / kBK] = ra[i];
-            else As[s][e / T][e % T] = ra[i];
-            if constexpr (BN) Bs[s][e / T][e % T] = rb[i];
-            else Bs[s][e % kBK][e / kBK] = rb[i];
+            for (int q = 0; q < V4; q++) {
+                const int g = tid + kMmThreads * q;
+#pragma unroll
+                for (int j = 0; j < 4; j++) As[s][(g % 4) * 4 + j][g / 4] = ra[4 * q + j];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < LPT; i++) {
+                const int e = tid + kMmThreads * i;
+                if constexpr (AK) As[s][e % kBK][e / kBK] = ra[i];
+                else As[s][e / T][e % T] = ra[i];
+            }
+        }
+        if (vec_b(k0)) {
+#pragma unroll
+            for (int q = 0; q < V4; q++) {
+                const int g = tid + kMmThreads * q;
+                *reinterpret_cast<float4 *>(&Bs[s][g / (T / 4)][(g % (T / 4)) * 4]) =
+                    make_float4(rb[4 * q], rb[4 * q + 1], rb[4 * q + 2], rb[4 * q + 3]);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < LPT; i++) {
+                const int e = tid + kMmThreads * i;
+                if constexpr (BN) Bs[s][e / T][e % T] = rb[i];
+                else Bs[s][e % kBK][e / kBK] = rb[i];
+            }
         }
     };
 
@@ -193,7 +245,7 @@ __device__ __forceinline__ void matmul_body(const MatmulP &p) {
     };
 
     load(kbeg);
-    stash(0);
+    stash(0, kbeg);
     __syncthreads();
     int s = 0;
     for (int k0 = kbeg; k0 < kend; k0 += kBK) {
@@ -224,7 +276,7 @@ __device__ __forceinline__ void matmul_body(const MatmulP &p) {
                     }
             }
         }
-        if (more) stash(s ^ 1);  // the other buffer was last read before the previous barrier
+        if (more) stash(s ^ 1, k0 + kBK);  // the other buffer was last read before the previous barrier
         __syncthreads();
         s ^= 1;
     }
@@ -604,6 +656,17 @@ int nt_hip_matmul(const float *a, const NtLayout *al, const float *b, const NtLa
     if (p.blocks > int64_t(0x7fffffff)) return fail(NT_E_ARG, "matmul: too many output tiles");
     const bool ak = k == 1 || p.a_cs == 1;
     const bool bn = n == 1 || p.b_cs == 1;
+    {
+        // 16-byte panel loads: row-major operands whose rows, batch offsets and base are 16-byte aligned
+        auto aligned = [&](const int64_t *bs, int64_t off, int64_t rs, const float *base) {
+            if (off % 4 != 0 || rs % 4 != 0 || (reinterpret_cast<uintptr_t>(base) & 15) != 0) return false;
+            for (int d = 0; d < r - 2; d++)
+                if (bs[d] % 4 != 0) return false;
+            return true;
+        };
+        p.avec = p.a_cs == 1 && aligned(p.a_bs, p.a_off, p.a_rs, a);
+        p.bvec = p.b_cs == 1 && aligned(p.b_bs, p.b_off, p.b_rs, b);
+    }
     std::unique_lock<std::mutex> lk;
     if (int rc = enter(&lk)) return rc;
     hipStream_t st = ctx().stream;
