@@ -104,19 +104,22 @@ __device__ __forceinline__ void matmul_body(const MatmulP &p) {
     const int M = p.m, N = p.n, K = p.k;
 
     float ra[LPT], rb[LPT];
-    // Interior panels of a row-major view (A along k, B along n, 16-byte aligned) load four
-    // values per instruction: group g of A is row g / 4, k (g % 4) * 4 .. + 3; of B, k g / (T / 4),
-    // columns (g % (T / 4)) * 4 .. + 3.
+    // Interior panels of a view contiguous along one axis (16-byte aligned) load four values per
+    // instruction. Along k (A row-major, B transposed): group g is row or column g / 4, k (g % 4) * 4
+    // .. + 3. Along m or n (A transposed, B row-major): group g is k g / (T / 4), rows or columns
+    // (g % (T / 4)) * 4 .. + 3.
     constexpr int V4 = LPT / 4;
-    auto vec_a = [&](int k0) { return AK && p.avec && row0 + T <= M && k0 + kBK <= K; };
-    auto vec_b = [&](int k0) { return BN && p.bvec && col0 + T <= N && k0 + kBK <= K; };
+    auto vec_a = [&](int k0) { return p.avec && row0 + T <= M && k0 + kBK <= K; };
+    auto vec_b = [&](int k0) { return p.bvec && col0 + T <= N && k0 + kBK <= K; };
     auto load = [&](int k0) {
         const bool va = vec_a(k0), vb = vec_b(k0);
         if (va) {
 #pragma unroll
             for (int q = 0; q < V4; q++) {
                 const int g = tid + kMmThreads * q;
-                const float4 v = *reinterpret_cast<const float4 *>(a + int64_t(row0 + g / 4) * p.a_rs + k0 + (g % 4) * 4);
+                const float *src = AK ? a + int64_t(row0 + g / 4) * p.a_rs + k0 + (g % 4) * 4
+                                      : a + int64_t(k0 + g / (T / 4)) * p.a_cs + row0 + (g % (T / 4)) * 4;
+                const float4 v = *reinterpret_cast<const float4 *>(src);
                 ra[4 * q] = v.x;
                 ra[4 * q + 1] = v.y;
                 ra[4 * q + 2] = v.z;
@@ -127,8 +130,9 @@ __device__ __forceinline__ void matmul_body(const MatmulP &p) {
 #pragma unroll
             for (int q = 0; q < V4; q++) {
                 const int g = tid + kMmThreads * q;
-                const float4 v = *reinterpret_cast<const float4 *>(b + int64_t(k0 + g / (T / 4)) * p.b_rs + col0 +
-                                                                   (g % (T / 4)) * 4);
+                const float *src = BN ? b + int64_t(k0 + g / (T / 4)) * p.b_rs + col0 + (g % (T / 4)) * 4
+                                      : b + int64_t(col0 + g / 4) * p.b_cs + k0 + (g % 4) * 4;
+                const float4 v = *reinterpret_cast<const float4 *>(src);
                 rb[4 * q] = v.x;
                 rb[4 * q + 1] = v.y;
                 rb[4 * q + 2] = v.z;
@@ -165,8 +169,13 @@ __device__ __forceinline__ void matmul_body(const MatmulP &p) {
 #pragma unroll
             for (int q = 0; q < V4; q++) {
                 const int g = tid + kMmThreads * q;
+                if constexpr (AK) {
 #pragma unroll
-                for (int j = 0; j < 4; j++) As[s][(g % 4) * 4 + j][g / 4] = ra[4 * q + j];
+                    for (int j = 0; j < 4; j++) As[s][(g % 4) * 4 + j][g / 4] = ra[4 * q + j];
+                } else {
+                    *reinterpret_cast<float4 *>(&As[s][g / (T / 4)][(g % (T / 4)) * 4]) =
+                        make_float4(ra[4 * q], ra[4 * q + 1], ra[4 * q + 2], ra[4 * q + 3]);
+                }
             }
         } else {
 #pragma unroll
@@ -180,8 +189,13 @@ __device__ __forceinline__ void matmul_body(const MatmulP &p) {
 #pragma unroll
             for (int q = 0; q < V4; q++) {
                 const int g = tid + kMmThreads * q;
-                *reinterpret_cast<float4 *>(&Bs[s][g / (T / 4)][(g % (T / 4)) * 4]) =
-                    make_float4(rb[4 * q], rb[4 * q + 1], rb[4 * q + 2], rb[4 * q + 3]);
+                if constexpr (BN) {
+                    *reinterpret_cast<float4 *>(&Bs[s][g / (T / 4)][(g % (T / 4)) * 4]) =
+                        make_float4(rb[4 * q], rb[4 * q + 1], rb[4 * q + 2], rb[4 * q + 3]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; j++) Bs[s][(g % 4) * 4 + j][g / 4] = rb[4 * q + j];
+                }
             }
         } else {
 #pragma unroll
@@ -657,15 +671,18 @@ int nt_hip_matmul(const float *a, const NtLayout *al, const float *b, const NtLa
     const bool ak = k == 1 || p.a_cs == 1;
     const bool bn = n == 1 || p.b_cs == 1;
     {
-        // 16-byte panel loads: row-major operands whose rows, batch offsets and base are 16-byte aligned
-        auto aligned = [&](const int64_t *bs, int64_t off, int64_t rs, const float *base) {
-            if (off % 4 != 0 || rs % 4 != 0 || (reinterpret_cast<uintptr_t>(base) & 15) != 0) return false;
+        // 16-byte panel loads: a view contiguous along its read axis whose other stride, batch
+        // offsets and base are 16-byte aligned
+        auto aligned = [&](const int64_t *bs, int64_t off, int64_t other, const float *base) {
+            if (off % 4 != 0 || other % 4 != 0 || (reinterpret_cast<uintptr_t>(base) & 15) != 0) return false;
             for (int d = 0; d < r - 2; d++)
                 if (bs[d] % 4 != 0) return false;
             return true;
         };
-        p.avec = p.a_cs == 1 && aligned(p.a_bs, p.a_off, p.a_rs, a);
-        p.bvec = p.b_cs == 1 && aligned(p.b_bs, p.b_off, p.b_rs, b);
+        p.avec = ak ? (p.a_cs == 1 && aligned(p.a_bs, p.a_off, p.a_rs, a))
+                    : (p.a_rs == 1 && aligned(p.a_bs, p.a_off, p.a_cs, a));
+        p.bvec = bn ? (p.b_cs == 1 && aligned(p.b_bs, p.b_off, p.b_rs, b))
+                    : (p.b_rs == 1 && aligned(p.b_bs, p.b_off, p.b_cs, b));
     }
     std::unique_lock<std::mutex> lk;
     if (int rc = enter(&lk)) return rc;
