@@ -1,5 +1,5 @@
 """Benchmark of the north-star path: fused masked sample + log-probability at
-[S=1, B=256, T=1, V=128256] bf16 with a u8 grammar mask and temperature 0.7.
+[S=1, B=256, T=1, V=128256] bf16 with a u8 grammar mask and temperature 0.7 (benchmark configuration 4).
 
 One step = one launch of nt_hip_rl_sample over the 256 rows, inputs resident in HBM (the
 per-step uniforms are uploaded before the timed region) and cycled over copies totalling 1 GiB,

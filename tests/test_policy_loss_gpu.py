@@ -66,7 +66,7 @@ def ppo_data(shape, seed, dual=False):
 @pytest.mark.parametrize("shape", [(8, 16, 512), (4, 32, 1024)])
 @pytest.mark.parametrize("variant", ["pg", "pg_per_seq", "ppo", "ppo_asym", "ppo_dual", "ppo_open"])
 def test_policy_losses_per_token_against_the_oracle(shape, variant):
-    # BASELINE configs 3 and 5's [S, B, T]; every clip setting of tests/rl.rs:251-317, 678-717
+    # benchmark configurations 3 and 5's [S, B, T]; every clip setting of tests/rl.rs:251-317, 678-717
     S, B, T = shape
     clip = {"ppo": nr.Clip.symmetric(0.2), "ppo_asym": nr.Clip.new(0.2, 0.28),
             "ppo_dual": nr.Clip.symmetric(0.2).with_dual(3.0),

@@ -322,7 +322,7 @@ def _sample_rows(rows, n, seed):
 
 
 def test_c3_full_size_scoring():
-    # BASELINE config 3 at its real size: 2 x bf16 [8,16,512,50304] (13.2 GB). Rows spread over
+    # benchmark configuration 3 at its real size: 2 x bf16 [8,16,512,50304] (13.2 GB). Rows spread over
     # the tensor against the oracle; every row through size-independent properties.
     w = W.c3()
     rows, V = w["rows"], w["V"]
@@ -349,7 +349,7 @@ def test_c3_full_size_scoring():
 
 
 def test_c5_full_size_scoring_and_group_advantages():
-    # BASELINE config 5 at its real size: f32 [4,32,1024,151936] (79.7 GB) + u8 mask (19.9 GB).
+    # benchmark configuration 5 at its real size: f32 [4,32,1024,151936] (79.7 GB) + u8 mask (19.9 GB).
     w = W.c5()
     rows, V = w["rows"], w["V"]
     S, B, T = w["logits"].shape[:-1]

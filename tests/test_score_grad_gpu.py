@@ -91,7 +91,7 @@ def compare_to_oracle(name, z, r, tok, g, kl, ent, tau, grad_f32, grad_bf16=None
 
 
 def test_c3_backward_parity_on_a_row_slice():
-    # BASELINE config 3's rows (bf16, V 50304, the reference's logits beside the policy's):
+    # benchmark configuration 3's rows (bf16, V 50304, the reference's logits beside the policy's):
     # d(g_lp logp + g_kl KL + g_H H)/dx in f32 and bf16.
     w = W.c3(rows=64)
     rows, V = w["rows"], w["V"]
@@ -222,7 +222,7 @@ def test_refused_rows_give_nan_gradients():
 
 
 def test_c3_full_size_backward():
-    # BASELINE config 3 at its real size (2 x bf16 [8,16,512,50304]): the f32 gradient of every
+    # benchmark configuration 3 at its real size (2 x bf16 [8,16,512,50304]): the f32 gradient of every
     # row sums to zero (each of the three objectives' gradients does: softmax sums to one), to
     # 1e-5 of the row's total term magnitude (the per-element scale summed over the row: with
     # sum pi |log pi| = H and sum pi |log pi_ref| = H + KL it is 2|g_lp| + |g_kl| KL + |g_H| H +
