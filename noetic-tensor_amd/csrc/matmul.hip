@@ -353,13 +353,13 @@ __global__ void k_fold(const float *slices, int64_t outputs, int nkc, float *out
 // 128x128 tile: each wave a 64x64 quarter as 2x2 v_mfma_f32_32x32x16_bf16 tiles, over k panels of
 // 32 staged through LDS as bf16 ([row][k] for A, [column][k] for B, so that every MFMA operand
 // is one 16-byte LDS read: lane l takes row or column l % 32 and k 8 (l / 32) .. 8 (l / 32) + 7).
+// (The 64x64 tile takes k panels of 64.)
 // The next panel's f32 loads are issued before the current panel's MFMAs. Interior panels of an
 // operand whose view is contiguous along one axis (16-byte aligned) are staged four values per
 // load: along k they go to LDS as they are, along m or n each thread loads a 4x4 block and
 // transposes it in registers, so that every LDS store writes four bf16 of one row.
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
-constexpr int kHK = 32;   // k per panel
 constexpr int kHPad = 8;  // bf16 padding per LDS row (rows stay 16-byte aligned)
 
 __device__ __forceinline__ uint16_t bf16_bits(float x) {
@@ -373,10 +373,16 @@ __device__ __forceinline__ uint16_t bf16_bits(float x) {
 template <int T, bool AK, bool BN>
 __global__ __launch_bounds__(kMmThreads) void k_matmul_half(MatmulP p) {
     constexpr int kHT = T;
+    // k per panel: 64 for the 64 tile (longer panels cover more of the loads' latency); 32 for the
+    // 128 tile, whose registers would otherwise hold it to one wave per SIMD
+    constexpr int kHK = T == 64 ? 64 : 32;
     constexpr int W = T / 64;                         // MFMA tiles per wave along m and along n
     constexpr int kHLoads = kHT * kHK / kMmThreads;   // scalar f32 loads per operand and thread
     constexpr int kQuads = kHT * (kHK / 4) / kMmThreads;  // 16-byte loads along k per thread
     constexpr int kRG = kHT / 4;                      // 4x4 blocks along m or n
+    constexpr int kQ4 = kHK / 4;                      // 4-k groups along k
+    constexpr int kBlk = (kRG * kQ4 + kMmThreads - 1) / kMmThreads;  // 4x4 blocks per thread
+    constexpr int kRegs = kHLoads > 16 * kBlk ? kHLoads : 16 * kBlk;
     __shared__ __attribute__((aligned(16))) uint16_t As[kHT][kHK + kHPad];
     __shared__ __attribute__((aligned(16))) uint16_t Bs[kHT][kHK + kHPad];
     const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
@@ -401,57 +407,62 @@ __global__ __launch_bounds__(kMmThreads) void k_matmul_half(MatmulP p) {
     const float *b = p.b + bo;
     const int M = p.m, N = p.n, K = p.k;
 
-    float ra[16], rb[16];
-    // a 4x4 block (4 rows or columns by 4 k) per thread, for threads tid < 2 T
-    const int rg = tid % kRG, kg = tid / kRG;
-    const bool blk = kg < kHK / 4;
+    float ra[kRegs], rb[kRegs];
     // 16-byte staging for this panel? (an interior panel of a vector-eligible view)
     auto vec_a = [&](int k0) { return p.avec && row0 + kHT <= M && k0 + kHK <= K; };
     auto vec_b = [&](int k0) { return p.bvec && col0 + kHT <= N && k0 + kHK <= K; };
     auto load = [&](int k0) {
         if (vec_a(k0)) {
-            if constexpr (AK) {  // along k: group g covers row g / 8, k (g % 8) * 4 .. + 3
+            if constexpr (AK) {  // along k: group g covers row g / kQ4, k (g % kQ4) * 4 .. + 3
 #pragma unroll
                 for (int q = 0; q < kQuads; q++) {
                     const int g = tid + kMmThreads * q;
                     const float4 v =
-                        *reinterpret_cast<const float4 *>(a + int64_t(row0 + g / 8) * p.a_rs + k0 + (g % 8) * 4);
+                        *reinterpret_cast<const float4 *>(a + int64_t(row0 + g / kQ4) * p.a_rs + k0 + (g % kQ4) * 4);
                     ra[4 * q] = v.x;
                     ra[4 * q + 1] = v.y;
                     ra[4 * q + 2] = v.z;
                     ra[4 * q + 3] = v.w;
                 }
-            } else if (blk) {  // along m: rows rg * 4 .. + 3 at k kg * 4 + q
+            } else {  // along m: block id: rows (id % kRG) * 4 .. + 3 at k (id / kRG) * 4 + q
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const float4 v =
-                        *reinterpret_cast<const float4 *>(a + row0 + rg * 4 + int64_t(k0 + kg * 4 + q) * p.a_cs);
-                    ra[4 * q] = v.x;
-                    ra[4 * q + 1] = v.y;
-                    ra[4 * q + 2] = v.z;
-                    ra[4 * q + 3] = v.w;
+                for (int bb = 0; bb < kBlk; bb++) {
+                    const int id = tid + kMmThreads * bb, rg = id % kRG, kg = id / kRG;
+                    if (kg >= kQ4) continue;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const float4 v =
+                            *reinterpret_cast<const float4 *>(a + row0 + rg * 4 + int64_t(k0 + kg * 4 + q) * p.a_cs);
+                        ra[16 * bb + 4 * q] = v.x;
+                        ra[16 * bb + 4 * q + 1] = v.y;
+                        ra[16 * bb + 4 * q + 2] = v.z;
+                        ra[16 * bb + 4 * q + 3] = v.w;
+                    }
                 }
             }
         }
         if (vec_b(k0)) {
-            if constexpr (BN) {  // along n: columns rg * 4 .. + 3 at k kg * 4 + q
-                if (blk) {
+            if constexpr (BN) {  // along n: block id: columns (id % kRG) * 4 .. + 3 at k (id / kRG) * 4 + q
+#pragma unroll
+                for (int bb = 0; bb < kBlk; bb++) {
+                    const int id = tid + kMmThreads * bb, rg = id % kRG, kg = id / kRG;
+                    if (kg >= kQ4) continue;
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
                         const float4 v =
                             *reinterpret_cast<const float4 *>(b + int64_t(k0 + kg * 4 + q) * p.b_rs + col0 + rg * 4);
-                        rb[4 * q] = v.x;
-                        rb[4 * q + 1] = v.y;
-                        rb[4 * q + 2] = v.z;
-                        rb[4 * q + 3] = v.w;
+                        rb[16 * bb + 4 * q] = v.x;
+                        rb[16 * bb + 4 * q + 1] = v.y;
+                        rb[16 * bb + 4 * q + 2] = v.z;
+                        rb[16 * bb + 4 * q + 3] = v.w;
                     }
                 }
-            } else {  // along k: group g covers column g / 8, k (g % 8) * 4 .. + 3
+            } else {  // along k: group g covers column g / kQ4, k (g % kQ4) * 4 .. + 3
 #pragma unroll
                 for (int q = 0; q < kQuads; q++) {
                     const int g = tid + kMmThreads * q;
                     const float4 v =
-                        *reinterpret_cast<const float4 *>(b + int64_t(col0 + g / 8) * p.b_cs + k0 + (g % 8) * 4);
+                        *reinterpret_cast<const float4 *>(b + int64_t(col0 + g / kQ4) * p.b_cs + k0 + (g % kQ4) * 4);
                     rb[4 * q] = v.x;
                     rb[4 * q + 1] = v.y;
                     rb[4 * q + 2] = v.z;
@@ -498,12 +509,18 @@ __global__ __launch_bounds__(kMmThreads) void k_matmul_half(MatmulP p) {
 #pragma unroll
                 for (int q = 0; q < kQuads; q++) {
                     const int g = tid + kMmThreads * q;
-                    put4(&As[g / 8][(g % 8) * 4], ra[4 * q], ra[4 * q + 1], ra[4 * q + 2], ra[4 * q + 3]);
+                    put4(&As[g / kQ4][(g % kQ4) * 4], ra[4 * q], ra[4 * q + 1], ra[4 * q + 2], ra[4 * q + 3]);
                 }
-            } else if (blk) {
+            } else {
 #pragma unroll
-                for (int j = 0; j < 4; j++)  // row rg * 4 + j, k kg * 4 .. + 3
-                    put4(&As[rg * 4 + j][kg * 4], ra[j], ra[4 + j], ra[8 + j], ra[12 + j]);
+                for (int bb = 0; bb < kBlk; bb++) {
+                    const int id = tid + kMmThreads * bb, rg = id % kRG, kg = id / kRG;
+                    if (kg >= kQ4) continue;
+                    const float *w = ra + 16 * bb;
+#pragma unroll
+                    for (int j = 0; j < 4; j++)  // row rg * 4 + j, k kg * 4 .. + 3
+                        put4(&As[rg * 4 + j][kg * 4], w[j], w[4 + j], w[8 + j], w[12 + j]);
+                }
             }
         } else {
 #pragma unroll
@@ -515,16 +532,20 @@ __global__ __launch_bounds__(kMmThreads) void k_matmul_half(MatmulP p) {
         }
         if (vec_b(k0)) {
             if constexpr (BN) {
-                if (blk) {
+#pragma unroll
+                for (int bb = 0; bb < kBlk; bb++) {
+                    const int id = tid + kMmThreads * bb, rg = id % kRG, kg = id / kRG;
+                    if (kg >= kQ4) continue;
+                    const float *w = rb + 16 * bb;
 #pragma unroll
                     for (int j = 0; j < 4; j++)  // column rg * 4 + j, k kg * 4 .. + 3
-                        put4(&Bs[rg * 4 + j][kg * 4], rb[j], rb[4 + j], rb[8 + j], rb[12 + j]);
+                        put4(&Bs[rg * 4 + j][kg * 4], w[j], w[4 + j], w[8 + j], w[12 + j]);
                 }
             } else {
 #pragma unroll
                 for (int q = 0; q < kQuads; q++) {
                     const int g = tid + kMmThreads * q;
-                    put4(&Bs[g / 8][(g % 8) * 4], rb[4 * q], rb[4 * q + 1], rb[4 * q + 2], rb[4 * q + 3]);
+                    put4(&Bs[g / kQ4][(g % kQ4) * 4], rb[4 * q], rb[4 * q + 1], rb[4 * q + 2], rb[4 * q + 3]);
                 }
             }
         } else {
