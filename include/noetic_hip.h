@@ -97,13 +97,44 @@ uint64_t nt_hip_launches(void);
  * `ld` elements (ld >= V). A row is one (s, b, t) position. The float arithmetic is f32 with
  * bf16 inputs converted exactly (float.rs:61-67); per-row scalars are combined in f64. */
 
-/* Fused masked categorical sample + log-probability (+ entropy) of each row: one pass over
- * the logits and the mask. Replaces, for a Hip tensor, the op sequence of
- *   ids  = sample_categorical(logits, temperature, mask, rng)      (rl.rs:510-529)
+/* Gumbel-max categorical sample of each row: the reference's own sampler,
+ *   ids = sample_categorical(logits, temperature, mask, rng)        (rl.rs:488-529)
+ * for a Hip tensor. z = tempered_logits(logits, temperature, mask) in f32 (rl.rs:475-486: the
+ * f32 divide, skipped at temperature 1, then the f32 mask add; a u8 keep-mask puts -inf at an
+ * excluded token); g_i = f32(-ln(-ln u_i)) with u_i = ((k_i >> 11) + 0.5) / 2^53 from the i-th
+ * u64 k_i of the stream in row-major element order (one u64 per logit, rl.rs:490-498); the
+ * token is the first index of the maximum of z + g (argmax_dim, src/tensor/kernels.rs:183-209).
+ * The draws are generated on the device from the stream's ChaCha20 key and word position, so
+ * nothing of size rows x V crosses PCIe. The call does not move the caller's stream: after it
+ * has checked the status (a refused row draws nothing, as the reference panics before its
+ * draw, rl.rs:515-519), the caller advances the stream by rows x V u64 (nt_rng_skip_u64, or
+ * rand_chacha's set_word_pos) when temperature > 0. Temperature 0 is greedy: the first argmax
+ * of the masked logits, no draws. */
+typedef struct NtRlGumbelArgs {
+    const void *logits;       /* [rows, ld] f32 or bf16 */
+    int32_t dtype;            /* NT_F32 | NT_BF16 */
+    int32_t mask_kind;        /* NT_MASK_* */
+    int64_t rows, vocab, ld;
+    const void *mask;         /* u8 or f32 [rows or 1, mask_ld]; NULL with NT_MASK_NONE */
+    int64_t mask_ld;          /* mask row stride; 0 = one row shared by every logits row */
+    double temperature;       /* >= 0 and finite; 0 = greedy */
+    uint32_t key[8];          /* the stream's ChaCha20 key (its 32-byte seed as little-endian words) */
+    uint64_t block;           /* the stream's position: its next u64 starts at word `word` of */
+    int32_t word;             /*   keystream block `block` (nt_rng_word_pos); word in 0..15 */
+    int32_t pad0;
+    int32_t *ids;             /* [rows] out: the sampled token (-1 on a refused row) */
+    uint8_t *status;          /* [rows] out: NT_ROW_OK, NT_ROW_NO_TOKEN or NT_ROW_NAN (required) */
+} NtRlGumbelArgs;
+int nt_hip_rl_sample_gumbel(const NtRlGumbelArgs *a);
+
+/* Fused masked categorical sample + log-probability (+ entropy) of each row by the inverse
+ * CDF of one uniform per row: one pass over the logits and the mask. This is a new nn::rl
+ * entry (`sample_categorical_inv_cdf`; the reference has no counterpart), which does, for a
+ * Hip tensor, what the op sequence
+ *   ids  = <an inverse-CDF draw of softmax(z)>                      (cf. rl.rs:510-529)
  *   logp = token_log_probs(tempered_logits(logits, temperature, mask), ids)  (rl.rs:134-141)
  *   ent  = categorical_entropy(tempered_logits(...), None, TokenReduction::None) (rl.rs:405-414)
- * with the inverse-CDF draw of one uniform per row in place of Gumbel-max: with z the
- * tempered logits, m = max z, w_v = exp(z_v - m) and S = sum w, the token is
+ * would: with z the tempered logits, m = max z, w_v = exp(z_v - m) and S = sum w, the token is
  * min{v : sum_{j<=v} w_j > u*S} (excluded tokens have w = 0 and are never drawn; if rounding
  * leaves no crossing, the last token with w > 0). temperature 0 is greedy: the first argmax
  * of the masked logits (rl.rs:510-513), no uniform read; logp/entropy are then those of the

@@ -33,6 +33,16 @@ uint32_t nt_rng_next_u32(NtRng *r);
 uint64_t nt_rng_next_u64(NtRng *r);
 /* n uniforms on (0,1), one next_u64 each: ((k >> 11) + 0.5) / 2^53 (src/nn/rl.rs:493-494). */
 int nt_rng_uniforms(NtRng *r, size_t n, double *out);
+/* The stream's word position, rand_chacha 0.3.1's `get_word_pos` in two parts: the next unread
+ * keystream word is word `*word` (0..15) of block `*block`. The Gumbel sampler
+ * (nt_hip_rl_sample_gumbel) takes this position and generates the draws on the device. */
+int nt_rng_word_pos(const NtRng *r, uint64_t *block, int32_t *word);
+/* rand_chacha's `set_word_pos`: move the stream to word `word` (0..15) of block `block`. */
+int nt_rng_set_word_pos(NtRng *r, uint64_t block, int32_t word);
+/* Advance the stream by n u64 draws (2n keystream words) without handing them out: the state
+ * after n calls of nt_rng_next_u64 (the reference's sampler consumes one u64 per logit,
+ * src/nn/rl.rs:490-498, src/nn/tests/rl.rs:596-599). */
+int nt_rng_skip_u64(NtRng *r, uint64_t n);
 /* SHA-256 of data (src/hash.rs:6-7). */
 int nt_sha256(const void *data, size_t len, uint8_t out[32]);
 

@@ -149,6 +149,42 @@ uint64_t nt_rng_next_u64(NtRng *r) {
     return lo | uint64_t(nt_rng_next_u32(r)) << 32;
 }
 
+int nt_rng_word_pos(const NtRng *r, uint64_t *block, int32_t *word) {
+    if (!r || !block || !word || r->idx < 0 || r->idx > 16) return -1;
+    // buf holds block counter - 1 and idx is its next unread word; idx 16 (empty) is word 0 of
+    // block counter.
+    if (r->idx == 16) {
+        *block = r->counter;
+        *word = 0;
+    } else {
+        *block = r->counter - 1;
+        *word = r->idx;
+    }
+    return 0;
+}
+
+int nt_rng_set_word_pos(NtRng *r, uint64_t block, int32_t word) {
+    if (!r || word < 0 || word > 15) return -1;
+    if (word == 0) {
+        r->counter = block;
+        r->idx = 16;
+    } else {
+        chacha_block(r->key, block, r->buf);
+        r->counter = block + 1;
+        r->idx = word;
+    }
+    return 0;
+}
+
+int nt_rng_skip_u64(NtRng *r, uint64_t n) {
+    uint64_t block;
+    int32_t word;
+    if (nt_rng_word_pos(r, &block, &word)) return -1;
+    // 2n words past (block, word); n < 2^63
+    const uint64_t w = uint64_t(word) + 2 * (n % 8);
+    return nt_rng_set_word_pos(r, block + n / 8 + w / 16, int32_t(w % 16));
+}
+
 int nt_rng_uniforms(NtRng *r, size_t n, double *out) {
     if (!r || (!out && n)) return -1;
     for (size_t i = 0; i < n; i++) out[i] = (double(nt_rng_next_u64(r) >> 11) + 0.5) * 0x1p-53;

@@ -10,38 +10,13 @@
 #include "../../include/noetic_hip.h"
 #include "../../include/noetic_rng.h"
 #include "../../include/noetic_synth.h"
+#include "nt_chacha.hpp"
 #include "nt_internal.hpp"
 
 namespace nt {
 namespace {
 
-struct Key {
-    uint32_t k[8];
-};
-
-__device__ __forceinline__ uint32_t rotl(uint32_t x, int n) { return (x << n) | (x >> (32 - n)); }
-
-// ChaCha20 block `counter` of the stream keyed by `key` (stream id 0).
-__device__ void chacha_block_dev(const Key &key, uint64_t counter, uint32_t out[16]) {
-    uint32_t s[16] = {0x61707865u, 0x3320646eu, 0x79622d32u, 0x6b206574u,
-                      key.k[0], key.k[1], key.k[2], key.k[3], key.k[4], key.k[5], key.k[6], key.k[7],
-                      uint32_t(counter), uint32_t(counter >> 32), 0u, 0u};
-    uint32_t x[16];
-#pragma unroll
-    for (int i = 0; i < 16; i++) x[i] = s[i];
-#define NT_QR(a, b, c, d)                                   \
-    x[a] += x[b]; x[d] = rotl(x[d] ^ x[a], 16);             \
-    x[c] += x[d]; x[b] = rotl(x[b] ^ x[c], 12);             \
-    x[a] += x[b]; x[d] = rotl(x[d] ^ x[a], 8);              \
-    x[c] += x[d]; x[b] = rotl(x[b] ^ x[c], 7);
-    for (int r = 0; r < 10; r++) {
-        NT_QR(0, 4, 8, 12) NT_QR(1, 5, 9, 13) NT_QR(2, 6, 10, 14) NT_QR(3, 7, 11, 15)
-        NT_QR(0, 5, 10, 15) NT_QR(1, 6, 11, 12) NT_QR(2, 7, 8, 13) NT_QR(3, 4, 9, 14)
-    }
-#undef NT_QR
-#pragma unroll
-    for (int i = 0; i < 16; i++) out[i] = x[i] + s[i];
-}
+using Key = ChachaKey;
 
 __device__ __forceinline__ uint64_t u64_at(const uint32_t w[16], int j) {
     return uint64_t(w[2 * j]) | (uint64_t(w[2 * j + 1]) << 32);

@@ -44,6 +44,14 @@ class NtRlSampleArgs(C.Structure):
                 ("entropy", C.c_void_p), ("status", C.c_void_p)]
 
 
+class NtRlGumbelArgs(C.Structure):
+    _fields_ = [("logits", C.c_void_p), ("dtype", C.c_int32), ("mask_kind", C.c_int32),
+                ("rows", C.c_int64), ("vocab", C.c_int64), ("ld", C.c_int64),
+                ("mask", C.c_void_p), ("mask_ld", C.c_int64), ("temperature", C.c_double),
+                ("key", C.c_uint32 * 8), ("block", C.c_uint64), ("word", C.c_int32), ("pad0", C.c_int32),
+                ("ids", C.c_void_p), ("status", C.c_void_p)]
+
+
 class NtRlScoreArgs(C.Structure):
     _fields_ = [("logits", C.c_void_p), ("ref_logits", C.c_void_p), ("dtype", C.c_int32),
                 ("mask_kind", C.c_int32), ("rows", C.c_int64), ("vocab", C.c_int64), ("ld", C.c_int64),
@@ -108,6 +116,7 @@ _SIGS = {
     "nt_hip_stream": (C.c_int, [C.POINTER(C.c_void_p)]),
     "nt_hip_launches": (C.c_uint64, []),
     "nt_hip_rl_sample": (C.c_int, [C.POINTER(NtRlSampleArgs)]),
+    "nt_hip_rl_sample_gumbel": (C.c_int, [C.POINTER(NtRlGumbelArgs)]),
     "nt_hip_rl_score": (C.c_int, [C.POINTER(NtRlScoreArgs)]),
     "nt_hip_rl_score_backward": (C.c_int, [C.POINTER(NtRlScoreGradArgs)]),
     "nt_hip_rl_kl_estimate": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_int32, C.c_double,
@@ -152,6 +161,9 @@ _SIGS = {
     "nt_rng_next_u32": (C.c_uint32, [C.POINTER(NtRng)]),
     "nt_rng_next_u64": (C.c_uint64, [C.POINTER(NtRng)]),
     "nt_rng_uniforms": (C.c_int, [C.POINTER(NtRng), C.c_size_t, C.c_void_p]),
+    "nt_rng_word_pos": (C.c_int, [C.POINTER(NtRng), C.POINTER(C.c_uint64), C.POINTER(C.c_int32)]),
+    "nt_rng_set_word_pos": (C.c_int, [C.POINTER(NtRng), C.c_uint64, C.c_int32]),
+    "nt_rng_skip_u64": (C.c_int, [C.POINTER(NtRng), C.c_uint64]),
     "nt_sha256": (C.c_int, [C.c_char_p, C.c_size_t, C.c_char_p]),
     # noetic_synth.h
     "nt_synth_normal": (C.c_int, [C.POINTER(NtSynthNormal)]),
@@ -342,6 +354,16 @@ class Rng:
     def key(self):
         return (C.c_uint32 * 8)(*self.s.key)
 
+    def word_pos(self):
+        """(block, word): the next unread keystream word (rand_chacha `get_word_pos`)."""
+        b, w = C.c_uint64(), C.c_int32()
+        _check(lib().nt_rng_word_pos(C.byref(self.s), C.byref(b), C.byref(w)), "rng word_pos")
+        return int(b.value), int(w.value)
+
+    def skip_u64(self, n: int):
+        """The state after n next_u64 calls, without generating them."""
+        _check(lib().nt_rng_skip_u64(C.byref(self.s), n), "rng skip")
+
 
 # ----------------------------------------------------------------------------------- nn::rl
 
@@ -413,10 +435,11 @@ def _rows(x: Tensor):
 
 def sample_logp(logits: Tensor, temperature: float, mask: Optional[Tensor], rng: Optional[Rng],
                 entropy: bool = False, uniforms: Optional[Tensor] = None, check: bool = True):
-    """The fused path: (ids, logp[, entropy]) of the inverse-CDF sample of each row, drawing one
-    uniform per row from `rng` (none at temperature 0). `uniforms` (device f64 [rows]) may be
-    given instead of `rng`. `check` reads the per-row status and refuses a row with no allowed
-    token, as sample_categorical does (rl.rs:516-519)."""
+    """sample_categorical_inv_cdf with its log-probabilities, the fused path: (ids, logp[,
+    entropy]) of the inverse-CDF sample of each row, drawing one uniform per row from `rng`
+    (none at temperature 0). `uniforms` (device f64 [rows]) may be given instead of `rng`.
+    `check` reads the per-row status and refuses a row with no allowed token, as
+    sample_categorical does (rl.rs:516-519)."""
     if not (temperature >= 0.0 and math.isfinite(temperature)):
         raise ValueError(f"sample_categorical: temperature {temperature} (must be ≥ 0)")
     t = Tempered(logits, 1.0 if temperature == 0.0 else temperature, mask)
@@ -444,7 +467,36 @@ def sample_logp(logits: Tensor, temperature: float, mask: Optional[Tensor], rng:
 
 
 def sample_categorical(logits: Tensor, temperature: float, mask: Optional[Tensor], rng: Rng) -> Tensor:
-    """rl.rs:510-529 with the inverse-CDF draw (one uniform per row) in place of Gumbel-max."""
+    """rl.rs:510-529, the reference's Gumbel-max sampler: argmax(z + g) with z the tempered logits
+    and one Gumbel draw per logit from `rng` in row-major order, so the stream advances by one
+    u64 per logit (none at temperature 0). The draws are generated on the device at the stream's
+    position (nt_hip_rl_sample_gumbel); the stream is advanced here, after the rows are accepted:
+    a row with no allowed token is refused with the reference's message and draws nothing."""
+    if not (temperature >= 0.0 and math.isfinite(temperature)):
+        raise ValueError(f"sample_categorical: temperature {temperature} (must be ≥ 0)")
+    t = Tempered(logits, 1.0 if temperature == 0.0 else temperature, mask)
+    rows, V = _rows(logits)
+    out_shape = logits.shape[:-1]
+    ids = IntTensor(out_shape)
+    status = Tensor(out_shape, "u8")
+    kind, mptr, mld = _mask_fields(t, rows, V)
+    block, word = rng.word_pos()
+    a = NtRlGumbelArgs(logits.ptr, _dtype_code(logits), kind, rows, V, V, mptr, mld, float(temperature),
+                       rng.key(), block, word, 0, ids.ptr, status.ptr)
+    _check(lib().nt_hip_rl_sample_gumbel(C.byref(a)), "sample_categorical")
+    st = status.to_numpy().ravel()
+    bad = np.nonzero(st != NT_ROW_OK)[0]
+    if bad.size:
+        raise ValueError(f"sample_categorical: position {bad[0]} has no allowed token (every logit −∞ or a NaN)")
+    if temperature != 0.0:
+        rng.skip_u64(rows * V)
+    return ids
+
+
+def sample_categorical_inv_cdf(logits: Tensor, temperature: float, mask: Optional[Tensor], rng: Rng) -> Tensor:
+    """A new nn::rl entry beside sample_categorical (rl.rs:510-529): the same distribution, drawn
+    by the inverse CDF of one uniform per row (one u64 of `rng` per row, none at temperature 0)
+    in one fused pass over the logits. `sample_logp` also returns the tokens' log-probabilities."""
     return sample_logp(logits, temperature, mask, rng)[0]
 
 

@@ -465,13 +465,23 @@ void or_cpuref_log_softmax(const float *x, int64_t rows, int64_t V, float *y) {
 
 /* tempered_logits over [rows, V]: a materialised divide, then a materialised broadcast add of
  * the additive form of the keep-mask (0 / -inf), as the reference's op sequence runs. */
-static float *cpuref_tempered(const float *x, int64_t rows, int64_t V, double tau,
-                              const uint8_t *keep, int64_t keep_ld) {
+/* tempered_logits (rl.rs:475-486) as CpuRef materialises it: div_scalar (skipped at tau 1,
+ * float.rs:494-499), then the broadcast add of the additive mask, f32 throughout. A u8 keep
+ * row stands for the additive row (0 kept, -inf excluded). */
+static float *cpuref_tempered_add(const float *x, int64_t rows, int64_t V, double tau,
+                                  const float *addmask, int64_t add_ld, const uint8_t *keep, int64_t keep_ld) {
     size_t n = (size_t)rows * (size_t)V;
     float *z = (float *)malloc(n * sizeof(float));
     float t = (float)tau;
     if (tau == 1.0) memcpy(z, x, n * sizeof(float));
     else for (size_t i = 0; i < n; i++) z[i] = x[i] / t;
+    if (addmask) {
+        float *z2 = (float *)malloc(n * sizeof(float));
+        for (int64_t r = 0; r < rows; r++)
+            for (int64_t v = 0; v < V; v++) z2[r * V + v] = z[r * V + v] + addmask[r * add_ld + v];
+        free(z);
+        z = z2;
+    }
     if (keep) {
         int64_t mrows = keep_ld == 0 ? 1 : rows;
         float *add = (float *)malloc((size_t)mrows * (size_t)V * sizeof(float));
@@ -485,6 +495,36 @@ static float *cpuref_tempered(const float *x, int64_t rows, int64_t V, double ta
         z = z2;
     }
     return z;
+}
+
+static float *cpuref_tempered(const float *x, int64_t rows, int64_t V, double tau,
+                              const uint8_t *keep, int64_t keep_ld) {
+    return cpuref_tempered_add(x, rows, V, tau, NULL, 0, keep, keep_ld);
+}
+
+int64_t or_cpuref_sample_gumbel(const float *x, int64_t rows, int64_t V, double tau, const float *addmask,
+                                int64_t add_ld, const uint8_t *keep, int64_t keep_ld, or_chacha *rng, int64_t *ids) {
+    size_t n = (size_t)rows * (size_t)V;
+    float *z = cpuref_tempered_add(x, rows, V, tau == 0.0 ? 1.0 : tau, addmask, add_ld, keep, keep_ld);
+    for (int64_t r = 0; r < rows; r++) { /* max_dim + host check (rl.rs:515-519), before any draw */
+        float m = first_max_f32(z + r * V, V, NULL);
+        if (m != m || m == -INFINITY) {
+            free(z);
+            return 1 + r;
+        }
+    }
+    if (tau != 0.0) {
+        /* gumbel (rl.rs:490-498): one u64 per element in row-major order, f64 noise, cast to
+         * f32 by from_f64s (float.rs:257-260), then z + g in f32. */
+        for (size_t i = 0; i < n; i++) {
+            double u = or_uniform_open01(or_chacha_next_u64(rng));
+            float g = (float)(-log(-log(u)));
+            z[i] = z[i] + g;
+        }
+    }
+    for (int64_t r = 0; r < rows; r++) first_max_f32(z + r * V, V, &ids[r]);
+    free(z);
+    return 0;
 }
 
 int64_t or_cpuref_sample_logp(const float *x, int64_t rows, int64_t V, double tau,
@@ -749,6 +789,42 @@ void or_reference_rnd_f32(uint64_t seed, uint64_t inc, int64_t n, float lo, floa
             volatile float v01 = v.f - 1.0f;
             volatile float prod = v01 * scale;
             const float res = prod + lo;
+            if (res < hi) {
+                out[i] = res;
+                break;
+            }
+        }
+    }
+}
+
+/* The nn tests' helper rnd (src/nn/tests/mod.rs:35-38): ChaCha8Rng::seed_from_u64(seed), then n
+ * draws of rand 0.8's gen_range(lo..hi) for f64: a u64 from the stream (two consecutive words,
+ * low first), its top 52 bits as the mantissa of a value in [1, 2), minus 1, times (hi - lo),
+ * plus lo (f64 arithmetic, no fused multiply-add), drawn again in the rare case the result
+ * reaches hi. */
+void or_reference_rnd_f64(uint64_t seed, uint64_t inc, int64_t n, double lo, double hi, double *out) {
+    uint8_t sd[32];
+    or_seed_from_u64(seed, inc, sd);
+    or_chacha r;
+    or_chacha_seed(&r, sd);
+    const double scale = hi - lo;
+    for (int64_t i = 0; i < n; i++) {
+        for (;;) {
+            uint32_t w[2];
+            for (int h = 0; h < 2; h++) {
+                if (r.idx >= 16) {
+                    or_chacha_block_rounds(r.key, r.counter, 0, 8, r.buf);
+                    r.counter++;
+                    r.idx = 0;
+                }
+                w[h] = r.buf[r.idx++];
+            }
+            const uint64_t u = (uint64_t)w[0] | ((uint64_t)w[1] << 32);
+            union { uint64_t b; double f; } v;
+            v.b = (u >> 12) | 0x3ff0000000000000ull;
+            volatile double v01 = v.f - 1.0;
+            volatile double prod = v01 * scale;
+            const double res = prod + lo;
             if (res < hi) {
                 out[i] = res;
                 break;

@@ -47,6 +47,7 @@ void or_chacha_block(const uint32_t key[8], uint64_t counter, uint64_t stream, u
 void or_chacha_block_rounds(const uint32_t key[8], uint64_t counter, uint64_t stream, int rounds, uint32_t out[16]);
 void or_seed_from_u64(uint64_t state, uint64_t inc, uint8_t seed[32]);
 void or_reference_rnd_f32(uint64_t seed, uint64_t inc, int64_t n, float lo, float hi, float *out);
+void or_reference_rnd_f64(uint64_t seed, uint64_t inc, int64_t n, double lo, double hi, double *out);
 /* One f32 product in the reference's matmul order: fmaf chains over k closed every 256. */
 void or_matmul_f32(const float *a, int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs, int64_t b_cs,
                    int64_t m, int64_t k, int64_t n, float *c);
@@ -148,6 +149,12 @@ void or_cpuref_log_softmax(const float *x, int64_t rows, int64_t V, float *y);
 int64_t or_cpuref_sample_logp(const float *x, int64_t rows, int64_t V, double tau,
                               const uint8_t *keep, int64_t keep_ld, or_chacha *rng,
                               int64_t *ids, float *logp);
+/* sample_categorical alone (rl.rs:510-529) on Cpu(Reference), with either mask form: addmask
+ * is an additive f32 mask [rows or 1, V] (add_ld 0 = one shared row), keep a u8 keep-mask
+ * (0 = -inf). The refusal check (first maximum NaN or -inf, rl.rs:515-519) runs before any
+ * draw, so a refused call leaves the stream untouched. Returns 0, or 1 + the first refused row. */
+int64_t or_cpuref_sample_gumbel(const float *x, int64_t rows, int64_t V, double tau, const float *addmask,
+                                int64_t add_ld, const uint8_t *keep, int64_t keep_ld, or_chacha *rng, int64_t *ids);
 /* The same sequence with the inverse-CDF draw in place of Gumbel-max (one uniform per row),
  * still unfused and in f32 where the reference is f32: the "port" CPU baseline of the fused
  * path. threads > 1 splits rows across pthreads (Cpu(Fast)-style, backend.rs:59-72). */

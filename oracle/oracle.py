@@ -79,6 +79,7 @@ def lib():
         L.or_reduce_tokens.argtypes = [_c_double_p, _c_double_p, C.c_int64, C.c_int64, C.c_int64, C.c_int, _c_double_p]
         L.or_reduce_tokens.restype = C.c_int64
         L.or_reference_rnd_f32.argtypes = [C.c_uint64, C.c_uint64, C.c_int64, C.c_float, C.c_float, _c_float_p]
+        L.or_reference_rnd_f64.argtypes = [C.c_uint64, C.c_uint64, C.c_int64, C.c_double, C.c_double, _c_double_p]
         L.or_policy_loss.argtypes = [C.c_int, C.c_int64, C.c_int64, _c_double_p, _c_double_p, _c_double_p, C.c_int,
                                      _c_double_p, C.c_double, C.c_double, C.c_double, C.c_double, _c_double_p,
                                      _c_double_p, _c_double_p]
@@ -95,6 +96,9 @@ def lib():
         L.or_cpuref_sample_logp.argtypes = [_c_float_p, C.c_int64, C.c_int64, C.c_double, _c_u8_p, C.c_int64,
                                             C.POINTER(ChaCha), _c_int64_p, _c_float_p]
         L.or_cpuref_sample_logp.restype = C.c_int64
+        L.or_cpuref_sample_gumbel.argtypes = [_c_float_p, C.c_int64, C.c_int64, C.c_double, _c_float_p, C.c_int64,
+                                              _c_u8_p, C.c_int64, C.POINTER(ChaCha), _c_int64_p]
+        L.or_cpuref_sample_gumbel.restype = C.c_int64
         L.or_cpu_sample_logp_invcdf.argtypes = [_c_float_p, C.c_int64, C.c_int64, C.c_double, _c_u8_p, C.c_int64,
                                                 _c_double_p, _c_int64_p, _c_float_p, C.c_int]
         L.or_cpu_sample_logp_invcdf.restype = C.c_int64
@@ -286,6 +290,14 @@ def reference_rnd_f32(seed, n, lo, hi):
     return out
 
 
+def reference_rnd_f64(seed, n, lo, hi):
+    """The nn tests' helper rnd (src/nn/tests/mod.rs:35-38): ChaCha8Rng::seed_from_u64 then
+    gen_range(lo..hi) as f64 (or_reference_rnd_f64)."""
+    out = np.empty(n, dtype=np.float64)
+    lib().or_reference_rnd_f64(seed, PCG32_INC, n, lo, hi, _ptr(out, _c_double_p))
+    return out
+
+
 def _d(a):
     return None if a is None else np.ascontiguousarray(a, dtype=np.float64).ravel()
 
@@ -393,6 +405,26 @@ def cpuref_sample_logp(x, tau, keep, rng: Rng):
     if rc:
         raise ValueError(f"sample_categorical: position {rc - 1} has no allowed token (every logit −∞ or a NaN)")
     return ids, lp
+
+
+def cpuref_sample_gumbel(x, tau, rng: Rng, addmask=None, keep=None):
+    """The reference's sample_categorical (rl.rs:510-529) on Cpu(Reference): ids [R] of rows
+    x [R, V] under an additive f32 mask [R or 1, V] or a u8 keep-mask; one u64 of `rng` per
+    logit (none at tau 0 or when a row is refused)."""
+    x = _f32(np.atleast_2d(x))
+    R, V = x.shape
+    am = None if addmask is None else _f32(np.atleast_2d(addmask))
+    kp = None if keep is None else np.ascontiguousarray(np.atleast_2d(keep), dtype=np.uint8)
+    ids = np.empty(R, dtype=np.int64)
+    rc = lib().or_cpuref_sample_gumbel(_ptr(x, _c_float_p), R, V, tau,
+                                       None if am is None else _ptr(am, _c_float_p),
+                                       0 if am is None or am.shape[0] == 1 else V,
+                                       None if kp is None else _ptr(kp, _c_u8_p),
+                                       0 if kp is None or kp.shape[0] == 1 else V,
+                                       C.byref(rng.s), _ptr(ids, _c_int64_p))
+    if rc:
+        raise ValueError(f"sample_categorical: position {rc - 1} has no allowed token (every logit −∞ or a NaN)")
+    return ids
 
 
 def cpu_sample_logp_invcdf(x, tau, keep, u, threads=1):

@@ -44,7 +44,8 @@ def test_argument_struct_layouts_match_the_header():
     fields = {"NtRlSampleArgs": [f[0] for f in nr.NtRlSampleArgs._fields_],
               "NtRlScoreArgs": [f[0] for f in nr.NtRlScoreArgs._fields_],
               "NtRlScoreGradArgs": [f[0] for f in nr.NtRlScoreGradArgs._fields_],
-              "NtRlPolicyLossArgs": [f[0] for f in nr.NtRlPolicyLossArgs._fields_]}
+              "NtRlPolicyLossArgs": [f[0] for f in nr.NtRlPolicyLossArgs._fields_],
+              "NtRlGumbelArgs": [f[0] for f in nr.NtRlGumbelArgs._fields_]}
     body = []
     for st, fs in fields.items():
         body.append(f'printf("{st} %zu\\n", sizeof({st}));')
@@ -64,6 +65,7 @@ def test_argument_struct_layouts_match_the_header():
             assert int(got[f"{st}.{f}"]) == getattr(cls, f).offset, (st, f)
     assert int(got["NtRlSampleArgs"]) == 104 and int(got["NtRlScoreArgs"]) == 152
     assert int(got["NtRlScoreGradArgs"]) == 176 and int(got["NtRlPolicyLossArgs"]) == 120
+    assert int(got["NtRlGumbelArgs"]) == 128
 
 
 def test_without_a_claimed_device_calls_fail_cleanly():
@@ -142,6 +144,43 @@ def test_product_stream_equals_the_oracle_stream():
     out = C.create_string_buffer(32)
     nr.lib().nt_sha256(b"abc", 3, out)
     assert out.raw.hex() == "ba7816bf8f01cfea414140de5dae2223b00361a396177a9cb410ff61f20015ad"
+
+
+def test_stream_positions_and_skips_equal_the_draws():
+    # nt_rng_word_pos / set_word_pos / skip_u64 (rand_chacha's get_word_pos / set_word_pos): the
+    # Gumbel sampler generates its draws at the stream's position and then advances the stream by
+    # one u64 per logit (src/nn/tests/rl.rs:596-599); that must equal drawing them one by one,
+    # from every word offset inside a block (odd offsets after a next_u32 included)
+    for pre in range(0, 17):
+        for n in (0, 1, 7, 8, 9, 63, 64, 65, 1000, 12345):
+            a, b = nr.Rng(3, "skip"), nr.Rng(3, "skip")
+            for _ in range(pre):
+                a.next_u32()
+                b.next_u32()
+            blk, word = a.word_pos()
+            assert 16 * blk + word == pre
+            a.skip_u64(n)
+            for _ in range(n):
+                b.next_u64()
+            assert a.word_pos() == b.word_pos()
+            assert [a.next_u64() for _ in range(5)] == [b.next_u64() for _ in range(5)], (pre, n)
+    r = nr.Rng(4, "pos")
+    assert nr.lib().nt_rng_set_word_pos(C.byref(r.s), 1000, 5) == 0
+    assert r.word_pos() == (1000, 5)
+    w = O.chacha_block(list(r.s.key), 1000)
+    assert r.next_u32() == w[5] and r.next_u64() == w[6] | (w[7] << 32)
+    assert nr.lib().nt_rng_set_word_pos(C.byref(r.s), 0, 16) == -1
+
+
+def test_gumbel_sampler_arguments_are_checked_before_the_device():
+    L = nr.lib()
+    a = nr.NtRlGumbelArgs(None, nr.NT_F32, nr.NT_MASK_NONE, 4, 16, 16, None, 0, 1.0)
+    a.word = 16
+    assert L.nt_hip_rl_sample_gumbel(C.byref(a)) == -1
+    assert b"word" in L.nt_hip_last_error()
+    a.word, a.temperature = 0, float("nan")
+    assert L.nt_hip_rl_sample_gumbel(C.byref(a)) == -1
+    assert "temperature" in L.nt_hip_last_error().decode()
 
 
 def test_runs_mask_generator_host():

@@ -338,6 +338,50 @@ def test_cpuref_gumbel_sampler_frequencies_and_consumption():
                              O.Rng(0, "x"))
 
 
+def test_cpuref_gumbel_with_additive_masks_is_the_references_sampler_test():
+    # tests/rl.rs:579-625 on or_cpuref_sample_gumbel (the checker of the device's Gumbel sampler):
+    # 40,000 copies of one row under an additive [1, V] mask, frequencies within 4.5 s.e., one u64
+    # per logit, the same stream the same tokens and another stream other tokens; greedy is the
+    # masked argmax [4, 4] and draws nothing; a refused row draws nothing.
+    row = f32([0.4, -1.0, 1.2, 3.0, 0.0, -0.3])
+    maskrow = f32([[0.0, 0.0, 0.0, -np.inf, 0.5, 0.0]])
+    n, v = 40_000, 6
+    x = np.repeat(row[None, :], n, 0)
+    for tau in (0.7, 1.0, 2.5):
+        rng, copy = O.Rng(5, "sampler test"), O.Rng(5, "sampler test")
+        tok = O.cpuref_sample_gumbel(x, tau, rng, addmask=maskrow)
+        for _ in range(n * v):
+            copy.next_u64()
+        assert rng.next_u64() == copy.next_u64(), "one u64 per logit"
+        p = np.exp(log_softmax(row.astype(np.float64) / tau + maskrow[0].astype(np.float64)))
+        cnt = np.bincount(tok, minlength=v)
+        assert cnt[3] == 0
+        se = np.sqrt(p * (1 - p) / n)
+        assert np.all(np.abs(cnt / n - p) <= 4.5 * se + 1e-12), (tau, cnt / n, p)
+        assert np.array_equal(O.cpuref_sample_gumbel(x, tau, O.Rng(5, "sampler test"), addmask=maskrow), tok)
+        assert not np.array_equal(O.cpuref_sample_gumbel(x, tau, O.Rng(6, "sampler test"), addmask=maskrow), tok)
+    # the keep-mask form gives the additive form's tokens (0 / -inf)
+    keep = np.array([[1, 1, 1, 0, 1, 1]], np.uint8)
+    zero_half = f32([[0.0, 0.0, 0.0, -np.inf, 0.0, 0.0]])
+    assert np.array_equal(O.cpuref_sample_gumbel(x[:500], 0.9, O.Rng(1, "k"), keep=keep),
+                          O.cpuref_sample_gumbel(x[:500], 0.9, O.Rng(1, "k"), addmask=zero_half))
+    # greedy (tests/rl.rs:617-625)
+    greedy_mask = f32([[0.0, 0.0, 0.0, -np.inf, 2.0, 0.0]])
+    rng, copy = O.Rng(1, "greedy"), O.Rng(1, "greedy")
+    assert O.cpuref_sample_gumbel(np.stack([row, row]), 0.0, rng, addmask=greedy_mask).tolist() == [4, 4]
+    assert rng.next_u64() == copy.next_u64(), "greedy draws nothing"
+    # a refused row draws nothing (the reference's check precedes its draw, rl.rs:515-519)
+    rng, copy = O.Rng(0, "x"), O.Rng(0, "x")
+    with pytest.raises(ValueError, match="position 1 has no allowed token"):
+        O.cpuref_sample_gumbel(f32(np.zeros((2, 3))), 1.0, rng, addmask=f32([[0, 0, 0], [-np.inf] * 3]))
+    assert rng.next_u64() == copy.next_u64()
+    # V = 2 in closed form: P(token 0) = sigmoid(z0 - z1)
+    n2 = 50_000
+    tok = O.cpuref_sample_gumbel(np.repeat(f32([[0.3, -0.9]]), n2, 0), 1.0, O.Rng(8, "two"))
+    p0 = 1.0 / (1.0 + math.exp(-(0.3 - -0.9)))
+    assert abs(np.mean(tok == 0) - p0) <= 4.5 * math.sqrt(p0 * (1 - p0) / n2)
+
+
 # ------------------------------------------------------------------------ golden C1 fixture
 
 def test_c1_golden_fixture():

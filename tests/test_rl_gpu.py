@@ -152,11 +152,12 @@ def test_greedy_is_the_first_masked_argmax():
 def test_rows_with_no_allowed_token_are_refused():
     x = nr.Tensor.from_numpy(np.zeros((2, 3), np.float32))
     keep = nr.Tensor.from_numpy(np.array([[1, 1, 1], [0, 0, 0]], np.uint8))
-    with pytest.raises(ValueError, match="position 1 has no allowed token"):
-        nr.sample_categorical(x, 1.0, keep, nr.Rng(0, "x"))
     nanrow = nr.Tensor.from_numpy(np.array([[0.0, np.nan, 1.0], [0.0, 1.0, 2.0]], np.float32))
-    with pytest.raises(ValueError, match="position 0"):
-        nr.sample_categorical(nanrow, 1.0, None, nr.Rng(0, "x"))
+    for sampler in (nr.sample_categorical, nr.sample_categorical_inv_cdf):
+        with pytest.raises(ValueError, match="position 1 has no allowed token"):
+            sampler(x, 1.0, keep, nr.Rng(0, "x"))
+        with pytest.raises(ValueError, match="position 0"):
+            sampler(nanrow, 1.0, None, nr.Rng(0, "x"))
 
 
 def test_additive_minus_1e9_equals_minus_infinity_to_the_bit():
@@ -178,13 +179,13 @@ def test_additive_minus_1e9_equals_minus_infinity_to_the_bit():
         assert a == b
 
 
-def test_reference_sampler_body_shape():
-    # src/nn/tests/gpu/rl.rs:155-174: [4,128,96] logits in [-3,3], mask k%7==3 -> -inf,
-    # temperatures 1, 0.7 and 0 (greedy)
-    rng = np.random.default_rng(960)
+def test_inv_cdf_sampler_on_the_reference_body_inputs():
+    # The inverse-CDF entry on the inputs of src/nn/tests/gpu/rl.rs:155-174 (rnd(n V, 960, -3, 3),
+    # mask k%7==3 -> -inf, temperatures 1, 0.7 and 0), against the oracle's inverse-CDF draw for
+    # the same uniforms (the reference's Gumbel sampler body itself runs in test_gumbel_gpu.py).
     shape = (4, 128, 96)
     n = 4 * 128
-    x = rng.uniform(-3, 3, shape).astype(np.float32)
+    x = O.reference_rnd_f64(960, n * 96, -3.0, 3.0).astype(np.float32).reshape(shape)
     mask = np.array([[[-np.inf if k % 7 == 3 else 0.0 for k in range(96)]]], np.float32)
     xt, mt = nr.Tensor.from_numpy(x), nr.Tensor.from_numpy(mask)
     for tau, root in [(1.0, 11), (0.7, 12), (0.0, 13)]:
@@ -203,13 +204,18 @@ def test_reference_sampler_body_shape():
 
 
 def test_frequencies_over_many_rows_on_device():
-    # the reference's frequency check (tests/rl.rs:579-611) on the device sampler
+    # the reference's frequency check (tests/rl.rs:579-611) on the inverse-CDF entry; one u64 per
+    # row consumed
     row = np.array([0.4, -1.0, 1.2, 3.0, 0.0, -0.3], np.float32)
     n = 40_000
     x = nr.Tensor.from_numpy(np.repeat(row[None, :], n, 0))
     mask = nr.Tensor.from_numpy(np.array([[0.0, 0.0, 0.0, -np.inf, 0.5, 0.0]], np.float32))
     for tau in (0.7, 2.5):
-        ids = nr.sample_categorical(x, tau, mask, nr.Rng(5, "sampler test")).to_numpy()
+        rng = nr.Rng(5, "sampler test")
+        copy = rng.clone()
+        ids = nr.sample_categorical_inv_cdf(x, tau, mask, rng).to_numpy()
+        copy.skip_u64(n)
+        assert rng.next_u64() == copy.next_u64(), "one u64 per row"
         p = np.exp(log_softmax(row.astype(np.float64) / tau + np.array([0, 0, 0, -np.inf, 0.5, 0])))
         cnt = np.bincount(ids, minlength=6)
         assert cnt[3] == 0
