@@ -25,1151 +25,10 @@
 // for the policy and (max, sum exp) for the reference, rescaled when its max grows (online
 // log-sum-exp); waves and then the workgroup merge them in a fixed order; per-row scalars are
 // finished in f64.
-#include <hip/hip_runtime.h>
-
-#include <cfloat>
-#include <cmath>
-#include <cstdint>
-#include <cstdio>
-#include <string>
-#include <type_traits>
-
-#include "../../include/noetic_hip.h"
-#include "nt_internal.hpp"
+#include "nt_rows.hpp"
 
 namespace nt {
 namespace {
-
-constexpr int kWave = 64;
-constexpr int kEpl = 8;                  // elements per lane per chunk
-constexpr int kChunk = kWave * kEpl;     // 512 elements per chunk
-constexpr int kBatch = 4;                // chunks per wave with loads in flight together
-// The most a lane's 8 weights of one chunk may sum to before its exponent reference moves to the
-// chunk's maximum, where a finishing difference of two log-sums must stay small (entropy, KL):
-// the reference then trails the maximum by at most log2 32 = 5 (log2 units).
-constexpr float kChunkSumCap = 32.0f;
-constexpr float kLog2e = 1.44269504088896340736f;
-constexpr double kLn2 = 0.69314718055994530942;
-constexpr int kRowBadToken = NT_ROW_BAD_TOKEN;
-
-// ------------------------------------------------------------------ element access
-
-template <int DT>
-struct Elem;
-template <>
-struct Elem<NT_F32> {
-    static constexpr int kWords = 8;     // 8 f32 per lane per chunk
-    static constexpr uint32_t kNegInf = 0xff800000u;
-    static constexpr int kBytes = 4;
-};
-template <>
-struct Elem<NT_BF16> {
-    static constexpr int kWords = 4;     // 8 bf16 packed two per word
-    static constexpr uint32_t kNegInf = 0xff80ff80u;
-    static constexpr int kBytes = 2;
-};
-
-template <int MK>
-struct MaskWords {
-    static constexpr int kWords = MK == NT_MASK_U8 ? 2 : (MK == NT_MASK_F32 ? 8 : 0);
-    static constexpr int kBytes = MK == NT_MASK_U8 ? 1 : (MK == NT_MASK_F32 ? 4 : 0);
-};
-
-// The raw bits of one lane's 8 elements of one chunk (logits and mask).
-template <int DT, int MK>
-struct Raw {
-    uint32_t x[Elem<DT>::kWords];
-    uint32_t m[MaskWords<MK>::kWords > 0 ? MaskWords<MK>::kWords : 1];
-};
-
-// Load the 8 elements at e0 of a row. AL: the row and mask are 16-/8-byte aligned and V % 8
-// == 0, so a lane's 8 elements are all inside the row or all outside it. Elements outside
-// the row read as -inf logits.
-template <int DT, int MK, bool AL>
-__device__ __forceinline__ void load_raw(Raw<DT, MK> &r, const void *xrow, const void *mrow, int64_t e0,
-                                         int64_t V) {
-    if constexpr (MK == NT_MASK_NONE) r.m[0] = 0;
-    if constexpr (AL) {
-        if (e0 < V) {
-            if constexpr (DT == NT_F32) {
-                const uint4 *q = reinterpret_cast<const uint4 *>(static_cast<const float *>(xrow) + e0);
-                uint4 a = q[0], b = q[1];
-                r.x[0] = a.x; r.x[1] = a.y; r.x[2] = a.z; r.x[3] = a.w;
-                r.x[4] = b.x; r.x[5] = b.y; r.x[6] = b.z; r.x[7] = b.w;
-            } else {
-                uint4 a = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(xrow) + e0);
-                r.x[0] = a.x; r.x[1] = a.y; r.x[2] = a.z; r.x[3] = a.w;
-            }
-            if constexpr (MK == NT_MASK_U8) {
-                uint2 k = *reinterpret_cast<const uint2 *>(static_cast<const uint8_t *>(mrow) + e0);
-                r.m[0] = k.x; r.m[1] = k.y;
-            } else if constexpr (MK == NT_MASK_F32) {
-                const uint4 *q = reinterpret_cast<const uint4 *>(static_cast<const float *>(mrow) + e0);
-                uint4 a = q[0], b = q[1];
-                r.m[0] = a.x; r.m[1] = a.y; r.m[2] = a.z; r.m[3] = a.w;
-                r.m[4] = b.x; r.m[5] = b.y; r.m[6] = b.z; r.m[7] = b.w;
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < Elem<DT>::kWords; i++) r.x[i] = Elem<DT>::kNegInf;
-#pragma unroll
-            for (int i = 0; i < (MaskWords<MK>::kWords > 0 ? MaskWords<MK>::kWords : 1); i++) r.m[i] = 0;
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < kEpl; j++) {
-            const int64_t e = e0 + j;
-            const bool in = e < V;
-            if constexpr (DT == NT_F32) {
-                r.x[j] = in ? __float_as_uint(static_cast<const float *>(xrow)[e]) : Elem<DT>::kNegInf;
-            } else {
-                uint32_t h = in ? uint32_t(static_cast<const uint16_t *>(xrow)[e]) : 0xff80u;
-                if (j % 2 == 0) r.x[j / 2] = h;
-                else r.x[j / 2] |= h << 16;
-            }
-            if constexpr (MK == NT_MASK_U8) {
-                uint32_t k = in ? uint32_t(static_cast<const uint8_t *>(mrow)[e]) : 0u;
-                if (j % 4 == 0) r.m[j / 4] = k;
-                else r.m[j / 4] |= k << (8 * (j % 4));
-            } else if constexpr (MK == NT_MASK_F32) {
-                r.m[j] = in ? __float_as_uint(static_cast<const float *>(mrow)[e]) : 0u;
-            }
-        }
-    }
-}
-
-// Aligned load of the 8 elements at e0 with no bounds test (the caller passes an in-bounds
-// e0), so that a run of these loads is straight-line code the compiler can wait on one by one.
-template <int DT, int MK>
-__device__ __forceinline__ void load_raw_inbounds(Raw<DT, MK> &r, const void *xrow, const void *mrow, int64_t e0) {
-    if constexpr (DT == NT_F32) {
-        const uint4 *q = reinterpret_cast<const uint4 *>(static_cast<const float *>(xrow) + e0);
-        uint4 a = q[0], b = q[1];
-        r.x[0] = a.x; r.x[1] = a.y; r.x[2] = a.z; r.x[3] = a.w;
-        r.x[4] = b.x; r.x[5] = b.y; r.x[6] = b.z; r.x[7] = b.w;
-    } else {
-        uint4 a = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(xrow) + e0);
-        r.x[0] = a.x; r.x[1] = a.y; r.x[2] = a.z; r.x[3] = a.w;
-    }
-    if constexpr (MK == NT_MASK_U8) {
-        uint2 k = *reinterpret_cast<const uint2 *>(static_cast<const uint8_t *>(mrow) + e0);
-        r.m[0] = k.x; r.m[1] = k.y;
-    } else if constexpr (MK == NT_MASK_F32) {
-        const uint4 *q = reinterpret_cast<const uint4 *>(static_cast<const float *>(mrow) + e0);
-        uint4 a = q[0], b = q[1];
-        r.m[0] = a.x; r.m[1] = a.y; r.m[2] = a.z; r.m[3] = a.w;
-        r.m[4] = b.x; r.m[5] = b.y; r.m[6] = b.z; r.m[7] = b.w;
-    } else {
-        r.m[0] = 0;
-    }
-}
-
-// Logit j of a lane's chunk as f32 (bf16 widened exactly).
-template <int DT>
-__device__ __forceinline__ float logit(const uint32_t *x, int j) {
-    if constexpr (DT == NT_F32) return __uint_as_float(x[j]);
-    else return __uint_as_float((j % 2 == 0) ? (x[j / 2] << 16) : (x[j / 2] & 0xffff0000u));
-}
-
-// The "value" of an element, the quantity the kernels take maxima and exponentials of.
-//  - no mask / u8 mask: v = x (an excluded token -> -inf); the temperature is applied through
-//    the exponent scale c = log2(e)/T, and m_z = max(x)/T is exact because correctly rounded
-//    division by T > 0 is monotonic.
-//  - additive f32 mask: v = z = x / T + mask exactly as tempered_logits computes it
-//    (rl.rs:477-484, float.rs:494-499); c = log2(e).
-template <int DT, int MK>
-__device__ __forceinline__ void decode_words(const uint32_t *xw, const uint32_t *mw, float v[kEpl], float tau,
-                                             bool tau_one) {
-#pragma unroll
-    for (int j = 0; j < kEpl; j++) {
-        float x = logit<DT>(xw, j);
-        if constexpr (MK == NT_MASK_U8) {
-            const uint32_t keep = (mw[j / 4] >> (8 * (j % 4))) & 0xffu;
-            v[j] = keep ? x : -INFINITY;
-        } else if constexpr (MK == NT_MASK_F32) {
-            const float z = tau_one ? x : x / tau;
-            v[j] = z + __uint_as_float(mw[j]);
-        } else {
-            v[j] = x;
-        }
-    }
-}
-
-template <int DT, int MK>
-__device__ __forceinline__ void decode(const Raw<DT, MK> &r, float v[kEpl], float tau, bool tau_one) {
-    decode_words<DT, MK>(r.x, r.m, v, tau, tau_one);
-}
-
-template <int MK>
-__device__ __forceinline__ void load_mask_inbounds(uint32_t *m, const void *mrow, int64_t e0) {
-    if constexpr (MK == NT_MASK_U8) {
-        uint2 k = *reinterpret_cast<const uint2 *>(static_cast<const uint8_t *>(mrow) + e0);
-        m[0] = k.x; m[1] = k.y;
-    } else if constexpr (MK == NT_MASK_F32) {
-        const uint4 *q = reinterpret_cast<const uint4 *>(static_cast<const float *>(mrow) + e0);
-        uint4 a = q[0], b = q[1];
-        m[0] = a.x; m[1] = a.y; m[2] = a.z; m[3] = a.w;
-        m[4] = b.x; m[5] = b.y; m[6] = b.z; m[7] = b.w;
-    }
-}
-
-// Write decoded values back into the logit words (exact: each value is the widened logit or
-// -inf, both representable in the storage type), so the mask is no longer needed.
-template <int DT>
-__device__ __forceinline__ void fold_values(uint32_t *x, const float v[kEpl]) {
-#pragma unroll
-    for (int j = 0; j < kEpl; j++) {
-        if constexpr (DT == NT_F32) {
-            x[j] = __float_as_uint(v[j]);
-        } else if (j % 2 == 1) {
-            x[j / 2] = (__float_as_uint(v[j]) & 0xffff0000u) | (__float_as_uint(v[j - 1]) >> 16);
-        }
-    }
-}
-
-// Decode words that were folded (the mask already applied) or, for an f32 mask, not.
-template <int DT, int MK, bool FOLDED>
-__device__ __forceinline__ void decode_folded(const Raw<DT, MK> &r, float v[kEpl], float tau, bool tau_one) {
-    if constexpr (FOLDED) decode_words<DT, NT_MASK_NONE>(r.x, r.m, v, tau, tau_one);
-    else decode_words<DT, MK>(r.x, r.m, v, tau, tau_one);
-}
-
-__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// ln x for a finite x >= 2^-1021 in f64, within about 1e-7 absolute: the binary exponent exactly,
-// plus v_log_f32 of the mantissa in [0.5, 1) rounded to f32 (2^-24 relative, then the
-// instruction's 1 ulp). A dozen instructions where the f64 library log takes about a hundred
-// on the row's critical path.
-__device__ __forceinline__ double ln_fast(double x) {
-    const uint64_t b = uint64_t(__double_as_longlong(x));
-    const int e = int((b >> 52) & 0x7ff) - 1022;
-    const double m = __longlong_as_double(int64_t((b & 0x000fffffffffffffull) | (1022ull << 52)));
-    return (double(e) + double(__builtin_amdgcn_logf(float(m)))) * 0.69314718055994530942;
-}
-
-__device__ __forceinline__ float max8(const float v[kEpl]) {
-    return fmaxf(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])), fmaxf(fmaxf(v[4], v[5]), fmaxf(v[6], v[7])));
-}
-
-__device__ __forceinline__ float tree8(const float w[kEpl]) {
-    return ((w[0] + w[1]) + (w[2] + w[3])) + ((w[4] + w[5]) + (w[6] + w[7]));
-}
-
-// Butterfly reductions over the 64 lanes: every lane ends with the same bits (the operations
-// are commutative), the order is fixed.
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-    return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
-}
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
-}
-// Inclusive prefix sum over lanes (Hillis-Steele, fixed order).
-__device__ __forceinline__ double wave_scan_d(double v, int lane) {
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-        double n = __shfl_up(v, o, kWave);
-        if (lane >= o) v += n;
-    }
-    return v;
-}
-__device__ __forceinline__ int first_lane(uint64_t ballot) { return ballot ? __builtin_ctzll(ballot) : -1; }
-__device__ __forceinline__ int last_lane(uint64_t ballot) { return ballot ? 63 - __builtin_clzll(ballot) : -1; }
-
-// ------------------------------------------------------------------ sampler
-
-struct SampleP {
-    const void *logits;
-    const void *mask;
-    int64_t V, ld, mask_ld;
-    float c;          // exponent scale: log2(e)/T (no/u8 mask) or log2(e) (f32 mask)
-    float tau;        // (float)T, the reference's divisor (float.rs:494-499)
-    int tau_one;      // T == 1 (or greedy): no divide
-    int greedy;
-    int nc;           // chunks per row
-    const double *u;
-    int32_t *ids;
-    float *logp;
-    float *ent;
-    uint8_t *status;
-};
-
-template <int DT, int MK, bool ENT, bool AL>
-__global__ __launch_bounds__(1024) void k_sample(SampleP p) {
-    extern __shared__ float smem[];
-    float *cmax = smem;                 // [nc] chunk max (value space)
-    float *csum = smem + p.nc;          // [nc] chunk sum of exp2((v - cmax) c)
-    float *cent = smem + 2 * p.nc;      // [nc] chunk sum of w * (v - cmax) c   (ENT only)
-    const int64_t row = blockIdx.x;
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    const int nw = blockDim.x / kWave;
-    const bool tau_one = p.tau_one != 0;
-    const void *xrow = static_cast<const char *>(p.logits) + row * p.ld * Elem<DT>::kBytes;
-    const void *mrow = nullptr;
-    if constexpr (MK != NT_MASK_NONE) mrow = static_cast<const char *>(p.mask) + row * p.mask_ld * MaskWords<MK>::kBytes;
-
-    // ---- phase 1: stream the row once, per-chunk (max, sum exp[, sum exp * d]) into LDS.
-    for (int c0 = wave; c0 < p.nc; c0 += nw * kBatch) {
-        Raw<DT, MK> raw[kBatch];
-#pragma unroll
-        for (int b = 0; b < kBatch; b++) {
-            const int c = c0 + b * nw;
-            const int64_t e0 = int64_t(c < p.nc ? c : 0) * kChunk + lane * kEpl;
-            load_raw<DT, MK, AL>(raw[b], xrow, mrow, c < p.nc ? e0 : p.V, p.V);
-        }
-#pragma unroll
-        for (int b = 0; b < kBatch; b++) {
-            const int c = c0 + b * nw;
-            if (c < p.nc) {
-            float v[kEpl];
-            decode<DT, MK>(raw[b], v, p.tau, tau_one);
-            const float cm = wave_max(max8(v));
-            const float sh = (cm == -INFINITY) ? 0.0f : cm;
-            float w[kEpl], h[kEpl];
-#pragma unroll
-            for (int j = 0; j < kEpl; j++) {
-                const float d = (v[j] - sh) * p.c;
-                w[j] = exp2_hw(d);
-                if constexpr (ENT) h[j] = w[j] * fmaxf(d, -FLT_MAX);
-            }
-            const float cs = wave_sum(tree8(w));
-            float ce = 0.0f;
-            if constexpr (ENT) ce = wave_sum(tree8(h));
-            if (lane == 0) {
-                cmax[c] = cm;
-                csum[c] = cs;
-                if constexpr (ENT) cent[c] = ce;
-            }
-            }
-        }
-    }
-    __syncthreads();
-    if (wave != 0) return;
-
-    // ---- phase 2 (wave 0): merge the chunks in index order, in f64.
-    const int nc = p.nc;
-    const int q = (nc + kWave - 1) / kWave;
-    const int cb = min(lane * q, nc), ce_ = min(cb + q, nc);
-    float lm = -INFINITY;
-    for (int c = cb; c < ce_; c++) lm = fmaxf(lm, cmax[c]);
-    const float a = wave_max(lm);
-    auto refuse = [&](uint8_t st) {
-        if (lane == 0) {
-            p.ids[row] = -1;
-            if (p.logp) p.logp[row] = NAN;
-            if (p.ent) p.ent[row] = NAN;
-            p.status[row] = st;
-        }
-    };
-    if (a == -INFINITY) {
-        refuse(NT_ROW_NO_TOKEN);
-        return;
-    }
-    double lsum = 0.0, lh = 0.0;
-    for (int c = cb; c < ce_; c++) {
-        const float f = exp2_hw((cmax[c] - a) * p.c);
-        lsum += double(f) * double(csum[c]);
-        if constexpr (ENT) {
-            if (csum[c] > 0.0f) lh += double(f) * (double(cent[c]) + double((cmax[c] - a) * p.c) * double(csum[c]));
-        }
-    }
-    const double incl = wave_scan_d(lsum, lane);
-    const double S = __shfl(incl, kWave - 1, kWave);
-    double H2 = 0.0;
-    if constexpr (ENT) H2 = wave_sum_d(lh);
-    if (!(S == S)) {
-        refuse(NT_ROW_NAN);
-        return;
-    }
-    int cstar = -1;
-    double tloc = 0.0;  // target inside chunk cstar, in the chunk's own scale
-    if (p.greedy) {
-        int mine = -1;
-        for (int c = cb; c < ce_; c++)
-            if (cmax[c] == a) { mine = c; break; }
-        const int l = first_lane(__ballot(mine >= 0));
-        cstar = l >= 0 ? __shfl(mine, l, kWave) : -1;
-    } else {
-        const double t = p.u[row] * S;
-        // Every lane runs the shuffle: a disabled source lane would read as 0.
-        const double prev = __shfl_up(incl, 1, kWave);
-        const double excl = (lane == 0) ? 0.0 : prev;
-        // Only a lane that holds weight can contain the crossing (a zero-weight lane's
-        // inclusive sum may round above its neighbour's in the scan tree).
-        int l = first_lane(__ballot(incl > t && lsum > 0.0));
-        int mine = -1;
-        double mt = INFINITY;
-        if (l >= 0) {
-            if (lane == l) {
-                double C = excl;
-                int lastpos = -1;
-                for (int c = cb; c < ce_; c++) {
-                    const float f = exp2_hw((cmax[c] - a) * p.c);
-                    const double wt = double(f) * double(csum[c]);
-                    if (wt > 0.0) lastpos = c;
-                    if (C + wt > t) {
-                        mine = c;
-                        mt = (t - C) / double(f);
-                        break;
-                    }
-                    C += wt;
-                }
-                if (mine < 0) mine = lastpos;  // rounding: no crossing inside the lane
-            }
-        } else {
-            // u*S rounded up to S: the last chunk with weight.
-            int lastpos = -1;
-            for (int c = cb; c < ce_; c++)
-                if (csum[c] > 0.0f && cmax[c] != -INFINITY) lastpos = c;
-            l = last_lane(__ballot(lastpos >= 0));
-            if (lane == l) mine = lastpos;
-        }
-        cstar = l >= 0 ? __shfl(mine, l, kWave) : -1;
-        tloc = l >= 0 ? __shfl(mt, l, kWave) : INFINITY;
-    }
-    if (cstar < 0 || cstar >= nc) {
-        // Unreachable with S > 0 (some chunk holds weight); kept so that no path re-reads
-        // outside the row: take the first chunk holding the maximum.
-        int mine = -1;
-        for (int c = cb; c < ce_; c++)
-            if (cmax[c] == a) { mine = c; break; }
-        const int l = first_lane(__ballot(mine >= 0));
-        cstar = l >= 0 ? __shfl(mine, l, kWave) : 0;
-        tloc = INFINITY;
-    }
-
-    // ---- phase 3 (wave 0): re-read chunk cstar, find the token inside it.
-    Raw<DT, MK> raw;
-    const int64_t e0 = int64_t(cstar) * kChunk + lane * kEpl;
-    load_raw<DT, MK, AL>(raw, xrow, mrow, e0, p.V);
-    float v[kEpl];
-    decode<DT, MK>(raw, v, p.tau, tau_one);
-    int jsel = -1, lsel = -1;
-    if (p.greedy) {
-        int mine = -1;
-#pragma unroll
-        for (int j = kEpl - 1; j >= 0; j--)
-            if (v[j] == a) mine = j;
-        lsel = first_lane(__ballot(mine >= 0));
-        jsel = lsel >= 0 ? __shfl(mine, lsel, kWave) : -1;
-    } else {
-        const float cm = cmax[cstar];
-        const float sh = (cm == -INFINITY) ? 0.0f : cm;
-        float w[kEpl];
-        double ls = 0.0;
-#pragma unroll
-        for (int j = 0; j < kEpl; j++) {
-            w[j] = exp2_hw((v[j] - sh) * p.c);
-            ls += double(w[j]);
-        }
-        const double incl2 = wave_scan_d(ls, lane);
-        const double prev2 = __shfl_up(incl2, 1, kWave);
-        const double excl2 = (lane == 0) ? 0.0 : prev2;
-        int mine = -1;
-        int lastj = -1;
-#pragma unroll
-        for (int j = 0; j < kEpl; j++)
-            if (w[j] > 0.0f) lastj = j;
-        lsel = first_lane(__ballot(incl2 > tloc && ls > 0.0));
-        if (lsel >= 0) {
-            if (lane == lsel) {
-                double C = excl2;
-                for (int j = 0; j < kEpl; j++) {
-                    C += double(w[j]);
-                    if (C > tloc) { mine = j; break; }
-                }
-                if (mine < 0) mine = lastj;
-            }
-        } else {
-            lsel = last_lane(__ballot(lastj >= 0));
-            if (lane == lsel) mine = lastj;
-        }
-        jsel = lsel >= 0 ? __shfl(mine, lsel, kWave) : -1;
-    }
-    if (lsel < 0 || jsel < 0) {
-        // Unreachable (chunk cstar holds weight, or the maximum when greedy); the first
-        // element equal to the chunk's maximum keeps the result a valid token.
-        int mine = -1;
-#pragma unroll
-        for (int j = kEpl - 1; j >= 0; j--)
-            if (v[j] == cmax[cstar]) mine = j;
-        lsel = first_lane(__ballot(mine >= 0));
-        jsel = lsel >= 0 ? __shfl(mine, lsel, kWave) : 0;
-        if (lsel < 0) lsel = 0;
-    }
-    if (lane == lsel) {
-        // jsel indexes this lane's registers: select it without a dynamic register index.
-        float vz = v[0];
-#pragma unroll
-        for (int j = 1; j < kEpl; j++)
-            if (j == jsel) vz = v[j];
-        const int64_t id = int64_t(cstar) * kChunk + lane * kEpl + jsel;
-        // logp = (z_id - m) - ln S, with z_id - m the reference's f32 subtraction
-        // (activation.rs:32-35).
-        float zid = vz, mz = a;
-        if constexpr (MK != NT_MASK_F32) {
-            if (!tau_one) {
-                zid = vz / p.tau;
-                mz = a / p.tau;
-            }
-        }
-        const double lnS = log(S);
-        p.ids[row] = int32_t(id);
-        if (p.logp) p.logp[row] = float((double(zid) - double(mz)) - lnS);
-        if (p.ent) p.ent[row] = float(lnS - kLn2 * H2 / S);
-        p.status[row] = NT_ROW_OK;
-    }
-}
-
-// ------------------------------------------------------------------ register-resident sampler
-//
-// For rows of at most 16*K chunks (V <= 131072 for bf16 at K = 16) one 1024-thread workgroup
-// keeps the whole row on chip: each wave's logit words stay in VGPRs (64 registers at K = 16)
-// and the u8 mask is copied by the load unit straight into LDS (buffer_load ... lds, 128 KiB at
-// K = 16), so nothing is read twice. Each wave issues chunk k + 1 while it processes chunk k,
-// after decoding it (kRRWindow = 1): phase 1 is VALU-bound, and on MI355X that measured faster
-// than two or three chunks ahead (17.40 against 17.57 and 18.27 us at c4, before the issue point
-// moved into the chunk).
-//
-// Wave w owns the K consecutive chunks [w K, w K + K) of the row, so the index order of the
-// row is the order of the waves, then of each wave's chunks.
-// Phase 1 (all waves): as each chunk lands, w = 2^(v c - s) with s the wave's exponent
-// reference (the maximum of its first chunk holding an allowed value; moved only when a chunk's
-// weights overflow), so no exponential waits on a reduction. The chunk's sum of weights is a
-// fixed-order DPP reduction written to LDS as four 16-lane partials. Each wave then takes the
-// f64 prefix over its own chunks (kept in registers) and publishes its total.
-// Phase 2 (every wave, after the one barrier): f64 scan over the 16 wave totals in index order,
-// the wave whose chunks hold u*S. That wave alone goes on (no second barrier).
-// Phase 3 (that wave): the crossing chunk from its prefix, then a scan of that chunk's registers.
-// Measured at c4 against one 256-chunk scan by wave 0 and a second barrier: 20.2 against 20.6 us
-// HBM-cold, 17.0-17.2 against 17.2-17.4 us cache-warm.
-
-constexpr int kRRWaves = 16;
-constexpr int kRRThreads = kRRWaves * kWave;
-constexpr int kRRWindow = 1;  // chunks in flight ahead of the one being consumed
-
-typedef __attribute__((address_space(3))) void *lds_ptr_t;
-// Word 3 of a gfx9-family buffer resource: 32-bit data format, no swizzle; with stride 0 every
-// access is range-checked against the byte count in word 2.
-constexpr int kBufferWord3 = 0x00020000;
-// Four dwords as the buffer load/store builtins take them.
-typedef uint32_t v4u __attribute__((ext_vector_type(4)));
-// Buffer access cache policy for data read or written once: non-temporal.
-constexpr int kCachePolicyNT = 2;
-typedef __attribute__((address_space(1))) void *glb_ptr_t;
-
-template <int B, int E, class F>
-__device__ __forceinline__ void static_for(F &&f) {
-    if constexpr (B < E) {
-        f(std::integral_constant<int, B>{});
-        static_for<B + 1, E>(f);
-    }
-}
-
-// s_waitcnt with only the vector-memory counter constrained (expcnt and lgkmcnt at their
-// maxima): gfx9 encoding, vmcnt bits [3:0] and [15:14].
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
-// An LDS read the compiler does not track (it would otherwise wait for every outstanding load
-// because the data came from an LDS DMA); the caller has waited for that DMA.
-__device__ __forceinline__ uint2 lds_read_b64(uint32_t addr) {
-    uint2 r;
-    asm volatile("ds_read_b64 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(addr) : "memory");
-    return r;
-}
-template <int OFF>
-__device__ __forceinline__ uint2 lds_read_b64_off(uint32_t addr) {
-    static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
-    uint2 r;
-    asm volatile("ds_read_b64 %0, %1 offset:%2\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
-    return r;
-}
-__device__ __forceinline__ uint4 lds_read_b128(uint32_t addr) {
-    uint4 r;
-    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(addr) : "memory");
-    return r;
-}
-
-// v_max3_f32 without the canonicalising moves the compiler puts in front of fmaxf: the inputs
-// are widened logits or -inf, and a NaN among them reaches the row's sum through exp2 anyway.
-__device__ __forceinline__ float max3_hw(float a, float b, float c) {
-    float r;
-    asm volatile("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
-}
-__device__ __forceinline__ float max8_hw(const float v[kEpl]) {
-    const float t0 = max3_hw(v[0], v[1], v[2]);
-    const float t1 = max3_hw(v[3], v[4], v[5]);
-    return max3_hw(t0, t1, max3_hw(v[6], v[7], v[7]));
-}
-
-template <int CTRL>
-__device__ __forceinline__ float dpp_mov(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
-}
-__device__ __forceinline__ double readlane_d(double v, int l) {
-    const uint64_t b = uint64_t(__double_as_longlong(v));
-    const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b)), l));
-    const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b >> 32)), l));
-    return __longlong_as_double(int64_t((uint64_t(hi) << 32) | lo));
-}
-__device__ __forceinline__ float readlane_f(float v, int l) {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
-}
-// Maximum over the 64 lanes: xor-1 and xor-2 quad permutes, the 8- and 16-lane mirrors, then
-// the four rows in a fixed order, each step a v_max3_f32 (no canonicalising moves; the inputs
-// are maxima of widened logits or -inf). The result is uniform and independent of timing.
-// Maximum inside each 16-lane row (the first four steps of wave_max3_dpp): every lane of a row
-// holds its row's maximum.
-__device__ __forceinline__ float row_max3_dpp(float v) {
-    v = max3_hw(v, dpp_mov<0xB1>(v), dpp_mov<0xB1>(v));
-    v = max3_hw(v, dpp_mov<0x4E>(v), dpp_mov<0x4E>(v));
-    v = max3_hw(v, dpp_mov<0x141>(v), dpp_mov<0x141>(v));
-    return max3_hw(v, dpp_mov<0x140>(v), dpp_mov<0x140>(v));
-}
-__device__ __forceinline__ float wave_max3_dpp(float v) {
-    v = row_max3_dpp(v);
-    return max3_hw(max3_hw(readlane_f(v, 0), readlane_f(v, 16), readlane_f(v, 32)), readlane_f(v, 48),
-                   readlane_f(v, 48));
-}
-// One DPP step on an f64: both 32-bit halves move with the same control; lanes with no
-// source (or in rows the row mask leaves out) read 0, the identity of the sum.
-template <int CTRL, int ROWS>
-__device__ __forceinline__ double dpp_f64(double v) {
-    const uint64_t b = __double_as_longlong(v);
-    const int lo = __builtin_amdgcn_update_dpp(0, int(uint32_t(b)), CTRL, ROWS, 0xf, true);
-    const int hi = __builtin_amdgcn_update_dpp(0, int(uint32_t(b >> 32)), CTRL, ROWS, 0xf, true);
-    return __longlong_as_double(int64_t((uint64_t(uint32_t(hi)) << 32) | uint32_t(lo)));
-}
-// Inclusive prefix sum over the 64 lanes in f64, in a fixed order: shifts by 1, 2, 4 and 8
-// inside each 16-lane row, then the row broadcasts of lanes 15 and 31 (the gfx9 DPP scan).
-// Inclusive prefix sum inside each 16-lane row in f64 (the first four steps of wave_scan_dpp).
-__device__ __forceinline__ double row_scan_dpp(double v) {
-    v += dpp_f64<0x111, 0xf>(v);  // row_shr:1
-    v += dpp_f64<0x112, 0xf>(v);  // row_shr:2
-    v += dpp_f64<0x114, 0xf>(v);  // row_shr:4
-    v += dpp_f64<0x118, 0xf>(v);  // row_shr:8
-    return v;
-}
-__device__ __forceinline__ double wave_scan_dpp(double v) {
-    v = row_scan_dpp(v);
-    v += dpp_f64<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
-    v += dpp_f64<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
-    return v;
-}
-
-// Sum over each 16-lane row in four DPP steps (the two quad permutes, then the 8- and 16-lane
-// mirrors); every lane of a row holds its row's sum.
-__device__ __forceinline__ float row_sum_dpp(float v) {
-    v = v + dpp_mov<0xB1>(v);
-    v = v + dpp_mov<0x4E>(v);
-    v = v + dpp_mov<0x141>(v);
-    v = v + dpp_mov<0x140>(v);
-    return v;
-}
-__device__ __forceinline__ int wave_min_i(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, kWave));
-    return v;
-}
-
-// Per-lane data of one chunk of the register-resident sampler: EPL elements (8 or 16), read
-// as 16-byte pieces (8 bf16 or 4 f32 each).
-template <int DT, int EPL>
-struct RRX {
-    static constexpr int kWords = DT == NT_F32 ? EPL : EPL / 2;
-    static constexpr int kPieces = kWords / 4;
-    uint32_t x[kWords];
-};
-
-// Mask bytes per chunk in LDS and the LDS DMA instructions that bring one chunk's mask: lane l
-// of DMA instruction d writes B bytes at slot + d * 64 B + l B (B = 16 when the chunk's mask is
-// a whole number of 1 KiB, else 4).
-template <int MK, int EPL>
-struct RRMask {
-    static constexpr int kBytes = MK == NT_MASK_U8 ? kWave * EPL : (MK == NT_MASK_F32 ? 4 * kWave * EPL : 0);
-    static constexpr int kDmaBytes = kBytes % (16 * kWave) == 0 ? 16 : 4;
-    static constexpr int kDma = kBytes / (kDmaBytes * kWave);
-    static constexpr int kWords = MK == NT_MASK_U8 ? EPL / 4 : (MK == NT_MASK_F32 ? EPL : 1);  // per lane
-};
-
-// x if byte B (0, 1 or 2) of a mask word is nonzero, else -inf: one SDWA compare against the
-// inline 0 (the compiler masks bytes 1 and 2 with a separate AND and keeps a zero register for
-// byte 0; byte 3 it compares in one instruction).
-template <int B>
-__device__ __forceinline__ float keep_byte(uint32_t mw, float x, float ninf) {
-    float r;
-    if constexpr (B == 0)
-        asm("v_cmp_ne_u32_sdwa vcc, %1, 0 src0_sel:BYTE_0 src1_sel:DWORD\n\tv_cndmask_b32 %0, %2, %3, vcc"
-            : "=v"(r) : "v"(mw), "v"(ninf), "v"(x) : "vcc");
-    else if constexpr (B == 1)
-        asm("v_cmp_ne_u32_sdwa vcc, %1, 0 src0_sel:BYTE_1 src1_sel:DWORD\n\tv_cndmask_b32 %0, %2, %3, vcc"
-            : "=v"(r) : "v"(mw), "v"(ninf), "v"(x) : "vcc");
-    else
-        asm("v_cmp_ne_u32_sdwa vcc, %1, 0 src0_sel:BYTE_2 src1_sel:DWORD\n\tv_cndmask_b32 %0, %2, %3, vcc"
-            : "=v"(r) : "v"(mw), "v"(ninf), "v"(x) : "vcc");
-    return r;
-}
-
-// Decode EPL elements (logit words + mask words) into the kernel's value space.
-template <int DT, int MK, int EPL>
-__device__ __forceinline__ void decode_e(const uint32_t *xw, const uint32_t *mw, float *v, float tau, bool tau_one) {
-#pragma unroll
-    for (int j = 0; j < EPL; j++) {
-        const float x = logit<DT>(xw, j);
-        if constexpr (MK == NT_MASK_U8) {
-            if (j % 4 == 0) {
-                v[j] = keep_byte<0>(mw[j / 4], x, -INFINITY);
-            } else if (j % 4 == 1) {
-                v[j] = keep_byte<1>(mw[j / 4], x, -INFINITY);
-            } else if (j % 4 == 2) {
-                v[j] = keep_byte<2>(mw[j / 4], x, -INFINITY);
-            } else {
-                const uint32_t keep = (mw[j / 4] >> (8 * (j % 4))) & 0xffu;
-                v[j] = keep ? x : -INFINITY;
-            }
-        } else if constexpr (MK == NT_MASK_F32) {
-            const float z = tau_one ? x : x / tau;
-            v[j] = z + __uint_as_float(mw[j]);
-        } else {
-            v[j] = x;
-        }
-    }
-}
-
-// The lane's mask words of one chunk, from its LDS slot (the caller has waited for the DMA).
-template <int MK, int EPL>
-__device__ __forceinline__ void lds_mask_words(uint32_t a, uint32_t *mw) {
-    if constexpr (MK == NT_MASK_U8 && EPL == 8) {
-        const uint2 m2 = lds_read_b64(a);
-        mw[0] = m2.x;
-        mw[1] = m2.y;
-    } else if constexpr (MK != NT_MASK_NONE) {
-#pragma unroll
-        for (int q = 0; q < RRMask<MK, EPL>::kWords / 4; q++) {
-            const uint4 m4 = lds_read_b128(a + 16 * q);
-            mw[4 * q] = m4.x;
-            mw[4 * q + 1] = m4.y;
-            mw[4 * q + 2] = m4.z;
-            mw[4 * q + 3] = m4.w;
-        }
-    } else {
-        mw[0] = 0;
-    }
-}
-
-template <int N>
-__device__ __forceinline__ float max_hw(const float *v) {
-    if constexpr (N == 8) {
-        return max8_hw(v);
-    } else {
-        const float a = max8_hw(v), b = max8_hw(v + 8);
-        return max3_hw(a, b, b);
-    }
-}
-
-template <int N>
-__device__ __forceinline__ float tree_sum(const float *w) {
-    if constexpr (N == 8) return tree8(w);
-    else return tree8(w) + tree8(w + 8);
-}
-
-template <int DT, int MK, int K, bool ENT, int EPL>
-__global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
-    constexpr int CH = kWave * EPL;                // elements per chunk
-    constexpr int NCH = K * kRRWaves;
-    constexpr int LX = RRX<DT, EPL>::kPieces;      // logit load instructions per chunk
-    constexpr int LD = RRMask<MK, EPL>::kDma;      // mask DMA instructions per chunk
-    constexpr int MB = RRMask<MK, EPL>::kBytes;    // mask bytes per chunk
-    constexpr int DB = RRMask<MK, EPL>::kDmaBytes;
-    constexpr int L = LX + LD;
-    __shared__ __attribute__((aligned(16))) uint8_t mlds[MK == NT_MASK_NONE ? 16 : NCH * MB];
-    __shared__ __attribute__((aligned(16))) float csum4[NCH * 4];  // per chunk and 16-lane row: sum of 2^(v c - wref)
-    __shared__ __attribute__((aligned(16))) float cent4[ENT ? NCH * 4 : 4];  // per chunk and row: sum of w (v c - wref)
-    __shared__ float wref[kRRWaves];    // per wave: its final exponent reference
-    __shared__ float wmax[kRRWaves];    // per wave: its maximum (greedy) or its reference's source
-    __shared__ double wtot[kRRWaves];   // per wave: its sum of weights, relative to its reference
-    __shared__ double went[ENT ? kRRWaves : 1];  // per wave: its sum of w (v c - wref)
-    __shared__ int wpick[kRRWaves];
-
-    const int64_t row = blockIdx.x;
-    const int tid = threadIdx.x;
-    const int lane = tid & (kWave - 1);
-    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const int nc = p.nc;
-    const float c = p.c;
-    const bool tau_one = p.tau_one != 0;
-    const void *xrow = static_cast<const char *>(p.logits) + row * p.ld * Elem<DT>::kBytes;
-    const uint8_t *mrow = nullptr;
-    if constexpr (MK != NT_MASK_NONE)
-        mrow = static_cast<const uint8_t *>(p.mask) + row * p.mask_ld * MaskWords<MK>::kBytes;
-    const uint32_t mbase = uint32_t((uintptr_t)(lds_ptr_t)(mlds));
-    // The row's uniform, read now so that its latency hides under the row's loads.
-    const double u_row = p.greedy ? 0.0 : p.u[row];
-
-    // ---- loads: the first W chunks now, chunk k + W while chunk k is consumed.
-    constexpr int W = K < kRRWindow ? K : kRRWindow;
-    RRX<DT, EPL> raw[K];
-    // Buffer resources over the row's logits and mask bytes: a read at or past the end returns
-    // zeros (mask 0 = excluded), so chunks past the row need no address clamping. All of the
-    // offset goes in the per-lane register, which the hardware range-checks.
-    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<void *>(xrow), short(0), int(p.V * Elem<DT>::kBytes), kBufferWord3);
-    __amdgpu_buffer_rsrc_t mres;
-    if constexpr (MK != NT_MASK_NONE)
-        mres = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(mrow), short(0),
-                                                 int(p.V * MaskWords<MK>::kBytes), kBufferWord3);
-    auto issue = [&](auto kc) {
-        constexpr int k = decltype(kc)::value;
-        const int ch = wave * K + k;
-        const int xo = (ch * CH + lane * EPL) * Elem<DT>::kBytes;
-#pragma unroll
-        for (int q = 0; q < LX; q++) {
-            // default cache policy: non-temporal loads leave the Infinity Cache unfilled, which
-            // measured slower when a row is read again (19.4 against 17.1 us at c4) and no faster
-            // HBM-cold
-            const auto a = __builtin_amdgcn_raw_buffer_load_b128(xres, xo + 16 * q, 0, 0);
-            raw[k].x[4 * q] = a[0];
-            raw[k].x[4 * q + 1] = a[1];
-            raw[k].x[4 * q + 2] = a[2];
-            raw[k].x[4 * q + 3] = a[3];
-        }
-        if constexpr (MK != NT_MASK_NONE) {
-            // The chunk's mask bytes, DB bytes per lane per instruction, into the chunk's slot
-            // of mlds (lane l writes slot + DB l).
-#pragma unroll
-            for (int d = 0; d < LD; d++) {
-                if constexpr (DB == 16)
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(mres, (lds_ptr_t)(mlds + ch * MB + d * DB * kWave), 16,
-                                                             ch * MB + d * DB * kWave + DB * lane, 0, 0, 0);
-                else
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(mres, (lds_ptr_t)(mlds + ch * MB + d * DB * kWave), 4,
-                                                             ch * MB + d * DB * kWave + DB * lane, 0, 0, 0);
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    static_for<0, W>(issue);
-
-    // ---- phase 1: each chunk as it lands. The wave's exponent reference is set from its first
-    // chunk holding an allowed value (its exact maximum) and moves only when a chunk's weights
-    // overflow (a weight or a lane sum of at least 2^128), to that chunk's maximum; the partials
-    // already written are then rescaled. No maximum is taken per chunk otherwise.
-    // Each chunk's row partial goes to csum4[4 ch + lane / 16]: a per-lane base, plus 256 bytes
-    // per k (an immediate offset).
-    float *const cpart = csum4 + 4 * K * wave + lane / 16;
-    float *const epart = ENT ? cent4 + 4 * K * wave + lane / 16 : nullptr;
-    const bool row_leader = (lane & 15) == 0;
-    const int Vi = int(p.V);  // < 2^31 (at most 16 K chunks of CH)
-    // This lane's mask bytes of the wave's chunk k: mlw + k MB.
-    const uint32_t mlw = mbase + wave * K * MB + lane * EPL * MaskWords<MK>::kBytes;
-    bool have_ref = false;     // sref set (uniform)
-    float lmax = -INFINITY;    // the exact maximum, kept when greedy only
-    float sref = -INFINITY;    // RN(sref_v c), uniform
-    float sref_v = -INFINITY;  // the wave maximum the reference was taken from
-    static_for<0, K>([&](auto kc) {
-        constexpr int k = decltype(kc)::value;
-        const int ch = wave * K + k;
-        if (ch < nc) {
-            const int64_t e0 = int64_t(ch) * CH + lane * EPL;
-            uint32_t mw[RRMask<MK, EPL>::kWords];
-            if constexpr (MK != NT_MASK_NONE) {
-                // Chunks k+1 .. min(K, k+W)-1 may still be in flight.
-                wait_vmcnt<L * ((K < k + W ? K : k + W) - 1 - k)>();
-                constexpr int kOff = k * MB;
-                if constexpr (MK == NT_MASK_U8 && EPL == 8 && kOff < 65536) {
-                    const uint2 m2 = lds_read_b64_off<kOff < 65536 ? kOff : 0>(mlw);
-                    mw[0] = m2.x;
-                    mw[1] = m2.y;
-                } else {
-                    lds_mask_words<MK, EPL>(mlw + kOff, mw);
-                }
-            } else {
-                mw[0] = 0;
-            }
-            float v[EPL];
-            decode_e<DT, MK, EPL>(raw[k].x, mw, v, p.tau, tau_one);
-            if ((ch + 1) * CH > Vi) {  // only the row's last chunk can be partial
-#pragma unroll
-                for (int j = 0; j < EPL; j++)
-                    if (e0 + j >= p.V) v[j] = -INFINITY;
-            }
-            // The next chunk's loads go out once this chunk's data is in registers: between one
-            // and two chunks in flight per wave (measured faster than issuing after the chunk,
-            // 17.11 against 17.38 us at c4, and than two whole chunks ahead).
-            if constexpr (k + W < K) issue(std::integral_constant<int, k + W>{});
-            if (p.greedy) {
-                const float m8 = max_hw<EPL>(v);
-                lmax = max3_hw(lmax, m8, m8);
-            }
-            if (!have_ref) {
-                const float wm = wave_max3_dpp(max_hw<EPL>(v));
-                if (wm != -INFINITY) {
-                    have_ref = true;
-                    sref_v = wm;
-                    sref = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(wm * c)));
-                }
-            }
-            float gs = 0.0f, gh = 0.0f;
-            auto weigh = [&]() {
-                float w[EPL], h[EPL];
-#pragma unroll
-                for (int j = 0; j < EPL; j++) {
-                    const float d = fmaf(v[j], c, -sref);
-                    w[j] = exp2_hw(d);
-                    if constexpr (ENT) h[j] = w[j] * fmaxf(d, -FLT_MAX);
-                }
-                gs = tree_sum<EPL>(w);
-                if constexpr (ENT) gh = tree_sum<EPL>(h);
-            };
-            if (have_ref) {
-                weigh();
-                // An overflow (or a NaN, which compares false below and stays in the sums) moves
-                // the wave's reference to the chunk's maximum. With the entropy wanted, so does a
-                // lane's 8 weights summing to more than kChunkSumCap: the entropy is ln S - ln2 H / S,
-                // and a reference far below the maximum would make both terms large and cancelling.
-                bool move = !(gs < INFINITY);
-                if constexpr (ENT) move = !(gs <= kChunkSumCap);
-                if (__ballot(move) != 0) {
-                    const float wm = wave_max3_dpp(max_hw<EPL>(v));
-                    const float nref = wm * c;
-                    if (nref > sref) {
-                        const float dk = sref - nref, f = exp2_hw(dk);
-                        if ((lane & 15) == 0) {
-                            // this wave's earlier partials, owned by lanes 0, 16, 32, 48
-                            static_for<0, k>([&](auto jc) {
-                                constexpr int kk = decltype(jc)::value;
-                                const int idx = (wave * K + kk) * 4 + lane / 16;
-                                const float o = csum4[idx];
-                                csum4[idx] = f * o;
-                                if constexpr (ENT) cent4[idx] = f * (cent4[idx] + dk * o);
-                            });
-                        }
-                        sref = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(nref)));
-                        sref_v = wm;
-                        weigh();
-                    }
-                }
-            }
-            // The chunk's four 16-lane row sums (phase 2 adds them in a fixed order).
-            const float cs = row_sum_dpp(gs);
-            float ce = 0.0f;
-            if constexpr (ENT) ce = row_sum_dpp(gh);
-            if (row_leader) {
-                cpart[4 * k] = cs;
-                if constexpr (ENT) epart[4 * k] = ce;
-            }
-        }
-        if constexpr (k + W < K) {
-            if (!(ch < nc)) issue(std::integral_constant<int, k + W>{});  // (no chunk here to process)
-        }
-    });
-    // ---- end of phase 1 (each wave on its own, while the others still stream): lane k < K
-    // takes chunk k's sum (its four 16-lane partials, in a fixed order) in f64, in the wave's
-    // scale; the f64 prefix over the wave's chunks stays in registers and the wave's totals go
-    // to LDS.
-    double wcs = 0.0, wce = 0.0;
-    {
-        const int ch = wave * K + lane;
-        if (lane < K && ch < nc) {
-            const float4 q = *reinterpret_cast<const float4 *>(csum4 + 4 * ch);
-            wcs = double((q.x + q.y) + (q.z + q.w));
-            if constexpr (ENT) {
-                const float4 e = *reinterpret_cast<const float4 *>(cent4 + 4 * ch);
-                wce = double((e.x + e.y) + (e.z + e.w));
-            }
-        }
-    }
-    const double wincl = row_scan_dpp(wcs);  // lane k < 16: the wave's sum through its chunk k
-    {
-        // the wave's maximum when greedy; otherwise the value its reference came from (a lower
-        // bound of its maximum: every sum is taken relative to RN(value c))
-        const float wm = p.greedy ? wave_max3_dpp(lmax) : sref_v;
-        double wh = 0.0;
-        if constexpr (ENT) wh = row_scan_dpp(wce);
-        if (lane == kRRWaves - 1) {
-            wtot[wave] = wincl;
-            if constexpr (ENT) went[wave] = wh;
-        }
-        if (lane == 0) {
-            wmax[wave] = wm;
-            wref[wave] = sref;
-        }
-    }
-    __syncthreads();
-
-    // ---- phase 2 (every wave, to the same bits): lane w of each 16-lane row takes wave w's
-    // totals. The row's reference value M (the largest wave reference; the exact maximum when
-    // greedy), the row's sums relative to A = M c by an f64 scan over the waves in index order,
-    // and the wave whose chunks hold u S. No second barrier: that wave goes on alone.
-    const int lw = lane & (kRRWaves - 1);
-    const float rw = wref[lw];
-    const double tw = wtot[lw];
-    double hw = 0.0;
-    if constexpr (ENT) hw = went[lw];
-    const float M = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(row_max3_dpp(wmax[lw]))));
-    auto refuse = [&](uint8_t st, bool leader) {
-        if (leader) {
-            p.ids[row] = -1;
-            if (p.logp) p.logp[row] = NAN;
-            if (p.ent) p.ent[row] = NAN;
-            p.status[row] = st;
-        }
-    };
-    if (M == -INFINITY) {
-        refuse(NT_ROW_NO_TOKEN, tid == 0);
-        return;
-    }
-    const float A = M * c;  // >= every wave reference (rounding is monotonic)
-    const bool wlive = rw != -INFINITY;
-    const float wf = wlive ? exp2_hw(rw - A) : 0.0f;
-    const double wt = wlive ? double(wf) * tw : 0.0;
-    const double incl = row_scan_dpp(wt);
-    const double S = readlane_d(incl, kRRWaves - 1);
-    if (!(S == S)) {
-        refuse(NT_ROW_NAN, tid == 0);
-        return;
-    }
-    // The entropy sum relative to A, taken only by the wave that writes the row (every wave
-    // works this phase on the same values, four to a SIMD, so it holds no more than it needs).
-    auto entropy_sum = [&]() -> double {
-        if constexpr (!ENT) return 0.0;
-        const double lh = (wlive && tw > 0.0) ? double(wf) * (hw + double(rw - A) * tw) : 0.0;
-        return readlane_d(row_scan_dpp(lh), kRRWaves - 1);
-    };
-    // ln sum exp(z - m) and the entropy, from the sums relative to A = M c (computed by the
-    // one lane that writes the row).
-    auto write_row = [&](int64_t id, float vz, double H) {
-        const double shiftA = double(A) - double(M) * double(c);
-        const double lnS = ln_fast(S) + shiftA * kLn2;
-        const bool zv = MK == NT_MASK_F32 || tau_one;
-        const float zid = zv ? vz : vz / p.tau;
-        const float mz = zv ? M : M / p.tau;  // the maximum in z units
-        p.ids[row] = int32_t(id);
-        if (p.logp) p.logp[row] = float((double(zid) - double(mz)) - lnS);
-        if (p.ent) p.ent[row] = float(lnS - kLn2 * (H / S + shiftA));
-        p.status[row] = NT_ROW_OK;
-    };
-    // Decode chunk k of this wave again (the mask from LDS; every DMA has completed).
-    auto chunk_values = [&](const RRX<DT, EPL> &r, int ch, float *v) {
-        uint32_t mw[RRMask<MK, EPL>::kWords];
-        lds_mask_words<MK, EPL>(mbase + ch * MB + lane * EPL * MaskWords<MK>::kBytes, mw);
-        decode_e<DT, MK, EPL>(r.x, mw, v, p.tau, tau_one);
-        if (int64_t(ch + 1) * CH > p.V) {
-            const int64_t e0 = int64_t(ch) * CH + lane * EPL;
-#pragma unroll
-            for (int j = 0; j < EPL; j++)
-                if (e0 + j >= p.V) v[j] = -INFINITY;
-        }
-    };
-
-    if (p.greedy) {
-        // The first element equal to the maximum, in index order.
-        int first = 0x7fffffff;
-        static_for<0, K>([&](auto kc) {
-            constexpr int k = decltype(kc)::value;
-            const int ch = wave * K + k;
-            if (ch < nc) {
-                float v[EPL];
-                chunk_values(raw[k], ch, v);
-#pragma unroll
-                for (int j = EPL - 1; j >= 0; j--)
-                    if (v[j] == M) first = min(first, ch * CH + lane * EPL + j);
-            }
-        });
-        first = wave_min_i(first);
-        if (lane == 0) wpick[wave] = first;
-        __syncthreads();
-        int best = 0x7fffffff;
-        for (int i = 0; i < kRRWaves; i++) best = min(best, wpick[i]);
-        const double H = entropy_sum();
-        if (tid == 0) write_row(best, M, H);
-        return;
-    }
-
-    // The wave whose chunks hold t = u S: the first with its inclusive sum past t.
-    const double t = u_row * S;
-    const bool wl = lane < kRRWaves;
-    int wsel = first_lane(__ballot(wl && incl > t && wt > 0.0));
-    if (wsel < 0) wsel = last_lane(__ballot(wl && wt > 0.0));  // u S rounded up to S
-    if (wsel < 0) {  // unreachable: M's wave has weight; never leave stale outputs
-        refuse(NT_ROW_NAN, tid == 0);
-        return;
-    }
-    if (wave != wsel) return;
-    // ---- phase 3 (that wave alone): the target in its own scale (the part of t past the waves
-    // before it, divided by 2^(s - A)), the crossing chunk from the prefix held since phase 1,
-    // then that chunk's registers.
-    const double tl = readlane_d((t - (incl - wt)) * double(exp2_hw(A - rw)), wsel);
-    const bool lk = lane < K;
-    int kstar = first_lane(__ballot(lk && wincl > tl && wcs > 0.0));
-    if (kstar < 0) kstar = last_lane(__ballot(lk && wcs > 0.0));  // rounding between the two scans
-    if (kstar < 0) {  // unreachable: the wave has weight
-        refuse(NT_ROW_NAN, lane == 0);
-        return;
-    }
-    const double tloc = readlane_d(tl - (wincl - wcs), kstar);
-    const int cstar = wave * K + kstar;
-    const double H = entropy_sum();
-    RRX<DT, EPL> r = raw[0];
-    static_for<1, K>([&](auto kc) {
-        constexpr int k = decltype(kc)::value;
-        if (k == kstar) r = raw[k];
-    });
-    float v[EPL];
-    chunk_values(r, cstar, v);
-    const float sr = sref;
-    float w[EPL];
-    int jlast = -1;
-#pragma unroll
-    for (int j = 0; j < EPL; j++) {
-        w[j] = exp2_hw(fmaf(v[j], c, -sr));
-        if (w[j] > 0.0f) jlast = j;
-    }
-    const double ls = double(tree_sum<EPL>(w));
-    const double cincl = wave_scan_dpp(ls);
-    int lsel = first_lane(__ballot(cincl > tloc && ls > 0.0));
-    const bool none = lsel < 0;
-    if (none) lsel = last_lane(__ballot(jlast >= 0));  // rounding: the last lane with weight
-    if (lsel < 0) {  // unreachable: the chunk holds weight
-        refuse(NT_ROW_NAN, lane == 0);
-        return;
-    }
-    // The crossing lane walks its elements from the prefix before them (f32 partial sums
-    // inside the lane, compared against the f64 target).
-    int jsel = -1;
-    {
-        const double t0 = tloc - (cincl - ls);
-        float C = 0.0f;
-#pragma unroll
-        for (int j = 0; j < EPL; j++) {
-            C += w[j];
-            if (jsel < 0 && !none && double(C) > t0) jsel = j;
-        }
-        if (jsel < 0) jsel = jlast;
-    }
-    if (lane == lsel) {
-        if (jsel < 0) jsel = 0;
-        float vz = v[0];
-#pragma unroll
-        for (int j = 1; j < EPL; j++)
-            if (j == jsel) vz = v[j];
-        write_row(int64_t(cstar) * CH + lane * EPL + jsel, vz, H);
-    }
-}
 
 // ------------------------------------------------------------------ scorer
 
@@ -2035,97 +894,6 @@ __global__ void k_kl_estimate_grad(const float *lp, const float *lr, const float
 
 // ------------------------------------------------------------------ dispatch helpers
 
-int check_rows(int64_t rows, int64_t V, int64_t ld, int32_t dtype, int32_t mk, const void *mask, int64_t mask_ld,
-               const char *who) {
-    char buf[256];
-    if (rows < 0 || V < 1 || ld < V || (dtype != NT_F32 && dtype != NT_BF16) || mk < NT_MASK_NONE ||
-        mk > NT_MASK_F32 || ((mk == NT_MASK_NONE) != (mask == nullptr)) || (mask_ld != 0 && mask_ld < V) ||
-        rows > 0x7fffffffLL) {
-        std::snprintf(buf, sizeof buf,
-                      "%s: invalid rows %lld, V %lld, ld %lld, dtype %d, mask kind %d (mask %s), mask_ld %lld", who,
-                      (long long)rows, (long long)V, (long long)ld, dtype, mk, mask ? "set" : "null",
-                      (long long)mask_ld);
-        return fail(NT_E_ARG, buf);
-    }
-    return 0;
-}
-
-bool aligned_rows(const void *x, int64_t V, int64_t ld, int32_t dtype, int32_t mk, const void *mask, int64_t mask_ld) {
-    if (V % kEpl != 0 || ld % kEpl != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0) return false;
-    (void)dtype;
-    if (mk == NT_MASK_U8) return mask_ld % 8 == 0 && reinterpret_cast<uintptr_t>(mask) % 8 == 0;
-    if (mk == NT_MASK_F32) return mask_ld % 4 == 0 && reinterpret_cast<uintptr_t>(mask) % 16 == 0;
-    return true;
-}
-
-template <int DT, int MK, bool ENT, bool AL>
-void launch_sample(const SampleP &p, int64_t rows, int threads, size_t shm, hipStream_t s) {
-    hipLaunchKernelGGL((k_sample<DT, MK, ENT, AL>), dim3(unsigned(rows)), dim3(threads), shm, s, p);
-}
-
-template <int DT, int MK, bool ENT>
-void pick_al_sample(bool al, const SampleP &p, int64_t rows, int threads, size_t shm, hipStream_t s) {
-    if (al) launch_sample<DT, MK, ENT, true>(p, rows, threads, shm, s);
-    else launch_sample<DT, MK, ENT, false>(p, rows, threads, shm, s);
-}
-
-template <int DT, int MK>
-void pick_ent_sample(bool ent, bool al, const SampleP &p, int64_t rows, int threads, size_t shm, hipStream_t s) {
-    if (ent) pick_al_sample<DT, MK, true>(al, p, rows, threads, shm, s);
-    else pick_al_sample<DT, MK, false>(al, p, rows, threads, shm, s);
-}
-
-template <int DT>
-void pick_mk_sample(int mk, bool ent, bool al, const SampleP &p, int64_t rows, int threads, size_t shm,
-                    hipStream_t s) {
-    if (mk == NT_MASK_U8) pick_ent_sample<DT, NT_MASK_U8>(ent, al, p, rows, threads, shm, s);
-    else if (mk == NT_MASK_F32) pick_ent_sample<DT, NT_MASK_F32>(ent, al, p, rows, threads, shm, s);
-    else pick_ent_sample<DT, NT_MASK_NONE>(ent, al, p, rows, threads, shm, s);
-}
-
-// Largest chunks-per-wave of the register-resident sampler at EPL elements per lane: K chunks
-// of logit words live in VGPRs (64 registers: bf16 EPL/2 words per chunk, f32 EPL) and the mask
-// of every chunk in LDS (u8 64 EPL bytes, f32 256 EPL bytes; at most 128 KiB).
-int rr_kmax(int dtype, int mk, int epl) {
-    int k = (dtype == NT_BF16 ? 128 : 64) / epl;
-    if (mk == NT_MASK_F32) k = k < 32 / epl ? k : 32 / epl;  // 16 waves * K * 256 EPL bytes <= 128 KiB
-    return k;
-}
-
-template <int DT, int MK, int K, int EPL>
-void launch_rr_k(bool ent, const SampleP &p, int64_t rows, hipStream_t s) {
-    if (ent) hipLaunchKernelGGL((k_sample_rr<DT, MK, K, true, EPL>), dim3(unsigned(rows)), dim3(kRRThreads), 0, s, p);
-    else hipLaunchKernelGGL((k_sample_rr<DT, MK, K, false, EPL>), dim3(unsigned(rows)), dim3(kRRThreads), 0, s, p);
-}
-
-// K is a power of two up to rr_kmax(DT, MK, EPL); the instantiations are exactly those.
-template <int DT, int MK, int EPL>
-void launch_rr_mk(int K, bool ent, const SampleP &p, int64_t rows, hipStream_t s) {
-    constexpr int KREG = (DT == NT_BF16 ? 128 : 64) / EPL;
-    constexpr int KMAX = MK == NT_MASK_F32 && 32 / EPL < KREG ? 32 / EPL : KREG;
-    switch (K) {
-        case 1: launch_rr_k<DT, MK, 1, EPL>(ent, p, rows, s); break;
-        case 2: launch_rr_k<DT, MK, 2, EPL>(ent, p, rows, s); break;
-        case 4: if constexpr (KMAX >= 4) launch_rr_k<DT, MK, 4, EPL>(ent, p, rows, s); break;
-        case 8: if constexpr (KMAX >= 8) launch_rr_k<DT, MK, 8, EPL>(ent, p, rows, s); break;
-        case 16: if constexpr (KMAX >= 16) launch_rr_k<DT, MK, 16, EPL>(ent, p, rows, s); break;
-        default: break;
-    }
-}
-
-template <int EPL>
-void launch_rr(int dtype, int mk, int K, bool ent, const SampleP &p, int64_t rows, hipStream_t s) {
-    if (dtype == NT_F32) {
-        if (mk == NT_MASK_U8) launch_rr_mk<NT_F32, NT_MASK_U8, EPL>(K, ent, p, rows, s);
-        else if (mk == NT_MASK_F32) launch_rr_mk<NT_F32, NT_MASK_F32, EPL>(K, ent, p, rows, s);
-        else launch_rr_mk<NT_F32, NT_MASK_NONE, EPL>(K, ent, p, rows, s);
-    } else {
-        if (mk == NT_MASK_U8) launch_rr_mk<NT_BF16, NT_MASK_U8, EPL>(K, ent, p, rows, s);
-        else if (mk == NT_MASK_F32) launch_rr_mk<NT_BF16, NT_MASK_F32, EPL>(K, ent, p, rows, s);
-        else launch_rr_mk<NT_BF16, NT_MASK_NONE, EPL>(K, ent, p, rows, s);
-    }
-}
-
 template <int DT, int MK, bool REF, bool KL, bool ENT>
 void pick_al_score(bool al, const ScoreP &p, int64_t rows, hipStream_t s) {
     if (al) hipLaunchKernelGGL((k_score<DT, MK, REF, KL, ENT, true>), dim3(unsigned(rows)), dim3(kScoreThreads), 0, s, p);
@@ -2159,66 +927,6 @@ void pick_mk_score(int mk, bool ref, bool kl, bool ent, bool al, const ScoreP &p
 using namespace nt;
 
 extern "C" {
-
-int nt_hip_rl_sample(const NtRlSampleArgs *a) {
-    if (!a) return fail(NT_E_ARG, "nt_hip_rl_sample: null args");
-    if (int rc = check_rows(a->rows, a->vocab, a->ld, a->dtype, a->mask_kind, a->mask, a->mask_ld, "nt_hip_rl_sample"))
-        return rc;
-    if (!(a->temperature >= 0.0) || !std::isfinite(a->temperature))
-        return fail(NT_E_ARG, "sample_categorical: temperature " + std::to_string(a->temperature) + " (must be ≥ 0)");
-    const bool greedy = a->temperature == 0.0;
-    if (!a->logits || !a->ids || !a->status || (!greedy && !a->uniforms))
-        return fail(NT_E_ARG, "nt_hip_rl_sample: null logits, ids, status or uniforms");
-    std::unique_lock<std::mutex> lk;
-    if (int rc = enter(&lk)) return rc;
-    if (a->rows == 0) return 0;
-    const int64_t nc = (a->vocab + kChunk - 1) / kChunk;
-    const bool ent = a->entropy != nullptr;
-    const size_t shm = size_t(nc) * sizeof(float) * (ent ? 3 : 2);
-    if (shm > 64 * 1024) return fail(NT_E_UNSUPPORTED, "nt_hip_rl_sample: V " + std::to_string(a->vocab) + " too large");
-    SampleP p;
-    p.logits = a->logits;
-    p.mask = a->mask;
-    p.V = a->vocab;
-    p.ld = a->ld;
-    p.mask_ld = a->mask_ld;
-    const double T = greedy ? 1.0 : a->temperature;
-    p.tau = float(T);
-    p.tau_one = (T == 1.0);
-    p.c = (a->mask_kind == NT_MASK_F32 || T == 1.0) ? kLog2e : float(double(kLog2e) / double(p.tau));
-    p.greedy = greedy;
-    p.nc = int(nc);
-    p.u = a->uniforms;
-    p.ids = a->ids;
-    p.logp = a->logp;
-    p.ent = a->entropy;
-    p.status = a->status;
-    // Waves per row: about four chunks per wave, at most 16; many rows get smaller groups.
-    int nw = int(nc / 4);
-    nw = nw < 1 ? 1 : (nw > 16 ? 16 : nw);
-    if (a->rows >= 2048 && nw > 4) nw = 4;
-    const bool al = aligned_rows(a->logits, a->vocab, a->ld, a->dtype, a->mask_kind, a->mask, a->mask_ld);
-    hipStream_t s = ctx().stream;
-    // Rows that fit the register-resident kernel take it (chunks per wave K = 1..16); the
-    // streaming kernel takes everything else (unaligned rows, larger V).
-    if (al) {
-        // 8 elements per lane (512-element chunks): 16 per lane measured slower on MI355X at c4
-        // (19.37 us, or 18.81 with a one-chunk window, against 18.24-18.52 us at 8).
-        constexpr int epl = 8;
-        const int64_t nch = (a->vocab + kWave * epl - 1) / (kWave * epl);
-        const int kmax = rr_kmax(a->dtype, a->mask_kind, epl);
-        if (nch <= int64_t(kRRWaves) * kmax) {
-            int K = 1;
-            while (int64_t(kRRWaves) * K < nch) K *= 2;
-            p.nc = int(nch);
-            launch_rr<8>(a->dtype, a->mask_kind, K, ent, p, a->rows, s);
-            return launched("nt_hip_rl_sample");
-        }
-    }
-    if (a->dtype == NT_F32) pick_mk_sample<NT_F32>(a->mask_kind, ent, al, p, a->rows, nw * kWave, shm, s);
-    else pick_mk_sample<NT_BF16>(a->mask_kind, ent, al, p, a->rows, nw * kWave, shm, s);
-    return launched("nt_hip_rl_sample");
-}
 
 int nt_hip_rl_score(const NtRlScoreArgs *a) {
     if (!a) return fail(NT_E_ARG, "nt_hip_rl_score: null args");

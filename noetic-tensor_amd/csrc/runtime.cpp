@@ -52,6 +52,16 @@ int launched(const char *what) {
 static std::mutex g_pending_mu;
 static std::vector<void *> g_pending;
 
+int enter_nofree(std::unique_lock<std::mutex> *out) {
+    Ctx &c = ctx();
+    std::unique_lock<std::mutex> lk(c.mu);
+    if (c.device < 0) return fail(NT_E_UNCLAIMED, "no HIP device claimed in this process (nt_hip_claim)");
+    hipError_t e = hipSetDevice(c.device);
+    if (e != hipSuccess) return hip_check(e, "hipSetDevice");
+    *out = std::move(lk);
+    return 0;
+}
+
 int enter(std::unique_lock<std::mutex> *out) {
     Ctx &c = ctx();
     std::unique_lock<std::mutex> lk(c.mu);

@@ -1,4 +1,5 @@
-"""The register-resident sampler at every chunks-per-wave K it is built for, against the oracle.
+"""The register-resident and the segmented samplers at every shape they are built for, against
+the oracle.
 
 The kernel cuts a row into 512-element chunks and gives wave w (of 16) the K consecutive chunks
 [w K, w K + K), K the smallest power of two with 16 K chunks covering the row (bf16 up to 16,
@@ -84,7 +85,40 @@ def cases():
 
 
 @pytest.mark.parametrize("dtype,mask,K,V", cases())
-def test_register_resident_sampler_levels(dtype, mask, K, V):
+def test_register_resident_sampler_levels(dtype, mask, K, V, monkeypatch):
+    monkeypatch.setenv("NOETIC_HIP_SAMPLE_SEG", "off")  # one workgroup per row, whatever the row count
+    check_levels(dtype, mask, K, V)
+
+
+def seg_cases():
+    """(dtype, mask, NW, K, window, V) for the segmented sampler: every shape it is built for, V
+    one element past a segment boundary (the last segment holds one partial chunk) and just below
+    a whole number of segments, the f32 additive and no mask, both load windows."""
+    out = []
+    for dtype in ("bf16", "f32"):
+        for nw, k in ((4, 4), (8, 4), (4, 8), (8, 8), (4, 16), (8, 16)):
+            if dtype == "f32" and k > 8:
+                continue
+            seg = nw * k * CHUNK
+            out += [(dtype, "u8", nw, k, "one", 2 * seg + 8), (dtype, "u8", nw, k, "one", 3 * seg - 40)]
+            if k == 4:
+                out += [(dtype, "u8", nw, k, "all", 5 * seg - 8)]
+    out += [("f32", "f32add", 4, 4, "one", 4 * 4 * 4 * CHUNK - 8), ("bf16", "f32add", 8, 8, "one", 2 * 8 * 8 * CHUNK),
+            ("bf16", "none", 8, 4, "all", 128256), ("f32", "none", 8, 8, "one", 50304)]
+    return out
+
+
+@pytest.mark.parametrize("dtype,mask,nw,K,window,V", seg_cases())
+def test_segmented_sampler_levels(dtype, mask, nw, K, window, V, monkeypatch):
+    """The same rows through the segmented sampler: the row cut into segments of nw waves of K
+    chunks (one workgroup each); the last segment to arrive merges the wave records (phase 2 over
+    up to 64 records), finds the crossing wave and chunk and reads that chunk again."""
+    monkeypatch.setenv("NOETIC_HIP_SAMPLE_SEG", f"{nw},{K}")
+    monkeypatch.setenv("NOETIC_HIP_SAMPLE_WINDOW", window)
+    check_levels(dtype, mask, K, V)
+
+
+def check_levels(dtype, mask, K, V):
     rng = np.random.default_rng(V * 7 + K)
     x, keep = rows_for(V, rng, K)
     rows = x.shape[0]
@@ -126,15 +160,17 @@ def test_register_resident_sampler_levels(dtype, mask, K, V):
             assert ids[2] == V - 1 and ids[3] == 0
 
 
+@pytest.mark.parametrize("seg", ["off", "8,4", "4,8"])
 @pytest.mark.parametrize("dtype,mask,V", [("bf16", "u8", WAVES * 16 * CHUNK - 8), ("f32", "u8", WAVES * 4 * CHUNK - 8),
                                           ("f32", "f32add", WAVES * 2 * CHUNK), ("bf16", "none", 4096)])
-def test_register_resident_sampler_refusals(dtype, mask, V):
+def test_register_resident_sampler_refusals(dtype, mask, V, seg, monkeypatch):
     """Each row is refused on its own: a NaN in the first wave's range, in a middle wave's, in the
     row's last element, or a +inf logit (its weight is inf - inf) gives NT_ROW_NAN; a row with
     every token excluded gives NT_ROW_NO_TOKEN; the rows between them sample as the oracle does.
     A NaN at a token the u8 mask excludes does not reach the row; under an f32 mask's -inf it
     does (NaN + -inf), as in the reference's tempered_logits."""
     import ctypes as C
+    monkeypatch.setenv("NOETIC_HIP_SAMPLE_SEG", seg)
     rows = 10
     rng = np.random.default_rng(V)
     x = rng.normal(0, 2, (rows, V)).astype(np.float32)
