@@ -155,6 +155,17 @@ typedef struct NtRlSampleArgs {
 } NtRlSampleArgs;
 int nt_hip_rl_sample(const NtRlSampleArgs *a);
 
+/* nt_hip_rl_sample without allocation. No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). Same arguments, kernels and results as nt_hip_rl_sample; the segmented
+ * sampler's workspace (its per-row arrival counters and wave records) is a fixed device array
+ * of 2 MiB per GPU instead of the library's allocation, and a launch that needs more is refused
+ * (NT_E_ARG) before anything runs. The call makes no hipMalloc, hipFree or other allocating call
+ * (pointers released with nt_hip_free are freed by the next other entry point). Calls share that
+ * GPU's array and leave the last call's records in it; they are ordered on the library's stream,
+ * and calls that overlap on one GPU race. */
+int nt_hip_rl_sample_noalloc(const NtRlSampleArgs *a);
+
 /* Fused row scoring: for each row, any of
  *   logp[r]     = token_log_probs(z, tokens)[r]                 (rl.rs:134-141)
  *   ref_logp[r] = token_log_probs(zr, tokens)[r]                (rl.rs:134-141, reference)

@@ -117,6 +117,7 @@ _SIGS = {
     "nt_hip_launches": (C.c_uint64, []),
     "nt_hip_rl_sample": (C.c_int, [C.POINTER(NtRlSampleArgs)]),
     "nt_hip_rl_sample_gumbel": (C.c_int, [C.POINTER(NtRlGumbelArgs)]),
+    "nt_hip_rl_sample_noalloc": (C.c_int, [C.POINTER(NtRlSampleArgs)]),
     "nt_hip_rl_score": (C.c_int, [C.POINTER(NtRlScoreArgs)]),
     "nt_hip_rl_score_backward": (C.c_int, [C.POINTER(NtRlScoreGradArgs)]),
     "nt_hip_rl_kl_estimate": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_int32, C.c_double,
