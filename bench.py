@@ -136,11 +136,22 @@ def line(metric, value, steps, warmup, ms, dtype, config, roof, **extra):
     return out
 
 
-def cpu_baseline(w, rows_sample, seed, min_seconds=10.0):
-    """The reference's CPU path on a bounded sample of the same rows: tempered_logits, the
-    max_dim check, one Gumbel draw per logit from the ChaCha stream, argmax, log_softmax and
-    gather, single-threaded in f32 (Cpu(Reference), oracle/oracle.c). Also the same unfused
-    sequence with the inverse-CDF draw split over every host core (a Cpu(Fast)-style port)."""
+def cpu_threads():
+    """The Cpu(Fast) worker count: NOETIC_THREADS, else every host core (src/tensor/backend.rs:59-61)."""
+    try:
+        n = int(os.environ.get("NOETIC_THREADS", ""))
+    except ValueError:
+        n = 0
+    return max(1, n or (os.cpu_count() or 1))
+
+
+def cpu_baseline(w, rows_sample, seed, min_seconds=10.0, gpu=None):
+    """The reference's CPU path on a bounded sample of the same rows (restated in oracle/oracle.c):
+    tempered_logits, the max_dim check, one Gumbel draw per logit from the ChaCha stream, argmax,
+    then token_log_probs (log_softmax and gather), in f32, on Cpu(Reference) (one thread) and on
+    Cpu(Fast) (its thresholds and threading, NOETIC_THREADS workers). Also the build's own unfused
+    inverse-CDF port on every core. `gpu` = (ids, logp, uniforms) of one device launch over the
+    same rows: its parity against the oracle is checked here, outside any timed region."""
     import workloads as W
     from oracle import oracle as O
     V = w["V"]
@@ -155,18 +166,56 @@ def cpu_baseline(w, rows_sample, seed, min_seconds=10.0):
         O.cpuref_sample_logp(x, w["temperature"], keep, rng)
         t_ref += time.perf_counter() - t0
         reps += 1
+    threads = cpu_threads()
+    rng_f = O.Rng(seed, f"{w['name']}/gumbel")
+    reps_f, t_fast = 0, 0.0
+    while reps_f < 1 or (t_fast < min_seconds / 2 and reps_f < 1000):
+        t0 = time.perf_counter()
+        O.cpufast_sample_logp(x, w["temperature"], keep, rng_f, threads)
+        t_fast += time.perf_counter() - t0
+        reps_f += 1
     cores = os.cpu_count() or 1
     u = O.Rng(seed, f"{w['name']}/uniforms").uniforms(rows_sample)
     t0 = time.perf_counter()
     O.cpu_sample_logp_invcdf(x, w["temperature"], keep, u, threads=cores)
-    t_fast = time.perf_counter() - t0
-    return {
+    t_inv = time.perf_counter() - t0
+    out = {
         "value": reps * rows_sample / t_ref, "unit": "rows/s", "cores": 1, "kind": "port", "cpu": cpu_model(),
         "sample": f"{reps} x {rows_sample} {w['name']} rows (V={V}, values widened to f32): the reference's "
-                  f"Cpu(Reference) op sequence with Gumbel-max sampling, single thread, {t_ref:.2f} s",
-        "fast_port": {"value": rows_sample / t_fast, "unit": "rows/s", "cores": cores,
-                      "what": "unfused op sequence with the inverse-CDF draw, rows split over threads"},
+                  f"Cpu(Reference) op sequence (Gumbel-max sample_categorical, then token_log_probs), single "
+                  f"thread, {t_ref:.2f} s",
+        "fast": {"value": reps_f * rows_sample / t_fast, "unit": "rows/s", "cores": threads, "kind": "port",
+                 "sample": f"{reps_f} x {rows_sample} rows, the same op sequence on Cpu(Fast): maps threaded from "
+                           f"2^20 elements, equal-shape zips and last-axis sums from 2^22, {threads} threads "
+                           f"(NOETIC_THREADS, else all cores), {t_fast:.2f} s; the Gumbel draws stay one "
+                           f"sequential stream"},
+        "inv_cdf_port": {"value": rows_sample / t_inv, "unit": "rows/s", "cores": cores,
+                         "what": "the build's own unfused op sequence with the inverse-CDF draw (one uniform per "
+                                 "row), rows split over threads; not a reference backend"},
     }
+    if gpu is not None:
+        out["parity"] = parity_against_oracle(O, x, keep, w["temperature"], *gpu)
+    return out
+
+
+def parity_against_oracle(O, x, keep, tau, ids, logp, u):
+    """One device launch's ids and log-probs against the oracle's f64 inverse-CDF draw on the same
+    rows and uniforms: ids must be equal except draws within 1e-6 of a CDF edge (counted), log-
+    probs within the f32 tolerance (1e-5 relative, 1e-6 absolute; the bf16 inputs are exact in
+    f32). The largest errors observed are reported."""
+    z = O.tempered(x, tau, keep=keep)
+    want, edges = O.sample_invcdf(z, u)
+    boundary = edges < 1e-6
+    differ = ids != want
+    ref_lp = O.token_logp(z, ids)
+    err = np.abs(logp.astype(np.float64) - ref_lp)
+    ok = bool(np.all(boundary[differ]) and np.all(err <= 1e-6 + 1e-5 * np.abs(ref_lp)))
+    return {"rows": int(len(ids)), "ids_differ": int(differ.sum()), "boundary_draws": int(boundary.sum()),
+            "ids_differ_off_boundary": int((differ & ~boundary).sum()),
+            "logp_max_abs_err": float(err.max()), "logp_max_rel_err": float(np.max(err / np.maximum(np.abs(ref_lp), 1e-30))),
+            "logp_max_ref_tol": float(np.max(err / (1.0 + np.abs(ref_lp)))),
+            "tolerance": "ids exact except |u - CDF edge| < 1e-6; logp |d| <= 1e-6 + 1e-5 |ref| (f32)",
+            "within_tolerance": ok}
 
 
 def cpu_baseline_scoring(w, rows_sample, min_seconds=10.0):
@@ -255,6 +304,13 @@ def bench_sample(nr, W, args, name):
     if np.any(st != 0):
         raise SystemExit(f"bench: {int(np.sum(st != 0))} rows refused")
     ms_warm, _ = timed(nr, args.steps, args.warmup, lambda i: L.nt_hip_rl_sample(C.byref(warm[i])))
+    # More repetitions of the same K cold launches, outside the contract's timed region: the spread
+    # of the per-launch average from one K-launch window to the next.
+    repeats = [timed(nr, args.steps, 0, lambda i: L.nt_hip_rl_sample(C.byref(cold[i])))[0] for _ in range(5)]
+    # One launch on copy 0 with the first uniforms, for the parity check of the CPU leg.
+    nr._check(L.nt_hip_rl_sample(C.byref(cold[0])), "sample")
+    gpu_out = (ids.to_numpy().ravel().astype(np.int64), logp.to_numpy().ravel().copy(),
+               U.to_numpy().ravel()[:rows].copy())
     roof = roofline(bytes_launch, ms, "k_sample_rr_c4_traffic.json" if name == "c4" else None)
     roof["inputs"] = (f"HBM-cold: launches cycle over {copies} input copies "
                       f"({copies * bytes_launch / 2**20:.0f} MiB), beyond the 256 MB Infinity Cache")
@@ -282,9 +338,12 @@ def bench_sample(nr, W, args, name):
                               "all) so every read comes from HBM", "rows": rows, "vocab": V,
                   "parallelism": "none (1 GPU)"}
     out = line(metric, rows / (ms * 1e-3), args.steps, args.warmup, ms, "bf16" if esz == 2 else "f32", config, roof,
-               achieved_gbs=roof["achieved"], wall_s_timed_region=wall, key=nr.key())
+               achieved_gbs=roof["achieved"], wall_s_timed_region=wall, key=nr.key(),
+               ms_per_step_repeats=repeats, ms_per_step_median_of_repeats=float(np.median(repeats)))
     if args.cpu_rows > 0:
-        out["cpu_baseline"] = cpu_baseline(w, min(args.cpu_rows, rows), args.seed, args.cpu_seconds)
+        n_cpu = min(args.cpu_rows, rows)
+        gpu = tuple(a[:n_cpu] for a in gpu_out)
+        out["cpu_baseline"] = cpu_baseline(w, n_cpu, args.seed, args.cpu_seconds, gpu=gpu)
     return out
 
 

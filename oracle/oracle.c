@@ -463,8 +463,6 @@ void or_cpuref_log_softmax(const float *x, int64_t rows, int64_t V, float *y) {
     free(mx); free(shifted); free(e); free(lse);
 }
 
-/* tempered_logits over [rows, V]: a materialised divide, then a materialised broadcast add of
- * the additive form of the keep-mask (0 / -inf), as the reference's op sequence runs. */
 /* tempered_logits (rl.rs:475-486) as CpuRef materialises it: div_scalar (skipped at tau 1,
  * float.rs:494-499), then the broadcast add of the additive mask, f32 throughout. A u8 keep
  * row stands for the additive row (0 kept, -inf excluded). */
@@ -562,6 +560,131 @@ int64_t or_cpuref_sample_logp(const float *x, int64_t rows, int64_t V, double ta
     free(y);
     free(zg);
     free(z);
+    return 0;
+}
+
+/* ===================================================================== Cpu(Fast)
+ * The reference's Cpu(Fast) backend (src/tensor/backend.rs:57-239) as the sampler's op sequence
+ * meets it: elementwise maps run on threads from FAST_MIN_MAP = 2^20 elements, zips of equal
+ * shapes from FAST_MIN_ZIP = 2^22, last-axis sums from FAST_MIN_SUM = 2^22 with the 16-accumulator
+ * lane sum (simd_sum); everything else (max_dim, argmax, broadcast zips, the Gumbel draws, the
+ * gather) runs as Cpu(Reference) does. Threads are spawned per op call, as the reference's
+ * scoped threads are, each taking one contiguous part of ceil(n / threads) elements. */
+#define OR_FAST_MIN_MAP ((size_t)1 << 20)
+#define OR_FAST_MIN_ZIP ((size_t)1 << 22)
+#define OR_FAST_MIN_SUM ((size_t)1 << 22)
+
+typedef struct {
+    int op; /* 0: y = x / t, 1: y = a + b, 2: y = expf(x), 3: lane sums */
+    const float *a, *b;
+    float *y;
+    float t;
+    size_t lo, hi; /* elements (ops 0-2) or lanes (op 3) */
+    int64_t n;     /* lane length (op 3) */
+} fast_job;
+
+/* simd_sum (backend.rs:92-115): 16 accumulators over chunks of 16, added in order, then the
+ * remainder. */
+static float fast_simd_sum(const float *x, int64_t n) {
+    float acc[16] = {0};
+    int64_t i = 0;
+    for (; i + 16 <= n; i += 16)
+        for (int k = 0; k < 16; k++) acc[k] = acc[k] + x[i + k];
+    float total = 0.0f;
+    for (int k = 0; k < 16; k++) total = total + acc[k];
+    for (; i < n; i++) total = total + x[i];
+    return total;
+}
+
+static void *fast_run(void *arg) {
+    fast_job *j = (fast_job *)arg;
+    switch (j->op) {
+        case 0: for (size_t i = j->lo; i < j->hi; i++) j->y[i] = j->a[i] / j->t; break;
+        case 1: for (size_t i = j->lo; i < j->hi; i++) j->y[i] = j->a[i] + j->b[i]; break;
+        case 2: for (size_t i = j->lo; i < j->hi; i++) j->y[i] = expf(j->a[i]); break;
+        default: for (size_t l = j->lo; l < j->hi; l++) j->y[l] = fast_simd_sum(j->a + (int64_t)l * j->n, j->n); break;
+    }
+    return NULL;
+}
+
+/* One op over [0, n) on `parts` threads (fill, backend.rs:74-89). */
+static void fast_par(int op, const float *a, const float *b, float *y, float t, size_t n, int64_t lane, int parts) {
+    size_t per = (n + (size_t)parts - 1) / (size_t)parts;
+    if (per == 0) per = 1;
+    int used = (int)((n + per - 1) / per);
+    pthread_t th[256];
+    fast_job jobs[256];
+    if (used > 256) used = 256;
+    for (int i = 0; i < used; i++) {
+        size_t lo = (size_t)i * per, hi = lo + per < n ? lo + per : n;
+        fast_job j = {op, a, b, y, t, lo, hi, lane};
+        jobs[i] = j;
+        pthread_create(&th[i], NULL, fast_run, &jobs[i]);
+    }
+    for (int i = 0; i < used; i++) pthread_join(th[i], NULL);
+}
+
+int64_t or_cpufast_sample_logp(const float *x, int64_t rows, int64_t V, double tau, const uint8_t *keep,
+                               int64_t keep_ld, or_chacha *rng, int threads, int64_t *ids, float *logp) {
+    size_t n = (size_t)rows * (size_t)V;
+    const int parts = threads < 1 ? 1 : (threads > 256 ? 256 : threads);
+    const double tt = tau == 0.0 ? 1.0 : tau;
+    /* tempered_logits: div_scalar (a map), then + the additive mask (a zip of equal shapes, or a
+     * broadcast zip for a shared mask row) */
+    float *z = (float *)malloc(n * sizeof(float));
+    if (tt == 1.0) memcpy(z, x, n * sizeof(float));
+    else if (n >= OR_FAST_MIN_MAP && parts > 1) fast_par(0, x, NULL, z, (float)tt, n, 0, parts);
+    else for (size_t i = 0; i < n; i++) z[i] = x[i] / (float)tt;
+    if (keep) {
+        int64_t mrows = keep_ld == 0 ? 1 : rows;
+        float *add = (float *)malloc((size_t)mrows * (size_t)V * sizeof(float));
+        for (int64_t r = 0; r < mrows; r++)
+            for (int64_t v = 0; v < V; v++) add[r * V + v] = keep[r * keep_ld + v] ? 0.0f : -INFINITY;
+        float *z2 = (float *)malloc(n * sizeof(float));
+        if (mrows == rows && n >= OR_FAST_MIN_ZIP && parts > 1) fast_par(1, z, add, z2, 0.0f, n, 0, parts);
+        else
+            for (int64_t r = 0; r < rows; r++)
+                for (int64_t v = 0; v < V; v++) z2[r * V + v] = z[r * V + v] + add[(keep_ld ? r : 0) * V + v];
+        free(add);
+        free(z);
+        z = z2;
+    }
+    for (int64_t r = 0; r < rows; r++) { /* max_dim (Reference) + the host check */
+        float m = first_max_f32(z + r * V, V, NULL);
+        if (m != m || m == -INFINITY) {
+            free(z);
+            return 1 + r;
+        }
+    }
+    float *zg = (float *)malloc(n * sizeof(float));
+    if (tau == 0.0) {
+        memcpy(zg, z, n * sizeof(float));
+    } else {
+        /* the Gumbel draws: the host loop of rl.rs:490-498, one thread (the stream is sequential),
+         * cast to f32 by from_f64s, then z + g (a zip of equal shapes) */
+        float *gf = (float *)malloc(n * sizeof(float));
+        for (size_t i = 0; i < n; i++) gf[i] = (float)(-log(-log(or_uniform_open01(or_chacha_next_u64(rng)))));
+        if (n >= OR_FAST_MIN_ZIP && parts > 1) fast_par(1, z, gf, zg, 0.0f, n, 0, parts);
+        else for (size_t i = 0; i < n; i++) zg[i] = z[i] + gf[i];
+        free(gf);
+    }
+    for (int64_t r = 0; r < rows; r++) first_max_f32(zg + r * V, V, &ids[r]); /* argmax (Reference) */
+    /* token_log_probs: log_softmax = max_dim, a broadcast sub (Reference), exp (a map), sum_dim
+     * on the last axis (simd_sum per lane on threads), ln of the row sums (a map of `rows`
+     * elements), a broadcast sub; then the gather */
+    float *mx = (float *)malloc((size_t)rows * sizeof(float));
+    float *sh = (float *)malloc(n * sizeof(float));
+    float *e = (float *)malloc(n * sizeof(float));
+    float *lse = (float *)malloc((size_t)rows * sizeof(float));
+    for (int64_t r = 0; r < rows; r++) mx[r] = first_max_f32(z + r * V, V, NULL);
+    for (size_t i = 0; i < n; i++) sh[i] = z[i] - mx[i / (size_t)V];
+    if (n >= OR_FAST_MIN_MAP && parts > 1) fast_par(2, sh, NULL, e, 0.0f, n, 0, parts);
+    else for (size_t i = 0; i < n; i++) e[i] = expf(sh[i]);
+    if (n >= OR_FAST_MIN_SUM && parts > 1) fast_par(3, e, NULL, lse, 0.0f, (size_t)rows, V, parts);
+    else for (int64_t r = 0; r < rows; r++) lse[r] = or_unrolled_sum_f32(e + r * V, V);
+    for (int64_t r = 0; r < rows; r++) lse[r] = logf(lse[r]);
+    for (int64_t r = 0; r < rows; r++) logp[r] = sh[r * V + ids[r]] - lse[r];
+    free(mx); free(sh); free(e); free(lse); free(zg); free(z);
     return 0;
 }
 

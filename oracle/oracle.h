@@ -155,6 +155,13 @@ int64_t or_cpuref_sample_logp(const float *x, int64_t rows, int64_t V, double ta
  * draw, so a refused call leaves the stream untouched. Returns 0, or 1 + the first refused row. */
 int64_t or_cpuref_sample_gumbel(const float *x, int64_t rows, int64_t V, double tau, const float *addmask,
                                 int64_t add_ld, const uint8_t *keep, int64_t keep_ld, or_chacha *rng, int64_t *ids);
+/* The same sequence (sample_categorical, then token_log_probs) on the reference's Cpu(Fast)
+ * backend (src/tensor/backend.rs:57-239) with `threads` workers: threaded maps from 2^20
+ * elements, equal-shape zips from 2^22, last-axis sums from 2^22 by 16 accumulators; the rest
+ * as Cpu(Reference). The tokens equal or_cpuref_sample_logp's for the same stream; a log-prob may
+ * differ in its last bits (the sum order). The timed Cpu(Fast) baseline. */
+int64_t or_cpufast_sample_logp(const float *x, int64_t rows, int64_t V, double tau, const uint8_t *keep,
+                               int64_t keep_ld, or_chacha *rng, int threads, int64_t *ids, float *logp);
 /* The same sequence with the inverse-CDF draw in place of Gumbel-max (one uniform per row),
  * still unfused and in f32 where the reference is f32: the "port" CPU baseline of the fused
  * path. threads > 1 splits rows across pthreads (Cpu(Fast)-style, backend.rs:59-72). */

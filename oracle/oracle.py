@@ -99,6 +99,9 @@ def lib():
         L.or_cpuref_sample_gumbel.argtypes = [_c_float_p, C.c_int64, C.c_int64, C.c_double, _c_float_p, C.c_int64,
                                               _c_u8_p, C.c_int64, C.POINTER(ChaCha), _c_int64_p]
         L.or_cpuref_sample_gumbel.restype = C.c_int64
+        L.or_cpufast_sample_logp.argtypes = [_c_float_p, C.c_int64, C.c_int64, C.c_double, _c_u8_p, C.c_int64,
+                                             C.POINTER(ChaCha), C.c_int, _c_int64_p, _c_float_p]
+        L.or_cpufast_sample_logp.restype = C.c_int64
         L.or_cpu_sample_logp_invcdf.argtypes = [_c_float_p, C.c_int64, C.c_int64, C.c_double, _c_u8_p, C.c_int64,
                                                 _c_double_p, _c_int64_p, _c_float_p, C.c_int]
         L.or_cpu_sample_logp_invcdf.restype = C.c_int64
@@ -402,6 +405,22 @@ def cpuref_sample_logp(x, tau, keep, rng: Rng):
                                      None if kp is None else _ptr(kp, _c_u8_p),
                                      0 if kp is None or kp.shape[0] == 1 else V,
                                      C.byref(rng.s), _ptr(ids, _c_int64_p), _ptr(lp, _c_float_p))
+    if rc:
+        raise ValueError(f"sample_categorical: position {rc - 1} has no allowed token (every logit −∞ or a NaN)")
+    return ids, lp
+
+
+def cpufast_sample_logp(x, tau, keep, rng: Rng, threads):
+    """sample_categorical + token_log_probs on the reference's Cpu(Fast) backend with `threads`
+    workers (or_cpufast_sample_logp)."""
+    x = _f32(np.atleast_2d(x))
+    R, V = x.shape
+    kp = None if keep is None else np.ascontiguousarray(np.atleast_2d(keep), dtype=np.uint8)
+    ids = np.empty(R, dtype=np.int64)
+    lp = np.empty(R, dtype=np.float32)
+    rc = lib().or_cpufast_sample_logp(_ptr(x, _c_float_p), R, V, tau, None if kp is None else _ptr(kp, _c_u8_p),
+                                      0 if kp is None or kp.shape[0] == 1 else V, C.byref(rng.s), threads,
+                                      _ptr(ids, _c_int64_p), _ptr(lp, _c_float_p))
     if rc:
         raise ValueError(f"sample_categorical: position {rc - 1} has no allowed token (every logit −∞ or a NaN)")
     return ids, lp

@@ -382,6 +382,41 @@ def test_cpuref_gumbel_with_additive_masks_is_the_references_sampler_test():
     assert abs(np.mean(tok == 0) - p0) <= 4.5 * math.sqrt(p0 * (1 - p0) / n2)
 
 
+def test_cpufast_restatement_against_cpuref_and_the_f64_oracle():
+    # Cpu(Fast) (src/tensor/backend.rs:57-239) differs from Cpu(Reference) only in how maps, zips
+    # and sums are split: above its thresholds (here 64 x 65536 = 2^22 elements) the tokens, whose
+    # argmax runs the Reference kernel on the same noise, equal CpuRef's for the same stream; the
+    # log-probabilities differ only in the sum order (16 accumulators against 8 partials) and hold
+    # the f64 oracle's value within f32 tolerance; the stream advances one u64 per logit; threads
+    # do not change the result. The sum order itself has no reference record (parity unpinned
+    # below the tolerance).
+    rng = np.random.default_rng(4)
+    R, V = 64, 65536
+    x = rng.normal(0, 2, (R, V)).astype(np.float32)
+    keep = (rng.random((R, V)) < 0.4).astype(np.uint8)
+    keep[:, 3] = 1
+    a_ids, a_lp = O.cpuref_sample_logp(x, 0.7, keep, O.Rng(5, "fast"))
+    outs = []
+    for threads in (1, 3, 8):
+        r = O.Rng(5, "fast")
+        ids, lp = O.cpufast_sample_logp(x, 0.7, keep, r, threads)
+        copy = O.Rng(5, "fast")
+        for _ in range(R * V):
+            copy.next_u64()
+        assert r.next_u64() == copy.next_u64(), "one u64 per logit"
+        assert np.array_equal(ids, a_ids)
+        outs.append(lp.tobytes())
+        z = O.tempered(x, 0.7, keep=keep)
+        want = O.token_logp(z, ids)
+        assert np.all(np.abs(lp - want) <= 1e-6 + 1e-5 * np.abs(want))
+    assert outs[1] == outs[2], "threads change nothing above the thresholds"
+    # below the thresholds every op is Reference's: bit-identical to CpuRef
+    small = x[:4, :1024]
+    b_ids, b_lp = O.cpufast_sample_logp(small, 0.7, keep[:4, :1024], O.Rng(6, "fast"), 8)
+    c_ids, c_lp = O.cpuref_sample_logp(small, 0.7, keep[:4, :1024], O.Rng(6, "fast"))
+    assert np.array_equal(b_ids, c_ids) and b_lp.tobytes() == c_lp.tobytes()
+
+
 # ------------------------------------------------------------------------ golden C1 fixture
 
 def test_c1_golden_fixture():

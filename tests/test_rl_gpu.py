@@ -99,7 +99,8 @@ def test_c4_north_star_parity_and_rerun_bits():
     keep = w["mask"].to_numpy().reshape(rows, V)
     assert keep[np.arange(rows), a].all(), "an excluded token was drawn"
     z = O.tempered(x, w["temperature"], keep=keep)
-    check_sample("c4", z, u, a, b, bf16=True)
+    # the f32 tolerance (the bf16 inputs are exact in f32; the kernel computes in f32 and f64)
+    check_sample("c4", z, u, a, b, bf16=False)
 
 
 def test_c2_decode_parity():
