@@ -609,11 +609,15 @@ def bench_matmul(nr, args):
 
 
 def bench_readout(nr, W, args):
-    """What fusing the sampler into the decoder readout could save at C4's decode shape: the readout
-    GEMM logits[256, 128256] = h[256, 4096] · W[4096, 128256] in bf16 (torch.matmul, hipBLASLt,
-    as the baseline a fused kernel would have to match), then nt_hip_rl_sample on the logits it
-    just wrote, both on the library's stream. The sampler's share of the step is the most a
-    readout-fused epilogue could remove; the GEMM itself reads the 1.05 GB weight matrix."""
+    """One decode step at C4's shape with the readout: logits[256, 128256] = h[256, 4096] . W in
+    bf16, then the masked inverse-CDF sample + log-prob (u8 C4 mask, tau 0.7).
+
+    Fused (the value): nt_hip_rl_readout_sample, the product and the sampler's row records in one
+    MFMA kernel and a per-row resolve, the logits never written; the weight packed once from the
+    reference's [d, V] Linear layout into the matrix cores' fragment order (timed separately, as a
+    loader would run it once).
+    Unfused (beside it): torch.matmul (hipBLASLt) into bf16 logits, then nt_hip_rl_sample on
+    them, with the weight in the reference's [d, V] layout and in the vocabulary-major one."""
     import torch
 
     rows, d, V = 256, 4096, 128256
@@ -624,51 +628,107 @@ def bench_readout(nr, W, args):
     w = W.c4(args.seed)
     with torch.cuda.stream(ts):
         h = torch.randn(rows, d, device="cuda:0", dtype=torch.bfloat16, generator=g)
-        wt = (torch.randn(d, V, device="cuda:0", dtype=torch.bfloat16, generator=g) * (2.0 / 64.0)).to(torch.bfloat16)
+        w_vd = (torch.randn(V, d, device="cuda:0", dtype=torch.bfloat16, generator=g) * (2.0 / 64.0)).to(torch.bfloat16)
         logits = torch.empty(rows, V, device="cuda:0", dtype=torch.bfloat16)
     torch.cuda.synchronize()
+    # the reference's layout [d, V], made once by the library's own transposing copy (what a
+    # loader would run once, the other way)
+    L = nr.lib()
+    w_dv = torch.empty(d, V, device="cuda:0", dtype=torch.bfloat16)
+    lay = nr.NtLayout()
+    lay.rank, lay.offset = 2, 0
+    lay.shape[0], lay.shape[1] = d, V
+    lay.strides[0], lay.strides[1] = 1, d  # the [V, d] buffer read as its [d, V] transpose
+    t0 = time.perf_counter()
+    nr._check(L.nt_hip_copy(C.c_void_p(w_vd.data_ptr()), C.byref(lay), 2, C.c_void_p(w_dv.data_ptr())), "transpose")
+    nr.sync()
+    transpose_s = time.perf_counter() - t0
+    nbytes = int(L.nt_hip_rl_readout_packed_bytes(V, d))
+    w_packed = torch.empty(nbytes, device="cuda:0", dtype=torch.uint8)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    nr._check(L.nt_hip_rl_readout_pack_weight(C.c_void_p(w_dv.data_ptr()), nr.NT_READOUT_W_DV, V, d, V,
+                                              C.c_void_p(w_packed.data_ptr())), "pack")
+    nr.sync()
+    pack_s = time.perf_counter() - t0
     U = nr.Tensor.from_numpy(nr.Rng(args.seed, "readout/uniforms").uniforms(rows), "f64")
     ids, logp, st = nr.IntTensor((rows,)), nr.Tensor((rows,), "f32"), nr.Tensor((rows,), "u8")
     a = nr.NtRlSampleArgs(logits.data_ptr(), nr.NT_BF16, nr.NT_MASK_U8, rows, V, V, w["mask"].ptr, V, 0.7, U.ptr,
                           ids.ptr, logp.ptr, None, st.ptr)
-    L = nr.lib()
+    ids2, logp2, st2 = nr.IntTensor((rows,)), nr.Tensor((rows,), "f32"), nr.Tensor((rows,), "u8")
+    fa = nr.NtRlReadoutSampleArgs(h.data_ptr(), w_packed.data_ptr(), rows, V, d, d, nr.NT_MASK_U8, 0, w["mask"].ptr, V,
+                                  0.7, U.ptr, ids2.ptr, logp2.ptr, st2.ptr, None, None, None)
 
-    def gemm(i):
+    def fused(i):
+        nr._check(L.nt_hip_rl_readout_sample(C.byref(fa)), "readout sample")
+
+    def gemm_dv(i):
         with torch.cuda.stream(ts):
-            torch.matmul(h, wt, out=logits)
+            torch.matmul(h, w_dv, out=logits)
+
+    def gemm_vd(i):
+        with torch.cuda.stream(ts):
+            torch.matmul(h, w_vd.t(), out=logits)
 
     def sample(i):
         nr._check(L.nt_hip_rl_sample(C.byref(a)), "sample")
 
-    def step(i):
-        gemm(i)
+    def step_dv(i):
+        gemm_dv(i)
         sample(i)
 
-    steps, warmup = min(args.steps, 50), min(args.warmup, 5)
-    # three interleaved rounds of each; medians (the GEMM's own time varies by a few us)
-    res = {"gemm": [], "sample": [], "step": []}
-    for _ in range(3):
-        res["gemm"].append(timed(nr, steps, warmup, gemm)[0])
-        gemm(0)
-        res["sample"].append(timed(nr, steps, warmup, sample)[0])
-        res["step"].append(timed(nr, steps, warmup, step)[0])
-    ms_gemm, ms_sample, ms_step = (float(np.median(res[k])) for k in ("gemm", "sample", "step"))
-    stn = st.to_numpy()
-    if np.any(stn != 0):
+    def step_vd(i):
+        gemm_vd(i)
+        sample(i)
+
+    steps, warmup = args.steps, args.warmup
+    fused(0)
+    ms, wall = timed(nr, steps, warmup, fused)
+    if np.any(st2.to_numpy() != 0):
         raise RuntimeError("readout: refused rows")
-    gemm_bytes = 2 * (rows * d + d * V + rows * V)
-    return {"metric": "decode step at C4's shape: bf16 readout GEMM + fused sample, and the sampler's share",
-            "value": rows / (ms_step * 1e-3), "unit": "rows/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
-            "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-            "dtype": "bf16", "data": "synthetic",
-            "config": {"workload": "readout: h[256,4096] @ W[4096,128256] bf16 (torch.matmul) then nt_hip_rl_sample "
-                                   "(u8 c4 mask, tau 0.7) on the logits just written"},
-            "readout": {"gemm_us": round(ms_gemm * 1e3, 2), "step_us": round(ms_step * 1e3, 2),
-                        "sampler_alone_us": round(ms_sample * 1e3, 2),
-                        "step_minus_gemm_us": round((ms_step - ms_gemm) * 1e3, 2),
-                        "sampler_share_of_gemm_plus_sampler": round(ms_sample / (ms_gemm + ms_sample), 4),
-                        "gemm_gbs": round(gemm_bytes / (ms_gemm * 1e-3) / 1e9, 1),
-                        "gemm_tflops": round(2 * rows * d * V / (ms_gemm * 1e-3) / 1e12, 1)}}
+    # the unfused steps beside it: three interleaved rounds, medians
+    res = {k: [] for k in ("fused", "gemm_dv", "gemm_vd", "sample", "step_dv", "step_vd")}
+    for _ in range(3):
+        res["fused"].append(timed(nr, steps, warmup, fused)[0])
+        res["gemm_dv"].append(timed(nr, steps, warmup, gemm_dv)[0])
+        res["gemm_vd"].append(timed(nr, steps, warmup, gemm_vd)[0])
+        gemm_dv(0)
+        res["sample"].append(timed(nr, steps, warmup, sample)[0])
+        res["step_dv"].append(timed(nr, steps, warmup, step_dv)[0])
+        res["step_vd"].append(timed(nr, steps, warmup, step_vd)[0])
+    med = {k: float(np.median(v)) * 1e3 for k, v in res.items()}
+    if np.any(st.to_numpy() != 0):
+        raise RuntimeError("readout: refused rows (unfused)")
+    w_bytes = V * d * 2
+    step_bytes = w_bytes + rows * d * 2 + rows * V + rows * (8 + 4 + 4 + 1)
+    flops = 2.0 * rows * d * V
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    tfs = flops / (ms * 1e-3) / 1e12
+    roof = {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
+            "traffic": None, "algorithmic_bytes_per_launch": step_bytes,
+            "what": "the whole fused step (both launches) against the weight stream: the weight (1.05 GB) once, "
+                    "h, the mask, the uniforms and the outputs",
+            "mfma": {"achieved": tfs, "peak": 2500.0, "unit": "TFLOP/s", "frac": tfs / 2500.0,
+                     "flops_per_step": flops}}
+    return {"metric": "decode step at C4's shape: bf16 readout (h[256,4096] . W, V 128256) + masked sample + logprob",
+            "value": rows / (ms * 1e-3), "unit": "rows/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+            "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic",
+            "config": {"workload": "readout: nt_hip_rl_readout_sample, logits never written; weight [d, V] bf16 "
+                                   "~ N(0, (2/64)^2) packed once, h ~ N(0,1), u8 C4 grammar mask, tau 0.7",
+                       "rows": rows, "dim": d, "vocab": V},
+            "roofline": roof, "wall_s_timed_region": wall,
+            "unfused": {"fused_step_us_median_of_3": round(med["fused"], 2),
+                        "hipblaslt_gemm_w_dv_us": round(med["gemm_dv"], 2),
+                        "hipblaslt_gemm_w_vd_us": round(med["gemm_vd"], 2),
+                        "sampler_on_bf16_logits_us": round(med["sample"], 2),
+                        "gemm_plus_sampler_w_dv_us": round(med["step_dv"], 2),
+                        "gemm_plus_sampler_w_vd_us": round(med["step_vd"], 2),
+                        "speedup_vs_best_unfused": round(min(med["step_dv"], med["step_vd"]) / med["fused"], 3),
+                        "note": "the unfused GEMM writes bf16 logits (hipBLASLt's output for bf16 operands); the "
+                                "fused product keeps them in f32"},
+            "weight_transpose_once_s": round(transpose_s, 4), "weight_pack_once_s": round(pack_s, 4),
+            "key": nr.key()}
 
 
 def main():

@@ -166,6 +166,48 @@ int nt_hip_rl_sample(const NtRlSampleArgs *a);
  * and calls that overlap on one GPU race. */
 int nt_hip_rl_sample_noalloc(const NtRlSampleArgs *a);
 
+/* The readout-fused sampler: one decode step's readout product and its inverse-CDF sample +
+ * log-probability, with the logits never written. For each row r,
+ *   logits[r, v] = sum_k hidden[r, k] W[k, v]          (the decoder's readout x . W,
+ *                                                        src/nn/decoder.rs:272,286; linear.rs:1-3)
+ * in f32 from bf16 operands on the matrix cores (the reference's half-precision product,
+ * src/tensor/gpu/half_gemm.rs:1-10), then exactly nt_hip_rl_sample's draw on those logits
+ * (tempered by the temperature, the u8 keep-mask applied; one uniform per row; temperature 0 is
+ * the first argmax). The weight is packed once, when loaded, into the order the matrix cores
+ * read it (nt_hip_rl_readout_pack_weight, from the reference's [d, V] layout or a [V, d] one).
+ * rows <= 256; vocab <= 262144; dim a multiple of 16; ldh a multiple of 8, hidden 16-byte
+ * aligned; a u8 mask with one row per logits row (mask_ld >= vocab). Three launches on the
+ * library stream: h into the same order (2 MB at 256 x 4096), the product with the sampler's
+ * per-row records in its epilogue, then one workgroup per row that merges them and recomputes
+ * only the 32 logits of the block holding the draw. The debug pointers (NULL in use) write the
+ * f32 logits, the recomputed block and its index, for the parity tests. */
+#define NT_READOUT_W_DV 0 /* the reference's Linear weight [d, V]: W[k, v] at w + k ld + v */
+#define NT_READOUT_W_VD 1 /* vocabulary-major [V, d]: W[k, v] at w + v ld + k */
+/* Bytes of the packed weight: ceil(vocab / 32) 32 dim 2 (-1 for an invalid shape). */
+int64_t nt_hip_rl_readout_packed_bytes(int64_t vocab, int64_t dim);
+/* Pack a bf16 readout weight (layout NT_READOUT_W_*, row stride ld) into `packed` (device,
+ * nt_hip_rl_readout_packed_bytes bytes, 16-byte aligned): one kernel on the library stream. */
+int nt_hip_rl_readout_pack_weight(const void *weight, int32_t layout, int64_t vocab, int64_t dim, int64_t ld,
+                                  void *packed);
+typedef struct NtRlReadoutSampleArgs {
+    const void *hidden;        /* [rows, ldh] bf16: the readout's input */
+    const void *weight_packed; /* the readout weight, packed by nt_hip_rl_readout_pack_weight */
+    int64_t rows, vocab, dim, ldh;
+    int32_t mask_kind;         /* NT_MASK_NONE | NT_MASK_U8 */
+    int32_t pad0;
+    const void *mask;          /* u8 [rows, mask_ld] or NULL */
+    int64_t mask_ld;
+    double temperature;        /* >= 0 and finite; 0 = greedy */
+    const double *uniforms;    /* [rows] device, each in (0,1); unused when greedy */
+    int32_t *ids;              /* [rows] out: the sampled token (-1 on a refused row) */
+    float *logp;               /* [rows] out or NULL */
+    uint8_t *status;           /* [rows] out: NT_ROW_* */
+    float *logits;             /* debug: [rows, vocab] f32 out or NULL */
+    float *debug_block;        /* debug: [rows, 32] the crossing block's recomputed logits, or NULL */
+    int32_t *debug_block_index; /* debug: [rows] that block's index (columns 32 b .. 32 b + 31), or NULL */
+} NtRlReadoutSampleArgs;
+int nt_hip_rl_readout_sample(const NtRlReadoutSampleArgs *a);
+
 /* Fused row scoring: for each row, any of
  *   logp[r]     = token_log_probs(z, tokens)[r]                 (rl.rs:134-141)
  *   ref_logp[r] = token_log_probs(zr, tokens)[r]                (rl.rs:134-141, reference)

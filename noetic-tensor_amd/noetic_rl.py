@@ -52,6 +52,14 @@ class NtRlGumbelArgs(C.Structure):
                 ("ids", C.c_void_p), ("status", C.c_void_p)]
 
 
+class NtRlReadoutSampleArgs(C.Structure):
+    _fields_ = [("hidden", C.c_void_p), ("weight_packed", C.c_void_p), ("rows", C.c_int64), ("vocab", C.c_int64),
+                ("dim", C.c_int64), ("ldh", C.c_int64), ("mask_kind", C.c_int32),
+                ("pad0", C.c_int32), ("mask", C.c_void_p), ("mask_ld", C.c_int64), ("temperature", C.c_double),
+                ("uniforms", C.c_void_p), ("ids", C.c_void_p), ("logp", C.c_void_p), ("status", C.c_void_p),
+                ("logits", C.c_void_p), ("debug_block", C.c_void_p), ("debug_block_index", C.c_void_p)]
+
+
 class NtRlScoreArgs(C.Structure):
     _fields_ = [("logits", C.c_void_p), ("ref_logits", C.c_void_p), ("dtype", C.c_int32),
                 ("mask_kind", C.c_int32), ("rows", C.c_int64), ("vocab", C.c_int64), ("ld", C.c_int64),
@@ -117,6 +125,9 @@ _SIGS = {
     "nt_hip_launches": (C.c_uint64, []),
     "nt_hip_rl_sample": (C.c_int, [C.POINTER(NtRlSampleArgs)]),
     "nt_hip_rl_sample_gumbel": (C.c_int, [C.POINTER(NtRlGumbelArgs)]),
+    "nt_hip_rl_readout_sample": (C.c_int, [C.POINTER(NtRlReadoutSampleArgs)]),
+    "nt_hip_rl_readout_packed_bytes": (C.c_int64, [C.c_int64, C.c_int64]),
+    "nt_hip_rl_readout_pack_weight": (C.c_int, [C.c_void_p, C.c_int32, C.c_int64, C.c_int64, C.c_int64, C.c_void_p]),
     "nt_hip_rl_sample_noalloc": (C.c_int, [C.POINTER(NtRlSampleArgs)]),
     "nt_hip_rl_score": (C.c_int, [C.POINTER(NtRlScoreArgs)]),
     "nt_hip_rl_score_backward": (C.c_int, [C.POINTER(NtRlScoreGradArgs)]),
@@ -499,6 +510,75 @@ def sample_categorical_inv_cdf(logits: Tensor, temperature: float, mask: Optiona
     by the inverse CDF of one uniform per row (one u64 of `rng` per row, none at temperature 0)
     in one fused pass over the logits. `sample_logp` also returns the tokens' log-probabilities."""
     return sample_logp(logits, temperature, mask, rng)[0]
+
+
+NT_READOUT_W_DV, NT_READOUT_W_VD = 0, 1
+
+
+class PackedReadout:
+    """A readout weight packed once for nt_hip_rl_readout_sample (the order the matrix cores read
+    it): from the reference's Linear weight [d, V] (`layout` "dv") or a vocabulary-major [V, d]."""
+
+    def __init__(self, weight: Tensor, layout: str = "dv"):
+        if weight.dtype != "bf16" or len(weight.shape) != 2:
+            raise ValueError("readout weight: a bf16 matrix")
+        if layout == "dv":
+            self.dim, self.vocab = weight.shape
+            code, ld = NT_READOUT_W_DV, self.vocab
+        elif layout == "vd":
+            self.vocab, self.dim = weight.shape
+            code, ld = NT_READOUT_W_VD, self.dim
+        else:
+            raise ValueError(f"readout weight layout {layout!r} (dv or vd)")
+        nbytes = int(lib().nt_hip_rl_readout_packed_bytes(self.vocab, self.dim))
+        if nbytes < 0:
+            raise ValueError(f"readout weight [{self.vocab}, {self.dim}]: dim a multiple of 16")
+        self.buf = Buffer(nbytes)
+        _check(lib().nt_hip_rl_readout_pack_weight(weight.ptr, code, self.vocab, self.dim, ld, self.buf.ptr),
+               "readout pack")
+
+    def buf_bytes(self) -> bytes:
+        """The packed bytes (a synchronising download; for tests)."""
+        out = (C.c_uint8 * self.buf.nbytes)()
+        _check(lib().nt_hip_download(out, C.c_void_p(self.buf.ptr), self.buf.nbytes), "download packed")
+        return bytes(out)
+
+
+def readout_sample_logp(hidden: Tensor, weight: PackedReadout, temperature: float, mask: Optional[Tensor],
+                        rng: Optional[Rng], uniforms: Optional[Tensor] = None, debug: bool = False,
+                        check: bool = True):
+    """One decode step fused: logits = hidden [rows, d] . W (the readout, decoder.rs:272,286),
+    then sample_logp's inverse-CDF draw and log-probability on them (rl.rs:134-141, 475-529), the
+    logits never written. `weight` is the readout weight packed once (PackedReadout). Returns
+    (ids, logp), plus with `debug` the f32 logits [rows, V], the recomputed crossing block
+    [rows, 32] and its index [rows]."""
+    if not (temperature >= 0.0 and math.isfinite(temperature)):
+        raise ValueError(f"sample_categorical: temperature {temperature} (must be ≥ 0)")
+    if hidden.dtype != "bf16" or len(hidden.shape) != 2:
+        raise ValueError("readout: hidden [rows, d] in bf16")
+    rows, d = hidden.shape
+    V = weight.vocab
+    if weight.dim != d:
+        raise ValueError(f"readout: hidden's d {d} against the weight's {weight.dim}")
+    if temperature != 0.0 and uniforms is None:
+        if rng is None:
+            raise ValueError("sample_categorical: a stream is needed at temperature > 0")
+        uniforms = Tensor.from_numpy(rng.uniforms(rows), "f64")
+    ids, lp, status = IntTensor((rows,)), Tensor((rows,), "f32"), Tensor((rows,), "u8")
+    dbg = (Tensor((rows, V), "f32"), Tensor((rows, 32), "f32"), IntTensor((rows,))) if debug else (None, None, None)
+    if mask is not None and (mask.dtype != "u8" or mask.numel != rows * V):
+        raise ValueError("readout: a u8 keep-mask [rows, V]")
+    a = NtRlReadoutSampleArgs(hidden.ptr, weight.buf.ptr, rows, V, d, d, NT_MASK_U8 if mask is not None else NT_MASK_NONE,
+                              0, None if mask is None else mask.ptr, V if mask is not None else 0, float(temperature),
+                              None if uniforms is None else uniforms.ptr, ids.ptr, lp.ptr, status.ptr,
+                              *(None if t is None else t.ptr for t in dbg))
+    _check(lib().nt_hip_rl_readout_sample(C.byref(a)), "readout sample")
+    if check:
+        st = status.to_numpy().ravel()
+        bad = np.nonzero(st != NT_ROW_OK)[0]
+        if bad.size:
+            raise ValueError(f"sample_categorical: position {bad[0]} has no allowed token (every logit −∞ or a NaN)")
+    return (ids, lp, *dbg) if debug else (ids, lp)
 
 
 def _score(policy, ref, tokens, want_logp, want_ref_logp, want_kl, want_ent, want_stats=False):
