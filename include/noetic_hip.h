@@ -175,7 +175,7 @@ int nt_hip_rl_sample_noalloc(const NtRlSampleArgs *a);
  * (tempered by the temperature, the u8 keep-mask applied; one uniform per row; temperature 0 is
  * the first argmax). The weight is packed once, when loaded, into the order the matrix cores
  * read it (nt_hip_rl_readout_pack_weight, from the reference's [d, V] layout or a [V, d] one).
- * rows <= 256; vocab <= 262144; dim a multiple of 16; ldh a multiple of 8, hidden 16-byte
+ * rows <= 256; vocab <= 262144; dim a multiple of 16, at most 16384; ldh a multiple of 8, hidden 16-byte
  * aligned; a u8 mask with one row per logits row (mask_ld >= vocab). Three launches on the
  * library stream: h into the same order (2 MB at 256 x 4096), the product with the sampler's
  * per-row records in its epilogue, then one workgroup per row that merges them and recomputes
@@ -183,7 +183,8 @@ int nt_hip_rl_sample_noalloc(const NtRlSampleArgs *a);
  * f32 logits, the recomputed block and its index, for the parity tests. */
 #define NT_READOUT_W_DV 0 /* the reference's Linear weight [d, V]: W[k, v] at w + k ld + v */
 #define NT_READOUT_W_VD 1 /* vocabulary-major [V, d]: W[k, v] at w + v ld + k */
-/* Bytes of the packed weight: ceil(vocab / 32) 32 dim 2 (-1 for an invalid shape). */
+/* Bytes of the packed weight: ceil(vocab / 256) 256 dim 2, the vocabulary padded with zero
+ * columns to whole tiles of 256 (-1 for an invalid shape). */
 int64_t nt_hip_rl_readout_packed_bytes(int64_t vocab, int64_t dim);
 /* Pack a bf16 readout weight (layout NT_READOUT_W_*, row stride ld) into `packed` (device,
  * nt_hip_rl_readout_packed_bytes bytes, 16-byte aligned): one kernel on the library stream. */

@@ -42,14 +42,14 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 
-constexpr int kRoThreads = 512;       // 8 waves: two per SIMD, so one wave's LDS reads overlap the other's MFMAs
+constexpr int kRoThreads = 256;       // 4 waves, one per SIMD: each holds 16 MFMA tiles in its AGPRs
 constexpr int kRoCols = 256;          // vocabulary columns per workgroup (tile)
 constexpr int kRoRows = 256;          // rows per launch at most
 constexpr int64_t kRoMaxVocab = 262144;  // the resolve's per-thread block and tile arrays
 constexpr int kRoBlock = 32;          // columns per record block
-constexpr int kRoDepth = 8;           // k-steps of 16 in flight
-constexpr int kRoStages = kRoDepth + 1;
-constexpr int kRoStageBytes = 16384;  // 8 A fragments + 8 B fragments of 1 KiB
+constexpr int kRoDepth = 12;          // k-steps in flight: the weight's register ring
+constexpr int kRoStages = 14;         // h's LDS stages (one k-step each)
+constexpr int kRoStageBytes = 8192;   // one k-step of h: eight row-group fragments of 1 KiB
 constexpr int kBufferWord3 = 0x00020000;
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr double kLn2 = 0.69314718055994530942;
@@ -60,43 +60,16 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-// Wait until at most n (an even number up to 16) vector memory operations of this wave are
-// outstanding.
-__device__ __forceinline__ void wait_vmcnt_upto16(int n) {
-    switch (n) {
-        case 0: wait_vmcnt<0>(); break;
-        case 2: wait_vmcnt<2>(); break;
-        case 4: wait_vmcnt<4>(); break;
-        case 6: wait_vmcnt<6>(); break;
-        case 8: wait_vmcnt<8>(); break;
-        case 10: wait_vmcnt<10>(); break;
-        case 12: wait_vmcnt<12>(); break;
-        case 14: wait_vmcnt<14>(); break;
-        default: wait_vmcnt<16>(); break;
-    }
-}
-
-// Wait until at most 2 n vector memory operations of this wave are outstanding (n in 0..7): the
-// DMAs of the n k-steps issued after the one awaited.
-__device__ __forceinline__ void wait_vmcnt_steps(int n) {
-    switch (n) {
-        case 0: wait_vmcnt<0>(); break;
-        case 1: wait_vmcnt<2>(); break;
-        case 2: wait_vmcnt<4>(); break;
-        case 3: wait_vmcnt<6>(); break;
-        case 4: wait_vmcnt<8>(); break;
-        case 5: wait_vmcnt<10>(); break;
-        case 6: wait_vmcnt<12>(); break;
-        default: wait_vmcnt<14>(); break;
-    }
-}
 
 // Fragment order: the MFMA operands of 32 rows (or vocabulary columns) g 32 .. g 32 + 31 for
-// k-step s (k 16 s .. 16 s + 15) are 1 KiB at ((g S + s) 64 + l) 16 bytes, lane l holding row
-// g 32 + l % 32 at k 16 s + 8 (l / 32) .. + 7: a DMA of one fragment reads 1 KiB contiguous.
+// k-step s (k 16 s .. 16 s + 15) are one 1 KiB fragment, lane l's 16 bytes at 16 l holding row
+// g 32 + l % 32 at k 16 s + 8 (l / 32) .. + 7, so a DMA of one fragment reads 1 KiB contiguous.
+// h: row group g's fragment of step s at (g S + s) KiB. The weight, tile-major: column group g
+// (tile t = g / 8, gi = g % 8) at ((t S + s) 8 + gi) KiB, a tile's eight fragments of one step
+// 8 KiB contiguous, the vocabulary padded with zero columns to whole tiles of 256.
 struct ReadoutP {
     const uint8_t *hp;   // h in fragment order, ceil(rows / 32) row groups
-    const uint8_t *wp;   // the weight in fragment order, ceil(V / 32) column groups
+    const uint8_t *wp;   // the weight in fragment order, tile-major, ntile tiles
     int rows, V, K;
     int ntile, nblk;     // tiles of 256 columns, blocks of 32 columns
     const uint8_t *mask; // u8 keep-mask [rows, mask_ld] or null
@@ -110,105 +83,220 @@ struct ReadoutP {
     float *logits;       // [rows][V] debug copy or null
 };
 
-// Six 16-byte LDS reads (four A fragments 1 KiB apart, two B fragments) and the wait for them,
-// in one statement: the data came from LDS DMA, which the compiler's own wait insertion would
-// treat as outstanding vector memory (a wait for every load in flight).
-__device__ __forceinline__ void lds_read_frags(uint32_t a, uint32_t b, v4u (&fa)[4], v4u (&fb)[2]) {
+// Eight reads of 16 bytes: the A fragments of the eight row groups (1 KiB apart), and the wait
+// for them, in one statement: the data came from LDS DMA, which the compiler's own wait insertion
+// would treat as outstanding vector memory (a wait for every load in flight).
+__device__ __forceinline__ void lds_read_a8(uint32_t a, v4u (&fa)[8]) {
     asm volatile(
-        "ds_read_b128 %0, %6\n\t"
-        "ds_read_b128 %1, %6 offset:1024\n\t"
-        "ds_read_b128 %2, %6 offset:2048\n\t"
-        "ds_read_b128 %3, %6 offset:3072\n\t"
-        "ds_read_b128 %4, %7\n\t"
-        "ds_read_b128 %5, %7 offset:1024\n\t"
+        "ds_read_b128 %0, %8\n\t"
+        "ds_read_b128 %1, %8 offset:1024\n\t"
+        "ds_read_b128 %2, %8 offset:2048\n\t"
+        "ds_read_b128 %3, %8 offset:3072\n\t"
+        "ds_read_b128 %4, %8 offset:4096\n\t"
+        "ds_read_b128 %5, %8 offset:5120\n\t"
+        "ds_read_b128 %6, %8 offset:6144\n\t"
+        "ds_read_b128 %7, %8 offset:7168\n\t"
         "s_waitcnt lgkmcnt(0)"
-        : "=&v"(fa[0]), "=&v"(fa[1]), "=&v"(fa[2]), "=&v"(fa[3]), "=&v"(fb[0]), "=&v"(fb[1])
-        : "v"(a), "v"(b)
+        : "=&v"(fa[0]), "=&v"(fa[1]), "=&v"(fa[2]), "=&v"(fa[3]), "=&v"(fa[4]), "=&v"(fa[5]), "=&v"(fa[6]), "=&v"(fa[7])
+        : "v"(a)
         : "memory");
+}
+
+// The eight A fragments of the next k-step (1 KiB apart in LDS) into `na`, issued only: the
+// registers are in flight until lds_wait_a8 below, and nothing may read them before it.
+__device__ __forceinline__ void lds_issue_a8(uint32_t a, v4u (&na)[8]) {
+    asm volatile(
+        "ds_read_b128 %0, %8\n\t"
+        "ds_read_b128 %1, %8 offset:1024\n\t"
+        "ds_read_b128 %2, %8 offset:2048\n\t"
+        "ds_read_b128 %3, %8 offset:3072\n\t"
+        "ds_read_b128 %4, %8 offset:4096\n\t"
+        "ds_read_b128 %5, %8 offset:5120\n\t"
+        "ds_read_b128 %6, %8 offset:6144\n\t"
+        "ds_read_b128 %7, %8 offset:7168"
+        : "=&v"(na[0]), "=&v"(na[1]), "=&v"(na[2]), "=&v"(na[3]), "=&v"(na[4]), "=&v"(na[5]), "=&v"(na[6]), "=&v"(na[7])
+        : "v"(a)
+        : "memory");
+}
+
+// The wait for lds_issue_a8's reads; it takes the registers as in-out operands, so that every use
+// of them comes after it.
+__device__ __forceinline__ void lds_wait_a8(v4u (&na)[8]) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(na[0]), "+v"(na[1]), "+v"(na[2]), "+v"(na[3]), "+v"(na[4]), "+v"(na[5]), "+v"(na[6]),
+                   "+v"(na[7])
+                 :
+                 : "memory");
 }
 
 template <bool MASK, bool DBG>
 __global__ __launch_bounds__(kRoThreads) void k_readout_tiles(ReadoutP p) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[kRoStages * kRoStageBytes];
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int rh = wave >> 2, cq = wave & 3;  // this wave's 128 rows and 64 columns
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // this wave's columns 64 wave .. + 63
     const int tile = blockIdx.x;
     const int n0 = tile * kRoCols;
-    const int ncols = min(kRoCols, p.V - n0);
     const int S = p.K / 16;
-    // Buffer resources over the packed operands: reads past the row groups (or past the
-    // vocabulary's column groups) return zeros.
-    const int hgroups = (p.rows + 31) / 32, wgroups = (ncols + 31) / 32;
+    // Buffer resources over the packed operands. Loads past a range return zeros and touch no
+    // memory: the loop below issues the copies of steps past the last (never used) instead of
+    // branching around them. h's row groups past the rows are such zeros too.
+    const int hgroups = (p.rows + 31) / 32;
     const __amdgpu_buffer_rsrc_t hres = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t *>(p.hp), short(0), hgroups * S * 1024, kBufferWord3);
-    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t *>(p.wp + int64_t(n0 / 32) * S * 1024), short(0), wgroups * S * 1024, kBufferWord3);
-    const uint32_t lbase = uint32_t((uintptr_t)(lds_ptr_t)(lds));
-    // This wave's DMA share of a k-step: A fragment `wave` (row group) and B fragment `wave`
-    // (column group of the tile), 1 KiB contiguous each in fragment order; lane l's 16 bytes land
-    // at 16 l of the fragment's LDS slot, the MFMA operand of that lane.
+    const uint32_t lbase = uint32_t((uintptr_t)(lds_ptr_t)(lds)) + lane * 16;
     const int fr = lane & 31;
-    const int frag = wave * S * 1024 + lane * 16;
-    auto issue = [&](int s) {
-        uint8_t *st = lds + (s % kRoStages) * kRoStageBytes;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(hres, (lds_ptr_t)(st + wave * 1024), 16, frag + s * 1024, 0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, (lds_ptr_t)(st + 8192 + wave * 1024), 16, frag + s * 1024, 0, 0, 0);
+    // Step t's operands. h (A, shared by the waves) through LDS: this wave copies row groups
+    // 2 wave, 2 wave + 1 of it by DMA into stage t % kRoStages (lane l's 16 bytes at 16 l of the
+    // fragment's slot). The weight (B, this wave's own two column groups) straight into registers.
+    const int hoff = 2 * wave * S * 1024 + lane * 16, woff = 2 * wave * 1024 + lane * 16;
+    // the weight's resource as four scalar words for the loads below (base, stride 0, size, flags)
+    const uint64_t wbase = reinterpret_cast<uint64_t>(p.wp + int64_t(tile) * S * 8192);
+    const v4u wrs = {uint32_t(wbase), uint32_t(wbase >> 32), uint32_t(S * 8192), uint32_t(kBufferWord3)};
+    auto issue_a = [&](int t) {
+        uint8_t *st = lds + (t % kRoStages) * kRoStageBytes + 2 * wave * 1024;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(hres, (lds_ptr_t)(st), 16, hoff + t * 1024, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(hres, (lds_ptr_t)(st + 1024), 16, hoff + S * 1024 + t * 1024, 0, 0,
+                                                 0);
     };
-    f32x16_t acc[4][2];
+    // The weight loads are written out, not left to the compiler: it cannot follow a register
+    // ring across loop iterations and would wait for every load in flight before each step. The
+    // waits below (for h's DMAs that this wave issued after these loads) cover them; nothing reads
+    // the registers before that.
+    auto load_b = [&](int t, v4u &b0, v4u &b1) {
+        asm volatile(
+            "buffer_load_dwordx4 %0, %2, %3, 0 offen\n\t"
+            "buffer_load_dwordx4 %1, %2, %3, 0 offen offset:1024"
+            : "=&v"(b0), "=&v"(b1)
+            : "v"(woff + t * 8192), "s"(wrs)
+            : "memory");
+    };
+    auto stage = [&](int t) { return lbase + (t % kRoStages) * kRoStageBytes; };
+    f32x16_t acc[8][2];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 8; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[i][j][v] = 0.0f;
-    const int pre = S < kRoDepth ? S : kRoDepth;
-    for (int s = 0; s < pre; s++) issue(s);
-    for (int s = 0; s < S; s++) {
-        // step s's fragments (this wave's DMAs) have landed once at most 2 (steps in flight after
-        // it) remain; the barrier makes every wave's visible and retires step s - 1's reads
-        const int after = min(S - 1 - s, kRoDepth - 1);
-        if (after == kRoDepth - 1) wait_vmcnt<2 * (kRoDepth - 1)>();
-        else wait_vmcnt_steps(after);
-        // a bare barrier: each wave has waited for its own DMAs above, and LDS is coherent within
-        // the workgroup (__syncthreads' fence would wait for every DMA in flight)
-        asm volatile("s_barrier" ::: "memory");
-        if (s + kRoDepth < S) issue(s + kRoDepth);
-        const uint32_t sb = lbase + (s % kRoStages) * kRoStageBytes + lane * 16;
-        v4u fa[4], fb[2];
-        lds_read_frags(sb + rh * 4096, sb + 8192 + cq * 2048, fa, fb);
+    // Steps go in pairs u, u + 1 (u even): a group is their four DMAs of h, then their four
+    // weight loads, and every wave issues its groups in order. Group u + 12 goes out in the
+    // iteration of steps u, u + 1. "Group u's DMAs have landed" is then "at most 4 + 8 n vector
+    // memory operations outstanding", n the later groups issued; it also means every earlier
+    // group, weights included, has landed.
+    v4u br[kRoDepth][2];
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+    for (int u = 0; u < kRoDepth; u += 2) {
+        issue_a(u);
+        issue_a(u + 1);
+        asm volatile("" ::: "memory");
+        load_b(u, br[u][0], br[u][1]);
+        load_b(u + 1, br[u + 1][0], br[u + 1][1]);
+        asm volatile("" ::: "memory");
+    }
+    v4u fx[8], fy[8];  // even steps' A fragments, odd steps'
+    constexpr int kGroupsAhead = kRoDepth / 2 - 1;  // groups issued after the one awaited
+    static_assert(4 + 8 * kGroupsAhead == 44, "the wait below");
+    asm volatile("s_waitcnt vmcnt(44)" ::: "memory");  // group 0's DMAs
+    // a bare barrier: each wave has waited for its own DMAs, and LDS is coherent within the
+    // workgroup (__syncthreads' fence would wait for every DMA in flight)
+    asm volatile("s_barrier" ::: "memory");
+    lds_read_a8(stage(0), fx);
+    // Iteration i: steps 2 i, 2 i + 1. Wait for group 2 i + 2 and a barrier (every wave's DMAs of
+    // steps 2 i + 2, 2 i + 3 have landed, and every wave is done reading steps 2 i - 2, 2 i - 1,
+    // whose stages group 2 i + 12 reuses); group 2 i + 12's DMAs; step 2 i's MFMAs with step
+    // 2 i + 1's reads between, step 2 i + 1's with step 2 i + 2's; group 2 i + 12's weight loads
+    // into the ring slots just used.
+    auto mfmas = [&](const v4u(&fa)[8], const v4u &b0, const v4u &b1) {
 #pragma unroll
-            for (int j = 0; j < 2; j++)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, fa[i]),
-                                                                    __builtin_bit_cast(bf16x8_t, fb[j]), acc[i][j], 0, 0, 0);
+        for (int i = 0; i < 8; i++) {
+            acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, fa[i]),
+                                                                __builtin_bit_cast(bf16x8_t, b0), acc[i][0], 0, 0, 0);
+            acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, fa[i]),
+                                                                __builtin_bit_cast(bf16x8_t, b1), acc[i][1], 0, 0, 0);
+        }
+    };
+    const int NI = S / 2;
+    int i0 = 0;
+    while (i0 < NI) {
+#pragma unroll
+        for (int k = 0; k < kRoDepth / 2; k++) {
+            const int i = i0 + k, u = 2 * i;
+            if (i < NI) {
+                // (the wait is an asm statement that takes this iteration's weight registers as
+                // in-out operands: nothing that reads them can be placed before it)
+                static_assert(4 + 8 * (kGroupsAhead - 1) == 36, "the wait below");
+                asm volatile("s_waitcnt vmcnt(36)"
+                             : "+v"(br[2 * k][0]), "+v"(br[2 * k][1]), "+v"(br[2 * k + 1][0]), "+v"(br[2 * k + 1][1])
+                             :
+                             : "memory");
+                asm volatile("s_barrier" ::: "memory");
+                issue_a(u + kRoDepth);
+                issue_a(u + kRoDepth + 1);
+                asm volatile("" ::: "memory");
+                // step u + 1's A fragments in flight while step u's sixteen MFMAs run (the
+                // scheduling barriers keep the MFMAs between the reads' issue and their wait)
+                lds_issue_a8(stage(u + 1), fy);
+                __builtin_amdgcn_sched_barrier(0);
+                mfmas(fx, br[2 * k][0], br[2 * k][1]);
+                __builtin_amdgcn_sched_barrier(0);
+                lds_wait_a8(fy);
+                lds_issue_a8(stage(u + 2), fx);
+                __builtin_amdgcn_sched_barrier(0);
+                mfmas(fy, br[2 * k + 1][0], br[2 * k + 1][1]);
+                __builtin_amdgcn_sched_barrier(0);
+                lds_wait_a8(fx);
+                load_b(u + kRoDepth, br[2 * k][0], br[2 * k][1]);
+                load_b(u + kRoDepth + 1, br[2 * k + 1][0], br[2 * k + 1][1]);
+                asm volatile("" ::: "memory");
+            }
+        }
+        i0 += kRoDepth / 2;
+    }
+    // Every copy, the ones past the last step included, lands before the stages are reused, and
+    // every weight load lands before its registers can be given to anything else: the ring's
+    // last loads are never read, so the wait takes the registers as in-out operands (a load into
+    // a register the compiler thinks free would overwrite whatever it put there).
+    asm volatile("s_waitcnt vmcnt(0)"
+                 : "+v"(br[0][0]), "+v"(br[0][1]), "+v"(br[1][0]), "+v"(br[1][1]), "+v"(br[2][0]), "+v"(br[2][1]),
+                   "+v"(br[3][0]), "+v"(br[3][1]), "+v"(br[4][0]), "+v"(br[4][1]), "+v"(br[5][0]), "+v"(br[5][1])
+                 :
+                 : "memory");
+    asm volatile(""
+                 : "+v"(br[6][0]), "+v"(br[6][1]), "+v"(br[7][0]), "+v"(br[7][1]), "+v"(br[8][0]), "+v"(br[8][1]),
+                   "+v"(br[9][0]), "+v"(br[9][1]), "+v"(br[10][0]), "+v"(br[10][1]), "+v"(br[11][0]), "+v"(br[11][1])
+                 :
+                 : "memory");
+    static_assert(kRoDepth == 12, "the drain above names every ring slot");
+    if (S & 1) {  // the last step, S - 1 = 2 NI: its fragments are in fx, its weight in slot (S - 1) % 12
+        const int slot = (S - 1) % kRoDepth;
+        v4u b0 = br[0][0], b1 = br[0][1];
+#pragma unroll
+        for (int k = 1; k < kRoDepth; k++)
+            if (slot == k) {
+                b0 = br[k][0];
+                b1 = br[k][1];
+            }
+        mfmas(fx, b0, b1);
     }
     __syncthreads();
 
     // ---- epilogue: eight passes of 32 rows x 256 columns through LDS ([32][256 + 4] f32). In pass
-    // q the four waves holding rows 32 q .. 32 q + 31 store them; then thread t < 256 takes row
-    // t / 8 and the 32 columns 32 (t % 8) .. + 31 of it.
+    // q every wave stores its tiles of rows 32 q .. 32 q + 31; then thread t takes row t / 8 and
+    // the 32 columns 32 (t % 8) .. + 31 of it.
     float *T = reinterpret_cast<float *>(lds);
     constexpr int TLD = kRoCols + 4;
+    static_assert(32 * TLD * 4 <= kRoStages * kRoStageBytes, "the epilogue's tile fits the stages");
     const int prow = tid >> 3, part = tid & 7;
 #pragma unroll
     for (int q = 0; q < 8; q++) {
-        const int qh = q >> 2, qi = q & 3;  // row half and row tile within it (constants once unrolled)
-        if (rh == qh) {
 #pragma unroll
-            for (int j = 0; j < 2; j++)
+        for (int j = 0; j < 2; j++)
 #pragma unroll
-                for (int v = 0; v < 16; v++) {
-                    const int r = 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
-                    T[r * TLD + cq * 64 + j * 32 + fr] = acc[qi][j][v];
-                }
-        }
+            for (int v = 0; v < 16; v++) {
+                const int r = 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
+                T[r * TLD + wave * 64 + j * 32 + fr] = acc[q][j][v];
+            }
         __syncthreads();
-        if (tid >= 256) {  // 256 threads take the 32 rows x 256 columns
-            __syncthreads();
-            continue;
-        }
         const int row = 32 * q + prow;
         const int col0 = n0 + 32 * part;
         float x[32];
@@ -309,33 +397,51 @@ struct ResolveP {
 constexpr int kResThreads = 256;
 constexpr int kResMaxBlocks = 32;  // blocks of 32 columns per thread: V <= 262144
 constexpr int kResMaxTiles = 4;    // tiles of 256 columns per thread
-constexpr int kResPhase = 16;     // k-steps per phase of the recomputation's ring
-constexpr int kResSlots = 4;      // phases in the ring (three in flight)
+constexpr int kResMaxK = 16384;    // dim at most: the row of h is held in LDS (32 KiB)
+constexpr int kResPhase = 32;      // k-steps per phase of the weight ring (32 KiB)
+constexpr int kResSlots = 3;       // phases in the ring: two in flight while wave 0 uses one
 
-// Sixteen 16-byte LDS reads: the A and B fragments of eight consecutive k-steps (2 KiB apart,
-// B 1 KiB after A), and the wait for them (see lds_read_frags).
-__device__ __forceinline__ void lds_read_8x2(uint32_t a, v4u (&fa)[8], v4u (&fb)[8]) {
+// Wait until at most n (0 .. 8) vector memory operations of this wave are outstanding.
+__device__ __forceinline__ void wait_vmcnt_upto8(int n) {
+    switch (n) {
+        case 0: wait_vmcnt<0>(); break;
+        case 1: wait_vmcnt<1>(); break;
+        case 2: wait_vmcnt<2>(); break;
+        case 3: wait_vmcnt<3>(); break;
+        case 4: wait_vmcnt<4>(); break;
+        case 5: wait_vmcnt<5>(); break;
+        case 6: wait_vmcnt<6>(); break;
+        case 7: wait_vmcnt<7>(); break;
+        default: wait_vmcnt<8>(); break;
+    }
+}
+
+// The operands of four consecutive k-steps (A: the row of h, 32 bytes a step apart in LDS;
+// B: the block's fragments, 1 KiB apart) and the wait for them (see lds_read_frags).
+__device__ __forceinline__ void lds_read4(uint32_t a, uint32_t b, v4u (&fa)[4], v4u (&fb)[4]) {
     asm volatile(
-        "ds_read_b128 %0, %16\n\t"
-        "ds_read_b128 %1, %16 offset:2048\n\t"
-        "ds_read_b128 %2, %16 offset:4096\n\t"
-        "ds_read_b128 %3, %16 offset:6144\n\t"
-        "ds_read_b128 %4, %16 offset:8192\n\t"
-        "ds_read_b128 %5, %16 offset:10240\n\t"
-        "ds_read_b128 %6, %16 offset:12288\n\t"
-        "ds_read_b128 %7, %16 offset:14336\n\t"
-        "ds_read_b128 %8, %16 offset:1024\n\t"
-        "ds_read_b128 %9, %16 offset:3072\n\t"
-        "ds_read_b128 %10, %16 offset:5120\n\t"
-        "ds_read_b128 %11, %16 offset:7168\n\t"
-        "ds_read_b128 %12, %16 offset:9216\n\t"
-        "ds_read_b128 %13, %16 offset:11264\n\t"
-        "ds_read_b128 %14, %16 offset:13312\n\t"
-        "ds_read_b128 %15, %16 offset:15360\n\t"
+        "ds_read_b128 %0, %8\n\t"
+        "ds_read_b128 %1, %8 offset:32\n\t"
+        "ds_read_b128 %2, %8 offset:64\n\t"
+        "ds_read_b128 %3, %8 offset:96\n\t"
+        "ds_read_b128 %4, %9\n\t"
+        "ds_read_b128 %5, %9 offset:1024\n\t"
+        "ds_read_b128 %6, %9 offset:2048\n\t"
+        "ds_read_b128 %7, %9 offset:3072\n\t"
         "s_waitcnt lgkmcnt(0)"
-        : "=&v"(fa[0]), "=&v"(fa[1]), "=&v"(fa[2]), "=&v"(fa[3]), "=&v"(fa[4]), "=&v"(fa[5]), "=&v"(fa[6]), "=&v"(fa[7]),
-          "=&v"(fb[0]), "=&v"(fb[1]), "=&v"(fb[2]), "=&v"(fb[3]), "=&v"(fb[4]), "=&v"(fb[5]), "=&v"(fb[6]), "=&v"(fb[7])
-        : "v"(a)
+        : "=&v"(fa[0]), "=&v"(fa[1]), "=&v"(fa[2]), "=&v"(fa[3]), "=&v"(fb[0]), "=&v"(fb[1]), "=&v"(fb[2]), "=&v"(fb[3])
+        : "v"(a), "v"(b)
+        : "memory");
+}
+
+// One k-step's operands (A: this row of h; B: the block's fragment) and the wait for them.
+__device__ __forceinline__ void lds_read1(uint32_t a, uint32_t b, v4u &fa, v4u &fb) {
+    asm volatile(
+        "ds_read_b128 %0, %2\n\t"
+        "ds_read_b128 %1, %3\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(fa), "=&v"(fb)
+        : "v"(a), "v"(b)
         : "memory");
 }
 
@@ -355,7 +461,8 @@ __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
     __shared__ int wsel[kResThreads / 64];
     __shared__ int s_blk;
     __shared__ double s_tl;
-    __shared__ __attribute__((aligned(16))) uint8_t ring[kResSlots * kResPhase * 2048];
+    __shared__ __attribute__((aligned(16))) uint8_t hrow[kResMaxK * 2];
+    __shared__ __attribute__((aligned(16))) uint8_t ring[kResSlots * kResPhase * 1024];
     const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *tref = p.tref + int64_t(row) * p.ntile;
     const float *tmax = p.tmax + int64_t(row) * p.ntile;
@@ -368,13 +475,27 @@ __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
             p.status[row] = st;
         }
     };
-    // ---- the row's maximum over the tiles (exact; the order does not matter for a maximum)
-    float m = -INFINITY;
+    // every load of the row's records first (one round trip): the tiles' maxima, then this
+    // thread's contiguous run of blocks and their tiles' references
+    float tm[kResMaxTiles];
 #pragma unroll
     for (int i = 0; i < kResMaxTiles; i++) {
         const int t = tid + i * kResThreads;
-        if (t < p.ntile) m = fmaxf(m, tmax[t]);
+        tm[i] = t < p.ntile ? tmax[t] : -INFINITY;
     }
+    const int per = (p.nblk + kResThreads - 1) / kResThreads;  // at most kResMaxBlocks
+    const int b0 = tid * per, b1 = min(p.nblk, b0 + per);
+    float bs[kResMaxBlocks], br[kResMaxBlocks];
+#pragma unroll
+    for (int i = 0; i < kResMaxBlocks; i++) {
+        const int b = b0 + i;
+        const bool in = i < per && b < b1;
+        bs[i] = in ? bsum[b] : 0.0f;
+        br[i] = in ? tref[b / (kRoCols / kRoBlock)] : -INFINITY;
+    }
+    // ---- the row's maximum over the tiles (exact; the order does not matter for a maximum)
+    static_assert(kResMaxTiles == 4, "the maximum over the thread's tiles");
+    float m = fmaxf(fmaxf(tm[0], tm[1]), fmaxf(tm[2], tm[3]));
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
     if (lane == 0) wmax[wave] = m;
@@ -385,18 +506,7 @@ __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
         return;
     }
     const float A = M * p.c;
-    // ---- block weights relative to A, each thread a contiguous run of blocks, f64 in index order
-    const int per = (p.nblk + kResThreads - 1) / kResThreads;  // at most kResMaxBlocks
-    const int b0 = tid * per, b1 = min(p.nblk, b0 + per);
-    // every load of the thread's blocks first (one wait), then the f64 sums in order
-    float bs[kResMaxBlocks], br[kResMaxBlocks];
-#pragma unroll
-    for (int i = 0; i < kResMaxBlocks; i++) {
-        const int b = b0 + i;
-        const bool in = i < per && b < b1;
-        bs[i] = in ? bsum[b] : 0.0f;
-        br[i] = in ? tref[b / (kRoCols / kRoBlock)] : -INFINITY;
-    }
+    // ---- block weights relative to A, f64 in index order
     double wbk[kResMaxBlocks];
     double run = 0.0;
 #pragma unroll
@@ -494,63 +604,71 @@ __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
     const double tl = s_tl;
     // ---- recompute the block's 32 logits: the same MFMA over the same k order from zero. Every
     // lane's A row is this row (so every output row holds it); lane l's B column is 32 b + l % 32.
-    // The four waves copy the operand fragments into an LDS ring by DMA, three phases of 16
-    // k-steps ahead; wave 0 runs the MFMA chain from LDS.
-    const int fr = lane & 31, fk = 8 * (lane >> 5);
+    // The row of h goes into LDS once (1 KiB pieces, piece c by wave c % 4); the block's weight
+    // fragments (1 KiB a k-step) stream through a ring of three 32-step phases, two in flight,
+    // each wave copying every fourth step; wave 0 runs the MFMA chain from LDS.
+    const int fr = lane & 31;
     const int col = bstar * kRoBlock + fr;
     const bool colok = col < p.V;
     const int S2 = p.K / 16;
     const int NP = (S2 + kResPhase - 1) / kResPhase;
-    // the row of h (every lane's A operand: k 16 s + 8 (l / 32) .. + 7 of it) and the block's
-    // column group of the packed weight (1 KiB per k-step, the B operands in lane order)
+    const int bt = bstar / 8, bg = bstar % 8;  // the block's tile and column group within it
     const __amdgpu_buffer_rsrc_t hres = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t *>(p.h + int64_t(row) * p.ldh), short(0), p.K * 2, kBufferWord3);
     const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t *>(p.wp + int64_t(bstar) * S2 * 1024), short(0), S2 * 1024, kBufferWord3);
-    const int hoff = fk * 2, woff = lane * 16;
-    const uint32_t rbase = uint32_t((uintptr_t)(lds_ptr_t)(ring));
-    // phase q: step q 16 + i is issued by wave i % 4 (two DMAs: its A and B fragments), into
-    // slot (q % 4) of the ring: 16 steps x 2 KiB
+        const_cast<uint8_t *>(p.wp + (int64_t(bt) * S2 * 8 + bg) * 1024), short(0), (S2 - 1) * 8192 + 1024,
+        kBufferWord3);
+    for (int c = wave; c * 1024 < p.K * 2; c += 4)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(hres, (lds_ptr_t)(hrow + c * 1024), 16, c * 1024 + lane * 16, 0, 0,
+                                                 0);
+    const uint32_t rbase = uint32_t((uintptr_t)(lds_ptr_t)(ring)) + lane * 16;
+    const uint32_t hbase = uint32_t((uintptr_t)(lds_ptr_t)(hrow)) + (lane >> 5) * 16;
     auto issue_phase = [&](int q) {
+        uint8_t *slot = ring + (q % kResSlots) * kResPhase * 1024;
         for (int i = wave; i < kResPhase; i += 4) {
             const int st = q * kResPhase + i;
-            if (st < S2) {
-                uint8_t *d = ring + ((q % kResSlots) * kResPhase + i) * 2048;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(hres, (lds_ptr_t)(d), 16, hoff + st * 32, 0, 0, 0);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, (lds_ptr_t)(d + 1024), 16, woff + st * 1024, 0, 0, 0);
-            }
+            if (st < S2)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, (lds_ptr_t)(slot + i * 1024), 16, lane * 16 + st * 8192,
+                                                         0, 0, 0);
         }
     };
-    // the DMAs this wave issues for phase q: two per step i = wave, wave + 4, ... below S2
+    // the DMAs this wave issues for phase q: one per step i = wave, wave + 4, ... below S2
     auto own_dmas = [&](int q) {
         int n = 0;
-        for (int i = wave; i < kResPhase; i += 4) n += q * kResPhase + i < S2 ? 2 : 0;
+        for (int i = wave; i < kResPhase; i += 4) n += q * kResPhase + i < S2 ? 1 : 0;
         return n;
     };
-    const int pre = NP < kResSlots - 1 ? NP : kResSlots - 1;
-    for (int q = 0; q < pre; q++) issue_phase(q);
+    issue_phase(0);
+    if (NP > 1) issue_phase(1);
     f32x16_t acc;
 #pragma unroll
     for (int v = 0; v < 16; v++) acc[v] = 0.0f;
     for (int q = 0; q < NP; q++) {
-        // this wave's DMAs of phase q have landed when at most those it issued for the (up to
-        // two) phases after it remain
-        int later = 0;
-        for (int q2 = q + 1; q2 < NP && q2 < q + kResSlots - 1; q2++) later += own_dmas(q2);
-        wait_vmcnt_upto16(later);
+        // this wave's DMAs of phase q (and, before them, of h) have landed when at most those it
+        // issued for phase q + 1 remain; after the barrier every wave's have, and every wave is
+        // past phase q - 1, whose slot phase q + 2 then reuses
+        wait_vmcnt_upto8(q + 1 < NP ? own_dmas(q + 1) : 0);
         asm volatile("s_barrier" ::: "memory");
-        if (q + kResSlots - 1 < NP) issue_phase(q + kResSlots - 1);
+        if (q + 2 < NP) issue_phase(q + 2);
         if (wave == 0) {
-            const uint32_t pb = rbase + (q % kResSlots) * kResPhase * 2048 + lane * 16;
+            // the MFMAs are the compiler's (it places the wait states their results need); the
+            // operands of four steps at a time come in by one read statement
             const int n = min(kResPhase, S2 - q * kResPhase);
-            for (int i0 = 0; i0 < n; i0 += 8) {
-                v4u fa[8], fb[8];
-                lds_read_8x2(pb + i0 * 2048, fa, fb);
+            const uint32_t ab = hbase + q * kResPhase * 32, bb = rbase + (q % kResSlots) * kResPhase * 1024;
+            int i = 0;
+            for (; i + 4 <= n; i += 4) {
+                v4u fa[4], fb[4];
+                lds_read4(ab + i * 32, bb + i * 1024, fa, fb);
 #pragma unroll
-                for (int i = 0; i < 8; i++)
-                    if (i0 + i < n)
-                        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, fa[i]),
-                                                                      __builtin_bit_cast(bf16x8_t, fb[i]), acc, 0, 0, 0);
+                for (int j = 0; j < 4; j++)
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, fa[j]),
+                                                                  __builtin_bit_cast(bf16x8_t, fb[j]), acc, 0, 0, 0);
+            }
+            for (; i < n; i++) {
+                v4u fa, fb;
+                lds_read1(ab + i * 32, bb + i * 1024, fa, fb);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, fa),
+                                                              __builtin_bit_cast(bf16x8_t, fb), acc, 0, 0, 0);
             }
         }
     }
@@ -590,17 +708,27 @@ __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
 // ------------------------------------------------------------------ packing
 
 // Fragment order (see ReadoutP) of a [R, K] bf16 matrix: k contiguous (row r at src + r ld) or,
-// K_MAJOR, the transpose of a [K, R] one (row r is column r of src, k at src + k ld + r). Rows
-// from R up to the next multiple of 32 are zeros. One thread writes one lane's 16 bytes.
-template <bool K_MAJOR>
+// K_MAJOR, the transpose of a [K, R] one (row r is column r of src, k at src + k ld + r); TILED,
+// the weight's tile-major order over `groups` column groups (a multiple of 8), else h's
+// group-major order. Rows from R up to the groups' end are zeros. One thread writes one lane's
+// 16 bytes.
+template <bool K_MAJOR, bool TILED>
 __global__ void k_pack_frags(const uint16_t *src, int R, int K, int64_t ld, v4u *out, int64_t total) {
     const int S = K / 16;
     for (int64_t idx = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; idx < total;
          idx += int64_t(gridDim.x) * blockDim.x) {
         const int l = int(idx % 64);
-        const int64_t gs = idx / 64;
-        const int s = int(gs % S);
-        const int64_t g = gs / S;
+        const int64_t q = idx / 64;
+        int s;
+        int64_t g;
+        if constexpr (TILED) {
+            const int64_t ts = q / 8;  // tile t, step s: t S + s
+            s = int(ts % S);
+            g = ts / S * 8 + q % 8;
+        } else {
+            s = int(q % S);
+            g = q / S;
+        }
         const int64_t r = g * 32 + (l & 31);
         const int k0 = 16 * s + 8 * (l >> 5);
         v4u v = {0, 0, 0, 0};
@@ -620,17 +748,16 @@ __global__ void k_pack_frags(const uint16_t *src, int R, int K, int64_t ld, v4u 
     }
 }
 
-int launch_pack(const void *src, int R, int K, int64_t ld, bool k_major, void *out) {
-    const int64_t total = int64_t((R + 31) / 32) * (K / 16) * 64;
+// h (group-major, ceil(R / 32) groups) or the weight (tile-major, whole tiles of 256 columns).
+template <bool K_MAJOR, bool TILED>
+int launch_pack_t(const void *src, int R, int K, int64_t ld, void *out) {
+    const int64_t groups = TILED ? int64_t((R + kRoCols - 1) / kRoCols) * 8 : (R + 31) / 32;
+    const int64_t total = groups * (K / 16) * 64;
     int64_t blocks = (total + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     const dim3 g{unsigned(blocks), 1, 1}, b{256, 1, 1};
-    if (k_major)
-        hipLaunchKernelGGL(k_pack_frags<true>, g, b, 0, ctx().stream, static_cast<const uint16_t *>(src), R, K, ld,
-                           static_cast<v4u *>(out), total);
-    else
-        hipLaunchKernelGGL(k_pack_frags<false>, g, b, 0, ctx().stream, static_cast<const uint16_t *>(src), R, K, ld,
-                           static_cast<v4u *>(out), total);
+    hipLaunchKernelGGL((k_pack_frags<K_MAJOR, TILED>), g, b, 0, ctx().stream, static_cast<const uint16_t *>(src), R,
+                       K, ld, static_cast<v4u *>(out), total);
     return launched("readout pack");
 }
 
@@ -641,7 +768,7 @@ using namespace nt;
 
 extern "C" int64_t nt_hip_rl_readout_packed_bytes(int64_t vocab, int64_t dim) {
     if (vocab < 1 || dim < 16 || dim % 16 != 0) return -1;
-    return (vocab + 31) / 32 * 32 * dim * 2;
+    return (vocab + kRoCols - 1) / kRoCols * kRoCols * dim * 2;
 }
 
 extern "C" int nt_hip_rl_readout_pack_weight(const void *weight, int32_t layout, int64_t vocab, int64_t dim,
@@ -650,26 +777,27 @@ extern "C" int nt_hip_rl_readout_pack_weight(const void *weight, int32_t layout,
     const bool dv = layout == NT_READOUT_W_DV;
     if ((layout != NT_READOUT_W_VD && !dv) || vocab < 1 || vocab > kRoMaxVocab || dim < 16 || dim % 16 != 0 ||
         !weight || !packed || ld < (dv ? vocab : dim) || (!dv && (ld % 8 != 0 || reinterpret_cast<uintptr_t>(weight) % 16)) ||
-        reinterpret_cast<uintptr_t>(packed) % 16 || (vocab + 31) / 32 * (dim / 16) * 1024 >= (int64_t(1) << 31))
+        reinterpret_cast<uintptr_t>(packed) % 16 || (vocab + kRoCols - 1) / kRoCols * (dim / 16) * 8192 >= (int64_t(1) << 31))
         return fail(NT_E_ARG, std::string(who) + ": layout " + std::to_string(layout) + ", vocab " +
                                   std::to_string(vocab) + " (at most 262144), dim " + std::to_string(dim) +
                                   " (a multiple of 16), ld " + std::to_string(ld) +
                                   " (at least the row; [V, d] rows a multiple of 8 and 16-byte aligned)");
     std::unique_lock<std::mutex> lk;
     if (int rc = enter(&lk)) return rc;
-    return launch_pack(weight, int(vocab), int(dim), ld, dv, packed);
+    return dv ? launch_pack_t<true, true>(weight, int(vocab), int(dim), ld, packed)
+              : launch_pack_t<false, true>(weight, int(vocab), int(dim), ld, packed);
 }
 
 extern "C" int nt_hip_rl_readout_sample(const NtRlReadoutSampleArgs *a) {
     const char *who = "nt_hip_rl_readout_sample";
     if (!a) return fail(NT_E_ARG, std::string(who) + ": null args");
     const int64_t rows = a->rows, V = a->vocab, K = a->dim;
-    if (rows < 0 || rows > kRoRows || V < 1 || V > kRoMaxVocab || K < 16 || K % 16 != 0 || a->ldh < K ||
+    if (rows < 0 || rows > kRoRows || V < 1 || V > kRoMaxVocab || K < 16 || K % 16 != 0 || K > kResMaxK || a->ldh < K ||
         a->ldh % 8 != 0 || rows * a->ldh * 2 >= (int64_t(1) << 31) ||
-        (V + 31) / 32 * (K / 16) * 1024 >= (int64_t(1) << 31))
+        (V + kRoCols - 1) / kRoCols * (K / 16) * 8192 >= (int64_t(1) << 31))
         return fail(NT_E_ARG, std::string(who) + ": rows " + std::to_string(rows) + " (at most 256), vocab " +
                                   std::to_string(V) + " (at most 262144), dim " + std::to_string(K) +
-                                  " (a multiple of 16), ldh (>= dim, a multiple of 8)");
+                                  " (a multiple of 16, at most 16384), ldh (>= dim, a multiple of 8)");
     if (a->mask_kind != NT_MASK_NONE && a->mask_kind != NT_MASK_U8)
         return fail(NT_E_UNSUPPORTED, std::string(who) + ": only no mask or a u8 keep-mask");
     if ((a->mask_kind == NT_MASK_U8) != (a->mask != nullptr))
@@ -695,7 +823,7 @@ extern "C" int nt_hip_rl_readout_sample(const NtRlReadoutSampleArgs *a) {
     if (int rc = scratch_alloc(need, &ws)) return rc;
     uint8_t *wb = static_cast<uint8_t *>(ws);
     // h into fragment order (2 MB at 256 rows of 4096)
-    if (int rc = launch_pack(a->hidden, int(rows), int(K), a->ldh, false, wb)) return rc;
+    if (int rc = launch_pack_t<false, false>(a->hidden, int(rows), int(K), a->ldh, wb)) return rc;
     const double T = greedy ? 1.0 : a->temperature;
     ReadoutP p;
     p.hp = wb;
