@@ -660,9 +660,11 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
 // row's bytes stream through G compute units. Each wave of a segment runs phase 1 of the
 // register-resident sampler on its K chunks, then publishes a wave record in device scratch:
 // its exponent reference, its maximum (or the value its reference came from), the first index of
-// its maximum (greedy), its f64 totals and its K f32 chunk sums. The workgroup then releases its
-// records (an agent-scope fence) and increments the row's arrival counter with one agent-scope
-// acq_rel vector atomic. No workgroup waits for another: every one but the last to arrive exits;
+// its maximum (greedy), its f64 totals and its K f32 chunk sums, with agent-scope atomic stores
+// (coherent across the XCDs' L2s). The workgroup waits until those stores have completed, then
+// increments the row's arrival counter with one agent-scope vector atomic; the last arriver reads
+// the records with agent-scope atomic loads. No workgroup waits for another: every one but the
+// last to arrive exits;
 // the last one's first wave merges the G NW wave records of the row in index order (phase 2 over
 // up to 64 records, one per lane), finds the crossing wave and chunk from the records, reads the
 // crossing chunk again (512 elements, about 1.5 KB, from the caches in practice) and resolves
