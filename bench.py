@@ -743,6 +743,9 @@ def main():
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--workload", default="c4",
                     choices=["c4", "c4s", "c2", "c3", "c3b", "c5", "ops", "readout", "matmul"])
+    ap.add_argument("--kernels", default="aot", choices=["aot", "rtc"],
+                    help="how the sampler kernels are loaded: the library's hipcc code objects (the default) "
+                         "or hiprtc at first use (compiled in the warmup)")
     ap.add_argument("--cpu-rows", type=int, default=256, help="rows of the CPU baseline sample (0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="repeat the CPU sample up to this long")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -775,6 +778,7 @@ def main():
         # torch's own HIP runtime must find the device before the library claims it
         import torch
         torch.zeros(1, device="cuda:0")
+    nr.set_kernel_path(args.kernels)
     nr.claim(0)
     if args.workload in ("c4", "c4s", "c2"):
         out = bench_sample(nr, W, args, args.workload)
@@ -788,6 +792,7 @@ def main():
         out = bench_readout(nr, W, args)
     else:
         out = bench_score(nr, W, args, args.workload)
+    out["kernels"] = nr.kernel_path()
     print(json.dumps(out), flush=True)
 
 

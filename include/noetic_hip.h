@@ -21,7 +21,9 @@
 #ifndef NOETIC_HIP_H
 #define NOETIC_HIP_H
 
+#ifndef __HIPCC_RTC__ /* the library's kernels compiled at run time by hiprtc see size_t from it */
 #include <stddef.h>
+#endif
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -34,6 +36,7 @@ extern "C" {
 #define NT_E_UNCLAIMED (-2)   /* no device claimed in this process */
 #define NT_E_CLAIMED (-3)     /* another device is already claimed by this process */
 #define NT_E_UNSUPPORTED (-4) /* a valid request this build does not implement */
+#define NT_E_RTC (-5)         /* the run-time kernel compiler (hiprtc) failed; the log is in nt_hip_last_error */
 
 /* ---- dtypes and mask kinds ------------------------------------------------------------ */
 #define NT_F32 0  /* f32 logits */
@@ -91,6 +94,21 @@ int nt_hip_sync(void);
 int nt_hip_stream(void **out);
 /* Launch counter (the reference's `launches()`, src/tensor/cuda/backend.rs:1034-1036). */
 uint64_t nt_hip_launches(void);
+
+/* Where the sampler kernels (nt_hip_rl_sample, nt_hip_rl_sample_noalloc) launch from. The CUDA
+ * backend compiles its kernels with NVRTC at first use and caches the functions
+ * (src/tensor/cuda/mod.rs:169-218, cuda/backend.rs:281-293, 322-358); here both ways exist for
+ * one device source: NT_KERNELS_AOT, the code objects hipcc built into this library (the
+ * default), and NT_KERNELS_RTC, each template instance compiled by hiprtc at its first launch
+ * from the source embedded in the library (0.2-1.3 s each), loaded with hipModuleLoadData, launched
+ * with hipModuleLaunchKernel and cached per process and on disk (NOETIC_HIP_CACHE_DIR, else
+ * $HOME/.cache/noetic-hip). The environment's NOETIC_HIP_KERNELS=aot|rtc sets the first value;
+ * nt_hip_set_kernel_path changes it for the process and returns the previous path (or NT_E_ARG).
+ * With NT_KERNELS_RTC, nt_hip_key also names hiprtc's version and the embedded source's SHA-256. */
+#define NT_KERNELS_AOT 0
+#define NT_KERNELS_RTC 1
+int nt_hip_set_kernel_path(int path);
+int nt_hip_kernel_path(void);
 
 /* ===================================================================== nn::rl fused rows
  * Logits are row-major [rows, V] (rows = S*B*T of `[S, B, T, V]`, rl.rs:8-14) with row stride

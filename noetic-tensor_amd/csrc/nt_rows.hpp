@@ -3,6 +3,17 @@
 // fixed-order DPP reductions and scans, and the host-side argument checks of the row entry points.
 #pragma once
 
+#ifdef __HIPCC_RTC__
+// compiled at run time by hiprtc (rtc.cpp): the device part only, the C header under its own name
+#include <stdint.h>
+#include <type_traits>
+
+#include "noetic_hip.h"
+// <cmath>'s and <cfloat>'s constants, as the compiler defines them there
+#define INFINITY __builtin_inff()
+#define NAN __builtin_nanf("")
+#define FLT_MAX __FLT_MAX__
+#else
 #include <hip/hip_runtime.h>
 
 #include <cfloat>
@@ -14,6 +25,7 @@
 
 #include "../../include/noetic_hip.h"
 #include "nt_internal.hpp"
+#endif
 
 namespace nt {
 namespace {
@@ -512,6 +524,7 @@ struct SampleP {
 
 // ------------------------------------------------------------------ host-side checks
 
+#ifndef __HIPCC_RTC__
 inline int check_rows(int64_t rows, int64_t V, int64_t ld, int32_t dtype, int32_t mk, const void *mask, int64_t mask_ld,
                const char *who) {
     char buf[256];
@@ -534,6 +547,7 @@ inline bool aligned_rows(const void *x, int64_t V, int64_t ld, int32_t dtype, in
     if (mk == NT_MASK_F32) return mask_ld % 4 == 0 && reinterpret_cast<uintptr_t>(mask) % 16 == 0;
     return true;
 }
+#endif
 
 }  // namespace
 }  // namespace nt

@@ -1,0 +1,32 @@
+// The sampler kernels' run-time path: compiled by hiprtc at first use from the device source
+// embedded in the library (rl_sample_kernels.hpp and the headers it includes), loaded with
+// hipModuleLoadData and launched with hipModuleLaunchKernel, one function per template instance.
+// The ahead-of-time code objects (hipcc, the library's default) run the same source.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <string>
+
+#include "../../include/noetic_hip.h"
+
+namespace nt {
+
+// NT_KERNELS_AOT or NT_KERNELS_RTC: from nt_hip_set_kernel_path, else NOETIC_HIP_KERNELS
+// ("aot" or "rtc"), else NT_KERNELS_AOT.
+int kernel_path();
+
+// Launch `name` (a name expression of the embedded source, such as
+// "nt::k_sample_rr<1, 1, 16, false, 8, 1>") on `s`: compiled, loaded and cached on first use on
+// the current device. `arg` is the kernel's one by-value argument. Call with the context lock
+// held; a compile failure is returned as NT_E_RTC with hiprtc's log, a load failure as HIP's.
+int rtc_launch(const std::string &name, dim3 grid, dim3 block, size_t shm, hipStream_t s, const void *arg);
+
+// The key's middle for the run-time path: "hiprtc<version>-kernels-<sha16 of the embedded source>".
+std::string rtc_key_part();
+
+// "true" / "false" for a name expression.
+inline const char *rtc_bool(bool b) { return b ? "true" : "false"; }
+
+}  // namespace nt

@@ -12,6 +12,7 @@
 
 #include "../../include/noetic_hip.h"
 #include "nt_internal.hpp"
+#include "nt_rtc.hpp"
 
 #ifndef NT_KERNELS_SHA
 #define NT_KERNELS_SHA "unknown"
@@ -183,6 +184,9 @@ int nt_hip_key(char *buf, size_t cap) {
         if (ch == ':') ch = '_';
     std::string sha(NT_KERNELS_SHA);
     std::string key = "hip-" + arch + "-hiprt" + std::to_string(rt) + "-kernels-" + sha.substr(0, 16);
+    // the sampler kernels compiled at run time add hiprtc's version and the embedded source's hash
+    // (the CUDA backend's key names NVRTC and its sources, cuda/backend.rs:962-966)
+    if (kernel_path() == NT_KERNELS_RTC) key += "-" + rtc_key_part();
     std::snprintf(buf, cap, "%s", key.c_str());
     return 0;
 }

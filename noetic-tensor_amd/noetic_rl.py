@@ -123,6 +123,8 @@ _SIGS = {
     "nt_hip_sync": (C.c_int, []),
     "nt_hip_stream": (C.c_int, [C.POINTER(C.c_void_p)]),
     "nt_hip_launches": (C.c_uint64, []),
+    "nt_hip_set_kernel_path": (C.c_int, [C.c_int]),
+    "nt_hip_kernel_path": (C.c_int, []),
     "nt_hip_rl_sample": (C.c_int, [C.POINTER(NtRlSampleArgs)]),
     "nt_hip_rl_sample_gumbel": (C.c_int, [C.POINTER(NtRlGumbelArgs)]),
     "nt_hip_rl_readout_sample": (C.c_int, [C.POINTER(NtRlReadoutSampleArgs)]),
@@ -236,6 +238,27 @@ def key() -> str:
     buf = C.create_string_buffer(256)
     _check(_dev().nt_hip_key(buf, 256), "key")
     return buf.value.decode()
+
+
+KERNELS_AOT, KERNELS_RTC = 0, 1
+
+
+def set_kernel_path(path: str) -> str:
+    """Choose how the sampler kernels are loaded for the rest of the process: "aot" (the code
+    objects hipcc built into the library) or "rtc" (compiled by hiprtc from the embedded source at
+    first use, as the reference compiles its CUDA kernels with NVRTC: cuda/mod.rs:169-218).
+    Returns the previous choice. Needs no device."""
+    code = {"aot": KERNELS_AOT, "rtc": KERNELS_RTC}.get(path)
+    if code is None:
+        raise ValueError(f"kernel path {path!r}: 'aot' or 'rtc'")
+    prev = lib().nt_hip_set_kernel_path(code)
+    if prev < 0:
+        _check(prev, "set_kernel_path")
+    return "rtc" if prev == KERNELS_RTC else "aot"
+
+
+def kernel_path() -> str:
+    return "rtc" if lib().nt_hip_kernel_path() == KERNELS_RTC else "aot"
 
 
 def platform_details() -> str:

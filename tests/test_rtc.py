@@ -1,0 +1,68 @@
+"""CPU tests of the sampler kernels' run-time path (hiprtc): the path switch needs no device, and
+hiprtc compiles the embedded device source into a gfx950 code object here, without a GPU, with
+the options the library passes (rtc.cpp)."""
+import ctypes as C
+import os
+
+import pytest
+
+import noetic_rl as nr
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CSRC = os.path.join(ROOT, "noetic-tensor_amd", "csrc")
+
+# The files the library embeds, under the names the program includes them by (Makefile: RTC_SRC).
+EMBEDDED = {
+    "noetic_hip.h": os.path.join(ROOT, "include", "noetic_hip.h"),
+    "nt_rows.hpp": os.path.join(CSRC, "nt_rows.hpp"),
+    "rl_sample_kernels.hpp": os.path.join(CSRC, "rl_sample_kernels.hpp"),
+}
+OPTIONS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
+           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def test_kernel_path_switch_needs_no_device():
+    prev = nr.set_kernel_path("rtc")
+    try:
+        assert nr.kernel_path() == "rtc"
+        assert nr.set_kernel_path("aot") == "rtc"
+        assert nr.kernel_path() == "aot"
+        assert nr.lib().nt_hip_set_kernel_path(7) == -1  # NT_E_ARG
+        assert b"NT_KERNELS_AOT or NT_KERNELS_RTC" in nr.lib().nt_hip_last_error()
+        with pytest.raises(ValueError):
+            nr.set_kernel_path("jit")
+    finally:
+        nr.set_kernel_path(prev)
+
+
+def test_hiprtc_compiles_the_c4_sampler_instance_on_the_cpu():
+    try:
+        rtc = C.CDLL("libhiprtc.so")
+    except OSError:
+        rtc = C.CDLL("/opt/rocm/lib/libhiprtc.so")
+    names = list(EMBEDDED)
+    texts = [open(EMBEDDED[n], "rb").read() for n in names]
+    Arr = C.c_char_p * len(names)
+    prog = C.c_void_p()
+    src = b'#include "rl_sample_kernels.hpp"\n'
+    assert rtc.hiprtcCreateProgram(C.byref(prog), src, b"nt_rtc.hip", len(names), Arr(*texts),
+                                   Arr(*[n.encode() for n in names])) == 0
+    expr = b"nt::k_sample_rr<1, 1, 16, false, 8, 1>"  # bf16 rows, u8 mask, 16 chunks per wave (C4)
+    assert rtc.hiprtcAddNameExpression(prog, expr) == 0
+    opts = (C.c_char_p * len(OPTIONS))(*[o.encode() for o in OPTIONS])
+    rc = rtc.hiprtcCompileProgram(prog, len(OPTIONS), opts)
+    if rc != 0:
+        n = C.c_size_t()
+        rtc.hiprtcGetProgramLogSize(prog, C.byref(n))
+        log = C.create_string_buffer(n.value + 1)
+        rtc.hiprtcGetProgramLog(prog, log)
+        pytest.fail(log.value.decode(errors="replace")[:4000])
+    lowered = C.c_char_p()
+    assert rtc.hiprtcGetLoweredName(prog, expr, C.byref(lowered)) == 0
+    assert lowered.value.startswith(b"_ZN2nt") and b"k_sample_rr" in lowered.value
+    size = C.c_size_t()
+    assert rtc.hiprtcGetCodeSize(prog, C.byref(size)) == 0 and size.value > 0
+    code = C.create_string_buffer(size.value)
+    assert rtc.hiprtcGetCode(prog, code) == 0
+    assert code.raw[:4] == b"\x7fELF"
+    rtc.hiprtcDestroyProgram(C.byref(prog))
