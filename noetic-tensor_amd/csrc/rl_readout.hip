@@ -7,14 +7,15 @@
 //
 //  Pass 1 (k_readout_tiles): logits = h · W on the matrix cores, bf16 operands and f32
 //  accumulation (v_mfma_f32_32x32x16_bf16, as the reference's half-precision product,
-//  src/tensor/gpu/half_gemm.rs:1-10). One 512-thread workgroup owns 256 vocabulary columns for
-//  every row (up to 256 rows); each wave a 128 x 64 part as 4 x 2 MFMA tiles. Both operands are
-//  in fragment order (the weight packed once by nt_hip_rl_readout_pack_weight, h per call), so
-//  one k-step's operands for 32 rows or columns are 1 KiB contiguous, which the load unit copies
-//  straight into LDS (buffer_load ... lds), nine 16 KiB stages deep, eight in flight. The
-//  epilogue turns the tile into the sampler's per-row records instead of writing it: the tile's
-//  maximum and exponent reference, and the sum of the weights 2^(x c - ref) of each 32-column
-//  block (f32). A debug pointer also writes the logits.
+//  src/tensor/gpu/half_gemm.rs:1-10). One 256-thread workgroup (a wave per SIMD) owns 256
+//  vocabulary columns for every row (up to 256 rows); each wave a 256 x 64 part as 8 x 2 MFMA
+//  tiles in its AGPRs. Both operands are in fragment order (the weight packed once by
+//  nt_hip_rl_readout_pack_weight, h per call), so one k-step's operands for 32 rows or columns
+//  are 1 KiB contiguous: h, shared by the waves, is copied by the load unit straight into LDS
+//  (buffer_load ... lds) through 14 stages of 8 KiB; each wave loads its own weight columns into
+//  a register ring 12 k-steps deep. The epilogue turns the tile into the sampler's per-row
+//  records instead of writing it: the tile's maximum and exponent reference, and the sum of the
+//  weights 2^(x c - ref) of each 32-column block (f32). A debug pointer also writes the logits.
 //
 //  Pass 2 (k_readout_resolve): one workgroup per row merges the records in index order in f64,
 //  finds the block holding u S, recomputes that block's 32 logits with the same MFMA chain (the
@@ -201,52 +202,96 @@ __global__ __launch_bounds__(kRoThreads) void k_readout_tiles(ReadoutP p) {
     // workgroup (__syncthreads' fence would wait for every DMA in flight)
     asm volatile("s_barrier" ::: "memory");
     lds_read_a8(stage(0), fx);
-    // Iteration i: steps 2 i, 2 i + 1. Wait for group 2 i + 2 and a barrier (every wave's DMAs of
-    // steps 2 i + 2, 2 i + 3 have landed, and every wave is done reading steps 2 i - 2, 2 i - 1,
-    // whose stages group 2 i + 12 reuses); group 2 i + 12's DMAs; step 2 i's MFMAs with step
-    // 2 i + 1's reads between, step 2 i + 1's with step 2 i + 2's; group 2 i + 12's weight loads
-    // into the ring slots just used.
+    // Iteration i: steps u = 2 i and u + 1, the matrix cores kept fed across the iteration's other
+    // work by placing it between the MFMAs (one wave per SIMD: an instruction that is not an MFMA
+    // runs while the MFMA before it executes, and a run of them leaves the matrix core idle).
+    //  - wait for this wave's weight of step u; step u + 1's A fragments (stage u + 1, complete
+    //    for every wave since the previous iteration's barrier) go in flight;
+    //  - step u's sixteen MFMAs, with, after the first two: the wait for group u + 2 (this wave's
+    //    DMAs of steps u + 2, u + 3) and the barrier (every wave's have landed, and every wave is
+    //    done reading stages u - 2 and u - 1, which the next DMAs reuse), then group u + 12's four
+    //    DMAs one between each pair of MFMAs;
+    //  - step u + 2's A fragments in flight, step u + 1's sixteen MFMAs with step u + 12's weight
+    //    loads after the first (ring slot 2 k: step u's MFMAs have all issued);
+    //  - step u + 13's weight loads into ring slot 2 k + 1 after the last MFMA that reads it.
+    // Each wave issues per group: h(u + 12) and h(u + 13) (four DMAs), then the weight of u + 12
+    // and of u + 13 (two loads each), in that order, so "at most n vector memory operations
+    // outstanding" names a point in that sequence: the weight of step u has landed at 42 (the
+    // weight of u + 1 and five later groups after it), group u + 2's DMAs at 36.
+    auto mfma1 = [&](int i, int j, const v4u &a, const v4u &b) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                            __builtin_bit_cast(bf16x8_t, b), acc[i][j], 0, 0, 0);
+    };
     auto mfmas = [&](const v4u(&fa)[8], const v4u &b0, const v4u &b1) {
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, fa[i]),
-                                                                __builtin_bit_cast(bf16x8_t, b0), acc[i][0], 0, 0, 0);
-            acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, fa[i]),
-                                                                __builtin_bit_cast(bf16x8_t, b1), acc[i][1], 0, 0, 0);
+            mfma1(i, 0, fa[i], b0);
+            mfma1(i, 1, fa[i], b1);
         }
+    };
+    auto dma_half = [&](int t, int g) {  // one of issue_a(t)'s two DMAs (row group 2 wave + g)
+        uint8_t *st = lds + (t % kRoStages) * kRoStageBytes + (2 * wave + g) * 1024;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(hres, (lds_ptr_t)(st), 16, hoff + g * S * 1024 + t * 1024, 0, 0, 0);
     };
     const int NI = S / 2;
     int i0 = 0;
+    static_assert(2 + 8 * (kGroupsAhead - 1) + 8 == 42 && 4 + 8 * (kGroupsAhead - 1) == 36, "the waits below");
     while (i0 < NI) {
 #pragma unroll
         for (int k = 0; k < kRoDepth / 2; k++) {
             const int i = i0 + k, u = 2 * i;
             if (i < NI) {
-                // (the wait is an asm statement that takes this iteration's weight registers as
+                v4u(&b)[2] = br[2 * k];
+                v4u(&c)[2] = br[2 * k + 1];
+                // (each wait is an asm statement that takes the weight registers it covers as
                 // in-out operands: nothing that reads them can be placed before it)
-                static_assert(4 + 8 * (kGroupsAhead - 1) == 36, "the wait below");
-                asm volatile("s_waitcnt vmcnt(36)"
-                             : "+v"(br[2 * k][0]), "+v"(br[2 * k][1]), "+v"(br[2 * k + 1][0]), "+v"(br[2 * k + 1][1])
-                             :
-                             : "memory");
-                asm volatile("s_barrier" ::: "memory");
-                issue_a(u + kRoDepth);
-                issue_a(u + kRoDepth + 1);
-                asm volatile("" ::: "memory");
-                // step u + 1's A fragments in flight while step u's sixteen MFMAs run (the
-                // scheduling barriers keep the MFMAs between the reads' issue and their wait)
+                asm volatile("s_waitcnt vmcnt(42)" : "+v"(b[0]), "+v"(b[1]) : : "memory");
                 lds_issue_a8(stage(u + 1), fy);
                 __builtin_amdgcn_sched_barrier(0);
-                mfmas(fx, br[2 * k][0], br[2 * k][1]);
+                mfma1(0, 0, fx[0], b[0]);
+                mfma1(0, 1, fx[0], b[1]);
+                __builtin_amdgcn_sched_barrier(0);
+                asm volatile("s_waitcnt vmcnt(36)" : "+v"(c[0]), "+v"(c[1]) : : "memory");
+                asm volatile("s_barrier" ::: "memory");
+                __builtin_amdgcn_sched_barrier(0);
+                mfma1(1, 0, fx[1], b[0]);
+                __builtin_amdgcn_sched_barrier(0);
+                dma_half(u + kRoDepth, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                mfma1(1, 1, fx[1], b[1]);
+                __builtin_amdgcn_sched_barrier(0);
+                dma_half(u + kRoDepth, 1);
+                __builtin_amdgcn_sched_barrier(0);
+                mfma1(2, 0, fx[2], b[0]);
+                __builtin_amdgcn_sched_barrier(0);
+                dma_half(u + kRoDepth + 1, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                mfma1(2, 1, fx[2], b[1]);
+                __builtin_amdgcn_sched_barrier(0);
+                dma_half(u + kRoDepth + 1, 1);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int r = 3; r < 8; r++) {
+                    mfma1(r, 0, fx[r], b[0]);
+                    mfma1(r, 1, fx[r], b[1]);
+                }
                 __builtin_amdgcn_sched_barrier(0);
                 lds_wait_a8(fy);
                 lds_issue_a8(stage(u + 2), fx);
                 __builtin_amdgcn_sched_barrier(0);
-                mfmas(fy, br[2 * k + 1][0], br[2 * k + 1][1]);
+                mfma1(0, 0, fy[0], c[0]);
+                __builtin_amdgcn_sched_barrier(0);
+                load_b(u + kRoDepth, b[0], b[1]);
+                __builtin_amdgcn_sched_barrier(0);
+                mfma1(0, 1, fy[0], c[1]);
+#pragma unroll
+                for (int r = 1; r < 8; r++) {
+                    mfma1(r, 0, fy[r], c[0]);
+                    mfma1(r, 1, fy[r], c[1]);
+                }
                 __builtin_amdgcn_sched_barrier(0);
                 lds_wait_a8(fx);
-                load_b(u + kRoDepth, br[2 * k][0], br[2 * k][1]);
-                load_b(u + kRoDepth + 1, br[2 * k + 1][0], br[2 * k + 1][1]);
+                load_b(u + kRoDepth + 1, c[0], c[1]);
                 asm volatile("" ::: "memory");
             }
         }
@@ -278,15 +323,38 @@ __global__ __launch_bounds__(kRoThreads) void k_readout_tiles(ReadoutP p) {
             }
         mfmas(fx, b0, b1);
     }
-    __syncthreads();
 
     // ---- epilogue: eight passes of 32 rows x 256 columns through LDS ([32][256 + 4] f32). In pass
     // q every wave stores its tiles of rows 32 q .. 32 q + 31; then thread t takes row t / 8 and
     // the 32 columns 32 (t % 8) .. + 31 of it.
+    //
+    // The mask bytes of all eight passes are loaded first (their registers were the weight ring's),
+    // so the passes wait for one load's latency, not eight. The barriers between passes order LDS
+    // only: each thread writes its own records and reads no global memory another thread writes,
+    // so no pass waits for the stores of the one before.
+    const int prow = tid >> 3, part = tid & 7;
+    const int col0 = n0 + 32 * part;
+    uint32_t mpre[8][8];  // pass q's mask words when its row is whole and 16-byte aligned, else 0
+    if constexpr (MASK) {
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const int row = 32 * q + prow;
+#pragma unroll
+            for (int e = 0; e < 8; e++) mpre[q][e] = 0;
+            if (row < p.rows && col0 + 32 <= p.V && p.mask_vec) {
+                const uint8_t *mrow = p.mask + int64_t(row) * p.mask_ld + col0;
+                const uint4 m0 = *reinterpret_cast<const uint4 *>(mrow);
+                const uint4 m1 = *reinterpret_cast<const uint4 *>(mrow + 16);
+                mpre[q][0] = m0.x; mpre[q][1] = m0.y; mpre[q][2] = m0.z; mpre[q][3] = m0.w;
+                mpre[q][4] = m1.x; mpre[q][5] = m1.y; mpre[q][6] = m1.z; mpre[q][7] = m1.w;
+            }
+        }
+    }
+    // every wave is done reading the stages (its last reads were waited for), which T reuses
+    asm volatile("s_barrier" ::: "memory");
     float *T = reinterpret_cast<float *>(lds);
     constexpr int TLD = kRoCols + 4;
     static_assert(32 * TLD * 4 <= kRoStages * kRoStageBytes, "the epilogue's tile fits the stages");
-    const int prow = tid >> 3, part = tid & 7;
 #pragma unroll
     for (int q = 0; q < 8; q++) {
 #pragma unroll
@@ -296,9 +364,8 @@ __global__ __launch_bounds__(kRoThreads) void k_readout_tiles(ReadoutP p) {
                 const int r = 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
                 T[r * TLD + wave * 64 + j * 32 + fr] = acc[q][j][v];
             }
-        __syncthreads();
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // the pass's tile is in T
         const int row = 32 * q + prow;
-        const int col0 = n0 + 32 * part;
         float x[32];
 #pragma unroll
         for (int e = 0; e < 32; e += 4) {
@@ -318,15 +385,10 @@ __global__ __launch_bounds__(kRoThreads) void k_readout_tiles(ReadoutP p) {
         // the sampler's values: an excluded column or one past the vocabulary is -inf
         uint32_t mw[8];
         if constexpr (MASK) {
-            const uint8_t *mrow = p.mask + (live ? int64_t(row) * p.mask_ld : 0) + col0;
 #pragma unroll
-            for (int e = 0; e < 8; e++) mw[e] = 0;
-            if (live && col0 + 32 <= p.V && p.mask_vec) {
-                const uint4 m0 = *reinterpret_cast<const uint4 *>(mrow);
-                const uint4 m1 = *reinterpret_cast<const uint4 *>(mrow + 16);
-                mw[0] = m0.x; mw[1] = m0.y; mw[2] = m0.z; mw[3] = m0.w;
-                mw[4] = m1.x; mw[5] = m1.y; mw[6] = m1.z; mw[7] = m1.w;
-            } else if (live) {
+            for (int e = 0; e < 8; e++) mw[e] = mpre[q][e];
+            if (live && !(col0 + 32 <= p.V && p.mask_vec)) {  // a partial or unaligned row: bytes
+                const uint8_t *mrow = p.mask + int64_t(row) * p.mask_ld + col0;
                 for (int e = 0; e < 32 && col0 + e < p.V; e++) mw[e / 4] |= uint32_t(mrow[e]) << (8 * (e % 4));
             }
         }
@@ -369,7 +431,7 @@ __global__ __launch_bounds__(kRoThreads) void k_readout_tiles(ReadoutP p) {
             p.tmax[int64_t(row) * p.ntile + tile] = m;
             p.tfirst[int64_t(row) * p.ntile + tile] = first;
         }
-        __syncthreads();
+        if (q < 7) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // T read by all: reusable
     }
 }
 
