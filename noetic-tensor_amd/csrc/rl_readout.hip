@@ -103,25 +103,15 @@ __device__ __forceinline__ void lds_read_a8(uint32_t a, v4u (&fa)[8]) {
         : "memory");
 }
 
-// The eight A fragments of the next k-step (1 KiB apart in LDS) into `na`, issued only: the
-// registers are in flight until lds_wait_a8 below, and nothing may read them before it.
-__device__ __forceinline__ void lds_issue_a8(uint32_t a, v4u (&na)[8]) {
-    asm volatile(
-        "ds_read_b128 %0, %8\n\t"
-        "ds_read_b128 %1, %8 offset:1024\n\t"
-        "ds_read_b128 %2, %8 offset:2048\n\t"
-        "ds_read_b128 %3, %8 offset:3072\n\t"
-        "ds_read_b128 %4, %8 offset:4096\n\t"
-        "ds_read_b128 %5, %8 offset:5120\n\t"
-        "ds_read_b128 %6, %8 offset:6144\n\t"
-        "ds_read_b128 %7, %8 offset:7168"
-        : "=&v"(na[0]), "=&v"(na[1]), "=&v"(na[2]), "=&v"(na[3]), "=&v"(na[4]), "=&v"(na[5]), "=&v"(na[6]), "=&v"(na[7])
-        : "v"(a)
-        : "memory");
+// One A fragment of a later k-step (OFF bytes past `a` in LDS) into `na`, issued only: the
+// register is in flight until lds_wait_a8 below, and nothing may read it before it.
+template <int OFF>
+__device__ __forceinline__ void lds_issue_a1(uint32_t a, v4u &na) {
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=&v"(na) : "v"(a), "i"(OFF) : "memory");
 }
 
-// The wait for lds_issue_a8's reads; it takes the registers as in-out operands, so that every use
-// of them comes after it.
+// The wait for the eight lds_issue_a1 reads of a k-step; it takes the registers as in-out
+// operands, so that every use of them comes after it.
 __device__ __forceinline__ void lds_wait_a8(v4u (&na)[8]) {
     asm volatile("s_waitcnt lgkmcnt(0)"
                  : "+v"(na[0]), "+v"(na[1]), "+v"(na[2]), "+v"(na[3]), "+v"(na[4]), "+v"(na[5]), "+v"(na[6]),
@@ -205,15 +195,16 @@ __global__ __launch_bounds__(kRoThreads) void k_readout_tiles(ReadoutP p) {
     // Iteration i: steps u = 2 i and u + 1, the matrix cores kept fed across the iteration's other
     // work by placing it between the MFMAs (one wave per SIMD: an instruction that is not an MFMA
     // runs while the MFMA before it executes, and a run of them leaves the matrix core idle).
-    //  - wait for this wave's weight of step u; step u + 1's A fragments (stage u + 1, complete
-    //    for every wave since the previous iteration's barrier) go in flight;
-    //  - step u's sixteen MFMAs, with, after the first two: the wait for group u + 2 (this wave's
-    //    DMAs of steps u + 2, u + 3) and the barrier (every wave's have landed, and every wave is
-    //    done reading stages u - 2 and u - 1, which the next DMAs reuse), then group u + 12's four
-    //    DMAs one between each pair of MFMAs;
-    //  - step u + 2's A fragments in flight, step u + 1's sixteen MFMAs with step u + 12's weight
-    //    loads after the first (ring slot 2 k: step u's MFMAs have all issued);
-    //  - step u + 13's weight loads into ring slot 2 k + 1 after the last MFMA that reads it.
+    //  - wait for this wave's weight of step u;
+    //  - step u's sixteen MFMAs (A in fx). Between the first eight go the eight reads of step
+    //    u + 1's A fragments into fy (stage u + 1, complete for every wave since the previous
+    //    iteration's barrier; fy's last reader, step u - 1's block, has issued). After the
+    //    first two: the wait for group u + 2 (this wave's DMAs of steps u + 2, u + 3) and the
+    //    barrier (every wave's have landed, and every wave is done reading stages u - 2 and
+    //    u - 1, which the next DMAs reuse); between MFMAs 8 to 12, group u + 12's four DMAs;
+    //  - step u + 1's sixteen MFMAs (A in fy), with step u + 2's reads into fx between the first
+    //    eight and step u + 12's weight loads after the first (ring slot 2 k: step u's MFMAs
+    //    have all issued); step u + 13's weight loads into slot 2 k + 1 after its last reader.
     // Each wave issues per group: h(u + 12) and h(u + 13) (four DMAs), then the weight of u + 12
     // and of u + 13 (two loads each), in that order, so "at most n vector memory operations
     // outstanding" names a point in that sequence: the weight of step u has landed at 42 (the
@@ -233,6 +224,17 @@ __global__ __launch_bounds__(kRoThreads) void k_readout_tiles(ReadoutP p) {
         uint8_t *st = lds + (t % kRoStages) * kRoStageBytes + (2 * wave + g) * 1024;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(hres, (lds_ptr_t)(st), 16, hoff + g * S * 1024 + t * 1024, 0, 0, 0);
     };
+    // MFMA pair r of a step (A fragment r against both weight fragments), each followed by one
+    // read of the next step's fragments (2 r, then 2 r + 1) into `nx`, pinned in that order.
+#define NT_RO_PAIR_RD(r, fa, bb, nx, sa)                      \
+    mfma1(r, 0, fa[r], bb[0]);                                \
+    __builtin_amdgcn_sched_barrier(0);                        \
+    lds_issue_a1<(2 * (r)) * 1024>(sa, nx[2 * (r)]);          \
+    __builtin_amdgcn_sched_barrier(0);                        \
+    mfma1(r, 1, fa[r], bb[1]);                                \
+    __builtin_amdgcn_sched_barrier(0);                        \
+    lds_issue_a1<(2 * (r) + 1) * 1024>(sa, nx[2 * (r) + 1]);  \
+    __builtin_amdgcn_sched_barrier(0);
     const int NI = S / 2;
     int i0 = 0;
     static_assert(2 + 8 * (kGroupsAhead - 1) + 8 == 42 && 4 + 8 * (kGroupsAhead - 1) == 36, "the waits below");
@@ -243,60 +245,69 @@ __global__ __launch_bounds__(kRoThreads) void k_readout_tiles(ReadoutP p) {
             if (i < NI) {
                 v4u(&b)[2] = br[2 * k];
                 v4u(&c)[2] = br[2 * k + 1];
+                const uint32_t s1 = stage(u + 1), s2 = stage(u + 2);
                 // (each wait is an asm statement that takes the weight registers it covers as
                 // in-out operands: nothing that reads them can be placed before it)
                 asm volatile("s_waitcnt vmcnt(42)" : "+v"(b[0]), "+v"(b[1]) : : "memory");
-                lds_issue_a8(stage(u + 1), fy);
                 __builtin_amdgcn_sched_barrier(0);
-                mfma1(0, 0, fx[0], b[0]);
-                mfma1(0, 1, fx[0], b[1]);
-                __builtin_amdgcn_sched_barrier(0);
+                NT_RO_PAIR_RD(0, fx, b, fy, s1)
                 asm volatile("s_waitcnt vmcnt(36)" : "+v"(c[0]), "+v"(c[1]) : : "memory");
                 asm volatile("s_barrier" ::: "memory");
                 __builtin_amdgcn_sched_barrier(0);
-                mfma1(1, 0, fx[1], b[0]);
+                NT_RO_PAIR_RD(1, fx, b, fy, s1)
+                NT_RO_PAIR_RD(2, fx, b, fy, s1)
+                NT_RO_PAIR_RD(3, fx, b, fy, s1)
+                mfma1(4, 0, fx[4], b[0]);
                 __builtin_amdgcn_sched_barrier(0);
                 dma_half(u + kRoDepth, 0);
                 __builtin_amdgcn_sched_barrier(0);
-                mfma1(1, 1, fx[1], b[1]);
+                mfma1(4, 1, fx[4], b[1]);
                 __builtin_amdgcn_sched_barrier(0);
                 dma_half(u + kRoDepth, 1);
                 __builtin_amdgcn_sched_barrier(0);
-                mfma1(2, 0, fx[2], b[0]);
+                mfma1(5, 0, fx[5], b[0]);
                 __builtin_amdgcn_sched_barrier(0);
                 dma_half(u + kRoDepth + 1, 0);
                 __builtin_amdgcn_sched_barrier(0);
-                mfma1(2, 1, fx[2], b[1]);
+                mfma1(5, 1, fx[5], b[1]);
                 __builtin_amdgcn_sched_barrier(0);
                 dma_half(u + kRoDepth + 1, 1);
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int r = 3; r < 8; r++) {
+                for (int r = 6; r < 8; r++) {
                     mfma1(r, 0, fx[r], b[0]);
                     mfma1(r, 1, fx[r], b[1]);
                 }
                 __builtin_amdgcn_sched_barrier(0);
                 lds_wait_a8(fy);
-                lds_issue_a8(stage(u + 2), fx);
                 __builtin_amdgcn_sched_barrier(0);
                 mfma1(0, 0, fy[0], c[0]);
+                __builtin_amdgcn_sched_barrier(0);
+                lds_issue_a1<0>(s2, fx[0]);
                 __builtin_amdgcn_sched_barrier(0);
                 load_b(u + kRoDepth, b[0], b[1]);
                 __builtin_amdgcn_sched_barrier(0);
                 mfma1(0, 1, fy[0], c[1]);
+                __builtin_amdgcn_sched_barrier(0);
+                lds_issue_a1<1024>(s2, fx[1]);
+                __builtin_amdgcn_sched_barrier(0);
+                NT_RO_PAIR_RD(1, fy, c, fx, s2)
+                NT_RO_PAIR_RD(2, fy, c, fx, s2)
+                NT_RO_PAIR_RD(3, fy, c, fx, s2)
 #pragma unroll
-                for (int r = 1; r < 8; r++) {
+                for (int r = 4; r < 8; r++) {
                     mfma1(r, 0, fy[r], c[0]);
                     mfma1(r, 1, fy[r], c[1]);
                 }
                 __builtin_amdgcn_sched_barrier(0);
-                lds_wait_a8(fx);
                 load_b(u + kRoDepth + 1, c[0], c[1]);
+                lds_wait_a8(fx);
                 asm volatile("" ::: "memory");
             }
         }
         i0 += kRoDepth / 2;
     }
+#undef NT_RO_PAIR_RD
     // Every copy, the ones past the last step included, lands before the stages are reused, and
     // every weight load lands before its registers can be given to anything else: the ring's
     // last loads are never read, so the wait takes the registers as in-out operands (a load into
