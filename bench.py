@@ -88,6 +88,21 @@ def copy_peak(nr, nbytes=1 << 29, reps=10):
     return 2 * nbytes * reps / (ms.value * 1e-3) / 1e9
 
 
+def clock_warmup(nr, step, seconds):
+    """Run `step(i)` untimed for about `seconds` of wall time (synchronising every 64 calls), so
+    that the timed windows that follow see the device's steady clocks: MI355X raises its shader
+    clock over the first tenths of a second of sustained work (a kernel measured 343 us at the
+    start of a run and 260-275 us after one second of it)."""
+    t0 = time.perf_counter()
+    i = 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(64):
+            step(i)
+            i += 1
+        nr.sync()
+    return time.perf_counter() - t0
+
+
 def timed(nr, steps, warmup, step):
     """Average milliseconds of `step(i)` over `steps` calls after `warmup` untimed ones, from HIP
     events on the library's stream (where every kernel runs), plus the wall seconds."""
@@ -299,6 +314,7 @@ def bench_sample(nr, W, args, name):
     cold = argv_for(lambda i: ws[i % copies])
     warm = argv_for(lambda i: w)
     nr._check(L.nt_hip_rl_sample(C.byref(cold[0])), "sample")
+    warm_s = clock_warmup(nr, lambda i: L.nt_hip_rl_sample(C.byref(cold[i % len(cold)])), args.clock_warmup)
     ms, wall = timed(nr, args.steps, args.warmup, lambda i: L.nt_hip_rl_sample(C.byref(cold[i])))
     st = status.to_numpy()
     if np.any(st != 0):
@@ -339,7 +355,8 @@ def bench_sample(nr, W, args, name):
                   "parallelism": "none (1 GPU)"}
     out = line(metric, rows / (ms * 1e-3), args.steps, args.warmup, ms, "bf16" if esz == 2 else "f32", config, roof,
                achieved_gbs=roof["achieved"], wall_s_timed_region=wall, key=nr.key(),
-               ms_per_step_repeats=repeats, ms_per_step_median_of_repeats=float(np.median(repeats)))
+               ms_per_step_repeats=repeats, ms_per_step_median_of_repeats=float(np.median(repeats)),
+               clock_warmup_s=round(warm_s, 3))
     if args.cpu_rows > 0:
         n_cpu = min(args.cpu_rows, rows)
         gpu = tuple(a[:n_cpu] for a in gpu_out)
@@ -687,6 +704,7 @@ def bench_readout(nr, W, args):
 
     steps, warmup = args.steps, args.warmup
     fused(0)
+    warm_s = clock_warmup(nr, fused, args.clock_warmup)
     ms, wall = timed(nr, steps, warmup, fused)
     if np.any(st2.to_numpy() != 0):
         raise RuntimeError("readout: refused rows")
@@ -732,7 +750,7 @@ def bench_readout(nr, W, args):
                         "note": "the unfused GEMM writes bf16 logits (hipBLASLt's output for bf16 operands); the "
                                 "fused product keeps them in f32"},
             "weight_transpose_once_s": round(transpose_s, 4), "weight_pack_once_s": round(pack_s, 4),
-            "key": nr.key()}
+            "clock_warmup_s": round(warm_s, 3), "key": nr.key()}
 
 
 def main():
@@ -746,6 +764,8 @@ def main():
     ap.add_argument("--kernels", default="aot", choices=["aot", "rtc"],
                     help="how the sampler kernels are loaded: the library's hipcc code objects (the default) "
                          "or hiprtc at first use (compiled in the warmup)")
+    ap.add_argument("--clock-warmup", type=float, default=1.0,
+                    help="seconds of untimed launches before the warmup steps (the device's clocks settle)")
     ap.add_argument("--cpu-rows", type=int, default=256, help="rows of the CPU baseline sample (0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="repeat the CPU sample up to this long")
     ap.add_argument("--copy-bytes", type=int, default=0,
