@@ -31,6 +31,7 @@
 #include <cmath>
 #include <cstdint>
 #include <string>
+#include <type_traits>
 
 #include "../../include/noetic_hip.h"
 #include "nt_internal.hpp"
@@ -468,54 +469,36 @@ struct ResolveP {
 };
 
 constexpr int kResThreads = 256;
-constexpr int kResMaxBlocks = 32;  // blocks of 32 columns per thread: V <= 262144
+constexpr int kResMaxBlocks = 32;  // blocks of 32 columns per thread: V <= 262144 (16: V <= 131072)
 constexpr int kResMaxTiles = 4;    // tiles of 256 columns per thread
 constexpr int kResMaxK = 16384;    // dim at most: the row of h is held in LDS (32 KiB)
-constexpr int kResPhase = 32;      // k-steps per phase of the weight ring (32 KiB)
-constexpr int kResSlots = 3;       // phases in the ring: two in flight while wave 0 uses one
+constexpr int kResRing = 48;       // the block's weight fragments in flight in wave 0's registers
+constexpr int kResAGroup = 4;      // k-steps of h read from LDS per statement
+// (an even number of groups per pass of the ring: the two read buffers alternate across passes)
+static_assert(kResRing % (2 * kResAGroup) == 0 && kResRing < 64, "the ring's passes and waits");
 
-// Wait until at most n (0 .. 8) vector memory operations of this wave are outstanding.
-__device__ __forceinline__ void wait_vmcnt_upto8(int n) {
-    switch (n) {
-        case 0: wait_vmcnt<0>(); break;
-        case 1: wait_vmcnt<1>(); break;
-        case 2: wait_vmcnt<2>(); break;
-        case 3: wait_vmcnt<3>(); break;
-        case 4: wait_vmcnt<4>(); break;
-        case 5: wait_vmcnt<5>(); break;
-        case 6: wait_vmcnt<6>(); break;
-        case 7: wait_vmcnt<7>(); break;
-        default: wait_vmcnt<8>(); break;
-    }
+// One k-step's weight fragment (16 bytes of lane l at `off`) into `d`, issued only: `d` is in
+// flight until the wait that takes it as an in-out operand.
+__device__ __forceinline__ void load_frag(v4u &d, uint32_t off, const v4u &rs) {
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=&v"(d) : "v"(off), "s"(rs) : "memory");
 }
 
-// The operands of four consecutive k-steps (A: the row of h, 32 bytes a step apart in LDS;
-// B: the block's fragments, 1 KiB apart) and the wait for them (see lds_read_frags).
-__device__ __forceinline__ void lds_read4(uint32_t a, uint32_t b, v4u (&fa)[4], v4u (&fb)[4]) {
+// The A operands of kResAGroup consecutive k-steps (this row of h, 32 bytes a step apart in
+// LDS), issued only; lds_wait_group waits for them.
+__device__ __forceinline__ void lds_issue_group(uint32_t a, v4u (&fa)[kResAGroup]) {
+    static_assert(kResAGroup == 4, "four reads");
     asm volatile(
-        "ds_read_b128 %0, %8\n\t"
-        "ds_read_b128 %1, %8 offset:32\n\t"
-        "ds_read_b128 %2, %8 offset:64\n\t"
-        "ds_read_b128 %3, %8 offset:96\n\t"
-        "ds_read_b128 %4, %9\n\t"
-        "ds_read_b128 %5, %9 offset:1024\n\t"
-        "ds_read_b128 %6, %9 offset:2048\n\t"
-        "ds_read_b128 %7, %9 offset:3072\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(fa[0]), "=&v"(fa[1]), "=&v"(fa[2]), "=&v"(fa[3]), "=&v"(fb[0]), "=&v"(fb[1]), "=&v"(fb[2]), "=&v"(fb[3])
-        : "v"(a), "v"(b)
+        "ds_read_b128 %0, %4\n\t"
+        "ds_read_b128 %1, %4 offset:32\n\t"
+        "ds_read_b128 %2, %4 offset:64\n\t"
+        "ds_read_b128 %3, %4 offset:96"
+        : "=&v"(fa[0]), "=&v"(fa[1]), "=&v"(fa[2]), "=&v"(fa[3])
+        : "v"(a)
         : "memory");
 }
 
-// One k-step's operands (A: this row of h; B: the block's fragment) and the wait for them.
-__device__ __forceinline__ void lds_read1(uint32_t a, uint32_t b, v4u &fa, v4u &fb) {
-    asm volatile(
-        "ds_read_b128 %0, %2\n\t"
-        "ds_read_b128 %1, %3\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(fa), "=&v"(fb)
-        : "v"(a), "v"(b)
-        : "memory");
+__device__ __forceinline__ void lds_wait_group(v4u (&fa)[kResAGroup]) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fa[0]), "+v"(fa[1]), "+v"(fa[2]), "+v"(fa[3]) : : "memory");
 }
 
 // Inclusive prefix sum over the 64 lanes in f64 by a fixed sequence of shuffles.
@@ -528,90 +511,141 @@ __device__ __forceinline__ double wave_incl_scan(double v, int lane) {
     return v;
 }
 
+// Pass 2, one workgroup per row:
+//  - the row's records come in by coalesced loads (thread t takes elements t, t + 256, ...) and
+//    through LDS to each thread's run of consecutive blocks; the row of h is copied into LDS and
+//    the row's uniform loaded at the start, so that their latency hides under the records';
+//  - the maximum over the tiles, the blocks' weights relative to it in f64 in index order (each
+//    thread its run, a wave scan, the waves in order), the block holding u S (four barriers);
+//  - wave 0 alone recomputes that block's 32 logits: the same MFMA over the same k order from
+//    zero, so that they equal pass 1's bit for bit. The block's weight fragments (1 KiB a k-step,
+//    256 KiB at C4's dim) stream into a ring of kResRing registers, loaded kResRing steps ahead of
+//    their MFMA, and h's steps come from LDS four at a time, the next four in flight. Each MFMA
+//    waits for the one before it (a dependent chain of K/16), so nothing else waits: no barrier
+//    stands between the copies and the chain.
+// Block b's sum sits at s_bs[b + b / 16] in LDS: a thread's run of 16 (or 32) consecutive blocks
+// then starts 17 (34) words after the previous thread's, so a wave's reads of it spread over the
+// banks.
+__device__ __forceinline__ int bs_slot(int b) { return b + (b >> 4); }
+
+template <int MAXB>
 __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
     __shared__ double wsum[kResThreads / 64];
     __shared__ float wmax[kResThreads / 64];
     __shared__ int wsel[kResThreads / 64];
+    __shared__ int wlast[kResThreads / 64];
     __shared__ int s_blk;
+    __shared__ float s_ref;
     __shared__ double s_tl;
+    __shared__ __attribute__((aligned(16))) float s_bs[MAXB * kResThreads * 17 / 16];  // the row's block sums
+    __shared__ float s_tr[kResMaxTiles * kResThreads];                                 // its tile references
     __shared__ __attribute__((aligned(16))) uint8_t hrow[kResMaxK * 2];
-    __shared__ __attribute__((aligned(16))) uint8_t ring[kResSlots * kResPhase * 1024];
     const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *tref = p.tref + int64_t(row) * p.ntile;
     const float *tmax = p.tmax + int64_t(row) * p.ntile;
     const int *tfirst = p.tfirst + int64_t(row) * p.ntile;
     const float *bsum = p.bsum + int64_t(row) * p.nblk;
+    // The row of h into LDS (1 KiB pieces, piece c by wave c % 4): whichever block the records
+    // pick, the recomputation needs it.
+    const __amdgpu_buffer_rsrc_t hres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t *>(p.h + int64_t(row) * p.ldh), short(0), p.K * 2, kBufferWord3);
+    for (int c = wave; c * 1024 < p.K * 2; c += 4)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(hres, (lds_ptr_t)(hrow + c * 1024), 16, c * 1024 + lane * 16, 0, 0,
+                                                 0);
+    const double u_row = p.greedy ? 0.0 : p.u[row];
+    // The records, coalesced. (Every load reads a valid index and the unused ones are masked
+    // after: a load under a condition becomes a branch of its own, with its wait before the next.)
+    float tm[kResMaxTiles], tr[kResMaxTiles], bv[MAXB];
+#pragma unroll
+    for (int i = 0; i < kResMaxTiles; i++) {
+        const int t = tid + i * kResThreads, tc = min(t, p.ntile - 1);
+        const float vm = tmax[tc], vr = tref[tc];
+        tm[i] = t < p.ntile ? vm : -INFINITY;
+        tr[i] = vr;
+    }
+    const int nb_rounds = (p.nblk + kResThreads - 1) / kResThreads;  // at most MAXB
+#pragma unroll
+    for (int i = 0; i < MAXB; i++) {
+        if (i < nb_rounds) bv[i] = bsum[min(tid + i * kResThreads, p.nblk - 1)];
+    }
+#pragma unroll
+    for (int i = 0; i < kResMaxTiles; i++) s_tr[tid + i * kResThreads] = tr[i];
+#pragma unroll
+    for (int i = 0; i < MAXB; i++)
+        if (i < nb_rounds) s_bs[bs_slot(tid + i * kResThreads)] = bv[i];
+    // (a wave that leaves early first lets its copies into LDS land: the LDS is the workgroup's
+    // until its last wave ends; the loads above were issued after them and have landed, so they
+    // have too)
     auto refuse = [&](uint8_t st) {
+        wait_vmcnt<0>();
         if (tid == 0) {
             p.ids[row] = -1;
             if (p.logp) p.logp[row] = NAN;
             p.status[row] = st;
         }
     };
-    // every load of the row's records first (one round trip): the tiles' maxima, then this
-    // thread's contiguous run of blocks and their tiles' references
-    float tm[kResMaxTiles];
-#pragma unroll
-    for (int i = 0; i < kResMaxTiles; i++) {
-        const int t = tid + i * kResThreads;
-        tm[i] = t < p.ntile ? tmax[t] : -INFINITY;
-    }
-    const int per = (p.nblk + kResThreads - 1) / kResThreads;  // at most kResMaxBlocks
-    const int b0 = tid * per, b1 = min(p.nblk, b0 + per);
-    float bs[kResMaxBlocks], br[kResMaxBlocks];
-#pragma unroll
-    for (int i = 0; i < kResMaxBlocks; i++) {
-        const int b = b0 + i;
-        const bool in = i < per && b < b1;
-        bs[i] = in ? bsum[b] : 0.0f;
-        br[i] = in ? tref[b / (kRoCols / kRoBlock)] : -INFINITY;
-    }
     // ---- the row's maximum over the tiles (exact; the order does not matter for a maximum)
     static_assert(kResMaxTiles == 4, "the maximum over the thread's tiles");
     float m = fmaxf(fmaxf(tm[0], tm[1]), fmaxf(tm[2], tm[3]));
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
     if (lane == 0) wmax[wave] = m;
-    __syncthreads();
+    __syncthreads();  // (1) the maximum's parts, the block sums and references in LDS
     const float M = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
     if (M == -INFINITY) {
         refuse(NT_ROW_NO_TOKEN);
         return;
     }
     const float A = M * p.c;
-    // ---- block weights relative to A, f64 in index order
-    double wbk[kResMaxBlocks];
+    // ---- block weights relative to A, f64 in index order: this thread's run b0 .. b1 - 1
+    const int per = nb_rounds;
+    const int b0 = tid * per, b1 = min(p.nblk, b0 + per);
+    // (a run of at most 32 blocks spans at most five tiles of 8: their factors 2^(ref - A) once each)
+    double wbk[MAXB];
     double run = 0.0;
+    const int t0 = b0 / (kRoCols / kRoBlock);
+    double tf[MAXB / 8 + 1];
 #pragma unroll
-    for (int i = 0; i < kResMaxBlocks; i++) {
-        const double f = br[i] == -INFINITY ? 0.0 : double(__builtin_amdgcn_exp2f(br[i] - A));
-        wbk[i] = f * double(bs[i]);
-        run += wbk[i];
+    for (int j = 0; j <= MAXB / 8; j++) {
+        const float r = s_tr[min(t0 + j, kResMaxTiles * kResThreads - 1)];
+        tf[j] = r == -INFINITY ? 0.0 : double(__builtin_amdgcn_exp2f(r - A));
+    }
+#pragma unroll
+    for (int i = 0; i < MAXB; i++) {
+        const int b = b0 + i;
+        double wb = 0.0;
+        if (i < per && b < b1) {
+            double f = tf[0];
+#pragma unroll
+            for (int j = 1; j <= MAXB / 8; j++)
+                if (b / (kRoCols / kRoBlock) - t0 == j) f = tf[j];
+            wb = f * double(s_bs[bs_slot(b)]);
+        }
+        wbk[i] = wb;
+        run += wb;
     }
     const double incl_w = wave_incl_scan(run, lane);
     if (lane == 63) wsum[wave] = incl_w;
-    __syncthreads();
+    __syncthreads();  // (2) the waves' totals
     double before = 0.0;
     for (int w2 = 0; w2 < wave; w2++) before += wsum[w2];
     const double incl = before + incl_w, excl = incl - run;
     // the row's sum: the last thread's inclusive prefix (the same additions in the same order)
-    __shared__ double s_tot;
-    if (tid == kResThreads - 1) s_tot = incl;
-    __syncthreads();
-    const double Sall = s_tot;
+    const double Sall = (((0.0 + wsum[0]) + wsum[1]) + wsum[2]) + wsum[3];
     if (!(Sall == Sall)) {
         refuse(NT_ROW_NAN);
         return;
     }
     const double shiftA = double(A) - double(M) * double(p.c);
-    const double lnS = log(Sall) + shiftA * kLn2;
     if (p.greedy) {
+        wait_vmcnt<0>();
+        const double lnS = log(Sall) + shiftA * kLn2;
         // the first column holding the maximum: the first tile whose maximum it is
         int best = 0x7fffffff;
 #pragma unroll
         for (int i = 0; i < kResMaxTiles; i++) {
             const int t = tid + i * kResThreads;
-            if (t < p.ntile && tmax[t] == M) best = min(best, tfirst[t]);
+            if (t < p.ntile && tm[i] == M) best = min(best, tfirst[t]);
         }
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) best = min(best, __shfl_xor(best, o, 64));
@@ -627,26 +661,24 @@ __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
     }
     // ---- the block holding t = u S: the first thread whose inclusive prefix passes t (with
     // weight), then its blocks in order; rounding that leaves no crossing takes the last weight
-    const double t = p.u[row] * Sall;
+    const double t = u_row * Sall;
     {
         const uint64_t cross = __ballot(incl > t && run > 0.0);
         const uint64_t any = __ballot(run > 0.0);
         if (lane == 0) wsel[wave] = cross ? wave * 64 + __builtin_ctzll(cross) : -1;
-        __shared__ int wlast[kResThreads / 64];
         if (lane == 0) wlast[wave] = any ? wave * 64 + 63 - __builtin_clzll(any) : -1;
-        __syncthreads();
+        __syncthreads();  // (3) the waves' crossings
         int sel = -1;
         for (int w2 = 0; w2 < 4 && sel < 0; w2++) sel = wsel[w2];
         if (sel < 0)
             for (int w2 = 3; w2 >= 0 && sel < 0; w2--) sel = wlast[w2];
         if (tid == 0) s_blk = -1;
-        __syncthreads();
         if (tid == sel) {
             double acc = excl;
             int bstar = -1, blast = -1;
             double bexcl = 0.0, lexcl = 0.0;
 #pragma unroll
-            for (int i = 0; i < kResMaxBlocks; i++) {
+            for (int i = 0; i < MAXB; i++) {
                 const double wb = wbk[i];
                 if (wb > 0.0) {
                     blast = b0 + i;
@@ -662,98 +694,93 @@ __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
                 bstar = blast;
                 bexcl = lexcl;
             }
-            const float r = tref[bstar / (kRoCols / kRoBlock)];
+            const float r = s_tr[bstar / (kRoCols / kRoBlock)];
             s_blk = bstar;
+            s_ref = r;
             // the target inside the block, in the scale of its tile's reference
             s_tl = (t - bexcl) * double(__builtin_amdgcn_exp2f(A - r));
         }
-        __syncthreads();
+        __syncthreads();  // (4) the block
     }
     const int bstar = s_blk;
     if (bstar < 0) {
         refuse(NT_ROW_NAN);
         return;
     }
+    if (wave != 0) return;  // (their copies of h landed before barrier 1)
     const double tl = s_tl;
-    // ---- recompute the block's 32 logits: the same MFMA over the same k order from zero. Every
-    // lane's A row is this row (so every output row holds it); lane l's B column is 32 b + l % 32.
-    // The row of h goes into LDS once (1 KiB pieces, piece c by wave c % 4); the block's weight
-    // fragments (1 KiB a k-step) stream through a ring of three 32-step phases, two in flight,
-    // each wave copying every fourth step; wave 0 runs the MFMA chain from LDS.
+    const float r = s_ref;
+    // ---- wave 0: recompute the block's 32 logits. Every lane's A row is this row (so every
+    // output row holds it); lane l's B column is 32 b + l % 32.
     const int fr = lane & 31;
     const int col = bstar * kRoBlock + fr;
     const bool colok = col < p.V;
     const int S2 = p.K / 16;
-    const int NP = (S2 + kResPhase - 1) / kResPhase;
     const int bt = bstar / 8, bg = bstar % 8;  // the block's tile and column group within it
-    const __amdgpu_buffer_rsrc_t hres = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t *>(p.h + int64_t(row) * p.ldh), short(0), p.K * 2, kBufferWord3);
-    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t *>(p.wp + (int64_t(bt) * S2 * 8 + bg) * 1024), short(0), (S2 - 1) * 8192 + 1024,
-        kBufferWord3);
-    for (int c = wave; c * 1024 < p.K * 2; c += 4)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(hres, (lds_ptr_t)(hrow + c * 1024), 16, c * 1024 + lane * 16, 0, 0,
-                                                 0);
-    const uint32_t rbase = uint32_t((uintptr_t)(lds_ptr_t)(ring)) + lane * 16;
-    const uint32_t hbase = uint32_t((uintptr_t)(lds_ptr_t)(hrow)) + (lane >> 5) * 16;
-    auto issue_phase = [&](int q) {
-        uint8_t *slot = ring + (q % kResSlots) * kResPhase * 1024;
-        for (int i = wave; i < kResPhase; i += 4) {
-            const int st = q * kResPhase + i;
-            if (st < S2)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, (lds_ptr_t)(slot + i * 1024), 16, lane * 16 + st * 8192,
-                                                         0, 0, 0);
-        }
-    };
-    // the DMAs this wave issues for phase q: one per step i = wave, wave + 4, ... below S2
-    auto own_dmas = [&](int q) {
-        int n = 0;
-        for (int i = wave; i < kResPhase; i += 4) n += q * kResPhase + i < S2 ? 1 : 0;
-        return n;
-    };
-    issue_phase(0);
-    if (NP > 1) issue_phase(1);
+    // the mask byte of this lane's column, loaded before the ring (so that it has landed whenever
+    // the ring's oldest load has)
+    bool keep = lane < 32 && colok;
+    if (keep && p.mask) keep = p.mask[int64_t(row) * p.mask_ld + col] != 0;
+    // the block's fragments: step s at (s 8 + 0) KiB from the block's first (tile-major order)
+    const uint64_t wbase = reinterpret_cast<uint64_t>(p.wp + (int64_t(bt) * S2 * 8 + bg) * 1024);
+    const v4u wrs = {uint32_t(wbase), uint32_t(wbase >> 32), uint32_t((S2 - 1) * 8192 + 1024), uint32_t(kBufferWord3)};
+    const uint32_t woff = uint32_t(lane) * 16;
+    v4u ring[kResRing];
+#pragma unroll
+    for (int j = 0; j < kResRing; j++) load_frag(ring[j], woff + uint32_t(j) * 8192, wrs);  // past the block: zeros
+    // ln S (for the log-probability at the end), while the first loads are in flight
+    const double lnS = log(Sall) + shiftA * kLn2;
     f32x16_t acc;
 #pragma unroll
     for (int v = 0; v < 16; v++) acc[v] = 0.0f;
-    for (int q = 0; q < NP; q++) {
-        // this wave's DMAs of phase q (and, before them, of h) have landed when at most those it
-        // issued for phase q + 1 remain; after the barrier every wave's have, and every wave is
-        // past phase q - 1, whose slot phase q + 2 then reuses
-        wait_vmcnt_upto8(q + 1 < NP ? own_dmas(q + 1) : 0);
-        asm volatile("s_barrier" ::: "memory");
-        if (q + 2 < NP) issue_phase(q + 2);
-        if (wave == 0) {
-            // the MFMAs are the compiler's (it places the wait states their results need); the
-            // operands of four steps at a time come in by one read statement
-            const int n = min(kResPhase, S2 - q * kResPhase);
-            const uint32_t ab = hbase + q * kResPhase * 32, bb = rbase + (q % kResSlots) * kResPhase * 1024;
-            int i = 0;
-            for (; i + 4 <= n; i += 4) {
-                v4u fa[4], fb[4];
-                lds_read4(ab + i * 32, bb + i * 1024, fa, fb);
+    const uint32_t hbase = uint32_t((uintptr_t)(lds_ptr_t)(hrow)) + (lane >> 5) * 16;
+    const uint32_t hlim = uint32_t((uintptr_t)(lds_ptr_t)(hrow)) + kResMaxK * 2;  // reads stay in hrow
+    v4u fa0[kResAGroup], fa1[kResAGroup];
 #pragma unroll
-                for (int j = 0; j < 4; j++)
-                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, fa[j]),
-                                                                  __builtin_bit_cast(bf16x8_t, fb[j]), acc, 0, 0, 0);
-            }
-            for (; i < n; i++) {
-                v4u fa, fb;
-                lds_read1(ab + i * 32, bb + i * 1024, fa, fb);
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, fa),
-                                                              __builtin_bit_cast(bf16x8_t, fb), acc, 0, 0, 0);
+    for (int j = 0; j < kResAGroup; j++) fa0[j] = fa1[j] = v4u{0, 0, 0, 0};
+    auto issue_a = [&](int s0, v4u(&fa)[kResAGroup]) {
+        const uint32_t a = hbase + uint32_t(s0) * 32;
+        if (s0 < S2 && a + kResAGroup * 32 <= hlim) lds_issue_group(a, fa);
+    };
+    // one pass of the ring from step `base`; PARTIAL: the last, with steps past S2 (their MFMAs
+    // skipped, their waits and loads kept so that every slot's load is waited for)
+    auto pass = [&](int base, auto partial_c) {
+        constexpr bool PARTIAL = decltype(partial_c)::value;
+#pragma unroll
+        for (int g = 0; g < kResRing / kResAGroup; g++) {
+            v4u(&cur)[kResAGroup] = (g & 1) ? fa1 : fa0;
+            v4u(&nxt)[kResAGroup] = (g & 1) ? fa0 : fa1;
+            lds_wait_group(cur);
+            issue_a(base + (g + 1) * kResAGroup, nxt);
+#pragma unroll
+            for (int j = 0; j < kResAGroup; j++) {
+                const int k = g * kResAGroup + j, st = base + k;
+                // the ring's oldest load (step st) has landed when kResRing - 1 remain
+                asm volatile("s_waitcnt vmcnt(47)" : "+v"(ring[k]) : : "memory");
+                static_assert(kResRing - 1 == 47, "the wait above");
+                if (!PARTIAL || st < S2)
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, cur[j]),
+                                                                  __builtin_bit_cast(bf16x8_t, ring[k]), acc, 0, 0, 0);
+                load_frag(ring[k], woff + uint32_t(st + kResRing) * 8192, wrs);
             }
         }
-    }
-    if (wave != 0) return;
+    };
+    issue_a(0, fa0);
+    int base = 0;
+    for (; base + kResRing <= S2; base += kResRing) pass(base, std::false_type{});
+    if (base < S2) pass(base, std::true_type{});
+    // every load lands before its register is given to anything else (the ring's last loads are
+    // never read): the wait, then each register taken as an in-out operand after it
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(ring[0]) : : "memory");
+#pragma unroll
+    for (int j = 1; j < kResRing; j++) asm volatile("" : "+v"(ring[j]) : : "memory");
+    lds_wait_group(fa0);
+    lds_wait_group(fa1);
     // lane l (< 32) holds column 32 b + l (output row 0, every row being this row)
     float x = acc[0];
     if (p.dbg_block && lane < 32) p.dbg_block[int64_t(row) * 32 + lane] = x;
     if (p.dbg_index && lane == 0) p.dbg_index[row] = bstar;
-    bool keep = lane < 32 && colok;
-    if (keep && p.mask) keep = p.mask[int64_t(row) * p.mask_ld + col] != 0;
     x = keep ? x : -INFINITY;
-    const float r = p.tref[int64_t(row) * p.ntile + bstar / (kRoCols / kRoBlock)];
     const float w = keep ? __builtin_amdgcn_exp2f(fmaf(x, p.c, -r)) : 0.0f;
     const double cw = wave_incl_scan(double(w), lane);
     int lsel = -1;
@@ -950,7 +977,10 @@ extern "C" int nt_hip_rl_readout_sample(const NtRlReadoutSampleArgs *a) {
     q.status = a->status;
     q.dbg_block = a->debug_block;
     q.dbg_index = a->debug_block_index;
-    hipLaunchKernelGGL(k_readout_resolve, dim3(unsigned(rows)), dim3(kResThreads), 0, st, q);
+    if (nblk <= 16 * kResThreads)
+        hipLaunchKernelGGL(k_readout_resolve<16>, dim3(unsigned(rows)), dim3(kResThreads), 0, st, q);
+    else
+        hipLaunchKernelGGL(k_readout_resolve<kResMaxBlocks>, dim3(unsigned(rows)), dim3(kResThreads), 0, st, q);
     if (int rc = launched(who)) return rc;
     return scratch_release(ws);
 }
