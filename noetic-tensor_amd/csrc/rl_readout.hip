@@ -85,7 +85,7 @@ struct ReadoutP {
     float *logits;       // [rows][V] debug copy or null
 };
 
-// Eight reads of 16 bytes: the A fragments of the eight row groups (1 KiB apart), and the wait
+// Eight reads of 16 bytes: h's fragments of the eight row groups (1 KiB apart), and the wait
 // for them, in one statement: the data came from LDS DMA, which the compiler's own wait insertion
 // would treat as outstanding vector memory (a wait for every load in flight).
 __device__ __forceinline__ void lds_read_a8(uint32_t a, v4u (&fa)[8]) {
@@ -104,7 +104,7 @@ __device__ __forceinline__ void lds_read_a8(uint32_t a, v4u (&fa)[8]) {
         : "memory");
 }
 
-// One A fragment of a later k-step (OFF bytes past `a` in LDS) into `na`, issued only: the
+// One h fragment of a later k-step (OFF bytes past `a` in LDS) into `na`, issued only: the
 // register is in flight until lds_wait_a8 below, and nothing may read it before it.
 template <int OFF>
 __device__ __forceinline__ void lds_issue_a1(uint32_t a, v4u &na) {
@@ -121,7 +121,9 @@ __device__ __forceinline__ void lds_wait_a8(v4u (&na)[8]) {
                  : "memory");
 }
 
-template <bool MASK, bool DBG>
+// FIRST: the tile records carry each row's first column of the maximum (the greedy draw's
+// answer); the sampler otherwise needs only the maximum.
+template <bool MASK, bool DBG, bool FIRST>
 __global__ __launch_bounds__(kRoThreads) void k_readout_tiles(ReadoutP p) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[kRoStages * kRoStageBytes];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -136,10 +138,9 @@ __global__ __launch_bounds__(kRoThreads) void k_readout_tiles(ReadoutP p) {
     const __amdgpu_buffer_rsrc_t hres = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t *>(p.hp), short(0), hgroups * S * 1024, kBufferWord3);
     const uint32_t lbase = uint32_t((uintptr_t)(lds_ptr_t)(lds)) + lane * 16;
-    const int fr = lane & 31;
-    // Step t's operands. h (A, shared by the waves) through LDS: this wave copies row groups
+    // Step t's operands. h (shared by the waves) through LDS: this wave copies row groups
     // 2 wave, 2 wave + 1 of it by DMA into stage t % kRoStages (lane l's 16 bytes at 16 l of the
-    // fragment's slot). The weight (B, this wave's own two column groups) straight into registers.
+    // fragment's slot). The weight (this wave's own two column groups) straight into registers.
     const int hoff = 2 * wave * S * 1024 + lane * 16, woff = 2 * wave * 1024 + lane * 16;
     // the weight's resource as four scalar words for the loads below (base, stride 0, size, flags)
     const uint64_t wbase = reinterpret_cast<uint64_t>(p.wp + int64_t(tile) * S * 8192);
@@ -185,7 +186,7 @@ __global__ __launch_bounds__(kRoThreads) void k_readout_tiles(ReadoutP p) {
         load_b(u + 1, br[u + 1][0], br[u + 1][1]);
         asm volatile("" ::: "memory");
     }
-    v4u fx[8], fy[8];  // even steps' A fragments, odd steps'
+    v4u fx[8], fy[8];  // even steps' h fragments, odd steps'
     constexpr int kGroupsAhead = kRoDepth / 2 - 1;  // groups issued after the one awaited
     static_assert(4 + 8 * kGroupsAhead == 44, "the wait below");
     asm volatile("s_waitcnt vmcnt(44)" ::: "memory");  // group 0's DMAs
@@ -197,22 +198,24 @@ __global__ __launch_bounds__(kRoThreads) void k_readout_tiles(ReadoutP p) {
     // work by placing it between the MFMAs (one wave per SIMD: an instruction that is not an MFMA
     // runs while the MFMA before it executes, and a run of them leaves the matrix core idle).
     //  - wait for this wave's weight of step u;
-    //  - step u's sixteen MFMAs (A in fx). Between the first eight go the eight reads of step
-    //    u + 1's A fragments into fy (stage u + 1, complete for every wave since the previous
+    //  - step u's sixteen MFMAs (h in fx). Between the first eight go the eight reads of step
+    //    u + 1's h fragments into fy (stage u + 1, complete for every wave since the previous
     //    iteration's barrier; fy's last reader, step u - 1's block, has issued). After the
     //    first two: the wait for group u + 2 (this wave's DMAs of steps u + 2, u + 3) and the
     //    barrier (every wave's have landed, and every wave is done reading stages u - 2 and
     //    u - 1, which the next DMAs reuse); between MFMAs 8 to 12, group u + 12's four DMAs;
-    //  - step u + 1's sixteen MFMAs (A in fy), with step u + 2's reads into fx between the first
+    //  - step u + 1's sixteen MFMAs (h in fy), with step u + 2's reads into fx between the first
     //    eight and step u + 12's weight loads after the first (ring slot 2 k: step u's MFMAs
     //    have all issued); step u + 13's weight loads into slot 2 k + 1 after its last reader.
     // Each wave issues per group: h(u + 12) and h(u + 13) (four DMAs), then the weight of u + 12
     // and of u + 13 (two loads each), in that order, so "at most n vector memory operations
     // outstanding" names a point in that sequence: the weight of step u has landed at 42 (the
     // weight of u + 1 and five later groups after it), group u + 2's DMAs at 36.
+    // (the weight is the A operand and h the B one: tile (i, j) of the output is the transposed
+    // [32 columns][32 rows] block, so that a lane's accumulators hold one row; see the epilogue)
     auto mfma1 = [&](int i, int j, const v4u &a, const v4u &b) {
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                            __builtin_bit_cast(bf16x8_t, b), acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, b),
+                                                            __builtin_bit_cast(bf16x8_t, a), acc[i][j], 0, 0, 0);
     };
     auto mfmas = [&](const v4u(&fa)[8], const v4u &b0, const v4u &b1) {
 #pragma unroll
@@ -225,7 +228,7 @@ __global__ __launch_bounds__(kRoThreads) void k_readout_tiles(ReadoutP p) {
         uint8_t *st = lds + (t % kRoStages) * kRoStageBytes + (2 * wave + g) * 1024;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(hres, (lds_ptr_t)(st), 16, hoff + g * S * 1024 + t * 1024, 0, 0, 0);
     };
-    // MFMA pair r of a step (A fragment r against both weight fragments), each followed by one
+    // MFMA pair r of a step (h fragment r against both weight fragments), each followed by one
     // read of the next step's fragments (2 r, then 2 r + 1) into `nx`, pinned in that order.
 #define NT_RO_PAIR_RD(r, fa, bb, nx, sa)                      \
     mfma1(r, 0, fa[r], bb[0]);                                \
@@ -324,6 +327,39 @@ __global__ __launch_bounds__(kRoThreads) void k_readout_tiles(ReadoutP p) {
                  :
                  : "memory");
     static_assert(kRoDepth == 12, "the drain above names every ring slot");
+    // ---- epilogue, in the MFMA output's own layout. The product is the transposed block, so lane
+    // l of wave w holds in acc[i][j][4 a + b] row r = 32 i + l % 32 at tile column
+    // 64 w + 32 j + 8 a + 4 (l / 32) + b (j < 2, a < 4, b < 4): 32 of the row's 64 columns of this
+    // wave, the partner lane l ^ 32 the other 32. Per row group i each lane takes its row's
+    // maximum and first column over its 32 (in column order) and the partner's; the four waves'
+    // go through LDS (one barrier), then each lane weighs its 32 against the tile's reference and
+    // sums each 32-column block with the partner's half.
+    const int rw = lane & 31, hh = lane >> 5;
+    const int cw0 = n0 + 64 * wave + 4 * hh;  // column of acc[i][0][0]; + 32 j + 8 a + b
+    // The tile's mask (256 rows x 256 bytes) comes into LDS by coalesced 1 KiB copies, four rows
+    // each, over the stages (every wave is past its last read of them after the barrier). Row r's
+    // sixteen 16-byte chunks sit rotated by r (chunk k at position (k + r) % 16), so that the 32
+    // lanes of a half, reading one column of 32 consecutive rows, spread over the banks. Rows past
+    // the last and bytes past the mask read as zeros (the buffer's range); columns past the
+    // vocabulary are excluded below. Rows that are not 16-byte aligned take byte loads instead.
+    // The last odd step's MFMAs run while the copies are in flight.
+    uint8_t *const lmask = lds;                                           // [256 rows][256 bytes]
+    float *const Sm = reinterpret_cast<float *>(lds + kRoRows * kRoCols);  // [4 waves][256 rows] maxima
+    int *const Sf = reinterpret_cast<int *>(Sm + 4 * kRoRows);            // [4 waves][256 rows] first columns
+    static_assert(kRoRows * kRoCols + 8 * kRoRows * 4 <= kRoStages * kRoStageBytes, "the mask and the exchange fit");
+    const bool mdma = MASK && p.mask_vec;
+    asm volatile("s_barrier" ::: "memory");
+    if (mdma) {
+        const __amdgpu_buffer_rsrc_t mres = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(p.mask), short(0), int((int64_t(p.rows) - 1) * p.mask_ld + p.V), kBufferWord3);
+#pragma unroll
+        for (int qq = 0; qq < kRoRows / 16; qq++) {
+            const int q = 4 * qq + wave;  // four rows per copy, copy q by wave q % 4
+            const int r = 4 * q + (lane >> 4), pos = lane & 15, k = (pos - r) & 15;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(mres, (lds_ptr_t)(lmask + q * 1024), 16,
+                                                     int(int64_t(r) * p.mask_ld) + n0 + 16 * k, 0, 0, 0);
+        }
+    }
     if (S & 1) {  // the last step, S - 1 = 2 NI: its fragments are in fx, its weight in slot (S - 1) % 12
         const int slot = (S - 1) % kRoDepth;
         v4u b0 = br[0][0], b1 = br[0][1];
@@ -336,114 +372,143 @@ __global__ __launch_bounds__(kRoThreads) void k_readout_tiles(ReadoutP p) {
         mfmas(fx, b0, b1);
     }
 
-    // ---- epilogue: eight passes of 32 rows x 256 columns through LDS ([32][256 + 4] f32). In pass
-    // q every wave stores its tiles of rows 32 q .. 32 q + 31; then thread t takes row t / 8 and
-    // the 32 columns 32 (t % 8) .. + 31 of it.
-    //
-    // The mask bytes of all eight passes are loaded first (their registers were the weight ring's),
-    // so the passes wait for one load's latency, not eight. The barriers between passes order LDS
-    // only: each thread writes its own records and reads no global memory another thread writes,
-    // so no pass waits for the stores of the one before.
-    const int prow = tid >> 3, part = tid & 7;
-    const int col0 = n0 + 32 * part;
-    uint32_t mpre[8][8];  // pass q's mask words when its row is whole and 16-byte aligned, else 0
-    if constexpr (MASK) {
-#pragma unroll
-        for (int q = 0; q < 8; q++) {
-            const int row = 32 * q + prow;
-#pragma unroll
-            for (int e = 0; e < 8; e++) mpre[q][e] = 0;
-            if (row < p.rows && col0 + 32 <= p.V && p.mask_vec) {
-                const uint8_t *mrow = p.mask + int64_t(row) * p.mask_ld + col0;
-                const uint4 m0 = *reinterpret_cast<const uint4 *>(mrow);
-                const uint4 m1 = *reinterpret_cast<const uint4 *>(mrow + 16);
-                mpre[q][0] = m0.x; mpre[q][1] = m0.y; mpre[q][2] = m0.z; mpre[q][3] = m0.w;
-                mpre[q][4] = m1.x; mpre[q][5] = m1.y; mpre[q][6] = m1.z; mpre[q][7] = m1.w;
-            }
-        }
+    if (mdma) {
+        wait_vmcnt<0>();
+        asm volatile("s_barrier" ::: "memory");  // every wave's copies of the mask have landed
     }
-    // every wave is done reading the stages (its last reads were waited for), which T reuses
-    asm volatile("s_barrier" ::: "memory");
-    float *T = reinterpret_cast<float *>(lds);
-    constexpr int TLD = kRoCols + 4;
-    static_assert(32 * TLD * 4 <= kRoStages * kRoStageBytes, "the epilogue's tile fits the stages");
+    // per (i, j, a) the row's four bytes at column cw0 + 32 j + 8 a (all ones without a mask);
+    // zero for a row past the last, so that the byte test below also excludes it
+    uint32_t mk[8][2][4];
 #pragma unroll
-    for (int q = 0; q < 8; q++) {
+    for (int i = 0; i < 8; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int r = 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
-                T[r * TLD + wave * 64 + j * 32 + fr] = acc[q][j][v];
-            }
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // the pass's tile is in T
-        const int row = 32 * q + prow;
-        float x[32];
+            for (int a4 = 0; a4 < 4; a4++) mk[i][j][a4] = 32 * i + rw < p.rows ? 0xffffffffu : 0u;
+    if constexpr (MASK) {
 #pragma unroll
-        for (int e = 0; e < 32; e += 4) {
-            const float4 f = *reinterpret_cast<const float4 *>(&T[prow * TLD + 32 * part + e]);
-            x[e] = f.x;
-            x[e + 1] = f.y;
-            x[e + 2] = f.z;
-            x[e + 3] = f.w;
+        for (int i = 0; i < 8; i++) {
+            const int r = 32 * i + rw;
+            if (r >= p.rows) continue;
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int c2 = 0; c2 < 2; c2++) {
+                    if (mdma) {
+                        const int k = 4 * wave + 2 * j + c2;
+                        const uint32_t *w32 =
+                            reinterpret_cast<const uint32_t *>(lmask + r * kRoCols + ((k + r) & 15) * 16 + 4 * hh);
+                        mk[i][j][2 * c2] = w32[0];
+                        mk[i][j][2 * c2 + 1] = w32[2];
+                    } else {
+                        const uint8_t *mrow = p.mask + int64_t(r < p.rows ? r : 0) * p.mask_ld;
+#pragma unroll
+                        for (int a2 = 0; a2 < 2; a2++) {
+                            const int c0 = cw0 + 32 * j + 8 * (2 * c2 + a2);
+                            uint32_t wd = 0;
+                            for (int e = 0; e < 4 && c0 + e < p.V; e++) wd |= uint32_t(mrow[c0 + e]) << (8 * e);
+                            mk[i][j][2 * c2 + a2] = wd;
+                        }
+                    }
+                }
         }
-        const bool live = row < p.rows;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int r = 32 * i + rw;
+        const bool live = r < p.rows;
         if constexpr (DBG) {
             if (live)
 #pragma unroll
-                for (int e = 0; e < 32; e++)
-                    if (col0 + e < p.V) p.logits[int64_t(row) * p.V + col0 + e] = x[e];
-        }
-        // the sampler's values: an excluded column or one past the vocabulary is -inf
-        uint32_t mw[8];
-        if constexpr (MASK) {
+                for (int j = 0; j < 2; j++)
 #pragma unroll
-            for (int e = 0; e < 8; e++) mw[e] = mpre[q][e];
-            if (live && !(col0 + 32 <= p.V && p.mask_vec)) {  // a partial or unaligned row: bytes
-                const uint8_t *mrow = p.mask + int64_t(row) * p.mask_ld + col0;
-                for (int e = 0; e < 32 && col0 + e < p.V; e++) mw[e / 4] |= uint32_t(mrow[e]) << (8 * (e % 4));
-            }
+                    for (int v = 0; v < 16; v++) {
+                        const int col = cw0 + 32 * j + 8 * (v / 4) + (v % 4);
+                        if (col < p.V) p.logits[int64_t(r) * p.V + col] = acc[i][j][v];
+                    }
         }
+        // the sampler's values: an excluded column or one past the vocabulary is -inf (the
+        // column bound only in the tile that crosses the vocabulary's end)
         float m = -INFINITY;
         int first = 0x7fffffff;
+        auto maxima = [&](auto full_c) {
+            constexpr bool FULL = decltype(full_c)::value;
 #pragma unroll
-        for (int e = 0; e < 32; e++) {
-            bool keep = live && col0 + e < p.V;
-            if constexpr (MASK) keep = keep && ((mw[e / 4] >> (8 * (e % 4))) & 0xffu) != 0;
-            x[e] = keep ? x[e] : -INFINITY;
-            if (x[e] > m) {
-                m = x[e];
-                first = col0 + e;
-            }
-        }
-        // the tile's maximum over the row's eight threads (consecutive lanes), the first column
-        // holding it
+            for (int j = 0; j < 2; j++)
 #pragma unroll
-        for (int o = 1; o < 8; o <<= 1) {
-            const float om = __shfl_xor(m, o, 64);
-            const int of = __shfl_xor(first, o, 64);
+                for (int v = 0; v < 16; v++) {
+                    const int off = 32 * j + 8 * (v / 4) + (v % 4);  // column cw0 + off
+                    bool keep = ((mk[i][j][v / 4] >> (8 * (v % 4))) & 0xffu) != 0;
+                    if constexpr (!FULL) keep = keep && cw0 + off < p.V;
+                    const float x = keep ? acc[i][j][v] : -INFINITY;
+                    acc[i][j][v] = x;
+                    if constexpr (FIRST) {
+                        if (x > m) {
+                            m = x;
+                            first = off;
+                        }
+                    } else {
+                        m = fmaxf(m, x);
+                    }
+                }
+        };
+        if (n0 + kRoCols <= p.V) maxima(std::true_type{});
+        else maxima(std::false_type{});
+        const float om = __shfl_xor(m, 32, 64);
+        if constexpr (FIRST) {
+            first = first == 0x7fffffff ? first : cw0 + first;
+            const int of = __shfl_xor(first, 32, 64);
             if (om > m || (om == m && of < first)) {
                 m = om;
                 first = of;
             }
+        } else {
+            m = fmaxf(m, om);
         }
-        const float ref = m * p.c;  // RN(max c); -inf when nothing is allowed
-        float w[32];
-#pragma unroll
-        for (int e = 0; e < 32; e++) w[e] = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(fmaf(x[e], p.c, -ref));
-        // the block's sum in a fixed tree
-#pragma unroll
-        for (int span = 1; span < 32; span <<= 1)
-#pragma unroll
-            for (int e = 0; e < 32; e += 2 * span) w[e] = w[e] + w[e + span];
-        const int blk = tile * (kRoCols / kRoBlock) + part;
-        if (live && blk < p.nblk) p.bsum[int64_t(row) * p.nblk + blk] = w[0];
-        if (live && part == 0) {
-            p.tref[int64_t(row) * p.ntile + tile] = ref;
-            p.tmax[int64_t(row) * p.ntile + tile] = m;
-            p.tfirst[int64_t(row) * p.ntile + tile] = first;
+        if (hh == 0) {
+            Sm[wave * kRoRows + r] = m;
+            if constexpr (FIRST) Sf[wave * kRoRows + r] = first;
         }
-        if (q < 7) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // T read by all: reusable
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // every wave's maxima in LDS
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int r = 32 * i + rw;
+        const bool live = r < p.rows;
+        // the tile's maximum and first column (the waves in column order; a tie keeps the earlier)
+        float M = Sm[r];
+        int F = 0x7fffffff;
+        if constexpr (FIRST) F = Sf[r];
+#pragma unroll
+        for (int w2 = 1; w2 < 4; w2++) {
+            const float m2 = Sm[w2 * kRoRows + r];
+            if (m2 > M) {
+                M = m2;
+                if constexpr (FIRST) F = Sf[w2 * kRoRows + r];
+            }
+        }
+        const float ref = M * p.c;  // RN(max c); -inf when nothing is allowed
+        // (with nothing allowed every value is -inf: a finite reference weighs them all 0)
+        const float wref = M == -INFINITY ? 0.0f : ref;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            float w[16];
+#pragma unroll
+            for (int v = 0; v < 16; v++) w[v] = __builtin_amdgcn_exp2f(fmaf(acc[i][j][v], p.c, -wref));
+            // this half's 16 in a fixed tree, then the two halves (column 4 (l / 32) of each 8)
+#pragma unroll
+            for (int span = 1; span < 16; span <<= 1)
+#pragma unroll
+                for (int e = 0; e < 16; e += 2 * span) w[e] = w[e] + w[e + span];
+            const float other = __shfl_xor(w[0], 32, 64);
+            const int blk = tile * (kRoCols / kRoBlock) + 2 * wave + j;
+            if (hh == 0 && live && blk < p.nblk) p.bsum[int64_t(r) * p.nblk + blk] = w[0] + other;
+        }
+        if (wave == 0 && hh == 0 && live) {
+            p.tref[int64_t(r) * p.ntile + tile] = ref;
+            p.tmax[int64_t(r) * p.ntile + tile] = M;
+            if constexpr (FIRST) p.tfirst[int64_t(r) * p.ntile + tile] = F;
+        }
     }
 }
 
@@ -758,9 +823,9 @@ __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
                 // the ring's oldest load (step st) has landed when kResRing - 1 remain
                 asm volatile("s_waitcnt vmcnt(47)" : "+v"(ring[k]) : : "memory");
                 static_assert(kResRing - 1 == 47, "the wait above");
-                if (!PARTIAL || st < S2)
-                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, cur[j]),
-                                                                  __builtin_bit_cast(bf16x8_t, ring[k]), acc, 0, 0, 0);
+                if (!PARTIAL || st < S2)  // (the weight as A, h as B: pass 1's order)
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, ring[k]),
+                                                                  __builtin_bit_cast(bf16x8_t, cur[j]), acc, 0, 0, 0);
                 load_frag(ring[k], woff + uint32_t(st + kResRing) * 8192, wrs);
             }
         }
@@ -776,8 +841,19 @@ __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
     for (int j = 1; j < kResRing; j++) asm volatile("" : "+v"(ring[j]) : : "memory");
     lds_wait_group(fa0);
     lds_wait_group(fa1);
-    // lane l (< 32) holds column 32 b + l (output row 0, every row being this row)
-    float x = acc[0];
+    // Block column c (lane c < 32) is acc[4 (c / 8) + c % 4] of a lane in half (c / 4) % 2, as in
+    // pass 1's layout (this row is each of B's 32 columns): this lane's half at that index, or its
+    // partner's (lane c ^ 32, the same index).
+    float x;
+    {
+        const int c = lane & 31, v = 4 * (c / 8) + (c % 4);
+        float own = acc[0];
+#pragma unroll
+        for (int vv = 1; vv < 16; vv++)
+            if (vv == v) own = acc[vv];
+        const float other = __shfl_xor(own, 32, 64);
+        x = (lane >> 5) == ((c / 4) & 1) ? own : other;
+    }
     if (p.dbg_block && lane < 32) p.dbg_block[int64_t(row) * 32 + lane] = x;
     if (p.dbg_index && lane == 0) p.dbg_index[row] = bstar;
     x = keep ? x : -INFINITY;
@@ -944,12 +1020,17 @@ extern "C" int nt_hip_rl_readout_sample(const NtRlReadoutSampleArgs *a) {
     p.logits = a->logits;
     hipStream_t st = ctx().stream;
     const dim3 g1{unsigned(ntile), 1, 1}, b1{unsigned(kRoThreads), 1, 1};
+    auto launch1 = [&](auto mask_c, auto dbg_c) {
+        constexpr bool MK = decltype(mask_c)::value, DB = decltype(dbg_c)::value;
+        if (greedy) hipLaunchKernelGGL((k_readout_tiles<MK, DB, true>), g1, b1, 0, st, p);
+        else hipLaunchKernelGGL((k_readout_tiles<MK, DB, false>), g1, b1, 0, st, p);
+    };
     if (a->logits) {
-        if (p.mask) hipLaunchKernelGGL((k_readout_tiles<true, true>), g1, b1, 0, st, p);
-        else hipLaunchKernelGGL((k_readout_tiles<false, true>), g1, b1, 0, st, p);
+        if (p.mask) launch1(std::true_type{}, std::true_type{});
+        else launch1(std::false_type{}, std::true_type{});
     } else {
-        if (p.mask) hipLaunchKernelGGL((k_readout_tiles<true, false>), g1, b1, 0, st, p);
-        else hipLaunchKernelGGL((k_readout_tiles<false, false>), g1, b1, 0, st, p);
+        if (p.mask) launch1(std::true_type{}, std::false_type{});
+        else launch1(std::false_type{}, std::false_type{});
     }
     if (int rc = launched(who)) return rc;
     ResolveP q;
