@@ -19,11 +19,14 @@
 #include <algorithm>
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
+#include <cstring>
 #include <string>
 
 #include "../../include/noetic_hip.h"
 #include "../../include/noetic_ops.h"
 #include "nt_internal.hpp"
+#include "nt_mfma_pipe.hpp"
 
 #ifndef NT_KERNELS_SHA
 #define NT_KERNELS_SHA "unknown"
@@ -604,6 +607,133 @@ __global__ __launch_bounds__(kMmThreads) void k_matmul_half(MatmulP p) {
         }
 }
 
+// ------------------------------------------------- matmul_half, packed operands (large products)
+// For products of many 256 x 256 output tiles the operands are rounded to bf16 once, into the
+// matrix cores' fragment order (the row operand A in row groups of 32, the column operand B
+// tile-major in tiles of 256 columns; rows, columns and k past the ends are zeros), and each
+// workgroup then runs the bf16 MFMA pipeline of nt_mfma_pipe.hpp over one 256 x 256 tile of one
+// batch: the same instruction over the same k order from zero as the staged kernel above, so each
+// output is the same sum. The packing reads each f32 operand once and writes half its bytes; the
+// tiles then read bf16 fragments only, 16 or 32 bytes per lane per load.
+
+// The batch element offsets of A and B for output batch z (broadcast dimensions repeat).
+__device__ __forceinline__ void batch_offsets(const MatmulP &p, int64_t z, int64_t *ao, int64_t *bo) {
+    int64_t a = p.a_off, b = p.b_off, q = z;
+    for (int d = p.nbd - 1; d >= 0; --d) {
+        const int64_t i = q % p.bshape[d];
+        q /= p.bshape[d];
+        a += i * p.a_bs[d];
+        b += i * p.b_bs[d];
+    }
+    *ao = a;
+    *bo = b;
+}
+
+// Eight f32 at src + e stride (e < 8, those at or past `lim` zero) as eight bf16, nearest even.
+__device__ __forceinline__ uint4 pack8(const float *src, int64_t stride, int lim) {
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) x[e] = e < lim ? src[e * stride] : 0.0f;
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(w[q]) : "v"(x[2 * q]), "v"(x[2 * q + 1]));
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// A (batch z = blockIdx.y) into row-group fragments: fragment (g, s) of G x S at (g S + s) KiB
+// from the batch's start (G S KiB apart); lane l's 16 bytes are row 32 g + l % 32, k 16 s +
+// 8 (l / 32) .. + 7. One thread per lane of a fragment.
+__global__ void k_pack_half_rows(MatmulP p, int G, int S, uint8_t *out) {
+    const int64_t z = blockIdx.y;
+    int64_t ao, bo;
+    batch_offsets(p, z, &ao, &bo);
+    const int64_t total = int64_t(G) * S * 64;
+    for (int64_t idx = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; idx < total;
+         idx += int64_t(gridDim.x) * blockDim.x) {
+        const int l = int(idx % 64);
+        const int64_t q = idx / 64;
+        const int s = int(q % S), g = int(q / S);
+        const int row = 32 * g + (l & 31), k0 = 16 * s + 8 * (l >> 5);
+        const int lim = row < p.m ? min(8, p.k - k0) : 0;
+        const uint4 v = pack8(p.a + ao + int64_t(row < p.m ? row : 0) * p.a_rs + int64_t(k0) * p.a_cs, p.a_cs, lim);
+        *reinterpret_cast<uint4 *>(out + (z * G * S + (int64_t(g) * S + s)) * 1024 + l * 16) = v;
+    }
+}
+
+// B (batch z = blockIdx.y) into tile-major column fragments: tile t of T, step s, column group gi
+// at ((t S + s) 8 + gi) KiB from the batch's start (T S 8 KiB apart); lane l's 16 bytes are
+// column 32 (8 t + gi) + l % 32, k 16 s + 8 (l / 32) .. + 7.
+__global__ void k_pack_half_cols(MatmulP p, int T, int S, uint8_t *out) {
+    const int64_t z = blockIdx.y;
+    int64_t ao, bo;
+    batch_offsets(p, z, &ao, &bo);
+    const int64_t total = int64_t(T) * S * 8 * 64;
+    for (int64_t idx = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; idx < total;
+         idx += int64_t(gridDim.x) * blockDim.x) {
+        const int l = int(idx % 64);
+        const int64_t q = idx / 64;  // (t S + s) 8 + gi
+        const int gi = int(q % 8);
+        const int64_t ts = q / 8;
+        const int s = int(ts % S), t = int(ts / S);
+        const int col = 32 * (8 * t + gi) + (l & 31), k0 = 16 * s + 8 * (l >> 5);
+        const int lim = col < p.n ? min(8, p.k - k0) : 0;
+        const uint4 v = pack8(p.b + bo + int64_t(col < p.n ? col : 0) * p.b_cs + int64_t(k0) * p.b_rs, p.b_rs, lim);
+        *reinterpret_cast<uint4 *>(out + (z * T * S * 8 + q) * 1024 + l * 16) = v;
+    }
+}
+
+// The packed path from this many 256 x 256 output tiles and this k (below them the staged kernel,
+// whose operands need no second pass).
+constexpr int64_t kHalfPackedTiles = 64;
+constexpr int64_t kHalfPackedK = 256;
+
+// One 256 x 256 output tile (tm_i, tn_i) of batch z per workgroup. Workgroup w is tile
+// (w / (tm tn)) of the batches, then row tiles in order within a column tile: consecutive
+// workgroups share their B tile, and the 8 XCDs (dealt workgroups in turn) each hold every
+// eighth row tile of it.
+__global__ __launch_bounds__(256) void k_half_tiles(MatmulP p, const uint8_t *pa, const uint8_t *pb, int G, int T,
+                                                     int S) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[pipe::kPipeStages * pipe::kPipeStageBytes];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t wg = blockIdx.x, per_batch = int64_t(p.tm) * p.tn;
+    const int64_t z = wg / per_batch;
+    const int rem = int(wg - z * per_batch);
+    const int tn_i = rem / p.tm, tm_i = rem % p.tm;
+    // this tile's row groups of A (rows past the batch's last group read as zeros: the range)
+    const int g0 = 8 * tm_i, ng = min(8, G - g0);
+    const __amdgpu_buffer_rsrc_t hres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(pa + (z * G + g0) * int64_t(S) * 1024), short(0), ng * S * 1024, pipe::kBufferWord3);
+    const int hoff = 2 * wave * S * 1024 + lane * 16, woff = 2 * wave * 1024 + lane * 16;
+    const uint64_t wbase = reinterpret_cast<uint64_t>(pb + (z * T + tn_i) * int64_t(S) * 8192);
+    const pipe::v4u wrs = {uint32_t(wbase), uint32_t(wbase >> 32), uint32_t(S * 8192), uint32_t(pipe::kBufferWord3)};
+    pipe::f32x16_t acc[8][2];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[i][j][v] = 0.0f;
+    pipe::MfmaPipe<false> pp;
+    pp.run(lds, hres, hoff, wrs, woff, S, wave, lane, acc);
+    pp.last_odd_step(S, acc);
+    // lane l holds rows 32 i + 8 (v / 4) + 4 (l / 32) + v % 4, column 64 wave + 32 j + l % 32
+    float *c = p.c + z * int64_t(p.m) * p.n;
+    const int row0 = 256 * tm_i, col0 = 256 * tn_i + 64 * wave + (lane & 31);
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int col = col0 + 32 * j;
+        if (col >= p.n) continue;
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int row = row0 + 32 * i + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
+                if (row < p.m) c[int64_t(row) * p.n + col] = acc[i][j][v];
+            }
+    }
+}
+
 template <int H, bool SPLIT>
 int launch_matmul(const MatmulP &p, bool ak, bool bn, hipStream_t s) {
     const dim3 grid(unsigned(p.blocks)), block(kMmThreads);
@@ -762,6 +892,46 @@ int nt_hip_matmul_half(const float *a, const NtLayout *al, const float *b, const
     p.m = int32_t(m);
     p.n = int32_t(n);
     p.k = int32_t(k);
+    // Packed operands and 256 x 256 tiles for a product of many such tiles (see k_half_tiles);
+    // NOETIC_HIP_HALF_GEMM=packed|staged picks one path (a tuning knob). The packed path keeps
+    // every offset in 32 bits: k <= 65536, at most 65535 batches and 1 GiB of packed operands.
+    {
+        const int64_t S = (k + 15) / 16, G = (m + 31) / 32, T256 = (n + 255) / 256, TM = (m + 255) / 256;
+        const int64_t tiles = nb * TM * T256;
+        const int64_t bytes_a = nb * G * S * 1024, bytes_b = nb * T256 * S * 8192;
+        const bool fits = k <= 65536 && nb <= 65535 && bytes_a + bytes_b <= (int64_t(1) << 30) && tiles <= 0x7fffffff;
+        bool packed = fits && tiles >= kHalfPackedTiles && k >= kHalfPackedK;
+        if (const char *e = std::getenv("NOETIC_HIP_HALF_GEMM")) {
+            if (std::strcmp(e, "packed") == 0) packed = fits;
+            else if (std::strcmp(e, "staged") == 0) packed = false;
+        }
+        if (packed) {
+            p.tm = int32_t(TM);
+            p.tn = int32_t(T256);
+            std::unique_lock<std::mutex> lk;
+            if (int rc = enter(&lk)) return rc;
+            hipStream_t st = ctx().stream;
+            void *ws = nullptr;
+            if (int rc = scratch_alloc(size_t(bytes_a + bytes_b), &ws)) return rc;
+            uint8_t *pa = static_cast<uint8_t *>(ws), *pb = pa + bytes_a;
+            const int64_t ta = G * S * 64, tb = T256 * S * 8 * 64;
+            const dim3 ga(unsigned(std::min<int64_t>((ta + 255) / 256, 4096)), unsigned(nb));
+            const dim3 gb(unsigned(std::min<int64_t>((tb + 255) / 256, 4096)), unsigned(nb));
+            hipLaunchKernelGGL(k_pack_half_rows, ga, dim3(256), 0, st, p, int(G), int(S), pa);
+            int rc = launched("k_pack_half_rows");
+            if (!rc) {
+                hipLaunchKernelGGL(k_pack_half_cols, gb, dim3(256), 0, st, p, int(T256), int(S), pb);
+                rc = launched("k_pack_half_cols");
+            }
+            if (!rc) {
+                hipLaunchKernelGGL(k_half_tiles, dim3(unsigned(tiles)), dim3(256), 0, st, p, pa, pb, int(G),
+                                   int(T256), int(S));
+                rc = launched("k_half_tiles");
+            }
+            const int rf = scratch_release(ws);
+            return rc ? rc : rf;
+        }
+    }
     // 128x128 tiles when they give at least 512 workgroups, else 64x64
     const int64_t big = nb * ((m + 127) / 128) * ((n + 127) / 128);
     const int T = big >= 512 ? 128 : 64;
