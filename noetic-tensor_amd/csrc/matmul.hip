@@ -629,11 +629,18 @@ __device__ __forceinline__ void batch_offsets(const MatmulP &p, int64_t z, int64
     *bo = b;
 }
 
-// Eight f32 at src + e stride (e < 8, those at or past `lim` zero) as eight bf16, nearest even.
+// Eight f32 at src + e stride (e < 8, those at or past `lim` zero) as eight bf16, nearest even
+// (two 16-byte loads when the eight are contiguous and aligned).
 __device__ __forceinline__ uint4 pack8(const float *src, int64_t stride, int lim) {
     float x[8];
+    if (stride == 1 && lim == 8 && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+        const float4 u = reinterpret_cast<const float4 *>(src)[0], v = reinterpret_cast<const float4 *>(src)[1];
+        x[0] = u.x; x[1] = u.y; x[2] = u.z; x[3] = u.w;
+        x[4] = v.x; x[5] = v.y; x[6] = v.z; x[7] = v.w;
+    } else {
 #pragma unroll
-    for (int e = 0; e < 8; e++) x[e] = e < lim ? src[e * stride] : 0.0f;
+        for (int e = 0; e < 8; e++) x[e] = e < lim ? src[e * stride] : 0.0f;
+    }
     uint32_t w[4];
 #pragma unroll
     for (int q = 0; q < 4; q++) asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(w[q]) : "v"(x[2 * q]), "v"(x[2 * q + 1]));
