@@ -761,9 +761,10 @@ def main():
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--workload", default="c4",
                     choices=["c4", "c4s", "c2", "c3", "c3b", "c5", "ops", "readout", "matmul"])
-    ap.add_argument("--kernels", default="aot", choices=["aot", "rtc"],
-                    help="how the sampler kernels are loaded: the library's hipcc code objects (the default) "
-                         "or hiprtc at first use (compiled in the warmup)")
+    ap.add_argument("--kernels", default="rtc", choices=["aot", "rtc"],
+                    help="how the sampler kernels are loaded: hiprtc at first use, the reference's NVRTC route "
+                         "(the default; compiled by the first, untimed launch, or read from the disk cache), "
+                         "or the library's hipcc code objects")
     ap.add_argument("--clock-warmup", type=float, default=1.0,
                     help="seconds of untimed launches before the warmup steps (the device's clocks settle)")
     ap.add_argument("--cpu-rows", type=int, default=256, help="rows of the CPU baseline sample (0 = skip)")

@@ -1,5 +1,6 @@
-// The sampler kernels' run-time path: compiled by hiprtc at first use from the device source
-// embedded in the library (rl_sample_kernels.hpp and the headers it includes), loaded with
+// The row kernels' run-time path (the samplers, the scorer and its backward): compiled by hiprtc
+// at first use from the device source embedded in the library (rl_sample_kernels.hpp,
+// rl_score_kernels.hpp and the headers they include), loaded with
 // hipModuleLoadData and launched with hipModuleLaunchKernel, one function per template instance.
 // The ahead-of-time code objects (hipcc, the library's default) run the same source.
 #pragma once
@@ -22,6 +23,11 @@ int kernel_path();
 // the current device. `arg` is the kernel's one by-value argument. Call with the context lock
 // held; a compile failure is returned as NT_E_RTC with hiprtc's log, a load failure as HIP's.
 int rtc_launch(const std::string &name, dim3 grid, dim3 block, size_t shm, hipStream_t s, const void *arg);
+
+// The status of the run-time path's launches since an entry point last cleared it (0: none
+// failed). Entry points clear it before their launches and return it if set; they are serialised
+// by the context lock.
+int &rtc_status();
 
 // The key's middle for the run-time path: "hiprtc<version>-kernels-<sha16 of the embedded source>".
 std::string rtc_key_part();

@@ -7,27 +7,13 @@
 #include <cstdlib>
 #include <cstring>
 
-#include "nt_rtc.hpp"
+#include "nt_launch.hpp"
 #include "rl_sample_kernels.hpp"
 
 namespace nt {
 namespace {
 
 // ------------------------------------------------------------------ dispatch
-
-// The status of the last launch made through hiprtc (0 on the ahead-of-time path, whose launch
-// errors hipGetLastError reports): entries are serialised by the context lock.
-int g_rtc_rc = 0;
-
-// One launch of kernel `name`'s instance: from the library's code objects, or compiled by hiprtc.
-template <class P>
-void launch_path(void (*aot)(P), const char *name, dim3 grid, dim3 block, size_t shm, hipStream_t s, const P &p) {
-    if (kernel_path() == NT_KERNELS_RTC) {
-        if (g_rtc_rc == 0) g_rtc_rc = rtc_launch(name, grid, block, shm, s, &p);
-        return;
-    }
-    hipLaunchKernelGGL(aot, grid, block, shm, s, p);
-}
 
 template <int DT, int MK, bool ENT, bool AL>
 void launch_sample(const SampleP &p, int64_t rows, int threads, size_t shm, hipStream_t s) {
@@ -340,9 +326,9 @@ int sample_entry(const NtRlSampleArgs *a, WorkspaceFn workspace, bool nofree, co
             q.rec_bytes = int(sizeof(SegRec)) + 4 * sg.k;
             q.count = reinterpret_cast<uint32_t *>(ws);
             q.recs = ws + kSegCounterBytes;
-            g_rtc_rc = 0;
+            rtc_status() = 0;
             launch_seg(a->dtype, a->mask_kind, sg, ent, all_in_flight(a->rows * sg.g), q, a->rows, s);
-            return g_rtc_rc ? g_rtc_rc : launched(who);
+            return rtc_status() ? rtc_status() : launched(who);
         }
         const int kmax = rr_kmax(a->dtype, a->mask_kind, epl);
         const char *rr_env = std::getenv("NOETIC_HIP_SAMPLE_RR");  // "off": the streaming kernel (a tuning knob)
@@ -350,15 +336,15 @@ int sample_entry(const NtRlSampleArgs *a, WorkspaceFn workspace, bool nofree, co
             int K = 1;
             while (int64_t(kRRWaves) * K < nch) K *= 2;
             p.nc = int(nch);
-            g_rtc_rc = 0;
+            rtc_status() = 0;
             launch_rr<8>(a->dtype, a->mask_kind, K, ent, all_in_flight(a->rows), p, a->rows, s);
-            return g_rtc_rc ? g_rtc_rc : launched(who);
+            return rtc_status() ? rtc_status() : launched(who);
         }
     }
-    g_rtc_rc = 0;
+    rtc_status() = 0;
     if (a->dtype == NT_F32) pick_mk_sample<NT_F32>(a->mask_kind, ent, al, p, a->rows, nw * kWave, shm, s);
     else pick_mk_sample<NT_BF16>(a->mask_kind, ent, al, p, a->rows, nw * kWave, shm, s);
-    return g_rtc_rc ? g_rtc_rc : launched(who);
+    return rtc_status() ? rtc_status() : launched(who);
 }
 
 namespace {

@@ -1,6 +1,6 @@
-// The sampler kernels' run-time path (nt_rtc.hpp): hiprtc compiles one template instance per
-// program from the embedded device source, with the options the ahead-of-time build uses, so the
-// two paths run the same code. Functions are cached per device and instance for the process, and
+// The row kernels' run-time path (nt_rtc.hpp: the samplers, the scorer and its backward): hiprtc
+// compiles one template instance per program from the embedded device source, with the options
+// the ahead-of-time build uses, so the two paths run the same code. Functions are cached per device and instance for the process, and
 // code objects on disk (NOETIC_HIP_CACHE_DIR, else $HOME/.cache/noetic-hip) under a name that
 // carries the source's SHA-256, the hiprtc version, the options and the instance, so a later
 // process loads instead of compiling. The reference compiles its CUDA kernels with NVRTC at first
@@ -106,7 +106,7 @@ void cache_write(const std::string &path, const std::string &lowered, const std:
 
 int compile(const std::string &name, std::string *lowered, std::vector<char> *code) {
     hiprtcProgram prog;
-    const char *src = "#include \"rl_sample_kernels.hpp\"\n";
+    const char *src = "#include \"rl_sample_kernels.hpp\"\n#include \"rl_score_kernels.hpp\"\n";
     if (hiprtcCreateProgram(&prog, src, "nt_rtc.hip", kRtcFiles, kRtcTexts, kRtcNames) != HIPRTC_SUCCESS)
         return fail(NT_E_RTC, "hiprtcCreateProgram failed");
     hiprtcResult r = hiprtcAddNameExpression(prog, name.c_str());
@@ -183,6 +183,11 @@ int rtc_launch(const std::string &name, dim3 grid, dim3 block, size_t shm, hipSt
     return hip_check(hipModuleLaunchKernel(fn, grid.x, grid.y, grid.z, block.x, block.y, block.z, unsigned(shm), s,
                                            params, nullptr),
                      "hipModuleLaunchKernel");
+}
+
+int &rtc_status() {
+    static int rc = 0;
+    return rc;
 }
 
 std::string rtc_key_part() {

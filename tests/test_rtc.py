@@ -1,6 +1,6 @@
-"""CPU tests of the sampler kernels' run-time path (hiprtc): the path switch needs no device, and
-hiprtc compiles the embedded device source into a gfx950 code object here, without a GPU, with
-the options the library passes (rtc.cpp)."""
+"""CPU tests of the row kernels' run-time path (hiprtc: the samplers, the scorer and its backward):
+the path switch needs no device, and hiprtc compiles the embedded device source into a gfx950 code
+object here, without a GPU, with the program text and options the library passes (rtc.cpp)."""
 import ctypes as C
 import os
 
@@ -16,7 +16,9 @@ EMBEDDED = {
     "noetic_hip.h": os.path.join(ROOT, "include", "noetic_hip.h"),
     "nt_rows.hpp": os.path.join(CSRC, "nt_rows.hpp"),
     "rl_sample_kernels.hpp": os.path.join(CSRC, "rl_sample_kernels.hpp"),
+    "rl_score_kernels.hpp": os.path.join(CSRC, "rl_score_kernels.hpp"),
 }
+PROGRAM = b'#include "rl_sample_kernels.hpp"\n#include "rl_score_kernels.hpp"\n'
 OPTIONS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
@@ -35,7 +37,15 @@ def test_kernel_path_switch_needs_no_device():
         nr.set_kernel_path(prev)
 
 
-def test_hiprtc_compiles_the_c4_sampler_instance_on_the_cpu():
+@pytest.mark.parametrize("expr, kernel", [
+    # bf16 rows, u8 mask, 16 chunks per wave: C4's sampler
+    (b"nt::k_sample_rr<1, 1, 16, false, 8, 1>", b"k_sample_rr"),
+    # bf16 policy and reference rows, no mask, logp + KL + entropy, aligned: C3's scorer
+    (b"nt::k_score<1, 0, true, true, true, true>", b"k_score"),
+    # its backward with the KL term into a bf16 gradient
+    (b"nt::k_score_grad<1, 0, true, 1, true>", b"k_score_grad"),
+])
+def test_hiprtc_compiles_the_row_kernel_instances_on_the_cpu(expr, kernel):
     try:
         rtc = C.CDLL("libhiprtc.so")
     except OSError:
@@ -44,10 +54,8 @@ def test_hiprtc_compiles_the_c4_sampler_instance_on_the_cpu():
     texts = [open(EMBEDDED[n], "rb").read() for n in names]
     Arr = C.c_char_p * len(names)
     prog = C.c_void_p()
-    src = b'#include "rl_sample_kernels.hpp"\n'
-    assert rtc.hiprtcCreateProgram(C.byref(prog), src, b"nt_rtc.hip", len(names), Arr(*texts),
+    assert rtc.hiprtcCreateProgram(C.byref(prog), PROGRAM, b"nt_rtc.hip", len(names), Arr(*texts),
                                    Arr(*[n.encode() for n in names])) == 0
-    expr = b"nt::k_sample_rr<1, 1, 16, false, 8, 1>"  # bf16 rows, u8 mask, 16 chunks per wave (C4)
     assert rtc.hiprtcAddNameExpression(prog, expr) == 0
     opts = (C.c_char_p * len(OPTIONS))(*[o.encode() for o in OPTIONS])
     rc = rtc.hiprtcCompileProgram(prog, len(OPTIONS), opts)
@@ -59,7 +67,7 @@ def test_hiprtc_compiles_the_c4_sampler_instance_on_the_cpu():
         pytest.fail(log.value.decode(errors="replace")[:4000])
     lowered = C.c_char_p()
     assert rtc.hiprtcGetLoweredName(prog, expr, C.byref(lowered)) == 0
-    assert lowered.value.startswith(b"_ZN2nt") and b"k_sample_rr" in lowered.value
+    assert lowered.value.startswith(b"_ZN2nt") and kernel in lowered.value
     size = C.c_size_t()
     assert rtc.hiprtcGetCodeSize(prog, C.byref(size)) == 0 and size.value > 0
     code = C.create_string_buffer(size.value)

@@ -1,8 +1,10 @@
-"""GPU tests of the sampler kernels' run-time path: the same calls through the ahead-of-time code
+"""GPU tests of the row kernels' run-time path: the same calls through the ahead-of-time code
 objects and through hiprtc (compiled at first use from the embedded source, loaded with
-hipModuleLoadData) give byte-identical ids, log-probabilities and entropies, C4 among them with
-its oracle parity; the provenance key names the path; a second process loads the compiled code
-objects from the disk cache instead of compiling."""
+hipModuleLoadData) give byte-identical ids, log-probabilities and entropies (C4 among them, with
+its oracle parity), and byte-identical scores, saved statistics and gradients from the scorer and
+its fused backward (C3's rows among them, the gradient with its oracle parity); the provenance key
+names the path; a second process loads the compiled code objects from the disk cache instead of
+compiling."""
 import os
 import subprocess
 import sys
@@ -15,6 +17,7 @@ import noetic_rl as nr
 import workloads as W
 from oracle import oracle as O
 from tests.test_rl_gpu import check_sample
+from tests.test_score_grad_gpu import compare_to_oracle, upstream
 
 pytestmark = pytest.mark.gpu
 
@@ -90,6 +93,54 @@ def test_each_sampler_kernel_is_byte_identical_through_both_paths(case):
     u = nr.Tensor.from_numpy(nr.Rng(11, case).uniforms(rows), "f64")
     aot, rtc1, rtc2 = both_paths(lambda: nr.sample_logp(xt, tau, mt, None, entropy=True, uniforms=u))
     assert rtc1 == aot and rtc2 == aot, f"{case}: hiprtc and hipcc code objects disagree"
+
+
+@pytest.mark.parametrize("case", ["c3_bf16_aligned", "f32_masked_tempered_unaligned"])
+def test_scorer_and_backward_are_byte_identical_through_both_paths(case):
+    """k_score (logp, the reference's logp, exact KL, entropy and the log-sum-exp statistics it
+    saves) and k_score_grad (f32 and bf16 gradients of g_logp logp + g_kl KL + g_H H): C3's bf16
+    rows with the reference (the buffer-resource kernels), and f32 rows of V = 1001 under a u8 mask
+    and a temperature (the general kernels)."""
+    rng = np.random.default_rng(5)
+    if case == "c3_bf16_aligned":
+        w = W.c3(rows=64)
+        rows, tau = w["rows"], 1.0
+        pol, ref, tok = w["logits"], w["ref"], w["tokens"]
+        z = W.bf16_to_f32(pol.to_numpy())
+        r = W.bf16_to_f32(ref.to_numpy())
+    else:
+        rows, V, tau = 40, 1001, 0.8
+        x = rng.normal(0, 3, (rows, V)).astype(np.float32)
+        y = (x + rng.normal(0, 0.5, (rows, V))).astype(np.float32)
+        keep = (rng.random((rows, V)) < 0.8).astype(np.uint8)
+        keep[:, 0] = 1
+        tokens = np.array([rng.choice(np.nonzero(keep[i])[0]) for i in range(rows)], np.int32)
+        mt = nr.Tensor.from_numpy(keep)
+        pol = nr.tempered_logits(nr.Tensor.from_numpy(x), tau, mt)
+        ref = nr.tempered_logits(nr.Tensor.from_numpy(y), tau, mt)
+        tok = nr.Tensor.from_numpy(tokens)
+        z, r = O.tempered(x, tau, keep=keep), O.tempered(y, tau, keep=keep)
+    g = upstream(rows, 9)
+    gt = {k: nr.Tensor.from_numpy(v) for k, v in g.items()}
+
+    def call():
+        lp, rlp, kl, ent, st = nr.score_with_stats(pol, ref, tok)
+        out = [lp, rlp, kl, ent, st.lse_base, st.lse_rest, st.ref_lse_base, st.ref_lse_rest]
+        for gdt in ("f32", "bf16"):
+            out.append(nr.score_grad(pol, ref, tok, st, kl=kl, entropy=ent, g_logp=gt["g_lp"], g_kl=gt["g_kl"],
+                                     g_entropy=gt["g_h"], grad_dtype=gdt))
+        return out
+
+    aot, rtc1, rtc2 = both_paths(call)
+    names = ["logp", "ref_logp", "kl", "entropy", "lse_base", "lse_rest", "ref_lse_base", "ref_lse_rest",
+             "grad f32", "grad bf16"]
+    for i, n in enumerate(names):
+        assert rtc1[i] == aot[i] and rtc2[i] == aot[i], f"{case}: {n} differs between hiprtc and hipcc code objects"
+    kl = np.frombuffer(aot[2], np.float32)
+    ent = np.frombuffer(aot[3], np.float32)
+    gf = np.frombuffer(aot[8], np.float32).reshape(z.shape)
+    gb = np.frombuffer(aot[9], np.uint16).reshape(z.shape)
+    compare_to_oracle(f"{case} (aot = rtc)", z, r, tok.to_numpy(), g, kl, ent, tau, gf, gb)
 
 
 def test_key_names_the_path():
