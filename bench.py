@@ -20,7 +20,10 @@ object (the reference's Cpu(Reference) op sequence, restated in oracle/, timed o
       the per-sequence mean log-probability (nt_hip_rl_reduce_tokens) and group-relative
       advantages over groups of 8 along B (nt_hip_rl_group_advantages, f64 on the device);
   matmul  the general ops' f32 matmul (CpuRef's arithmetic) at the reference's throughput
-      shapes and 4096^3.
+      shapes and 4096^3;
+  readout  C4's decode step from the hidden states: h[256,4096] . W (V 128256) fused with the
+      sample + logp (nt_hip_rl_readout_sample), and with the scoring of the drawn tokens
+      (nt_hip_rl_readout_score), each beside hipBLASLt's GEMM and the unfused kernel.
 """
 import argparse
 import ctypes as C
@@ -638,7 +641,10 @@ def bench_readout(nr, W, args):
     reference's [d, V] Linear layout into the matrix cores' fragment order (timed separately, as a
     loader would run it once).
     Unfused (beside it): torch.matmul (hipBLASLt) into bf16 logits, then nt_hip_rl_sample on
-    them, with the weight in the reference's [d, V] layout and in the vocabulary-major one."""
+    them, with the weight in the reference's [d, V] layout and in the vocabulary-major one.
+    Scoring (`score`, beside it): nt_hip_rl_readout_score (the log-probability of each row's drawn
+    token and the entropy, the logits never written) against hipBLASLt's GEMM and nt_hip_rl_score
+    on the bf16 logits."""
     import torch
 
     rows, d, V = 256, 4096, 128256
@@ -683,6 +689,20 @@ def bench_readout(nr, W, args):
     def fused(i):
         nr._check(L.nt_hip_rl_readout_sample(C.byref(fa)), "readout sample")
 
+    # scoring the drawn tokens (ids2, the fused step's draws): fused, and on the written logits
+    slp, sent, sst = nr.Tensor((rows,), "f32"), nr.Tensor((rows,), "f32"), nr.Tensor((rows,), "u8")
+    sa = nr.NtRlReadoutScoreArgs(h.data_ptr(), w_packed.data_ptr(), rows, V, d, d, nr.NT_MASK_U8, 0, w["mask"].ptr,
+                                 V, 0.7, ids2.ptr, slp.ptr, sent.ptr, sst.ptr, None)
+    ulp, uent, ust = nr.Tensor((rows,), "f32"), nr.Tensor((rows,), "f32"), nr.Tensor((rows,), "u8")
+    ua = nr.NtRlScoreArgs(logits.data_ptr(), None, nr.NT_BF16, nr.NT_MASK_U8, rows, V, V, w["mask"].ptr, V, 0.7,
+                          ids2.ptr, ulp.ptr, None, None, uent.ptr, ust.ptr, None, None, None, None)
+
+    def fused_score(i):
+        nr._check(L.nt_hip_rl_readout_score(C.byref(sa)), "readout score")
+
+    def score_on_logits(i):
+        nr._check(L.nt_hip_rl_score(C.byref(ua)), "score")
+
     def gemm_dv(i):
         with torch.cuda.stream(ts):
             torch.matmul(h, w_dv, out=logits)
@@ -702,6 +722,10 @@ def bench_readout(nr, W, args):
         gemm_vd(i)
         sample(i)
 
+    def score_step_vd(i):
+        gemm_vd(i)
+        score_on_logits(i)
+
     steps, warmup = args.steps, args.warmup
     fused(0)
     warm_s = clock_warmup(nr, fused, args.clock_warmup)
@@ -709,7 +733,8 @@ def bench_readout(nr, W, args):
     if np.any(st2.to_numpy() != 0):
         raise RuntimeError("readout: refused rows")
     # the unfused steps beside it: three interleaved rounds, medians
-    res = {k: [] for k in ("fused", "gemm_dv", "gemm_vd", "sample", "step_dv", "step_vd")}
+    res = {k: [] for k in ("fused", "gemm_dv", "gemm_vd", "sample", "step_dv", "step_vd", "fused_score", "score",
+                           "score_step_vd")}
     for _ in range(3):
         res["fused"].append(timed(nr, steps, warmup, fused)[0])
         res["gemm_dv"].append(timed(nr, steps, warmup, gemm_dv)[0])
@@ -718,9 +743,19 @@ def bench_readout(nr, W, args):
         res["sample"].append(timed(nr, steps, warmup, sample)[0])
         res["step_dv"].append(timed(nr, steps, warmup, step_dv)[0])
         res["step_vd"].append(timed(nr, steps, warmup, step_vd)[0])
+        res["fused_score"].append(timed(nr, steps, warmup, fused_score)[0])
+        gemm_vd(0)
+        res["score"].append(timed(nr, steps, warmup, score_on_logits)[0])
+        res["score_step_vd"].append(timed(nr, steps, warmup, score_step_vd)[0])
     med = {k: float(np.median(v)) * 1e3 for k, v in res.items()}
     if np.any(st.to_numpy() != 0):
         raise RuntimeError("readout: refused rows (unfused)")
+    if np.any(sst.to_numpy() != 0) or np.any(ust.to_numpy() != 0):
+        raise RuntimeError("readout: refused rows (scoring)")
+    # the fused scorer against the unfused one on the same tokens (the unfused logits are bf16, the
+    # fused f32: the difference is the logits' rounding, reported, not asserted)
+    d_lp = float(np.max(np.abs(slp.to_numpy().astype(np.float64) - ulp.to_numpy())))
+    d_ent = float(np.max(np.abs(sent.to_numpy().astype(np.float64) - uent.to_numpy())))
     w_bytes = V * d * 2
     step_bytes = w_bytes + rows * d * 2 + rows * V + rows * (8 + 4 + 4 + 1)
     flops = 2.0 * rows * d * V
@@ -749,6 +784,12 @@ def bench_readout(nr, W, args):
                         "speedup_vs_best_unfused": round(min(med["step_dv"], med["step_vd"]) / med["fused"], 3),
                         "note": "the unfused GEMM writes bf16 logits (hipBLASLt's output for bf16 operands); the "
                                 "fused product keeps them in f32"},
+            "score": {"what": "log-probability of each row's drawn token + entropy, same shape and mask",
+                      "fused_readout_score_us": round(med["fused_score"], 2),
+                      "score_on_bf16_logits_us": round(med["score"], 2),
+                      "gemm_w_vd_plus_score_us": round(med["score_step_vd"], 2),
+                      "speedup": round(med["score_step_vd"] / med["fused_score"], 3),
+                      "max_abs_diff_logp_vs_bf16_logits": d_lp, "max_abs_diff_entropy_vs_bf16_logits": d_ent},
             "weight_transpose_once_s": round(transpose_s, 4), "weight_pack_once_s": round(pack_s, 4),
             "clock_warmup_s": round(warm_s, 3), "key": nr.key()}
 

@@ -228,6 +228,34 @@ typedef struct NtRlReadoutSampleArgs {
 } NtRlReadoutSampleArgs;
 int nt_hip_rl_readout_sample(const NtRlReadoutSampleArgs *a);
 
+/* The readout-fused scorer: the same readout product, then for each row
+ *   logp[r]    = token_log_probs(z, tokens)[r]       (rl.rs:134-141)
+ *   entropy[r] = categorical_entropy(z)[r]          (rl.rs:405-414)
+ * with z = tempered_logits(hidden . W, T, mask) (rl.rs:475-486), as nt_hip_rl_score computes
+ * them on written logits (same refusals and statuses: an excluded token has logp -inf, a token
+ * outside [0, vocab) gives NT_ROW_BAD_TOKEN and logp NaN), with the logits never written: the
+ * scoring pass of an RL step from the decoder's hidden states (decoder.rs:272,286). Shapes,
+ * packing and limits as nt_hip_rl_readout_sample; temperature > 0. Three launches: h into the
+ * matrix cores' order, the product with per-row records in its epilogue (block sums and, for
+ * the entropy, each block's sum of w (x c - ref)), then one workgroup per row that merges them
+ * and recomputes only the 32 logits of the token's block. */
+typedef struct NtRlReadoutScoreArgs {
+    const void *hidden;        /* [rows, ldh] bf16 */
+    const void *weight_packed; /* packed by nt_hip_rl_readout_pack_weight */
+    int64_t rows, vocab, dim, ldh;
+    int32_t mask_kind;         /* NT_MASK_NONE | NT_MASK_U8 */
+    int32_t pad0;
+    const void *mask;          /* u8 [rows, mask_ld] or NULL */
+    int64_t mask_ld;
+    double temperature;        /* > 0 and finite */
+    const int32_t *tokens;     /* [rows] device, or NULL when only the entropy is asked for */
+    float *logp;               /* [rows] out or NULL */
+    float *entropy;            /* [rows] out or NULL (one of logp, entropy) */
+    uint8_t *status;           /* [rows] out: NT_ROW_* */
+    float *logits;             /* debug: [rows, vocab] f32 out or NULL */
+} NtRlReadoutScoreArgs;
+int nt_hip_rl_readout_score(const NtRlReadoutScoreArgs *a);
+
 /* Fused row scoring: for each row, any of
  *   logp[r]     = token_log_probs(z, tokens)[r]                 (rl.rs:134-141)
  *   ref_logp[r] = token_log_probs(zr, tokens)[r]                (rl.rs:134-141, reference)

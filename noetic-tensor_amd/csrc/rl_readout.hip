@@ -71,12 +71,14 @@ struct ReadoutP {
     float *tmax;         // [rows][ntile] the tile's maximum of the allowed logits
     int *tfirst;         // [rows][ntile] the first column holding it
     float *bsum;         // [rows][nblk] the block's sum of 2^(x c - tref)
+    float *ebsum;        // [rows][nblk] the block's sum of 2^(x c - tref) (x c - tref) (ENT)
     float *logits;       // [rows][V] debug copy or null
 };
 
 // FIRST: the tile records carry each row's first column of the maximum (the greedy draw's
-// answer); the sampler otherwise needs only the maximum.
-template <bool MASK, bool DBG, bool FIRST>
+// answer); the sampler otherwise needs only the maximum. ENT: each block also records the sum
+// of w y over its columns (w = 2^y, y = x c - tref), the entropy's term.
+template <bool MASK, bool DBG, bool FIRST, bool ENT>
 __global__ __launch_bounds__(kRoThreads) void k_readout_tiles(ReadoutP p) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[kRoStages * kRoStageBytes];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -262,17 +264,29 @@ __global__ __launch_bounds__(kRoThreads) void k_readout_tiles(ReadoutP p) {
         const float wref = M == -INFINITY ? 0.0f : ref;
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            float w[16];
+            float w[16], wy[16];
 #pragma unroll
-            for (int v = 0; v < 16; v++) w[v] = __builtin_amdgcn_exp2f(fmaf(acc[i][j][v], p.c, -wref));
+            for (int v = 0; v < 16; v++) {
+                const float y = fmaf(acc[i][j][v], p.c, -wref);
+                w[v] = __builtin_amdgcn_exp2f(y);
+                // (an excluded column: y = -inf, w = 0, a term of 0)
+                if constexpr (ENT) wy[v] = w[v] * fmaxf(y, -FLT_MAX);
+            }
             // this half's 16 in a fixed tree, then the two halves (column 4 (l / 32) of each 8)
 #pragma unroll
             for (int span = 1; span < 16; span <<= 1)
 #pragma unroll
-                for (int e = 0; e < 16; e += 2 * span) w[e] = w[e] + w[e + span];
+                for (int e = 0; e < 16; e += 2 * span) {
+                    w[e] = w[e] + w[e + span];
+                    if constexpr (ENT) wy[e] = wy[e] + wy[e + span];
+                }
             const float other = __shfl_xor(w[0], 32, 64);
             const int blk = tile * (kRoCols / kRoBlock) + 2 * wave + j;
             if (hh == 0 && live && blk < p.nblk) p.bsum[int64_t(r) * p.nblk + blk] = w[0] + other;
+            if constexpr (ENT) {
+                const float eo = __shfl_xor(wy[0], 32, 64);
+                if (hh == 0 && live && blk < p.nblk) p.ebsum[int64_t(r) * p.nblk + blk] = wy[0] + eo;
+            }
         }
         if (wave == 0 && hh == 0 && live) {
             p.tref[int64_t(r) * p.ntile + tile] = ref;
@@ -295,9 +309,12 @@ struct ResolveP {
     const float *tref, *tmax;
     const int *tfirst;
     const float *bsum;
+    const float *ebsum;  // [rows][nblk] the entropy's block terms (scoring with entropy) or null
     const double *u;
-    int32_t *ids;
+    const int32_t *tokens;  // [rows] scoring: the token whose log-probability is asked for, or null
+    int32_t *ids;        // sampling: the draw
     float *logp;
+    float *ent;          // scoring: the entropy, or null
     uint8_t *status;
     float *dbg_block;  // [rows][32] the recomputed logits of the crossing block, or null
     int *dbg_index;    // [rows] that block's index, or null
@@ -363,9 +380,11 @@ __device__ __forceinline__ double wave_incl_scan(double v, int lane) {
 // banks.
 __device__ __forceinline__ int bs_slot(int b) { return b + (b >> 4); }
 
-template <int MAXB>
+// SCORE: the row's token (not a draw) picks the block, and the entropy comes from the records.
+template <int MAXB, bool SCORE>
 __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
     __shared__ double wsum[kResThreads / 64];
+    __shared__ double hsum[kResThreads / 64];
     __shared__ float wmax[kResThreads / 64];
     __shared__ int wsel[kResThreads / 64];
     __shared__ int wlast[kResThreads / 64];
@@ -387,10 +406,11 @@ __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
     for (int c = wave; c * 1024 < p.K * 2; c += 4)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(hres, (lds_ptr_t)(hrow + c * 1024), 16, c * 1024 + lane * 16, 0, 0,
                                                  0);
-    const double u_row = p.greedy ? 0.0 : p.u[row];
+    const double u_row = (SCORE || p.greedy) ? 0.0 : p.u[row];
+    const int tok = SCORE && p.tokens ? p.tokens[row] : -1;
     // The records, coalesced. (Every load reads a valid index and the unused ones are masked
     // after: a load under a condition becomes a branch of its own, with its wait before the next.)
-    float tm[kResMaxTiles], tr[kResMaxTiles], bv[MAXB];
+    float tm[kResMaxTiles], tr[kResMaxTiles], bv[MAXB], ev[MAXB];
 #pragma unroll
     for (int i = 0; i < kResMaxTiles; i++) {
         const int t = tid + i * kResThreads, tc = min(t, p.ntile - 1);
@@ -402,6 +422,7 @@ __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
 #pragma unroll
     for (int i = 0; i < MAXB; i++) {
         if (i < nb_rounds) bv[i] = bsum[min(tid + i * kResThreads, p.nblk - 1)];
+        if (SCORE && p.ebsum && i < nb_rounds) ev[i] = p.ebsum[int64_t(row) * p.nblk + min(tid + i * kResThreads, p.nblk - 1)];
     }
 #pragma unroll
     for (int i = 0; i < kResMaxTiles; i++) s_tr[tid + i * kResThreads] = tr[i];
@@ -414,8 +435,9 @@ __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
     auto refuse = [&](uint8_t st) {
         wait_vmcnt<0>();
         if (tid == 0) {
-            p.ids[row] = -1;
+            if (p.ids) p.ids[row] = -1;
             if (p.logp) p.logp[row] = NAN;
+            if (p.ent) p.ent[row] = NAN;
             p.status[row] = st;
         }
     };
@@ -461,6 +483,26 @@ __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
     }
     const double incl_w = wave_incl_scan(run, lane);
     if (lane == 63) wsum[wave] = incl_w;
+    if constexpr (SCORE) {
+        // the entropy's sum relative to A, sum_v 2^(x c - A) (x c - A): per block
+        // 2^(ref - A) (E + (ref - A) B) from its records, over this thread's blocks in order
+        double hp = 0.0;
+        if (p.ebsum) {
+#pragma unroll
+            for (int i = 0; i < MAXB; i++) {
+                const int b = tid + i * kResThreads;
+                if (i < nb_rounds && b < p.nblk) {
+                    const float r = s_tr[b / (kRoCols / kRoBlock)];
+                    if (r != -INFINITY) {
+                        const double d = double(r) - double(A);
+                        hp += double(__builtin_amdgcn_exp2f(r - A)) * (double(ev[i]) + d * double(bv[i]));
+                    }
+                }
+            }
+        }
+        const double incl_h = wave_incl_scan(hp, lane);
+        if (lane == 63) hsum[wave] = incl_h;
+    }
     __syncthreads();  // (2) the waves' totals
     double before = 0.0;
     for (int w2 = 0; w2 < wave; w2++) before += wsum[w2];
@@ -472,7 +514,27 @@ __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
         return;
     }
     const double shiftA = double(A) - double(M) * double(p.c);
-    if (p.greedy) {
+    if constexpr (SCORE) {
+        // H = ln S - ln2 (sum 2^(x c - A) (x c - A)) / S, both sums relative to A
+        const double Hall = (((0.0 + hsum[0]) + hsum[1]) + hsum[2]) + hsum[3];
+        const bool tok_ok = tok >= 0 && tok < p.V;
+        if (!p.logp || !tok_ok) {
+            wait_vmcnt<0>();
+            if (tid == 0) {
+                if (p.ent) p.ent[row] = float(log(Sall) - kLn2 * Hall / Sall);
+                if (p.logp) p.logp[row] = NAN;
+                p.status[row] = (p.tokens && !tok_ok) ? NT_ROW_BAD_TOKEN : NT_ROW_OK;
+            }
+            return;
+        }
+        if (tid == 0) {
+            if (p.ent) p.ent[row] = float(log(Sall) - kLn2 * Hall / Sall);
+            s_blk = tok / kRoBlock;
+            s_ref = s_tr[tok / kRoCols];
+            s_tl = 0.0;
+        }
+        __syncthreads();  // (3) the block
+    } else if (p.greedy) {
         wait_vmcnt<0>();
         const double lnS = log(Sall) + shiftA * kLn2;
         // the first column holding the maximum: the first tile whose maximum it is
@@ -497,7 +559,7 @@ __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
     // ---- the block holding t = u S: the first thread whose inclusive prefix passes t (with
     // weight), then its blocks in order; rounding that leaves no crossing takes the last weight
     const double t = u_row * Sall;
-    {
+    if constexpr (!SCORE) {
         const uint64_t cross = __ballot(incl > t && run > 0.0);
         const uint64_t any = __ballot(run > 0.0);
         if (lane == 0) wsel[wave] = cross ? wave * 64 + __builtin_ctzll(cross) : -1;
@@ -627,6 +689,16 @@ __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
     if (p.dbg_block && lane < 32) p.dbg_block[int64_t(row) * 32 + lane] = x;
     if (p.dbg_index && lane == 0) p.dbg_index[row] = bstar;
     x = keep ? x : -INFINITY;
+    if constexpr (SCORE) {
+        // the token's log-probability (an excluded token: -inf)
+        if (lane == tok % kRoBlock) {
+            const float zt = p.tau_one ? x : x / p.tau;
+            const float mz = p.tau_one ? M : M / p.tau;
+            p.logp[row] = float((double(zt) - double(mz)) - lnS);
+            p.status[row] = NT_ROW_OK;
+        }
+        return;
+    }
     const float w = keep ? __builtin_amdgcn_exp2f(fmaf(x, p.c, -r)) : 0.0f;
     const double cw = wave_incl_scan(double(w), lane);
     int lsel = -1;
@@ -734,68 +806,86 @@ extern "C" int nt_hip_rl_readout_pack_weight(const void *weight, int32_t layout,
               : launch_pack_t<false, true>(weight, int(vocab), int(dim), ld, packed);
 }
 
-extern "C" int nt_hip_rl_readout_sample(const NtRlReadoutSampleArgs *a) {
-    const char *who = "nt_hip_rl_readout_sample";
-    if (!a) return fail(NT_E_ARG, std::string(who) + ": null args");
-    const int64_t rows = a->rows, V = a->vocab, K = a->dim;
-    if (rows < 0 || rows > kRoRows || V < 1 || V > kRoMaxVocab || K < 16 || K % 16 != 0 || K > kResMaxK || a->ldh < K ||
-        a->ldh % 8 != 0 || rows * a->ldh * 2 >= (int64_t(1) << 31) ||
+namespace nt {
+namespace {
+
+// One readout call of either entry point: the checks they share, h into fragment order, pass 1
+// and the resolve, on the library stream.
+struct ReadoutCall {
+    const char *who;
+    const void *hidden, *weight_packed, *mask;
+    int64_t rows, V, K, ldh, mask_ld;
+    int32_t mask_kind;
+    double T;                  // > 0 (1 when greedy)
+    bool greedy, score;
+    const double *u;           // sampling
+    const int32_t *tokens;     // scoring
+    int32_t *ids;              // sampling
+    float *logp, *ent;         // ent: scoring
+    uint8_t *status;
+    float *logits, *dbg_block;
+    int32_t *dbg_index;
+};
+
+int readout_run(const ReadoutCall &c) {
+    const char *who = c.who;
+    const int64_t rows = c.rows, V = c.V, K = c.K;
+    if (rows < 0 || rows > kRoRows || V < 1 || V > kRoMaxVocab || K < 16 || K % 16 != 0 || K > kResMaxK || c.ldh < K ||
+        c.ldh % 8 != 0 || rows * c.ldh * 2 >= (int64_t(1) << 31) ||
         (V + kRoCols - 1) / kRoCols * (K / 16) * 8192 >= (int64_t(1) << 31))
         return fail(NT_E_ARG, std::string(who) + ": rows " + std::to_string(rows) + " (at most 256), vocab " +
                                   std::to_string(V) + " (at most 262144), dim " + std::to_string(K) +
                                   " (a multiple of 16, at most 16384), ldh (>= dim, a multiple of 8)");
-    if (a->mask_kind != NT_MASK_NONE && a->mask_kind != NT_MASK_U8)
+    if (c.mask_kind != NT_MASK_NONE && c.mask_kind != NT_MASK_U8)
         return fail(NT_E_UNSUPPORTED, std::string(who) + ": only no mask or a u8 keep-mask");
-    if ((a->mask_kind == NT_MASK_U8) != (a->mask != nullptr))
+    if ((c.mask_kind == NT_MASK_U8) != (c.mask != nullptr))
         return fail(NT_E_ARG, std::string(who) + ": mask kind and mask pointer disagree");
-    if (a->mask && a->mask_ld < V)
-        return fail(NT_E_ARG, std::string(who) + ": mask_ld " + std::to_string(a->mask_ld) +
+    if (c.mask && c.mask_ld < V)
+        return fail(NT_E_ARG, std::string(who) + ": mask_ld " + std::to_string(c.mask_ld) +
                                   " (one mask row of at least vocab bytes per logits row)");
-    if (!a->hidden || !a->weight_packed || !a->ids || !a->status || reinterpret_cast<uintptr_t>(a->hidden) % 16 ||
-        reinterpret_cast<uintptr_t>(a->weight_packed) % 16)
-        return fail(NT_E_ARG, std::string(who) + ": null or unaligned hidden, packed weight, ids or status");
-    if (!(a->temperature >= 0.0) || !std::isfinite(a->temperature))
-        return fail(NT_E_ARG, "sample_categorical: temperature " + std::to_string(a->temperature) + " (must be ≥ 0)");
-    const bool greedy = a->temperature == 0.0;
-    if (!greedy && !a->uniforms) return fail(NT_E_ARG, std::string(who) + ": null uniforms");
+    if (!c.hidden || !c.weight_packed || !c.status || reinterpret_cast<uintptr_t>(c.hidden) % 16 ||
+        reinterpret_cast<uintptr_t>(c.weight_packed) % 16)
+        return fail(NT_E_ARG, std::string(who) + ": null or unaligned hidden or packed weight, or null status");
     std::unique_lock<std::mutex> lk;
     if (int rc = enter(&lk)) return rc;
     if (rows == 0) return 0;
+    const bool ent = c.score && c.ent;
     const int ntile = int((V + kRoCols - 1) / kRoCols), nblk = int((V + kRoBlock - 1) / kRoBlock);
-    const size_t rec = size_t(rows) * size_t(ntile) * 4;
+    const size_t rec = size_t(rows) * size_t(ntile) * 4, brec = size_t(rows) * size_t(nblk) * 4;
     const size_t hpack = size_t((rows + 31) / 32) * size_t(K / 16) * 1024;
-    const size_t need = hpack + 3 * rec + size_t(rows) * size_t(nblk) * 4;
+    const size_t need = hpack + 3 * rec + (ent ? 2 : 1) * brec;
     void *ws = nullptr;
     if (int rc = scratch_alloc(need, &ws)) return rc;
     uint8_t *wb = static_cast<uint8_t *>(ws);
     // h into fragment order (2 MB at 256 rows of 4096)
-    if (int rc = launch_pack_t<false, false>(a->hidden, int(rows), int(K), a->ldh, wb)) return rc;
-    const double T = greedy ? 1.0 : a->temperature;
+    if (int rc = launch_pack_t<false, false>(c.hidden, int(rows), int(K), c.ldh, wb)) return rc;
     ReadoutP p;
     p.hp = wb;
-    p.wp = static_cast<const uint8_t *>(a->weight_packed);
+    p.wp = static_cast<const uint8_t *>(c.weight_packed);
     p.rows = int(rows);
     p.V = int(V);
     p.K = int(K);
     p.ntile = ntile;
     p.nblk = nblk;
-    p.mask = static_cast<const uint8_t *>(a->mask);
-    p.mask_ld = a->mask_ld;
-    p.mask_vec = a->mask && a->mask_ld % 16 == 0 && reinterpret_cast<uintptr_t>(a->mask) % 16 == 0;
-    p.c = T == 1.0 ? kLog2e : float(double(kLog2e) / double(float(T)));
+    p.mask = static_cast<const uint8_t *>(c.mask);
+    p.mask_ld = c.mask_ld;
+    p.mask_vec = c.mask && c.mask_ld % 16 == 0 && reinterpret_cast<uintptr_t>(c.mask) % 16 == 0;
+    p.c = c.T == 1.0 ? kLog2e : float(double(kLog2e) / double(float(c.T)));
     p.tref = reinterpret_cast<float *>(wb + hpack);
     p.tmax = reinterpret_cast<float *>(wb + hpack + rec);
     p.tfirst = reinterpret_cast<int *>(wb + hpack + 2 * rec);
     p.bsum = reinterpret_cast<float *>(wb + hpack + 3 * rec);
-    p.logits = a->logits;
+    p.ebsum = ent ? reinterpret_cast<float *>(wb + hpack + 3 * rec + brec) : nullptr;
+    p.logits = c.logits;
     hipStream_t st = ctx().stream;
     const dim3 g1{unsigned(ntile), 1, 1}, b1{unsigned(kRoThreads), 1, 1};
     auto launch1 = [&](auto mask_c, auto dbg_c) {
         constexpr bool MK = decltype(mask_c)::value, DB = decltype(dbg_c)::value;
-        if (greedy) hipLaunchKernelGGL((k_readout_tiles<MK, DB, true>), g1, b1, 0, st, p);
-        else hipLaunchKernelGGL((k_readout_tiles<MK, DB, false>), g1, b1, 0, st, p);
+        if (c.greedy) hipLaunchKernelGGL((k_readout_tiles<MK, DB, true, false>), g1, b1, 0, st, p);
+        else if (ent) hipLaunchKernelGGL((k_readout_tiles<MK, DB, false, true>), g1, b1, 0, st, p);
+        else hipLaunchKernelGGL((k_readout_tiles<MK, DB, false, false>), g1, b1, 0, st, p);
     };
-    if (a->logits) {
+    if (c.logits) {
         if (p.mask) launch1(std::true_type{}, std::true_type{});
         else launch1(std::false_type{}, std::true_type{});
     } else {
@@ -804,34 +894,106 @@ extern "C" int nt_hip_rl_readout_sample(const NtRlReadoutSampleArgs *a) {
     }
     if (int rc = launched(who)) return rc;
     ResolveP q;
-    q.h = static_cast<const uint16_t *>(a->hidden);
+    q.h = static_cast<const uint16_t *>(c.hidden);
     q.wp = p.wp;
     q.rows = p.rows;
     q.V = p.V;
     q.K = p.K;
-    q.ldh = int(a->ldh);
+    q.ldh = int(c.ldh);
     q.ntile = ntile;
     q.nblk = nblk;
     q.mask = p.mask;
     q.mask_ld = p.mask_ld;
     q.c = p.c;
-    q.tau = float(T);
-    q.tau_one = T == 1.0;
-    q.greedy = greedy;
+    q.tau = float(c.T);
+    q.tau_one = c.T == 1.0;
+    q.greedy = c.greedy;
     q.tref = p.tref;
     q.tmax = p.tmax;
     q.tfirst = p.tfirst;
     q.bsum = p.bsum;
-    q.u = a->uniforms;
-    q.ids = a->ids;
-    q.logp = a->logp;
-    q.status = a->status;
-    q.dbg_block = a->debug_block;
-    q.dbg_index = a->debug_block_index;
-    if (nblk <= 16 * kResThreads)
-        hipLaunchKernelGGL(k_readout_resolve<16>, dim3(unsigned(rows)), dim3(kResThreads), 0, st, q);
-    else
-        hipLaunchKernelGGL(k_readout_resolve<kResMaxBlocks>, dim3(unsigned(rows)), dim3(kResThreads), 0, st, q);
+    q.ebsum = p.ebsum;
+    q.u = c.u;
+    q.tokens = c.tokens;
+    q.ids = c.ids;
+    q.logp = c.logp;
+    q.ent = c.ent;
+    q.status = c.status;
+    q.dbg_block = c.dbg_block;
+    q.dbg_index = c.dbg_index;
+    const dim3 g2{unsigned(rows), 1, 1}, b2{unsigned(kResThreads), 1, 1};
+    const bool small = nblk <= 16 * kResThreads;
+    if (c.score) {
+        if (small) hipLaunchKernelGGL((k_readout_resolve<16, true>), g2, b2, 0, st, q);
+        else hipLaunchKernelGGL((k_readout_resolve<kResMaxBlocks, true>), g2, b2, 0, st, q);
+    } else {
+        if (small) hipLaunchKernelGGL((k_readout_resolve<16, false>), g2, b2, 0, st, q);
+        else hipLaunchKernelGGL((k_readout_resolve<kResMaxBlocks, false>), g2, b2, 0, st, q);
+    }
     if (int rc = launched(who)) return rc;
     return scratch_release(ws);
+}
+
+}  // namespace
+}  // namespace nt
+
+extern "C" int nt_hip_rl_readout_sample(const NtRlReadoutSampleArgs *a) {
+    const char *who = "nt_hip_rl_readout_sample";
+    if (!a) return fail(NT_E_ARG, std::string(who) + ": null args");
+    if (!(a->temperature >= 0.0) || !std::isfinite(a->temperature))
+        return fail(NT_E_ARG, "sample_categorical: temperature " + std::to_string(a->temperature) + " (must be ≥ 0)");
+    const bool greedy = a->temperature == 0.0;
+    if (!greedy && !a->uniforms) return fail(NT_E_ARG, std::string(who) + ": null uniforms");
+    if (!a->ids) return fail(NT_E_ARG, std::string(who) + ": null ids");
+    ReadoutCall c{};
+    c.who = who;
+    c.hidden = a->hidden;
+    c.weight_packed = a->weight_packed;
+    c.mask = a->mask;
+    c.rows = a->rows;
+    c.V = a->vocab;
+    c.K = a->dim;
+    c.ldh = a->ldh;
+    c.mask_ld = a->mask_ld;
+    c.mask_kind = a->mask_kind;
+    c.T = greedy ? 1.0 : a->temperature;
+    c.greedy = greedy;
+    c.score = false;
+    c.u = a->uniforms;
+    c.ids = a->ids;
+    c.logp = a->logp;
+    c.status = a->status;
+    c.logits = a->logits;
+    c.dbg_block = a->debug_block;
+    c.dbg_index = a->debug_block_index;
+    return readout_run(c);
+}
+
+extern "C" int nt_hip_rl_readout_score(const NtRlReadoutScoreArgs *a) {
+    const char *who = "nt_hip_rl_readout_score";
+    if (!a) return fail(NT_E_ARG, std::string(who) + ": null args");
+    if (!(a->temperature > 0.0) || !std::isfinite(a->temperature))
+        return fail(NT_E_ARG, "tempered_logits: temperature " + std::to_string(a->temperature) + " (must be positive)");
+    if (a->logp && !a->tokens) return fail(NT_E_ARG, std::string(who) + ": log-probabilities need tokens");
+    if (!a->logp && !a->entropy) return fail(NT_E_ARG, std::string(who) + ": neither logp nor entropy asked for");
+    ReadoutCall c{};
+    c.who = who;
+    c.hidden = a->hidden;
+    c.weight_packed = a->weight_packed;
+    c.mask = a->mask;
+    c.rows = a->rows;
+    c.V = a->vocab;
+    c.K = a->dim;
+    c.ldh = a->ldh;
+    c.mask_ld = a->mask_ld;
+    c.mask_kind = a->mask_kind;
+    c.T = a->temperature;
+    c.greedy = false;
+    c.score = true;
+    c.tokens = a->tokens;
+    c.logp = a->logp;
+    c.ent = a->entropy;
+    c.status = a->status;
+    c.logits = a->logits;
+    return readout_run(c);
 }

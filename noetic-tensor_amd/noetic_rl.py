@@ -60,6 +60,14 @@ class NtRlReadoutSampleArgs(C.Structure):
                 ("logits", C.c_void_p), ("debug_block", C.c_void_p), ("debug_block_index", C.c_void_p)]
 
 
+class NtRlReadoutScoreArgs(C.Structure):
+    _fields_ = [("hidden", C.c_void_p), ("weight_packed", C.c_void_p), ("rows", C.c_int64), ("vocab", C.c_int64),
+                ("dim", C.c_int64), ("ldh", C.c_int64), ("mask_kind", C.c_int32),
+                ("pad0", C.c_int32), ("mask", C.c_void_p), ("mask_ld", C.c_int64), ("temperature", C.c_double),
+                ("tokens", C.c_void_p), ("logp", C.c_void_p), ("entropy", C.c_void_p), ("status", C.c_void_p),
+                ("logits", C.c_void_p)]
+
+
 class NtRlScoreArgs(C.Structure):
     _fields_ = [("logits", C.c_void_p), ("ref_logits", C.c_void_p), ("dtype", C.c_int32),
                 ("mask_kind", C.c_int32), ("rows", C.c_int64), ("vocab", C.c_int64), ("ld", C.c_int64),
@@ -128,6 +136,7 @@ _SIGS = {
     "nt_hip_rl_sample": (C.c_int, [C.POINTER(NtRlSampleArgs)]),
     "nt_hip_rl_sample_gumbel": (C.c_int, [C.POINTER(NtRlGumbelArgs)]),
     "nt_hip_rl_readout_sample": (C.c_int, [C.POINTER(NtRlReadoutSampleArgs)]),
+    "nt_hip_rl_readout_score": (C.c_int, [C.POINTER(NtRlReadoutScoreArgs)]),
     "nt_hip_rl_readout_packed_bytes": (C.c_int64, [C.c_int64, C.c_int64]),
     "nt_hip_rl_readout_pack_weight": (C.c_int, [C.c_void_p, C.c_int32, C.c_int64, C.c_int64, C.c_int64, C.c_void_p]),
     "nt_hip_rl_sample_noalloc": (C.c_int, [C.POINTER(NtRlSampleArgs)]),
@@ -602,6 +611,45 @@ def readout_sample_logp(hidden: Tensor, weight: PackedReadout, temperature: floa
         if bad.size:
             raise ValueError(f"sample_categorical: position {bad[0]} has no allowed token (every logit −∞ or a NaN)")
     return (ids, lp, *dbg) if debug else (ids, lp)
+
+
+def readout_score(hidden: Tensor, weight: PackedReadout, temperature: float, mask: Optional[Tensor],
+                  tokens: Optional[Tensor], entropy: bool = True, debug: bool = False):
+    """The scoring pass fused with the readout: logits = hidden [rows, d] . W (decoder.rs:272,286)
+    tempered and masked (rl.rs:475-486), then token_log_probs (rl.rs:134-141) of `tokens` and, with
+    `entropy`, categorical_entropy (rl.rs:405-414) per row, as `score` gives them on written
+    logits, the logits never written. Returns (logp or None, entropy or None), plus with `debug`
+    the f32 logits [rows, V]."""
+    if not (temperature > 0.0 and math.isfinite(temperature)):
+        raise ValueError(f"tempered_logits: temperature {temperature} (must be positive)")
+    if hidden.dtype != "bf16" or len(hidden.shape) != 2:
+        raise ValueError("readout: hidden [rows, d] in bf16")
+    rows, d = hidden.shape
+    V = weight.vocab
+    if weight.dim != d:
+        raise ValueError(f"readout: hidden's d {d} against the weight's {weight.dim}")
+    if tokens is not None and (tokens.dtype != "i32" or tokens.numel != rows):
+        raise ValueError("token_log_probs: tokens [rows] (i32)")
+    if tokens is None and not entropy:
+        raise ValueError("readout_score: neither log-probabilities nor the entropy asked for")
+    if mask is not None and (mask.dtype != "u8" or mask.numel != rows * V):
+        raise ValueError("readout: a u8 keep-mask [rows, V]")
+    lp = Tensor((rows,), "f32") if tokens is not None else None
+    ent = Tensor((rows,), "f32") if entropy else None
+    status = Tensor((rows,), "u8")
+    logits = Tensor((rows, V), "f32") if debug else None
+    ptr = lambda t: None if t is None else t.ptr
+    a = NtRlReadoutScoreArgs(hidden.ptr, weight.buf.ptr, rows, V, d, d,
+                             NT_MASK_U8 if mask is not None else NT_MASK_NONE, 0, ptr(mask),
+                             V if mask is not None else 0, float(temperature), ptr(tokens), ptr(lp), ptr(ent),
+                             status.ptr, ptr(logits))
+    _check(lib().nt_hip_rl_readout_score(C.byref(a)), "readout score")
+    if tokens is not None:
+        st = status.to_numpy().ravel()
+        bad = np.nonzero(st == NT_ROW_BAD_TOKEN)[0]
+        if bad.size:
+            raise IndexError(f"gather index out of range {V} at position {bad[0]}")
+    return (lp, ent, logits) if debug else (lp, ent)
 
 
 def _score(policy, ref, tokens, want_logp, want_ref_logp, want_kl, want_ent, want_stats=False):

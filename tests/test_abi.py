@@ -46,7 +46,8 @@ def test_argument_struct_layouts_match_the_header():
               "NtRlScoreGradArgs": [f[0] for f in nr.NtRlScoreGradArgs._fields_],
               "NtRlPolicyLossArgs": [f[0] for f in nr.NtRlPolicyLossArgs._fields_],
               "NtRlGumbelArgs": [f[0] for f in nr.NtRlGumbelArgs._fields_],
-              "NtRlReadoutSampleArgs": [f[0] for f in nr.NtRlReadoutSampleArgs._fields_]}
+              "NtRlReadoutSampleArgs": [f[0] for f in nr.NtRlReadoutSampleArgs._fields_],
+              "NtRlReadoutScoreArgs": [f[0] for f in nr.NtRlReadoutScoreArgs._fields_]}
     body = []
     for st, fs in fields.items():
         body.append(f'printf("{st} %zu\\n", sizeof({st}));')
@@ -67,6 +68,7 @@ def test_argument_struct_layouts_match_the_header():
     assert int(got["NtRlSampleArgs"]) == 104 and int(got["NtRlScoreArgs"]) == 152
     assert int(got["NtRlScoreGradArgs"]) == 176 and int(got["NtRlPolicyLossArgs"]) == 120
     assert int(got["NtRlGumbelArgs"]) == 128 and int(got["NtRlReadoutSampleArgs"]) == 136
+    assert int(got["NtRlReadoutScoreArgs"]) == 120
 
 
 def test_without_a_claimed_device_calls_fail_cleanly():
