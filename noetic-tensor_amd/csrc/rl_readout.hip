@@ -422,7 +422,12 @@ __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
 #pragma unroll
     for (int i = 0; i < MAXB; i++) {
         if (i < nb_rounds) bv[i] = bsum[min(tid + i * kResThreads, p.nblk - 1)];
-        if (SCORE && p.ebsum && i < nb_rounds) ev[i] = p.ebsum[int64_t(row) * p.nblk + min(tid + i * kResThreads, p.nblk - 1)];
+    }
+    if (SCORE && p.ebsum) {
+        // every slot loaded (a clamped index), so that the loads issue together
+        const float *eb = p.ebsum + int64_t(row) * p.nblk;
+#pragma unroll
+        for (int i = 0; i < MAXB; i++) ev[i] = eb[min(tid + i * kResThreads, p.nblk - 1)];
     }
 #pragma unroll
     for (int i = 0; i < kResMaxTiles; i++) s_tr[tid + i * kResThreads] = tr[i];
