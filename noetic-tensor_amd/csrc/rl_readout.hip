@@ -116,7 +116,10 @@ __global__ __launch_bounds__(kRoThreads) void k_readout_tiles(ReadoutP p) {
     // maximum and first column over its 32 (in column order) and the partner's; the four waves'
     // go through LDS (one barrier), then each lane weighs its 32 against the tile's reference and
     // sums each 32-column block with the partner's half.
-    const int rw = lane & 31, hh = lane >> 5;
+    // (the lane index again, from the exec mask's count below this lane: keeping the thread id
+    // live through the loop would take a register the loop needs)
+    const int el = int(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)));
+    const int rw = el & 31, hh = el >> 5;
     const int cw0 = n0 + 64 * wave + 4 * hh;  // column of acc[i][0][0]; + 32 j + 8 a + b
     // The tile's mask (256 rows x 256 bytes) comes into LDS by coalesced 1 KiB copies, four rows
     // each, over the stages (every wave is past its last read of them after the barrier). Row r's
@@ -137,7 +140,7 @@ __global__ __launch_bounds__(kRoThreads) void k_readout_tiles(ReadoutP p) {
 #pragma unroll
         for (int qq = 0; qq < kRoRows / 16; qq++) {
             const int q = 4 * qq + wave;  // four rows per copy, copy q by wave q % 4
-            const int r = 4 * q + (lane >> 4), pos = lane & 15, k = (pos - r) & 15;
+            const int r = 4 * q + (el >> 4), pos = el & 15, k = (pos - r) & 15;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(mres, (lds_ptr_t)(lmask + q * 1024), 16,
                                                      int(int64_t(r) * p.mask_ld) + n0 + 16 * k, 0, 0, 0);
         }
