@@ -109,6 +109,12 @@ def test_readout_sampler_small_shapes(rows, V, d, tau, masked):
     run_case(f"r{rows}v{V}d{d}t{tau}m{int(masked)}", rows, V, d, tau, masked, seed=rows + V + d)
 
 
+@pytest.mark.parametrize("tau,masked", [(0.7, True), (0.0, True)])
+def test_readout_sampler_above_131072_columns(tau, masked):
+    # V 151936 (benchmark configuration 5's vocabulary): the resolve's larger per-thread arrays
+    run_case(f"r24v151936d64t{tau}", 24, 151936, 64, tau, masked, seed=151936)
+
+
 def test_readout_sampler_at_the_decode_shape():
     # C4's decode step: 256 rows, d 4096, V 128256, a 30% keep-mask, T 0.7
     run_case("c4 readout", 256, 128256, 4096, 0.7, True, seed=2024, check_gemm_rows=np.arange(0, 256, 16))

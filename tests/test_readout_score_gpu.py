@@ -78,7 +78,8 @@ def run_case(name, rows, V, d, tau, masked, seed):
     print(f"{name}: {rows} rows, logp max |d| {e1:.1e}, entropy max |d| {e2:.1e}")
 
 
-@pytest.mark.parametrize("rows,V,d", [(40, 1000, 256), (256, 4104, 512), (1, 300, 64), (97, 257, 16), (64, 600, 528)])
+@pytest.mark.parametrize("rows,V,d", [(40, 1000, 256), (256, 4104, 512), (1, 300, 64), (97, 257, 16), (64, 600, 528),
+                                      (24, 151936, 64)])
 @pytest.mark.parametrize("tau,masked", [(0.7, True), (1.0, False)])
 def test_readout_scorer_small_shapes(rows, V, d, tau, masked):
     run_case(f"r{rows}v{V}d{d}t{tau}m{int(masked)}", rows, V, d, tau, masked, seed=rows + V + d + 1)
