@@ -866,7 +866,10 @@ int readout_run(const ReadoutCall &c) {
     if (int rc = scratch_alloc(need, &ws)) return rc;
     uint8_t *wb = static_cast<uint8_t *>(ws);
     // h into fragment order (2 MB at 256 rows of 4096)
-    if (int rc = launch_pack_t<false, false>(c.hidden, int(rows), int(K), c.ldh, wb)) return rc;
+    if (int rc = launch_pack_t<false, false>(c.hidden, int(rows), int(K), c.ldh, wb)) {
+        scratch_release(ws);
+        return rc;
+    }
     ReadoutP p;
     p.hp = wb;
     p.wp = static_cast<const uint8_t *>(c.weight_packed);
@@ -900,7 +903,10 @@ int readout_run(const ReadoutCall &c) {
         if (p.mask) launch1(std::true_type{}, std::false_type{});
         else launch1(std::false_type{}, std::false_type{});
     }
-    if (int rc = launched(who)) return rc;
+    if (int rc = launched(who)) {
+        scratch_release(ws);
+        return rc;
+    }
     ResolveP q;
     q.h = static_cast<const uint16_t *>(c.hidden);
     q.wp = p.wp;
@@ -938,8 +944,9 @@ int readout_run(const ReadoutCall &c) {
         if (small) hipLaunchKernelGGL((k_readout_resolve<16, false>), g2, b2, 0, st, q);
         else hipLaunchKernelGGL((k_readout_resolve<kResMaxBlocks, false>), g2, b2, 0, st, q);
     }
-    if (int rc = launched(who)) return rc;
-    return scratch_release(ws);
+    const int rc = launched(who);
+    const int rf = scratch_release(ws);
+    return rc ? rc : rf;
 }
 
 }  // namespace
