@@ -9,8 +9,11 @@ library's own stream; the same launches re-reading one input are reported as `wa
 bytes per launch / average launch time against the 8 TB/s HBM peak) and a `cpu_baseline`
 object (the reference's Cpu(Reference) op sequence, restated in oracle/, timed on this host).
 
-`--workload c4s|c2|c3|c3b|c5|matmul` measures the other configurations the same way, one JSON line each:
+`--workload c4s|c4g|c2|c3|c3b|c5|matmul|readout` measures the other configurations the same way, one JSON
+line each:
   c4s C4 with one u8 grammar mask [1,V] shared by every row (mask_ld 0);
+  c4g C4's rows through the reference's own Gumbel-max sample_categorical (one u64 per logit,
+      generated on the device at the stream's position; nt_hip_rl_sample_gumbel);
   c2  decode step, f32 [1,64,1,32000], no mask, tau 0.8: the fused sample + logp;
   c3  PPO scoring, bf16 policy + reference [8,16,512,50304]: logp, reference logp, exact KL,
       entropy (nt_hip_rl_score) and the k3 per-token KL (nt_hip_rl_kl_estimate);
@@ -368,6 +371,68 @@ def bench_sample(nr, W, args, name):
         # timed region) is the line's own object
         if "parity" in out["cpu_baseline"]:
             out["parity"] = out["cpu_baseline"].pop("parity")
+    return out
+
+
+def bench_gumbel(nr, W, args):
+    """c4g: the reference's own sampler, Gumbel-max sample_categorical (rl.rs:488-529), at C4's
+    shape on the device: one launch of nt_hip_rl_sample_gumbel per step, each draw's u64 generated
+    where it is used (ChaCha20 at the stream's word position, one u64 per logit in row-major
+    order), each launch at its own position of one stream. Inputs cycle over the same HBM-cold
+    copies as c4. The CPU baseline is the same op sequence on Cpu(Reference) and Cpu(Fast)."""
+    from oracle import oracle as O
+    w = W.c4(args.seed)
+    rows, V = w["rows"], w["V"]
+    per_row = 2 * V + V + 4 + 1  # logits, mask, id, status (the draws are generated, not read)
+    bytes_launch = per_row * rows
+    copies = max(2, -(-CACHE_BYTES // bytes_launch))
+    ws = [w] + [W.c4(args.seed + 1 + k) for k in range(copies - 1)]
+    rng = nr.Rng(args.seed, "c4g/stream")
+    key = rng.key()
+    block0, word0 = rng.word_pos()
+    blocks_per_launch = rows * V // 8  # one u64 per logit, eight to a 64-byte keystream block
+    ids, st = nr.IntTensor((rows,)), nr.Tensor((rows,), "u8")
+    L = nr.lib()
+
+    def argv(x, i):
+        return nr.NtRlGumbelArgs(x["logits"].ptr, nr.NT_BF16, nr.NT_MASK_U8, rows, V, V, x["mask"].ptr, V,
+                                 w["temperature"], key, block0 + i * blocks_per_launch, word0, 0, ids.ptr, st.ptr)
+
+    n_launch = args.warmup + args.steps
+    cold = [argv(ws[i % copies], i) for i in range(n_launch)]
+    warm = [argv(w, i) for i in range(n_launch)]
+    nr._check(L.nt_hip_rl_sample_gumbel(C.byref(cold[0])), "sample_gumbel")
+    warm_s = clock_warmup(nr, lambda i: L.nt_hip_rl_sample_gumbel(C.byref(cold[i % len(cold)])), args.clock_warmup)
+    ms, wall = timed(nr, args.steps, args.warmup, lambda i: L.nt_hip_rl_sample_gumbel(C.byref(cold[i])))
+    if np.any(st.to_numpy() != 0):
+        raise SystemExit("bench c4g: refused rows")
+    ms_warm, _ = timed(nr, args.steps, args.warmup, lambda i: L.nt_hip_rl_sample_gumbel(C.byref(warm[i])))
+    # parity, outside the timed regions: launch 0 (copy 0, the stream's start) against the
+    # oracle's Cpu(Reference) op sequence on the same stream, for the first rows
+    nr._check(L.nt_hip_rl_sample_gumbel(C.byref(cold[0])), "sample_gumbel")
+    n_par = min(32, rows)
+    dev = ids.to_numpy().ravel()[:n_par].astype(np.int64)
+    x = W.bf16_to_f32(w["logits"].to_numpy().reshape(rows, V)[:n_par])
+    keep = w["mask"].to_numpy().reshape(rows, V)[:n_par]
+    cpu = O.cpuref_sample_gumbel(x, w["temperature"], O.Rng(args.seed, "c4g/stream"), keep=keep)
+    roof = roofline(bytes_launch, ms)
+    roof["inputs"] = (f"HBM-cold: launches cycle over {copies} input copies "
+                      f"({copies * bytes_launch / 2**20:.0f} MiB), beyond the 256 MB Infinity Cache")
+    roof["note"] = ("bound by generating the draws (a ChaCha20 block per 8 logits and two f64 logarithms per "
+                    "allowed logit), not by HBM")
+    roof["warm_cache"] = {"ms": ms_warm, "achieved": bytes_launch / (ms_warm * 1e-3) / 1e9,
+                          "frac": bytes_launch / (ms_warm * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    config = {"workload": "c4 rows through the reference's Gumbel-max sample_categorical: bf16 logits "
+                          "[1,256,1,128256] ~ N(0,2^2), u8 grammar mask of contiguous runs (~30% kept), temperature "
+                          "0.7, one u64 of the caller's ChaCha20 stream per logit; launches cycle over independent "
+                          "input copies (1 GiB in all)", "rows": rows, "vocab": V, "parallelism": "none (1 GPU)"}
+    out = line("rows/sec, the reference's Gumbel-max sample_categorical at c4's shape (V=128256 bf16, u8 mask)",
+               rows / (ms * 1e-3), args.steps, args.warmup, ms, "bf16", config, roof, wall_s_timed_region=wall,
+               key=nr.key(), clock_warmup_s=round(warm_s, 3),
+               parity={"rows": n_par, "ids_differ_from_cpuref": int(np.sum(dev != cpu)),
+                       "what": "device draws against Cpu(Reference)'s op sequence for the same stream"})
+    if args.cpu_rows > 0:
+        out["cpu_baseline"] = cpu_baseline(w, min(args.cpu_rows, rows), args.seed, args.cpu_seconds)
     return out
 
 
@@ -801,7 +866,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 20; 3 for c3/c5)")
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--workload", default="c4",
-                    choices=["c4", "c4s", "c2", "c3", "c3b", "c5", "ops", "readout", "matmul"])
+                    choices=["c4", "c4s", "c4g", "c2", "c3", "c3b", "c5", "ops", "readout", "matmul"])
     ap.add_argument("--kernels", default="rtc", choices=["aot", "rtc"],
                     help="how the sampler kernels are loaded: hiprtc at first use, the reference's NVRTC route "
                          "(the default; compiled by the first, untimed launch, or read from the disk cache), "
@@ -844,6 +909,8 @@ def main():
     nr.claim(0)
     if args.workload in ("c4", "c4s", "c2"):
         out = bench_sample(nr, W, args, args.workload)
+    elif args.workload == "c4g":
+        out = bench_gumbel(nr, W, args)
     elif args.workload == "c3b":
         out = bench_score_grad(nr, W, args)
     elif args.workload == "ops":
