@@ -177,3 +177,18 @@ def test_additive_masks_nan_and_infinite_logits():
     x[5, 11] = np.nan
     with pytest.raises(ValueError, match="position 5 has no allowed token"):
         nr.sample_categorical(nr.Tensor.from_numpy(x), 0.8, None, nr.Rng(9, "masks"))
+
+
+@pytest.mark.parametrize("pre_u32", [0, 1])
+def test_many_near_ties_take_the_exact_path(pre_u32):
+    # logits near 1e9, 64 apart (f32's spacing there): z + g rounds back to z unless g passes 32,
+    # so every block's elements of the largest z tie, the threads' candidate slots run out and
+    # those rows take the exact evaluation of every element. The first maximum in index order
+    # must still be CpuRef's, on an even and an odd stream position, beside rows (1e4 + noise)
+    # that take the screen.
+    rng = np.random.default_rng(17)
+    rows, V = 12, 4099
+    x = (1e9 + 64.0 * rng.integers(0, 3, (rows, V))).astype(np.float32)
+    x[6:] = (1e4 + rng.normal(0, 0.01, (rows - 6, V))).astype(np.float32)
+    d, c = both(x, 1.0, 21, "near ties", pre_u32=pre_u32)
+    assert np.array_equal(d, c), f"tokens differ from CpuRef: {np.nonzero(d != c)[0]}"
