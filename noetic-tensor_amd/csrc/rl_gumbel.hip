@@ -20,6 +20,7 @@
 #include <cmath>
 #include <cstdint>
 #include <string>
+#include <type_traits>
 
 #include "../../include/noetic_hip.h"
 #include "nt_chacha.hpp"
@@ -161,6 +162,7 @@ __device__ __forceinline__ float gumbel_screen(uint32_t lo, uint32_t hi) {
 }
 
 constexpr int kGumbelCand = 4;         // screened candidates a thread keeps
+constexpr int kGumbelQueue = 128;      // a wave's queue of blocks with an allowed element (LDS)
 constexpr float kGumbelScreen = 1e-3f;  // the screen's margin: 50 times its error bound
 
 // The row's first maximum of z + g. Past temperature 0 it runs in two steps: every allowed
@@ -175,6 +177,9 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
     __shared__ float sbest[kGumbelMaxThreads / 64];
     __shared__ int sidx[kGumbelMaxThreads / 64];
     __shared__ int sflags[kGumbelMaxThreads / 64];
+    // per wave, the queue of blocks to draw: their index and their 8 values ([8][kGumbelQueue])
+    __shared__ int gqb[GREEDY ? 1 : kGumbelMaxThreads / 64 * kGumbelQueue];
+    __shared__ float gqz[GREEDY ? 1 : kGumbelMaxThreads / 64 * 8 * kGumbelQueue];
     const int64_t row = blockIdx.x;
     const int64_t V = p.V;
     // Pair q = h + row V + v holds element v's u64; block q >> 3, pair q & 7 of it.
@@ -182,9 +187,14 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
     const uint64_t b0 = q0 >> 3, b1 = (q0 + uint64_t(V) - 1) >> 3;
     const int wave = threadIdx.x / 64, nw = blockDim.x / 64, lane = threadIdx.x & 63;
     int flags = 0;  // bit 0: a candidate (z > -inf); bit 1: a NaN; bit 2: a thread's slots overflowed
-    // Every block holding an allowed element, in index order per thread: fn(b, v0, z), z the
-    // block's 8 tempered values (elements v0 .. v0 + 7; -inf outside the row).
-    auto walk = [&](auto &&fn) {
+    // Every block holding an allowed element: fn(b, v0, z), z the block's 8 tempered values
+    // (elements v0 .. v0 + 7; -inf outside the row). Without COMPACT each thread takes its own
+    // blocks in index order. With COMPACT (the aligned path) a wave's blocks that hold an allowed
+    // element go through its queue, and each call takes whichever queued block falls to the lane,
+    // so that the keystream is generated by full waves (the order does not matter to the caller:
+    // its merges break ties by index).
+    auto walk = [&](auto compact_c, auto &&fn) {
+        constexpr bool COMPACT = decltype(compact_c)::value && !GREEDY;
         if (!ODD && p.vec && (q0 & 7) == 0) {
             // The aligned path: keystream block b0 + i holds elements 8 i .. 8 i + 7 exactly. Each
             // thread takes blocks i, i + n, ... in index order, with the next block's loads issued
@@ -200,24 +210,81 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
                     const_cast<char *>(static_cast<const char *>(p.mask) + row * p.mask_ld * (MK == NT_MASK_F32 ? 4 : 1)),
                     short(0), int(V * (MK == NT_MASK_F32 ? 4 : 1)), kBufferWord3);
             const int n = blockDim.x;
-            int i = threadIdx.x;
             GumbelRaw<DT, MK> cur, nxt;
-            if (i < nb) gumbel_load<DT, MK>(cur, xres, mres, 8 * i);
-            for (; i < nb; i += n) {
-                if (i + n < nb) gumbel_load<DT, MK>(nxt, xres, mres, 8 * (i + n));
-                float z[8];
-                gumbel_values<DT, MK>(cur, p, 8 * i, z);
-                bool any = false;
+            if constexpr (COMPACT) {
+                int *qb = gqb + wave * kGumbelQueue;
+                float *qz = gqz + wave * 8 * kGumbelQueue;
+                int head = 0, count = 0;  // the queue's first entry and its length (uniform)
+                auto pop = [&](bool have) {
+                    // (every lane's queue writes are in LDS before any lane reads)
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                    __builtin_amdgcn_wave_barrier();
+                    if (have) {
+                        const int e = (head + lane) % kGumbelQueue;
+                        const int ie = qb[e];
+                        float ze[8];
 #pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    if (z[j] != z[j]) flags |= 2;
-                    any |= z[j] > -INFINITY;
+                        for (int j = 0; j < 8; j++) ze[j] = qz[j * kGumbelQueue + e];
+                        fn(b0 + uint64_t(ie), 8 * int64_t(ie), ze);
+                    }
+                    // (the reads are done before a later write reuses their slots)
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                    __builtin_amdgcn_wave_barrier();
+                };
+                // a wave's blocks: 64 consecutive ones per step, n apart
+                const int base0 = 64 * wave;
+                if (base0 + lane < nb) gumbel_load<DT, MK>(cur, xres, mres, 8 * (base0 + lane));
+                for (int base = base0; base < nb; base += n) {
+                    const int i = base + lane;
+                    if (i + n < nb) gumbel_load<DT, MK>(nxt, xres, mres, 8 * (i + n));
+                    float z[8];
+                    bool any = false;
+                    if (i < nb) {
+                        gumbel_values<DT, MK>(cur, p, 8 * i, z);
+#pragma unroll
+                        for (int j = 0; j < 8; j++) {
+                            if (z[j] != z[j]) flags |= 2;
+                            any |= z[j] > -INFINITY;
+                        }
+                    }
+                    const uint64_t bal = __ballot(any);
+                    if (any) {
+                        flags |= 1;
+                        const int pos = (head + count + int(__builtin_amdgcn_mbcnt_hi(
+                                                               uint32_t(bal >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(bal), 0u)))) %
+                                        kGumbelQueue;
+                        qb[pos] = i;
+#pragma unroll
+                        for (int j = 0; j < 8; j++) qz[j * kGumbelQueue + pos] = z[j];
+                    }
+                    count += __builtin_popcountll(bal);
+                    if (count >= 64) {
+                        pop(true);
+                        head = (head + 64) % kGumbelQueue;
+                        count -= 64;
+                    }
+                    cur = nxt;
                 }
-                if (any) {
-                    flags |= 1;
-                    fn(b0 + uint64_t(i), 8 * int64_t(i), z);
+                if (count > 0) pop(lane < count);
+            } else {
+                int i = threadIdx.x;
+                if (i < nb) gumbel_load<DT, MK>(cur, xres, mres, 8 * i);
+                for (; i < nb; i += n) {
+                    if (i + n < nb) gumbel_load<DT, MK>(nxt, xres, mres, 8 * (i + n));
+                    float z[8];
+                    gumbel_values<DT, MK>(cur, p, 8 * i, z);
+                    bool any = false;
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        if (z[j] != z[j]) flags |= 2;
+                        any |= z[j] > -INFINITY;
+                    }
+                    if (any) {
+                        flags |= 1;
+                        fn(b0 + uint64_t(i), 8 * int64_t(i), z);
+                    }
+                    cur = nxt;
                 }
-                cur = nxt;
             }
         } else {
             for (uint64_t b = b0 + threadIdx.x; b <= b1; b += blockDim.x) {
@@ -293,7 +360,7 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
         flags = rf;
     };
     if constexpr (GREEDY) {
-        walk([&](uint64_t, int64_t v0, const float (&z)[8]) {
+        walk(std::false_type{}, [&](uint64_t, int64_t v0, const float (&z)[8]) {
 #pragma unroll
             for (int j = 0; j < 8; j++)
                 if (z[j] > best) {  // strictly greater: the first maximum of this thread's elements
@@ -310,7 +377,7 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
         float ca0 = -INFINITY, ca1 = -INFINITY, ca2 = -INFINITY, ca3 = -INFINITY;  // screened values
         float cz0 = 0.0f, cz1 = 0.0f, cz2 = 0.0f, cz3 = 0.0f;                       // tempered logits
         int cv0 = 0, cv1 = 0, cv2 = 0, cv3 = 0;                                     // elements
-        walk([&](uint64_t b, int64_t v0, const float (&z)[8]) {
+        walk(std::true_type{}, [&](uint64_t b, int64_t v0, const float (&z)[8]) {
             draws(b, v0, z, [&](int64_t v, float zj, uint32_t lo, uint32_t hi) {
                 const float a = zj + gumbel_screen(lo, hi);
                 if (a > amax) amax = a;
@@ -342,7 +409,7 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
         bidx = 0x7fffffff;
         if (flags & 4) {
             // a thread ran out of slots: every element exactly
-            walk([&](uint64_t b, int64_t v0, const float (&z)[8]) { draws(b, v0, z, exact); });
+            walk(std::true_type{}, [&](uint64_t b, int64_t v0, const float (&z)[8]) { draws(b, v0, z, exact); });
         } else if (!(flags & 2)) {
             // the candidates within the margin of the row's largest, exactly (their blocks again)
             auto resolve = [&](float ca, float cz, int cv) {
