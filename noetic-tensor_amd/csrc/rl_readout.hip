@@ -72,13 +72,16 @@ struct ReadoutP {
     int *tfirst;         // [rows][ntile] the first column holding it
     float *bsum;         // [rows][nblk] the block's sum of 2^(x c - tref)
     float *ebsum;        // [rows][nblk] the block's sum of 2^(x c - tref) (x c - tref) (ENT)
+    const int32_t *tokens;  // [rows] the tokens being scored (TOKX)
+    float *xtok;         // [rows] their logits, -inf where the mask excludes them (TOKX)
     float *logits;       // [rows][V] debug copy or null
 };
 
 // FIRST: the tile records carry each row's first column of the maximum (the greedy draw's
 // answer); the sampler otherwise needs only the maximum. ENT: each block also records the sum
-// of w y over its columns (w = 2^y, y = x c - tref), the entropy's term.
-template <bool MASK, bool DBG, bool FIRST, bool ENT>
+// of w y over its columns (w = 2^y, y = x c - tref), the entropy's term. TOKX: the lane holding
+// a row's token column writes that logit (-inf if excluded) for the scorer.
+template <bool MASK, bool DBG, bool FIRST, bool ENT, bool TOKX>
 __global__ __launch_bounds__(kRoThreads) void k_readout_tiles(ReadoutP p) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[kRoStages * kRoStageBytes];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -150,6 +153,16 @@ __global__ __launch_bounds__(kRoThreads) void k_readout_tiles(ReadoutP p) {
     if (mdma) {
         wait_vmcnt<0>();
         asm volatile("s_barrier" ::: "memory");  // every wave's copies of the mask have landed
+    }
+    // the scored token of each of this lane's rows, relative to its first column (loaded once the
+    // weight ring's registers are free; with the debug copy of the logits, one row at a time)
+    int tkd[8];
+    if constexpr (TOKX && !DBG) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int r = 32 * i + rw;
+            tkd[i] = p.tokens[r < p.rows ? r : 0] - cw0;
+        }
     }
     // per (i, j, a) the row's four bytes at column cw0 + 32 j + 8 a (all ones without a mask);
     // zero for a row past the last, so that the byte test below also excludes it
@@ -229,6 +242,22 @@ __global__ __launch_bounds__(kRoThreads) void k_readout_tiles(ReadoutP p) {
         };
         if (n0 + kRoCols <= p.V) maxima(std::true_type{});
         else maxima(std::false_type{});
+        if constexpr (TOKX) {
+            // the token's logit, if it is one of this lane's columns 32 j + 8 a + b (a, b < 4)
+            // (excluded: -inf, as the maxima left it)
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int d = (DBG ? p.tokens[live ? r : 0] - cw0 : tkd[i]) - 32 * j;
+                if (live && d >= 0 && d < 32 && (d & 4) == 0) {
+                    const int v = 4 * (d >> 3) + (d & 3);
+                    float x = acc[i][j][0];
+#pragma unroll
+                    for (int vv = 1; vv < 16; vv++)
+                        if (vv == v) x = acc[i][j][vv];
+                    p.xtok[r] = x;
+                }
+            }
+        }
         const float om = __shfl_xor(m, 32, 64);
         if constexpr (FIRST) {
             first = first == 0x7fffffff ? first : cw0 + first;
@@ -315,6 +344,7 @@ struct ResolveP {
     const float *ebsum;  // [rows][nblk] the entropy's block terms (scoring with entropy) or null
     const double *u;
     const int32_t *tokens;  // [rows] scoring: the token whose log-probability is asked for, or null
+    const float *xtok;   // [rows] scoring: that token's logit from pass 1
     int32_t *ids;        // sampling: the draw
     float *logp;
     float *ent;          // scoring: the entropy, or null
@@ -535,13 +565,18 @@ __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
             }
             return;
         }
+        // the token's logit comes from pass 1 (the same value a recomputation gives)
+        wait_vmcnt<0>();
         if (tid == 0) {
             if (p.ent) p.ent[row] = float(log(Sall) - kLn2 * Hall / Sall);
-            s_blk = tok / kRoBlock;
-            s_ref = s_tr[tok / kRoCols];
-            s_tl = 0.0;
+            const float x = p.xtok[row];
+            const double lnS = log(Sall) + shiftA * kLn2;
+            const float zt = p.tau_one ? x : x / p.tau;
+            const float mz = p.tau_one ? M : M / p.tau;
+            p.logp[row] = float((double(zt) - double(mz)) - lnS);
+            p.status[row] = NT_ROW_OK;
         }
-        __syncthreads();  // (3) the block
+        return;
     } else if (p.greedy) {
         wait_vmcnt<0>();
         const double lnS = log(Sall) + shiftA * kLn2;
@@ -697,16 +732,6 @@ __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
     if (p.dbg_block && lane < 32) p.dbg_block[int64_t(row) * 32 + lane] = x;
     if (p.dbg_index && lane == 0) p.dbg_index[row] = bstar;
     x = keep ? x : -INFINITY;
-    if constexpr (SCORE) {
-        // the token's log-probability (an excluded token: -inf)
-        if (lane == tok % kRoBlock) {
-            const float zt = p.tau_one ? x : x / p.tau;
-            const float mz = p.tau_one ? M : M / p.tau;
-            p.logp[row] = float((double(zt) - double(mz)) - lnS);
-            p.status[row] = NT_ROW_OK;
-        }
-        return;
-    }
     const float w = keep ? __builtin_amdgcn_exp2f(fmaf(x, p.c, -r)) : 0.0f;
     const double cw = wave_incl_scan(double(w), lane);
     int lsel = -1;
@@ -861,7 +886,8 @@ int readout_run(const ReadoutCall &c) {
     const int ntile = int((V + kRoCols - 1) / kRoCols), nblk = int((V + kRoBlock - 1) / kRoBlock);
     const size_t rec = size_t(rows) * size_t(ntile) * 4, brec = size_t(rows) * size_t(nblk) * 4;
     const size_t hpack = size_t((rows + 31) / 32) * size_t(K / 16) * 1024;
-    const size_t need = hpack + 3 * rec + (ent ? 2 : 1) * brec;
+    const bool tokx = c.score && c.tokens && c.logp;  // the scored tokens' logits from pass 1
+    const size_t need = hpack + 3 * rec + (ent ? 2 : 1) * brec + (tokx ? size_t(rows) * 4 : 0);
     void *ws = nullptr;
     if (int rc = scratch_alloc(need, &ws)) return rc;
     uint8_t *wb = static_cast<uint8_t *>(ws);
@@ -887,14 +913,18 @@ int readout_run(const ReadoutCall &c) {
     p.tfirst = reinterpret_cast<int *>(wb + hpack + 2 * rec);
     p.bsum = reinterpret_cast<float *>(wb + hpack + 3 * rec);
     p.ebsum = ent ? reinterpret_cast<float *>(wb + hpack + 3 * rec + brec) : nullptr;
+    p.tokens = c.tokens;
+    p.xtok = tokx ? reinterpret_cast<float *>(wb + hpack + 3 * rec + (ent ? 2 : 1) * brec) : nullptr;
     p.logits = c.logits;
     hipStream_t st = ctx().stream;
     const dim3 g1{unsigned(ntile), 1, 1}, b1{unsigned(kRoThreads), 1, 1};
     auto launch1 = [&](auto mask_c, auto dbg_c) {
         constexpr bool MK = decltype(mask_c)::value, DB = decltype(dbg_c)::value;
-        if (c.greedy) hipLaunchKernelGGL((k_readout_tiles<MK, DB, true, false>), g1, b1, 0, st, p);
-        else if (ent) hipLaunchKernelGGL((k_readout_tiles<MK, DB, false, true>), g1, b1, 0, st, p);
-        else hipLaunchKernelGGL((k_readout_tiles<MK, DB, false, false>), g1, b1, 0, st, p);
+        if (c.greedy) hipLaunchKernelGGL((k_readout_tiles<MK, DB, true, false, false>), g1, b1, 0, st, p);
+        else if (ent && tokx) hipLaunchKernelGGL((k_readout_tiles<MK, DB, false, true, true>), g1, b1, 0, st, p);
+        else if (ent) hipLaunchKernelGGL((k_readout_tiles<MK, DB, false, true, false>), g1, b1, 0, st, p);
+        else if (tokx) hipLaunchKernelGGL((k_readout_tiles<MK, DB, false, false, true>), g1, b1, 0, st, p);
+        else hipLaunchKernelGGL((k_readout_tiles<MK, DB, false, false, false>), g1, b1, 0, st, p);
     };
     if (c.logits) {
         if (p.mask) launch1(std::true_type{}, std::true_type{});
@@ -929,6 +959,7 @@ int readout_run(const ReadoutCall &c) {
     q.ebsum = p.ebsum;
     q.u = c.u;
     q.tokens = c.tokens;
+    q.xtok = p.xtok;
     q.ids = c.ids;
     q.logp = c.logp;
     q.ent = c.ent;
