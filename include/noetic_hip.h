@@ -236,9 +236,9 @@ int nt_hip_rl_readout_sample(const NtRlReadoutSampleArgs *a);
  * outside [0, vocab) gives NT_ROW_BAD_TOKEN and logp NaN), with the logits never written: the
  * scoring pass of an RL step from the decoder's hidden states (decoder.rs:272,286). Shapes,
  * packing and limits as nt_hip_rl_readout_sample; temperature > 0. Three launches: h into the
- * matrix cores' order, the product with per-row records in its epilogue (block sums and, for
- * the entropy, each block's sum of w (x c - ref)), then one workgroup per row that merges them
- * and recomputes only the 32 logits of the token's block. */
+ * matrix cores' order, the product with per-row records in its epilogue (block sums, for the
+ * entropy each block's sum of w (x c - ref), and each row's token logit), then one workgroup per
+ * row that merges the records. */
 typedef struct NtRlReadoutScoreArgs {
     const void *hidden;        /* [rows, ldh] bf16 */
     const void *weight_packed; /* packed by nt_hip_rl_readout_pack_weight */

@@ -413,7 +413,8 @@ __device__ __forceinline__ double wave_incl_scan(double v, int lane) {
 // banks.
 __device__ __forceinline__ int bs_slot(int b) { return b + (b >> 4); }
 
-// SCORE: the row's token (not a draw) picks the block, and the entropy comes from the records.
+// SCORE: the row's token logit comes from pass 1 (no block is recomputed), and the entropy from
+// the records.
 template <int MAXB, bool SCORE>
 __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
     __shared__ double wsum[kResThreads / 64];
