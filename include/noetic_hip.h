@@ -95,8 +95,8 @@ int nt_hip_stream(void **out);
 /* Launch counter (the reference's `launches()`, src/tensor/cuda/backend.rs:1034-1036). */
 uint64_t nt_hip_launches(void);
 
-/* Where the nn::rl row kernels (nt_hip_rl_sample, nt_hip_rl_sample_noalloc, nt_hip_rl_score,
- * nt_hip_rl_score_backward) launch from. The CUDA
+/* Where the nn::rl row kernels (nt_hip_rl_sample, nt_hip_rl_sample_noalloc, nt_hip_rl_sample_gumbel,
+ * nt_hip_rl_score, nt_hip_rl_score_backward) launch from. The CUDA
  * backend compiles its kernels with NVRTC at first use and caches the functions
  * (src/tensor/cuda/mod.rs:169-218, cuda/backend.rs:281-293, 322-358); here both ways exist for
  * one device source: NT_KERNELS_AOT, the code objects hipcc built into this library (the

@@ -5,9 +5,11 @@
 // of block w / 16, so any position is reached without generating what comes before it.
 #pragma once
 
+#ifndef __HIPCC_RTC__  // (hiprtc: the device part of the library's headers, stdint from nt_rows.hpp)
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#endif
 
 namespace nt {
 

@@ -106,7 +106,8 @@ void cache_write(const std::string &path, const std::string &lowered, const std:
 
 int compile(const std::string &name, std::string *lowered, std::vector<char> *code) {
     hiprtcProgram prog;
-    const char *src = "#include \"rl_sample_kernels.hpp\"\n#include \"rl_score_kernels.hpp\"\n";
+    const char *src =
+        "#include \"rl_sample_kernels.hpp\"\n#include \"rl_score_kernels.hpp\"\n#include \"rl_gumbel_kernels.hpp\"\n";
     if (hiprtcCreateProgram(&prog, src, "nt_rtc.hip", kRtcFiles, kRtcTexts, kRtcNames) != HIPRTC_SUCCESS)
         return fail(NT_E_RTC, "hiprtcCreateProgram failed");
     hiprtcResult r = hiprtcAddNameExpression(prog, name.c_str());

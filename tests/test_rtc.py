@@ -17,8 +17,11 @@ EMBEDDED = {
     "nt_rows.hpp": os.path.join(CSRC, "nt_rows.hpp"),
     "rl_sample_kernels.hpp": os.path.join(CSRC, "rl_sample_kernels.hpp"),
     "rl_score_kernels.hpp": os.path.join(CSRC, "rl_score_kernels.hpp"),
+    "nt_chacha.hpp": os.path.join(CSRC, "nt_chacha.hpp"),
+    "rl_gumbel_kernels.hpp": os.path.join(CSRC, "rl_gumbel_kernels.hpp"),
 }
-PROGRAM = b'#include "rl_sample_kernels.hpp"\n#include "rl_score_kernels.hpp"\n'
+PROGRAM = (b'#include "rl_sample_kernels.hpp"\n#include "rl_score_kernels.hpp"\n'
+           b'#include "rl_gumbel_kernels.hpp"\n')
 OPTIONS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
@@ -44,6 +47,8 @@ def test_kernel_path_switch_needs_no_device():
     (b"nt::k_score<1, 0, true, true, true, true>", b"k_score"),
     # its backward with the KL term into a bf16 gradient
     (b"nt::k_score_grad<1, 0, true, 1, true>", b"k_score_grad"),
+    # the reference's Gumbel-max sampler on C4's rows (bf16, u8 mask, an even stream position)
+    (b"nt::k_sample_gumbel<1, 1, false, false>", b"k_sample_gumbel"),
 ])
 def test_hiprtc_compiles_the_row_kernel_instances_on_the_cpu(expr, kernel):
     try:

@@ -143,6 +143,22 @@ def test_scorer_and_backward_are_byte_identical_through_both_paths(case):
     compare_to_oracle(f"{case} (aot = rtc)", z, r, tok.to_numpy(), g, kl, ent, tau, gf, gb)
 
 
+@pytest.mark.parametrize("pre_u32", [0, 1])
+def test_gumbel_sampler_is_byte_identical_through_both_paths(pre_u32):
+    """The reference's Gumbel-max sampler on C4's rows (the aligned, screened path at an even
+    stream position; the element-wise path at an odd one), through both paths."""
+    w = W.c4()
+
+    def call():
+        rng = nr.Rng(5, "rtc/gumbel")
+        for _ in range(pre_u32):
+            rng.next_u32()
+        return [nr.sample_categorical(w["logits"], w["temperature"], w["mask"], rng)]
+
+    aot, rtc1, rtc2 = both_paths(call)
+    assert rtc1 == aot and rtc2 == aot, "hiprtc and hipcc code objects disagree"
+
+
 def test_key_names_the_path():
     k_aot = nr.key()
     nr.set_kernel_path("rtc")
