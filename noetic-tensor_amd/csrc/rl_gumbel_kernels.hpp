@@ -176,11 +176,65 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
     // its merges break ties by index).
     auto walk = [&](auto compact_c, auto &&fn) {
         constexpr bool COMPACT = decltype(compact_c)::value && !GREEDY;
+        const int n = blockDim.x;
+        // COMPACT: the row's blocks i = 0 .. nbk - 1 (keystream block b0 + i, elements
+        // 8 i - r .. 8 i - r + 7), a wave's 64 consecutive ones per step, n apart. z_of(i, z) fills
+        // block i's values (every lane calls it once per step, in order; -inf past the row).
+        // Blocks holding an allowed element are queued with their values; each time 64 are
+        // queued every lane takes one, and the rest are taken at the end.
+        auto queued = [&](int nbk, int r, auto &&z_of) {
+            int *qb = gqb + wave * kGumbelQueue;
+            float *qz = gqz + wave * 8 * kGumbelQueue;
+            int head = 0, count = 0;  // the queue's first entry and its length (uniform)
+            auto pop = [&](bool have) {
+                // (every lane's queue writes are in LDS before any lane reads)
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                __builtin_amdgcn_wave_barrier();
+                if (have) {
+                    const int e = (head + lane) % kGumbelQueue;
+                    const int ie = qb[e];
+                    float ze[8];
+#pragma unroll
+                    for (int j = 0; j < 8; j++) ze[j] = qz[j * kGumbelQueue + e];
+                    fn(b0 + uint64_t(ie), 8 * int64_t(ie) - r, ze);
+                }
+                // (the reads are done before a later write reuses their slots)
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                __builtin_amdgcn_wave_barrier();
+            };
+            for (int base = 64 * wave; base < nbk; base += n) {
+                const int i = base + lane;
+                float z[8];
+                z_of(i, z);
+                bool any = false;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    if (z[j] != z[j]) flags |= 2;
+                    any |= z[j] > -INFINITY;
+                }
+                const uint64_t bal = __ballot(any);
+                if (any) {
+                    flags |= 1;
+                    const int pos = (head + count + int(__builtin_amdgcn_mbcnt_hi(
+                                                           uint32_t(bal >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(bal), 0u)))) %
+                                    kGumbelQueue;
+                    qb[pos] = i;
+#pragma unroll
+                    for (int j = 0; j < 8; j++) qz[j * kGumbelQueue + pos] = z[j];
+                }
+                count += __builtin_popcountll(bal);
+                if (count >= 64) {
+                    pop(true);
+                    head = (head + 64) % kGumbelQueue;
+                    count -= 64;
+                }
+            }
+            if (count > 0) pop(lane < count);
+        };
         if (!ODD && p.vec && (q0 & 7) == 0) {
-            // The aligned path: keystream block b0 + i holds elements 8 i .. 8 i + 7 exactly. Each
-            // thread takes blocks i, i + n, ... in index order, with the next block's loads issued
-            // before this block is used. Loads past the row read zeros (the buffer's range) and
-            // those elements are -inf.
+            // The aligned path: keystream block b0 + i holds elements 8 i .. 8 i + 7 exactly, read
+            // with one or two 16-byte loads (the next block's issued before this block is used).
+            // Loads past the row read zeros (the buffer's range) and those elements are -inf.
             const int nb = int((V + 7) / 8);
             const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<char *>(static_cast<const char *>(p.logits) + row * p.ld * (DT == NT_F32 ? 4 : 2)),
@@ -190,63 +244,20 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
                 mres = __builtin_amdgcn_make_buffer_rsrc(
                     const_cast<char *>(static_cast<const char *>(p.mask) + row * p.mask_ld * (MK == NT_MASK_F32 ? 4 : 1)),
                     short(0), int(V * (MK == NT_MASK_F32 ? 4 : 1)), kBufferWord3);
-            const int n = blockDim.x;
             GumbelRaw<DT, MK> cur, nxt;
             if constexpr (COMPACT) {
-                int *qb = gqb + wave * kGumbelQueue;
-                float *qz = gqz + wave * 8 * kGumbelQueue;
-                int head = 0, count = 0;  // the queue's first entry and its length (uniform)
-                auto pop = [&](bool have) {
-                    // (every lane's queue writes are in LDS before any lane reads)
-                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                    __builtin_amdgcn_wave_barrier();
-                    if (have) {
-                        const int e = (head + lane) % kGumbelQueue;
-                        const int ie = qb[e];
-                        float ze[8];
-#pragma unroll
-                        for (int j = 0; j < 8; j++) ze[j] = qz[j * kGumbelQueue + e];
-                        fn(b0 + uint64_t(ie), 8 * int64_t(ie), ze);
-                    }
-                    // (the reads are done before a later write reuses their slots)
-                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                    __builtin_amdgcn_wave_barrier();
-                };
-                // a wave's blocks: 64 consecutive ones per step, n apart
-                const int base0 = 64 * wave;
-                if (base0 + lane < nb) gumbel_load<DT, MK>(cur, xres, mres, 8 * (base0 + lane));
-                for (int base = base0; base < nb; base += n) {
-                    const int i = base + lane;
+                const int i0 = 64 * wave + lane;
+                if (i0 < nb) gumbel_load<DT, MK>(cur, xres, mres, 8 * i0);
+                queued(nb, 0, [&](int i, float (&z)[8]) {
                     if (i + n < nb) gumbel_load<DT, MK>(nxt, xres, mres, 8 * (i + n));
-                    float z[8];
-                    bool any = false;
                     if (i < nb) {
                         gumbel_values<DT, MK>(cur, p, 8 * i, z);
+                    } else {
 #pragma unroll
-                        for (int j = 0; j < 8; j++) {
-                            if (z[j] != z[j]) flags |= 2;
-                            any |= z[j] > -INFINITY;
-                        }
-                    }
-                    const uint64_t bal = __ballot(any);
-                    if (any) {
-                        flags |= 1;
-                        const int pos = (head + count + int(__builtin_amdgcn_mbcnt_hi(
-                                                               uint32_t(bal >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(bal), 0u)))) %
-                                        kGumbelQueue;
-                        qb[pos] = i;
-#pragma unroll
-                        for (int j = 0; j < 8; j++) qz[j * kGumbelQueue + pos] = z[j];
-                    }
-                    count += __builtin_popcountll(bal);
-                    if (count >= 64) {
-                        pop(true);
-                        head = (head + 64) % kGumbelQueue;
-                        count -= 64;
+                        for (int j = 0; j < 8; j++) z[j] = -INFINITY;
                     }
                     cur = nxt;
-                }
-                if (count > 0) pop(lane < count);
+                });
             } else {
                 int i = threadIdx.x;
                 if (i < nb) gumbel_load<DT, MK>(cur, xres, mres, 8 * i);
@@ -267,6 +278,17 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
                     cur = nxt;
                 }
             }
+        } else if constexpr (COMPACT) {
+            // element by element: block b0 + i holds elements 8 i - r .. 8 i - r + 7
+            const int r = int(q0 & 7);
+            queued(int(b1 - b0 + 1), r, [&](int i, float (&z)[8]) {
+                const int64_t v0 = 8 * int64_t(i) - r;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const int64_t v = v0 + j;
+                    z[j] = (v >= 0 && v < V) ? tempered_at<DT, MK>(p, row, v) : -INFINITY;
+                }
+            });
         } else {
             for (uint64_t b = b0 + threadIdx.x; b <= b1; b += blockDim.x) {
                 const int64_t v0 = int64_t(8 * b - q0);  // element of pair 0 of block b (may be < 0)
