@@ -7,14 +7,20 @@
 // f32, then an add kernel and an argmax kernel). Here the noise is generated where it is used:
 // ChaCha20 is a counter-mode stream, so word w of the keystream is word w % 16 of block w / 16
 // and every element's u64 is computed from the stream's key and starting word position alone.
-// One workgroup takes one row; each thread takes whole keystream blocks (8 u64 = 8 elements
-// when the stream's position is even) in index order, keeps its first maximum, and the
-// workgroup combines the (value, index) pairs with "greater value, else smaller index", which
-// is associative, so the result is the sequential first maximum whatever the timing.
-//
-// A block whose eight logits are all excluded (-inf) is skipped without generating it: such an
-// element can never be the maximum of an accepted row (a row with no other candidate is
-// refused), so skipping changes no token.
+// One workgroup takes one row (rl_gumbel_kernels.hpp):
+//  - the row is cut into blocks of 8 elements, one keystream block each; a block whose eight
+//    logits are all excluded (-inf) is skipped without generating it (such an element can never
+//    be the maximum of an accepted row; a row with no other candidate is refused);
+//  - each wave queues its blocks that hold an allowed element in LDS and generates their
+//    keystream by full waves;
+//  - every allowed element's draw is first screened in f32 (hardware logarithms, within 1e-5 of
+//    the exact f32 value); only the elements within 1e-3 of the row's largest screened value are
+//    evaluated exactly, in f64 as the reference does, and the row's first maximum is taken among
+//    them with "greater value, else smaller index", which is associative, so the result is the
+//    sequential first maximum whatever the timing (a thread with more than four candidates sends
+//    its row to the exact evaluation of every element);
+//  - rows whose first u64 starts a block, on aligned rows, read a block's 8 logits and mask
+//    entries with vector loads issued a block ahead; others read element by element.
 #include <hip/hip_runtime.h>
 
 #include <cmath>

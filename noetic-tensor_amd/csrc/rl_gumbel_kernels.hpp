@@ -170,9 +170,9 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
     int flags = 0;  // bit 0: a candidate (z > -inf); bit 1: a NaN; bit 2: a thread's slots overflowed
     // Every block holding an allowed element: fn(b, v0, z), z the block's 8 tempered values
     // (elements v0 .. v0 + 7; -inf outside the row). Without COMPACT each thread takes its own
-    // blocks in index order. With COMPACT (the aligned path) a wave's blocks that hold an allowed
-    // element go through its queue, and each call takes whichever queued block falls to the lane,
-    // so that the keystream is generated by full waves (the order does not matter to the caller:
+    // blocks in index order. With COMPACT a wave's blocks that hold an allowed element go through
+    // its queue, and each call takes whichever queued block falls to the lane, so that the
+    // keystream is generated by full waves (the order does not matter to the caller:
     // its merges break ties by index).
     auto walk = [&](auto compact_c, auto &&fn) {
         constexpr bool COMPACT = decltype(compact_c)::value && !GREEDY;
