@@ -427,7 +427,8 @@ __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
     __shared__ double s_tl;
     __shared__ __attribute__((aligned(16))) float s_bs[MAXB * kResThreads * 17 / 16];  // the row's block sums
     __shared__ float s_tr[kResMaxTiles * kResThreads];                                 // its tile references
-    __shared__ __attribute__((aligned(16))) uint8_t hrow[kResMaxK * 2];
+    // (scoring recomputes no block: no row of h)
+    __shared__ __attribute__((aligned(16))) uint8_t hrow[SCORE ? 16 : kResMaxK * 2];
     const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *tref = p.tref + int64_t(row) * p.ntile;
     const float *tmax = p.tmax + int64_t(row) * p.ntile;
@@ -435,11 +436,13 @@ __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
     const float *bsum = p.bsum + int64_t(row) * p.nblk;
     // The row of h into LDS (1 KiB pieces, piece c by wave c % 4): whichever block the records
     // pick, the recomputation needs it.
-    const __amdgpu_buffer_rsrc_t hres = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t *>(p.h + int64_t(row) * p.ldh), short(0), p.K * 2, kBufferWord3);
-    for (int c = wave; c * 1024 < p.K * 2; c += 4)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(hres, (lds_ptr_t)(hrow + c * 1024), 16, c * 1024 + lane * 16, 0, 0,
-                                                 0);
+    if constexpr (!SCORE) {
+        const __amdgpu_buffer_rsrc_t hres = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t *>(p.h + int64_t(row) * p.ldh), short(0), p.K * 2, kBufferWord3);
+        for (int c = wave; c * 1024 < p.K * 2; c += 4)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(hres, (lds_ptr_t)(hrow + c * 1024), 16, c * 1024 + lane * 16, 0,
+                                                     0, 0);
+    }
     const double u_row = (SCORE || p.greedy) ? 0.0 : p.u[row];
     const int tok = SCORE && p.tokens ? p.tokens[row] : -1;
     // The records, coalesced. (Every load reads a valid index and the unused ones are masked
@@ -642,6 +645,8 @@ __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
             s_tl = (t - bexcl) * double(__builtin_amdgcn_exp2f(A - r));
         }
         __syncthreads();  // (4) the block
+    } else {
+        return;  // (the scoring path has ended above)
     }
     const int bstar = s_blk;
     if (bstar < 0) {
