@@ -114,32 +114,26 @@ __device__ __forceinline__ void gumbel_values(const GumbelRaw<DT, MK> &r, const 
 }
 
 // The screen (a draw's value in f32 from hardware logarithms): within 1e-5 of gumbel_f32's
-// value, and infinite exactly where it is. t = -ln u comes from u for u < 1/2, and from 1 - u
-// taken from the integer (2^53 - (k + 0.5), with the f64 sum's rounding to even from 2^52 on) by
-// 2 atanh(w), w = d / (2 - d) <= 1/3, for u >= 1/2, so that no precision is lost near u = 1.
+// value, and infinite exactly where it is, with no branch and no division. k = (hi:lo) >> 11 and
+// u = (k + 0.5) / 2^53. Below u = 1 - 2^-4, t = -ln u from u in f32 (hi's and k's low 21 bits
+// converted apart); t >= 0.06 there, so the logarithm's rounding stays a small relative error.
+// Above it, t = -ln(1 - d) = d (1 + d/2 + ... + d^5/6) (the next term is below 2^-24 of t) with
+// d = 1 - u taken from the integer: 2^53 d = (2^32 - hi) 2^21 - (k mod 2^21) - (k & 1), the f64
+// sum k + 0.5 rounding to even from 2^52 on, in one fused multiply-add. d = 0 (k = 2^53 - 1, u
+// rounds to 1) gives t = 0 and g = +inf, as the exact value is.
 __device__ __forceinline__ float gumbel_screen(uint32_t lo, uint32_t hi) {
-    const uint64_t k = ((uint64_t(hi) << 32) | lo) >> 11;
     constexpr float kLn2f = 0.69314718055994530942f;
-    float t;
-    if (k < (uint64_t(1) << 52)) {
-        const float u = float(k) * 0x1p-53f + 0x1p-54f;
-        t = -__builtin_amdgcn_logf(u) * kLn2f;
-    } else {
-        const uint64_t dint = (uint64_t(1) << 53) - k - (k & 1);
-        if (dint == 0) return INFINITY;  // u rounds to 1: -ln(-ln 1) = +inf
-        const float d = float(dint) * 0x1p-53f;
-        const float w = d / (2.0f - d), w2 = w * w;
-        float ser = 1.0f / 15.0f;
-        ser = fmaf(ser, w2, 1.0f / 13.0f);
-        ser = fmaf(ser, w2, 1.0f / 11.0f);
-        ser = fmaf(ser, w2, 1.0f / 9.0f);
-        ser = fmaf(ser, w2, 1.0f / 7.0f);
-        ser = fmaf(ser, w2, 1.0f / 5.0f);
-        ser = fmaf(ser, w2, 1.0f / 3.0f);
-        ser = fmaf(ser, w2, 1.0f);
-        t = 2.0f * w * ser;
-    }
-    return -__builtin_amdgcn_logf(t) * kLn2f;
+    const uint32_t kl = lo >> 11;  // k's low 21 bits (its high 32 are hi)
+    const float u = fmaf(float(hi), 0x1p-32f, fmaf(float(kl), 0x1p-53f, 0x1p-54f));
+    const float tl = __builtin_amdgcn_logf(u) * -kLn2f;
+    const float d = fmaf(float(kl + (kl & 1u)), -0x1p-53f, float(0u - hi) * 0x1p-32f);
+    float ser = fmaf(d, 1.0f / 6.0f, 1.0f / 5.0f);
+    ser = fmaf(ser, d, 1.0f / 4.0f);
+    ser = fmaf(ser, d, 1.0f / 3.0f);
+    ser = fmaf(ser, d, 0.5f);
+    ser = fmaf(ser, d, 1.0f);
+    const float t = hi >= 0xf0000000u ? d * ser : tl;
+    return __builtin_amdgcn_logf(t) * -kLn2f;
 }
 
 constexpr int kGumbelCand = 4;         // screened candidates a thread keeps

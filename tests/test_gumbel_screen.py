@@ -9,25 +9,30 @@ import numpy as np
 MARGIN = 1e-3
 
 
+def _fma(a, b, c):
+    """f32 fused multiply-add: the f64 product of two f32 values is exact; the sum is rounded to
+    f64, then to f32 (a double rounding that can differ from one rounding by an ulp at most)."""
+    return (np.asarray(a, np.float32).astype(np.float64) * np.asarray(b, np.float32).astype(np.float64)
+            + np.asarray(c, np.float32).astype(np.float64)).astype(np.float32)
+
+
 def screen(k):
     k = k.astype(np.uint64)
+    hi = (k >> np.uint64(21)).astype(np.uint32)           # the u64's high word
+    kl = (k & np.uint64(2**21 - 1)).astype(np.uint32)     # k's low 21 bits (the low word >> 11)
     ln2 = np.float32(np.log(2.0))
     with np.errstate(divide="ignore"):
-        # u < 1/2: from u in f32
-        u = k.astype(np.float32) * np.float32(2.0**-53) + np.float32(2.0**-54)
-        t_small = -(np.log2(u).astype(np.float32) * ln2)
-        # u >= 1/2: 1 - u from the integer, with the f64 sum k + 0.5 rounding to even from 2^52 on
-        dint = np.uint64(2**53) - k - (k & np.uint64(1))
-        d = dint.astype(np.float32) * np.float32(2.0**-53)
-        w = d / (np.float32(2) - d)
-        w2 = w * w
-        ser = np.float32(1 / 15)
-        for c in (1 / 13, 1 / 11, 1 / 9, 1 / 7, 1 / 5, 1 / 3, 1.0):
-            ser = (ser * w2 + np.float32(c)).astype(np.float32)
-        t_big = np.float32(2) * w * ser
-        t = np.where(k < np.uint64(2**52), t_small, t_big).astype(np.float32)
-        g = -(np.log2(t).astype(np.float32) * ln2)
-    return np.where(dint == 0, np.float32(np.inf), g)
+        u = _fma(hi.astype(np.float32), 2.0**-32, _fma(kl.astype(np.float32), 2.0**-53, 2.0**-54))
+        tl = np.log2(u).astype(np.float32) * -ln2
+        # 2^53 d = (2^32 - hi) 2^21 - kl - (kl & 1), in one fused multiply-add
+        nh = (np.uint32(0) - hi).astype(np.uint32)
+        d = _fma((kl + (kl & np.uint32(1))).astype(np.float32), -(2.0**-53),
+                 nh.astype(np.float32) * np.float32(2.0**-32))
+        ser = _fma(d, 1 / 6, 1 / 5)
+        for c in (1 / 4, 1 / 3, 0.5, 1.0):
+            ser = _fma(ser, d, c)
+        t = np.where(hi >= np.uint32(0xF0000000), (d * ser).astype(np.float32), tl).astype(np.float32)
+        return (np.log2(t).astype(np.float32) * -ln2).astype(np.float32)
 
 
 def exact(k):
@@ -43,6 +48,7 @@ def test_screen_bound_over_the_range_of_k():
         np.uint64(2**53 - 1) - rng.integers(0, 2**20, 200_000, dtype=np.uint64),  # u -> 1
         rng.integers(0, 2**20, 200_000, dtype=np.uint64),                         # u -> 0
         np.arange(2**52 - 2**15, 2**52 + 2**15, dtype=np.uint64),                 # u = 1/2
+        np.arange(15 * 2**49 - 2**15, 15 * 2**49 + 2**15, dtype=np.uint64),       # u = 1 - 2^-4
         np.array([0, 1, 2**52 - 1, 2**52, 2**53 - 2, 2**53 - 1], dtype=np.uint64),
     ])
     g, a = exact(k), screen(k)
