@@ -138,7 +138,17 @@ __device__ __forceinline__ float gumbel_screen(uint32_t lo, uint32_t hi) {
 
 constexpr int kGumbelCand = 4;         // screened candidates a thread keeps
 constexpr int kGumbelQueue = 128;      // a wave's queue of blocks with an allowed element (LDS)
-constexpr float kGumbelScreen = 1e-3f;  // the screen's margin: 50 times its error bound
+constexpr float kGumbelScreen = 1e-3f;  // the screen's margin, at least: 250 times its error bound
+
+// The lowest screened value kept as a candidate beside a largest screened value x: x less the
+// larger of kGumbelScreen and |x| rel. The value compared is z + g rounded to f32, so a screened
+// and an exact sum differ by the screen's error and up to an ulp of the sum; with rel = 2^-21
+// (four ulps of x) the margin exceeds two such differences at every magnitude, so an element
+// below it cannot reach or pass the element at x exactly. A thread keeps its own candidates
+// with rel = 2^-20, a superset of the row's. (x = +inf: the candidates are the infinite values.)
+__device__ __forceinline__ float screen_floor(float x, float rel) {
+    return x == INFINITY ? x : x - fmaxf(kGumbelScreen, fabsf(x) * rel);
+}
 
 // The row's first maximum of z + g. Past temperature 0 it runs in two steps: every allowed
 // element's value is screened in f32 (the keystream is generated, the logarithms are the
@@ -152,6 +162,7 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
     __shared__ float sbest[kGumbelMaxThreads / 64];
     __shared__ int sidx[kGumbelMaxThreads / 64];
     __shared__ int sflags[kGumbelMaxThreads / 64];
+    __shared__ int scount[kGumbelMaxThreads / 64];
     // per wave, the queue of blocks to draw: their index and their 8 values ([8][kGumbelQueue])
     __shared__ int gqb[GREEDY ? 1 : kGumbelMaxThreads / 64 * kGumbelQueue];
     __shared__ float gqz[GREEDY ? 1 : kGumbelMaxThreads / 64 * 8 * kGumbelQueue];
@@ -162,6 +173,7 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
     const uint64_t b0 = q0 >> 3, b1 = (q0 + uint64_t(V) - 1) >> 3;
     const int wave = threadIdx.x / 64, nw = blockDim.x / 64, lane = threadIdx.x & 63;
     int flags = 0;  // bit 0: a candidate (z > -inf); bit 1: a NaN; bit 2: a thread's slots overflowed
+    int count = 0;  // summed by the reductions
     // Every block holding an allowed element: fn(b, v0, z), z the block's 8 tempered values
     // (elements v0 .. v0 + 7; -inf outside the row). Without COMPACT each thread takes its own
     // blocks in index order. With COMPACT a wave's blocks that hold an allowed element go through
@@ -329,8 +341,8 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
     auto exact = [&](int64_t v, float zj, uint32_t lo, uint32_t hi) {
         best_merge(best, bidx, zj + gumbel_f32(lo, hi), int(v));
     };
-    // the workgroup's (best, bidx) first maximum and OR of the flags: a fixed butterfly inside each
-    // wave, then the waves in order (the result in every thread)
+    // the workgroup's (best, bidx) first maximum, OR of the flags and sum of the counts: a fixed
+    // butterfly inside each wave, then the waves in order (the result in every thread)
     auto reduce_best = [&]() {
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) {
@@ -338,23 +350,27 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
             const int oi = __shfl_xor(bidx, o, 64);
             best_merge(best, bidx, ob, oi);
             flags |= __shfl_xor(flags, o, 64);
+            count += __shfl_xor(count, o, 64);
         }
         if (lane == 0) {
             sbest[wave] = best;
             sidx[wave] = bidx;
             sflags[wave] = flags;
+            scount[wave] = count;
         }
         __syncthreads();
         float rb = sbest[0];
-        int ri = sidx[0], rf = sflags[0];
+        int ri = sidx[0], rf = sflags[0], rc = scount[0];
         for (int i = 1; i < nw; i++) {
             best_merge(rb, ri, sbest[i], sidx[i]);
             rf |= sflags[i];
+            rc += scount[i];
         }
         __syncthreads();  // (the arrays are written again by a later reduction)
         best = rb;
         bidx = ri;
         flags = rf;
+        count = rc;
     };
     if constexpr (GREEDY) {
         walk(std::false_type{}, [&](uint64_t, int64_t v0, const float (&z)[8]) {
@@ -378,11 +394,12 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
             draws(b, v0, z, [&](int64_t v, float zj, uint32_t lo, uint32_t hi) {
                 const float a = zj + gumbel_screen(lo, hi);
                 if (a > amax) amax = a;
-                if (a >= amax - kGumbelScreen) {
+                const float lo_keep = screen_floor(amax, 0x1p-20f);
+                if (a >= lo_keep) {
                     // into the first slot that holds nothing within the margin (slots are reused)
                     bool placed = false;
                     auto slot = [&](float &ca, float &cz, int &cv) {
-                        if (!placed && !(ca >= amax - kGumbelScreen)) {
+                        if (!placed && !(ca >= lo_keep)) {
                             ca = a;
                             cz = zj;
                             cv = int(v);
@@ -401,16 +418,37 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
         best = amax;
         bidx = 0;
         reduce_best();
-        const float amx = best;
+        const float amx = best, lo_row = screen_floor(amx, 0x1p-21f);
+        // the candidates within the row's margin: when there is one, it is the row's exact first
+        // maximum (every other element lies below it exactly), and its index is the answer
         best = -INFINITY;
         bidx = 0x7fffffff;
-        if (flags & 4) {
+        count = 0;
+        auto offer = [&](float ca, int cv) {
+            if (ca >= lo_row) {
+                best_merge(best, bidx, ca, cv);
+                count++;
+            }
+        };
+        offer(ca0, cv0);
+        offer(ca1, cv1);
+        offer(ca2, cv2);
+        offer(ca3, cv3);
+        reduce_best();
+        if (count == 1 && !(flags & 6)) {
+            // (bidx is that candidate's)
+        } else if (flags & 4) {
+            best = -INFINITY;
+            bidx = 0x7fffffff;
             // a thread ran out of slots: every element exactly
             walk(std::true_type{}, [&](uint64_t b, int64_t v0, const float (&z)[8]) { draws(b, v0, z, exact); });
+            reduce_best();
         } else if (!(flags & 2)) {
             // the candidates within the margin of the row's largest, exactly (their blocks again)
+            best = -INFINITY;
+            bidx = 0x7fffffff;
             auto resolve = [&](float ca, float cz, int cv) {
-                const bool take = ca >= amx - kGumbelScreen;
+                const bool take = ca >= lo_row;
                 if (__ballot(take) == 0) return;
                 if (take) {
                     const uint64_t w0 = 2 * (q0 + uint64_t(cv)) + (ODD ? 1 : 0);  // its low word
@@ -434,8 +472,8 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
             resolve(ca1, cz1, cv1);
             resolve(ca2, cz2, cv2);
             resolve(ca3, cz3, cv3);
+            reduce_best();
         }
-        reduce_best();
     }
     if (threadIdx.x != 0) return;
     // The reference refuses a row whose maximum is NaN (any NaN: max_dim propagates it) or -inf
