@@ -27,8 +27,9 @@ struct GumbelP {
 };
 
 // z_v = tempered_logits (rl.rs:475-486) in f32: x / tau (skipped at tau == 1), then the
-// additive f32 mask, or -inf at a token a u8 keep-mask excludes.
-template <int DT, int MK>
+// additive f32 mask, or -inf at a token a u8 keep-mask excludes. Without DIV the division is
+// left to the caller (with a u8 mask or none it commutes with the exclusion: -inf / tau = -inf).
+template <int DT, int MK, bool DIV = true>
 __device__ __forceinline__ float tempered_at(const GumbelP &p, int64_t row, int64_t v) {
     float x;
     if constexpr (DT == NT_F32) {
@@ -36,7 +37,7 @@ __device__ __forceinline__ float tempered_at(const GumbelP &p, int64_t row, int6
     } else {
         x = __uint_as_float(uint32_t(static_cast<const uint16_t *>(p.logits)[row * p.ld + v]) << 16);
     }
-    if (!p.tau_one) x = x / p.tau;
+    if (DIV && !p.tau_one) x = x / p.tau;
     if constexpr (MK == NT_MASK_U8) {
         if (static_cast<const uint8_t *>(p.mask)[row * p.mask_ld + v] == 0) x = -INFINITY;
     } else if constexpr (MK == NT_MASK_F32) {
@@ -96,14 +97,14 @@ __device__ __forceinline__ void gumbel_load(GumbelRaw<DT, MK> &r, __amdgpu_buffe
 }
 
 // tempered_at's values from a loaded block (elements v0 .. v0 + 7; those at or past V are -inf).
-template <int DT, int MK>
+template <int DT, int MK, bool DIV = true>
 __device__ __forceinline__ void gumbel_values(const GumbelRaw<DT, MK> &r, const GumbelP &p, int v0, float (&z)[8]) {
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         float x;
         if constexpr (DT == NT_F32) x = __uint_as_float(r.x[j]);
         else x = __uint_as_float((j & 1) ? (r.x[j / 2] & 0xffff0000u) : (r.x[j / 2] << 16));
-        if (!p.tau_one) x = x / p.tau;
+        if (DIV && !p.tau_one) x = x / p.tau;
         if constexpr (MK == NT_MASK_U8) {
             if (((r.m[j / 4] >> (8 * (j % 4))) & 0xffu) == 0) x = -INFINITY;
         } else if constexpr (MK == NT_MASK_F32) {
@@ -182,6 +183,10 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
     // its merges break ties by index).
     auto walk = [&](auto compact_c, auto &&fn) {
         constexpr bool COMPACT = decltype(compact_c)::value && !GREEDY;
+        // COMPACT without an additive mask: the blocks are queued before the division by tau,
+        // which is done for the queued blocks only (the NaN and candidate tests give the same
+        // answers before it: tau > 0, and -inf and NaN stay so)
+        constexpr bool DEFER = COMPACT && MK != NT_MASK_F32;
         const int n = blockDim.x;
         // COMPACT: the row's blocks i = 0 .. nbk - 1 (keystream block b0 + i, elements
         // 8 i - r .. 8 i - r + 7), a wave's 64 consecutive ones per step, n apart. z_of(i, z) fills
@@ -201,7 +206,10 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
                     const int ie = qb[e];
                     float ze[8];
 #pragma unroll
-                    for (int j = 0; j < 8; j++) ze[j] = qz[j * kGumbelQueue + e];
+                    for (int j = 0; j < 8; j++) {
+                        ze[j] = qz[j * kGumbelQueue + e];
+                        if (DEFER && !p.tau_one) ze[j] = ze[j] / p.tau;
+                    }
                     fn(b0 + uint64_t(ie), 8 * int64_t(ie) - r, ze);
                 }
                 // (the reads are done before a later write reuses their slots)
@@ -257,7 +265,7 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
                 queued(nb, 0, [&](int i, float (&z)[8]) {
                     if (i + n < nb) gumbel_load<DT, MK>(nxt, xres, mres, 8 * (i + n));
                     if (i < nb) {
-                        gumbel_values<DT, MK>(cur, p, 8 * i, z);
+                        gumbel_values<DT, MK, !DEFER>(cur, p, 8 * i, z);
                     } else {
 #pragma unroll
                         for (int j = 0; j < 8; j++) z[j] = -INFINITY;
@@ -292,7 +300,7 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
                     const int64_t v = v0 + j;
-                    z[j] = (v >= 0 && v < V) ? tempered_at<DT, MK>(p, row, v) : -INFINITY;
+                    z[j] = (v >= 0 && v < V) ? tempered_at<DT, MK, !DEFER>(p, row, v) : -INFINITY;
                 }
             });
         } else {
