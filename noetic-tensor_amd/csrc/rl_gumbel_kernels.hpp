@@ -443,15 +443,16 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
         offer(ca2, cv2);
         offer(ca3, cv3);
         reduce_best();
-        if (count == 1 && !(flags & 6)) {
-            // (bidx is that candidate's)
+        if ((flags & 2) || !(flags & 1) || (count == 1 && !(flags & 4))) {
+            // a refused row (a NaN, or nothing allowed), or bidx is the one candidate's (with no
+            // thread's slots overflowed: an element left out of them could lie within the margin)
         } else if (flags & 4) {
             best = -INFINITY;
             bidx = 0x7fffffff;
             // a thread ran out of slots: every element exactly
             walk(std::true_type{}, [&](uint64_t b, int64_t v0, const float (&z)[8]) { draws(b, v0, z, exact); });
             reduce_best();
-        } else if (!(flags & 2)) {
+        } else {
             // the candidates within the margin of the row's largest, exactly (their blocks again)
             best = -INFINITY;
             bidx = 0x7fffffff;
