@@ -154,10 +154,11 @@ __device__ __forceinline__ float screen_floor(float x, float rel) {
 // The row's first maximum of z + g. Past temperature 0 it runs in two steps: every allowed
 // element's value is screened in f32 (the keystream is generated, the logarithms are the
 // hardware's), and only the elements whose screened value lies within the margin of the row's
-// largest are evaluated exactly (gumbel_f32, their keystream block generated again). The exact
-// maximum is among them: every screened value is within the margin's fiftieth of its exact one.
-// A thread whose candidates within the margin of its own largest outnumber its slots makes the
-// row take the exact evaluation of every element instead.
+// largest (screen_floor) are evaluated exactly (gumbel_f32, their keystream block generated
+// again). The exact maximum is among them, since the margin covers the screen's error and the
+// rounding of z + g on both sides; so a row with a single candidate has its answer without the
+// exact evaluation. A thread whose candidates within the margin of its own largest outnumber its
+// slots makes the row take the exact evaluation of every element instead.
 template <int DT, int MK, bool ODD, bool GREEDY>
 __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) {
     __shared__ float sbest[kGumbelMaxThreads / 64];
