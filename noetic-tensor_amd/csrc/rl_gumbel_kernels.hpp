@@ -217,10 +217,11 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
                 __builtin_amdgcn_wave_barrier();
             };
-            for (int base = 64 * wave; base < nbk; base += n) {
+            // (two steps per pass: z_of keeps a set of loads in flight per step parity)
+            auto step = [&](int base, auto par_c) {
                 const int i = base + lane;
                 float z[8];
-                z_of(i, z);
+                z_of(i, z, par_c);
                 bool any = false;
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
@@ -243,6 +244,10 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
                     head = (head + 64) % kGumbelQueue;
                     count -= 64;
                 }
+            };
+            for (int base = 64 * wave; base < nbk; base += 2 * n) {
+                step(base, std::integral_constant<int, 0>{});
+                if (base + n < nbk) step(base + n, std::integral_constant<int, 1>{});
             }
             if (count > 0) pop(lane < count);
         };
@@ -261,17 +266,20 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
                     short(0), int(V * (MK == NT_MASK_F32 ? 4 : 1)), kBufferWord3);
             GumbelRaw<DT, MK> cur, nxt;
             if constexpr (COMPACT) {
+                // two steps of loads in flight: the set of a step's parity is used, then loaded
+                // again for the step two ahead
                 const int i0 = 64 * wave + lane;
                 if (i0 < nb) gumbel_load<DT, MK>(cur, xres, mres, 8 * i0);
-                queued(nb, 0, [&](int i, float (&z)[8]) {
-                    if (i + n < nb) gumbel_load<DT, MK>(nxt, xres, mres, 8 * (i + n));
+                if (i0 + n < nb) gumbel_load<DT, MK>(nxt, xres, mres, 8 * (i0 + n));
+                queued(nb, 0, [&](int i, float (&z)[8], auto par_c) {
+                    GumbelRaw<DT, MK> &rr = decltype(par_c)::value ? nxt : cur;
                     if (i < nb) {
-                        gumbel_values<DT, MK, !DEFER>(cur, p, 8 * i, z);
+                        gumbel_values<DT, MK, !DEFER>(rr, p, 8 * i, z);
                     } else {
 #pragma unroll
                         for (int j = 0; j < 8; j++) z[j] = -INFINITY;
                     }
-                    cur = nxt;
+                    if (i + 2 * n < nb) gumbel_load<DT, MK>(rr, xres, mres, 8 * (i + 2 * n));
                 });
             } else {
                 int i = threadIdx.x;
@@ -296,7 +304,7 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
         } else if constexpr (COMPACT) {
             // element by element: block b0 + i holds elements 8 i - r .. 8 i - r + 7
             const int r = int(q0 & 7);
-            queued(int(b1 - b0 + 1), r, [&](int i, float (&z)[8]) {
+            queued(int(b1 - b0 + 1), r, [&](int i, float (&z)[8], auto) {
                 const int64_t v0 = 8 * int64_t(i) - r;
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
