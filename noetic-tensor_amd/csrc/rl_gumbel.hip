@@ -20,7 +20,7 @@
 //    sequential first maximum whatever the timing (a thread with more than four candidates sends
 //    its row to the exact evaluation of every element);
 //  - rows whose first u64 starts a block, on aligned rows, read a block's 8 logits and mask
-//    entries with vector loads issued a block ahead; others read element by element.
+//    entries with vector loads issued two steps ahead; others read element by element.
 #include <hip/hip_runtime.h>
 
 #include <cmath>

@@ -253,7 +253,7 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
         };
         if (!ODD && p.vec && (q0 & 7) == 0) {
             // The aligned path: keystream block b0 + i holds elements 8 i .. 8 i + 7 exactly, read
-            // with one or two 16-byte loads (the next block's issued before this block is used).
+            // with one or two 16-byte loads (with the queue, issued two steps ahead of their use).
             // Loads past the row read zeros (the buffer's range) and those elements are -inf.
             const int nb = int((V + 7) / 8);
             const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
