@@ -14,11 +14,12 @@
 //  - each wave queues its blocks that hold an allowed element in LDS and generates their
 //    keystream by full waves;
 //  - every allowed element's draw is first screened in f32 (hardware logarithms, within 1e-5 of
-//    the exact f32 value); only the elements within 1e-3 of the row's largest screened value are
-//    evaluated exactly, in f64 as the reference does, and the row's first maximum is taken among
-//    them with "greater value, else smaller index", which is associative, so the result is the
-//    sequential first maximum whatever the timing (a thread with more than four candidates sends
-//    its row to the exact evaluation of every element);
+//    the exact f32 value); only the elements within a margin of the row's largest screened value
+//    (1e-3, or four ulps of it where that is wider) can be the row's maximum. A single one is the
+//    answer; several are evaluated exactly, in f64 as the reference does, and the row's first
+//    maximum is taken among them with "greater value, else smaller index", which is associative,
+//    so the result is the sequential first maximum whatever the timing (a thread with more than
+//    four candidates sends its row to the exact evaluation of every element);
 //  - rows whose first u64 starts a block, on aligned rows, read a block's 8 logits and mask
 //    entries with vector loads issued two steps ahead; others read element by element.
 #include <hip/hip_runtime.h>
