@@ -418,8 +418,9 @@ def bench_gumbel(nr, W, args):
     roof = roofline(bytes_launch, ms)
     roof["inputs"] = (f"HBM-cold: launches cycle over {copies} input copies "
                       f"({copies * bytes_launch / 2**20:.0f} MiB), beyond the 256 MB Infinity Cache")
-    roof["note"] = ("bound by generating the draws (a ChaCha20 block per 8 logits and two f64 logarithms per "
-                    "allowed logit), not by HBM")
+    roof["note"] = ("bound by generating the draws (a ChaCha20 block per 8 logits holding an allowed one, and "
+                    "two f32 hardware logarithms per allowed logit; f64 only where a row has several "
+                    "candidates): the VALU instruction count, not HBM")
     roof["warm_cache"] = {"ms": ms_warm, "achieved": bytes_launch / (ms_warm * 1e-3) / 1e9,
                           "frac": bytes_launch / (ms_warm * 1e-3) / 1e9 / HBM_PEAK_GBS}
     config = {"workload": "c4 rows through the reference's Gumbel-max sample_categorical: bf16 logits "
