@@ -194,8 +194,10 @@ def test_many_near_ties_take_the_exact_path(pre_u32):
     assert np.array_equal(d, c), f"tokens differ from CpuRef: {np.nonzero(d != c)[0]}"
 
 
+@pytest.mark.parametrize("mask", ["none", "keep", "add"])
+@pytest.mark.parametrize("tau", [1.0, 0.7])
 @pytest.mark.parametrize("pre_u32", [0, 1])
-def test_large_logits_where_an_ulp_of_the_sum_passes_the_absolute_margin(pre_u32):
+def test_large_logits_where_an_ulp_of_the_sum_passes_the_absolute_margin(pre_u32, tau, mask):
     # At |z| of 2^16 and 1e6 an ulp of z + g (2^-7, 2^-4) is wider than the screen's 1e-3: the
     # screened and exact sums of two elements can order differently by an ulp, and exact sums tie
     # often. The margin grows with |z| (4 ulps), so the row's few candidates within it are
@@ -206,5 +208,13 @@ def test_large_logits_where_an_ulp_of_the_sum_passes_the_absolute_margin(pre_u32
     x[:8] = 65536.0 + rng.normal(0, 1.0, (8, V))
     x[8:16] = 1e6 + rng.normal(0, 0.5, (8, V))
     x[16:] = -3e5 + rng.normal(0, 0.2, (8, V))
-    d, c = both(x, 1.0, 29, "large logits", pre_u32=pre_u32)
+    # (a u8 keep-mask divides only the queued blocks by tau; an additive f32 mask divides first)
+    keep = addmask = None
+    if mask == "keep":
+        keep = (rng.random((rows, V)) < 0.5).astype(np.uint8)
+        keep[:, 0] = 1
+    elif mask == "add":
+        addmask = np.where(rng.random((1, V)) < 0.5, -np.inf, 0.0).astype(np.float32)
+        addmask[0, 0] = 0.0
+    d, c = both(x, tau, 29, "large logits", keep=keep, addmask=addmask, pre_u32=pre_u32)
     assert np.array_equal(d, c), f"tokens differ from CpuRef: {np.nonzero(d != c)[0]}"
