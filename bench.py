@@ -137,6 +137,25 @@ def timed(nr, steps, warmup, step):
     return ms.value / steps, wall
 
 
+def practical_floor(nr, bytes_launch, traffic, ms, blocks):
+    """The practical floor of one launch on this box, measured in this run with the library's own
+    kernels (include/noetic_measure.h): the device's streaming-read rate over 2 GiB (beyond the
+    Infinity Cache) and the period of back-to-back launches of a kernel that does nothing, with
+    the sampler's grid (one 1024-thread workgroup per row). floor = period + bytes / read rate,
+    for the algorithmic bytes and for the HBM bytes the counters measured (`traffic`)."""
+    L = nr.lib()
+    gbs, us = C.c_double(), C.c_double()
+    nr._check(L.nt_measure_read(C.c_size_t(2 << 30), 10, C.byref(gbs)), "measure read")
+    nr._check(L.nt_measure_launch_period(blocks, 1024, 2000, C.byref(us)), "measure launch period")
+    out = {"read_gbs": gbs.value, "launch_period_us": us.value,
+           "floor_us": us.value + bytes_launch / (gbs.value * 1e3),
+           "what": "floor = launch period + algorithmic bytes / measured read rate; frac_of_floor = floor / launch time"}
+    out["frac_of_floor"] = out["floor_us"] / (ms * 1e3)
+    if traffic:
+        out["floor_us_on_traffic"] = us.value + traffic / (gbs.value * 1e3)
+    return out
+
+
 def roofline(bytes_launch, ms, traffic_file=None):
     gbs = bytes_launch / (ms * 1e-3) / 1e9
     r = {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
@@ -333,7 +352,7 @@ def bench_sample(nr, W, args, name):
     nr._check(L.nt_hip_rl_sample(C.byref(cold[0])), "sample")
     gpu_out = (ids.to_numpy().ravel().astype(np.int64), logp.to_numpy().ravel().copy(),
                U.to_numpy().ravel()[:rows].copy())
-    roof = roofline(bytes_launch, ms, "k_sample_rr_c4_traffic.json" if name == "c4" else None)
+    roof = roofline(bytes_launch, ms, "k_sample_rq_c4_traffic.json" if name == "c4" else None)
     roof["inputs"] = (f"HBM-cold: launches cycle over {copies} input copies "
                       f"({copies * bytes_launch / 2**20:.0f} MiB), beyond the 256 MB Infinity Cache")
     roof["warm_cache"] = {"ms": ms_warm, "achieved": bytes_launch / (ms_warm * 1e-3) / 1e9,
@@ -341,6 +360,7 @@ def bench_sample(nr, W, args, name):
                           "inputs": "one input re-read every launch (served partly by the Infinity Cache)"}
     if name == "c4":
         roof["measured_copy_gbs"] = copy_peak(nr)  # a device-to-device copy on this box, for scale
+        roof["practical"] = practical_floor(nr, bytes_launch, roof.get("traffic"), ms, rows)
     if name == "c4s":
         metric = "rows/sec + achieved HBM GB/s, fused masked sample+logprob, V=128256 bf16, one shared mask"
         config = {"workload": "c4 with one u8 grammar mask [1,V] shared by the 256 rows (mask_ld 0): bf16 logits "

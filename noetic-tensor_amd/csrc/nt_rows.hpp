@@ -314,6 +314,18 @@ __device__ __forceinline__ uint2 lds_read_b64_off(uint32_t addr) {
     asm volatile("ds_read_b64 %0, %1 offset:%2\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
     return r;
 }
+// Four such reads at immediate offsets from one address, then one wait. The results are
+// early-clobber: the reads are still in flight while the address register is read again.
+template <int O0, int O1, int O2, int O3>
+__device__ __forceinline__ void lds_read4_b64(uint32_t addr, uint2 &r0, uint2 &r1, uint2 &r2, uint2 &r3) {
+    static_assert(O0 >= 0 && O3 < 65536 && O1 < 65536 && O2 < 65536, "ds offset field");
+    asm volatile(
+        "ds_read_b64 %0, %4 offset:%5\n\tds_read_b64 %1, %4 offset:%6\n\t"
+        "ds_read_b64 %2, %4 offset:%7\n\tds_read_b64 %3, %4 offset:%8\n\ts_waitcnt lgkmcnt(0)"
+        : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
+        : "v"(addr), "i"(O0), "i"(O1), "i"(O2), "i"(O3)
+        : "memory");
+}
 __device__ __forceinline__ uint4 lds_read_b128(uint32_t addr) {
     uint4 r;
     asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(addr) : "memory");

@@ -103,6 +103,40 @@ void launch_rr(int dtype, int mk, int K, bool ent, bool allw, const SampleP &p, 
     }
 }
 
+// The queued sampler (u8 keep-masks): K chunks per wave in stages of 4 (K = 4) or 8 (K = 16)
+// chunks, two stages from K = 8 on.
+template <int DT, int K>
+void launch_rq_k(bool ent, const SampleP &p, int64_t rows, hipStream_t s) {
+    constexpr int NS = K >= 8 ? 2 : 1;
+    char nm[96];
+    std::snprintf(nm, sizeof nm, "nt::k_sample_rq<%d, %d, %s, %d>", DT, K, rtc_bool(ent), NS);
+    if (ent) launch_path(k_sample_rq<DT, K, true, NS>, nm, dim3(unsigned(rows)), dim3(kRRThreads), 0, s, p);
+    else launch_path(k_sample_rq<DT, K, false, NS>, nm, dim3(unsigned(rows)), dim3(kRRThreads), 0, s, p);
+}
+
+void launch_rq(int dtype, int K, bool ent, const SampleP &p, int64_t rows, hipStream_t s) {
+    if (dtype == NT_F32) {
+        if (K == 4) launch_rq_k<NT_F32, 4>(ent, p, rows, s);
+        else launch_rq_k<NT_F32, 8>(ent, p, rows, s);
+    } else {
+        if (K == 4) launch_rq_k<NT_BF16, 4>(ent, p, rows, s);
+        else if (K == 8) launch_rq_k<NT_BF16, 8>(ent, p, rows, s);
+        else launch_rq_k<NT_BF16, 16>(ent, p, rows, s);
+    }
+}
+
+// Whether a u8-masked launch of K chunks per wave takes the queued sampler: K of 4 or more (the
+// queue's stages are 4 chunks at least), a mask whose rows start on 16 bytes (the mask comes in
+// 16-byte pieces per lane), and no NOETIC_HIP_SAMPLE_QUEUE=off (a tuning knob that keeps the
+// register-resident sampler). Measured on MI355X at 256 rows of V = 128256 bf16, tau 0.7, HBM-cold
+// inputs: a grammar mask of runs (30% kept) 20.2 -> 16.8 us, a Bernoulli(0.9) mask 20.2 -> 20.4 us
+// (its waves take the dense path); at V = 50304 f32, runs 14.6 -> 10.2 us, Bernoulli 14.6 -> 14.4 us.
+bool use_queue(int mk, int K, const void *mask, int64_t mask_ld) {
+    if (mk != NT_MASK_U8 || K < 4) return false;
+    if (reinterpret_cast<uintptr_t>(mask) % 16 != 0 || mask_ld % 16 != 0) return false;
+    const char *env = std::getenv("NOETIC_HIP_SAMPLE_QUEUE");
+    return !(env && std::strcmp(env, "off") == 0);
+}
 
 // ------------------------------------------------------------------ segmented dispatch
 
@@ -337,7 +371,8 @@ int sample_entry(const NtRlSampleArgs *a, WorkspaceFn workspace, bool nofree, co
             while (int64_t(kRRWaves) * K < nch) K *= 2;
             p.nc = int(nch);
             rtc_status() = 0;
-            launch_rr<8>(a->dtype, a->mask_kind, K, ent, all_in_flight(a->rows), p, a->rows, s);
+            if (use_queue(a->mask_kind, K, a->mask, a->mask_ld)) launch_rq(a->dtype, K, ent, p, a->rows, s);
+            else launch_rr<8>(a->dtype, a->mask_kind, K, ent, all_in_flight(a->rows), p, a->rows, s);
             return rtc_status() ? rtc_status() : launched(who);
         }
     }

@@ -652,6 +652,482 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     }
 }
 
+// ------------------------------------------------------------------ queued sampler (u8 keep-masks)
+//
+// With a u8 keep-mask an excluded token's value is -inf whatever its logit (NaN and +inf
+// included), so its logit never needs to be read or weighed. This kernel is the
+// register-resident sampler reorganised around that: one 1024-thread workgroup per row, each
+// wave owning K consecutive chunks of 512 elements, taken in NS stages of KS = K / NS chunks.
+//  - The mask comes first: the wave's mask bytes of stage s + 1 stream into LDS (1 KiB per
+//    instruction) while stage s is queued.
+//  - Queue: a lane group is 8 consecutive elements (one 16-byte bf16 load, two f32 ones). The
+//    groups of a stage's chunks that keep a token are listed in index order in LDS (a ballot and
+//    a lane count per chunk).
+//  - Slot j of stage s holds the stage's queue entries [64 j, 64 j + 64), one per lane; its
+//    logits are loaded straight from HBM into the slot's registers. Lanes past the queue's end,
+//    and slots past it, load through an out-of-range buffer offset: no memory is read and they
+//    weigh nothing. A row whose kept tokens lie in runs reads only the 128-byte lines that hold
+//    one.
+//  - Slots are weighed as the register-resident sampler weighs chunks (the same exponent
+//    reference rule, the same four 16-lane partials per slot), one stage behind the loads.
+// A wave whose first stage keeps a token in more than kRqDense of its lane groups reads the
+// rest of its chunks as the register-resident sampler does instead (dense path): every lane
+// group loaded in place with its chunk's mask, one chunk ahead of the one being weighed, so a
+// dense mask pays only the first stage's wait for its mask bytes. Each wave keeps, per slot and
+// lane, the LDS address of its group's mask bytes (a zero word for an empty lane), from which the
+// group's element index and its mask are read again when the draw lands in it.
+// Phases 2 and 3 are the register-resident sampler's with slots in place of chunks: within a
+// wave the slots are in index order (queue entries, or chunks), so the waves' slots in order
+// run through the row's kept elements in order. Every load and wait on either path is in a fixed
+// order whatever the mask (empty slots load nothing but still issue), so each wait count is a
+// compile-time constant.
+
+// The share of a first stage's lane groups with a kept token above which a wave takes the dense
+// path.
+constexpr int kRqDensePct = 70;
+
+template <int DT, int K, bool ENT, int NS>
+__global__ __launch_bounds__(kRRThreads) void k_sample_rq(SampleP p) {
+    constexpr int MK = NT_MASK_U8;
+    constexpr int EPL = 8;
+    constexpr int CH = kWave * EPL;                // elements (and mask bytes) per chunk
+    constexpr int NCH = K * kRRWaves;
+    constexpr int KS = K / NS;                     // chunks per stage = slots per stage
+    static_assert(K % NS == 0 && KS % 4 == 0, "stages of a multiple of 4 chunks");
+    constexpr int MD = KS * CH / 1024;             // 1 KiB mask DMAs per stage
+    constexpr int LX = RRX<DT, EPL>::kPieces;      // 16-byte logit loads per lane group
+    __shared__ __attribute__((aligned(16))) uint8_t mlds[NCH * CH];            // the row's mask bytes
+    __shared__ __attribute__((aligned(16))) uint16_t qpos[kRRWaves * KS * kWave];  // per wave: a stage's queue
+    __shared__ __attribute__((aligned(16))) float csum4[NCH * 4];  // per slot and 16-lane row: sum of 2^(v c - wref)
+    __shared__ __attribute__((aligned(16))) float cent4[ENT ? NCH * 4 : 4];  // per slot and row: sum of w (v c - wref)
+    __shared__ float wref[kRRWaves];
+    __shared__ float wmax[kRRWaves];
+    __shared__ double wtot[kRRWaves];
+    __shared__ double went[ENT ? kRRWaves : 1];
+    __shared__ int wpick[kRRWaves];
+    __shared__ __attribute__((aligned(8))) uint32_t zmask[2];  // the mask words of an empty lane
+
+    const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const float c = p.c;
+    const bool tau_one = p.tau_one != 0;
+    const void *xrow = static_cast<const char *>(p.logits) + row * p.ld * Elem<DT>::kBytes;
+    const uint8_t *mrow = static_cast<const uint8_t *>(p.mask) + row * p.mask_ld;
+    const uint32_t mbase = uint32_t((uintptr_t)(lds_ptr_t)(mlds));
+    const uint32_t zaddr = uint32_t((uintptr_t)(lds_ptr_t)(zmask));
+    const double u_row = p.greedy ? 0.0 : p.u[row];
+    const int Vi = int(p.V);
+    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void *>(xrow), short(0), int(p.V * Elem<DT>::kBytes), kBufferWord3);
+    const __amdgpu_buffer_rsrc_t mres =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(mrow), short(0), Vi, kBufferWord3);
+    // Offsets past every row: such a load reads nothing and returns zeros. Each slot has its
+    // own, so that no two of a wave's loads are ever the same load (the compiler would merge
+    // those, and the waits below count loads).
+    constexpr int kNoRead = 0x40000000;
+    // Every wave zeroes the empty lane's words itself (the same bits), so its own reads of
+    // them follow its own store.
+    if (lane < 2) zmask[lane] = 0u;
+
+    RRX<DT, EPL> raw[K];  // slot k's logit words
+    uint32_t ma[K];       // slot k: the LDS address of this lane's group's mask bytes (zmask: none)
+    uint16_t *const q = qpos + wave * KS * kWave;
+
+    // The wave's mask bytes of stage s into mlds (the row's bytes at their own offsets), with
+    // non-temporal loads: at C4 (256 rows of V = 128256 bf16, a runs mask, tau 0.7, each process
+    // timing one policy) 16.8 -> 15.7 us per launch HBM-cold and 15.4 -> 14.5 us re-reading one
+    // input; non-temporal logit loads as well measured 15.6 and 15.1 us.
+    auto issue_mask = [&](auto sc) {
+        constexpr int s = decltype(sc)::value;
+        const int b0 = (wave * K + s * KS) * CH;
+        static_for<0, MD>([&](auto dc) {
+            constexpr int d = decltype(dc)::value;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(mres, (lds_ptr_t)(mlds + b0 + d * 1024), 16,
+                                                     b0 + d * 1024 + 16 * lane, 0, 0, kCachePolicyNT);
+        });
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // Queue stage s's lane groups that keep a token, in index order; returns the count (uniform).
+    auto build = [&](auto sc) -> int {
+        constexpr int s = decltype(sc)::value;
+        const int e00 = (wave * K + s * KS) * CH + lane * EPL;  // this lane's group in the stage's first chunk
+        int cnt = 0;
+        static_for<0, KS / 4>([&](auto gc) {
+            constexpr int g = decltype(gc)::value;
+            uint2 m[4];
+            lds_read4_b64<(4 * g) * CH, (4 * g + 1) * CH, (4 * g + 2) * CH, (4 * g + 3) * CH>(
+                mbase + e00, m[0], m[1], m[2], m[3]);
+            static_for<0, 4>([&](auto ic) {
+                constexpr int i = decltype(ic)::value;
+                constexpr int cl = 4 * g + i;
+                const bool act = ((m[i].x | m[i].y) != 0u) && e00 + cl * CH < Vi;
+                const uint64_t bal = __ballot(act);
+                if (act)
+                    q[cnt + int(__builtin_amdgcn_mbcnt_hi(uint32_t(bal >> 32),
+                                                          __builtin_amdgcn_mbcnt_lo(uint32_t(bal), 0u)))] =
+                        uint16_t(cl * kWave + lane);
+                cnt += __builtin_popcountll(bal);
+            });
+        });
+        return cnt;
+    };
+    // Stage s's slot loads: lane l of slot j takes queue entry 64 j + l.
+    auto issue_queued = [&](auto sc, int cnt) {
+        constexpr int s = decltype(sc)::value;
+        const int sb = (wave * K + s * KS) * CH;
+        static_for<0, KS>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            const int idx = j * kWave + lane;
+            const bool valid = idx < cnt;
+            const int e0 = sb + int(q[valid ? idx : 0]) * EPL;
+            ma[s * KS + j] = valid ? mbase + uint32_t(e0) : zaddr;
+            const int xo = valid ? e0 * Elem<DT>::kBytes : kNoRead + 4096 * (s * KS + j);
+#pragma unroll
+            for (int pc = 0; pc < LX; pc++) {
+                const auto a = __builtin_amdgcn_raw_buffer_load_b128(xres, xo + 16 * pc, 0, 0);
+                raw[s * KS + j].x[4 * pc] = a[0];
+                raw[s * KS + j].x[4 * pc + 1] = a[1];
+                raw[s * KS + j].x[4 * pc + 2] = a[2];
+                raw[s * KS + j].x[4 * pc + 3] = a[3];
+            }
+        });
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // ---- phase 1, weighing: as the register-resident sampler's, per slot.
+    float *const cpart = csum4 + 4 * K * wave + lane / 16;
+    float *const epart = ENT ? cent4 + 4 * K * wave + lane / 16 : nullptr;
+    const bool row_leader = (lane & 15) == 0;
+    bool have_ref = false;
+    float lmax = -INFINITY;
+    float sref = -INFINITY;
+    float sref_v = -INFINITY;
+    // Weigh slot k; its mask words are read here (the caller has waited for its loads, which
+    // follow its mask bytes).
+    auto weigh_slot = [&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        const uint2 m2 = lds_read_b64(ma[k]);
+        const uint32_t mw[2] = {m2.x, m2.y};
+        float v[EPL];
+        decode_e<DT, MK, EPL>(raw[k].x, mw, v, p.tau, tau_one);
+        if (p.greedy) {
+            const float m8 = max_hw<EPL>(v);
+            lmax = max3_hw(lmax, m8, m8);
+        }
+        if (!have_ref) {
+            const float wm = wave_max3_dpp(max_hw<EPL>(v));
+            if (wm != -INFINITY) {
+                have_ref = true;
+                sref_v = wm;
+                sref = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(wm * c)));
+            }
+        }
+        float gs = 0.0f, gh = 0.0f;
+        auto weigh = [&]() {
+            float w[EPL], h[EPL];
+#pragma unroll
+            for (int jj = 0; jj < EPL; jj++) {
+                const float d = fmaf(v[jj], c, -sref);
+                w[jj] = exp2_hw(d);
+                if constexpr (ENT) h[jj] = w[jj] * fmaxf(d, -FLT_MAX);
+            }
+            gs = tree_sum<EPL>(w);
+            if constexpr (ENT) gh = tree_sum<EPL>(h);
+        };
+        if (have_ref) {
+            weigh();
+            bool move = !(gs < INFINITY);
+            if constexpr (ENT) move = !(gs <= kChunkSumCap);
+            if (__ballot(move) != 0) {
+                const float wm = wave_max3_dpp(max_hw<EPL>(v));
+                const float nref = wm * c;
+                if (nref > sref) {
+                    const float dk = sref - nref, f = exp2_hw(dk);
+                    if ((lane & 15) == 0) {
+                        static_for<0, k>([&](auto kc2) {
+                            constexpr int kk = decltype(kc2)::value;
+                            const int idx = (wave * K + kk) * 4 + lane / 16;
+                            const float o = csum4[idx];
+                            csum4[idx] = f * o;
+                            if constexpr (ENT) cent4[idx] = f * (cent4[idx] + dk * o);
+                        });
+                    }
+                    sref = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(nref)));
+                    sref_v = wm;
+                    weigh();
+                }
+            }
+        }
+        const float cs = row_sum_dpp(gs);
+        float ce = 0.0f;
+        if constexpr (ENT) ce = row_sum_dpp(gh);
+        if (row_leader) {
+            cpart[4 * k] = cs;
+            if constexpr (ENT) epart[4 * k] = ce;
+        }
+    };
+    // An empty slot weighs nothing (its partials are read with the others').
+    auto empty_slot = [&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        ma[k] = zaddr;
+        if (row_leader) {
+            cpart[4 * k] = 0.0f;
+            if constexpr (ENT) epart[4 * k] = 0.0f;
+        }
+    };
+    // Weigh stage s's slots that hold entries; `after` is the number of loads issued after the
+    // stage's last one.
+    auto weigh_stage = [&](auto sc, auto afterc, int cnt) {
+        constexpr int s = decltype(sc)::value;
+        constexpr int after = decltype(afterc)::value;
+        const int nb = (cnt + kWave - 1) / kWave;
+        static_for<0, KS>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            if (j < nb) {
+                wait_vmcnt<after + (KS - 1 - j) * LX>();
+                weigh_slot(std::integral_constant<int, s * KS + j>{});
+            } else {
+                empty_slot(std::integral_constant<int, s * KS + j>{});
+            }
+        });
+    };
+
+    // ---- the first stage's mask, then the path.
+    issue_mask(std::integral_constant<int, 0>{});
+    wait_vmcnt<0>();
+    const int cnt0 = build(std::integral_constant<int, 0>{});
+    if (cnt0 * 100 > kRqDensePct * KS * kWave) {
+        // Dense path: chunk k's logits in place (and, past the first stage, its mask bytes,
+        // 4 per lane, as the register-resident sampler brings them), chunk k + 1 issued before
+        // chunk k is weighed.
+        constexpr int DMB = CH / (4 * kWave);  // mask DMAs per chunk past the first stage
+        auto issue_dense = [&](auto kc) {
+            constexpr int k = decltype(kc)::value;
+            const int ch = wave * K + k;
+            const int e0 = ch * CH + lane * EPL;
+            const bool in = e0 < Vi;
+            ma[k] = in ? mbase + uint32_t(e0) : zaddr;
+            const int xo = in ? e0 * Elem<DT>::kBytes : kNoRead + 4096 * k;
+#pragma unroll
+            for (int pc = 0; pc < LX; pc++) {
+                const auto a = __builtin_amdgcn_raw_buffer_load_b128(xres, xo + 16 * pc, 0, 0);
+                raw[k].x[4 * pc] = a[0];
+                raw[k].x[4 * pc + 1] = a[1];
+                raw[k].x[4 * pc + 2] = a[2];
+                raw[k].x[4 * pc + 3] = a[3];
+            }
+            if constexpr (k >= KS) {
+                static_for<0, DMB>([&](auto dc) {
+                    constexpr int d = decltype(dc)::value;
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(mres, (lds_ptr_t)(mlds + ch * CH + d * 4 * kWave), 4,
+                                                             ch * CH + d * 4 * kWave + 4 * lane, 0, 0, kCachePolicyNT);
+                });
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        issue_dense(std::integral_constant<int, 0>{});
+        static_for<0, K>([&](auto kc) {
+            constexpr int k = decltype(kc)::value;
+            if constexpr (k + 1 < K) {
+                issue_dense(std::integral_constant<int, k + 1>{});
+                wait_vmcnt<LX + (k + 1 >= KS ? DMB : 0)>();
+            } else {
+                wait_vmcnt<0>();
+            }
+            weigh_slot(kc);
+        });
+    } else {
+        // Queued path: M_0 | queue 0, M_1, L_0 | wait M_s, queue s, M_{s+1}, L_s, weigh s - 1 |
+        // weigh the last stage. After M_s only L_{s-1} is issued, so its wait leaves KS LX loads
+        // in flight.
+        int cnt[NS];
+        cnt[0] = cnt0;
+        static_for<0, NS>([&](auto sc) {
+            constexpr int s = decltype(sc)::value;
+            if constexpr (s > 0) {
+                wait_vmcnt<KS * LX>();
+                cnt[s] = build(sc);
+            }
+            if constexpr (s + 1 < NS) issue_mask(std::integral_constant<int, s + 1>{});
+            issue_queued(sc, cnt[s]);
+            if constexpr (s >= 1)
+                weigh_stage(std::integral_constant<int, s - 1>{},
+                            std::integral_constant<int, KS * LX + (s + 1 < NS ? MD : 0)>{}, cnt[s - 1]);
+        });
+        weigh_stage(std::integral_constant<int, NS - 1>{}, std::integral_constant<int, 0>{}, cnt[NS - 1]);
+    }
+
+    // ---- end of phase 1: lane k < K takes slot k's sum in f64; the f64 prefix over the wave's
+    // slots stays in registers and the wave's totals go to LDS.
+    double wcs = 0.0, wce = 0.0;
+    if (lane < K) {
+        const float4 qs = *reinterpret_cast<const float4 *>(csum4 + 4 * (wave * K + lane));
+        wcs = double((qs.x + qs.y) + (qs.z + qs.w));
+        if constexpr (ENT) {
+            const float4 e = *reinterpret_cast<const float4 *>(cent4 + 4 * (wave * K + lane));
+            wce = double((e.x + e.y) + (e.z + e.w));
+        }
+    }
+    const double wincl = row_scan_dpp(wcs);
+    {
+        const float wm = p.greedy ? wave_max3_dpp(lmax) : sref_v;
+        double wh = 0.0;
+        if constexpr (ENT) wh = row_scan_dpp(wce);
+        if (lane == kRRWaves - 1) {
+            wtot[wave] = wincl;
+            if constexpr (ENT) went[wave] = wh;
+        }
+        if (lane == 0) {
+            wmax[wave] = wm;
+            wref[wave] = sref;
+        }
+    }
+    __syncthreads();
+
+    // ---- phase 2: the register-resident sampler's.
+    const int lw = lane & (kRRWaves - 1);
+    const float rw = wref[lw];
+    const double tw = wtot[lw];
+    double hw = 0.0;
+    if constexpr (ENT) hw = went[lw];
+    const float M = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(row_max3_dpp(wmax[lw]))));
+    auto refuse = [&](uint8_t st, bool leader) {
+        if (leader) {
+            p.ids[row] = -1;
+            if (p.logp) p.logp[row] = NAN;
+            if (p.ent) p.ent[row] = NAN;
+            p.status[row] = st;
+        }
+    };
+    if (M == -INFINITY) {
+        refuse(NT_ROW_NO_TOKEN, tid == 0);
+        return;
+    }
+    const float A = M * c;
+    const bool wlive = rw != -INFINITY;
+    const float wf = wlive ? exp2_hw(rw - A) : 0.0f;
+    const double wt = wlive ? double(wf) * tw : 0.0;
+    const double incl = row_scan_dpp(wt);
+    const double S = readlane_d(incl, kRRWaves - 1);
+    if (!(S == S)) {
+        refuse(NT_ROW_NAN, tid == 0);
+        return;
+    }
+    auto entropy_sum = [&]() -> double {
+        if constexpr (!ENT) return 0.0;
+        const double lh = (wlive && tw > 0.0) ? double(wf) * (hw + double(rw - A) * tw) : 0.0;
+        return readlane_d(row_scan_dpp(lh), kRRWaves - 1);
+    };
+    auto write_row = [&](int64_t id, float vz, double H) {
+        const double shiftA = double(A) - double(M) * double(c);
+        const double lnS = ln_fast(S) + shiftA * kLn2;
+        const float zid = tau_one ? vz : vz / p.tau;
+        const float mz = tau_one ? M : M / p.tau;
+        p.ids[row] = int32_t(id);
+        if (p.logp) p.logp[row] = float((double(zid) - double(mz)) - lnS);
+        if (p.ent) p.ent[row] = float(lnS - kLn2 * (H / S + shiftA));
+        p.status[row] = NT_ROW_OK;
+    };
+    // A weighed slot's values, its mask read again (an empty lane reads the zero words: -inf).
+    auto slot_values = [&](const RRX<DT, EPL> &r, uint32_t a, float *v) {
+        const uint2 m2 = lds_read_b64(a);
+        const uint32_t mw[2] = {m2.x, m2.y};
+        decode_e<DT, MK, EPL>(r.x, mw, v, p.tau, tau_one);
+    };
+
+    if (p.greedy) {
+        int first = 0x7fffffff;
+        static_for<0, K>([&](auto kc) {
+            constexpr int k = decltype(kc)::value;
+            if (ma[k] != zaddr) {
+                float v[EPL];
+                slot_values(raw[k], ma[k], v);
+#pragma unroll
+                for (int j = EPL - 1; j >= 0; j--)
+                    if (v[j] == M) first = min(first, int(ma[k] - mbase) + j);
+            }
+        });
+        first = wave_min_i(first);
+        if (lane == 0) wpick[wave] = first;
+        __syncthreads();
+        int best = 0x7fffffff;
+        for (int i = 0; i < kRRWaves; i++) best = min(best, wpick[i]);
+        const double H = entropy_sum();
+        if (tid == 0) write_row(best, M, H);
+        return;
+    }
+
+    const double t = u_row * S;
+    const bool wl = lane < kRRWaves;
+    int wsel = first_lane(__ballot(wl && incl > t && wt > 0.0));
+    if (wsel < 0) wsel = last_lane(__ballot(wl && wt > 0.0));
+    if (wsel < 0) {
+        refuse(NT_ROW_NAN, tid == 0);
+        return;
+    }
+    if (wave != wsel) return;
+    // ---- phase 3 (that wave alone): the crossing slot from the prefix, then its registers.
+    const double tl = readlane_d((t - (incl - wt)) * double(exp2_hw(A - rw)), wsel);
+    const bool lk = lane < K;
+    int kstar = first_lane(__ballot(lk && wincl > tl && wcs > 0.0));
+    if (kstar < 0) kstar = last_lane(__ballot(lk && wcs > 0.0));
+    if (kstar < 0) {
+        refuse(NT_ROW_NAN, lane == 0);
+        return;
+    }
+    const double tloc = readlane_d(tl - (wincl - wcs), kstar);
+    const double H = entropy_sum();
+    RRX<DT, EPL> r = raw[0];
+    uint32_t ar = ma[0];
+    static_for<1, K>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        if (k == kstar) {
+            r = raw[k];
+            ar = ma[k];
+        }
+    });
+    float v[EPL];
+    slot_values(r, ar, v);
+    const float sr = sref;
+    float w[EPL];
+    int jlast = -1;
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {
+        w[j] = exp2_hw(fmaf(v[j], c, -sr));
+        if (w[j] > 0.0f) jlast = j;
+    }
+    const double ls = double(tree_sum<EPL>(w));
+    const double cincl = wave_scan_dpp(ls);
+    int lsel = first_lane(__ballot(cincl > tloc && ls > 0.0));
+    const bool none = lsel < 0;
+    if (none) lsel = last_lane(__ballot(jlast >= 0));
+    if (lsel < 0) {
+        refuse(NT_ROW_NAN, lane == 0);
+        return;
+    }
+    int jsel = -1;
+    {
+        const double t0 = tloc - (cincl - ls);
+        float C = 0.0f;
+#pragma unroll
+        for (int j = 0; j < EPL; j++) {
+            C += w[j];
+            if (jsel < 0 && !none && double(C) > t0) jsel = j;
+        }
+        if (jsel < 0) jsel = jlast;
+    }
+    if (lane == lsel) {
+        if (jsel < 0) jsel = 0;
+        float vz = v[0];
+#pragma unroll
+        for (int j = 1; j < EPL; j++)
+            if (j == jsel) vz = v[j];
+        write_row(int64_t(ar - mbase) + jsel, vz, H);
+    }
+}
+
 // ------------------------------------------------------------------ segmented sampler
 //
 // Rows too few to fill the chip (C2's 64 rows on 256 CUs), and rows whose tail should overlap

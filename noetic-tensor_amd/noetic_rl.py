@@ -197,6 +197,8 @@ _SIGS = {
     "nt_synth_keep_tokens": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_void_p]),
     "nt_synth_runs_mask_host": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_uint64, C.c_char_p, C.c_size_t,
                                           C.c_int32, C.c_int32]),
+    "nt_measure_read": (C.c_int, [C.c_size_t, C.c_int32, C.POINTER(C.c_double)]),
+    "nt_measure_launch_period": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, C.POINTER(C.c_double)]),
 }
 
 _lib = None

@@ -86,7 +86,17 @@ def cases():
 
 @pytest.mark.parametrize("dtype,mask,K,V", cases())
 def test_register_resident_sampler_levels(dtype, mask, K, V, monkeypatch):
+    """u8 rows of K >= 4 take the queued sampler by default (these masks keep 70% of the tokens,
+    so its waves take its dense path); the test below runs them through the register-resident
+    sampler itself."""
     monkeypatch.setenv("NOETIC_HIP_SAMPLE_SEG", "off")  # one workgroup per row, whatever the row count
+    check_levels(dtype, mask, K, V)
+
+
+@pytest.mark.parametrize("dtype,mask,K,V", [c for c in cases() if c[1] == "u8" and c[2] >= 4])
+def test_register_resident_sampler_levels_without_queue(dtype, mask, K, V, monkeypatch):
+    monkeypatch.setenv("NOETIC_HIP_SAMPLE_SEG", "off")
+    monkeypatch.setenv("NOETIC_HIP_SAMPLE_QUEUE", "off")
     check_levels(dtype, mask, K, V)
 
 
