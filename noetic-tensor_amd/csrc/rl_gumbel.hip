@@ -100,13 +100,15 @@ extern "C" int nt_hip_rl_sample_gumbel(const NtRlGumbelArgs *a) {
     const bool odd = (w0 & 1) != 0;
     p.ids = a->ids;
     p.status = a->status;
-    // the aligned path: rows and mask rows start on their vector loads' alignment, and a row's
-    // bytes fit a buffer resource's 32-bit range
+    // the aligned path: rows and mask rows start on their vector loads' alignment, V is a whole
+    // number of 8-element blocks (so no 16- or 8-byte load ends partly past the row's bytes, and
+    // what a load past the end returns is all zeros), and a row's bytes fit a buffer resource's
+    // 32-bit range
     const int esz = a->dtype == NT_F32 ? 4 : 2, msz = a->mask_kind == NT_MASK_F32 ? 4 : 1;
     const bool mask_vec = a->mask_kind == NT_MASK_NONE ||
                           (reinterpret_cast<uintptr_t>(a->mask) % (a->mask_kind == NT_MASK_F32 ? 16 : 8) == 0 &&
                            (a->mask_ld * msz) % (a->mask_kind == NT_MASK_F32 ? 16 : 8) == 0);
-    p.vec = reinterpret_cast<uintptr_t>(a->logits) % 16 == 0 && (a->ld * esz) % 16 == 0 && mask_vec &&
+    p.vec = reinterpret_cast<uintptr_t>(a->logits) % 16 == 0 && (a->ld * esz) % 16 == 0 && mask_vec && V % 8 == 0 &&
             V * 4 <= int64_t(0x7fffffff);
     // Threads per row: one per keystream block of the row, in whole waves, at most 1024.
     const int64_t nblk = V / 8 + 2;

@@ -185,8 +185,11 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
     auto walk = [&](auto compact_c, auto &&fn) {
         constexpr bool COMPACT = decltype(compact_c)::value && !GREEDY;
         // COMPACT without an additive mask: the blocks are queued before the division by tau,
-        // which is done for the queued blocks only (the NaN and candidate tests give the same
-        // answers before it: tau > 0, and -inf and NaN stay so)
+        // which is done for the queued blocks only. The NaN test gives the same answer before it
+        // (tau > 0: NaN stays NaN); the candidate test does not for a finite logit below
+        // -FLT_MAX tau, which the division takes to -inf, so a row's candidate flag is then set
+        // from the divided values (a row whose allowed logits all lie there has no candidate and
+        // is refused, as the reference's max_dim of -inf is, rl.rs:515-519).
         constexpr bool DEFER = COMPACT && MK != NT_MASK_F32;
         const int n = blockDim.x;
         // COMPACT: the row's blocks i = 0 .. nbk - 1 (keystream block b0 + i, elements
@@ -206,11 +209,14 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
                     const int e = (head + lane) % kGumbelQueue;
                     const int ie = qb[e];
                     float ze[8];
+                    bool cand = false;
 #pragma unroll
                     for (int j = 0; j < 8; j++) {
                         ze[j] = qz[j * kGumbelQueue + e];
                         if (DEFER && !p.tau_one) ze[j] = ze[j] / p.tau;
+                        cand |= ze[j] > -INFINITY;
                     }
+                    if (DEFER && !p.tau_one && cand) flags |= 1;
                     fn(b0 + uint64_t(ie), 8 * int64_t(ie) - r, ze);
                 }
                 // (the reads are done before a later write reuses their slots)
@@ -230,7 +236,7 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
                 }
                 const uint64_t bal = __ballot(any);
                 if (any) {
-                    flags |= 1;
+                    if (!DEFER || p.tau_one) flags |= 1;  // (deferred: from the divided values, in pop)
                     const int pos = (head + count + int(__builtin_amdgcn_mbcnt_hi(
                                                            uint32_t(bal >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(bal), 0u)))) %
                                     kGumbelQueue;

@@ -491,7 +491,8 @@ __global__ __launch_bounds__(kResThreads) void k_readout_resolve(ResolveP p) {
     if (lane == 0) wmax[wave] = m;
     __syncthreads();  // (1) the maximum's parts, the block sums and references in LDS
     const float M = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-    if (M == -INFINITY) {
+    // (nothing allowed, or every allowed logit below -FLT_MAX T, whose tempered value is -inf)
+    if (M == -INFINITY || (!p.tau_one && M / p.tau == -INFINITY)) {
         refuse(NT_ROW_NO_TOKEN);
         return;
     }

@@ -81,7 +81,8 @@ __global__ __launch_bounds__(1024) void k_sample(SampleP p) {
             p.status[row] = st;
         }
     };
-    if (a == -INFINITY) {
+    // (nothing allowed, or every allowed logit below -FLT_MAX T, whose tempered value is -inf)
+    if (a == -INFINITY || (MK != NT_MASK_F32 && p.tau_one == 0 && a / p.tau == -INFINITY)) {
         refuse(NT_ROW_NO_TOKEN);
         return;
     }
@@ -510,7 +511,8 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
             p.status[row] = st;
         }
     };
-    if (M == -INFINITY) {
+    // (nothing allowed, or every allowed logit below -FLT_MAX T, whose tempered value is -inf)
+    if (M == -INFINITY || (MK != NT_MASK_F32 && !tau_one && M / p.tau == -INFINITY)) {
         refuse(NT_ROW_NO_TOKEN, tid == 0);
         return;
     }
@@ -1001,7 +1003,8 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rq(SampleP p) {
             p.status[row] = st;
         }
     };
-    if (M == -INFINITY) {
+    // (nothing allowed, or every allowed logit below -FLT_MAX T, whose tempered value is -inf)
+    if (M == -INFINITY || (MK != NT_MASK_F32 && !tau_one && M / p.tau == -INFINITY)) {
         refuse(NT_ROW_NO_TOKEN, tid == 0);
         return;
     }
@@ -1446,7 +1449,8 @@ __global__ __launch_bounds__(NW * kWave) void k_sample_seg(SegP q) {
             p.status[row] = st;
         }
     };
-    if (M == -INFINITY) {
+    // (nothing allowed, or every allowed logit below -FLT_MAX T, whose tempered value is -inf)
+    if (M == -INFINITY || (MK != NT_MASK_F32 && p.tau_one == 0 && M / p.tau == -INFINITY)) {
         refuse(NT_ROW_NO_TOKEN);
         return;
     }

@@ -310,15 +310,16 @@ __global__ __launch_bounds__(kScoreThreads) void k_score(ScoreP p) {
         }
         if (REF && ws[i].ar != -INFINITY) Sr += exp2(double(ws[i].ar - arf) * double(c)) * double(ws[i].Sr);
     }
-    int stt = NT_ROW_OK;
-    if (af == -INFINITY) stt = NT_ROW_NO_TOKEN;
-    else if (!(S == S)) stt = NT_ROW_NAN;
-    const double lnS = log(S);
     // The value-space max as the reference's f32 max of the tempered logits.
     auto zmax = [&](float a) -> float {
         if constexpr (MK != NT_MASK_F32) return tau_one ? a : a / p.tau;
         else return a;
     };
+    int stt = NT_ROW_OK;
+    // (nothing allowed, or every allowed logit below -FLT_MAX T, whose tempered value is -inf)
+    if (af == -INFINITY || zmax(af) == -INFINITY) stt = NT_ROW_NO_TOKEN;
+    else if (!(S == S)) stt = NT_ROW_NAN;
+    const double lnS = log(S);
     // The tempered logit of one token, with the reference's f32 arithmetic.
     auto ztok = [&](const void *rowp, int64_t tok) -> float {
         float x;

@@ -465,7 +465,9 @@ void or_cpuref_log_softmax(const float *x, int64_t rows, int64_t V, float *y) {
 
 /* tempered_logits (rl.rs:475-486) as CpuRef materialises it: div_scalar (skipped at tau 1,
  * float.rs:494-499), then the broadcast add of the additive mask, f32 throughout. A u8 keep
- * row stands for the additive row (0 kept, -inf excluded). */
+ * row is this library's mask kind, not the reference's: it selects, as mask_fill does
+ * (float.rs:984-1000), so an excluded token is -inf whatever its logit (a NaN or +inf there does
+ * not reach the row), the rule every device kernel applies to a u8 mask. */
 static float *cpuref_tempered_add(const float *x, int64_t rows, int64_t V, double tau,
                                   const float *addmask, int64_t add_ld, const uint8_t *keep, int64_t keep_ld) {
     size_t n = (size_t)rows * (size_t)V;
@@ -481,14 +483,10 @@ static float *cpuref_tempered_add(const float *x, int64_t rows, int64_t V, doubl
         z = z2;
     }
     if (keep) {
-        int64_t mrows = keep_ld == 0 ? 1 : rows;
-        float *add = (float *)malloc((size_t)mrows * (size_t)V * sizeof(float));
-        for (int64_t r = 0; r < mrows; r++)
-            for (int64_t v = 0; v < V; v++) add[r * V + v] = keep[r * keep_ld + v] ? 0.0f : -INFINITY;
         float *z2 = (float *)malloc(n * sizeof(float));
         for (int64_t r = 0; r < rows; r++)
-            for (int64_t v = 0; v < V; v++) z2[r * V + v] = z[r * V + v] + add[(keep_ld ? r : 0) * V + v];
-        free(add);
+            for (int64_t v = 0; v < V; v++)
+                z2[r * V + v] = keep[(keep_ld ? r * keep_ld : 0) + v] ? z[r * V + v] : -INFINITY;
         free(z);
         z = z2;
     }
@@ -575,7 +573,7 @@ int64_t or_cpuref_sample_logp(const float *x, int64_t rows, int64_t V, double ta
 #define OR_FAST_MIN_SUM ((size_t)1 << 22)
 
 typedef struct {
-    int op; /* 0: y = x / t, 1: y = a + b, 2: y = expf(x), 3: lane sums */
+    int op; /* 0: y = x / t, 1: y = a + b, 2: y = expf(x), 3: lane sums, 4: y = b != 0 ? a : -inf */
     const float *a, *b;
     float *y;
     float t;
@@ -602,6 +600,7 @@ static void *fast_run(void *arg) {
         case 0: for (size_t i = j->lo; i < j->hi; i++) j->y[i] = j->a[i] / j->t; break;
         case 1: for (size_t i = j->lo; i < j->hi; i++) j->y[i] = j->a[i] + j->b[i]; break;
         case 2: for (size_t i = j->lo; i < j->hi; i++) j->y[i] = expf(j->a[i]); break;
+        case 4: for (size_t i = j->lo; i < j->hi; i++) j->y[i] = j->b[i] != 0.0f ? j->a[i] : -INFINITY; break;
         default: for (size_t l = j->lo; l < j->hi; l++) j->y[l] = fast_simd_sum(j->a + (int64_t)l * j->n, j->n); break;
     }
     return NULL;
@@ -629,23 +628,25 @@ int64_t or_cpufast_sample_logp(const float *x, int64_t rows, int64_t V, double t
     size_t n = (size_t)rows * (size_t)V;
     const int parts = threads < 1 ? 1 : (threads > 256 ? 256 : threads);
     const double tt = tau == 0.0 ? 1.0 : tau;
-    /* tempered_logits: div_scalar (a map), then + the additive mask (a zip of equal shapes, or a
-     * broadcast zip for a shared mask row) */
+    /* tempered_logits: div_scalar (a map), then the u8 keep-mask as a select (a zip of equal
+     * shapes, or a broadcast zip for a shared mask row): an excluded token is -inf whatever its
+     * logit, the device kernels' rule */
     float *z = (float *)malloc(n * sizeof(float));
     if (tt == 1.0) memcpy(z, x, n * sizeof(float));
     else if (n >= OR_FAST_MIN_MAP && parts > 1) fast_par(0, x, NULL, z, (float)tt, n, 0, parts);
     else for (size_t i = 0; i < n; i++) z[i] = x[i] / (float)tt;
     if (keep) {
         int64_t mrows = keep_ld == 0 ? 1 : rows;
-        float *add = (float *)malloc((size_t)mrows * (size_t)V * sizeof(float));
+        float *kf = (float *)malloc((size_t)mrows * (size_t)V * sizeof(float));  /* the condition tensor */
         for (int64_t r = 0; r < mrows; r++)
-            for (int64_t v = 0; v < V; v++) add[r * V + v] = keep[r * keep_ld + v] ? 0.0f : -INFINITY;
+            for (int64_t v = 0; v < V; v++) kf[r * V + v] = keep[r * keep_ld + v] ? 1.0f : 0.0f;
         float *z2 = (float *)malloc(n * sizeof(float));
-        if (mrows == rows && n >= OR_FAST_MIN_ZIP && parts > 1) fast_par(1, z, add, z2, 0.0f, n, 0, parts);
+        if (mrows == rows && n >= OR_FAST_MIN_ZIP && parts > 1) fast_par(4, z, kf, z2, 0.0f, n, 0, parts);
         else
             for (int64_t r = 0; r < rows; r++)
-                for (int64_t v = 0; v < V; v++) z2[r * V + v] = z[r * V + v] + add[(keep_ld ? r : 0) * V + v];
-        free(add);
+                for (int64_t v = 0; v < V; v++)
+                    z2[r * V + v] = kf[(keep_ld ? r : 0) * V + v] != 0.0f ? z[r * V + v] : -INFINITY;
+        free(kf);
         free(z);
         z = z2;
     }

@@ -218,3 +218,133 @@ def test_large_logits_where_an_ulp_of_the_sum_passes_the_absolute_margin(pre_u32
         addmask[0, 0] = 0.0
     d, c = both(x, tau, 29, "large logits", keep=keep, addmask=addmask, pre_u32=pre_u32)
     assert np.array_equal(d, c), f"tokens differ from CpuRef: {np.nonzero(d != c)[0]}"
+
+
+def gumbel_call(xt, dtype, kind, rows, V, ld, mt, mask_ld, tau, rng):
+    """nt_hip_rl_sample_gumbel through the C ABI at `rng`'s position: (ids, status); the stream
+    is not moved."""
+    import ctypes as C
+    ids, st = nr.IntTensor((rows,)), nr.Tensor((rows,), "u8")
+    block, word = rng.word_pos()
+    a = nr.NtRlGumbelArgs(xt.ptr, dtype, kind, rows, V, ld, None if mt is None else mt.ptr, mask_ld, tau,
+                          rng.key(), block, word, 0, ids.ptr, st.ptr)
+    nr._check(nr.lib().nt_hip_rl_sample_gumbel(C.byref(a)), "sample_gumbel")
+    return ids.to_numpy().ravel().astype(np.int64), st.to_numpy().ravel()
+
+
+@pytest.mark.parametrize("pre_u32", [0, 1])
+@pytest.mark.parametrize("V", [4096, 4099])
+def test_u8_excluded_non_finite_logits_do_not_reach_the_row(V, pre_u32):
+    """A u8 keep-mask selects: NaN and +inf at excluded tokens (inside blocks that keep a token
+    and in blocks that keep none) leave the row to sample as Cpu(Reference)'s sequence does with
+    the same rule; +inf at a kept token wins (the first one); NaN at a kept token refuses the row.
+    V = 4096 at an even stream position takes the aligned path, the rest the element-wise one."""
+    rng = np.random.default_rng(V + pre_u32)
+    rows = 8
+    x = rng.normal(0, 2, (rows, V)).astype(np.float32)
+    keep = (rng.random((rows, V)) < 0.6).astype(np.uint8)
+    keep[:, 100] = 1
+    x[0, 5], keep[0, 5] = np.nan, 0
+    x[1, 9], keep[1, 9] = np.inf, 0
+    keep[2, 16:24] = 0
+    x[2, 16:24] = np.nan  # a whole block excluded
+    keep[3, 40:48] = [1, 0, 1, 0, 1, 1, 0, 1]
+    x[3, 41], x[3, 43], x[3, 46] = np.nan, np.inf, -np.inf
+    x[4, 200], keep[4, 200] = np.inf, 1
+    x[4, 300], keep[4, 300] = np.inf, 1
+    x[5, V - 1], keep[5, V - 1] = np.nan, 0
+    for tau in (1.0, 0.7, 0.0):
+        dev, cpu = both(x, tau, 31, "u8 non-finite", keep=keep, pre_u32=pre_u32)
+        assert np.array_equal(dev, cpu), f"tau={tau}: rows {np.nonzero(dev != cpu)[0]}"
+        assert keep[np.arange(rows), dev].all()
+        assert dev[4] == 200
+    # NaN at a kept token: that row alone is refused (status through the C ABI), nothing drawn
+    x2 = x.copy()
+    x2[6, 100] = np.nan
+    rd = nr.Rng(31, "u8 non-finite")
+    for _ in range(pre_u32):
+        rd.next_u32()
+    ids, st = gumbel_call(nr.Tensor.from_numpy(x2), nr.NT_F32, nr.NT_MASK_U8, rows, V, V,
+                          nr.Tensor.from_numpy(keep, "u8"), V, 0.7, rd)
+    assert st[6] == nr.NT_ROW_NAN and ids[6] == -1
+    assert np.all(st[np.arange(rows) != 6] == nr.NT_ROW_OK)
+
+
+@pytest.mark.parametrize("pre_u32", [0, 1])
+@pytest.mark.parametrize("V", [4096, 4099])
+@pytest.mark.parametrize("mask", ["none", "keep"])
+def test_rows_below_minus_flt_max_tau_have_no_token(mask, V, pre_u32):
+    """Every allowed logit at -3.3e38 with T = 0.7: the tempered values x / T are all -inf, so the
+    reference's max_dim is -inf and the row is refused before any draw (rl.rs:515-519), even where
+    the keep-mask excludes token 0. A row with only some of its allowed logits there samples
+    among the others as Cpu(Reference) does."""
+    rows = 4
+    rng = np.random.default_rng(V)
+    x = rng.normal(0, 1, (rows, V)).astype(np.float32)
+    keep = np.ones((rows, V), np.uint8) if mask == "keep" else None
+    x[1] = -3.3e38
+    if keep is not None:
+        keep[1, 0] = 0
+    mt = None if keep is None else nr.Tensor.from_numpy(keep, "u8")
+    kind = nr.NT_MASK_NONE if keep is None else nr.NT_MASK_U8
+    rd = nr.Rng(41, "below -FLT_MAX T")
+    for _ in range(pre_u32):
+        rd.next_u32()
+    ids, st = gumbel_call(nr.Tensor.from_numpy(x), nr.NT_F32, kind, rows, V, V, mt, 0 if mt is None else V, 0.7, rd)
+    assert st[1] == nr.NT_ROW_NO_TOKEN and ids[1] == -1, (st, ids)
+    assert np.all(st[[0, 2, 3]] == nr.NT_ROW_OK)
+    copy = rd.clone()
+    with pytest.raises(ValueError, match="position 1 has no allowed token"):
+        nr.sample_categorical(nr.Tensor.from_numpy(x), 0.7, mt, rd)
+    assert rd.next_u64() == copy.next_u64(), "a refused call moved the stream"
+    # half of row 1's logits back to normal values: it samples among them
+    x[1, ::2] = rng.normal(0, 1, (V + 1) // 2).astype(np.float32)
+    dev, cpu = both(x, 0.7, 41, "below -FLT_MAX T", keep=keep, pre_u32=pre_u32)
+    assert np.array_equal(dev, cpu) and dev[1] % 2 == 0
+
+
+@pytest.mark.parametrize("pre_u32", [0, 1])
+@pytest.mark.parametrize("V", [1001, 4096, 4099])
+@pytest.mark.parametrize("mask", ["u8", "f32add"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_strided_rows_through_the_c_abi(dtype, mask, V, pre_u32):
+    """Rows and mask rows with a padded stride (ld and mask_ld V rounded up to 8, and 16 more)
+    whose padding holds NaN logits and keep bytes of 1 / NaN mask values: nothing past V is
+    read. Every token equal to Cpu(Reference)'s on the unpadded rows, at an even and an odd
+    stream position."""
+    rows = 9
+    rng = np.random.default_rng(V * 4 + pre_u32)
+    x = rng.normal(0, 2, (rows, V)).astype(np.float32)
+    ld = -(-V // 8) * 8 + 16
+    if dtype == "bf16":
+        xb = O.bf16_from_f32(x)
+        x = O.bf16_to_f32(xb)
+        pad = np.full((rows, ld), 0x7fc0, np.uint16)
+        pad[:, :V] = xb
+        xt, dt = nr.Tensor.from_numpy(pad, "bf16"), nr.NT_BF16
+    else:
+        pad = np.full((rows, ld), np.nan, np.float32)
+        pad[:, :V] = x
+        xt, dt = nr.Tensor.from_numpy(pad), nr.NT_F32
+    keep = addmask = None
+    if mask == "u8":
+        keep = (rng.random((rows, V)) < 0.5).astype(np.uint8)
+        keep[:, V // 2] = 1
+        mpad = np.ones((rows, ld), np.uint8)
+        mpad[:, :V] = keep
+        mt, kind = nr.Tensor.from_numpy(mpad, "u8"), nr.NT_MASK_U8
+    else:
+        addmask = np.where(rng.random((rows, V)) < 0.5, -np.inf, 0.0).astype(np.float32)
+        addmask[:, V // 2] = 0.0
+        mpad = np.full((rows, ld), np.nan, np.float32)
+        mpad[:, :V] = addmask
+        mt, kind = nr.Tensor.from_numpy(mpad), nr.NT_MASK_F32
+    for tau in (1.0, 0.7):
+        rd, rc = nr.Rng(53, "strided"), O.Rng(53, "strided")
+        for _ in range(pre_u32):
+            rd.next_u32()
+            rc.next_u32()
+        ids, st = gumbel_call(xt, dt, kind, rows, V, ld, mt, ld, tau, rd)
+        assert np.all(st == nr.NT_ROW_OK), st
+        cpu = O.cpuref_sample_gumbel(x, tau, rc, addmask=addmask, keep=keep)
+        assert np.array_equal(ids, cpu), f"tau={tau}: rows {np.nonzero(ids != cpu)[0]}"

@@ -382,6 +382,32 @@ def test_cpuref_gumbel_with_additive_masks_is_the_references_sampler_test():
     assert abs(np.mean(tok == 0) - p0) <= 4.5 * math.sqrt(p0 * (1 - p0) / n2)
 
 
+def test_u8_keep_mask_selects_in_every_checker():
+    """A u8 keep-mask selects: an excluded token is -inf whatever its logit, so a NaN or +inf there
+    does not reach the row (the device kernels' rule). The reference's additive -inf mask lets
+    them through (NaN + -inf and +inf + -inf are NaN) and the row is refused. The three CPU
+    checkers that take a keep-mask (the f64 row oracle's tempered, the Cpu(Reference) Gumbel
+    sequence, the Cpu(Fast) inverse-CDF sequence) apply the same rule."""
+    f32 = lambda a: np.asarray(a, np.float32)
+    x = f32([[0.3, np.nan, 1.2, np.inf, -0.5, 0.8], [1.0, 2.0, np.nan, 0.0, np.inf, -1.0]])
+    keep = np.array([[1, 0, 1, 0, 1, 1], [1, 1, 0, 1, 0, 1]], np.uint8)
+    add = np.where(keep == 1, 0.0, -np.inf).astype(np.float32)
+    z = O.tempered(x, 0.7, keep=keep)
+    assert np.all(np.isneginf(z[keep == 0])) and np.all(np.isfinite(z[keep == 1]))
+    for tau in (1.0, 0.7, 0.0):
+        ids = O.cpuref_sample_gumbel(x, tau, O.Rng(3, "keep rule"), keep=keep)
+        assert keep[np.arange(2), ids].all()
+        # the same tokens as the finite rows with the excluded logits replaced
+        xf = np.where(keep == 1, x, 0.0).astype(np.float32)
+        assert np.array_equal(ids, O.cpuref_sample_gumbel(xf, tau, O.Rng(3, "keep rule"), keep=keep))
+        with pytest.raises(ValueError, match="position 0 has no allowed token"):
+            O.cpuref_sample_gumbel(x, tau, O.Rng(3, "keep rule"), addmask=add)
+    ids, lp = O.cpufast_sample_logp(x, 0.7, keep, O.Rng(4, "keep rule"), 2)
+    assert keep[np.arange(2), ids].all() and np.all(np.isfinite(lp))
+    ids2, lp2 = O.cpufast_sample_logp(np.where(keep == 1, x, 0.0).astype(np.float32), 0.7, keep, O.Rng(4, "keep rule"), 2)
+    assert np.array_equal(ids, ids2) and np.array_equal(lp, lp2)
+
+
 def test_cpufast_restatement_against_cpuref_and_the_f64_oracle():
     # Cpu(Fast) (src/tensor/backend.rs:57-239) differs from Cpu(Reference) only in how maps, zips
     # and sums are split: above its thresholds (here 64 x 65536 = 2^22 elements) the tokens, whose

@@ -463,3 +463,40 @@ def test_peaked_rows_sampling_keeps_the_tolerance(dtype, V):
     ids, lp, ent = nr.sample_logp(xt, 1.0, None, None, entropy=True, uniforms=nr.Tensor.from_numpy(u, "f64"))
     check_sample(f"peaked {dtype} V{V}", x, u, ids.to_numpy().ravel(), lp.to_numpy().ravel(), ent.to_numpy().ravel())
     assert np.mean(ids.to_numpy().ravel() == peak) > 0.9
+
+
+@pytest.mark.parametrize("V,seg", [(4096, "off"), (50304, "off"), (128256, "off"), (4099, "off"), (128256, "8,4")])
+@pytest.mark.parametrize("mask", ["none", "u8"])
+def test_rows_below_minus_flt_max_tau_have_no_token(V, seg, mask, monkeypatch):
+    """Every allowed logit at -3.3e38 with T = 0.7: the tempered values x / T are all -inf, so the
+    row has no allowed token (the reference's max_dim is -inf, rl.rs:515-519) and every kernel
+    refuses it with NT_ROW_NO_TOKEN: the samplers (register-resident, queued, streaming at an
+    unaligned V, segmented) and the scorer. The other rows are unaffected."""
+    import ctypes as C
+    monkeypatch.setenv("NOETIC_HIP_SAMPLE_SEG", seg)
+    rows = 4
+    rng = np.random.default_rng(V)
+    x = rng.normal(0, 1, (rows, V)).astype(np.float32)
+    x[2] = -3.3e38
+    keep = None
+    if mask == "u8":
+        keep = np.ones((rows, V), np.uint8)
+        keep[:, ::3] = 0
+        mt, kind = nr.Tensor.from_numpy(keep), nr.NT_MASK_U8
+    else:
+        mt, kind = None, nr.NT_MASK_NONE
+    xt = nr.Tensor.from_numpy(x)
+    u = nr.Tensor.from_numpy(np.full(rows, 0.5), "f64")
+    ids, lp, st = nr.IntTensor((rows,)), nr.Tensor((rows,), "f32"), nr.Tensor((rows,), "u8")
+    a = nr.NtRlSampleArgs(xt.ptr, nr.NT_F32, kind, rows, V, V, None if mt is None else mt.ptr, 0 if mt is None else V,
+                          0.7, u.ptr, ids.ptr, lp.ptr, None, st.ptr)
+    nr._check(nr.lib().nt_hip_rl_sample(C.byref(a)), "sample")
+    s = st.to_numpy()
+    assert s[2] == nr.NT_ROW_NO_TOKEN and ids.to_numpy()[2] == -1, s
+    assert np.all(s[[0, 1, 3]] == nr.NT_ROW_OK), s
+    tok = nr.Tensor.from_numpy(np.zeros(rows, np.int32))
+    slp, sst = nr.Tensor((rows,), "f32"), nr.Tensor((rows,), "u8")
+    b = nr.NtRlScoreArgs(xt.ptr, None, nr.NT_F32, kind, rows, V, V, None if mt is None else mt.ptr,
+                         0 if mt is None else V, 0.7, tok.ptr, slp.ptr, None, None, None, sst.ptr, None, None, None, None)
+    nr._check(nr.lib().nt_hip_rl_score(C.byref(b)), "score")
+    assert sst.to_numpy()[2] == nr.NT_ROW_NO_TOKEN, sst.to_numpy()

@@ -47,7 +47,8 @@ def test_small_batch_decode_rows_take_segments(rows):
         assert all(a.to_numpy().tobytes() == b.to_numpy().tobytes() for a, b in zip(again, out[0])), "rerun bits"
     x = W.bf16_to_f32(w["logits"].to_numpy().reshape(rows, V))
     keep = w["mask"].to_numpy().reshape(rows, V)
-    check(f"c4 row shape, {rows} rows", O.tempered(x, 0.7, keep=keep), u, ids, lp, ent, bf16=True)
+    # the f32 tolerance: the bf16 inputs are exact in f32, and the kernel computes in f32 and f64
+    check(f"c4 row shape, {rows} rows", O.tempered(x, 0.7, keep=keep), u, ids, lp, ent, bf16=False)
 
 
 @pytest.mark.parametrize("rows", [8, 256, 1024])
