@@ -156,6 +156,29 @@ def practical_floor(nr, bytes_launch, traffic, ms, blocks):
     return out
 
 
+def valu_roofline(nr, ms, counters_file):
+    """A VALU-bound kernel's roofline: its VALU instructions per launch (SQ_INSTS_VALU, read from
+    the committed rocprofv3 summary `counters_file`) over the launch time, against the issue
+    capacity of the chip's SIMDs: 256 CUs x 4 SIMDs, one 64-lane instruction every 4 cycles each
+    (16 lanes wide), at the shader clock measured in this run under a load of dependent fused
+    multiply-adds on every SIMD (include/noetic_measure.h). `achieved` and `peak` are in G
+    wave-instructions/s."""
+    mhz = C.c_double()
+    nr._check(nr.lib().nt_measure_shader_clock(1000, C.byref(mhz)), "measure shader clock")
+    peak = 256 * 4 * mhz.value * 1e6 / 4 / 1e9
+    path = os.path.join(ROOT, "profiles", counters_file)
+    n = achieved = None
+    if os.path.exists(path):  # (absent while the counters themselves are being collected)
+        with open(path) as f:
+            n = json.load(f)["sq_insts_valu_per_dispatch"]
+        achieved = n / (ms * 1e-3) / 1e9
+    return {"bound": "valu", "achieved": achieved, "peak": peak, "unit": "G wave-instructions/s",
+            "frac": None if n is None else achieved / peak, "traffic": None, "valu_instructions_per_launch": n,
+            "shader_clock_mhz": mhz.value,
+            "what": "VALU wave-instructions per launch (SQ_INSTS_VALU) / launch time, against 256 CUs x 4 SIMDs "
+                    "x one wave-instruction per 4 cycles at the measured shader clock"}
+
+
 def roofline(bytes_launch, ms, traffic_file=None):
     gbs = bytes_launch / (ms * 1e-3) / 1e9
     r = {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
@@ -435,14 +458,17 @@ def bench_gumbel(nr, W, args):
     x = W.bf16_to_f32(w["logits"].to_numpy().reshape(rows, V)[:n_par])
     keep = w["mask"].to_numpy().reshape(rows, V)[:n_par]
     cpu = O.cpuref_sample_gumbel(x, w["temperature"], O.Rng(args.seed, "c4g/stream"), keep=keep)
-    roof = roofline(bytes_launch, ms)
-    roof["inputs"] = (f"HBM-cold: launches cycle over {copies} input copies "
-                      f"({copies * bytes_launch / 2**20:.0f} MiB), beyond the 256 MB Infinity Cache")
+    hbm = roofline(bytes_launch, ms)
+    roof = valu_roofline(nr, ms, "k_sample_gumbel_c4_valu.json")
+    roof["hbm"] = {"achieved": hbm["achieved"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": hbm["frac"],
+                   "algorithmic_bytes_per_launch": bytes_launch,
+                   "inputs": (f"HBM-cold: launches cycle over {copies} input copies "
+                              f"({copies * bytes_launch / 2**20:.0f} MiB), beyond the 256 MB Infinity Cache")}
     roof["note"] = ("bound by generating the draws (a ChaCha20 block per 8 logits holding an allowed one, and "
                     "two f32 hardware logarithms per allowed logit; f64 only where a row has several "
                     "candidates): the VALU instruction count, not HBM")
-    roof["warm_cache"] = {"ms": ms_warm, "achieved": bytes_launch / (ms_warm * 1e-3) / 1e9,
-                          "frac": bytes_launch / (ms_warm * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    roof["warm_cache"] = {"ms": ms_warm, "achieved_hbm": bytes_launch / (ms_warm * 1e-3) / 1e9,
+                          "frac_hbm": bytes_launch / (ms_warm * 1e-3) / 1e9 / HBM_PEAK_GBS}
     config = {"workload": "c4 rows through the reference's Gumbel-max sample_categorical: bf16 logits "
                           "[1,256,1,128256] ~ N(0,2^2), u8 grammar mask of contiguous runs (~30% kept), temperature "
                           "0.7, one u64 of the caller's ChaCha20 stream per logit; launches cycle over independent "

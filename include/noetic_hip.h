@@ -95,8 +95,9 @@ int nt_hip_stream(void **out);
 /* Launch counter (the reference's `launches()`, src/tensor/cuda/backend.rs:1034-1036). */
 uint64_t nt_hip_launches(void);
 
-/* Where the nn::rl row kernels (nt_hip_rl_sample, nt_hip_rl_sample_noalloc, nt_hip_rl_sample_gumbel,
- * nt_hip_rl_score, nt_hip_rl_score_backward) launch from. The CUDA
+/* Where the nn::rl row kernels (nt_hip_rl_sample, nt_hip_rl_sample_gumbel, nt_hip_rl_score,
+ * nt_hip_rl_score_backward) launch from; nt_hip_rl_sample_noalloc always launches the ahead-of-time
+ * code objects, since a run-time instance's first launch allocates. The CUDA
  * backend compiles its kernels with NVRTC at first use and caches the functions
  * (src/tensor/cuda/mod.rs:169-218, cuda/backend.rs:281-293, 322-358); here both ways exist for
  * one device source: NT_KERNELS_AOT, the code objects hipcc built into this library (the
@@ -180,7 +181,9 @@ int nt_hip_rl_sample(const NtRlSampleArgs *a);
  * sampler's workspace (its per-row arrival counters and wave records) is a fixed device array
  * of 2 MiB per GPU instead of the library's allocation, and a launch that needs more is refused
  * (NT_E_ARG) before anything runs. The call makes no hipMalloc, hipFree or other allocating call
- * (pointers released with nt_hip_free are freed by the next other entry point). Calls share that
+ * (pointers released with nt_hip_free are freed by the next other entry point), and it launches
+ * the library's ahead-of-time code objects whatever nt_hip_set_kernel_path chose: compiling and
+ * loading a hiprtc instance allocates device memory. Calls share that
  * GPU's array and leave the last call's records in it; they are ordered on the library's stream,
  * and calls that overlap on one GPU race. */
 int nt_hip_rl_sample_noalloc(const NtRlSampleArgs *a);

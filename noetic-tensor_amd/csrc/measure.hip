@@ -2,7 +2,10 @@
 // streaming-read rate and the period of dependent launches of an empty kernel.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <chrono>
 #include <string>
+#include <vector>
 
 #include "../../include/noetic_measure.h"
 #include "nt_internal.hpp"
@@ -31,6 +34,23 @@ __global__ __launch_bounds__(kReadThreads) void k_stream_read(const v4u32 *p, si
         for (int u = 0; u < kReadInFlight; u++) acc ^= v[u].x ^ v[u].w;
     }
     if (threadIdx.x == 0) sink[blockIdx.x] = acc;
+}
+
+// Shader clock against the 100 MHz real-time counter over a dependent chain of fused
+// multiply-adds on every lane (each block's first wave records both deltas).
+__global__ __launch_bounds__(256) void k_clock(uint64_t *out, int iters) {
+    const uint64_t c0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+    float a = float(threadIdx.x), b = 0.5f;
+    for (int i = 0; i < iters; i++) {
+        a = fmaf(a, 0.99993f, b);
+        b = fmaf(b, 0.99991f, 0.25f);
+    }
+    const uint64_t c1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    if (threadIdx.x == 0) {
+        out[2 * blockIdx.x] = c1 - c0;
+        out[2 * blockIdx.x + 1] = r1 - r0;
+    }
+    if (a == 1234.5f && b == 6.5f) out[0] = 0;  // keeps the chain
 }
 
 __global__ void k_nothing(uint32_t *never) {
@@ -92,6 +112,36 @@ int nt_measure_read(size_t bytes, int32_t reps, double *gbs) {
     (void)hipFree(sink);
     (void)hipFree(buf);
     return rc;
+}
+
+int nt_measure_shader_clock(int32_t seconds_ms, double *mhz) {
+    if (!mhz || seconds_ms < 1 || seconds_ms > 10000)
+        return fail(NT_E_ARG, "nt_measure_shader_clock: 1 to 10000 ms of load");
+    std::unique_lock<std::mutex> lk;
+    if (int rc = enter(&lk)) return rc;
+    constexpr int kBlocks = 256 * 8;   // eight 256-thread blocks per compute unit: every SIMD busy
+    constexpr int kIters = 1 << 16;    // about 0.25 ms per launch
+    void *out = nullptr;
+    if (int rc = hip_check(hipMalloc(&out, 2 * kBlocks * sizeof(uint64_t)), "hipMalloc")) return rc;
+    std::vector<uint64_t> h(2 * kBlocks);
+    int rc = 0;
+    const auto t0 = std::chrono::steady_clock::now();
+    while (!rc) {  // the load, for the clock to settle; the last launch is the one read
+        hipLaunchKernelGGL(k_clock, dim3(kBlocks), dim3(256), 0, ctx().stream, static_cast<uint64_t *>(out), kIters);
+        rc = launched("nt_measure_shader_clock");
+        if (!rc) rc = hip_check(hipStreamSynchronize(ctx().stream), "hipStreamSynchronize");
+        if (std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(seconds_ms)) break;
+    }
+    if (!rc) rc = hip_check(hipMemcpy(h.data(), out, h.size() * sizeof(uint64_t), hipMemcpyDeviceToHost), "hipMemcpy");
+    (void)hipFree(out);
+    if (rc) return rc;
+    std::vector<double> r;
+    for (int b = 0; b < kBlocks; b++)
+        if (h[2 * b + 1] > 0) r.push_back(double(h[2 * b]) / double(h[2 * b + 1]) * 100.0);
+    if (r.empty()) return fail(NT_E_ARG, "nt_measure_shader_clock: no sample");
+    std::nth_element(r.begin(), r.begin() + r.size() / 2, r.end());
+    *mhz = r[r.size() / 2];
+    return 0;
 }
 
 int nt_measure_launch_period(int32_t blocks, int32_t threads, int32_t launches, double *us) {

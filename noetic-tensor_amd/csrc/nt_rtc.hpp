@@ -32,6 +32,16 @@ int &rtc_status();
 // The key's middle for the run-time path: "hiprtc<version>-kernels-<sha16 of the embedded source>".
 std::string rtc_key_part();
 
+// Set while an entry point must launch the ahead-of-time code objects whatever kernel_path()
+// says: the allocation-free entry (compiling and loading a run-time code object allocates device
+// memory). Entry points are serialised by the context lock; the flag is per thread all the same.
+bool &aot_pinned();
+struct AotPin {
+    bool prev;
+    AotPin() : prev(aot_pinned()) { aot_pinned() = true; }
+    ~AotPin() { aot_pinned() = prev; }
+};
+
 // "true" / "false" for a name expression.
 inline const char *rtc_bool(bool b) { return b ? "true" : "false"; }
 

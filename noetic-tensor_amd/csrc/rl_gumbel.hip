@@ -41,7 +41,8 @@ template <int DT, int MK, bool ODD, bool GREEDY>
 void launch_gumbel(const GumbelP &p, int64_t rows, int threads, hipStream_t s) {
     char nm[96];
     std::snprintf(nm, sizeof nm, "nt::k_sample_gumbel<%d, %d, %s, %s>", DT, MK, rtc_bool(ODD), rtc_bool(GREEDY));
-    launch_path(k_sample_gumbel<DT, MK, ODD, GREEDY>, nm, dim3(unsigned(rows)), dim3(threads), 0, s, p);
+    launch_path(k_sample_gumbel<DT, MK, ODD, GREEDY>, nm, dim3(unsigned(rows)), dim3(threads),
+                gumbel_queue_bytes(threads, GREEDY), s, p);
 }
 
 template <int DT, int MK>

@@ -139,6 +139,11 @@ __device__ __forceinline__ float gumbel_screen(uint32_t lo, uint32_t hi) {
 
 constexpr int kGumbelCand = 4;         // screened candidates a thread keeps
 constexpr int kGumbelQueue = 128;      // a wave's queue of blocks with an allowed element (LDS)
+// The queue's dynamic LDS for a launch of `threads` threads: per wave kGumbelQueue block indices
+// and their 8 values each (36 KiB at 16 waves, 2.25 KiB for a one-wave row).
+constexpr size_t gumbel_queue_bytes(int threads, bool greedy) {
+    return greedy ? 0 : size_t(threads / 64) * kGumbelQueue * 9 * sizeof(float);
+}
 constexpr float kGumbelScreen = 1e-3f;  // the screen's margin, at least: 250 times its error bound
 
 // The lowest screened value kept as a candidate beside a largest screened value x: x less the
@@ -165,9 +170,11 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
     __shared__ int sidx[kGumbelMaxThreads / 64];
     __shared__ int sflags[kGumbelMaxThreads / 64];
     __shared__ int scount[kGumbelMaxThreads / 64];
-    // per wave, the queue of blocks to draw: their index and their 8 values ([8][kGumbelQueue])
-    __shared__ int gqb[GREEDY ? 1 : kGumbelMaxThreads / 64 * kGumbelQueue];
-    __shared__ float gqz[GREEDY ? 1 : kGumbelMaxThreads / 64 * 8 * kGumbelQueue];
+    // per wave, the queue of blocks to draw: their index and their 8 values ([8][kGumbelQueue]),
+    // in dynamic LDS sized by the launch for its waves (gumbel_queue_bytes; none when greedy)
+    extern __shared__ __attribute__((aligned(16))) int gdyn[];
+    int *const gqb = gdyn;
+    float *const gqz = reinterpret_cast<float *>(gdyn + (blockDim.x / 64) * kGumbelQueue);
     const int64_t row = blockIdx.x;
     const int64_t V = p.V;
     // Pair q = h + row V + v holds element v's u64; block q >> 3, pair q & 7 of it.

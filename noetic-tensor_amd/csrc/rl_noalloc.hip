@@ -2,7 +2,10 @@
 // (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It has
 // the same arguments, kernels and results; the one difference is where the segmented sampler's
 // workspace lives: a fixed device array, `scratch`, instead of the library's allocation. The
-// call makes no hipMalloc, hipFree or other allocating call.
+// call makes no hipMalloc, hipFree or other allocating call, and it always launches the
+// library's ahead-of-time code objects: on the run-time kernel path (hiprtc) a kernel instance's
+// first launch compiles it and loads its code object, which allocates device memory, so this
+// entry does not take that path (both paths compute the same bytes).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -10,6 +13,7 @@
 
 #include "../../include/noetic_hip.h"
 #include "nt_internal.hpp"
+#include "nt_rtc.hpp"
 
 namespace nt {
 namespace {
@@ -50,5 +54,6 @@ int scratch_workspace(size_t need, uint8_t **out) {
 }  // namespace nt
 
 extern "C" int nt_hip_rl_sample_noalloc(const NtRlSampleArgs *a) {
+    const nt::AotPin pin;  // the ahead-of-time code objects whatever the library's kernel path
     return nt::sample_entry(a, nt::scratch_workspace, true, "nt_hip_rl_sample_noalloc");
 }

@@ -168,6 +168,11 @@ int function_for(const std::string &name, hipFunction_t *out) {
 
 }  // namespace
 
+bool &aot_pinned() {
+    thread_local bool pinned = false;
+    return pinned;
+}
+
 int kernel_path() {
     std::lock_guard<std::mutex> lk(g_path_mu);
     if (g_path < 0) {

@@ -199,6 +199,7 @@ _SIGS = {
                                           C.c_int32, C.c_int32]),
     "nt_measure_read": (C.c_int, [C.c_size_t, C.c_int32, C.POINTER(C.c_double)]),
     "nt_measure_launch_period": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, C.POINTER(C.c_double)]),
+    "nt_measure_shader_clock": (C.c_int, [C.c_int32, C.POINTER(C.c_double)]),
 }
 
 _lib = None

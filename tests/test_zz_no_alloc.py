@@ -1,8 +1,10 @@
 """The allocation-free sampler entry point, nt_hip_rl_sample_noalloc, through the C ABI against
 nt_hip_rl_sample on the same inputs: the same kernels, so every output byte is equal. Two calls
 in a row, the second with a smaller input, at shapes that take the segmented sampler (whose
-workspace is the fixed device array); and a launch needing more than that array is refused
-before anything runs."""
+workspace is the fixed device array); the same with the library on its run-time (hiprtc) kernel
+path, where the entry still launches the ahead-of-time code objects and the device's free memory
+does not change over warm calls; and a launch needing more than that array is refused before
+anything runs."""
 import ctypes as C
 
 import numpy as np
@@ -66,3 +68,37 @@ def test_noalloc_refuses_a_launch_beyond_its_workspace(monkeypatch):
     assert nr.lib().nt_hip_rl_sample_noalloc(C.byref(a)) == -1  # NT_E_ARG
     assert "allocation-free maximum" in nr.lib().nt_hip_last_error().decode()
     assert nr.launches() == before
+
+
+def test_noalloc_on_the_run_time_kernel_path_allocates_nothing():
+    # with the library on the hiprtc path, the allocation-free entry still launches the
+    # ahead-of-time code objects (a hiprtc instance's first launch compiles and loads a code
+    # object, which allocates): its outputs equal the allocating entry's on that path, and after a
+    # first call the device's free memory is the same across further calls
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipMemGetInfo.argtypes = [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+
+    def free_bytes():
+        nr.sync()
+        f, t = C.c_size_t(), C.c_size_t()
+        assert hip.hipMemGetInfo(C.byref(f), C.byref(t)) == 0
+        return f.value
+
+    prev = nr.lib().nt_hip_set_kernel_path(1)  # NT_KERNELS_RTC
+    try:
+        w = W.c4(seed=3, rows=48)
+        U = nr.Tensor.from_numpy(nr.Rng(3, "noalloc/rtc").uniforms(48), "f64")
+        x2 = W.normal((8, 50304), "f32", 6, "noalloc/rtc/f32")
+        U2 = nr.Tensor.from_numpy(nr.Rng(4, "noalloc/rtc").uniforms(8), "f64")
+        calls = [(w["logits"], nr.NT_BF16, nr.NT_MASK_U8, w["mask"], 48, w["V"], 0.7, U, False),
+                 (x2, nr.NT_F32, nr.NT_MASK_NONE, None, 8, 50304, 0.8, U2, True)]
+        outs = [run("nt_hip_rl_sample_noalloc", *c) for c in calls]  # first calls
+        before = free_bytes()
+        for _ in range(3):
+            for c, o in zip(calls, outs):
+                assert run("nt_hip_rl_sample_noalloc", *c) == o
+        assert free_bytes() == before, "device memory allocated by warm allocation-free calls"
+        for c, o in zip(calls, outs):
+            assert run("nt_hip_rl_sample", *c) == o  # the allocating entry on the hiprtc path: the same bytes
+    finally:
+        nr.lib().nt_hip_set_kernel_path(prev)
