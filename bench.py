@@ -786,7 +786,7 @@ def bench_readout(nr, W, args):
     w_packed = torch.empty(nbytes, device="cuda:0", dtype=torch.uint8)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    nr._check(L.nt_hip_rl_readout_pack_weight(C.c_void_p(w_dv.data_ptr()), nr.NT_READOUT_W_DV, V, d, V,
+    nr._check(L.nt_hip_rl_readout_pack_weight(C.c_void_p(w_dv.data_ptr()), nr.NT_BF16, nr.NT_READOUT_W_DV, V, d, V,
                                               C.c_void_p(w_packed.data_ptr())), "pack")
     nr.sync()
     pack_s = time.perf_counter() - t0
@@ -795,16 +795,16 @@ def bench_readout(nr, W, args):
     a = nr.NtRlSampleArgs(logits.data_ptr(), nr.NT_BF16, nr.NT_MASK_U8, rows, V, V, w["mask"].ptr, V, 0.7, U.ptr,
                           ids.ptr, logp.ptr, None, st.ptr)
     ids2, logp2, st2 = nr.IntTensor((rows,)), nr.Tensor((rows,), "f32"), nr.Tensor((rows,), "u8")
-    fa = nr.NtRlReadoutSampleArgs(h.data_ptr(), w_packed.data_ptr(), rows, V, d, d, nr.NT_MASK_U8, 0, w["mask"].ptr, V,
-                                  0.7, U.ptr, ids2.ptr, logp2.ptr, st2.ptr, None, None, None)
+    fa = nr.NtRlReadoutSampleArgs(h.data_ptr(), w_packed.data_ptr(), rows, V, d, d, nr.NT_MASK_U8, nr.NT_BF16,
+                                  w["mask"].ptr, V, 0.7, U.ptr, ids2.ptr, logp2.ptr, st2.ptr, None, None, None)
 
     def fused(i):
         nr._check(L.nt_hip_rl_readout_sample(C.byref(fa)), "readout sample")
 
     # scoring the drawn tokens (ids2, the fused step's draws): fused, and on the written logits
     slp, sent, sst = nr.Tensor((rows,), "f32"), nr.Tensor((rows,), "f32"), nr.Tensor((rows,), "u8")
-    sa = nr.NtRlReadoutScoreArgs(h.data_ptr(), w_packed.data_ptr(), rows, V, d, d, nr.NT_MASK_U8, 0, w["mask"].ptr,
-                                 V, 0.7, ids2.ptr, slp.ptr, sent.ptr, sst.ptr, None)
+    sa = nr.NtRlReadoutScoreArgs(h.data_ptr(), w_packed.data_ptr(), rows, V, d, d, nr.NT_MASK_U8, nr.NT_BF16,
+                                 w["mask"].ptr, V, 0.7, ids2.ptr, slp.ptr, sent.ptr, sst.ptr, None)
     ulp, uent, ust = nr.Tensor((rows,), "f32"), nr.Tensor((rows,), "f32"), nr.Tensor((rows,), "u8")
     ua = nr.NtRlScoreArgs(logits.data_ptr(), None, nr.NT_BF16, nr.NT_MASK_U8, rows, V, V, w["mask"].ptr, V, 0.7,
                           ids2.ptr, ulp.ptr, None, None, uent.ptr, ust.ptr, None, None, None, None)

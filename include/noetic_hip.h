@@ -197,8 +197,8 @@ int nt_hip_rl_sample_noalloc(const NtRlSampleArgs *a);
  * (tempered by the temperature, the u8 keep-mask applied; one uniform per row; temperature 0 is
  * the first argmax). The weight is packed once, when loaded, into the order the matrix cores
  * read it (nt_hip_rl_readout_pack_weight, from the reference's [d, V] layout or a [V, d] one).
- * rows <= 256; vocab <= 262144; dim a multiple of 16, at most 16384; ldh a multiple of 8, hidden 16-byte
- * aligned; a u8 mask with one row per logits row (mask_ld >= vocab). Three launches on the
+ * rows <= 256; vocab <= 262144; dim a multiple of 16, at most 16384; a bf16 hidden has ldh a
+ * multiple of 8 and is 16-byte aligned (an f32 one: 4-byte aligned, one more launch rounds it); a u8 mask with one row per logits row (mask_ld >= vocab). Three launches on the
  * library stream: h into the same order (2 MB at 256 x 4096), the product with the sampler's
  * per-row records in its epilogue, then one workgroup per row that merges them and recomputes
  * only the 32 logits of the block holding the draw. The debug pointers (NULL in use) write the
@@ -208,16 +208,19 @@ int nt_hip_rl_sample_noalloc(const NtRlSampleArgs *a);
 /* Bytes of the packed weight: ceil(vocab / 256) 256 dim 2, the vocabulary padded with zero
  * columns to whole tiles of 256 (-1 for an invalid shape). */
 int64_t nt_hip_rl_readout_packed_bytes(int64_t vocab, int64_t dim);
-/* Pack a bf16 readout weight (layout NT_READOUT_W_*, row stride ld) into `packed` (device,
- * nt_hip_rl_readout_packed_bytes bytes, 16-byte aligned): one kernel on the library stream. */
-int nt_hip_rl_readout_pack_weight(const void *weight, int32_t layout, int64_t vocab, int64_t dim, int64_t ld,
-                                  void *packed);
+/* Pack a readout weight (dtype NT_BF16, or NT_F32 rounded to bf16 to nearest-even as it is packed,
+ * the half-precision product's rounding of f32 operands, src/tensor/precision.rs:4-8; layout
+ * NT_READOUT_W_*, row stride ld) into `packed` (device, nt_hip_rl_readout_packed_bytes bytes,
+ * 16-byte aligned): one kernel on the library stream. */
+int nt_hip_rl_readout_pack_weight(const void *weight, int32_t dtype, int32_t layout, int64_t vocab, int64_t dim,
+                                  int64_t ld, void *packed);
 typedef struct NtRlReadoutSampleArgs {
-    const void *hidden;        /* [rows, ldh] bf16: the readout's input */
+    const void *hidden;        /* [rows, ldh] hidden_dtype: the readout's input */
     const void *weight_packed; /* the readout weight, packed by nt_hip_rl_readout_pack_weight */
     int64_t rows, vocab, dim, ldh;
     int32_t mask_kind;         /* NT_MASK_NONE | NT_MASK_U8 */
-    int32_t pad0;
+    int32_t hidden_dtype;      /* NT_BF16, or NT_F32 (rounded to bf16 to nearest-even first, as
+                                  the weight is packed) */
     const void *mask;          /* u8 [rows, mask_ld] or NULL */
     int64_t mask_ld;
     double temperature;        /* >= 0 and finite; 0 = greedy */
@@ -243,11 +246,11 @@ int nt_hip_rl_readout_sample(const NtRlReadoutSampleArgs *a);
  * entropy each block's sum of w (x c - ref), and each row's token logit), then one workgroup per
  * row that merges the records. */
 typedef struct NtRlReadoutScoreArgs {
-    const void *hidden;        /* [rows, ldh] bf16 */
+    const void *hidden;        /* [rows, ldh] hidden_dtype */
     const void *weight_packed; /* packed by nt_hip_rl_readout_pack_weight */
     int64_t rows, vocab, dim, ldh;
     int32_t mask_kind;         /* NT_MASK_NONE | NT_MASK_U8 */
-    int32_t pad0;
+    int32_t hidden_dtype;      /* NT_BF16 | NT_F32 */
     const void *mask;          /* u8 [rows, mask_ld] or NULL */
     int64_t mask_ld;
     double temperature;        /* > 0 and finite */

@@ -22,7 +22,8 @@ from typing import List, Optional, Sequence, Tuple
 import numpy as np
 
 import noetic_rl as nr
-from noetic_rl import NtLayout, Tensor, _check, _dev
+from noetic_rl import (MatmulPrecision, NtLayout, Tensor, _check, _dev, matmul_precision, matmul_precision_scope,
+                       same_dtype, set_matmul_precision)
 
 MAX_RANK = 8
 _DT = {"f32": 0, "bf16": 1, "f16": 2, "bool": 3, "u8": 4, "i32": 5, "i64": 6}
@@ -342,13 +343,6 @@ def sort_desc(x: Tensor, lanes: Sequence[int]) -> Tuple[Tensor, Tensor]:
     return vals, idx
 
 
-class MatmulPrecision(enum.Enum):
-    """precision::MatmulPrecision: F32 (CpuRef's bits) or Half (bf16 operands on the matrix cores,
-    f32 accumulation)."""
-    F32 = "f32"
-    HALF = "half"
-
-
 def matmul(a: Tensor, al: Layout, b: Tensor, bl: Layout,
            precision: MatmulPrecision = MatmulPrecision.F32) -> Tuple[Tensor, List[int]]:
     """GpuBackend::matmul (or matmul_half with MatmulPrecision.HALF): the batched product of two f32
@@ -380,26 +374,30 @@ def half_gemm_key() -> str:
 # ----------------------------------------------------------------------------------- tensor level
 
 def tempered_logits(logits: Tensor, temperature: float, mask: Optional[Tensor] = None) -> Tensor:
-    """`tempered_logits` (rl.rs:475-486) materialised on the device with the general ops: bf16 is
-    cast to f32, `div_scalar(τ)` unless τ == 1, then `add(mask)` broadcast at rank (an f32
-    additive mask). The fused entry points take the tempered logits without materialising them;
+    """`tempered_logits` (rl.rs:475-486) materialised on the device with the general ops:
+    `div_scalar(τ)` unless τ == 1 (16-bit logits come out f32), then `add(mask)` broadcast at rank
+    (an f32 additive mask; 16-bit logits at τ == 1 are refused there, as the reference's add
+    refuses them). The fused entry points take the tempered logits without materialising them;
     this is the op sequence a caller gets when it asks for the tensor itself."""
     if not (temperature > 0.0 and np.isfinite(temperature)):
         raise ValueError(f"tempered_logits: temperature {temperature} (must be positive)")
     if temperature == 1.0 and mask is None:
         return logits  # rl.rs:476: no divide, no add
     lay = Layout.contiguous(logits.shape)
-    z = cast(logits, lay, "f32") if logits.dtype != "f32" else logits
-    if temperature != 1.0:
+    z = logits
+    if temperature != 1.0:  # div_scalar computes 16-bit logits in f32 (f32_operand)
+        z = cast(logits, lay, "f32") if logits.dtype != "f32" else logits
         z = unary(UnaryOp.DIV_SCALAR, z, lay, float(np.float32(temperature)))
     if mask is not None:
-        if mask.dtype != "f32":
-            raise TypeError("tempered_logits: an additive f32 mask")
         if len(mask.shape) != len(logits.shape):
             raise ValueError("tempered_logits: mask rank")
         if not all(a == b or a == 1 for a, b in zip(mask.shape, logits.shape)):
             raise ValueError(f"tempered_logits: mask {list(mask.shape)} does not broadcast to the logits "
                              f"{list(logits.shape)}")
+        # add's same_dtype check on the reference's z: 16-bit logits are not divided at τ == 1
+        same_dtype(logits.dtype if temperature == 1.0 else "f32", mask.dtype, "add")
+        if mask.dtype != "f32":
+            raise TypeError("tempered_logits: an additive f32 mask")
         out = broadcast_shape(logits.shape, mask.shape)
         z = binary(BinaryOp.ADD, z, lay.broadcast(out), mask, Layout.contiguous(mask.shape).broadcast(out))
     return z
@@ -475,9 +473,10 @@ class DTensor:
 
     # -- products
     def matmul(self, rhs: "DTensor") -> "DTensor":
-        """Tensor::matmul on the device (float.rs:926-960 -> gpu_matmul, gpu/mod.rs:458-470):
-        both operands as f32 views (16-bit ones cast first), batch dimensions broadcast."""
-        return self.matmul_with(rhs, MatmulPrecision.F32)
+        """Tensor::matmul on the device (float.rs:924-930 -> gpu_matmul, gpu/mod.rs:458-470) at the
+        calling thread's precision (`set_matmul_precision`): both operands as f32 views (16-bit
+        ones cast first), batch dimensions broadcast."""
+        return self.matmul_with(rhs, matmul_precision())
 
     def matmul_with(self, rhs: "DTensor", precision: MatmulPrecision) -> "DTensor":
         """Tensor::matmul_with (float.rs:934-944): the product at a named precision."""
@@ -546,7 +545,10 @@ class DTensor:
         return self.unary(UnaryOp.POW_SCALAR, p)
 
     def _binary(self, op: BinaryOp, other: "DTensor") -> "DTensor":
+        """float.rs:398-460: shapes broadcast, then one dtype (same_dtype, infer.rs:157-158: a bf16
+        tensor and an f32 one are refused, casts are explicit), then the f32 kernel."""
         out = broadcast_shape(self.shape, other.shape)
+        same_dtype(self.dtype, other.dtype, op.name.lower())
         a, b = self._f32(), other._f32()
         return DTensor(binary(op, a.storage, a.layout.broadcast(out), b.storage, b.layout.broadcast(out)))
 

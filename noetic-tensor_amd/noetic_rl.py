@@ -15,6 +15,7 @@ import ctypes as C
 import enum
 import math
 import os
+import threading
 from typing import Optional, Sequence
 
 import numpy as np
@@ -36,6 +37,82 @@ class HipError(RuntimeError):
     """A failed call into libnoetic_hip.so (the reference's TensorError::Device)."""
 
 
+class DTypeError(TypeError):
+    """TensorError::DType (src/tensor/error.rs:8-9): a value of another dtype than the operation
+    needs, with the reference's message (`same_dtype`, src/tensor/infer.rs:157-158)."""
+
+
+def same_dtype(a: str, b: str, op: str):
+    """infer::same_dtype (infer.rs:157-158): binary ops take one dtype; casts are explicit."""
+    if a != b:
+        raise DTypeError(f"{op}: {a} and {b} (casts are explicit)")
+
+
+_HALF = ("bf16", "f16")
+
+
+def tempered_dtype(dtype: str, temperature: float, mask_dtype: Optional[str]) -> str:
+    """The dtype of the reference's materialised `tempered_logits(logits, τ, mask)` (rl.rs:475-486),
+    or its DType refusal: `div_scalar` computes 16-bit values in f32 into f32 storage (`fdisp`,
+    float.rs:43-58, 494-499), τ == 1 keeps the logits' own dtype, and the additive mask is added
+    under `add`'s same_dtype check (float.rs:398-402). A u8 keep-mask stands for the f32 0/−∞ mask
+    it encodes."""
+    z = dtype if temperature == 1.0 else ("f32" if dtype in _HALF else dtype)
+    if mask_dtype is not None:
+        same_dtype(z, "f32" if mask_dtype in ("u8", "bool") else mask_dtype, "add")
+    return z
+
+
+def log_softmax_dtype(dtype: str) -> str:
+    """`log_softmax` (activation.rs:30-42) on logits of `dtype`, or its DType refusal: `max_dim`
+    returns f32 storage for 16-bit logits (fdisp, float.rs:710-722), so `x.sub(max)` of a bf16 or
+    f16 x fails same_dtype ("sub: bf16 and f32"). The reference's `token_log_probs`,
+    `categorical_kl` and `categorical_entropy` therefore take f32 logits, or 16-bit ones only
+    after a divide (τ ≠ 1) or an explicit `cast` (float.rs:113)."""
+    if dtype in _HALF:
+        same_dtype(dtype, "f32", "sub")
+    return dtype
+
+
+class MatmulPrecision(enum.Enum):
+    """precision::MatmulPrecision (src/tensor/precision.rs:27-38): F32 (the default: CpuRef's bits)
+    or Half (bf16 operands rounded to nearest-even as they are loaded, f32 accumulation, on the
+    matrix cores)."""
+    F32 = "f32"
+    HALF = "half"
+
+
+_precision = threading.local()
+
+
+def set_matmul_precision(p: MatmulPrecision) -> MatmulPrecision:
+    """precision::set_matmul_precision (precision.rs:53-58): the calling thread's precision of
+    GPU products; returns the previous setting."""
+    prev = matmul_precision()
+    _precision.value = MatmulPrecision(p)
+    return prev
+
+
+def matmul_precision() -> MatmulPrecision:
+    """precision::matmul_precision (precision.rs:60-63): F32 unless set on this thread."""
+    return getattr(_precision, "value", MatmulPrecision.F32)
+
+
+class matmul_precision_scope:
+    """`set_matmul_precision(p)` for a `with` block, the previous setting restored after it."""
+
+    def __init__(self, p: MatmulPrecision):
+        self.p = MatmulPrecision(p)
+
+    def __enter__(self):
+        self.prev = set_matmul_precision(self.p)
+        return self
+
+    def __exit__(self, *exc):
+        set_matmul_precision(self.prev)
+        return False
+
+
 class NtRlSampleArgs(C.Structure):
     _fields_ = [("logits", C.c_void_p), ("dtype", C.c_int32), ("mask_kind", C.c_int32),
                 ("rows", C.c_int64), ("vocab", C.c_int64), ("ld", C.c_int64),
@@ -55,16 +132,16 @@ class NtRlGumbelArgs(C.Structure):
 class NtRlReadoutSampleArgs(C.Structure):
     _fields_ = [("hidden", C.c_void_p), ("weight_packed", C.c_void_p), ("rows", C.c_int64), ("vocab", C.c_int64),
                 ("dim", C.c_int64), ("ldh", C.c_int64), ("mask_kind", C.c_int32),
-                ("pad0", C.c_int32), ("mask", C.c_void_p), ("mask_ld", C.c_int64), ("temperature", C.c_double),
-                ("uniforms", C.c_void_p), ("ids", C.c_void_p), ("logp", C.c_void_p), ("status", C.c_void_p),
+                ("hidden_dtype", C.c_int32), ("mask", C.c_void_p), ("mask_ld", C.c_int64),
+                ("temperature", C.c_double), ("uniforms", C.c_void_p), ("ids", C.c_void_p), ("logp", C.c_void_p), ("status", C.c_void_p),
                 ("logits", C.c_void_p), ("debug_block", C.c_void_p), ("debug_block_index", C.c_void_p)]
 
 
 class NtRlReadoutScoreArgs(C.Structure):
     _fields_ = [("hidden", C.c_void_p), ("weight_packed", C.c_void_p), ("rows", C.c_int64), ("vocab", C.c_int64),
                 ("dim", C.c_int64), ("ldh", C.c_int64), ("mask_kind", C.c_int32),
-                ("pad0", C.c_int32), ("mask", C.c_void_p), ("mask_ld", C.c_int64), ("temperature", C.c_double),
-                ("tokens", C.c_void_p), ("logp", C.c_void_p), ("entropy", C.c_void_p), ("status", C.c_void_p),
+                ("hidden_dtype", C.c_int32), ("mask", C.c_void_p), ("mask_ld", C.c_int64),
+                ("temperature", C.c_double), ("tokens", C.c_void_p), ("logp", C.c_void_p), ("entropy", C.c_void_p), ("status", C.c_void_p),
                 ("logits", C.c_void_p)]
 
 
@@ -138,7 +215,8 @@ _SIGS = {
     "nt_hip_rl_readout_sample": (C.c_int, [C.POINTER(NtRlReadoutSampleArgs)]),
     "nt_hip_rl_readout_score": (C.c_int, [C.POINTER(NtRlReadoutScoreArgs)]),
     "nt_hip_rl_readout_packed_bytes": (C.c_int64, [C.c_int64, C.c_int64]),
-    "nt_hip_rl_readout_pack_weight": (C.c_int, [C.c_void_p, C.c_int32, C.c_int64, C.c_int64, C.c_int64, C.c_void_p]),
+    "nt_hip_rl_readout_pack_weight": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_int64, C.c_int64, C.c_int64,
+                                                C.c_void_p]),
     "nt_hip_rl_sample_noalloc": (C.c_int, [C.POINTER(NtRlSampleArgs)]),
     "nt_hip_rl_score": (C.c_int, [C.POINTER(NtRlScoreArgs)]),
     "nt_hip_rl_score_backward": (C.c_int, [C.POINTER(NtRlScoreGradArgs)]),
@@ -282,9 +360,16 @@ def platform_details() -> str:
 
 
 def platform_key() -> str:
-    """`gpu_platform_key` (gpu/mod.rs:699-704) at the default f32 matmul precision:
-    `key()` followed by `platform_details()`."""
-    return f"{key()}-{platform_details()}"
+    """`gpu_platform_key` (gpu/mod.rs:690-704): `key()` followed by `platform_details()` and, when
+    the calling thread's matmul precision is Half, the reduced-precision product's part
+    (`half_gemm_key`, precision.rs:72-78): the kernels' source hash, which covers the readout
+    fusion's product as well as `matmul_half`."""
+    base = f"{key()}-{platform_details()}"
+    if matmul_precision() == MatmulPrecision.HALF:
+        buf = C.create_string_buffer(256)
+        _check(_dev().nt_hip_half_gemm_key(buf, 256), "half_gemm_key")
+        return f"{base}-{buf.value.decode()}"
+    return base
 
 
 def launches() -> int:
@@ -437,12 +522,18 @@ class Tempered:
     """`tempered_logits(logits, temperature, mask)` (rl.rs:475-486), kept unmaterialised: the
     fused kernels apply the divide and the vocabulary mask while streaming the logits.
     mask: None, a u8 keep-mask (0 excludes) or an additive f32 mask, [rows or 1, V] in the
-    logits' rank (a mask whose leading dims are all 1 is shared by every row)."""
+    logits' rank (a mask whose leading dims are all 1 is shared by every row).
+
+    Built directly, it is the fused entries' (logits, τ, mask) triple: 16-bit logits are widened
+    exactly to f32 at every τ, the values the reference's chain gives on `logits.cast(F32)`.
+    Built by `tempered_logits`, it also keeps the reference's dtype rules (`dtype`): the
+    reference-named functions refuse it where the materialised tensor would be refused."""
 
     def __init__(self, logits: Tensor, temperature: float, mask: Optional[Tensor]):
         if not (temperature > 0.0 and math.isfinite(temperature)):
             raise ValueError(f"tempered_logits: temperature {temperature} (must be positive)")
         self.logits, self.temperature, self.mask = logits, float(temperature), mask
+        self.dtype = None  # the materialised tensor's dtype, when built by tempered_logits
         if mask is not None:
             if len(mask.shape) != len(logits.shape):
                 raise ValueError("tempered_logits: mask rank")
@@ -455,7 +546,19 @@ class Tempered:
 
 
 def tempered_logits(logits: Tensor, temperature: float, mask: Optional[Tensor] = None) -> Tempered:
-    return Tempered(logits, temperature, mask)
+    """rl.rs:475-486, unmaterialised, with the reference's refusals: a 16-bit tensor at τ == 1 is
+    not divided, so adding the (f32) mask fails same_dtype ("add: bf16 and f32")."""
+    t = Tempered(logits, temperature, mask)
+    t.dtype = tempered_dtype(logits.dtype, t.temperature, None if mask is None else mask.dtype)
+    return t
+
+
+def _logits_dtype(x) -> str:
+    """The dtype the reference's op would see: a Tensor's own, a `tempered_logits` result's
+    materialised one; a Tempered built directly (the fused triple) reads as f32."""
+    if isinstance(x, Tempered):
+        return x.dtype if x.dtype is not None else "f32"
+    return x.dtype
 
 
 def _as_tempered(x) -> Tempered:
@@ -518,10 +621,16 @@ def sample_categorical(logits: Tensor, temperature: float, mask: Optional[Tensor
     and one Gumbel draw per logit from `rng` in row-major order, so the stream advances by one
     u64 per logit (none at temperature 0). The draws are generated on the device at the stream's
     position (nt_hip_rl_sample_gumbel); the stream is advanced here, after the rows are accepted:
-    a row with no allowed token is refused with the reference's message and draws nothing."""
+    a row with no allowed token is refused with the reference's message and draws nothing.
+
+    The reference's dtype rules hold, in its order: 16-bit logits at τ ∈ {0, 1} with a mask are
+    refused by tempered_logits' add, and at τ == 1 (after the row check) by `z + g`, the noise
+    being f32 (`from_f64s` computes 16-bit dtypes in f32, float.rs:257-260): "add: bf16 and f32".
+    `sample_logp` takes them at every τ, widened exactly."""
     if not (temperature >= 0.0 and math.isfinite(temperature)):
         raise ValueError(f"sample_categorical: temperature {temperature} (must be ≥ 0)")
     t = Tempered(logits, 1.0 if temperature == 0.0 else temperature, mask)
+    z = tempered_dtype(logits.dtype, t.temperature, None if mask is None else mask.dtype)
     rows, V = _rows(logits)
     out_shape = logits.shape[:-1]
     ids = IntTensor(out_shape)
@@ -536,6 +645,7 @@ def sample_categorical(logits: Tensor, temperature: float, mask: Optional[Tensor
     if bad.size:
         raise ValueError(f"sample_categorical: position {bad[0]} has no allowed token (every logit −∞ or a NaN)")
     if temperature != 0.0:
+        same_dtype(z, "f32" if z in _HALF else z, "add")
         rng.skip_u64(rows * V)
     return ids
 
@@ -548,66 +658,123 @@ def sample_categorical_inv_cdf(logits: Tensor, temperature: float, mask: Optiona
 
 
 NT_READOUT_W_DV, NT_READOUT_W_VD = 0, 1
+_ESIZE = {"f32": 4, "bf16": 2}
+_READOUT_ROWS = 256  # rows per readout call (include/noetic_hip.h)
 
 
 class PackedReadout:
-    """A readout weight packed once for nt_hip_rl_readout_sample (the order the matrix cores read
-    it): from the reference's Linear weight [d, V] (`layout` "dv") or a vocabulary-major [V, d]."""
+    """The decoder head's weight (`Linear`, linear.rs:1-12: `x.matmul(w)` with w [in, out], or
+    seed-batched [S, in, out]) packed once for the readout-fused entries, in the order the matrix
+    cores read it: from [d, V] or [S, d, V] (`layout` "dv"), or a vocabulary-major [V, d] /
+    [S, V, d] ("vd"). bf16 is packed as it is; f32 is rounded to bf16 to nearest-even as it is
+    packed, the rounding MatmulPrecision::Half gives f32 operands as they are loaded
+    (precision.rs:4-8). One packing kernel per seed."""
 
     def __init__(self, weight: Tensor, layout: str = "dv"):
-        if weight.dtype != "bf16" or len(weight.shape) != 2:
-            raise ValueError("readout weight: a bf16 matrix")
+        if weight.dtype not in _ESIZE or len(weight.shape) not in (2, 3):
+            raise ValueError("readout weight: an f32 or bf16 [d, V] or [S, d, V] matrix")
+        sh = tuple(weight.shape) if len(weight.shape) == 3 else (1,) + tuple(weight.shape)
+        self.seeds, self.batched, self.weight_dtype = sh[0], len(weight.shape) == 3, weight.dtype
         if layout == "dv":
-            self.dim, self.vocab = weight.shape
+            self.dim, self.vocab = sh[1], sh[2]
             code, ld = NT_READOUT_W_DV, self.vocab
         elif layout == "vd":
-            self.vocab, self.dim = weight.shape
+            self.vocab, self.dim = sh[1], sh[2]
             code, ld = NT_READOUT_W_VD, self.dim
         else:
             raise ValueError(f"readout weight layout {layout!r} (dv or vd)")
         nbytes = int(lib().nt_hip_rl_readout_packed_bytes(self.vocab, self.dim))
         if nbytes < 0:
             raise ValueError(f"readout weight [{self.vocab}, {self.dim}]: dim a multiple of 16")
-        self.buf = Buffer(nbytes)
-        _check(lib().nt_hip_rl_readout_pack_weight(weight.ptr, code, self.vocab, self.dim, ld, self.buf.ptr),
-               "readout pack")
+        self.seed_bytes = nbytes
+        self.buf = Buffer(nbytes * self.seeds)
+        dt = NT_F32 if weight.dtype == "f32" else NT_BF16
+        step = sh[1] * sh[2] * _ESIZE[weight.dtype]
+        for k in range(self.seeds):
+            _check(lib().nt_hip_rl_readout_pack_weight(weight.ptr + k * step, dt, code, self.vocab, self.dim, ld,
+                                                       self.seed_ptr(k)), "readout pack")
 
-    def buf_bytes(self) -> bytes:
-        """The packed bytes (a synchronising download; for tests)."""
-        out = (C.c_uint8 * self.buf.nbytes)()
-        _check(lib().nt_hip_download(out, C.c_void_p(self.buf.ptr), self.buf.nbytes), "download packed")
+    def seed_ptr(self, seed: int) -> int:
+        return self.buf.ptr + seed * self.seed_bytes
+
+    def buf_bytes(self, seed: int = 0) -> bytes:
+        """One seed's packed bytes (a synchronising download; for tests)."""
+        out = (C.c_uint8 * self.seed_bytes)()
+        _check(lib().nt_hip_download(out, C.c_void_p(self.seed_ptr(seed)), self.seed_bytes), "download packed")
         return bytes(out)
+
+
+def _readout_gate(who: str):
+    """The readout fusion's product has bf16 operands and f32 accumulation on the matrix cores, the
+    reduced-precision product: it stands for the head's `x.matmul(w)` only when the calling
+    thread's matmul precision is Half (`Tensor::matmul` reads it for a GPU tensor,
+    float.rs:924-930; precision.rs:59-63). At the default F32 the head's product is the f32 one:
+    multiply with `noetic_ops.DTensor.matmul` and sample or score the written logits."""
+    if matmul_precision() != MatmulPrecision.HALF:
+        raise ValueError(f"{who}: the readout fusion computes the MatmulPrecision::Half product; at this "
+                         "thread's f32 precision multiply with matmul and use the written logits")
+
+
+def _readout_shape(hidden: Tensor, weight: PackedReadout, who: str):
+    """(seeds, rows per seed, d) of the head's input: [.., d] against a [d, V] weight (the weight
+    broadcast over the leading dims, as `to_rank` does, linear.rs:52-58), [S, N, d] against a
+    seed-batched one."""
+    if hidden.dtype not in _ESIZE or len(hidden.shape) < 2:
+        raise ValueError(f"{who}: hidden [.., d] in f32 or bf16")
+    d = hidden.shape[-1]
+    if weight.batched:
+        if len(hidden.shape) != 3 or hidden.shape[0] != weight.seeds:
+            raise ValueError(f"{who}: hidden {list(hidden.shape)} against a weight of {weight.seeds} seeds "
+                             "(hidden [S, N, d])")
+        S, N = hidden.shape[0], hidden.shape[1]
+    else:
+        S, N = 1, hidden.numel // d
+    if d != weight.dim:
+        raise ValueError(f"{who}: hidden's d {d} against the weight's {weight.dim}")
+    return S, N, d
+
+
+def _readout_chunks(S: int, N: int):
+    """(seed, first row of the call over all rows, rows) of each call: one seed's rows, at most
+    256 per call."""
+    for k in range(S):
+        for r0 in range(0, N, _READOUT_ROWS):
+            yield k, k * N + r0, min(_READOUT_ROWS, N - r0)
 
 
 def readout_sample_logp(hidden: Tensor, weight: PackedReadout, temperature: float, mask: Optional[Tensor],
                         rng: Optional[Rng], uniforms: Optional[Tensor] = None, debug: bool = False,
                         check: bool = True):
-    """One decode step fused: logits = hidden [rows, d] . W (the readout, decoder.rs:272,286),
-    then sample_logp's inverse-CDF draw and log-probability on them (rl.rs:134-141, 475-529), the
-    logits never written. `weight` is the readout weight packed once (PackedReadout). Returns
-    (ids, logp), plus with `debug` the f32 logits [rows, V], the recomputed crossing block
-    [rows, 32] and its index [rows]."""
+    """One decode step fused at MatmulPrecision::Half: logits = hidden . W (the decoder's head,
+    decoder.rs:272,286; linear.rs:52-58) with bf16 operands (an f32 hidden rounded to nearest-even
+    first) and f32 accumulation, then sample_logp's inverse-CDF draw and log-probability on them
+    (rl.rs:134-141, 475-529), the logits never written. `weight` is the head's weight packed once
+    (PackedReadout); hidden is [.., d], or [S, N, d] for a seed-batched weight. Returns (ids, logp)
+    shaped like hidden without d, plus with `debug` the f32 logits [.., V], the recomputed crossing
+    block [.., 32] and its index."""
+    _readout_gate("readout_sample_logp")
     if not (temperature >= 0.0 and math.isfinite(temperature)):
         raise ValueError(f"sample_categorical: temperature {temperature} (must be ≥ 0)")
-    if hidden.dtype != "bf16" or len(hidden.shape) != 2:
-        raise ValueError("readout: hidden [rows, d] in bf16")
-    rows, d = hidden.shape
-    V = weight.vocab
-    if weight.dim != d:
-        raise ValueError(f"readout: hidden's d {d} against the weight's {weight.dim}")
+    S, N, d = _readout_shape(hidden, weight, "readout")
+    rows, V, es = S * N, weight.vocab, _ESIZE[hidden.dtype]
+    out_shape = hidden.shape[:-1]
+    if mask is not None and (mask.dtype != "u8" or mask.numel != rows * V):
+        raise ValueError("readout: a u8 keep-mask [.., V], one row per logits row")
     if temperature != 0.0 and uniforms is None:
         if rng is None:
             raise ValueError("sample_categorical: a stream is needed at temperature > 0")
         uniforms = Tensor.from_numpy(rng.uniforms(rows), "f64")
-    ids, lp, status = IntTensor((rows,)), Tensor((rows,), "f32"), Tensor((rows,), "u8")
-    dbg = (Tensor((rows, V), "f32"), Tensor((rows, 32), "f32"), IntTensor((rows,))) if debug else (None, None, None)
-    if mask is not None and (mask.dtype != "u8" or mask.numel != rows * V):
-        raise ValueError("readout: a u8 keep-mask [rows, V]")
-    a = NtRlReadoutSampleArgs(hidden.ptr, weight.buf.ptr, rows, V, d, d, NT_MASK_U8 if mask is not None else NT_MASK_NONE,
-                              0, None if mask is None else mask.ptr, V if mask is not None else 0, float(temperature),
-                              None if uniforms is None else uniforms.ptr, ids.ptr, lp.ptr, status.ptr,
-                              *(None if t is None else t.ptr for t in dbg))
-    _check(lib().nt_hip_rl_readout_sample(C.byref(a)), "readout sample")
+    ids, lp, status = IntTensor(out_shape), Tensor(out_shape, "f32"), Tensor(out_shape, "u8")
+    dbg = ((Tensor(out_shape + (V,), "f32"), Tensor(out_shape + (32,), "f32"), IntTensor(out_shape)) if debug
+           else (None, None, None))
+    for k, g0, n in _readout_chunks(S, N):
+        at = lambda t, w: None if t is None else t.ptr + g0 * w
+        a = NtRlReadoutSampleArgs(at(hidden, d * es), weight.seed_ptr(k if weight.batched else 0), n, V, d, d,
+                                  NT_MASK_U8 if mask is not None else NT_MASK_NONE,
+                                  NT_F32 if hidden.dtype == "f32" else NT_BF16, at(mask, V),
+                                  V if mask is not None else 0, float(temperature), at(uniforms, 8), at(ids, 4),
+                                  at(lp, 4), at(status, 1), at(dbg[0], V * 4), at(dbg[1], 32 * 4), at(dbg[2], 4))
+        _check(lib().nt_hip_rl_readout_sample(C.byref(a)), "readout sample")
     if check:
         st = status.to_numpy().ravel()
         bad = np.nonzero(st != NT_ROW_OK)[0]
@@ -618,35 +785,36 @@ def readout_sample_logp(hidden: Tensor, weight: PackedReadout, temperature: floa
 
 def readout_score(hidden: Tensor, weight: PackedReadout, temperature: float, mask: Optional[Tensor],
                   tokens: Optional[Tensor], entropy: bool = True, debug: bool = False):
-    """The scoring pass fused with the readout: logits = hidden [rows, d] . W (decoder.rs:272,286)
-    tempered and masked (rl.rs:475-486), then token_log_probs (rl.rs:134-141) of `tokens` and, with
-    `entropy`, categorical_entropy (rl.rs:405-414) per row, as `score` gives them on written
-    logits, the logits never written. Returns (logp or None, entropy or None), plus with `debug`
-    the f32 logits [rows, V]."""
+    """The scoring pass fused with the head at MatmulPrecision::Half: logits = hidden . W
+    (decoder.rs:272,286) tempered and masked (rl.rs:475-486), then token_log_probs (rl.rs:134-141)
+    of `tokens` and, with `entropy`, categorical_entropy (rl.rs:405-414) per row, as `score` gives
+    them on written logits, the logits never written. Shapes as readout_sample_logp; tokens are
+    shaped like hidden without d. Returns (logp or None, entropy or None), plus with `debug` the f32
+    logits [.., V]."""
+    _readout_gate("readout_score")
     if not (temperature > 0.0 and math.isfinite(temperature)):
         raise ValueError(f"tempered_logits: temperature {temperature} (must be positive)")
-    if hidden.dtype != "bf16" or len(hidden.shape) != 2:
-        raise ValueError("readout: hidden [rows, d] in bf16")
-    rows, d = hidden.shape
-    V = weight.vocab
-    if weight.dim != d:
-        raise ValueError(f"readout: hidden's d {d} against the weight's {weight.dim}")
+    S, N, d = _readout_shape(hidden, weight, "readout")
+    rows, V, es = S * N, weight.vocab, _ESIZE[hidden.dtype]
+    out_shape = hidden.shape[:-1]
     if tokens is not None and (tokens.dtype != "i32" or tokens.numel != rows):
-        raise ValueError("token_log_probs: tokens [rows] (i32)")
+        raise ValueError("token_log_probs: tokens shape (the logits' without the vocabulary axis)")
     if tokens is None and not entropy:
         raise ValueError("readout_score: neither log-probabilities nor the entropy asked for")
     if mask is not None and (mask.dtype != "u8" or mask.numel != rows * V):
-        raise ValueError("readout: a u8 keep-mask [rows, V]")
-    lp = Tensor((rows,), "f32") if tokens is not None else None
-    ent = Tensor((rows,), "f32") if entropy else None
-    status = Tensor((rows,), "u8")
-    logits = Tensor((rows, V), "f32") if debug else None
-    ptr = lambda t: None if t is None else t.ptr
-    a = NtRlReadoutScoreArgs(hidden.ptr, weight.buf.ptr, rows, V, d, d,
-                             NT_MASK_U8 if mask is not None else NT_MASK_NONE, 0, ptr(mask),
-                             V if mask is not None else 0, float(temperature), ptr(tokens), ptr(lp), ptr(ent),
-                             status.ptr, ptr(logits))
-    _check(lib().nt_hip_rl_readout_score(C.byref(a)), "readout score")
+        raise ValueError("readout: a u8 keep-mask [.., V], one row per logits row")
+    lp = Tensor(out_shape, "f32") if tokens is not None else None
+    ent = Tensor(out_shape, "f32") if entropy else None
+    status = Tensor(out_shape, "u8")
+    logits = Tensor(out_shape + (V,), "f32") if debug else None
+    for k, g0, n in _readout_chunks(S, N):
+        at = lambda t, w: None if t is None else t.ptr + g0 * w
+        a = NtRlReadoutScoreArgs(at(hidden, d * es), weight.seed_ptr(k if weight.batched else 0), n, V, d, d,
+                                 NT_MASK_U8 if mask is not None else NT_MASK_NONE,
+                                 NT_F32 if hidden.dtype == "f32" else NT_BF16, at(mask, V),
+                                 V if mask is not None else 0, float(temperature), at(tokens, 4), at(lp, 4),
+                                 at(ent, 4), at(status, 1), at(logits, V * 4))
+        _check(lib().nt_hip_rl_readout_score(C.byref(a)), "readout score")
     if tokens is not None:
         st = status.to_numpy().ravel()
         bad = np.nonzero(st == NT_ROW_BAD_TOKEN)[0]
@@ -734,7 +902,16 @@ def score_grad(logits, ref_logits, tokens: Optional[Tensor], stats: RowStats, kl
 
 
 def token_log_probs(logits, tokens: Tensor) -> Tensor:
-    """rl.rs:134-141: log_softmax(logits)[…, tokens[…]]; `logits` may be a `tempered_logits`."""
+    """rl.rs:134-141: log_softmax(logits)[…, tokens[…]]; `logits` may be a `tempered_logits`.
+    16-bit logits are refused as the reference's log_softmax refuses them (at τ == 1, or
+    untempered: "sub: bf16 and f32 (casts are explicit)"); `score` with a Tempered triple takes
+    them, widened exactly."""
+    x = _as_tempered(logits)
+    if len(x.logits.shape) < 1:
+        raise ValueError("token_log_probs: logits of rank 0")
+    if tuple(tokens.shape) != tuple(x.logits.shape[:-1]):
+        raise ValueError("token_log_probs: tokens shape (the logits' without the vocabulary axis)")
+    log_softmax_dtype(_logits_dtype(logits))
     return _score(logits, None, tokens, True, False, False, False)[0]
 
 
@@ -773,10 +950,15 @@ def _zero_masked(per: Tensor, mask: Optional[Tensor]) -> Tensor:
 
 def categorical_kl(logits, ref_logits, mask: Optional[Tensor] = None,
                    reduction: TokenReduction = TokenReduction.TOKEN_MEAN) -> Tensor:
-    """rl.rs:327-338 (exact KL per position, reduced per seed)."""
+    """rl.rs:327-338 (exact KL per position, reduced per seed); both sides' log_softmax keep the
+    reference's dtype refusal (as token_log_probs)."""
     x = _as_tempered(logits)
     if len(x.logits.shape) != 4:
         raise ValueError("categorical_kl: logits [S, B, T, V]")
+    if tuple(_as_tempered(ref_logits).logits.shape) != tuple(x.logits.shape):
+        raise ValueError("categorical_kl: reference logits shape")
+    log_softmax_dtype(_logits_dtype(logits))
+    log_softmax_dtype(_logits_dtype(ref_logits))
     kl = _score(logits, ref_logits, None, False, False, True, False)[2]
     return _reduce(_zero_masked(kl, mask), mask, reduction)
 
@@ -784,16 +966,17 @@ def categorical_kl(logits, ref_logits, mask: Optional[Tensor] = None,
 def reference_kl(logits: Tensor, ref_logits: Tensor, temperature: float, vocab_mask: Optional[Tensor],
                  mask: Optional[Tensor] = None, reduction: TokenReduction = TokenReduction.TOKEN_MEAN) -> Tensor:
     """rl.rs:347-351."""
-    return categorical_kl(Tempered(logits, temperature, vocab_mask), Tempered(ref_logits, temperature, vocab_mask),
-                          mask, reduction)
+    return categorical_kl(tempered_logits(logits, temperature, vocab_mask),
+                          tempered_logits(ref_logits, temperature, vocab_mask), mask, reduction)
 
 
 def categorical_entropy(logits, mask: Optional[Tensor] = None,
                         reduction: TokenReduction = TokenReduction.TOKEN_MEAN) -> Tensor:
-    """rl.rs:405-414."""
+    """rl.rs:405-414; log_softmax's dtype refusal as token_log_probs."""
     x = _as_tempered(logits)
     if len(x.logits.shape) != 4:
         raise ValueError("categorical_entropy: logits [S, B, T, V]")
+    log_softmax_dtype(_logits_dtype(logits))
     ent = _score(logits, None, None, False, False, False, True)[3]
     return _reduce(_zero_masked(ent, mask), mask, reduction)
 

@@ -9,6 +9,7 @@ pass 2 recomputes must equal pass 1's logits bit for bit, and reruns are byte-id
 import numpy as np
 import pytest
 
+import noetic_ops as ops
 import noetic_rl as nr
 import workloads as W
 from oracle import oracle as O
@@ -20,19 +21,31 @@ EDGE = 1e-6
 @pytest.fixture(scope="module", autouse=True)
 def device():
     nr.claim(0)
+    # the readout fusion is the reduced-precision product: it runs at MatmulPrecision::Half
+    prev = nr.set_matmul_precision(nr.MatmulPrecision.HALF)
     yield
+    nr.set_matmul_precision(prev)
 
 
-def run_case(name, rows, V, d, tau, masked, seed, check_gemm_rows=None):
-    h = W.normal((rows, d), "bf16", seed, f"readout/{name}/h", std=1.0)
+def rounded(t):
+    """A device tensor's values as the product reads them: bf16 as they are, f32 rounded to
+    nearest-even bf16 (precision.rs:4-8; the oracle's half.rs restatement), as f64."""
+    a = t.to_numpy()
+    return (W.bf16_to_f32(a) if t.dtype == "bf16" else O.bf16_to_f32(O.bf16_from_f32(a))).astype(np.float64)
+
+
+def run_case(name, rows, V, d, tau, masked, seed, check_gemm_rows=None, dtype="bf16"):
+    h = W.normal((rows, d), dtype, seed, f"readout/{name}/h", std=1.0)
     # the reference's Linear layout [d, V] (src/nn/linear.rs:1-3), packed once; also the
     # vocabulary-major layout, whose packing must give the same bytes
-    w = W.normal((d, V), "bf16", seed, f"readout/{name}/w", std=2.0 / np.sqrt(d))
+    w = W.normal((d, V), dtype, seed, f"readout/{name}/w", std=2.0 / np.sqrt(d))
     packed = nr.PackedReadout(w, "dv")
-    wt = nr.Tensor.from_numpy(np.ascontiguousarray(w.to_numpy().T), "bf16")
+    wt = nr.Tensor.from_numpy(np.ascontiguousarray(w.to_numpy().T), dtype)
     packed_vd = nr.PackedReadout(wt, "vd")
+    del wt
     nr.sync()
     assert packed.buf_bytes() == packed_vd.buf_bytes(), f"{name}: the two layouts pack differently"
+    del packed_vd
     keep = None
     mt = None
     if masked:
@@ -47,9 +60,9 @@ def run_case(name, rows, V, d, tau, masked, seed, check_gemm_rows=None):
     ids, lp, logits = ids.to_numpy().ravel(), lp.to_numpy().ravel(), logits.to_numpy()
     blk, bidx = blk.to_numpy(), bidx.to_numpy().ravel()
     # the product against f64 on a row sample, within f32 accumulation's bound
-    hb = W.bf16_to_f32(h.to_numpy()).astype(np.float64)
+    hb = rounded(h)
     sample = np.arange(rows) if check_gemm_rows is None else check_gemm_rows
-    wb = W.bf16_to_f32(w.to_numpy()).astype(np.float64)  # [d, V]
+    wb = rounded(w)  # [d, V]
     exact = hb[sample] @ wb
     scale = np.abs(hb[sample]) @ np.abs(wb)
     gerr = np.abs(logits[sample].astype(np.float64) - exact)
@@ -101,6 +114,18 @@ def run_case(name, rows, V, d, tau, masked, seed, check_gemm_rows=None):
     again = nr.readout_sample_logp(h, packed, tau, mt, None, uniforms=ut if tau else None)
     assert again[0].to_numpy().tobytes() == ids.astype(np.int32).tobytes(), f"{name}: rerun ids"
     assert again[1].to_numpy().tobytes() == lp.tobytes(), f"{name}: rerun logp"
+    if dtype == "f32":
+        # f32 operands are the device cast's bf16 operands: the same packed bytes, logits, ids and
+        # log-probabilities, bit for bit
+        lay = lambda t: ops.Layout.contiguous(t.shape)
+        hc, wc = ops.cast(h, lay(h), "bf16"), ops.cast(w, lay(w), "bf16")
+        pc = nr.PackedReadout(wc, "dv")
+        del wc
+        assert pc.buf_bytes() == packed.buf_bytes(), f"{name}: f32 packing differs from the bf16 cast's"
+        ic, lc, zc = nr.readout_sample_logp(hc, pc, tau, mt, None, uniforms=ut if tau else None, debug=True)[:3]
+        assert ic.to_numpy().tobytes() == ids.astype(np.int32).tobytes(), f"{name}: ids against the bf16 cast"
+        assert lc.to_numpy().tobytes() == lp.tobytes(), f"{name}: logp against the bf16 cast"
+        assert zc.to_numpy().tobytes() == logits.tobytes(), f"{name}: logits against the bf16 cast"
 
 
 @pytest.mark.parametrize("rows,V,d", [(40, 1000, 256), (256, 4104, 512), (1, 300, 64), (97, 257, 16), (64, 600, 528)])
@@ -118,6 +143,91 @@ def test_readout_sampler_above_131072_columns(tau, masked):
 def test_readout_sampler_at_the_decode_shape():
     # C4's decode step: 256 rows, d 4096, V 128256, a 30% keep-mask, T 0.7
     run_case("c4 readout", 256, 128256, 4096, 0.7, True, seed=2024, check_gemm_rows=np.arange(0, 256, 16))
+
+
+@pytest.mark.parametrize("rows,V,d", [(40, 1000, 256), (97, 257, 16)])
+@pytest.mark.parametrize("tau,masked", [(0.7, True), (0.0, False)])
+def test_readout_sampler_f32_operands_small_shapes(rows, V, d, tau, masked):
+    run_case(f"f32 r{rows}v{V}d{d}t{tau}m{int(masked)}", rows, V, d, tau, masked, seed=rows + V + d + 1,
+             dtype="f32")
+
+
+def test_readout_sampler_f32_operands_at_the_decode_shape():
+    # C4's decode step with the head's f32 weight [4096, 128256] and f32 hidden states, as the
+    # reference's decoder holds them, rounded to bf16 as MatmulPrecision::Half rounds its operands
+    run_case("c4 readout f32", 256, 128256, 4096, 0.7, True, seed=2025, check_gemm_rows=np.arange(3, 256, 16),
+             dtype="f32")
+
+
+def test_f32_weights_pack_rounded_to_nearest_even():
+    """Ties, their neighbours, subnormals, the overflow to infinity, signed zeros, infinities and
+    NaNs: packing f32 gives the bytes of packing the device cast's bf16 (half.rs:16-23, itself
+    checked against the oracle's restatement here), a NaN staying a NaN."""
+    d, V = 32, 300
+    rng = np.random.default_rng(8)
+    bits = rng.normal(0, 1, (d, V)).astype(np.float32).view(np.uint32)
+    special = np.array([0x3F808000, 0x3F818000, 0x3F808001, 0x3F807FFF, 0xBF808000, 0xBF818000,
+                        0x00008000, 0x00018000, 0x0000FFFF, 0x80007FFF, 0x00000001, 0x807F8000,
+                        0x7F7FFFFF, 0x7F7F7FFF, 0x7F7F8000, 0xFF7FFFFF, 0x7F800000, 0xFF800000,
+                        0x00000000, 0x80000000, 0x7FC00001, 0xFF800001, 0x7F812345], np.uint32)
+    pos = rng.choice(d * V, size=(8, special.size), replace=False)
+    for k in range(8):
+        bits.ravel()[pos[k]] = special
+    wf = bits.view(np.float32)
+    w = nr.Tensor.from_numpy(wf)
+    wc = ops.cast(w, ops.Layout.contiguous(w.shape), "bf16")
+    cast = wc.to_numpy()
+    nan = np.isnan(wf)
+    want = O.bf16_from_f32(wf)
+    assert np.array_equal(cast[~nan], want[~nan]), "the device cast is not half.rs's rounding"
+    assert np.all(np.isnan(W.bf16_to_f32(cast[nan])))
+    a = np.frombuffer(nr.PackedReadout(w, "dv").buf_bytes(), np.uint16)
+    b = np.frombuffer(nr.PackedReadout(wc, "dv").buf_bytes(), np.uint16)
+    differ = np.nonzero(a != b)[0]
+    # only NaNs may differ (in payload), and those stay NaNs
+    assert np.all(np.isnan(W.bf16_to_f32(a[differ]))) and np.all(np.isnan(W.bf16_to_f32(b[differ])))
+    assert np.sum(np.isnan(W.bf16_to_f32(a))) == int(nan.sum())
+    assert len(differ) <= int(nan.sum())
+
+
+def test_seed_batched_head():
+    # the decoder's seed-batched head: hidden [S, N, d] . W [S, d, V] (linear.rs:1-12), N above
+    # one call's 256 rows; each seed's rows equal the unbatched call on that seed's weight
+    S, N, d, V, tau = 2, 300, 64, 1000, 0.8
+    h = W.normal((S, N, d), "f32", 9, "readout/seeds/h")
+    w = W.normal((S, d, V), "f32", 9, "readout/seeds/w", std=2.0 / np.sqrt(d))
+    rng = np.random.default_rng(9)
+    keep = (rng.random((S, N, V)) < 0.4).astype(np.uint8)
+    keep[..., 7] = 1
+    u = nr.Rng(9, "readout/seeds/u").uniforms(S * N)
+    packed = nr.PackedReadout(w, "dv")
+    ids, lp, logits = nr.readout_sample_logp(h, packed, tau, nr.Tensor.from_numpy(keep), None,
+                                             uniforms=nr.Tensor.from_numpy(u, "f64"), debug=True)[:3]
+    assert ids.shape == (S, N) and lp.shape == (S, N) and logits.shape == (S, N, V)
+    ids, lp, logits = ids.to_numpy(), lp.to_numpy(), logits.to_numpy()
+    hn, wn = h.to_numpy(), w.to_numpy()
+    for k in range(S):
+        hk, wk = nr.Tensor.from_numpy(hn[k]), nr.Tensor.from_numpy(wn[k])
+        i1, l1, z1 = nr.readout_sample_logp(hk, nr.PackedReadout(wk, "dv"), tau, nr.Tensor.from_numpy(keep[k]), None,
+                                            uniforms=nr.Tensor.from_numpy(u[k * N:(k + 1) * N], "f64"),
+                                            debug=True)[:3]
+        assert i1.to_numpy().tobytes() == ids[k].tobytes(), f"seed {k}: ids"
+        assert l1.to_numpy().tobytes() == lp[k].tobytes(), f"seed {k}: logp"
+        assert z1.to_numpy().tobytes() == logits[k].tobytes(), f"seed {k}: logits"
+        hb, wb = rounded(hk), rounded(wk)
+        exact, scale = hb @ wb, np.abs(hb) @ np.abs(wb)
+        assert np.all(np.abs(logits[k].astype(np.float64) - exact) <= 2.0 ** -21 * d * scale), f"seed {k}: product"
+        z = O.tempered(logits[k], tau, keep=keep[k])
+        want, edges = O.sample_invcdf(z, u[k * N:(k + 1) * N])
+        assert np.all((ids[k] == want) | (edges < EDGE)), f"seed {k}: draws"
+        wl = O.token_logp(z, ids[k])
+        assert np.all(np.abs(lp[k] - wl) <= 1e-6 + 1e-5 * np.abs(wl)), f"seed {k}: logp"
+    # the scorer over the same batched head gives the sampler's log-probabilities
+    slp, _ = nr.readout_score(h, packed, tau, nr.Tensor.from_numpy(keep), nr.Tensor.from_numpy(ids), entropy=False)
+    assert slp.shape == (S, N) and slp.to_numpy().tobytes() == lp.tobytes()
+    with pytest.raises(ValueError, match="2 seeds"):
+        nr.readout_sample_logp(nr.Tensor.from_numpy(hn[0]), packed, tau, None, None,
+                               uniforms=nr.Tensor.from_numpy(u[:N], "f64"))
 
 
 def test_readout_refuses_a_row_with_no_allowed_token():

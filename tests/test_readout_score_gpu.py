@@ -21,7 +21,10 @@ pytestmark = pytest.mark.gpu
 @pytest.fixture(scope="module", autouse=True)
 def device():
     nr.claim(0)
+    # the readout fusion is the reduced-precision product: it runs at MatmulPrecision::Half
+    prev = nr.set_matmul_precision(nr.MatmulPrecision.HALF)
     yield
+    nr.set_matmul_precision(prev)
 
 
 def close(name, got, want):

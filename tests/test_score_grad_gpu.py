@@ -161,8 +161,9 @@ def test_backward_masks_temperatures_and_objectives(case):
         tok = np.where(k[np.arange(rows), tok] == 1, tok, 0).astype(np.int32)
     want_kl, want_h = "kl" in obj, "h" in obj
     g = upstream(rows, V, kl=want_kl, ent=want_h, lp="lp" in obj)
-    pol = nr.tempered_logits(xt, tau, mt)
-    ref = nr.tempered_logits(yt, tau, mt) if want_kl else None
+    # the fused (logits, τ, mask) triple: bf16 rows at τ 1 under a mask, widened exactly
+    pol = nr.Tempered(xt, tau, mt)
+    ref = nr.Tempered(yt, tau, mt) if want_kl else None
     tt = nr.Tensor.from_numpy(tok)
     gf, kl, ent = run_backward(pol, ref, tt, g, (rows,), "f32")
     gb, _, _ = run_backward(pol, ref, tt, g, (rows,), "bf16")
