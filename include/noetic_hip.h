@@ -193,7 +193,9 @@ int nt_hip_rl_sample_noalloc(const NtRlSampleArgs *a);
  *   logits[r, v] = sum_k hidden[r, k] W[k, v]          (the decoder's readout x . W,
  *                                                        src/nn/decoder.rs:272,286; linear.rs:1-3)
  * in f32 from bf16 operands on the matrix cores (the reference's half-precision product,
- * src/tensor/gpu/half_gemm.rs:1-10), then exactly nt_hip_rl_sample's draw on those logits
+ * src/tensor/gpu/half_gemm.rs:1-10; it stands for the decoder's product only when the caller's
+ * matmul precision is MatmulPrecision::Half, src/tensor/precision.rs:4-8, 59-63: at the default
+ * F32 the caller multiplies and samples the written logits), then exactly nt_hip_rl_sample's draw on those logits
  * (tempered by the temperature, the u8 keep-mask applied; one uniform per row; temperature 0 is
  * the first argmax). The weight is packed once, when loaded, into the order the matrix cores
  * read it (nt_hip_rl_readout_pack_weight, from the reference's [d, V] layout or a [V, d] one).
