@@ -41,6 +41,8 @@ extern "C" {
 /* ---- dtypes and mask kinds ------------------------------------------------------------ */
 #define NT_F32 0  /* f32 logits */
 #define NT_BF16 1 /* bf16 logits, stored as their bit patterns (src/tensor/half.rs:10-12) */
+#define NT_F16 2  /* f16 logits, IEEE binary16 bit patterns (src/tensor/half.rs:40-70), widened
+                     exactly as the reference computes 16-bit values in f32 (float.rs:43-58) */
 
 #define NT_MASK_NONE 0 /* no vocabulary mask */
 #define NT_MASK_U8 1   /* u8 keep-mask: 0 excludes the token, any other value keeps it. An excluded
@@ -50,6 +52,19 @@ extern "C" {
                           reference's additive masks do) */
 #define NT_MASK_F32 2  /* additive f32 mask (0, -inf, -1e9, any value), added after the divide
                           by the temperature: rl.rs:475-486 `logits / temperature + mask` */
+
+/* A mask of the logits' rank that broadcasts over any of the leading dimensions (rl.rs:477-483:
+ * each mask dimension equals the logits' or is 1). The logits rows are (s, b, t) positions, t
+ * fastest: row r = (s B + b) T + t with T = t_rows and B = b_rows, and it reads the mask row that
+ * starts at element s ld_s + b ld_b + t mask_ld (mask_ld being the args' own field). All zero (the
+ * default) is one group, T = rows and B = 1: row r reads the mask at r mask_ld. Each stride is 0
+ * (a broadcast dimension) or at least vocab; rows must be a multiple of T B. A logits tensor of
+ * any rank folds its leading dimensions into these three: adjacent dimensions that are both
+ * broadcast, or both read contiguously, merge. */
+typedef struct NtMaskRows {
+    int64_t t_rows, b_rows; /* T and B; 0 and 0 = one group of all rows */
+    int64_t ld_b, ld_s;     /* mask elements between consecutive b and s (0 = broadcast) */
+} NtMaskRows;
 
 /* ---- per-row status ------------------------------------------------------------------- */
 #define NT_ROW_OK 0
@@ -115,7 +130,7 @@ int nt_hip_kernel_path(void);
 /* ===================================================================== nn::rl fused rows
  * Logits are row-major [rows, V] (rows = S*B*T of `[S, B, T, V]`, rl.rs:8-14) with row stride
  * `ld` elements (ld >= V). A row is one (s, b, t) position. The float arithmetic is f32 with
- * bf16 inputs converted exactly (float.rs:61-67); per-row scalars are combined in f64. */
+ * bf16 and f16 inputs converted exactly (float.rs:43-67); per-row scalars are combined in f64. */
 
 /* Gumbel-max categorical sample of each row: the reference's own sampler,
  *   ids = sample_categorical(logits, temperature, mask, rng)        (rl.rs:488-529)
@@ -131,12 +146,12 @@ int nt_hip_kernel_path(void);
  * rand_chacha's set_word_pos) when temperature > 0. Temperature 0 is greedy: the first argmax
  * of the masked logits, no draws. */
 typedef struct NtRlGumbelArgs {
-    const void *logits;       /* [rows, ld] f32 or bf16 */
-    int32_t dtype;            /* NT_F32 | NT_BF16 */
+    const void *logits;       /* [rows, ld] f32, bf16 or f16 */
+    int32_t dtype;            /* NT_F32 | NT_BF16 | NT_F16 */
     int32_t mask_kind;        /* NT_MASK_* */
     int64_t rows, vocab, ld;
-    const void *mask;         /* u8 or f32 [rows or 1, mask_ld]; NULL with NT_MASK_NONE */
-    int64_t mask_ld;          /* mask row stride; 0 = one row shared by every logits row */
+    const void *mask;         /* u8 or f32 rows of vocab entries; NULL with NT_MASK_NONE */
+    int64_t mask_ld;          /* mask row stride (over t, see NtMaskRows); 0 = one row shared */
     double temperature;       /* >= 0 and finite; 0 = greedy */
     uint32_t key[8];          /* the stream's ChaCha20 key (its 32-byte seed as little-endian words) */
     uint64_t block;           /* the stream's position: its next u64 starts at word `word` of */
@@ -144,6 +159,7 @@ typedef struct NtRlGumbelArgs {
     int32_t pad0;
     int32_t *ids;             /* [rows] out: the sampled token (-1 on a refused row) */
     uint8_t *status;          /* [rows] out: NT_ROW_OK, NT_ROW_NO_TOKEN or NT_ROW_NAN (required) */
+    NtMaskRows mask_rows;     /* a mask broadcast over leading dimensions (zero: rows of mask_ld) */
 } NtRlGumbelArgs;
 int nt_hip_rl_sample_gumbel(const NtRlGumbelArgs *a);
 
@@ -160,18 +176,19 @@ int nt_hip_rl_sample_gumbel(const NtRlGumbelArgs *a);
  * of the masked logits (rl.rs:510-513), no uniform read; logp/entropy are then those of the
  * temperature-1 distribution (rl.rs:514). */
 typedef struct NtRlSampleArgs {
-    const void *logits;       /* [rows, ld] f32 or bf16 */
-    int32_t dtype;            /* NT_F32 | NT_BF16 */
+    const void *logits;       /* [rows, ld] f32, bf16 or f16 */
+    int32_t dtype;            /* NT_F32 | NT_BF16 | NT_F16 */
     int32_t mask_kind;        /* NT_MASK_* */
     int64_t rows, vocab, ld;
-    const void *mask;         /* u8 or f32 [rows or 1, mask_ld]; NULL with NT_MASK_NONE */
-    int64_t mask_ld;          /* mask row stride; 0 = one row shared by every logits row */
+    const void *mask;         /* u8 or f32 rows of vocab entries; NULL with NT_MASK_NONE */
+    int64_t mask_ld;          /* mask row stride (over t, see NtMaskRows); 0 = one row shared */
     double temperature;       /* >= 0 and finite; 0 = greedy */
     const double *uniforms;   /* [rows] device, each in (0,1); unused when greedy */
     int32_t *ids;             /* [rows] out: the sampled token (-1 on a refused row) */
     float *logp;              /* [rows] out or NULL */
     float *entropy;           /* [rows] out or NULL */
     uint8_t *status;          /* [rows] out: NT_ROW_* (required) */
+    NtMaskRows mask_rows;     /* a mask broadcast over leading dimensions (zero: rows of mask_ld) */
 } NtRlSampleArgs;
 int nt_hip_rl_sample(const NtRlSampleArgs *a);
 
@@ -276,7 +293,7 @@ int nt_hip_rl_readout_score(const NtRlReadoutScoreArgs *a);
 typedef struct NtRlScoreArgs {
     const void *logits;       /* [rows, ld] policy logits */
     const void *ref_logits;   /* [rows, ld] reference logits or NULL (no ref_logp / kl) */
-    int32_t dtype;            /* NT_F32 | NT_BF16 (both inputs) */
+    int32_t dtype;            /* NT_F32 | NT_BF16 | NT_F16 (both inputs) */
     int32_t mask_kind;
     int64_t rows, vocab, ld;
     const void *mask;
@@ -296,6 +313,7 @@ typedef struct NtRlScoreArgs {
     float *lse_rest;          /* [rows] out or NULL (policy) */
     float *ref_lse_base;      /* [rows] out or NULL (reference; needs ref_logits) */
     float *ref_lse_rest;      /* [rows] out or NULL (reference) */
+    NtMaskRows mask_rows;     /* a mask broadcast over leading dimensions (zero: rows of mask_ld) */
 } NtRlScoreArgs;
 int nt_hip_rl_score(const NtRlScoreArgs *a);
 
@@ -316,7 +334,7 @@ int nt_hip_rl_score(const NtRlScoreArgs *a);
  * reference stores a bf16 tensor's gradient), row stride grad_ld. One pass reads each logit
  * (and reference logit) once and writes each gradient element once. */
 typedef struct NtRlScoreGradArgs {
-    const void *logits;       /* [rows, ld] policy logits (NT_F32 | NT_BF16) */
+    const void *logits;       /* [rows, ld] policy logits (NT_F32 | NT_BF16 | NT_F16) */
     const void *ref_logits;   /* [rows, ld] reference logits; needed when g_kl is given */
     int32_t dtype;
     int32_t mask_kind;
@@ -336,6 +354,7 @@ typedef struct NtRlScoreGradArgs {
     int32_t grad_dtype;       /* NT_F32 | NT_BF16 */
     int32_t pad0;
     int64_t grad_ld;
+    NtMaskRows mask_rows;     /* the forward's */
 } NtRlScoreGradArgs;
 int nt_hip_rl_score_backward(const NtRlScoreGradArgs *a);
 

@@ -58,6 +58,33 @@ struct Elem<NT_BF16> {
     static constexpr uint32_t kNegInf = 0xff80ff80u;
     static constexpr int kBytes = 2;
 };
+template <>
+struct Elem<NT_F16> {
+    static constexpr int kWords = 4;     // 8 f16 packed two per word
+    static constexpr uint32_t kNegInf = 0xfc00fc00u;
+    static constexpr int kBytes = 2;
+};
+
+// A 16-bit logit (the low half of h) as f32, exactly: bf16 is f32's top half; f16 converts
+// with v_cvt_f32_f16, exact for every f16 value (subnormals, infinities and NaNs included).
+template <int DT>
+__device__ __forceinline__ float widen16(uint32_t h) {
+    if constexpr (DT == NT_BF16) return __uint_as_float(h << 16);
+    else return float(__builtin_bit_cast(_Float16, uint16_t(h)));
+}
+
+// The mask row a logits row reads (NtMaskRows): row = (s B + b) T + t reads the mask row at
+// element s ld_s + b ld_b + t ld. The host sets T = rows and B = 1 for rows of stride ld.
+struct MaskMap {
+    int64_t ld, ld_b, ld_s;
+    uint32_t T, B;
+};
+__device__ __forceinline__ int64_t mask_row_at(const MaskMap &m, int64_t row) {
+    const uint32_t r = uint32_t(row);
+    const uint32_t q = r / m.T, t = r - q * m.T;
+    const uint32_t s = q / m.B, b = q - s * m.B;
+    return int64_t(s) * m.ld_s + int64_t(b) * m.ld_b + int64_t(t) * m.ld;
+}
 
 template <int MK>
 struct MaskWords {
@@ -113,7 +140,7 @@ __device__ __forceinline__ void load_raw(Raw<DT, MK> &r, const void *xrow, const
             if constexpr (DT == NT_F32) {
                 r.x[j] = in ? __float_as_uint(static_cast<const float *>(xrow)[e]) : Elem<DT>::kNegInf;
             } else {
-                uint32_t h = in ? uint32_t(static_cast<const uint16_t *>(xrow)[e]) : 0xff80u;
+                uint32_t h = in ? uint32_t(static_cast<const uint16_t *>(xrow)[e]) : (Elem<DT>::kNegInf & 0xffffu);
                 if (j % 2 == 0) r.x[j / 2] = h;
                 else r.x[j / 2] |= h << 16;
             }
@@ -154,11 +181,12 @@ __device__ __forceinline__ void load_raw_inbounds(Raw<DT, MK> &r, const void *xr
     }
 }
 
-// Logit j of a lane's chunk as f32 (bf16 widened exactly).
+// Logit j of a lane's chunk as f32 (bf16 and f16 widened exactly).
 template <int DT>
 __device__ __forceinline__ float logit(const uint32_t *x, int j) {
     if constexpr (DT == NT_F32) return __uint_as_float(x[j]);
-    else return __uint_as_float((j % 2 == 0) ? (x[j / 2] << 16) : (x[j / 2] & 0xffff0000u));
+    else if constexpr (DT == NT_BF16) return __uint_as_float((j % 2 == 0) ? (x[j / 2] << 16) : (x[j / 2] & 0xffff0000u));
+    else return widen16<DT>((j % 2 == 0) ? (x[j / 2] & 0xffffu) : (x[j / 2] >> 16));
 }
 
 // The "value" of an element, the quantity the kernels take maxima and exponentials of.
@@ -211,8 +239,12 @@ __device__ __forceinline__ void fold_values(uint32_t *x, const float v[kEpl]) {
     for (int j = 0; j < kEpl; j++) {
         if constexpr (DT == NT_F32) {
             x[j] = __float_as_uint(v[j]);
+        } else if constexpr (DT == NT_BF16) {
+            if (j % 2 == 1) x[j / 2] = (__float_as_uint(v[j]) & 0xffff0000u) | (__float_as_uint(v[j - 1]) >> 16);
         } else if (j % 2 == 1) {
-            x[j / 2] = (__float_as_uint(v[j]) & 0xffff0000u) | (__float_as_uint(v[j - 1]) >> 16);
+            // f16: each value is a widened f16 or -inf, so the narrowing is exact in any rounding
+            x[j / 2] = uint32_t(__builtin_bit_cast(uint16_t, _Float16(v[j - 1]))) |
+                       (uint32_t(__builtin_bit_cast(uint16_t, _Float16(v[j]))) << 16);
         }
     }
 }
@@ -521,7 +553,8 @@ __device__ __forceinline__ float tree_sum(const float *w) {
 struct SampleP {
     const void *logits;
     const void *mask;
-    int64_t V, ld, mask_ld;
+    int64_t V, ld;
+    MaskMap mm;       // the mask row of each logits row
     float c;          // exponent scale: log2(e)/T (no/u8 mask) or log2(e) (f32 mask)
     float tau;        // (float)T, the reference's divisor (float.rs:494-499)
     int tau_one;      // T == 1 (or greedy): no divide
@@ -540,7 +573,7 @@ struct SampleP {
 inline int check_rows(int64_t rows, int64_t V, int64_t ld, int32_t dtype, int32_t mk, const void *mask, int64_t mask_ld,
                const char *who) {
     char buf[256];
-    if (rows < 0 || V < 1 || ld < V || (dtype != NT_F32 && dtype != NT_BF16) || mk < NT_MASK_NONE ||
+    if (rows < 0 || V < 1 || ld < V || (dtype != NT_F32 && dtype != NT_BF16 && dtype != NT_F16) || mk < NT_MASK_NONE ||
         mk > NT_MASK_F32 || ((mk == NT_MASK_NONE) != (mask == nullptr)) || (mask_ld != 0 && mask_ld < V) ||
         rows > 0x7fffffffLL) {
         std::snprintf(buf, sizeof buf,
@@ -552,11 +585,38 @@ inline int check_rows(int64_t rows, int64_t V, int64_t ld, int32_t dtype, int32_
     return 0;
 }
 
-inline bool aligned_rows(const void *x, int64_t V, int64_t ld, int32_t dtype, int32_t mk, const void *mask, int64_t mask_ld) {
+// The mask map of a call (NtMaskRows, validated): all zero is T = rows, B = 1 (rows of mask_ld).
+inline int mask_map(const NtMaskRows &mr, int64_t rows, int64_t V, int32_t mk, int64_t mask_ld, const char *who,
+                    MaskMap *out) {
+    MaskMap m{mask_ld, 0, 0, uint32_t(rows > 0 ? rows : 1), 1u};
+    const bool dflt = mr.t_rows == 0 && mr.b_rows == 0 && mr.ld_b == 0 && mr.ld_s == 0;
+    if (mk != NT_MASK_NONE && !dflt) {
+        const int64_t T = mr.t_rows, B = mr.b_rows;
+        const bool ok = T >= 1 && B >= 1 && T <= 0x7fffffffLL && B <= 0x7fffffffLL &&
+                        (rows == 0 || rows % (T * B) == 0) && (mr.ld_b == 0 || mr.ld_b >= V) &&
+                        (mr.ld_s == 0 || mr.ld_s >= V);
+        if (!ok) {
+            char buf[256];
+            std::snprintf(buf, sizeof buf,
+                          "%s: mask rows T %lld, B %lld, ld_b %lld, ld_s %lld for %lld rows of %lld (rows a multiple "
+                          "of T B; strides 0 or at least vocab)",
+                          who, (long long)T, (long long)B, (long long)mr.ld_b, (long long)mr.ld_s, (long long)rows,
+                          (long long)V);
+            return fail(NT_E_ARG, buf);
+        }
+        m = MaskMap{mask_ld, mr.ld_b, mr.ld_s, uint32_t(T), uint32_t(B)};
+    }
+    *out = m;
+    return 0;
+}
+
+inline bool aligned_rows(const void *x, int64_t V, int64_t ld, int32_t dtype, int32_t mk, const void *mask,
+                         const MaskMap &mm) {
     if (V % kEpl != 0 || ld % kEpl != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0) return false;
     (void)dtype;
-    if (mk == NT_MASK_U8) return mask_ld % 8 == 0 && reinterpret_cast<uintptr_t>(mask) % 8 == 0;
-    if (mk == NT_MASK_F32) return mask_ld % 4 == 0 && reinterpret_cast<uintptr_t>(mask) % 16 == 0;
+    const auto strides = [&](int64_t u) { return mm.ld % u == 0 && mm.ld_b % u == 0 && mm.ld_s % u == 0; };
+    if (mk == NT_MASK_U8) return strides(8) && reinterpret_cast<uintptr_t>(mask) % 8 == 0;
+    if (mk == NT_MASK_F32) return strides(4) && reinterpret_cast<uintptr_t>(mask) % 16 == 0;
     return true;
 }
 #endif

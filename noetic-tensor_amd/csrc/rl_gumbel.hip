@@ -67,7 +67,7 @@ using namespace nt;
 extern "C" int nt_hip_rl_sample_gumbel(const NtRlGumbelArgs *a) {
     if (!a) return fail(NT_E_ARG, "nt_hip_rl_sample_gumbel: null args");
     const int64_t rows = a->rows, V = a->vocab;
-    if (rows < 0 || V < 1 || a->ld < V || (a->dtype != NT_F32 && a->dtype != NT_BF16) ||
+    if (rows < 0 || V < 1 || a->ld < V || (a->dtype != NT_F32 && a->dtype != NT_BF16 && a->dtype != NT_F16) ||
         a->mask_kind < NT_MASK_NONE || a->mask_kind > NT_MASK_F32 ||
         ((a->mask_kind == NT_MASK_NONE) != (a->mask == nullptr)) || (a->mask_ld != 0 && a->mask_ld < V) ||
         rows > 0x7fffffffLL || V > 0x7fffffffLL || a->word < 0 || a->word > 15)
@@ -78,6 +78,8 @@ extern "C" int nt_hip_rl_sample_gumbel(const NtRlGumbelArgs *a) {
         return fail(NT_E_ARG, "sample_categorical: temperature " + std::to_string(a->temperature) + " (must be ≥ 0)");
     if (!a->logits || !a->ids || !a->status)
         return fail(NT_E_ARG, "nt_hip_rl_sample_gumbel: null logits, ids or status");
+    MaskMap mm;
+    if (int rc = mask_map(a->mask_rows, rows, V, a->mask_kind, a->mask_ld, "nt_hip_rl_sample_gumbel", &mm)) return rc;
     // The stream's block counter is 64-bit: the draws of this call must not wrap it.
     const uint64_t words = 2 * uint64_t(rows) * uint64_t(V);
     if (a->block > (~uint64_t(0) >> 5) || words > (uint64_t(1) << 62))
@@ -91,7 +93,7 @@ extern "C" int nt_hip_rl_sample_gumbel(const NtRlGumbelArgs *a) {
     p.mask = a->mask;
     p.V = V;
     p.ld = a->ld;
-    p.mask_ld = a->mask_ld;
+    p.mm = mm;
     const double T = greedy ? 1.0 : a->temperature;
     p.tau = float(T);  // the reference divides by `temperature as f32` (float.rs:494-499)
     p.tau_one = T == 1.0;
@@ -108,7 +110,9 @@ extern "C" int nt_hip_rl_sample_gumbel(const NtRlGumbelArgs *a) {
     const int esz = a->dtype == NT_F32 ? 4 : 2, msz = a->mask_kind == NT_MASK_F32 ? 4 : 1;
     const bool mask_vec = a->mask_kind == NT_MASK_NONE ||
                           (reinterpret_cast<uintptr_t>(a->mask) % (a->mask_kind == NT_MASK_F32 ? 16 : 8) == 0 &&
-                           (a->mask_ld * msz) % (a->mask_kind == NT_MASK_F32 ? 16 : 8) == 0);
+                           (mm.ld * msz) % (a->mask_kind == NT_MASK_F32 ? 16 : 8) == 0 &&
+                           (mm.ld_b * msz) % (a->mask_kind == NT_MASK_F32 ? 16 : 8) == 0 &&
+                           (mm.ld_s * msz) % (a->mask_kind == NT_MASK_F32 ? 16 : 8) == 0);
     p.vec = reinterpret_cast<uintptr_t>(a->logits) % 16 == 0 && (a->ld * esz) % 16 == 0 && mask_vec && V % 8 == 0 &&
             V * 4 <= int64_t(0x7fffffff);
     // Threads per row: one per keystream block of the row, in whole waves, at most 1024.
@@ -118,6 +122,7 @@ extern "C" int nt_hip_rl_sample_gumbel(const NtRlGumbelArgs *a) {
     hipStream_t s = ctx().stream;
     rtc_status() = 0;
     if (a->dtype == NT_F32) pick_gumbel_mk<NT_F32>(a->mask_kind, odd, greedy, p, rows, threads, s);
-    else pick_gumbel_mk<NT_BF16>(a->mask_kind, odd, greedy, p, rows, threads, s);
+    else if (a->dtype == NT_BF16) pick_gumbel_mk<NT_BF16>(a->mask_kind, odd, greedy, p, rows, threads, s);
+    else pick_gumbel_mk<NT_F16>(a->mask_kind, odd, greedy, p, rows, threads, s);
     return rtc_status() ? rtc_status() : launched("nt_hip_rl_sample_gumbel");
 }

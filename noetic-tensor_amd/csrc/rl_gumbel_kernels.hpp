@@ -16,7 +16,8 @@ constexpr int kGumbelMaxThreads = 1024;
 struct GumbelP {
     const void *logits;
     const void *mask;
-    int64_t V, ld, mask_ld;
+    int64_t V, ld;
+    MaskMap mm;  // the mask row of each logits row
     float tau;
     int tau_one;
     ChachaKey key;
@@ -29,19 +30,20 @@ struct GumbelP {
 // z_v = tempered_logits (rl.rs:475-486) in f32: x / tau (skipped at tau == 1), then the
 // additive f32 mask, or -inf at a token a u8 keep-mask excludes. Without DIV the division is
 // left to the caller (with a u8 mask or none it commutes with the exclusion: -inf / tau = -inf).
+// moff: the row's mask row (mask_row_at).
 template <int DT, int MK, bool DIV = true>
-__device__ __forceinline__ float tempered_at(const GumbelP &p, int64_t row, int64_t v) {
+__device__ __forceinline__ float tempered_at(const GumbelP &p, int64_t row, int64_t moff, int64_t v) {
     float x;
     if constexpr (DT == NT_F32) {
         x = static_cast<const float *>(p.logits)[row * p.ld + v];
     } else {
-        x = __uint_as_float(uint32_t(static_cast<const uint16_t *>(p.logits)[row * p.ld + v]) << 16);
+        x = widen16<DT>(uint32_t(static_cast<const uint16_t *>(p.logits)[row * p.ld + v]));
     }
     if (DIV && !p.tau_one) x = x / p.tau;
     if constexpr (MK == NT_MASK_U8) {
-        if (static_cast<const uint8_t *>(p.mask)[row * p.mask_ld + v] == 0) x = -INFINITY;
+        if (static_cast<const uint8_t *>(p.mask)[moff + v] == 0) x = -INFINITY;
     } else if constexpr (MK == NT_MASK_F32) {
-        x = x + static_cast<const float *>(p.mask)[row * p.mask_ld + v];
+        x = x + static_cast<const float *>(p.mask)[moff + v];
     }
     return x;
 }
@@ -102,8 +104,7 @@ __device__ __forceinline__ void gumbel_values(const GumbelRaw<DT, MK> &r, const 
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         float x;
-        if constexpr (DT == NT_F32) x = __uint_as_float(r.x[j]);
-        else x = __uint_as_float((j & 1) ? (r.x[j / 2] & 0xffff0000u) : (r.x[j / 2] << 16));
+        x = logit<DT>(r.x, j);
         if (DIV && !p.tau_one) x = x / p.tau;
         if constexpr (MK == NT_MASK_U8) {
             if (((r.m[j / 4] >> (8 * (j % 4))) & 0xffu) == 0) x = -INFINITY;
@@ -176,6 +177,7 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
     int *const gqb = gdyn;
     float *const gqz = reinterpret_cast<float *>(gdyn + (blockDim.x / 64) * kGumbelQueue);
     const int64_t row = blockIdx.x;
+    const int64_t moff = MK != NT_MASK_NONE ? mask_row_at(p.mm, row) : 0;  // the row's mask row
     const int64_t V = p.V;
     // Pair q = h + row V + v holds element v's u64; block q >> 3, pair q & 7 of it.
     const uint64_t q0 = p.h + uint64_t(row) * uint64_t(V);
@@ -275,7 +277,7 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
             __amdgpu_buffer_rsrc_t mres = xres;
             if constexpr (MK != NT_MASK_NONE)
                 mres = __builtin_amdgcn_make_buffer_rsrc(
-                    const_cast<char *>(static_cast<const char *>(p.mask) + row * p.mask_ld * (MK == NT_MASK_F32 ? 4 : 1)),
+                    const_cast<char *>(static_cast<const char *>(p.mask) + moff * (MK == NT_MASK_F32 ? 4 : 1)),
                     short(0), int(V * (MK == NT_MASK_F32 ? 4 : 1)), kBufferWord3);
             GumbelRaw<DT, MK> cur, nxt;
             if constexpr (COMPACT) {
@@ -322,7 +324,7 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
                     const int64_t v = v0 + j;
-                    z[j] = (v >= 0 && v < V) ? tempered_at<DT, MK, !DEFER>(p, row, v) : -INFINITY;
+                    z[j] = (v >= 0 && v < V) ? tempered_at<DT, MK, !DEFER>(p, row, moff, v) : -INFINITY;
                 }
             });
         } else {
@@ -333,7 +335,7 @@ __global__ __launch_bounds__(kGumbelMaxThreads) void k_sample_gumbel(GumbelP p) 
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
                     const int64_t v = v0 + j;
-                    z[j] = (v >= 0 && v < V) ? tempered_at<DT, MK>(p, row, v) : -INFINITY;
+                    z[j] = (v >= 0 && v < V) ? tempered_at<DT, MK>(p, row, moff, v) : -INFINITY;
                     if (z[j] != z[j]) flags |= 2;
                     any |= z[j] > -INFINITY;
                 }

@@ -307,6 +307,8 @@ int nt_hip_rl_score(const NtRlScoreArgs *a) {
     if (!a) return fail(NT_E_ARG, "nt_hip_rl_score: null args");
     if (int rc = check_rows(a->rows, a->vocab, a->ld, a->dtype, a->mask_kind, a->mask, a->mask_ld, "nt_hip_rl_score"))
         return rc;
+    MaskMap mm;
+    if (int rc = mask_map(a->mask_rows, a->rows, a->vocab, a->mask_kind, a->mask_ld, "nt_hip_rl_score", &mm)) return rc;
     if (!(a->temperature > 0.0) || !std::isfinite(a->temperature))
         return fail(NT_E_ARG, "tempered_logits: temperature " + std::to_string(a->temperature) + " (must be positive)");
     if (!a->logits) return fail(NT_E_ARG, "nt_hip_rl_score: null logits");
@@ -323,7 +325,7 @@ int nt_hip_rl_score(const NtRlScoreArgs *a) {
     p.mask = a->mask;
     p.V = a->vocab;
     p.ld = a->ld;
-    p.mask_ld = a->mask_ld;
+    p.mm = mm;
     p.tau = float(a->temperature);
     p.tau_one = (a->temperature == 1.0);
     p.c = (a->mask_kind == NT_MASK_F32 || p.tau_one) ? kLog2e : float(double(kLog2e) / double(p.tau));
@@ -342,13 +344,14 @@ int nt_hip_rl_score(const NtRlScoreArgs *a) {
     const bool kl = a->kl != nullptr;
     const bool ent = a->entropy != nullptr;
     // the aligned path addresses a row's bytes with 32-bit buffer offsets
-    bool al = aligned_rows(a->logits, a->vocab, a->ld, a->dtype, a->mask_kind, a->mask, a->mask_ld) &&
+    bool al = aligned_rows(a->logits, a->vocab, a->ld, a->dtype, a->mask_kind, a->mask, mm) &&
               a->vocab * 4 <= int64_t(0x7fffffff);
     if (ref) al = al && reinterpret_cast<uintptr_t>(a->ref_logits) % 16 == 0;
     hipStream_t s = ctx().stream;
     rtc_status() = 0;
     if (a->dtype == NT_F32) pick_mk_score<NT_F32>(a->mask_kind, ref, kl, ent, al, p, a->rows, s);
-    else pick_mk_score<NT_BF16>(a->mask_kind, ref, kl, ent, al, p, a->rows, s);
+    else if (a->dtype == NT_BF16) pick_mk_score<NT_BF16>(a->mask_kind, ref, kl, ent, al, p, a->rows, s);
+    else pick_mk_score<NT_F16>(a->mask_kind, ref, kl, ent, al, p, a->rows, s);
     return rtc_status() ? rtc_status() : launched("nt_hip_rl_score");
 }
 
@@ -356,6 +359,9 @@ int nt_hip_rl_score_backward(const NtRlScoreGradArgs *a) {
     if (!a) return fail(NT_E_ARG, "nt_hip_rl_score_backward: null args");
     if (int rc = check_rows(a->rows, a->vocab, a->ld, a->dtype, a->mask_kind, a->mask, a->mask_ld,
                             "nt_hip_rl_score_backward"))
+        return rc;
+    MaskMap mm;
+    if (int rc = mask_map(a->mask_rows, a->rows, a->vocab, a->mask_kind, a->mask_ld, "nt_hip_rl_score_backward", &mm))
         return rc;
     if (!(a->temperature > 0.0) || !std::isfinite(a->temperature))
         return fail(NT_E_ARG, "tempered_logits: temperature " + std::to_string(a->temperature) + " (must be positive)");
@@ -377,7 +383,7 @@ int nt_hip_rl_score_backward(const NtRlScoreGradArgs *a) {
     p.mask = a->mask;
     p.V = a->vocab;
     p.ld = a->ld;
-    p.mask_ld = a->mask_ld;
+    p.mm = mm;
     p.gld = a->grad_ld;
     p.tau = float(a->temperature);
     p.tau_one = a->temperature == 1.0;
@@ -394,7 +400,7 @@ int nt_hip_rl_score_backward(const NtRlScoreGradArgs *a) {
     p.grad = a->grad;
     const bool kl = a->g_kl != nullptr;
     // the buffer-resource path addresses a row's bytes with 32-bit offsets
-    bool al = aligned_rows(a->logits, a->vocab, a->ld, a->dtype, a->mask_kind, a->mask, a->mask_ld) &&
+    bool al = aligned_rows(a->logits, a->vocab, a->ld, a->dtype, a->mask_kind, a->mask, mm) &&
               reinterpret_cast<uintptr_t>(a->grad) % 16 == 0 && a->grad_ld % kEpl == 0 &&
               a->vocab * 4 <= int64_t(0x7fffffff);
     if (kl) al = al && reinterpret_cast<uintptr_t>(a->ref_logits) % 16 == 0;
@@ -427,7 +433,8 @@ int nt_hip_rl_score_backward(const NtRlScoreGradArgs *a) {
     };
     rtc_status() = 0;
     if (a->dtype == NT_F32) by_mk(std::integral_constant<int, NT_F32>{});
-    else by_mk(std::integral_constant<int, NT_BF16>{});
+    else if (a->dtype == NT_BF16) by_mk(std::integral_constant<int, NT_BF16>{});
+    else by_mk(std::integral_constant<int, NT_F16>{});
     return rtc_status() ? rtc_status() : launched("nt_hip_rl_score_backward");
 }
 

@@ -48,7 +48,7 @@ void pick_mk_sample(int mk, bool ent, bool al, const SampleP &p, int64_t rows, i
 // Unmasked f32 rows stop at 4 chunks per wave: at 8 the kernel needs more than 128 registers and
 // spills, and segments or the streaming kernel measured faster for those rows at every row count.
 int rr_kmax(int dtype, int mk, int epl) {
-    int k = (dtype == NT_BF16 ? 128 : 64) / epl;
+    int k = (dtype != NT_F32 ? 128 : 64) / epl;
     if (mk == NT_MASK_F32) k = k < 32 / epl ? k : 32 / epl;  // 16 waves * K * 256 EPL bytes <= 128 KiB
     if (dtype == NT_F32 && mk == NT_MASK_NONE) k = k < 32 / epl ? k : 32 / epl;
     return k;
@@ -78,7 +78,7 @@ void launch_rr_k(bool ent, bool allw, const SampleP &p, int64_t rows, hipStream_
 // K is a power of two up to rr_kmax(DT, MK, EPL); the instantiations are exactly those.
 template <int DT, int MK, int EPL>
 void launch_rr_mk(int K, bool ent, bool allw, const SampleP &p, int64_t rows, hipStream_t s) {
-    constexpr int KREG = (DT == NT_BF16 ? 128 : 64) / EPL;
+    constexpr int KREG = (DT != NT_F32 ? 128 : 64) / EPL;
     constexpr int KMAX = (MK == NT_MASK_F32 || (DT == NT_F32 && MK == NT_MASK_NONE)) && 32 / EPL < KREG ? 32 / EPL : KREG;
     switch (K) {
         case 1: launch_rr_k<DT, MK, 1, EPL>(ent, allw, p, rows, s); break;
@@ -96,10 +96,14 @@ void launch_rr(int dtype, int mk, int K, bool ent, bool allw, const SampleP &p, 
         if (mk == NT_MASK_U8) launch_rr_mk<NT_F32, NT_MASK_U8, EPL>(K, ent, allw, p, rows, s);
         else if (mk == NT_MASK_F32) launch_rr_mk<NT_F32, NT_MASK_F32, EPL>(K, ent, allw, p, rows, s);
         else launch_rr_mk<NT_F32, NT_MASK_NONE, EPL>(K, ent, allw, p, rows, s);
-    } else {
+    } else if (dtype == NT_BF16) {
         if (mk == NT_MASK_U8) launch_rr_mk<NT_BF16, NT_MASK_U8, EPL>(K, ent, allw, p, rows, s);
         else if (mk == NT_MASK_F32) launch_rr_mk<NT_BF16, NT_MASK_F32, EPL>(K, ent, allw, p, rows, s);
         else launch_rr_mk<NT_BF16, NT_MASK_NONE, EPL>(K, ent, allw, p, rows, s);
+    } else {
+        if (mk == NT_MASK_U8) launch_rr_mk<NT_F16, NT_MASK_U8, EPL>(K, ent, allw, p, rows, s);
+        else if (mk == NT_MASK_F32) launch_rr_mk<NT_F16, NT_MASK_F32, EPL>(K, ent, allw, p, rows, s);
+        else launch_rr_mk<NT_F16, NT_MASK_NONE, EPL>(K, ent, allw, p, rows, s);
     }
 }
 
@@ -118,10 +122,14 @@ void launch_rq(int dtype, int K, bool ent, const SampleP &p, int64_t rows, hipSt
     if (dtype == NT_F32) {
         if (K == 4) launch_rq_k<NT_F32, 4>(ent, p, rows, s);
         else launch_rq_k<NT_F32, 8>(ent, p, rows, s);
-    } else {
+    } else if (dtype == NT_BF16) {
         if (K == 4) launch_rq_k<NT_BF16, 4>(ent, p, rows, s);
         else if (K == 8) launch_rq_k<NT_BF16, 8>(ent, p, rows, s);
         else launch_rq_k<NT_BF16, 16>(ent, p, rows, s);
+    } else {
+        if (K == 4) launch_rq_k<NT_F16, 4>(ent, p, rows, s);
+        else if (K == 8) launch_rq_k<NT_F16, 8>(ent, p, rows, s);
+        else launch_rq_k<NT_F16, 16>(ent, p, rows, s);
     }
 }
 
@@ -131,9 +139,10 @@ void launch_rq(int dtype, int K, bool ent, const SampleP &p, int64_t rows, hipSt
 // register-resident sampler). Measured on MI355X at 256 rows of V = 128256 bf16, tau 0.7, HBM-cold
 // inputs: a grammar mask of runs (30% kept) 20.2 -> 16.8 us, a Bernoulli(0.9) mask 20.2 -> 20.4 us
 // (its waves take the dense path); at V = 50304 f32, runs 14.6 -> 10.2 us, Bernoulli 14.6 -> 14.4 us.
-bool use_queue(int mk, int K, const void *mask, int64_t mask_ld) {
+bool use_queue(int mk, int K, const void *mask, const MaskMap &mm) {
     if (mk != NT_MASK_U8 || K < 4) return false;
-    if (reinterpret_cast<uintptr_t>(mask) % 16 != 0 || mask_ld % 16 != 0) return false;
+    if (reinterpret_cast<uintptr_t>(mask) % 16 != 0 || mm.ld % 16 != 0 || mm.ld_b % 16 != 0 || mm.ld_s % 16 != 0)
+        return false;
     const char *env = std::getenv("NOETIC_HIP_SAMPLE_QUEUE");
     return !(env && std::strcmp(env, "off") == 0);
 }
@@ -273,7 +282,7 @@ template <int DT, int MK, int NW>
 void launch_seg_nw(int k, bool ent, bool allw, const SegP &q, int64_t rows, hipStream_t s) {
     if (k == 4) launch_seg_k<DT, MK, 4, NW>(ent, allw, q, rows, s);
     else if (k == 8) launch_seg_k<DT, MK, 8, NW>(ent, allw, q, rows, s);
-    else if constexpr (DT == NT_BF16 && (MK != NT_MASK_F32 || NW * 16 <= 64))
+    else if constexpr (DT != NT_F32 && (MK != NT_MASK_F32 || NW * 16 <= 64))
         launch_seg_k<DT, MK, 16, NW>(ent, allw, q, rows, s);
 }
 
@@ -288,10 +297,14 @@ void launch_seg(int dtype, int mk, const SegShape &sh, bool ent, bool allw, cons
         if (mk == NT_MASK_U8) launch_seg_mk<NT_F32, NT_MASK_U8>(sh.nw, sh.k, ent, allw, q, rows, s);
         else if (mk == NT_MASK_F32) launch_seg_mk<NT_F32, NT_MASK_F32>(sh.nw, sh.k, ent, allw, q, rows, s);
         else launch_seg_mk<NT_F32, NT_MASK_NONE>(sh.nw, sh.k, ent, allw, q, rows, s);
-    } else {
+    } else if (dtype == NT_BF16) {
         if (mk == NT_MASK_U8) launch_seg_mk<NT_BF16, NT_MASK_U8>(sh.nw, sh.k, ent, allw, q, rows, s);
         else if (mk == NT_MASK_F32) launch_seg_mk<NT_BF16, NT_MASK_F32>(sh.nw, sh.k, ent, allw, q, rows, s);
         else launch_seg_mk<NT_BF16, NT_MASK_NONE>(sh.nw, sh.k, ent, allw, q, rows, s);
+    } else {
+        if (mk == NT_MASK_U8) launch_seg_mk<NT_F16, NT_MASK_U8>(sh.nw, sh.k, ent, allw, q, rows, s);
+        else if (mk == NT_MASK_F32) launch_seg_mk<NT_F16, NT_MASK_F32>(sh.nw, sh.k, ent, allw, q, rows, s);
+        else launch_seg_mk<NT_F16, NT_MASK_NONE>(sh.nw, sh.k, ent, allw, q, rows, s);
     }
 }
 
@@ -303,6 +316,8 @@ void launch_seg(int dtype, int mk, const SegShape &sh, bool ent, bool allw, cons
 int sample_entry(const NtRlSampleArgs *a, WorkspaceFn workspace, bool nofree, const char *who) {
     if (!a) return fail(NT_E_ARG, std::string(who) + ": null args");
     if (int rc = check_rows(a->rows, a->vocab, a->ld, a->dtype, a->mask_kind, a->mask, a->mask_ld, who)) return rc;
+    MaskMap mm;
+    if (int rc = mask_map(a->mask_rows, a->rows, a->vocab, a->mask_kind, a->mask_ld, who, &mm)) return rc;
     if (!(a->temperature >= 0.0) || !std::isfinite(a->temperature))
         return fail(NT_E_ARG, "sample_categorical: temperature " + std::to_string(a->temperature) + " (must be ≥ 0)");
     const bool greedy = a->temperature == 0.0;
@@ -320,7 +335,7 @@ int sample_entry(const NtRlSampleArgs *a, WorkspaceFn workspace, bool nofree, co
     p.mask = a->mask;
     p.V = a->vocab;
     p.ld = a->ld;
-    p.mask_ld = a->mask_ld;
+    p.mm = mm;
     const double T = greedy ? 1.0 : a->temperature;
     p.tau = float(T);
     p.tau_one = (T == 1.0);
@@ -337,7 +352,7 @@ int sample_entry(const NtRlSampleArgs *a, WorkspaceFn workspace, bool nofree, co
     int nw = int(nc / 4);
     nw = nw < 1 ? 1 : (nw > 16 ? 16 : nw);
     if (a->rows >= 2048 && nw > 4) nw = 4;
-    const bool al = aligned_rows(a->logits, a->vocab, a->ld, a->dtype, a->mask_kind, a->mask, a->mask_ld);
+    const bool al = aligned_rows(a->logits, a->vocab, a->ld, a->dtype, a->mask_kind, a->mask, mm);
     hipStream_t s = ctx().stream;
     // Aligned rows: segments when few rows each hold many chunks, else one workgroup per row when
     // the row fits its registers (chunks per wave K = 1..16); the streaming kernel takes the rest
@@ -371,14 +386,15 @@ int sample_entry(const NtRlSampleArgs *a, WorkspaceFn workspace, bool nofree, co
             while (int64_t(kRRWaves) * K < nch) K *= 2;
             p.nc = int(nch);
             rtc_status() = 0;
-            if (use_queue(a->mask_kind, K, a->mask, a->mask_ld)) launch_rq(a->dtype, K, ent, p, a->rows, s);
+            if (use_queue(a->mask_kind, K, a->mask, mm)) launch_rq(a->dtype, K, ent, p, a->rows, s);
             else launch_rr<8>(a->dtype, a->mask_kind, K, ent, all_in_flight(a->rows), p, a->rows, s);
             return rtc_status() ? rtc_status() : launched(who);
         }
     }
     rtc_status() = 0;
     if (a->dtype == NT_F32) pick_mk_sample<NT_F32>(a->mask_kind, ent, al, p, a->rows, nw * kWave, shm, s);
-    else pick_mk_sample<NT_BF16>(a->mask_kind, ent, al, p, a->rows, nw * kWave, shm, s);
+    else if (a->dtype == NT_BF16) pick_mk_sample<NT_BF16>(a->mask_kind, ent, al, p, a->rows, nw * kWave, shm, s);
+    else pick_mk_sample<NT_F16>(a->mask_kind, ent, al, p, a->rows, nw * kWave, shm, s);
     return rtc_status() ? rtc_status() : launched(who);
 }
 

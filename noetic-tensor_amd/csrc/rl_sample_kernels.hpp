@@ -26,7 +26,7 @@ __global__ __launch_bounds__(1024) void k_sample(SampleP p) {
     const bool tau_one = p.tau_one != 0;
     const void *xrow = static_cast<const char *>(p.logits) + row * p.ld * Elem<DT>::kBytes;
     const void *mrow = nullptr;
-    if constexpr (MK != NT_MASK_NONE) mrow = static_cast<const char *>(p.mask) + row * p.mask_ld * MaskWords<MK>::kBytes;
+    if constexpr (MK != NT_MASK_NONE) mrow = static_cast<const char *>(p.mask) + mask_row_at(p.mm, row) * MaskWords<MK>::kBytes;
 
     // ---- phase 1: stream the row once, per-chunk (max, sum exp[, sum exp * d]) into LDS.
     for (int c0 = wave; c0 < p.nc; c0 += nw * kBatch) {
@@ -297,7 +297,7 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
     const void *xrow = static_cast<const char *>(p.logits) + row * p.ld * Elem<DT>::kBytes;
     const uint8_t *mrow = nullptr;
     if constexpr (MK != NT_MASK_NONE)
-        mrow = static_cast<const uint8_t *>(p.mask) + row * p.mask_ld * MaskWords<MK>::kBytes;
+        mrow = static_cast<const uint8_t *>(p.mask) + mask_row_at(p.mm, row) * MaskWords<MK>::kBytes;
     const uint32_t mbase = uint32_t((uintptr_t)(lds_ptr_t)(mlds));
     // The row's uniform, read now so that its latency hides under the row's loads.
     const double u_row = p.greedy ? 0.0 : p.u[row];
@@ -716,7 +716,7 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rq(SampleP p) {
     const float c = p.c;
     const bool tau_one = p.tau_one != 0;
     const void *xrow = static_cast<const char *>(p.logits) + row * p.ld * Elem<DT>::kBytes;
-    const uint8_t *mrow = static_cast<const uint8_t *>(p.mask) + row * p.mask_ld;
+    const uint8_t *mrow = static_cast<const uint8_t *>(p.mask) + mask_row_at(p.mm, row);
     const uint32_t mbase = uint32_t((uintptr_t)(lds_ptr_t)(mlds));
     const uint32_t zaddr = uint32_t((uintptr_t)(lds_ptr_t)(zmask));
     const double u_row = p.greedy ? 0.0 : p.u[row];
@@ -1201,7 +1201,7 @@ __global__ __launch_bounds__(NW * kWave) void k_sample_seg(SegP q) {
     const void *xrow = static_cast<const char *>(p.logits) + row * p.ld * Elem<DT>::kBytes;
     const uint8_t *mrow = nullptr;
     if constexpr (MK != NT_MASK_NONE)
-        mrow = static_cast<const uint8_t *>(p.mask) + row * p.mask_ld * MaskWords<MK>::kBytes;
+        mrow = static_cast<const uint8_t *>(p.mask) + mask_row_at(p.mm, row) * MaskWords<MK>::kBytes;
     const uint32_t mbase = uint32_t((uintptr_t)(lds_ptr_t)(mlds));
     // The row's uniform, read now (every segment reads it; the one that resolves uses it).
     const double u_row = p.greedy ? 0.0 : p.u[row];

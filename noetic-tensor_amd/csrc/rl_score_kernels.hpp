@@ -18,7 +18,8 @@ struct ScoreP {
     const void *logits;
     const void *ref;
     const void *mask;
-    int64_t V, ld, mask_ld;
+    int64_t V, ld;
+    MaskMap mm;  // the mask row of each logits row
     float c;
     float tau;
     int tau_one;
@@ -150,7 +151,7 @@ __global__ __launch_bounds__(kScoreThreads) void k_score(ScoreP p) {
     const void *yrow = nullptr;
     if constexpr (REF) yrow = static_cast<const char *>(p.ref) + row * p.ld * Elem<DT>::kBytes;
     const void *mrow = nullptr;
-    if constexpr (MK != NT_MASK_NONE) mrow = static_cast<const char *>(p.mask) + row * p.mask_ld * MaskWords<MK>::kBytes;
+    if constexpr (MK != NT_MASK_NONE) mrow = static_cast<const char *>(p.mask) + mask_row_at(p.mm, row) * MaskWords<MK>::kBytes;
 
     // (used by the aligned path only, whose rows are below 2^31 bytes)
     const int Vb = AL ? int(p.V) : 0;
@@ -324,7 +325,7 @@ __global__ __launch_bounds__(kScoreThreads) void k_score(ScoreP p) {
     auto ztok = [&](const void *rowp, int64_t tok) -> float {
         float x;
         if constexpr (DT == NT_F32) x = static_cast<const float *>(rowp)[tok];
-        else x = __uint_as_float(uint32_t(static_cast<const uint16_t *>(rowp)[tok]) << 16);
+        else x = widen16<DT>(uint32_t(static_cast<const uint16_t *>(rowp)[tok]));
         float z = tau_one ? x : x / p.tau;
         if constexpr (MK == NT_MASK_U8) {
             if (static_cast<const uint8_t *>(mrow)[tok] == 0) z = -INFINITY;
@@ -374,7 +375,8 @@ __global__ __launch_bounds__(kScoreThreads) void k_score(ScoreP p) {
 
 struct GradP {
     const void *logits, *ref, *mask;
-    int64_t V, ld, mask_ld, gld;
+    int64_t V, ld, gld;
+    MaskMap mm;  // the mask row of each logits row
     float tau;
     int tau_one;
     const int32_t *tokens;
@@ -508,7 +510,7 @@ __device__ __forceinline__ void grad_row_aligned(const GradP &p, const GradRow &
             const_cast<char *>(static_cast<const char *>(p.ref) + row * p.ld * XB), short(0), V * XB, kBufferWord3);
     if constexpr (MK != NT_MASK_NONE)
         mres = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<char *>(static_cast<const char *>(p.mask) + row * p.mask_ld * MB), short(0), V * MB,
+            const_cast<char *>(static_cast<const char *>(p.mask) + mask_row_at(p.mm, row) * MB), short(0), V * MB,
             kBufferWord3);
     const auto gres = __builtin_amdgcn_make_buffer_rsrc(static_cast<char *>(p.grad) + row * p.gld * GB, short(0),
                                                         V * GB, kBufferWord3);
@@ -607,7 +609,7 @@ template <int DT, int MK, bool KL, int GDT, bool TAU1>
 __device__ __forceinline__ void grad_row_general(const GradP &p, const GradRow &g, int64_t row) {
     const char *xrow = static_cast<const char *>(p.logits) + row * p.ld * Elem<DT>::kBytes;
     const char *yrow = KL ? static_cast<const char *>(p.ref) + row * p.ld * Elem<DT>::kBytes : nullptr;
-    const char *mrow = MK != NT_MASK_NONE ? static_cast<const char *>(p.mask) + row * p.mask_ld * MaskWords<MK>::kBytes
+    const char *mrow = MK != NT_MASK_NONE ? static_cast<const char *>(p.mask) + mask_row_at(p.mm, row) * MaskWords<MK>::kBytes
                                           : nullptr;
     char *grow = static_cast<char *>(p.grad) + row * p.gld * (GDT == NT_F32 ? 4 : 2);
     for (int64_t e0 = int64_t(threadIdx.x) * kEpl; e0 < p.V; e0 += kGradStep) {

@@ -24,7 +24,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libnoetic_hip.so")
 
 # include/noetic_hip.h
-NT_F32, NT_BF16 = 0, 1
+NT_F32, NT_BF16, NT_F16 = 0, 1, 2
 NT_MASK_NONE, NT_MASK_U8, NT_MASK_F32 = 0, 1, 2
 NT_ROW_OK, NT_ROW_NO_TOKEN, NT_ROW_NAN, NT_ROW_BAD_TOKEN = 0, 1, 2, 3
 
@@ -113,12 +113,18 @@ class matmul_precision_scope:
         return False
 
 
+class NtMaskRows(C.Structure):
+    """A mask broadcast over leading dimensions: logits row (s B + b) T + t reads the mask row at
+    element s ld_s + b ld_b + t mask_ld (all zero: rows of mask_ld)."""
+    _fields_ = [("t_rows", C.c_int64), ("b_rows", C.c_int64), ("ld_b", C.c_int64), ("ld_s", C.c_int64)]
+
+
 class NtRlSampleArgs(C.Structure):
     _fields_ = [("logits", C.c_void_p), ("dtype", C.c_int32), ("mask_kind", C.c_int32),
                 ("rows", C.c_int64), ("vocab", C.c_int64), ("ld", C.c_int64),
                 ("mask", C.c_void_p), ("mask_ld", C.c_int64), ("temperature", C.c_double),
                 ("uniforms", C.c_void_p), ("ids", C.c_void_p), ("logp", C.c_void_p),
-                ("entropy", C.c_void_p), ("status", C.c_void_p)]
+                ("entropy", C.c_void_p), ("status", C.c_void_p), ("mask_rows", NtMaskRows)]
 
 
 class NtRlGumbelArgs(C.Structure):
@@ -126,7 +132,7 @@ class NtRlGumbelArgs(C.Structure):
                 ("rows", C.c_int64), ("vocab", C.c_int64), ("ld", C.c_int64),
                 ("mask", C.c_void_p), ("mask_ld", C.c_int64), ("temperature", C.c_double),
                 ("key", C.c_uint32 * 8), ("block", C.c_uint64), ("word", C.c_int32), ("pad0", C.c_int32),
-                ("ids", C.c_void_p), ("status", C.c_void_p)]
+                ("ids", C.c_void_p), ("status", C.c_void_p), ("mask_rows", NtMaskRows)]
 
 
 class NtRlReadoutSampleArgs(C.Structure):
@@ -152,7 +158,7 @@ class NtRlScoreArgs(C.Structure):
                 ("tokens", C.c_void_p), ("logp", C.c_void_p), ("ref_logp", C.c_void_p),
                 ("kl", C.c_void_p), ("entropy", C.c_void_p), ("status", C.c_void_p),
                 ("lse_base", C.c_void_p), ("lse_rest", C.c_void_p), ("ref_lse_base", C.c_void_p),
-                ("ref_lse_rest", C.c_void_p)]
+                ("ref_lse_rest", C.c_void_p), ("mask_rows", NtMaskRows)]
 
 
 class NtRlScoreGradArgs(C.Structure):
@@ -162,7 +168,8 @@ class NtRlScoreGradArgs(C.Structure):
                 ("tokens", C.c_void_p), ("lse_base", C.c_void_p), ("lse_rest", C.c_void_p),
                 ("ref_lse_base", C.c_void_p), ("ref_lse_rest", C.c_void_p), ("kl", C.c_void_p),
                 ("entropy", C.c_void_p), ("g_logp", C.c_void_p), ("g_kl", C.c_void_p), ("g_entropy", C.c_void_p),
-                ("grad", C.c_void_p), ("grad_dtype", C.c_int32), ("pad0", C.c_int32), ("grad_ld", C.c_int64)]
+                ("grad", C.c_void_p), ("grad_dtype", C.c_int32), ("pad0", C.c_int32), ("grad_ld", C.c_int64),
+                ("mask_rows", NtMaskRows)]
 
 
 class NtRlPolicyLossArgs(C.Structure):
@@ -449,11 +456,10 @@ def IntTensor(shape, buf=None) -> Tensor:
 
 
 def _dtype_code(t: Tensor) -> int:
-    if t.dtype == "f32":
-        return NT_F32
-    if t.dtype == "bf16":
-        return NT_BF16
-    raise ValueError(f"logits of dtype {t.dtype} (f32 or bf16)")
+    code = {"f32": NT_F32, "bf16": NT_BF16, "f16": NT_F16}.get(t.dtype)
+    if code is None:
+        raise ValueError(f"logits of dtype {t.dtype} (f32, bf16 or f16)")
+    return code
 
 
 # ----------------------------------------------------------------------------------- rng
@@ -540,9 +546,9 @@ class Tempered:
             if not all(a == b or a == 1 for a, b in zip(mask.shape, logits.shape)):
                 raise ValueError(f"tempered_logits: mask {list(mask.shape)} does not broadcast to the logits "
                                  f"{list(logits.shape)}")
-            lead = mask.shape[:-1]
-            if mask.shape[-1] != logits.shape[-1] or not (all(d == 1 for d in lead) or lead == logits.shape[:-1]):
-                raise ValueError("tempered_logits: the vocabulary mask must be [.., V] per row or shared by all rows")
+            if mask.shape[-1] != logits.shape[-1]:
+                raise ValueError("tempered_logits: the fused kernels take a mask of the full vocabulary axis "
+                                 "(it may broadcast over any leading dimension)")
 
 
 def tempered_logits(logits: Tensor, temperature: float, mask: Optional[Tensor] = None) -> Tempered:
@@ -565,15 +571,51 @@ def _as_tempered(x) -> Tempered:
     return x if isinstance(x, Tempered) else Tempered(x, 1.0, None)
 
 
+def mask_groups(logits_shape, mask_shape):
+    """The leading dimensions of a mask that broadcasts to the logits (rl.rs:477-483), folded into
+    (rows, mask stride) groups, outermost first: the mask is contiguous, a dimension the mask has
+    as 1 reads stride 0, and adjacent dimensions merge when the outer one's stride is the inner
+    one's times its length (both broadcast, or both read in order). Dimensions of length 1 drop."""
+    V = mask_shape[-1]
+    stride, strides = V, []
+    for d in reversed(mask_shape[:-1]):
+        strides.append(stride if d > 1 else 0)
+        stride *= d
+    strides.reverse()
+    groups = []
+    for d, e in zip(logits_shape[:-1], strides):
+        if d == 1:
+            continue
+        if groups and groups[-1][1] == e * d:
+            groups[-1] = (groups[-1][0] * d, e)
+        else:
+            groups.append((d, e))
+    return groups
+
+
 def _mask_fields(t: Tempered, rows: int, V: int):
+    """(kind, pointer, mask_ld, NtMaskRows, the tensor to keep alive) of a Tempered's mask: rows of
+    mask_ld when its leading dimensions fold into one group, the (s, b, t) map for up to three; a
+    mask of more groups is first broadcast to [rows, V] on the device (noetic_ops.copy)."""
     m = t.mask
+    mr = NtMaskRows(0, 0, 0, 0)
     if m is None:
-        return NT_MASK_NONE, None, 0
+        return NT_MASK_NONE, None, 0, mr, None
     kind = {"u8": NT_MASK_U8, "f32": NT_MASK_F32}.get(m.dtype)
     if kind is None:
         raise ValueError(f"vocabulary mask of dtype {m.dtype} (u8 keep-mask or f32 additive)")
-    shared = all(d == 1 for d in m.shape[:-1])
-    return kind, m.ptr, (0 if shared else V)
+    g = mask_groups(t.logits.shape, m.shape)
+    if not g:
+        return kind, m.ptr, 0, mr, m
+    if len(g) == 1:
+        return kind, m.ptr, g[0][1], mr, m
+    if len(g) <= 3:
+        g = [(1, 0)] * (3 - len(g)) + g
+        (_, ls), (B, lb), (T, lt) = g
+        return kind, m.ptr, lt, NtMaskRows(T, B, lb, ls), m
+    import noetic_ops as ops  # (noetic_ops imports this module)
+    full = ops.copy(m, ops.Layout.contiguous(m.shape).broadcast(t.logits.shape))
+    return kind, full.ptr, V, mr, full
 
 
 def _rows(x: Tensor):
@@ -603,10 +645,10 @@ def sample_logp(logits: Tensor, temperature: float, mask: Optional[Tensor], rng:
     lp = Tensor(out_shape, "f32")
     ent = Tensor(out_shape, "f32") if entropy else None
     status = Tensor(out_shape, "u8")
-    kind, mptr, mld = _mask_fields(t, rows, V)
+    kind, mptr, mld, mrows, _keep = _mask_fields(t, rows, V)
     a = NtRlSampleArgs(logits.ptr, _dtype_code(logits), kind, rows, V, V, mptr, mld, float(temperature),
                        None if uniforms is None else uniforms.ptr, ids.ptr, lp.ptr,
-                       None if ent is None else ent.ptr, status.ptr)
+                       None if ent is None else ent.ptr, status.ptr, mrows)
     _check(lib().nt_hip_rl_sample(C.byref(a)), "sample")
     if check:
         st = status.to_numpy().ravel()
@@ -635,10 +677,10 @@ def sample_categorical(logits: Tensor, temperature: float, mask: Optional[Tensor
     out_shape = logits.shape[:-1]
     ids = IntTensor(out_shape)
     status = Tensor(out_shape, "u8")
-    kind, mptr, mld = _mask_fields(t, rows, V)
+    kind, mptr, mld, mrows, _keep = _mask_fields(t, rows, V)
     block, word = rng.word_pos()
     a = NtRlGumbelArgs(logits.ptr, _dtype_code(logits), kind, rows, V, V, mptr, mld, float(temperature),
-                       rng.key(), block, word, 0, ids.ptr, status.ptr)
+                       rng.key(), block, word, 0, ids.ptr, status.ptr, mrows)
     _check(lib().nt_hip_rl_sample_gumbel(C.byref(a)), "sample_categorical")
     st = status.to_numpy().ravel()
     bad = np.nonzero(st != NT_ROW_OK)[0]
@@ -842,12 +884,12 @@ def _score(policy, ref, tokens, want_logp, want_ref_logp, want_kl, want_ent, wan
     if want_stats:
         stats = RowStats(mk(True), mk(True), mk(ref is not None), mk(ref is not None))
     status = Tensor(out_shape, "u8")
-    kind, mptr, mld = _mask_fields(p, rows, V)
+    kind, mptr, mld, mrows, _keep = _mask_fields(p, rows, V)
     ptr = lambda t: None if t is None else t.ptr
     sp = (lambda f: ptr(getattr(stats, f))) if stats is not None else (lambda f: None)
     a = NtRlScoreArgs(p.logits.ptr, None if ref is None else _as_tempered(ref).logits.ptr, _dtype_code(p.logits),
                       kind, rows, V, V, mptr, mld, p.temperature, ptr(tokens), ptr(lp), ptr(rlp), ptr(kl), ptr(ent),
-                      status.ptr, sp("lse_base"), sp("lse_rest"), sp("ref_lse_base"), sp("ref_lse_rest"))
+                      status.ptr, sp("lse_base"), sp("lse_rest"), sp("ref_lse_base"), sp("ref_lse_rest"), mrows)
     _check(lib().nt_hip_rl_score(C.byref(a)), "score")
     if tokens is not None:
         st = status.to_numpy().ravel()
@@ -886,7 +928,7 @@ def score_grad(logits, ref_logits, tokens: Optional[Tensor], stats: RowStats, kl
     temperature's divide. `grad_dtype` defaults to the logits' dtype."""
     p = _as_tempered(logits)
     rows, V = _rows(p.logits)
-    kind, mptr, mld = _mask_fields(p, rows, V)
+    kind, mptr, mld, mrows, _keep = _mask_fields(p, rows, V)
     gdt = grad_dtype or p.logits.dtype
     if gdt not in ("f32", "bf16"):
         raise ValueError(f"gradient dtype {gdt}")
@@ -896,7 +938,7 @@ def score_grad(logits, ref_logits, tokens: Optional[Tensor], stats: RowStats, kl
     a = NtRlScoreGradArgs(p.logits.ptr, None if ref is None else ref.logits.ptr, _dtype_code(p.logits), kind, rows,
                           V, V, mptr, mld, p.temperature, ptr(tokens), ptr(stats.lse_base), ptr(stats.lse_rest),
                           ptr(stats.ref_lse_base), ptr(stats.ref_lse_rest), ptr(kl), ptr(entropy), ptr(g_logp),
-                          ptr(g_kl), ptr(g_entropy), grad.ptr, NT_F32 if gdt == "f32" else NT_BF16, 0, V)
+                          ptr(g_kl), ptr(g_entropy), grad.ptr, NT_F32 if gdt == "f32" else NT_BF16, 0, V, mrows)
     _check(lib().nt_hip_rl_score_backward(C.byref(a)), "score backward")
     return grad
 

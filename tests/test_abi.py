@@ -65,9 +65,9 @@ def test_argument_struct_layouts_match_the_header():
         assert int(got[st]) == C.sizeof(cls), st
         for f in fs:
             assert int(got[f"{st}.{f}"]) == getattr(cls, f).offset, (st, f)
-    assert int(got["NtRlSampleArgs"]) == 104 and int(got["NtRlScoreArgs"]) == 152
-    assert int(got["NtRlScoreGradArgs"]) == 176 and int(got["NtRlPolicyLossArgs"]) == 120
-    assert int(got["NtRlGumbelArgs"]) == 128 and int(got["NtRlReadoutSampleArgs"]) == 136
+    assert int(got["NtRlSampleArgs"]) == 136 and int(got["NtRlScoreArgs"]) == 184
+    assert int(got["NtRlScoreGradArgs"]) == 208 and int(got["NtRlPolicyLossArgs"]) == 120
+    assert int(got["NtRlGumbelArgs"]) == 160 and int(got["NtRlReadoutSampleArgs"]) == 136
     assert int(got["NtRlReadoutScoreArgs"]) == 120
 
 
@@ -229,3 +229,17 @@ def test_bench_refuses_more_than_one_gpu_before_touching_a_device():
     assert p.returncode == 2
     msg = json.loads(p.stdout.strip().splitlines()[-1])
     assert "one GPU" in msg["error"]
+
+
+def test_mask_groups_fold():
+    """The host's folding of a broadcast mask's leading dimensions into (rows, mask stride) groups,
+    the rows -> mask-row map it hands the kernels (NtMaskRows)."""
+    g = nr.mask_groups
+    V = 10
+    assert g((3, 4, 5, V), (3, 4, 5, V)) == [(60, V)]
+    assert g((3, 4, 5, V), (1, 1, 1, V)) == [(60, 0)]
+    assert g((3, 4, 5, V), (3, 1, 1, V)) == [(3, V), (20, 0)]
+    assert g((2, 3, 4, V), (1, 3, 1, V)) == [(2, 0), (3, V), (4, 0)]
+    assert g((2, 3, 4, V), (2, 1, 4, V)) == [(2, 4 * V), (3, 0), (4, V)]
+    assert g((2, 2, 2, 2, V), (2, 1, 2, 1, V)) == [(2, 2 * V), (2, 0), (2, V), (2, 0)]
+    assert g((1, 4, 1, V), (1, 4, 1, V)) == [(4, V)]
