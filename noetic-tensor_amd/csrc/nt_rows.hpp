@@ -20,6 +20,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
+#include <cstring>
 #include <string>
 #include <type_traits>
 
@@ -565,6 +566,9 @@ struct SampleP {
     float *logp;
     float *ent;
     uint8_t *status;
+    // The largest f32 M whose tempered maximum M / tau rounds to -inf (-inf when tau >= 1): a
+    // row whose maximum is at most this has no token (set by the host, neg_overflow_bound).
+    float m_ovf;
 };
 
 // ------------------------------------------------------------------ host-side checks
@@ -583,6 +587,29 @@ inline int check_rows(int64_t rows, int64_t V, int64_t ld, int32_t dtype, int32_
         return fail(NT_E_ARG, buf);
     }
     return 0;
+}
+
+// The largest f32 m with m / tau == -inf in f32 (correctly rounded division, as the kernels'), or
+// -inf when no finite m overflows (tau >= 1): a search over the f32 magnitudes, on which the
+// quotient is monotonic. It lets a kernel refuse a row by one comparison instead of a division on
+// its critical path.
+inline float neg_overflow_bound(float tau) {
+    const auto over = [&](uint32_t bits) {
+        float m;
+        std::memcpy(&m, &bits, 4);
+        volatile float q = -m / tau;  // (computed at run time, in f32)
+        return q == -INFINITY;
+    };
+    uint32_t lo = 0, hi = 0x7f7fffffu;  // magnitudes 0 .. FLT_MAX as their bit patterns
+    if (!(tau > 0.0f) || !over(hi)) return -INFINITY;
+    while (lo < hi) {
+        const uint32_t mid = lo + (hi - lo) / 2;
+        if (over(mid)) hi = mid;
+        else lo = mid + 1;
+    }
+    float m;
+    std::memcpy(&m, &lo, 4);
+    return -m;
 }
 
 // The mask map of a call (NtMaskRows, validated): all zero is T = rows, B = 1 (rows of mask_ld).

@@ -340,6 +340,7 @@ int sample_entry(const NtRlSampleArgs *a, WorkspaceFn workspace, bool nofree, co
     p.tau = float(T);
     p.tau_one = (T == 1.0);
     p.c = (a->mask_kind == NT_MASK_F32 || T == 1.0) ? kLog2e : float(double(kLog2e) / double(p.tau));
+    p.m_ovf = p.tau_one ? -INFINITY : neg_overflow_bound(p.tau);
     p.greedy = greedy;
     p.nc = int(nc);
     p.u = a->uniforms;

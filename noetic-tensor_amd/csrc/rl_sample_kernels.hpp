@@ -512,7 +512,7 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
         }
     };
     // (nothing allowed, or every allowed logit below -FLT_MAX T, whose tempered value is -inf)
-    if (M == -INFINITY || (MK != NT_MASK_F32 && !tau_one && M / p.tau == -INFINITY)) {
+    if (M == -INFINITY || (MK != NT_MASK_F32 && M <= p.m_ovf)) {
         refuse(NT_ROW_NO_TOKEN, tid == 0);
         return;
     }
@@ -1004,7 +1004,7 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rq(SampleP p) {
         }
     };
     // (nothing allowed, or every allowed logit below -FLT_MAX T, whose tempered value is -inf)
-    if (M == -INFINITY || (MK != NT_MASK_F32 && !tau_one && M / p.tau == -INFINITY)) {
+    if (M == -INFINITY || (MK != NT_MASK_F32 && M <= p.m_ovf)) {
         refuse(NT_ROW_NO_TOKEN, tid == 0);
         return;
     }
@@ -1450,7 +1450,7 @@ __global__ __launch_bounds__(NW * kWave) void k_sample_seg(SegP q) {
         }
     };
     // (nothing allowed, or every allowed logit below -FLT_MAX T, whose tempered value is -inf)
-    if (M == -INFINITY || (MK != NT_MASK_F32 && p.tau_one == 0 && M / p.tau == -INFINITY)) {
+    if (M == -INFINITY || (MK != NT_MASK_F32 && M <= p.m_ovf)) {
         refuse(NT_ROW_NO_TOKEN);
         return;
     }
