@@ -217,7 +217,9 @@ int nt_hip_rl_sample_noalloc(const NtRlSampleArgs *a);
  * the first argmax). The weight is packed once, when loaded, into the order the matrix cores
  * read it (nt_hip_rl_readout_pack_weight, from the reference's [d, V] layout or a [V, d] one).
  * rows <= 256; vocab <= 262144; dim a multiple of 16, at most 16384; a bf16 hidden has ldh a
- * multiple of 8 and is 16-byte aligned (an f32 one: 4-byte aligned, one more launch rounds it); a u8 mask with one row per logits row (mask_ld >= vocab). Three launches on the
+ * multiple of 8 and is 16-byte aligned (an f32 one: 4-byte aligned, one more launch rounds it); a
+ * u8 mask with one row per logits row (mask_ld >= vocab) or one row shared by all (mask_ld 0).
+ * Three launches on the
  * library stream: h into the same order (2 MB at 256 x 4096), the product with the sampler's
  * per-row records in its epilogue, then one workgroup per row that merges them and recomputes
  * only the 32 logits of the block holding the draw. The debug pointers (NULL in use) write the
@@ -240,7 +242,7 @@ typedef struct NtRlReadoutSampleArgs {
     int32_t mask_kind;         /* NT_MASK_NONE | NT_MASK_U8 */
     int32_t hidden_dtype;      /* NT_BF16, or NT_F32 (rounded to bf16 to nearest-even first, as
                                   the weight is packed) */
-    const void *mask;          /* u8 [rows, mask_ld] or NULL */
+    const void *mask;          /* u8 [rows, mask_ld] (mask_ld 0: one row shared) or NULL */
     int64_t mask_ld;
     double temperature;        /* >= 0 and finite; 0 = greedy */
     const double *uniforms;    /* [rows] device, each in (0,1); unused when greedy */
@@ -270,7 +272,7 @@ typedef struct NtRlReadoutScoreArgs {
     int64_t rows, vocab, dim, ldh;
     int32_t mask_kind;         /* NT_MASK_NONE | NT_MASK_U8 */
     int32_t hidden_dtype;      /* NT_BF16 | NT_F32 */
-    const void *mask;          /* u8 [rows, mask_ld] or NULL */
+    const void *mask;          /* u8 [rows, mask_ld] (mask_ld 0: one row shared) or NULL */
     int64_t mask_ld;
     double temperature;        /* > 0 and finite */
     const int32_t *tokens;     /* [rows] device, or NULL when only the entropy is asked for */

@@ -63,7 +63,7 @@ struct ReadoutP {
     const uint8_t *wp;   // the weight in fragment order, tile-major, ntile tiles
     int rows, V, K;
     int ntile, nblk;     // tiles of 256 columns, blocks of 32 columns
-    const uint8_t *mask; // u8 keep-mask [rows, mask_ld] or null
+    const uint8_t *mask; // u8 keep-mask [rows, mask_ld] (mask_ld 0: one row shared) or null
     int64_t mask_ld;
     int mask_vec;        // mask rows 16-byte aligned: 16-byte loads
     float c;             // log2(e) / T
@@ -922,7 +922,7 @@ int readout_run(const ReadoutCall &c) {
         return fail(NT_E_UNSUPPORTED, std::string(who) + ": only no mask or a u8 keep-mask");
     if ((c.mask_kind == NT_MASK_U8) != (c.mask != nullptr))
         return fail(NT_E_ARG, std::string(who) + ": mask kind and mask pointer disagree");
-    if (c.mask && c.mask_ld < V)
+    if (c.mask && c.mask_ld != 0 && c.mask_ld < V)
         return fail(NT_E_ARG, std::string(who) + ": mask_ld " + std::to_string(c.mask_ld) +
                                   " (one mask row of at least vocab bytes per logits row)");
     if (!c.hidden || !c.weight_packed || !c.status || reinterpret_cast<uintptr_t>(c.hidden) % (hf32 ? 4 : 16) ||

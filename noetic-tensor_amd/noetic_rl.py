@@ -776,6 +776,16 @@ def _readout_shape(hidden: Tensor, weight: PackedReadout, who: str):
     return S, N, d
 
 
+def _readout_mask_ld(mask: Optional[Tensor], rows: int, V: int) -> int:
+    """The readout mask's row stride: V for one u8 row per logits row, 0 for one row [.., V] that
+    every row shares."""
+    if mask is None:
+        return 0
+    if mask.dtype != "u8" or mask.numel not in (V, rows * V) or mask.shape[-1] != V:
+        raise ValueError("readout: a u8 keep-mask [.., V], one row per logits row or one shared row")
+    return V if mask.numel == rows * V and rows > 1 else 0
+
+
 def _readout_chunks(S: int, N: int):
     """(seed, first row of the call over all rows, rows) of each call: one seed's rows, at most
     256 per call."""
@@ -800,8 +810,7 @@ def readout_sample_logp(hidden: Tensor, weight: PackedReadout, temperature: floa
     S, N, d = _readout_shape(hidden, weight, "readout")
     rows, V, es = S * N, weight.vocab, _ESIZE[hidden.dtype]
     out_shape = hidden.shape[:-1]
-    if mask is not None and (mask.dtype != "u8" or mask.numel != rows * V):
-        raise ValueError("readout: a u8 keep-mask [.., V], one row per logits row")
+    mld = _readout_mask_ld(mask, rows, V)
     if temperature != 0.0 and uniforms is None:
         if rng is None:
             raise ValueError("sample_categorical: a stream is needed at temperature > 0")
@@ -813,8 +822,8 @@ def readout_sample_logp(hidden: Tensor, weight: PackedReadout, temperature: floa
         at = lambda t, w: None if t is None else t.ptr + g0 * w
         a = NtRlReadoutSampleArgs(at(hidden, d * es), weight.seed_ptr(k if weight.batched else 0), n, V, d, d,
                                   NT_MASK_U8 if mask is not None else NT_MASK_NONE,
-                                  NT_F32 if hidden.dtype == "f32" else NT_BF16, at(mask, V),
-                                  V if mask is not None else 0, float(temperature), at(uniforms, 8), at(ids, 4),
+                                  NT_F32 if hidden.dtype == "f32" else NT_BF16, at(mask, mld),
+                                  mld, float(temperature), at(uniforms, 8), at(ids, 4),
                                   at(lp, 4), at(status, 1), at(dbg[0], V * 4), at(dbg[1], 32 * 4), at(dbg[2], 4))
         _check(lib().nt_hip_rl_readout_sample(C.byref(a)), "readout sample")
     if check:
@@ -843,8 +852,7 @@ def readout_score(hidden: Tensor, weight: PackedReadout, temperature: float, mas
         raise ValueError("token_log_probs: tokens shape (the logits' without the vocabulary axis)")
     if tokens is None and not entropy:
         raise ValueError("readout_score: neither log-probabilities nor the entropy asked for")
-    if mask is not None and (mask.dtype != "u8" or mask.numel != rows * V):
-        raise ValueError("readout: a u8 keep-mask [.., V], one row per logits row")
+    mld = _readout_mask_ld(mask, rows, V)
     lp = Tensor(out_shape, "f32") if tokens is not None else None
     ent = Tensor(out_shape, "f32") if entropy else None
     status = Tensor(out_shape, "u8")
@@ -853,8 +861,8 @@ def readout_score(hidden: Tensor, weight: PackedReadout, temperature: float, mas
         at = lambda t, w: None if t is None else t.ptr + g0 * w
         a = NtRlReadoutScoreArgs(at(hidden, d * es), weight.seed_ptr(k if weight.batched else 0), n, V, d, d,
                                  NT_MASK_U8 if mask is not None else NT_MASK_NONE,
-                                 NT_F32 if hidden.dtype == "f32" else NT_BF16, at(mask, V),
-                                 V if mask is not None else 0, float(temperature), at(tokens, 4), at(lp, 4),
+                                 NT_F32 if hidden.dtype == "f32" else NT_BF16, at(mask, mld),
+                                 mld, float(temperature), at(tokens, 4), at(lp, 4),
                                  at(ent, 4), at(status, 1), at(logits, V * 4))
         _check(lib().nt_hip_rl_readout_score(C.byref(a)), "readout score")
     if tokens is not None:

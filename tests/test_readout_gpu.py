@@ -230,6 +230,28 @@ def test_seed_batched_head():
                                uniforms=nr.Tensor.from_numpy(u[:N], "f64"))
 
 
+@pytest.mark.parametrize("rows,V,d", [(40, 1000, 256), (256, 4104, 64)])
+def test_readout_shared_mask_row(rows, V, d):
+    # one grammar mask [1, V] shared by every row (mask_ld 0) gives the materialised mask's results
+    h = W.normal((rows, d), "bf16", 3, "readout/shared/h")
+    w = nr.PackedReadout(W.normal((d, V), "bf16", 3, "readout/shared/w", std=2.0 / np.sqrt(d)), "dv")
+    rng = np.random.default_rng(3)
+    keep = (rng.random((1, V)) < 0.3).astype(np.uint8)
+    keep[0, 11] = 1
+    full = nr.Tensor.from_numpy(np.ascontiguousarray(np.broadcast_to(keep, (rows, V))))
+    shared = nr.Tensor.from_numpy(keep)
+    ut = nr.Tensor.from_numpy(nr.Rng(3, "readout/shared/u").uniforms(rows), "f64")
+    a = nr.readout_sample_logp(h, w, 0.7, shared, None, uniforms=ut, debug=True)
+    b = nr.readout_sample_logp(h, w, 0.7, full, None, uniforms=ut, debug=True)
+    for x, y in zip(a, b):
+        assert x.to_numpy().tobytes() == y.to_numpy().tobytes()
+    assert keep[0, a[0].to_numpy()].all()
+    sa = nr.readout_score(h, w, 0.7, shared, a[0], entropy=True)
+    sb = nr.readout_score(h, w, 0.7, full, a[0], entropy=True)
+    for x, y in zip(sa, sb):
+        assert x.to_numpy().tobytes() == y.to_numpy().tobytes()
+
+
 def test_readout_refuses_a_row_with_no_allowed_token():
     rows, V, d = 8, 512, 64
     h = W.normal((rows, d), "bf16", 1, "readout/refuse/h")
