@@ -632,17 +632,19 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
         return;
     }
     // The crossing lane walks its elements from the prefix before them (f32 partial sums
-    // inside the lane, compared against the f64 target).
-    int jsel = -1;
+    // inside the lane, compared against the f64 target): every comparison at once, then the
+    // first that passes.
+    int jsel;
     {
         const double t0 = tloc - (cincl - ls);
-        float C = 0.0f;
+        float C[EPL];
+        C[0] = w[0];
 #pragma unroll
-        for (int j = 0; j < EPL; j++) {
-            C += w[j];
-            if (jsel < 0 && !none && double(C) > t0) jsel = j;
-        }
-        if (jsel < 0) jsel = jlast;
+        for (int j = 1; j < EPL; j++) C[j] = C[j - 1] + w[j];
+        uint32_t crossed = 0;
+#pragma unroll
+        for (int j = 0; j < EPL; j++) crossed |= uint32_t(double(C[j]) > t0) << j;
+        jsel = (!none && crossed != 0u) ? __builtin_ctz(crossed) : jlast;
     }
     if (lane == lsel) {
         if (jsel < 0) jsel = 0;
@@ -1110,16 +1112,17 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rq(SampleP p) {
         refuse(NT_ROW_NAN, lane == 0);
         return;
     }
-    int jsel = -1;
+    int jsel;  // (the register-resident sampler's walk)
     {
         const double t0 = tloc - (cincl - ls);
-        float C = 0.0f;
+        float C[EPL];
+        C[0] = w[0];
 #pragma unroll
-        for (int j = 0; j < EPL; j++) {
-            C += w[j];
-            if (jsel < 0 && !none && double(C) > t0) jsel = j;
-        }
-        if (jsel < 0) jsel = jlast;
+        for (int j = 1; j < EPL; j++) C[j] = C[j - 1] + w[j];
+        uint32_t crossed = 0;
+#pragma unroll
+        for (int j = 0; j < EPL; j++) crossed |= uint32_t(double(C[j]) > t0) << j;
+        jsel = (!none && crossed != 0u) ? __builtin_ctz(crossed) : jlast;
     }
     if (lane == lsel) {
         if (jsel < 0) jsel = 0;
