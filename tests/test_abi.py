@@ -243,3 +243,31 @@ def test_mask_groups_fold():
     assert g((2, 3, 4, V), (2, 1, 4, V)) == [(2, 4 * V), (3, 0), (4, V)]
     assert g((2, 2, 2, 2, V), (2, 1, 2, 1, V)) == [(2, 2 * V), (2, 0), (2, V), (2, 0)]
     assert g((1, 4, 1, V), (1, 4, 1, V)) == [(4, V)]
+
+
+def test_broadcast_mask_map_is_checked_before_the_device():
+    """NtMaskRows is validated before anything touches a device: rows a whole number of T B
+    groups, each stride 0 or at least the vocabulary; a logits dtype outside f32, bf16 and f16
+    is refused."""
+    L = nr.lib()
+    buf = np.zeros(64, np.uint8)
+    h = buf.ctypes.data
+    base = dict(logits=h, dtype=nr.NT_F32, mask_kind=nr.NT_MASK_U8, rows=12, vocab=16, ld=16, mask=h, mask_ld=16,
+                temperature=1.0, uniforms=h, ids=h, status=h)
+    cases = [
+        (nr.NtMaskRows(5, 1, 0, 0), "rows a multiple"),   # 12 rows are not whole groups of 5
+        (nr.NtMaskRows(3, 2, 8, 0), "strides 0 or at least vocab"),
+        (nr.NtMaskRows(3, 2, 16, 8), "strides 0 or at least vocab"),
+        (nr.NtMaskRows(0, 2, 16, 0), "mask rows T 0"),
+    ]
+    for mr, msg in cases:
+        a = nr.NtRlSampleArgs(**base, mask_rows=mr)
+        assert L.nt_hip_rl_sample(C.byref(a)) == -1, mr
+        assert msg in L.nt_hip_last_error().decode()
+        s = nr.NtRlScoreArgs(logits=h, dtype=nr.NT_F32, mask_kind=nr.NT_MASK_U8, rows=12, vocab=16, ld=16, mask=h,
+                             mask_ld=16, temperature=1.0, status=h, mask_rows=mr)
+        assert L.nt_hip_rl_score(C.byref(s)) == -1
+        assert msg in L.nt_hip_last_error().decode()
+    a = nr.NtRlSampleArgs(**dict(base, dtype=3))
+    assert L.nt_hip_rl_sample(C.byref(a)) == -1
+    assert "dtype 3" in L.nt_hip_last_error().decode()
