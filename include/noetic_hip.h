@@ -353,7 +353,7 @@ typedef struct NtRlScoreGradArgs {
     const float *g_kl;
     const float *g_entropy;
     void *grad;               /* [rows, grad_ld] out */
-    int32_t grad_dtype;       /* NT_F32 | NT_BF16 */
+    int32_t grad_dtype;       /* NT_F32 | NT_BF16 | NT_F16 (16-bit: the f32 gradient rounded to nearest even) */
     int32_t pad0;
     int64_t grad_ld;
     NtMaskRows mask_rows;     /* the forward's */

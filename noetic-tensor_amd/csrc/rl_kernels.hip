@@ -367,7 +367,7 @@ int nt_hip_rl_score_backward(const NtRlScoreGradArgs *a) {
         return fail(NT_E_ARG, "tempered_logits: temperature " + std::to_string(a->temperature) + " (must be positive)");
     if (!a->logits || !a->grad || !a->lse_base || !a->lse_rest)
         return fail(NT_E_ARG, "nt_hip_rl_score_backward: null logits, grad or log-sum-exp statistics");
-    if (a->grad_dtype != NT_F32 && a->grad_dtype != NT_BF16)
+    if (a->grad_dtype != NT_F32 && a->grad_dtype != NT_BF16 && a->grad_dtype != NT_F16)
         return fail(NT_E_ARG, "nt_hip_rl_score_backward: grad dtype " + std::to_string(a->grad_dtype));
     if (a->grad_ld < a->vocab) return fail(NT_E_ARG, "nt_hip_rl_score_backward: grad_ld < vocab");
     if (a->g_logp && !a->tokens) return fail(NT_E_ARG, "nt_hip_rl_score_backward: g_logp needs tokens");
@@ -421,7 +421,8 @@ int nt_hip_rl_score_backward(const NtRlScoreGradArgs *a) {
         };
         auto by_gdt = [&](auto klc) {
             if (a->grad_dtype == NT_F32) by_al(klc, std::integral_constant<int, NT_F32>{});
-            else by_al(klc, std::integral_constant<int, NT_BF16>{});
+            else if (a->grad_dtype == NT_BF16) by_al(klc, std::integral_constant<int, NT_BF16>{});
+            else by_al(klc, std::integral_constant<int, NT_F16>{});
         };
         if (kl) by_gdt(std::true_type{});
         else by_gdt(std::false_type{});

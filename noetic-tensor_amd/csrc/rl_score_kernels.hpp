@@ -393,6 +393,13 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
     asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
     return r;
 }
+// Two gradients in a 16-bit dtype, a in the low half: bf16 as above, or f16 rounded to nearest
+// even (v_cvt_f16_f32 in the default rounding mode; beyond 65504 they round to infinity).
+template <int GDT>
+__device__ __forceinline__ uint32_t pack16(float a, float b) {
+    if constexpr (GDT == NT_BF16) return pack_bf16(a, b);
+    else return uint32_t(__builtin_bit_cast(uint16_t, _Float16(a))) | (uint32_t(__builtin_bit_cast(uint16_t, _Float16(b))) << 16);
+}
 
 // The per-row constants of the backward (see above).
 struct GradRow {
@@ -584,7 +591,7 @@ __device__ __forceinline__ void grad_row_aligned(const GradP &p, const GradRow &
             __builtin_amdgcn_raw_buffer_store_b128(a, gres, e0 * 4, 0, kCachePolicyNT);
             __builtin_amdgcn_raw_buffer_store_b128(b, gres, e1 * 4, 0, kCachePolicyNT);
         } else {
-            const v4u w = {pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]), pack_bf16(o[4], o[5]), pack_bf16(o[6], o[7])};
+            const v4u w = {pack16<GDT>(o[0], o[1]), pack16<GDT>(o[2], o[3]), pack16<GDT>(o[4], o[5]), pack16<GDT>(o[6], o[7])};
             __builtin_amdgcn_raw_buffer_store_b128(w, gres, e0 * 2, 0, kCachePolicyNT);
         }
     };
@@ -624,7 +631,7 @@ __device__ __forceinline__ void grad_row_general(const GradP &p, const GradRow &
                 if (e0 + j < p.V) reinterpret_cast<float *>(grow)[e0 + j] = o[j];
                 if (e0 + j + 1 < p.V) reinterpret_cast<float *>(grow)[e0 + j + 1] = o[j + 1];
             } else {
-                const uint32_t w = pack_bf16(o[j], o[j + 1]);
+                const uint32_t w = pack16<GDT>(o[j], o[j + 1]);
                 if (e0 + j < p.V) reinterpret_cast<uint16_t *>(grow)[e0 + j] = uint16_t(w);
                 if (e0 + j + 1 < p.V) reinterpret_cast<uint16_t *>(grow)[e0 + j + 1] = uint16_t(w >> 16);
             }

@@ -938,7 +938,8 @@ def score_grad(logits, ref_logits, tokens: Optional[Tensor], stats: RowStats, kl
     rows, V = _rows(p.logits)
     kind, mptr, mld, mrows, _keep = _mask_fields(p, rows, V)
     gdt = grad_dtype or p.logits.dtype
-    if gdt not in ("f32", "bf16"):
+    gcode = {"f32": NT_F32, "bf16": NT_BF16, "f16": NT_F16}.get(gdt)
+    if gcode is None:
         raise ValueError(f"gradient dtype {gdt}")
     grad = Tensor(p.logits.shape, gdt)
     ptr = lambda t: None if t is None else t.ptr
@@ -946,7 +947,7 @@ def score_grad(logits, ref_logits, tokens: Optional[Tensor], stats: RowStats, kl
     a = NtRlScoreGradArgs(p.logits.ptr, None if ref is None else ref.logits.ptr, _dtype_code(p.logits), kind, rows,
                           V, V, mptr, mld, p.temperature, ptr(tokens), ptr(stats.lse_base), ptr(stats.lse_rest),
                           ptr(stats.ref_lse_base), ptr(stats.ref_lse_rest), ptr(kl), ptr(entropy), ptr(g_logp),
-                          ptr(g_kl), ptr(g_entropy), grad.ptr, NT_F32 if gdt == "f32" else NT_BF16, 0, V, mrows)
+                          ptr(g_kl), ptr(g_entropy), grad.ptr, gcode, 0, V, mrows)
     _check(lib().nt_hip_rl_score_backward(C.byref(a)), "score backward")
     return grad
 

@@ -131,6 +131,8 @@ def test_token_log_prob_gradient_is_onehot_minus_softmax():
     ("bf16", "u8", False, 4099, 1.0, "kl h"),      # no token term (KL and entropy only), unaligned rows
     ("bf16", "none", False, 32768, 0.7, "lp h"),   # no reference: logp and entropy only
     ("f32", "none", False, 7, 1.0, "lp kl h"),     # a row shorter than one lane's eight elements
+    ("f16", "u8", False, 4096, 0.9, "lp kl h"),    # f16 logits (aligned rows), f16 gradients too
+    ("f16", "f32", True, 1003, 1.0, "lp kl h"),    # f16 logits, unaligned rows, a shared additive mask
 ])
 def test_backward_masks_temperatures_and_objectives(case):
     dtype, mk, shared, V, tau, obj = case
@@ -142,6 +144,10 @@ def test_backward_masks_temperatures_and_objectives(case):
         xb, yb = O.bf16_from_f32(x), O.bf16_from_f32(y)
         x, y = O.bf16_to_f32(xb), O.bf16_to_f32(yb)
         xt, yt = nr.Tensor.from_numpy(xb, "bf16"), nr.Tensor.from_numpy(yb, "bf16")
+    elif dtype == "f16":
+        xh, yh = x.astype(np.float16), y.astype(np.float16)
+        x, y = xh.astype(np.float32), yh.astype(np.float32)
+        xt, yt = nr.Tensor.from_numpy(xh.view(np.uint16), "f16"), nr.Tensor.from_numpy(yh.view(np.uint16), "f16")
     else:
         xt, yt = nr.Tensor.from_numpy(x), nr.Tensor.from_numpy(y)
     mrows = 1 if shared else rows
@@ -172,6 +178,13 @@ def test_backward_masks_temperatures_and_objectives(case):
     compare_to_oracle(f"{dtype} {mk} V{V} T{tau} {obj}", z, r, tok if "lp" in obj else None, g,
                       None if kl is None else kl.to_numpy(), None if ent is None else ent.to_numpy(), tau,
                       gf.to_numpy(), gb.to_numpy())
+    if dtype == "f16":
+        # the f16 gradient (the logits' own dtype, score_grad's default) is the f32 one rounded
+        # to nearest even, as numpy's float16 cast rounds it
+        gh16, _, _ = run_backward(pol, ref, tt, g, (rows,), None)
+        assert gh16.dtype == "f16"
+        assert np.array_equal(gh16.to_numpy(), gf.to_numpy().astype(np.float16).view(np.uint16)), \
+            "f16 grad is not RNE of the f32 grad"
     if keep is not None:
         # excluded entries get no softmax term: only the token's own term could remain, and the
         # tokens are kept, so every excluded entry's gradient is exactly zero
