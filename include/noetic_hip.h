@@ -217,7 +217,8 @@ int nt_hip_rl_sample_noalloc(const NtRlSampleArgs *a);
  * the first argmax). The weight is packed once, when loaded, into the order the matrix cores
  * read it (nt_hip_rl_readout_pack_weight, from the reference's [d, V] layout or a [V, d] one).
  * rows <= 256; vocab <= 262144; dim a multiple of 16, at most 16384; a bf16 hidden has ldh a
- * multiple of 8 and is 16-byte aligned (an f32 one: 4-byte aligned, one more launch rounds it); a
+ * multiple of 8 and is 16-byte aligned (an f32 or f16 one: aligned to its element, one more launch
+ * rounds it); a
  * u8 mask with one row per logits row (mask_ld >= vocab) or one row shared by all (mask_ld 0).
  * Three launches on the
  * library stream: h into the same order (2 MB at 256 x 4096), the product with the sampler's
@@ -229,8 +230,9 @@ int nt_hip_rl_sample_noalloc(const NtRlSampleArgs *a);
 /* Bytes of the packed weight: ceil(vocab / 256) 256 dim 2, the vocabulary padded with zero
  * columns to whole tiles of 256 (-1 for an invalid shape). */
 int64_t nt_hip_rl_readout_packed_bytes(int64_t vocab, int64_t dim);
-/* Pack a readout weight (dtype NT_BF16, or NT_F32 rounded to bf16 to nearest-even as it is packed,
- * the half-precision product's rounding of f32 operands, src/tensor/precision.rs:4-8; layout
+/* Pack a readout weight (dtype NT_BF16, or NT_F32 or NT_F16 rounded to bf16 to nearest-even as it
+ * is packed, the half-precision product's rounding of its operands, src/tensor/precision.rs:4-8;
+ * an f16 value widens to f32 exactly first, so it is rounded once; layout
  * NT_READOUT_W_*, row stride ld) into `packed` (device, nt_hip_rl_readout_packed_bytes bytes,
  * 16-byte aligned): one kernel on the library stream. */
 int nt_hip_rl_readout_pack_weight(const void *weight, int32_t dtype, int32_t layout, int64_t vocab, int64_t dim,
@@ -240,8 +242,8 @@ typedef struct NtRlReadoutSampleArgs {
     const void *weight_packed; /* the readout weight, packed by nt_hip_rl_readout_pack_weight */
     int64_t rows, vocab, dim, ldh;
     int32_t mask_kind;         /* NT_MASK_NONE | NT_MASK_U8 */
-    int32_t hidden_dtype;      /* NT_BF16, or NT_F32 (rounded to bf16 to nearest-even first, as
-                                  the weight is packed) */
+    int32_t hidden_dtype;      /* NT_BF16, or NT_F32 / NT_F16 (rounded to bf16 to nearest-even
+                                  first, as the weight is packed) */
     const void *mask;          /* u8 [rows, mask_ld] (mask_ld 0: one row shared) or NULL */
     int64_t mask_ld;
     double temperature;        /* >= 0 and finite; 0 = greedy */
@@ -271,7 +273,7 @@ typedef struct NtRlReadoutScoreArgs {
     const void *weight_packed; /* packed by nt_hip_rl_readout_pack_weight */
     int64_t rows, vocab, dim, ldh;
     int32_t mask_kind;         /* NT_MASK_NONE | NT_MASK_U8 */
-    int32_t hidden_dtype;      /* NT_BF16 | NT_F32 */
+    int32_t hidden_dtype;      /* NT_BF16 | NT_F32 | NT_F16 */
     const void *mask;          /* u8 [rows, mask_ld] (mask_ld 0: one row shared) or NULL */
     int64_t mask_ld;
     double temperature;        /* > 0 and finite */

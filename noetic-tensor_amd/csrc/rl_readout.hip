@@ -774,15 +774,21 @@ __device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
     return r;
 }
 
-// Fragment order (see ReadoutP) of a [R, K] matrix, bf16 or (F32) f32 rounded to bf16 as it is
-// packed: k contiguous (row r at src + r ld) or, K_MAJOR, the transpose of a [K, R] one (row r is
+// One f32 or f16 element of an operand as f32 (an f16 widens exactly).
+template <int SRC>
+__device__ __forceinline__ float operand_f32(const void *src, int64_t i) {
+    if constexpr (SRC == NT_F32) return static_cast<const float *>(src)[i];
+    else return float(__builtin_bit_cast(_Float16, static_cast<const uint16_t *>(src)[i]));
+}
+
+// Fragment order (see ReadoutP) of a [R, K] matrix, bf16, or f32 or f16 (SRC) rounded to bf16 as
+// it is packed (an f16 widened to f32 exactly first, so one rounding): k contiguous (row r at src + r ld) or, K_MAJOR, the transpose of a [K, R] one (row r is
 // column r of src, k at src + k ld + r); TILED, the weight's tile-major order over `groups`
 // column groups (a multiple of 8), else h's group-major order. Rows from R up to the groups' end
 // are zeros. One thread writes one lane's 16 bytes.
-template <bool K_MAJOR, bool TILED, bool F32>
+template <bool K_MAJOR, bool TILED, int SRC>
 __global__ void k_pack_frags(const void *srcv, int R, int K, int64_t ld, v4u *out, int64_t total) {
     const uint16_t *src = static_cast<const uint16_t *>(srcv);
-    const float *srcf = static_cast<const float *>(srcv);
     const int S = K / 16;
     for (int64_t idx = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; idx < total;
          idx += int64_t(gridDim.x) * blockDim.x) {
@@ -802,13 +808,13 @@ __global__ void k_pack_frags(const void *srcv, int R, int K, int64_t ld, v4u *ou
         const int k0 = 16 * s + 8 * (l >> 5);
         v4u v = {0, 0, 0, 0};
         if (r < R) {
-            if constexpr (F32) {
+            if constexpr (SRC != NT_BF16) {
                 uint32_t w4[4];
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     const int64_t a0 = K_MAJOR ? int64_t(k0 + 2 * j) * ld + r : r * ld + k0 + 2 * j;
                     const int64_t a1 = K_MAJOR ? int64_t(k0 + 2 * j + 1) * ld + r : r * ld + k0 + 2 * j + 1;
-                    w4[j] = bf16_pair(srcf[a0], srcf[a1]);
+                    w4[j] = bf16_pair(operand_f32<SRC>(srcv, a0), operand_f32<SRC>(srcv, a1));
                 }
                 v = v4u{w4[0], w4[1], w4[2], w4[3]};
             } else if constexpr (!K_MAJOR) {
@@ -826,26 +832,27 @@ __global__ void k_pack_frags(const void *srcv, int R, int K, int64_t ld, v4u *ou
     }
 }
 
-// f32 rows [R, K] (row stride ld) rounded to bf16, row-major with stride K: an f32 readout input
-// as the bf16 operand both the product and the resolve read.
-__global__ void k_round_rows_bf16(const float *src, int R, int K, int64_t ld, uint32_t *dst) {
+// f32 or f16 (SRC) rows [R, K] (row stride ld) rounded to bf16, row-major with stride K: such a
+// readout input as the bf16 operand both the product and the resolve read.
+template <int SRC>
+__global__ void k_round_rows_bf16(const void *src, int R, int K, int64_t ld, uint32_t *dst) {
     const int64_t pairs = int64_t(R) * (K / 2);
     for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < pairs; i += int64_t(gridDim.x) * blockDim.x) {
         const int64_t r = i / (K / 2), k = 2 * (i % (K / 2));
-        dst[i] = bf16_pair(src[r * ld + k], src[r * ld + k + 1]);
+        dst[i] = bf16_pair(operand_f32<SRC>(src, r * ld + k), operand_f32<SRC>(src, r * ld + k + 1));
     }
 }
 
 // h (group-major, ceil(R / 32) groups) or the weight (tile-major, whole tiles of 256 columns),
-// from bf16 or (F32) f32.
-template <bool K_MAJOR, bool TILED, bool F32 = false>
+// from bf16, or f32 or f16 (SRC) rounded to bf16.
+template <bool K_MAJOR, bool TILED, int SRC = NT_BF16>
 int launch_pack_t(const void *src, int R, int K, int64_t ld, void *out) {
     const int64_t groups = TILED ? int64_t((R + kRoCols - 1) / kRoCols) * 8 : (R + 31) / 32;
     const int64_t total = groups * (K / 16) * 64;
     int64_t blocks = (total + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     const dim3 g{unsigned(blocks), 1, 1}, b{256, 1, 1};
-    hipLaunchKernelGGL((k_pack_frags<K_MAJOR, TILED, F32>), g, b, 0, ctx().stream, src, R, K, ld,
+    hipLaunchKernelGGL((k_pack_frags<K_MAJOR, TILED, SRC>), g, b, 0, ctx().stream, src, R, K, ld,
                        static_cast<v4u *>(out), total);
     return launched("readout pack");
 }
@@ -863,10 +870,11 @@ extern "C" int64_t nt_hip_rl_readout_packed_bytes(int64_t vocab, int64_t dim) {
 extern "C" int nt_hip_rl_readout_pack_weight(const void *weight, int32_t dtype, int32_t layout, int64_t vocab,
                                              int64_t dim, int64_t ld, void *packed) {
     const char *who = "nt_hip_rl_readout_pack_weight";
-    const bool dv = layout == NT_READOUT_W_DV, f32 = dtype == NT_F32;
-    if ((dtype != NT_F32 && dtype != NT_BF16) || (layout != NT_READOUT_W_VD && !dv) || vocab < 1 || vocab > kRoMaxVocab ||
-        dim < 16 || dim % 16 != 0 || !weight || !packed || ld < (dv ? vocab : dim) ||
-        (!dv && !f32 && (ld % 8 != 0 || reinterpret_cast<uintptr_t>(weight) % 16)) ||
+    const bool dv = layout == NT_READOUT_W_DV, bf16 = dtype == NT_BF16;
+    if ((dtype != NT_F32 && dtype != NT_BF16 && dtype != NT_F16) || (layout != NT_READOUT_W_VD && !dv) || vocab < 1 ||
+        vocab > kRoMaxVocab || dim < 16 || dim % 16 != 0 || !weight || !packed || ld < (dv ? vocab : dim) ||
+        (!dv && bf16 && (ld % 8 != 0 || reinterpret_cast<uintptr_t>(weight) % 16)) ||
+        reinterpret_cast<uintptr_t>(weight) % (dtype == NT_F32 ? 4 : 2) ||
         reinterpret_cast<uintptr_t>(packed) % 16 || (vocab + kRoCols - 1) / kRoCols * (dim / 16) * 8192 >= (int64_t(1) << 31))
         return fail(NT_E_ARG, std::string(who) + ": dtype " + std::to_string(dtype) + ", layout " + std::to_string(layout) +
                                   ", vocab " + std::to_string(vocab) + " (at most 262144), dim " + std::to_string(dim) +
@@ -874,9 +882,12 @@ extern "C" int nt_hip_rl_readout_pack_weight(const void *weight, int32_t dtype, 
                                   " (at least the row; bf16 [V, d] rows a multiple of 8 and 16-byte aligned)");
     std::unique_lock<std::mutex> lk;
     if (int rc = enter(&lk)) return rc;
-    if (f32)
-        return dv ? launch_pack_t<true, true, true>(weight, int(vocab), int(dim), ld, packed)
-                  : launch_pack_t<false, true, true>(weight, int(vocab), int(dim), ld, packed);
+    if (dtype == NT_F32)
+        return dv ? launch_pack_t<true, true, NT_F32>(weight, int(vocab), int(dim), ld, packed)
+                  : launch_pack_t<false, true, NT_F32>(weight, int(vocab), int(dim), ld, packed);
+    if (dtype == NT_F16)
+        return dv ? launch_pack_t<true, true, NT_F16>(weight, int(vocab), int(dim), ld, packed)
+                  : launch_pack_t<false, true, NT_F16>(weight, int(vocab), int(dim), ld, packed);
     return dv ? launch_pack_t<true, true>(weight, int(vocab), int(dim), ld, packed)
               : launch_pack_t<false, true>(weight, int(vocab), int(dim), ld, packed);
 }
@@ -891,7 +902,7 @@ struct ReadoutCall {
     const void *hidden, *weight_packed, *mask;
     int64_t rows, V, K, ldh, mask_ld;
     int32_t mask_kind;
-    int32_t hidden_dtype;      // NT_BF16, or NT_F32 (rounded to bf16 once, first)
+    int32_t hidden_dtype;      // NT_BF16, or NT_F32 / NT_F16 (rounded to bf16 once, first)
     double T;                  // > 0 (1 when greedy)
     bool greedy, score;
     const double *u;           // sampling
@@ -906,12 +917,12 @@ struct ReadoutCall {
 int readout_run(const ReadoutCall &c) {
     const char *who = c.who;
     const int64_t rows = c.rows, V = c.V, K = c.K;
-    if (c.hidden_dtype != NT_BF16 && c.hidden_dtype != NT_F32)
+    if (c.hidden_dtype != NT_BF16 && c.hidden_dtype != NT_F32 && c.hidden_dtype != NT_F16)
         return fail(NT_E_ARG, std::string(who) + ": hidden_dtype " + std::to_string(c.hidden_dtype) +
-                                  " (NT_BF16 or NT_F32)");
-    const bool hf32 = c.hidden_dtype == NT_F32;
-    // A bf16 h is read in place (16-byte loads, 32-bit offsets); an f32 one is first rounded
-    // into a packed bf16 copy, so only its row stride has to cover the row.
+                                  " (NT_BF16, NT_F32 or NT_F16)");
+    const bool hf32 = c.hidden_dtype != NT_BF16;  // (f32 or f16: rounded first)
+    // A bf16 h is read in place (16-byte loads, 32-bit offsets); an f32 or f16 one is first
+    // rounded into a packed bf16 copy, so only its row stride has to cover the row.
     if (rows < 0 || rows > kRoRows || V < 1 || V > kRoMaxVocab || K < 16 || K % 16 != 0 || K > kResMaxK || c.ldh < K ||
         (!hf32 && (c.ldh % 8 != 0 || rows * c.ldh * 2 >= (int64_t(1) << 31))) ||
         (V + kRoCols - 1) / kRoCols * (K / 16) * 8192 >= (int64_t(1) << 31))
@@ -925,7 +936,8 @@ int readout_run(const ReadoutCall &c) {
     if (c.mask && c.mask_ld != 0 && c.mask_ld < V)
         return fail(NT_E_ARG, std::string(who) + ": mask_ld " + std::to_string(c.mask_ld) +
                                   " (one mask row of at least vocab bytes per logits row)");
-    if (!c.hidden || !c.weight_packed || !c.status || reinterpret_cast<uintptr_t>(c.hidden) % (hf32 ? 4 : 16) ||
+    if (!c.hidden || !c.weight_packed || !c.status ||
+        reinterpret_cast<uintptr_t>(c.hidden) % (c.hidden_dtype == NT_F32 ? 4 : (hf32 ? 2 : 16)) ||
         reinterpret_cast<uintptr_t>(c.weight_packed) % 16)
         return fail(NT_E_ARG, std::string(who) + ": null or unaligned hidden or packed weight, or null status");
     std::unique_lock<std::mutex> lk;
@@ -936,22 +948,25 @@ int readout_run(const ReadoutCall &c) {
     const size_t rec = size_t(rows) * size_t(ntile) * 4, brec = size_t(rows) * size_t(nblk) * 4;
     const size_t hpack = size_t((rows + 31) / 32) * size_t(K / 16) * 1024;
     const bool tokx = c.score && c.tokens && c.logp;  // the scored tokens' logits from pass 1
-    const size_t hround = hf32 ? size_t(rows) * size_t(K) * 2 : 0;  // an f32 h in bf16, 256-byte aligned
+    const size_t hround = hf32 ? size_t(rows) * size_t(K) * 2 : 0;  // an f32 / f16 h in bf16, 256-byte aligned
     const size_t hoff = (hpack + 3 * rec + (ent ? 2 : 1) * brec + (tokx ? size_t(rows) * 4 : 0) + 255) & ~size_t(255);
     const size_t need = hoff + hround;
     void *ws = nullptr;
     if (int rc = scratch_alloc(need, &ws)) return rc;
     uint8_t *wb = static_cast<uint8_t *>(ws);
-    // An f32 h is rounded to bf16 once (row-major, stride K), the operand the product and the
-    // resolve both read.
+    // An f32 or f16 h is rounded to bf16 once (row-major, stride K), the operand the product
+    // and the resolve both read.
     const void *hidden = c.hidden;
     int64_t ldh = c.ldh;
     if (hround) {
         uint16_t *hb = reinterpret_cast<uint16_t *>(wb + hoff);
         const int64_t blocks = std::min<int64_t>((rows * K / 2 + 255) / 256, 4096);
-        hipLaunchKernelGGL(k_round_rows_bf16, dim3(unsigned(blocks)), dim3(256), 0, ctx().stream,
-                           static_cast<const float *>(c.hidden), int(rows), int(K), c.ldh,
-                           reinterpret_cast<uint32_t *>(hb));
+        if (c.hidden_dtype == NT_F32)
+            hipLaunchKernelGGL(k_round_rows_bf16<NT_F32>, dim3(unsigned(blocks)), dim3(256), 0, ctx().stream,
+                               c.hidden, int(rows), int(K), c.ldh, reinterpret_cast<uint32_t *>(hb));
+        else
+            hipLaunchKernelGGL(k_round_rows_bf16<NT_F16>, dim3(unsigned(blocks)), dim3(256), 0, ctx().stream,
+                               c.hidden, int(rows), int(K), c.ldh, reinterpret_cast<uint32_t *>(hb));
         if (int rc = launched(who)) {
             scratch_release(ws);
             return rc;

@@ -700,7 +700,8 @@ def sample_categorical_inv_cdf(logits: Tensor, temperature: float, mask: Optiona
 
 
 NT_READOUT_W_DV, NT_READOUT_W_VD = 0, 1
-_ESIZE = {"f32": 4, "bf16": 2}
+_ESIZE = {"f32": 4, "bf16": 2, "f16": 2}
+_DTCODE = {"f32": NT_F32, "bf16": NT_BF16, "f16": NT_F16}
 _READOUT_ROWS = 256  # rows per readout call (include/noetic_hip.h)
 
 
@@ -708,13 +709,13 @@ class PackedReadout:
     """The decoder head's weight (`Linear`, linear.rs:1-12: `x.matmul(w)` with w [in, out], or
     seed-batched [S, in, out]) packed once for the readout-fused entries, in the order the matrix
     cores read it: from [d, V] or [S, d, V] (`layout` "dv"), or a vocabulary-major [V, d] /
-    [S, V, d] ("vd"). bf16 is packed as it is; f32 is rounded to bf16 to nearest-even as it is
-    packed, the rounding MatmulPrecision::Half gives f32 operands as they are loaded
-    (precision.rs:4-8). One packing kernel per seed."""
+    [S, V, d] ("vd"). bf16 is packed as it is; f32 and f16 are rounded to bf16 to nearest-even as
+    they are packed, the rounding MatmulPrecision::Half gives its operands as they are loaded
+    (precision.rs:4-8; an f16 value widens to f32 exactly first). One packing kernel per seed."""
 
     def __init__(self, weight: Tensor, layout: str = "dv"):
         if weight.dtype not in _ESIZE or len(weight.shape) not in (2, 3):
-            raise ValueError("readout weight: an f32 or bf16 [d, V] or [S, d, V] matrix")
+            raise ValueError("readout weight: an f32, bf16 or f16 [d, V] or [S, d, V] matrix")
         sh = tuple(weight.shape) if len(weight.shape) == 3 else (1,) + tuple(weight.shape)
         self.seeds, self.batched, self.weight_dtype = sh[0], len(weight.shape) == 3, weight.dtype
         if layout == "dv":
@@ -730,7 +731,7 @@ class PackedReadout:
             raise ValueError(f"readout weight [{self.vocab}, {self.dim}]: dim a multiple of 16")
         self.seed_bytes = nbytes
         self.buf = Buffer(nbytes * self.seeds)
-        dt = NT_F32 if weight.dtype == "f32" else NT_BF16
+        dt = _DTCODE[weight.dtype]
         step = sh[1] * sh[2] * _ESIZE[weight.dtype]
         for k in range(self.seeds):
             _check(lib().nt_hip_rl_readout_pack_weight(weight.ptr + k * step, dt, code, self.vocab, self.dim, ld,
@@ -762,7 +763,7 @@ def _readout_shape(hidden: Tensor, weight: PackedReadout, who: str):
     broadcast over the leading dims, as `to_rank` does, linear.rs:52-58), [S, N, d] against a
     seed-batched one."""
     if hidden.dtype not in _ESIZE or len(hidden.shape) < 2:
-        raise ValueError(f"{who}: hidden [.., d] in f32 or bf16")
+        raise ValueError(f"{who}: hidden [.., d] in f32, bf16 or f16")
     d = hidden.shape[-1]
     if weight.batched:
         if len(hidden.shape) != 3 or hidden.shape[0] != weight.seeds:
@@ -773,6 +774,9 @@ def _readout_shape(hidden: Tensor, weight: PackedReadout, who: str):
         S, N = 1, hidden.numel // d
     if d != weight.dim:
         raise ValueError(f"{who}: hidden's d {d} against the weight's {weight.dim}")
+    # the head's x.matmul(w) takes one dtype (float.rs:946-949: "matmul: f32 and bf16 (casts are
+    # explicit)"), after the shape checks
+    same_dtype(hidden.dtype, weight.weight_dtype, "matmul")
     return S, N, d
 
 
@@ -822,7 +826,7 @@ def readout_sample_logp(hidden: Tensor, weight: PackedReadout, temperature: floa
         at = lambda t, w: None if t is None else t.ptr + g0 * w
         a = NtRlReadoutSampleArgs(at(hidden, d * es), weight.seed_ptr(k if weight.batched else 0), n, V, d, d,
                                   NT_MASK_U8 if mask is not None else NT_MASK_NONE,
-                                  NT_F32 if hidden.dtype == "f32" else NT_BF16, at(mask, mld),
+                                  _DTCODE[hidden.dtype], at(mask, mld),
                                   mld, float(temperature), at(uniforms, 8), at(ids, 4),
                                   at(lp, 4), at(status, 1), at(dbg[0], V * 4), at(dbg[1], 32 * 4), at(dbg[2], 4))
         _check(lib().nt_hip_rl_readout_sample(C.byref(a)), "readout sample")
@@ -861,7 +865,7 @@ def readout_score(hidden: Tensor, weight: PackedReadout, temperature: float, mas
         at = lambda t, w: None if t is None else t.ptr + g0 * w
         a = NtRlReadoutScoreArgs(at(hidden, d * es), weight.seed_ptr(k if weight.batched else 0), n, V, d, d,
                                  NT_MASK_U8 if mask is not None else NT_MASK_NONE,
-                                 NT_F32 if hidden.dtype == "f32" else NT_BF16, at(mask, mld),
+                                 _DTCODE[hidden.dtype], at(mask, mld),
                                  mld, float(temperature), at(tokens, 4), at(lp, 4),
                                  at(ent, 4), at(status, 1), at(logits, V * 4))
         _check(lib().nt_hip_rl_readout_score(C.byref(a)), "readout score")

@@ -119,3 +119,28 @@ def test_the_readout_fusion_is_gated_on_half_precision():
     assert nr.set_matmul_precision(nr.MatmulPrecision.HALF) == nr.MatmulPrecision.F32
     assert nr.set_matmul_precision(nr.MatmulPrecision.F32) == nr.MatmulPrecision.HALF
     assert nops.MatmulPrecision is nr.MatmulPrecision
+
+
+class PackedStub:
+    """A packed head's shape and original dtype, with no storage."""
+
+    def __init__(self, dim, vocab, dtype):
+        self.dim, self.vocab, self.weight_dtype, self.batched, self.seeds = dim, vocab, dtype, False, 1
+
+    def seed_ptr(self, seed):
+        raise AssertionError("a refusal under test reached a device call")
+
+
+def test_the_readout_fusion_takes_one_dtype_as_matmul_does():
+    # x.matmul(w) checks the shapes, then same_dtype (float.rs:946-949): mixed hidden and head
+    # dtypes are refused before any device call, whatever the pair
+    with nr.matmul_precision_scope(nr.MatmulPrecision.HALF):
+        for hd, wd in (("f32", "bf16"), ("bf16", "f32"), ("f16", "bf16"), ("f32", "f16")):
+            with pytest.raises(nr.DTypeError) as e:
+                nr.readout_sample_logp(Stub((4, 64), hd), PackedStub(64, 300, wd), 0.7, None, None)
+            assert str(e.value) == f"matmul: {hd} and {wd} (casts are explicit)"
+            with pytest.raises(nr.DTypeError):
+                nr.readout_score(Stub((4, 64), hd), PackedStub(64, 300, wd), 0.7, None, None)
+        # the shape check comes first
+        with pytest.raises(ValueError, match="d 32 against the weight's 64"):
+            nr.readout_sample_logp(Stub((4, 32), "f32"), PackedStub(64, 300, "bf16"), 0.7, None, None)

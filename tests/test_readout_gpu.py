@@ -28,17 +28,30 @@ def device():
 
 
 def rounded(t):
-    """A device tensor's values as the product reads them: bf16 as they are, f32 rounded to
-    nearest-even bf16 (precision.rs:4-8; the oracle's half.rs restatement), as f64."""
+    """A device tensor's values as the product reads them: bf16 as they are, f32 and f16 (widened
+    exactly) rounded to nearest-even bf16 (precision.rs:4-8; the oracle's half.rs restatement), as
+    f64."""
     a = t.to_numpy()
-    return (W.bf16_to_f32(a) if t.dtype == "bf16" else O.bf16_to_f32(O.bf16_from_f32(a))).astype(np.float64)
+    if t.dtype == "bf16":
+        return W.bf16_to_f32(a).astype(np.float64)
+    if t.dtype == "f16":
+        a = a.view(np.float16).astype(np.float32)
+    return O.bf16_to_f32(O.bf16_from_f32(a)).astype(np.float64)
+
+
+def normal(shape, dtype, seed, label, std):
+    """W.normal's values; f16 ones drawn in f32 and rounded to f16 on the host."""
+    if dtype != "f16":
+        return W.normal(shape, dtype, seed, label, std=std)
+    f = W.normal(shape, "f32", seed, label, std=std).to_numpy()
+    return nr.Tensor.from_numpy(f.astype(np.float16).view(np.uint16), "f16")
 
 
 def run_case(name, rows, V, d, tau, masked, seed, check_gemm_rows=None, dtype="bf16"):
-    h = W.normal((rows, d), dtype, seed, f"readout/{name}/h", std=1.0)
+    h = normal((rows, d), dtype, seed, f"readout/{name}/h", std=1.0)
     # the reference's Linear layout [d, V] (src/nn/linear.rs:1-3), packed once; also the
     # vocabulary-major layout, whose packing must give the same bytes
-    w = W.normal((d, V), dtype, seed, f"readout/{name}/w", std=2.0 / np.sqrt(d))
+    w = normal((d, V), dtype, seed, f"readout/{name}/w", std=2.0 / np.sqrt(d))
     packed = nr.PackedReadout(w, "dv")
     wt = nr.Tensor.from_numpy(np.ascontiguousarray(w.to_numpy().T), dtype)
     packed_vd = nr.PackedReadout(wt, "vd")
@@ -114,14 +127,14 @@ def run_case(name, rows, V, d, tau, masked, seed, check_gemm_rows=None, dtype="b
     again = nr.readout_sample_logp(h, packed, tau, mt, None, uniforms=ut if tau else None)
     assert again[0].to_numpy().tobytes() == ids.astype(np.int32).tobytes(), f"{name}: rerun ids"
     assert again[1].to_numpy().tobytes() == lp.tobytes(), f"{name}: rerun logp"
-    if dtype == "f32":
-        # f32 operands are the device cast's bf16 operands: the same packed bytes, logits, ids and
-        # log-probabilities, bit for bit
+    if dtype in ("f32", "f16"):
+        # f32 and f16 operands are the device cast's bf16 operands: the same packed bytes, logits,
+        # ids and log-probabilities, bit for bit
         lay = lambda t: ops.Layout.contiguous(t.shape)
         hc, wc = ops.cast(h, lay(h), "bf16"), ops.cast(w, lay(w), "bf16")
         pc = nr.PackedReadout(wc, "dv")
         del wc
-        assert pc.buf_bytes() == packed.buf_bytes(), f"{name}: f32 packing differs from the bf16 cast's"
+        assert pc.buf_bytes() == packed.buf_bytes(), f"{name}: {dtype} packing differs from the bf16 cast's"
         ic, lc, zc = nr.readout_sample_logp(hc, pc, tau, mt, None, uniforms=ut if tau else None, debug=True)[:3]
         assert ic.to_numpy().tobytes() == ids.astype(np.int32).tobytes(), f"{name}: ids against the bf16 cast"
         assert lc.to_numpy().tobytes() == lp.tobytes(), f"{name}: logp against the bf16 cast"
@@ -157,6 +170,56 @@ def test_readout_sampler_f32_operands_at_the_decode_shape():
     # reference's decoder holds them, rounded to bf16 as MatmulPrecision::Half rounds its operands
     run_case("c4 readout f32", 256, 128256, 4096, 0.7, True, seed=2025, check_gemm_rows=np.arange(3, 256, 16),
              dtype="f32")
+
+
+@pytest.mark.parametrize("rows,V,d", [(40, 1000, 256), (97, 257, 16)])
+@pytest.mark.parametrize("tau,masked", [(0.7, True), (0.0, False)])
+def test_readout_sampler_f16_operands_small_shapes(rows, V, d, tau, masked):
+    run_case(f"f16 r{rows}v{V}d{d}t{tau}m{int(masked)}", rows, V, d, tau, masked, seed=rows + V + d + 2,
+             dtype="f16")
+
+
+def test_readout_sampler_f16_operands_at_a_wide_head():
+    # 256 rows against an f16 head of V 50304 (benchmark configuration 3's vocabulary), d 1024
+    run_case("f16 r256v50304d1024", 256, 50304, 1024, 0.8, True, seed=2026, check_gemm_rows=np.arange(5, 256, 25),
+             dtype="f16")
+
+
+def test_f16_weights_pack_rounded_to_nearest_even():
+    """f16 widens to f32 exactly, so packing rounds once to nearest-even bf16: ties between bf16
+    neighbours (the low three of f16's ten fraction bits 100), their neighbours, subnormals, the
+    largest finite value, signed zeros, infinities and NaNs give numpy's widened values rounded by
+    the oracle's half.rs restatement, and the device cast f16 -> bf16's bytes."""
+    d, V = 32, 300
+    rng = np.random.default_rng(18)
+    h = rng.normal(0, 1, (d, V)).astype(np.float16).view(np.uint16)
+    special = np.array([0x3C04, 0x3C0C, 0x3C05, 0x3C03, 0xBC04, 0xBC0C, 0x0001, 0x0004, 0x000C, 0x03FF, 0x8003,
+                        0x0400, 0x7BFF, 0x7BFC, 0xFBFF, 0x7C00, 0xFC00, 0x0000, 0x8000, 0x7E01, 0xFC01, 0x7D23],
+                       np.uint16)
+    pos = rng.choice(d * V, size=(8, special.size), replace=False)
+    for k in range(8):
+        h.ravel()[pos[k]] = special
+    wide = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(wide)
+    want = O.bf16_from_f32(wide)
+    w = nr.Tensor.from_numpy(h, "f16")
+    wc = ops.cast(w, ops.Layout.contiguous(w.shape), "bf16")
+    cast = wc.to_numpy()
+    assert np.array_equal(cast[~nan], want[~nan]), "the device cast f16 -> bf16 is not the widened value's RNE"
+    assert np.all(np.isnan(W.bf16_to_f32(cast[nan])))
+    ref = nr.Tensor.from_numpy(np.where(nan, np.uint16(0x7FC0), want).astype(np.uint16), "bf16")
+    a = np.frombuffer(nr.PackedReadout(w, "dv").buf_bytes(), np.uint16)
+    b = np.frombuffer(nr.PackedReadout(ref, "dv").buf_bytes(), np.uint16)
+    c = np.frombuffer(nr.PackedReadout(wc, "dv").buf_bytes(), np.uint16)
+    for other in (b, c):
+        differ = np.nonzero(a != other)[0]
+        # only NaNs may differ (in payload), and those stay NaNs
+        assert np.all(np.isnan(W.bf16_to_f32(a[differ]))) and np.all(np.isnan(W.bf16_to_f32(other[differ])))
+        assert len(differ) <= int(nan.sum())
+    assert np.sum(np.isnan(W.bf16_to_f32(a))) == int(nan.sum())
+    # the vocabulary-major layout packs to the same bytes
+    wt = nr.Tensor.from_numpy(np.ascontiguousarray(h.T), "f16")
+    assert nr.PackedReadout(wt, "vd").buf_bytes() == a.tobytes()
 
 
 def test_f32_weights_pack_rounded_to_nearest_even():

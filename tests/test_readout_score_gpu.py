@@ -37,9 +37,17 @@ def close(name, got, want):
     return float(err.max()) if err.size else 0.0
 
 
-def make(name, rows, V, d, seed, masked):
-    h = W.normal((rows, d), "bf16", seed, f"readout/{name}/h", std=1.0)
-    w = W.normal((d, V), "bf16", seed, f"readout/{name}/w", std=2.0 / np.sqrt(d))
+def normal(shape, dtype, seed, label, std):
+    """W.normal's values; f16 ones drawn in f32 and rounded to f16 on the host."""
+    if dtype != "f16":
+        return W.normal(shape, dtype, seed, label, std=std)
+    f = W.normal(shape, "f32", seed, label, std=std).to_numpy()
+    return nr.Tensor.from_numpy(f.astype(np.float16).view(np.uint16), "f16")
+
+
+def make(name, rows, V, d, seed, masked, dtype="bf16"):
+    h = normal((rows, d), dtype, seed, f"readout/{name}/h", std=1.0)
+    w = normal((d, V), dtype, seed, f"readout/{name}/w", std=2.0 / np.sqrt(d))
     packed = nr.PackedReadout(w, "dv")
     rng = np.random.default_rng(seed)
     keep = mt = None
@@ -50,8 +58,8 @@ def make(name, rows, V, d, seed, masked):
     return h, packed, keep, mt, rng
 
 
-def run_case(name, rows, V, d, tau, masked, seed):
-    h, packed, keep, mt, rng = make(name, rows, V, d, seed, masked)
+def run_case(name, rows, V, d, tau, masked, seed, dtype="bf16"):
+    h, packed, keep, mt, rng = make(name, rows, V, d, seed, masked, dtype)
     tok = rng.integers(0, V, rows).astype(np.int32)
     if keep is not None:
         # mostly allowed tokens, and every fourth row's token as drawn (excluded ones among them)
@@ -86,6 +94,12 @@ def run_case(name, rows, V, d, tau, masked, seed):
 @pytest.mark.parametrize("tau,masked", [(0.7, True), (1.0, False)])
 def test_readout_scorer_small_shapes(rows, V, d, tau, masked):
     run_case(f"r{rows}v{V}d{d}t{tau}m{int(masked)}", rows, V, d, tau, masked, seed=rows + V + d + 1)
+
+
+@pytest.mark.parametrize("tau,masked", [(0.7, True), (1.0, False)])
+def test_readout_scorer_f16_operands(tau, masked):
+    # an f16 head and f16 hidden rows, each rounded to bf16 as MatmulPrecision::Half loads them
+    run_case(f"f16 r40v1000d256t{tau}m{int(masked)}", 40, 1000, 256, tau, masked, seed=1297, dtype="f16")
 
 
 def test_readout_scorer_at_the_decode_shape():
