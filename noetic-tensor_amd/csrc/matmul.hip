@@ -647,45 +647,44 @@ __device__ __forceinline__ uint4 pack8(const float *src, int64_t stride, int lim
     return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-// A (batch z = blockIdx.y) into row-group fragments: fragment (g, s) of G x S at (g S + s) KiB
-// from the batch's start (G S KiB apart); lane l's 16 bytes are row 32 g + l % 32, k 16 s +
-// 8 (l / 32) .. + 7. One thread per lane of a fragment.
-__global__ void k_pack_half_rows(MatmulP p, int G, int S, uint8_t *out) {
+// One batch's A (row-group fragments) and B (tile-major column fragments) in one launch, batch
+// z = blockIdx.y; the first `ablocks` blocks of a row of the grid take A's lanes, the rest B's.
+// A: fragment (g, s) of G x S at (g S + s) KiB from the batch's start (G S KiB apart); lane l's
+// 16 bytes are row 32 g + l % 32, k 16 s + 8 (l / 32) .. + 7.
+// B: tile t of T, step s, column group gi at ((t S + s) 8 + gi) KiB from the batch's start
+// (T S 8 KiB apart); lane l's 16 bytes are column 32 (8 t + gi) + l % 32, k 16 s + 8 (l / 32) ..
+// + 7. One thread per lane of a fragment.
+__global__ void k_pack_half(MatmulP p, int G, int T, int S, int ablocks, uint8_t *pa, uint8_t *pb) {
     const int64_t z = blockIdx.y;
     int64_t ao, bo;
     batch_offsets(p, z, &ao, &bo);
-    const int64_t total = int64_t(G) * S * 64;
-    for (int64_t idx = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; idx < total;
-         idx += int64_t(gridDim.x) * blockDim.x) {
-        const int l = int(idx % 64);
-        const int64_t q = idx / 64;
-        const int s = int(q % S), g = int(q / S);
-        const int row = 32 * g + (l & 31), k0 = 16 * s + 8 * (l >> 5);
-        const int lim = row < p.m ? min(8, p.k - k0) : 0;
-        const uint4 v = pack8(p.a + ao + int64_t(row < p.m ? row : 0) * p.a_rs + int64_t(k0) * p.a_cs, p.a_cs, lim);
-        *reinterpret_cast<uint4 *>(out + (z * G * S + (int64_t(g) * S + s)) * 1024 + l * 16) = v;
-    }
-}
-
-// B (batch z = blockIdx.y) into tile-major column fragments: tile t of T, step s, column group gi
-// at ((t S + s) 8 + gi) KiB from the batch's start (T S 8 KiB apart); lane l's 16 bytes are
-// column 32 (8 t + gi) + l % 32, k 16 s + 8 (l / 32) .. + 7.
-__global__ void k_pack_half_cols(MatmulP p, int T, int S, uint8_t *out) {
-    const int64_t z = blockIdx.y;
-    int64_t ao, bo;
-    batch_offsets(p, z, &ao, &bo);
-    const int64_t total = int64_t(T) * S * 8 * 64;
-    for (int64_t idx = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; idx < total;
-         idx += int64_t(gridDim.x) * blockDim.x) {
-        const int l = int(idx % 64);
-        const int64_t q = idx / 64;  // (t S + s) 8 + gi
-        const int gi = int(q % 8);
-        const int64_t ts = q / 8;
-        const int s = int(ts % S), t = int(ts / S);
-        const int col = 32 * (8 * t + gi) + (l & 31), k0 = 16 * s + 8 * (l >> 5);
-        const int lim = col < p.n ? min(8, p.k - k0) : 0;
-        const uint4 v = pack8(p.b + bo + int64_t(col < p.n ? col : 0) * p.b_cs + int64_t(k0) * p.b_rs, p.b_rs, lim);
-        *reinterpret_cast<uint4 *>(out + (z * T * S * 8 + q) * 1024 + l * 16) = v;
+    if (int(blockIdx.x) < ablocks) {
+        const int64_t total = int64_t(G) * S * 64;
+        for (int64_t idx = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; idx < total;
+             idx += int64_t(ablocks) * blockDim.x) {
+            const int l = int(idx % 64);
+            const int64_t q = idx / 64;
+            const int s = int(q % S), g = int(q / S);
+            const int row = 32 * g + (l & 31), k0 = 16 * s + 8 * (l >> 5);
+            const int lim = row < p.m ? min(8, p.k - k0) : 0;
+            const uint4 v = pack8(p.a + ao + int64_t(row < p.m ? row : 0) * p.a_rs + int64_t(k0) * p.a_cs, p.a_cs, lim);
+            *reinterpret_cast<uint4 *>(pa + (z * G * S + (int64_t(g) * S + s)) * 1024 + l * 16) = v;
+        }
+    } else {
+        const int64_t total = int64_t(T) * S * 8 * 64;
+        const int bblocks = int(gridDim.x) - ablocks;
+        for (int64_t idx = (blockIdx.x - ablocks) * int64_t(blockDim.x) + threadIdx.x; idx < total;
+             idx += int64_t(bblocks) * blockDim.x) {
+            const int l = int(idx % 64);
+            const int64_t q = idx / 64;  // (t S + s) 8 + gi
+            const int gi = int(q % 8);
+            const int64_t ts = q / 8;
+            const int s = int(ts % S), t = int(ts / S);
+            const int col = 32 * (8 * t + gi) + (l & 31), k0 = 16 * s + 8 * (l >> 5);
+            const int lim = col < p.n ? min(8, p.k - k0) : 0;
+            const uint4 v = pack8(p.b + bo + int64_t(col < p.n ? col : 0) * p.b_cs + int64_t(k0) * p.b_rs, p.b_rs, lim);
+            *reinterpret_cast<uint4 *>(pb + (z * T * S * 8 + q) * 1024 + l * 16) = v;
+        }
     }
 }
 
@@ -921,15 +920,12 @@ int nt_hip_matmul_half(const float *a, const NtLayout *al, const float *b, const
             void *ws = nullptr;
             if (int rc = scratch_alloc(size_t(bytes_a + bytes_b), &ws)) return rc;
             uint8_t *pa = static_cast<uint8_t *>(ws), *pb = pa + bytes_a;
+            // both operands in one launch, blocks in proportion to their fragments
             const int64_t ta = G * S * 64, tb = T256 * S * 8 * 64;
-            const dim3 ga(unsigned(std::min<int64_t>((ta + 255) / 256, 4096)), unsigned(nb));
-            const dim3 gb(unsigned(std::min<int64_t>((tb + 255) / 256, 4096)), unsigned(nb));
-            hipLaunchKernelGGL(k_pack_half_rows, ga, dim3(256), 0, st, p, int(G), int(S), pa);
-            int rc = launched("k_pack_half_rows");
-            if (!rc) {
-                hipLaunchKernelGGL(k_pack_half_cols, gb, dim3(256), 0, st, p, int(T256), int(S), pb);
-                rc = launched("k_pack_half_cols");
-            }
+            const int64_t ba = std::min<int64_t>((ta + 255) / 256, 4096), bb = std::min<int64_t>((tb + 255) / 256, 4096);
+            hipLaunchKernelGGL(k_pack_half, dim3(unsigned(ba + bb), unsigned(nb)), dim3(256), 0, st, p, int(G),
+                               int(T256), int(S), int(ba), pa, pb);
+            int rc = launched("k_pack_half");
             if (!rc) {
                 hipLaunchKernelGGL(k_half_tiles, dim3(unsigned(tiles)), dim3(256), 0, st, p, pa, pb, int(G),
                                    int(T256), int(S));
