@@ -527,8 +527,9 @@ KL_DELTA_CLAMP = 20.0  # rl.rs:150
 class Tempered:
     """`tempered_logits(logits, temperature, mask)` (rl.rs:475-486), kept unmaterialised: the
     fused kernels apply the divide and the vocabulary mask while streaming the logits.
-    mask: None, a u8 keep-mask (0 excludes) or an additive f32 mask, [rows or 1, V] in the
-    logits' rank (a mask whose leading dims are all 1 is shared by every row).
+    mask: None, a u8 keep-mask (0 excludes) or an additive f32 mask in the logits' rank, each
+    dimension equal to the logits' or 1 (a mask whose leading dims are all 1 is shared by every
+    row; one whose last dimension is 1 is a value per position).
 
     Built directly, it is the fused entries' (logits, τ, mask) triple: 16-bit logits are widened
     exactly to f32 at every τ, the values the reference's chain gives on `logits.cast(F32)`.
@@ -546,9 +547,6 @@ class Tempered:
             if not all(a == b or a == 1 for a, b in zip(mask.shape, logits.shape)):
                 raise ValueError(f"tempered_logits: mask {list(mask.shape)} does not broadcast to the logits "
                                  f"{list(logits.shape)}")
-            if mask.shape[-1] != logits.shape[-1]:
-                raise ValueError("tempered_logits: the fused kernels take a mask of the full vocabulary axis "
-                                 "(it may broadcast over any leading dimension)")
 
 
 def tempered_logits(logits: Tensor, temperature: float, mask: Optional[Tensor] = None) -> Tempered:
@@ -596,7 +594,8 @@ def mask_groups(logits_shape, mask_shape):
 def _mask_fields(t: Tempered, rows: int, V: int):
     """(kind, pointer, mask_ld, NtMaskRows, the tensor to keep alive) of a Tempered's mask: rows of
     mask_ld when its leading dimensions fold into one group, the (s, b, t) map for up to three; a
-    mask of more groups is first broadcast to [rows, V] on the device (noetic_ops.copy)."""
+    mask of more groups, or one that broadcasts along the vocabulary axis too (a value per
+    position, [.., 1]), is first broadcast to [rows, V] on the device (noetic_ops.copy)."""
     m = t.mask
     mr = NtMaskRows(0, 0, 0, 0)
     if m is None:
@@ -604,6 +603,10 @@ def _mask_fields(t: Tempered, rows: int, V: int):
     kind = {"u8": NT_MASK_U8, "f32": NT_MASK_F32}.get(m.dtype)
     if kind is None:
         raise ValueError(f"vocabulary mask of dtype {m.dtype} (u8 keep-mask or f32 additive)")
+    if m.shape[-1] != V:
+        import noetic_ops as ops  # (noetic_ops imports this module)
+        full = ops.copy(m, ops.Layout.contiguous(m.shape).broadcast(t.logits.shape))
+        return kind, full.ptr, V, mr, full
     g = mask_groups(t.logits.shape, m.shape)
     if not g:
         return kind, m.ptr, 0, mr, m

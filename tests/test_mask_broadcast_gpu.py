@@ -8,8 +8,9 @@ mask materialised to the logits' full shape: the results must be the same bits. 
 checked against the oracle's f64 restatement on the materialised mask: ids equal except within
 1e-6 of a CDF edge, values within 1e-5 relative / 1e-6 absolute. Shapes cover one, two and three
 folded groups, four groups (the host broadcasts the mask on the device first), odd vocabularies
-(the element-wise kernels), and C4's vocabulary at 8 and 256 rows (the segmented and the queued
-samplers)."""
+(the element-wise kernels), C4's vocabulary at 8 and 256 rows (the segmented and the queued
+samplers), and masks of one value per position ([.., 1], broadcast along the vocabulary too,
+which the host also broadcasts on the device first)."""
 import zlib
 
 import numpy as np
@@ -58,6 +59,10 @@ def make_mask(rng, mshape, kind):
         m = (rng.random(mshape) < 0.5).astype(np.uint8)
         m[..., 3] = 1
         return m
+    if kind == "u8 position":
+        return np.ones(mshape, np.uint8)  # [.., 1]: every position kept
+    if kind == "f32 position":
+        return rng.normal(0, 3, mshape).astype(np.float32)  # [.., 1]: a finite value per position
     m = np.where(rng.random(mshape) < 0.3, -np.inf, rng.normal(0, 0.5, mshape)).astype(np.float32)
     m[..., 5] = -1e9
     m[..., 3] = 0.0
@@ -74,6 +79,11 @@ CASES = [
     ("[1,B,1,V] C4 vocabulary, 8 rows", (1, 4, 2, 128256), (1, 4, 1, 128256), "u8", "bf16", 0.7, None),
     ("[1,B,1,V] C4 vocabulary, 256 rows", (1, 128, 2, 128256), (1, 128, 1, 128256), "u8", "bf16", 0.7,
      np.arange(0, 256, 17)),
+    # a mask that broadcasts along the vocabulary axis too: one value per position (the host
+    # broadcasts it to the logits' shape on the device first)
+    ("[S,B,T,1] f32 value per position", (2, 3, 4, 777), (2, 3, 4, 1), "f32 position", "f32", 0.8, None),
+    ("[S,1,T,1] f32 bf16 tau 1", (2, 3, 4, 1000), (2, 1, 4, 1), "f32 position", "bf16", 1.0, None),
+    ("[1,B,1,1] u8", (1, 5, 2, 600), (1, 5, 1, 1), "u8 position", "f16", 0.9, None),
 ]
 
 
@@ -88,7 +98,8 @@ def test_broadcast_masks(case):
     m = make_mask(rng, mshape, kind)
     full = np.ascontiguousarray(np.broadcast_to(m, shape))
     xt, yt = to_dev(x, dtype), to_dev(y, dtype)
-    mt, ft = nr.Tensor.from_numpy(m, kind), nr.Tensor.from_numpy(full, kind)
+    mdt = "u8" if kind.startswith("u8") else "f32"
+    mt, ft = nr.Tensor.from_numpy(m, mdt), nr.Tensor.from_numpy(full, mdt)
     u = nr.Rng(7, name).uniforms(rows)
     ut = nr.Tensor.from_numpy(u, "f64")
 
@@ -125,7 +136,7 @@ def test_broadcast_masks(case):
     xw = widened(x, dtype).reshape(rows, V)[r]
     yw = widened(y, dtype).reshape(rows, V)[r]
     fm = full.reshape(rows, V)[r]
-    kw = dict(keep=fm) if kind == "u8" else dict(addmask=fm)
+    kw = dict(keep=fm) if mdt == "u8" else dict(addmask=fm)
     z, zr = O.tempered(xw, tau, **kw), O.tempered(yw, tau, **kw)
     want, edges = O.sample_invcdf(z, u[r])
     differ = np.nonzero(ids[r] != want)[0]
