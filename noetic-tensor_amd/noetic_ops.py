@@ -376,8 +376,9 @@ def half_gemm_key() -> str:
 def tempered_logits(logits: Tensor, temperature: float, mask: Optional[Tensor] = None) -> Tensor:
     """`tempered_logits` (rl.rs:475-486) materialised on the device with the general ops:
     `div_scalar(τ)` unless τ == 1 (16-bit logits come out f32), then `add(mask)` broadcast at rank
-    (an f32 additive mask; 16-bit logits at τ == 1 are refused there, as the reference's add
-    refuses them). The fused entry points take the tempered logits without materialising them;
+    under add's same_dtype check (an f32 mask on f32 or divided logits; at τ == 1 a 16-bit mask
+    of the logits' own dtype, the sum computed in f32 into f32 storage; other pairs are refused
+    there, as the reference's add refuses them). The fused entry points take the tempered logits without materialising them;
     this is the op sequence a caller gets when it asks for the tensor itself."""
     if not (temperature > 0.0 and np.isfinite(temperature)):
         raise ValueError(f"tempered_logits: temperature {temperature} (must be positive)")
@@ -396,10 +397,14 @@ def tempered_logits(logits: Tensor, temperature: float, mask: Optional[Tensor] =
                              f"{list(logits.shape)}")
         # add's same_dtype check on the reference's z: 16-bit logits are not divided at τ == 1
         same_dtype(logits.dtype if temperature == 1.0 else "f32", mask.dtype, "add")
-        if mask.dtype != "f32":
-            raise TypeError("tempered_logits: an additive f32 mask")
+        if mask.dtype not in ("f32", "bf16", "f16"):
+            raise TypeError("tempered_logits: an additive float mask")
+        # the sum computes 16-bit operands in f32 into f32 storage (f32_operand, gpu/mod.rs:336-342)
+        m = cast(mask, Layout.contiguous(mask.shape), "f32") if mask.dtype != "f32" else mask
+        if z.dtype != "f32":
+            z = cast(z, lay, "f32")
         out = broadcast_shape(logits.shape, mask.shape)
-        z = binary(BinaryOp.ADD, z, lay.broadcast(out), mask, Layout.contiguous(mask.shape).broadcast(out))
+        z = binary(BinaryOp.ADD, z, lay.broadcast(out), m, Layout.contiguous(mask.shape).broadcast(out))
     return z
 
 

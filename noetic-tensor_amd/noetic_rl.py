@@ -55,11 +55,13 @@ def tempered_dtype(dtype: str, temperature: float, mask_dtype: Optional[str]) ->
     """The dtype of the reference's materialised `tempered_logits(logits, τ, mask)` (rl.rs:475-486),
     or its DType refusal: `div_scalar` computes 16-bit values in f32 into f32 storage (`fdisp`,
     float.rs:43-58, 494-499), τ == 1 keeps the logits' own dtype, and the additive mask is added
-    under `add`'s same_dtype check (float.rs:398-402). A u8 keep-mask stands for the f32 0/−∞ mask
-    it encodes."""
+    under `add`'s same_dtype check (float.rs:398-402), its sum of two 16-bit tensors computed in
+    f32 into f32 storage as well (fdisp; on a GPU, f32_operand, gpu/mod.rs:336-342, 381-391). A u8
+    keep-mask stands for the f32 0/−∞ mask it encodes."""
     z = dtype if temperature == 1.0 else ("f32" if dtype in _HALF else dtype)
     if mask_dtype is not None:
         same_dtype(z, "f32" if mask_dtype in ("u8", "bool") else mask_dtype, "add")
+        z = "f32" if z in _HALF else z
     return z
 
 
@@ -527,7 +529,8 @@ KL_DELTA_CLAMP = 20.0  # rl.rs:150
 class Tempered:
     """`tempered_logits(logits, temperature, mask)` (rl.rs:475-486), kept unmaterialised: the
     fused kernels apply the divide and the vocabulary mask while streaming the logits.
-    mask: None, a u8 keep-mask (0 excludes) or an additive f32 mask in the logits' rank, each
+    mask: None, a u8 keep-mask (0 excludes) or an additive f32, bf16 or f16 mask (a 16-bit one
+    widened exactly, as the reference's add computes it in f32) in the logits' rank, each
     dimension equal to the logits' or 1 (a mask whose leading dims are all 1 is shared by every
     row; one whose last dimension is 1 is a value per position).
 
@@ -600,9 +603,13 @@ def _mask_fields(t: Tempered, rows: int, V: int):
     mr = NtMaskRows(0, 0, 0, 0)
     if m is None:
         return NT_MASK_NONE, None, 0, mr, None
-    kind = {"u8": NT_MASK_U8, "f32": NT_MASK_F32}.get(m.dtype)
+    kind = {"u8": NT_MASK_U8, "f32": NT_MASK_F32, "bf16": NT_MASK_F32, "f16": NT_MASK_F32}.get(m.dtype)
     if kind is None:
-        raise ValueError(f"vocabulary mask of dtype {m.dtype} (u8 keep-mask or f32 additive)")
+        raise ValueError(f"vocabulary mask of dtype {m.dtype} (u8 keep-mask, or additive f32, bf16 or f16)")
+    if m.dtype in _HALF:
+        # a 16-bit additive mask is added in f32 (fdisp; f32_operand on a GPU): widened exactly
+        import noetic_ops as ops  # (noetic_ops imports this module)
+        m = ops.cast(m, ops.Layout.contiguous(m.shape), "f32")
     if m.shape[-1] != V:
         import noetic_ops as ops  # (noetic_ops imports this module)
         full = ops.copy(m, ops.Layout.contiguous(m.shape).broadcast(t.logits.shape))

@@ -48,7 +48,11 @@ def test_tempered_dtype_follows_the_reference():
     assert td("f32", 1.0, None) == "f32" and td("f32", 0.7, "f32") == "f32" and td("f32", 1.0, "u8") == "f32"
     assert td("bf16", 1.0, None) == "bf16" and td("f16", 1.0, None) == "f16"
     assert td("bf16", 0.7, None) == "f32" and td("bf16", 0.7, "u8") == "f32" and td("f16", 2.0, "f32") == "f32"
-    assert td("bf16", 1.0, "bf16") == "bf16"  # a bf16 additive mask on untempered bf16 logits adds
+    # a 16-bit additive mask of the logits' dtype on untempered 16-bit logits adds, computing in
+    # f32 into f32 storage (fdisp, float.rs:43-58; f32_operand on a GPU)
+    assert td("bf16", 1.0, "bf16") == "f32" and td("f16", 1.0, "f16") == "f32"
+    with pytest.raises(nr.DTypeError, match="add: bf16 and f16"):
+        td("bf16", 1.0, "f16")
     with pytest.raises(nr.DTypeError, match=ADD.replace("(", r"\(").replace(")", r"\)")):
         td("bf16", 1.0, "u8")
     with pytest.raises(nr.DTypeError, match="add: f16 and f32"):
@@ -94,6 +98,19 @@ def test_reference_named_functions_refuse_16_bit_logits_where_the_reference_does
     with pytest.raises(nr.DTypeError) as e:
         nops.tempered_logits(x4, 1.0, Stub((1, 1, 1, 50), "f32"))
     assert str(e.value) == ADD
+    # a bf16 additive mask on untempered bf16 logits: tempered_logits' result is f32, so the
+    # reference's functions take it, and sampling at τ == 1 adds f32 noise to f32 (no refusal
+    # before the device)
+    m16 = Stub((2, 3, 4, 50), "bf16")
+    assert nr.tempered_logits(x4, 1.0, m16).dtype == "f32"
+    for call in (lambda: nr.sample_categorical(x4, 1.0, m16, None),
+                 lambda: nr.sample_categorical(x4, 0.0, m16, None),
+                 lambda: nr.token_log_probs(nr.tempered_logits(x4, 1.0, m16), tok)):
+        with pytest.raises((AssertionError, nr.HipUnavailable)):  # past the dtype checks, at the device
+            call()
+    with pytest.raises(nr.DTypeError) as e:
+        nr.tempered_logits(x4, 0.7, m16)  # the divided logits are f32, the mask is not
+    assert str(e.value) == "add: f32 and bf16 (casts are explicit)"
     # shape checks come first, as in the reference
     with pytest.raises(ValueError, match="tokens shape"):
         nr.token_log_probs(x4, Stub((2, 3), "i32"))

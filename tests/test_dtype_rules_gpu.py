@@ -113,6 +113,55 @@ def test_fused_entries_take_bf16_at_every_temperature_as_widened_f32():
         assert np.all(d <= 1e-6 + 1e-5 * np.abs(la.to_numpy()))
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_16_bit_additive_masks_add_in_f32(dt):
+    """A 16-bit additive mask of the logits' own dtype on untempered logits: the reference's add
+    computes the sum in f32 into f32 storage (fdisp, float.rs:43-58; f32_operand on a GPU,
+    gpu/mod.rs:336-342), so tempered_logits is f32 and the reference's functions and its sampler
+    at τ == 1 take it. Every path gives the widened f32 inputs' results: the materialised sum bit
+    for bit, the Gumbel and greedy ids with the stream moved alike, and the scorer's values within
+    the f32 tolerance (bf16 and f32 rows are read in different lane orders)."""
+    rows, V = 12, 700
+    rng = np.random.default_rng(6)
+    x = rng.normal(0, 2, (rows, V)).astype(np.float32)
+    m = np.where(rng.random((rows, V)) < 0.3, -np.inf, rng.normal(0, 1, (rows, V))).astype(np.float32)
+    m[:, 3] = 0.0
+    if dt == "bf16":
+        xr, mr = O.bf16_from_f32(x), O.bf16_from_f32(m)
+        xw, mw = O.bf16_to_f32(xr), O.bf16_to_f32(mr)
+    else:
+        xr, mr = x.astype(np.float16).view(np.uint16), m.astype(np.float16).view(np.uint16)
+        xw, mw = xr.view(np.float16).astype(np.float32), mr.view(np.float16).astype(np.float32)
+    sh = (1, 3, 4, V)  # [S, B, T, V], as categorical_entropy takes it
+    t16, m16 = nr.Tensor.from_numpy(xr.reshape(sh), dt), nr.Tensor.from_numpy(mr.reshape(sh), dt)
+    t32, m32 = nr.Tensor.from_numpy(xw.reshape(sh)), nr.Tensor.from_numpy(mw.reshape(sh))
+    z16, z32 = nops.tempered_logits(t16, 1.0, m16), nops.tempered_logits(t32, 1.0, m32)
+    assert z16.dtype == "f32" and z16.to_numpy().tobytes() == z32.to_numpy().tobytes()
+    assert np.array_equal(z16.to_numpy(), (xw + mw).reshape(sh))
+    for tau in (1.0, 0.0, 0.8):
+        if tau == 0.8:
+            # divided logits are f32 and the mask is not: refused by add, before any draw
+            with pytest.raises(nr.DTypeError, match=f"add: f32 and {dt}"):
+                nr.sample_categorical(t16, tau, m16, nr.Rng(21, "m16"))
+            continue
+        ra, rb = nr.Rng(21, "m16"), nr.Rng(21, "m16")
+        a = nr.sample_categorical(t16, tau, m16, ra).to_numpy()
+        b = nr.sample_categorical(t32, tau, m32, rb).to_numpy()
+        assert np.array_equal(a, b), f"τ {tau}: ids"
+        assert ra.word_pos() == rb.word_pos()
+    tok = nr.Tensor.from_numpy(((np.arange(rows, dtype=np.int32) * 31) % V).reshape(sh[:-1]))
+    close(nr.token_log_probs(nr.tempered_logits(t16, 1.0, m16), tok).to_numpy(),
+          nr.token_log_probs(nr.tempered_logits(t32, 1.0, m32), tok).to_numpy())
+    close(nr.categorical_entropy(nr.tempered_logits(t16, 1.0, m16)).to_numpy(),
+          nr.categorical_entropy(nr.tempered_logits(t32, 1.0, m32)).to_numpy())
+    # the fused triple takes the 16-bit mask at every τ, widened
+    u = nr.Tensor.from_numpy(nr.Rng(22, "m16/u").uniforms(rows), "f64")
+    ia, la = nr.sample_logp(t16, 0.8, m16, None, uniforms=u)
+    ib, lb = nr.sample_logp(t32, 0.8, m32, None, uniforms=u)
+    assert np.array_equal(ia.to_numpy(), ib.to_numpy())
+    close(la.to_numpy(), lb.to_numpy())
+
+
 def test_platform_key_carries_the_half_product_part_only_at_half():
     base = nr.platform_key()
     assert "gemm-" not in base
