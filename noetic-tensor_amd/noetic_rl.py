@@ -1289,15 +1289,20 @@ def group_advantages(rewards: Sequence[float], n: int, norm="mean", eps: float =
 
 def group_advantages_tensor(rewards: Tensor, norm="mean", eps: float = 0.0, unbiased: bool = True) -> Tensor:
     """rl.rs:465-469: the last axis grouped, computed on the device (f64 per group, the
-    reference's host arithmetic) with no host round trip; same shape, f32."""
+    reference's host arithmetic) with no host round trip; same shape, f32. The reference's result
+    has the rewards' dtype through `from_f64s`, which stores 16-bit dtypes as f32 (fdisp,
+    float.rs:256-260): bf16 and f16 rewards, read exactly widened, give f32 as well."""
     norm, eps, unbiased = _norm(norm, eps, unbiased)
     if len(rewards.shape) == 0:
         raise ValueError("group_advantages_tensor: rewards of rank 0")
-    if rewards.dtype != "f32":
-        raise ValueError(f"group_advantages_tensor: rewards of dtype {rewards.dtype} (f32)")
+    if rewards.dtype not in ("f32",) + _HALF:
+        raise ValueError(f"group_advantages_tensor: rewards of dtype {rewards.dtype} (f32, bf16 or f16)")
     if norm not in ("mean", "std"):
         raise ValueError(f"group_advantages: norm {norm!r} (mean or std)")
     n = rewards.shape[-1]
+    if rewards.dtype in _HALF:
+        import noetic_ops as ops  # (noetic_ops imports this module)
+        rewards = ops.cast(rewards, ops.Layout.contiguous(rewards.shape), "f32")  # exact
     out = Tensor(rewards.shape, "f32")
     _check(lib().nt_hip_rl_group_advantages(rewards.ptr, rewards.numel // max(n, 1), n, 1 if norm == "std" else 0,
                                             float(eps), 1 if unbiased else 0, out.ptr), "group_advantages")

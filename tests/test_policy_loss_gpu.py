@@ -285,6 +285,15 @@ def test_group_advantages_on_the_device():
             got = nr.group_advantages_tensor(t(rw, (G, n)), norm, eps, unb).to_numpy().ravel()
             want = O.group_advantages(rw.astype(np.float64).ravel(), n, norm, eps, unb).astype(np.float32)
             assert np.array_equal(got, want), (G, n, norm, int((got != want).sum()))
+    # 16-bit rewards are read exactly widened, and the result is f32, as from_f64s stores a
+    # 16-bit dtype (float.rs:256-260)
+    rw = rng.normal(0, 1, (512, 8)).astype(np.float32)
+    rb, rh = O.bf16_from_f32(rw), rw.astype(np.float16)
+    for raw, dt, wide in ((rb, "bf16", O.bf16_to_f32(rb)), (rh.view(np.uint16), "f16", rh.astype(np.float32))):
+        adv = nr.group_advantages_tensor(nr.Tensor.from_numpy(raw, dt), "std", 1e-6, True)
+        assert adv.dtype == "f32"
+        want = O.group_advantages(wide.astype(np.float64).ravel(), 8, "std", 1e-6, True).astype(np.float32)
+        assert np.array_equal(adv.to_numpy().ravel(), want), dt
 
 
 def test_check_scored_finite_and_the_debug_refusal():
