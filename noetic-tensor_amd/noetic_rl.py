@@ -446,6 +446,8 @@ class Tensor:
         a = self.to_numpy()
         if self.dtype == "bf16":
             return (a.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+        if self.dtype == "f16":
+            return a.view(np.float16).astype(np.float64)
         return a.astype(np.float64)
 
     def dims(self):
@@ -988,9 +990,24 @@ def score(logits, ref_logits, tokens: Optional[Tensor], entropy=True, kl=True):
     return lp, rlp, k, ent
 
 
+def _f32_storage(t: Optional[Tensor], what: str) -> Optional[Tensor]:
+    """A per-token float argument as the f32 values the kernels read: f32 as it is, bf16 and f16
+    widened exactly on the device (the reference computes 16-bit storage in f32, fdisp,
+    float.rs:43-58); any other dtype is refused (the reference's float Tensor has no other)."""
+    if t is None or t.dtype == "f32":
+        return t
+    if t.dtype in _HALF:
+        import noetic_ops as ops  # (noetic_ops imports this module)
+        return ops.cast(t, ops.Layout.contiguous(t.shape), "f32")
+    raise ValueError(f"{what}: a float tensor (f32, bf16 or f16), not {t.dtype}")
+
+
 def _reduce(per: Tensor, mask: Optional[Tensor], reduction: TokenReduction) -> Tensor:
     if len(per.shape) != 3:
         raise ValueError("per-token values [S, B, T]")
+    if mask is not None and tuple(mask.shape) != tuple(per.shape):
+        raise AssertionError("rl: mask shape")
+    per, mask = _f32_storage(per, "reduce_tokens"), _f32_storage(mask, "rl: mask")
     S, B, T = per.shape
     reduction = TokenReduction(reduction)
     if reduction == TokenReduction.NONE:
@@ -1008,6 +1025,7 @@ def _zero_masked(per: Tensor, mask: Optional[Tensor]) -> Tensor:
         return per
     if mask.shape != per.shape:
         raise AssertionError("rl: mask shape")
+    per, mask = _f32_storage(per, "zero_masked"), _f32_storage(mask, "rl: mask")
     out = Tensor(per.shape, "f32")
     _check(lib().nt_hip_rl_zero_masked(per.ptr, mask.ptr, per.numel, out.ptr), "zero_masked")
     return out
@@ -1057,6 +1075,9 @@ def kl_estimate(logp: Tensor, ref_logp: Tensor, estimator: KlEstimator, delta_cl
         raise ValueError(f"kl_estimate: δ clamp {delta_clamp} (need b > 0)")
     if mask is not None and mask.shape != logp.shape:
         raise AssertionError("rl: mask shape")
+    same_dtype(ref_logp.dtype, logp.dtype, "sub")  # δ = ref_logp − logp (rl.rs:392)
+    logp, ref_logp = _f32_storage(logp, "kl_estimate"), _f32_storage(ref_logp, "kl_estimate")
+    mask = _f32_storage(mask, "rl: mask")
     out = Tensor(logp.shape, "f32")
     _check(lib().nt_hip_rl_kl_estimate(logp.ptr, ref_logp.ptr, None if mask is None else mask.ptr, logp.numel,
                                        int(estimator), 0.0 if delta_clamp is None else float(delta_clamp), out.ptr),
@@ -1078,6 +1099,13 @@ def reduce_tokens_backward(mask: Optional[Tensor], shape, reduction: TokenReduct
     reduction = TokenReduction(reduction)
     if upstream is not None and tuple(upstream.shape) != _reduced_shape(shape, reduction):
         raise ValueError(f"reduce_tokens backward: upstream shape {upstream.shape} for {reduction.name}")
+    if mask is not None and tuple(mask.shape) != (S, B, T):
+        raise AssertionError("rl: mask shape")
+    if local is not None and tuple(local.shape) != (S, B, T):
+        raise ValueError("reduce_tokens backward: per-token derivative [S, B, T]")
+    mask = _f32_storage(mask, "rl: mask")
+    upstream = _f32_storage(upstream, "reduce_tokens backward")
+    local = _f32_storage(local, "reduce_tokens backward")
     out = Tensor((S, B, T), "f32")
     _check(lib().nt_hip_rl_reduce_tokens_backward(None if mask is None else mask.ptr, S, B, T, int(reduction),
                                                   None if upstream is None else upstream.ptr, float(scale),
@@ -1095,6 +1123,11 @@ def kl_estimate_backward(logp: Tensor, ref_logp: Tensor, estimator: KlEstimator,
         raise ValueError("kl_estimate: logp and reference log-probabilities [S, B, T]")
     if delta_clamp is not None and not delta_clamp > 0.0:
         raise ValueError(f"kl_estimate: δ clamp {delta_clamp} (need b > 0)")
+    if mask is not None and mask.shape != logp.shape:
+        raise AssertionError("rl: mask shape")
+    same_dtype(ref_logp.dtype, logp.dtype, "sub")  # δ = ref_logp − logp (rl.rs:392)
+    logp, ref_logp = _f32_storage(logp, "kl_estimate"), _f32_storage(ref_logp, "kl_estimate")
+    mask = _f32_storage(mask, "rl: mask")
     local = Tensor(logp.shape, "f32")
     _check(lib().nt_hip_rl_kl_estimate_backward(logp.ptr, ref_logp.ptr, None if mask is None else mask.ptr,
                                                 logp.numel, int(estimator),
@@ -1187,10 +1220,21 @@ def _policy_loss(kind: int, what: str, logp: Tensor, old_logp: Optional[Tensor],
         raise ValueError("rl: old log-probabilities shape")
     if clip is not None:
         clip.check()
+    # The reference's binary ops between them (same_dtype): PG's logp · w (rl.rs:232); PPO's
+    # logp − old (rl.rs:240), then r · A with r = exp(log-ratio) computed in f32 (rl.rs:270);
+    # clip_fraction compares A with 0 only (rl.rs:303-304). A mask meets no other operand.
+    if kind == NT_LOSS_PG:
+        same_dtype(logp.dtype, weights.dtype, "mul")
+    else:
+        same_dtype(logp.dtype, old_logp.dtype, "sub")
+        if what != "clip_fraction":
+            same_dtype("f32", weights.dtype, "mul")
     if what != "clip_fraction":
         _debug_check(what, logp, mask)
         if old_logp is not None:
             _debug_check(f"{what} (old log-probabilities)", old_logp, mask)
+    logp, old_logp = _f32_storage(logp, what), _f32_storage(old_logp, what)
+    weights, mask = _f32_storage(weights, what), _f32_storage(mask, "rl: mask")
     loss, dloss, hit = Tensor(logp.shape, "f32"), Tensor(logp.shape, "f32"), Tensor(logp.shape, "f32")
     a = NtRlPolicyLossArgs(logp.ptr, None if old_logp is None else old_logp.ptr, weights.ptr,
                            None if mask is None else mask.ptr, S, B, T, kind, per_seq,

@@ -161,3 +161,38 @@ def test_the_readout_fusion_takes_one_dtype_as_matmul_does():
         # the shape check comes first
         with pytest.raises(ValueError, match="d 32 against the weight's 64"):
             nr.readout_sample_logp(Stub((4, 32), "f32"), PackedStub(64, 300, "bf16"), 0.7, None, None)
+
+
+def test_per_token_functions_keep_the_reference_dtype_rules():
+    """The losses and estimators meet their operands in the reference's binary ops (same_dtype):
+    policy_gradient_loss's logp · w (rl.rs:232), the log-ratio logp − old (rl.rs:240) and PPO's
+    r · A with r computed in f32 (rl.rs:270), kl_estimate's ref_logp − logp (rl.rs:392). Other
+    pairings, a 16-bit mask, and 16-bit operands of one dtype pass to the device (widened there)."""
+    f32, b16, h16 = (lambda d: Stub((2, 3, 4), d))("f32"), Stub((2, 3, 4), "bf16"), Stub((2, 3, 4), "f16")
+    clip = nr.Clip.symmetric(0.2)
+    msg = lambda e: str(e.value)
+    with pytest.raises(nr.DTypeError) as e:
+        nr.policy_gradient_loss(f32, b16)
+    assert msg(e) == "mul: f32 and bf16 (casts are explicit)"
+    with pytest.raises(nr.DTypeError) as e:
+        nr.clipped_policy_loss(b16, f32, f32, None, clip)
+    assert msg(e) == "sub: bf16 and f32 (casts are explicit)"
+    with pytest.raises(nr.DTypeError) as e:
+        nr.clipped_policy_loss(b16, b16, b16, None, clip)  # r = exp(logp − old) is f32
+    assert msg(e) == "mul: f32 and bf16 (casts are explicit)"
+    with pytest.raises(nr.DTypeError) as e:
+        nr.kl_estimate(f32, h16, nr.KlEstimator.K3)
+    assert msg(e) == "sub: f16 and f32 (casts are explicit)"
+    with pytest.raises(nr.DTypeError) as e:
+        nr.kl_estimate_backward(b16, f32, nr.KlEstimator.K1)
+    assert msg(e) == "sub: f32 and bf16 (casts are explicit)"
+    with pytest.raises(ValueError, match="a float tensor"):
+        nr.policy_gradient_loss(f32, f32, Stub((2, 3, 4), "u8"))
+    with pytest.raises(AssertionError, match="rl: mask shape"):
+        nr.kl_estimate(f32, f32, nr.KlEstimator.K1, None, Stub((2, 3, 5), "f32"))
+    for call in (lambda: nr.policy_gradient_loss(b16, b16, h16),
+                 lambda: nr.clipped_policy_loss(h16, h16, f32, b16, clip),
+                 lambda: nr.clip_fraction(b16, b16, h16, None, clip),
+                 lambda: nr.kl_estimate(h16, h16, nr.KlEstimator.K2, None, b16)):
+        with pytest.raises((AssertionError, nr.HipUnavailable)):  # past the dtype checks, at the device
+            call()

@@ -296,6 +296,45 @@ def test_group_advantages_on_the_device():
         assert np.array_equal(adv.to_numpy().ravel(), want), dt
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_16_bit_per_token_operands_are_widened(dt):
+    """16-bit log-probabilities, weights and masks (one dtype where the reference's binary ops meet
+    them; PPO's advantages f32, since its ratio is f32) give the widened f32 call's values bit for
+    bit: the reference computes 16-bit storage in f32 (fdisp, float.rs:43-58)."""
+    rng = np.random.default_rng(17)
+    sh = (2, 4, 16)
+    lp = -np.abs(rng.normal(1.0, 1.0, sh)).astype(np.float32)
+    old = (lp + rng.normal(0, 0.3, sh)).astype(np.float32)
+    w = rng.normal(0, 1, sh).astype(np.float32)
+    m = (rng.random(sh) < 0.8).astype(np.float32)
+
+    def pair(x):
+        if dt == "bf16":
+            r = O.bf16_from_f32(x)
+            return nr.Tensor.from_numpy(r, dt), nr.Tensor.from_numpy(O.bf16_to_f32(r))
+        r = x.astype(np.float16)
+        return nr.Tensor.from_numpy(r.view(np.uint16), dt), nr.Tensor.from_numpy(r.astype(np.float32))
+
+    (lp16, lp32), (old16, old32), (w16, w32), (m16, m32) = pair(lp), pair(old), pair(w), pair(m)
+    a32 = w32  # PPO's advantages stay f32 (r · A, with r f32)
+    clip = nr.Clip.symmetric(0.2).with_dual(3.0)
+    same = lambda x, y, what: (x.dtype == "f32" and x.to_numpy().tobytes() == y.to_numpy().tobytes()) or \
+        pytest.fail(f"{dt} {what}")
+    for red in (nr.TokenReduction.NONE, nr.TokenReduction.TOKEN_MEAN, nr.TokenReduction.SEQUENCE_MEAN):
+        same(nr.policy_gradient_loss(lp16, w16, m16, red), nr.policy_gradient_loss(lp32, w32, m32, red), f"pg {red}")
+        same(nr.clipped_policy_loss(lp16, old16, a32, m16, clip, red),
+             nr.clipped_policy_loss(lp32, old32, a32, m32, clip, red), f"ppo {red}")
+        for est in (nr.KlEstimator.K1, nr.KlEstimator.K3):
+            same(nr.kl_estimate(lp16, old16, est, 20.0, m16, red), nr.kl_estimate(lp32, old32, est, 20.0, m32, red),
+                 f"kl {est} {red}")
+            same(nr.kl_estimate_backward(lp16, old16, est, None, m16, red),
+                 nr.kl_estimate_backward(lp32, old32, est, None, m32, red), f"kl backward {est} {red}")
+        same(nr.policy_gradient_loss_backward(lp16, w16, m16, red),
+             nr.policy_gradient_loss_backward(lp32, w32, m32, red), f"pg backward {red}")
+    same(nr.clip_fraction(lp16, old16, w16, m16, clip), nr.clip_fraction(lp32, old32, w32, m32, clip), "clip_fraction")
+    assert nr.check_scored_finite("t", lp16, m16) is None
+
+
 def test_check_scored_finite_and_the_debug_refusal():
     # tests/rl.rs:836-855: a -inf at a scored position is named; at a masked position it passes
     lp = t([-1.0, -np.inf, -2.0], (1, 1, 3))
