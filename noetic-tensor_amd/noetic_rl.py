@@ -637,6 +637,20 @@ def _rows(x: Tensor):
     return x.numel // V, V
 
 
+def _row_arg(t: Optional[Tensor], rows: int, dtype: str, what: str) -> Optional[Tensor]:
+    """A per-row device argument the kernels read `rows` values of `dtype` from: checked here,
+    before any launch (16-bit floats where f32 is read are widened exactly on the device)."""
+    if t is None:
+        return None
+    if t.numel != rows:
+        raise ValueError(f"{what}: {t.numel} values for {rows} rows")
+    if t.dtype == dtype:
+        return t
+    if dtype == "f32":
+        return _f32_storage(t, what)
+    raise ValueError(f"{what}: dtype {t.dtype} ({dtype})")
+
+
 def sample_logp(logits: Tensor, temperature: float, mask: Optional[Tensor], rng: Optional[Rng],
                 entropy: bool = False, uniforms: Optional[Tensor] = None, check: bool = True):
     """sample_categorical_inv_cdf with its log-probabilities, the fused path: (ids, logp[,
@@ -653,6 +667,7 @@ def sample_logp(logits: Tensor, temperature: float, mask: Optional[Tensor], rng:
         if rng is None:
             raise ValueError("sample_categorical: a stream is needed at temperature > 0")
         uniforms = Tensor.from_numpy(rng.uniforms(rows), "f64")
+    uniforms = _row_arg(uniforms, rows, "f64", "sample_categorical: uniforms")
     ids = IntTensor(out_shape)
     lp = Tensor(out_shape, "f32")
     ent = Tensor(out_shape, "f32") if entropy else None
@@ -831,6 +846,7 @@ def readout_sample_logp(hidden: Tensor, weight: PackedReadout, temperature: floa
         if rng is None:
             raise ValueError("sample_categorical: a stream is needed at temperature > 0")
         uniforms = Tensor.from_numpy(rng.uniforms(rows), "f64")
+    uniforms = _row_arg(uniforms, rows, "f64", "sample_categorical: uniforms")
     ids, lp, status = IntTensor(out_shape), Tensor(out_shape, "f32"), Tensor(out_shape, "u8")
     dbg = ((Tensor(out_shape + (V,), "f32"), Tensor(out_shape + (32,), "f32"), IntTensor(out_shape)) if debug
            else (None, None, None))
@@ -902,6 +918,7 @@ def _score(policy, ref, tokens, want_logp, want_ref_logp, want_kl, want_ent, wan
     out_shape = p.logits.shape[:-1]
     if tokens is not None and tokens.shape != out_shape:
         raise ValueError("token_log_probs: tokens shape (the logits' without the vocabulary axis)")
+    tokens = _row_arg(tokens, rows, "i32", "token_log_probs: tokens")
     mk = lambda want: Tensor(out_shape, "f32") if want else None
     lp, rlp, kl, ent = mk(want_logp), mk(want_ref_logp), mk(want_kl), mk(want_ent)
     stats = None
@@ -952,6 +969,16 @@ def score_grad(logits, ref_logits, tokens: Optional[Tensor], stats: RowStats, kl
     temperature's divide. `grad_dtype` defaults to the logits' dtype."""
     p = _as_tempered(logits)
     rows, V = _rows(p.logits)
+    if ref_logits is not None and (tuple(_as_tempered(ref_logits).logits.shape) != tuple(p.logits.shape) or
+                                   _as_tempered(ref_logits).logits.dtype != p.logits.dtype):
+        raise ValueError("categorical_kl: reference logits shape")
+    tokens = _row_arg(tokens, rows, "i32", "token_log_probs: tokens")
+    kl, entropy = _row_arg(kl, rows, "f32", "score backward: kl"), _row_arg(entropy, rows, "f32", "score backward: entropy")
+    g_logp = _row_arg(g_logp, rows, "f32", "score backward: g_logp")
+    g_kl = _row_arg(g_kl, rows, "f32", "score backward: g_kl")
+    g_entropy = _row_arg(g_entropy, rows, "f32", "score backward: g_entropy")
+    for f in ("lse_base", "lse_rest", "ref_lse_base", "ref_lse_rest"):
+        _row_arg(getattr(stats, f), rows, "f32", f"score backward: {f}")
     kind, mptr, mld, mrows, _keep = _mask_fields(p, rows, V)
     gdt = grad_dtype or p.logits.dtype
     gcode = {"f32": NT_F32, "bf16": NT_BF16, "f16": NT_F16}.get(gdt)

@@ -196,3 +196,23 @@ def test_per_token_functions_keep_the_reference_dtype_rules():
                  lambda: nr.kl_estimate(h16, h16, nr.KlEstimator.K2, None, b16)):
         with pytest.raises((AssertionError, nr.HipUnavailable)):  # past the dtype checks, at the device
             call()
+
+
+def test_per_row_arguments_are_checked_before_any_launch():
+    """Uniforms, tokens, upstream gradients and saved statistics are read as rows of f64, i32 or
+    f32 by the kernels: a wrong dtype or count is refused before any device call."""
+    x = Stub((2, 3, 50), "f32")
+    with pytest.raises(ValueError, match=r"uniforms: dtype f32 \(f64\)"):
+        nr.sample_logp(x, 0.7, None, None, uniforms=Stub((6,), "f32"))
+    with pytest.raises(ValueError, match="uniforms: 5 values for 6 rows"):
+        nr.sample_logp(x, 0.7, None, None, uniforms=Stub((5,), "f64"))
+    with pytest.raises(ValueError, match=r"tokens: dtype u8 \(i32\)"):
+        nr.token_log_probs(x, Stub((2, 3), "u8"))
+    st = nr.RowStats(Stub((2, 3), "f32"), Stub((2, 3), "f32"))
+    with pytest.raises(ValueError, match="g_logp: 5 values for 6 rows"):
+        nr.score_grad(x, None, Stub((2, 3), "i32"), st, g_logp=Stub((5,), "f32"))
+    with pytest.raises(ValueError, match=r"g_entropy: a float tensor"):
+        nr.score_grad(x, None, None, st, entropy=Stub((2, 3), "f32"), g_entropy=Stub((2, 3), "i32"))
+    with pytest.raises(ValueError, match="lse_rest: 4 values for 6 rows"):
+        nr.score_grad(x, None, None, nr.RowStats(Stub((2, 3), "f32"), Stub((4,), "f32")),
+                      entropy=Stub((2, 3), "f32"), g_entropy=Stub((2, 3), "f32"))
