@@ -108,28 +108,45 @@ void launch_rr(int dtype, int mk, int K, bool ent, bool allw, const SampleP &p, 
 }
 
 // The queued sampler (u8 keep-masks): K chunks per wave in stages of 4 (K = 4) or 8 (K = 16)
-// chunks, two stages from K = 8 on.
-template <int DT, int K>
+// chunks, two stages from K = 8 on; SH when mask rows are shared by several logits rows.
+template <int DT, int K, bool SH>
 void launch_rq_k(bool ent, const SampleP &p, int64_t rows, hipStream_t s) {
     constexpr int NS = K >= 8 ? 2 : 1;
     char nm[96];
-    std::snprintf(nm, sizeof nm, "nt::k_sample_rq<%d, %d, %s, %d>", DT, K, rtc_bool(ent), NS);
-    if (ent) launch_path(k_sample_rq<DT, K, true, NS>, nm, dim3(unsigned(rows)), dim3(kRRThreads), 0, s, p);
-    else launch_path(k_sample_rq<DT, K, false, NS>, nm, dim3(unsigned(rows)), dim3(kRRThreads), 0, s, p);
+    std::snprintf(nm, sizeof nm, "nt::k_sample_rq<%d, %d, %s, %d, %s>", DT, K, rtc_bool(ent), NS, rtc_bool(SH));
+    if (ent) launch_path(k_sample_rq<DT, K, true, NS, SH>, nm, dim3(unsigned(rows)), dim3(kRRThreads), 0, s, p);
+    else launch_path(k_sample_rq<DT, K, false, NS, SH>, nm, dim3(unsigned(rows)), dim3(kRRThreads), 0, s, p);
+}
+
+template <int DT, bool SH>
+void launch_rq_dt(int K, bool ent, const SampleP &p, int64_t rows, hipStream_t s) {
+    if (K == 4) {
+        launch_rq_k<DT, 4, SH>(ent, p, rows, s);
+    } else if constexpr (DT == NT_F32) {
+        launch_rq_k<DT, 8, SH>(ent, p, rows, s);  // (f32 rows take at most 8 chunks per wave)
+    } else {
+        if (K == 8) launch_rq_k<DT, 8, SH>(ent, p, rows, s);
+        else launch_rq_k<DT, 16, SH>(ent, p, rows, s);
+    }
+}
+
+// Whether several of the launch's logits rows read one mask row: a stride 0 over a dimension of
+// the row map longer than one (rows = S T B).
+bool mask_shared(const MaskMap &m, int64_t rows) {
+    return (m.ld == 0 && m.T > 1u) || (m.ld_b == 0 && m.B > 1u) || (m.ld_s == 0 && rows > int64_t(m.T) * m.B);
 }
 
 void launch_rq(int dtype, int K, bool ent, const SampleP &p, int64_t rows, hipStream_t s) {
+    const bool sh = mask_shared(p.mm, rows);
     if (dtype == NT_F32) {
-        if (K == 4) launch_rq_k<NT_F32, 4>(ent, p, rows, s);
-        else launch_rq_k<NT_F32, 8>(ent, p, rows, s);
+        if (sh) launch_rq_dt<NT_F32, true>(K, ent, p, rows, s);
+        else launch_rq_dt<NT_F32, false>(K, ent, p, rows, s);
     } else if (dtype == NT_BF16) {
-        if (K == 4) launch_rq_k<NT_BF16, 4>(ent, p, rows, s);
-        else if (K == 8) launch_rq_k<NT_BF16, 8>(ent, p, rows, s);
-        else launch_rq_k<NT_BF16, 16>(ent, p, rows, s);
+        if (sh) launch_rq_dt<NT_BF16, true>(K, ent, p, rows, s);
+        else launch_rq_dt<NT_BF16, false>(K, ent, p, rows, s);
     } else {
-        if (K == 4) launch_rq_k<NT_F16, 4>(ent, p, rows, s);
-        else if (K == 8) launch_rq_k<NT_F16, 8>(ent, p, rows, s);
-        else launch_rq_k<NT_F16, 16>(ent, p, rows, s);
+        if (sh) launch_rq_dt<NT_F16, true>(K, ent, p, rows, s);
+        else launch_rq_dt<NT_F16, false>(K, ent, p, rows, s);
     }
 }
 

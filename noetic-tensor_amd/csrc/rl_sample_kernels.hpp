@@ -690,7 +690,10 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rr(SampleP p) {
 // path.
 constexpr int kRqDensePct = 70;
 
-template <int DT, int K, bool ENT, int NS>
+// SH: the launch's mask rows are each read by several logits rows (a stride 0 over a dimension
+// longer than one, mask_shared): they are loaded through the caches, where the other rows find
+// them; otherwise each row's mask is read once, non-temporal.
+template <int DT, int K, bool ENT, int NS, bool SH>
 __global__ __launch_bounds__(kRRThreads) void k_sample_rq(SampleP p) {
     constexpr int MK = NT_MASK_U8;
     constexpr int EPL = 8;
@@ -734,6 +737,7 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rq(SampleP p) {
     // Every wave zeroes the empty lane's words itself (the same bits), so its own reads of
     // them follow its own store.
     if (lane < 2) zmask[lane] = 0u;
+    constexpr int kMaskPolicy = SH ? 0 : kCachePolicyNT;
 
     RRX<DT, EPL> raw[K];  // slot k's logit words
     uint32_t ma[K];       // slot k: the LDS address of this lane's group's mask bytes (zmask: none)
@@ -749,7 +753,7 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rq(SampleP p) {
         static_for<0, MD>([&](auto dc) {
             constexpr int d = decltype(dc)::value;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(mres, (lds_ptr_t)(mlds + b0 + d * 1024), 16,
-                                                     b0 + d * 1024 + 16 * lane, 0, 0, kCachePolicyNT);
+                                                     b0 + d * 1024 + 16 * lane, 0, 0, kMaskPolicy);
         });
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -926,7 +930,7 @@ __global__ __launch_bounds__(kRRThreads) void k_sample_rq(SampleP p) {
                 static_for<0, DMB>([&](auto dc) {
                     constexpr int d = decltype(dc)::value;
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(mres, (lds_ptr_t)(mlds + ch * CH + d * 4 * kWave), 4,
-                                                             ch * CH + d * 4 * kWave + 4 * lane, 0, 0, kCachePolicyNT);
+                                                             ch * CH + d * 4 * kWave + 4 * lane, 0, 0, kMaskPolicy);
                 });
             }
             __builtin_amdgcn_sched_barrier(0);
