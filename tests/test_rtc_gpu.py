@@ -72,10 +72,11 @@ def test_c4_parity_and_rerun_bits_through_both_paths():
     check_sample("c4 (aot = rtc)", z, u, ids, lp, bf16=False)
 
 
-@pytest.mark.parametrize("case", ["c2_f32_entropy", "seg_bf16_16rows", "stream_unaligned_f32"])
+@pytest.mark.parametrize("case", ["c2_f32_entropy", "seg_bf16_16rows", "stream_unaligned_f32", "queued_shared_mask"])
 def test_each_sampler_kernel_is_byte_identical_through_both_paths(case):
     """One call per kernel family: the register-resident sampler with entropy (C2), the segmented
-    sampler (16 rows of V = 128256), the streaming sampler (unaligned rows)."""
+    sampler (16 rows of V = 128256), the streaming sampler (unaligned rows), and the queued
+    sampler's instance for a mask row shared by every row (C4's shape, 128 rows)."""
     rng = np.random.default_rng(7)
     if case == "c2_f32_entropy":
         w = W.c2()
@@ -85,6 +86,9 @@ def test_each_sampler_kernel_is_byte_identical_through_both_paths(case):
         xt = nr.Tensor.from_numpy(O.bf16_from_f32(rng.normal(0, 2, (rows, V)).astype(np.float32)), "bf16")
         mt = nr.Tensor.from_numpy((rng.random((rows, V)) < 0.9).astype(np.uint8))
         tau = 0.7
+    elif case == "queued_shared_mask":
+        w = W.c4(seed=13, rows=128, shared_mask=True)
+        rows, xt, mt, tau = w["rows"], w["logits"], w["mask"], w["temperature"]
     else:
         rows, V = 33, 1001
         xt = nr.Tensor.from_numpy(rng.normal(0, 3, (rows, V)).astype(np.float32))
@@ -93,6 +97,12 @@ def test_each_sampler_kernel_is_byte_identical_through_both_paths(case):
     u = nr.Tensor.from_numpy(nr.Rng(11, case).uniforms(rows), "f64")
     aot, rtc1, rtc2 = both_paths(lambda: nr.sample_logp(xt, tau, mt, None, entropy=True, uniforms=u))
     assert rtc1 == aot and rtc2 == aot, f"{case}: hiprtc and hipcc code objects disagree"
+    if case == "queued_shared_mask":
+        # the shared row read through the caches gives the bits of the same mask materialised per
+        # row (each row's own mask, read non-temporal)
+        full = nr.Tensor.from_numpy(np.ascontiguousarray(np.broadcast_to(mt.to_numpy(), (1, rows, 1, mt.shape[-1]))))
+        got = nr.sample_logp(xt, tau, full, None, entropy=True, uniforms=u)
+        assert [t.to_numpy().tobytes() for t in got] == aot, "shared and materialised masks differ"
 
 
 @pytest.mark.parametrize("case", ["c3_bf16_aligned", "f32_masked_tempered_unaligned"])
