@@ -807,14 +807,34 @@ def _readout_shape(hidden: Tensor, weight: PackedReadout, who: str):
     return S, N, d
 
 
-def _readout_mask_ld(mask: Optional[Tensor], rows: int, V: int) -> int:
-    """The readout mask's row stride: V for one u8 row per logits row, 0 for one row [.., V] that
-    every row shares."""
+def _readout_mask_ld(mask: Optional[Tensor], rows: int, V: int, seeds: int = 1):
+    """(row stride, stride between seeds) of the readout's u8 keep-mask [.., V]: one row per
+    logits row (V, rows / seeds V), one row per seed shared by that seed's rows (0, V; the
+    seed-batched head's [S, 1, V]), or one row shared by every row (0, 0)."""
     if mask is None:
-        return 0
-    if mask.dtype != "u8" or mask.numel not in (V, rows * V) or mask.shape[-1] != V:
-        raise ValueError("readout: a u8 keep-mask [.., V], one row per logits row or one shared row")
-    return V if mask.numel == rows * V and rows > 1 else 0
+        return 0, 0
+    if mask.dtype != "u8" or mask.shape[-1] != V:
+        raise ValueError("readout: a u8 keep-mask [.., V]")
+    if mask.numel == rows * V and rows > 1:
+        return V, (rows // seeds) * V
+    if mask.numel == V:
+        return 0, 0
+    if seeds > 1 and mask.numel == seeds * V:
+        return 0, V
+    raise ValueError("readout: a u8 keep-mask with one row per logits row, one per seed, or one shared row "
+                     "(or one that broadcasts to the logits' shape)")
+
+
+def _readout_mask(mask: Optional[Tensor], logits_shape, rows: int, V: int, seeds: int):
+    """The readout's mask and its (row, seed) strides: the forms _readout_mask_ld reads in place,
+    or a mask of the logits' rank that broadcasts to them (rl.rs:477-483), broadcast on the
+    device first."""
+    if mask is not None and mask.dtype == "u8" and mask.shape[-1] == V and len(mask.shape) == len(logits_shape) \
+            and mask.numel not in (V, rows * V) and not (seeds > 1 and mask.numel == seeds * V) \
+            and all(a == b or a == 1 for a, b in zip(mask.shape, logits_shape)):
+        import noetic_ops as ops  # (noetic_ops imports this module)
+        mask = ops.copy(mask, ops.Layout.contiguous(mask.shape).broadcast(tuple(logits_shape)))
+    return (mask,) + _readout_mask_ld(mask, rows, V, seeds)
 
 
 def _readout_chunks(S: int, N: int):
@@ -841,7 +861,7 @@ def readout_sample_logp(hidden: Tensor, weight: PackedReadout, temperature: floa
     S, N, d = _readout_shape(hidden, weight, "readout")
     rows, V, es = S * N, weight.vocab, _ESIZE[hidden.dtype]
     out_shape = hidden.shape[:-1]
-    mld = _readout_mask_ld(mask, rows, V)
+    mask, mld, msd = _readout_mask(mask, tuple(out_shape) + (V,), rows, V, S)
     if temperature != 0.0 and uniforms is None:
         if rng is None:
             raise ValueError("sample_categorical: a stream is needed at temperature > 0")
@@ -852,9 +872,11 @@ def readout_sample_logp(hidden: Tensor, weight: PackedReadout, temperature: floa
            else (None, None, None))
     for k, g0, n in _readout_chunks(S, N):
         at = lambda t, w: None if t is None else t.ptr + g0 * w
+        # this call's first mask row: its seed's rows, then its place among them
+        mask_at = lambda k, g0: None if mask is None else mask.ptr + k * msd + (g0 - k * N) * mld
         a = NtRlReadoutSampleArgs(at(hidden, d * es), weight.seed_ptr(k if weight.batched else 0), n, V, d, d,
                                   NT_MASK_U8 if mask is not None else NT_MASK_NONE,
-                                  _DTCODE[hidden.dtype], at(mask, mld),
+                                  _DTCODE[hidden.dtype], mask_at(k, g0),
                                   mld, float(temperature), at(uniforms, 8), at(ids, 4),
                                   at(lp, 4), at(status, 1), at(dbg[0], V * 4), at(dbg[1], 32 * 4), at(dbg[2], 4))
         _check(lib().nt_hip_rl_readout_sample(C.byref(a)), "readout sample")
@@ -884,16 +906,18 @@ def readout_score(hidden: Tensor, weight: PackedReadout, temperature: float, mas
         raise ValueError("token_log_probs: tokens shape (the logits' without the vocabulary axis)")
     if tokens is None and not entropy:
         raise ValueError("readout_score: neither log-probabilities nor the entropy asked for")
-    mld = _readout_mask_ld(mask, rows, V)
+    mask, mld, msd = _readout_mask(mask, tuple(out_shape) + (V,), rows, V, S)
     lp = Tensor(out_shape, "f32") if tokens is not None else None
     ent = Tensor(out_shape, "f32") if entropy else None
     status = Tensor(out_shape, "u8")
     logits = Tensor(out_shape + (V,), "f32") if debug else None
     for k, g0, n in _readout_chunks(S, N):
         at = lambda t, w: None if t is None else t.ptr + g0 * w
+        # this call's first mask row: its seed's rows, then its place among them
+        mask_at = lambda k, g0: None if mask is None else mask.ptr + k * msd + (g0 - k * N) * mld
         a = NtRlReadoutScoreArgs(at(hidden, d * es), weight.seed_ptr(k if weight.batched else 0), n, V, d, d,
                                  NT_MASK_U8 if mask is not None else NT_MASK_NONE,
-                                 _DTCODE[hidden.dtype], at(mask, mld),
+                                 _DTCODE[hidden.dtype], mask_at(k, g0),
                                  mld, float(temperature), at(tokens, 4), at(lp, 4),
                                  at(ent, 4), at(status, 1), at(logits, V * 4))
         _check(lib().nt_hip_rl_readout_score(C.byref(a)), "readout score")

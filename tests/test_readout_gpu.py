@@ -293,6 +293,41 @@ def test_seed_batched_head():
                                uniforms=nr.Tensor.from_numpy(u[:N], "f64"))
 
 
+def test_readout_masks_per_seed_and_broadcast():
+    """A seed-batched head's mask with one row per seed ([S, 1, V], read in place: each seed's calls
+    share its row) and a mask broadcast over a leading dimension ([B, 1, V] against hidden
+    [B, T, d], broadcast on the device first) give the bits of the same mask materialised per
+    row."""
+    S, N, d, V, tau = 2, 300, 64, 1000, 0.8
+    h = W.normal((S, N, d), "bf16", 21, "readout/seedmask/h")
+    w = nr.PackedReadout(W.normal((S, d, V), "bf16", 21, "readout/seedmask/w", std=2.0 / np.sqrt(d)), "dv")
+    rng = np.random.default_rng(21)
+    m = (rng.random((S, 1, V)) < 0.4).astype(np.uint8)
+    m[..., 9] = 1
+    full = np.ascontiguousarray(np.broadcast_to(m, (S, N, V)))
+    u = nr.Tensor.from_numpy(nr.Rng(21, "readout/seedmask/u").uniforms(S * N), "f64")
+    a = nr.readout_sample_logp(h, w, tau, nr.Tensor.from_numpy(m), None, uniforms=u)
+    b = nr.readout_sample_logp(h, w, tau, nr.Tensor.from_numpy(full), None, uniforms=u)
+    assert all(x.to_numpy().tobytes() == y.to_numpy().tobytes() for x, y in zip(a, b)), "per-seed mask"
+    sa = nr.readout_score(h, w, tau, nr.Tensor.from_numpy(m), a[0])
+    sb = nr.readout_score(h, w, tau, nr.Tensor.from_numpy(full), a[0])
+    assert all(x.to_numpy().tobytes() == y.to_numpy().tobytes() for x, y in zip(sa, sb)), "per-seed mask, scorer"
+    assert sa[0].to_numpy().tobytes() == a[1].to_numpy().tobytes(), "scoring the draws gives their logp"
+    # unbatched head, hidden [B, T, d], mask [B, 1, V]
+    B, T = 6, 50
+    h2 = W.normal((B, T, d), "bf16", 22, "readout/bcast/h")
+    w2 = nr.PackedReadout(W.normal((d, V), "bf16", 22, "readout/bcast/w", std=2.0 / np.sqrt(d)), "dv")
+    m2 = (rng.random((B, 1, V)) < 0.4).astype(np.uint8)
+    m2[..., 4] = 1
+    full2 = np.ascontiguousarray(np.broadcast_to(m2, (B, T, V)))
+    u2 = nr.Tensor.from_numpy(nr.Rng(22, "readout/bcast/u").uniforms(B * T), "f64")
+    a2 = nr.readout_sample_logp(h2, w2, tau, nr.Tensor.from_numpy(m2), None, uniforms=u2)
+    b2 = nr.readout_sample_logp(h2, w2, tau, nr.Tensor.from_numpy(full2), None, uniforms=u2)
+    assert all(x.to_numpy().tobytes() == y.to_numpy().tobytes() for x, y in zip(a2, b2)), "broadcast mask"
+    with pytest.raises(ValueError, match="keep-mask"):
+        nr.readout_sample_logp(h2, w2, tau, nr.Tensor.from_numpy(m2[:, :, :V - 1].copy()), None, uniforms=u2)
+
+
 @pytest.mark.parametrize("rows,V,d", [(40, 1000, 256), (256, 4104, 64)])
 def test_readout_shared_mask_row(rows, V, d):
     # one grammar mask [1, V] shared by every row (mask_ld 0) gives the materialised mask's results
