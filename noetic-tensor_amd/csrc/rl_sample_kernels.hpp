@@ -43,7 +43,9 @@ __global__ __launch_bounds__(1024) void k_sample(SampleP p) {
             if (c < p.nc) {
             float v[kEpl];
             decode<DT, MK>(raw[b], v, p.tau, tau_one);
-            const float cm = wave_max(max8(v));
+            // (cross-lane steps by DPP, no LDS round trips: the sums' order is fixed, rows of 16
+            // lanes and then the four rows in order)
+            const float cm = wave_max3_dpp(max8_hw(v));
             const float sh = (cm == -INFINITY) ? 0.0f : cm;
             float w[kEpl], h[kEpl];
 #pragma unroll
@@ -52,9 +54,13 @@ __global__ __launch_bounds__(1024) void k_sample(SampleP p) {
                 w[j] = exp2_hw(d);
                 if constexpr (ENT) h[j] = w[j] * fmaxf(d, -FLT_MAX);
             }
-            const float cs = wave_sum(tree8(w));
+            auto rows4 = [](float x) {
+                const float r = row_sum_dpp(x);
+                return ((readlane_f(r, 0) + readlane_f(r, 16)) + readlane_f(r, 32)) + readlane_f(r, 48);
+            };
+            const float cs = rows4(tree8(w));
             float ce = 0.0f;
-            if constexpr (ENT) ce = wave_sum(tree8(h));
+            if constexpr (ENT) ce = rows4(tree8(h));
             if (lane == 0) {
                 cmax[c] = cm;
                 csum[c] = cs;
