@@ -29,13 +29,46 @@ __global__ __launch_bounds__(1024) void k_sample(SampleP p) {
     if constexpr (MK != NT_MASK_NONE) mrow = static_cast<const char *>(p.mask) + mask_row_at(p.mm, row) * MaskWords<MK>::kBytes;
 
     // ---- phase 1: stream the row once, per-chunk (max, sum exp[, sum exp * d]) into LDS.
+    // Aligned 16-bit rows (below 2^31 bytes of mask) load through per-row buffer resources,
+    // non-temporal (every input is read once); a group past the row's end reads zeros and is set
+    // to -inf (a lane's 8 elements lie wholly inside the row or wholly past it, V % 8 == 0).
+    constexpr bool kBuf = AL && DT != NT_F32;
+    const int Vb = kBuf ? int(p.V) : 0;
+    const __amdgpu_buffer_rsrc_t xres =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(xrow), short(0), Vb * Elem<DT>::kBytes, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t mres =
+        MK != NT_MASK_NONE ? __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(mrow), short(0),
+                                                               Vb * MaskWords<MK>::kBytes, kBufferWord3)
+                           : xres;
     for (int c0 = wave; c0 < p.nc; c0 += nw * kBatch) {
         Raw<DT, MK> raw[kBatch];
 #pragma unroll
         for (int b = 0; b < kBatch; b++) {
             const int c = c0 + b * nw;
             const int64_t e0 = int64_t(c < p.nc ? c : 0) * kChunk + lane * kEpl;
-            load_raw<DT, MK, AL>(raw[b], xrow, mrow, c < p.nc ? e0 : p.V, p.V);
+            if constexpr (kBuf) {
+                const int eb = c < p.nc ? int(e0) : Vb;
+                const auto xa = __builtin_amdgcn_raw_buffer_load_b128(xres, eb * 2, 0, kCachePolicyNT);
+                for (int i = 0; i < 4; i++) raw[b].x[i] = xa[i];
+                if constexpr (MK == NT_MASK_U8) {
+                    const auto k = __builtin_amdgcn_raw_buffer_load_b64(mres, eb, 0, kCachePolicyNT);
+                    raw[b].m[0] = k[0];
+                    raw[b].m[1] = k[1];
+                } else if constexpr (MK == NT_MASK_F32) {
+#pragma unroll
+                    for (int q = 0; q < 2; q++) {
+                        const auto a = __builtin_amdgcn_raw_buffer_load_b128(mres, eb * 4 + 16 * q, 0, kCachePolicyNT);
+                        for (int i = 0; i < 4; i++) raw[b].m[4 * q + i] = a[i];
+                    }
+                } else {
+                    raw[b].m[0] = 0;
+                }
+                if (eb >= Vb) {
+                    for (int i = 0; i < 4; i++) raw[b].x[i] = Elem<DT>::kNegInf;
+                }
+            } else {
+                load_raw<DT, MK, AL>(raw[b], xrow, mrow, c < p.nc ? e0 : p.V, p.V);
+            }
         }
 #pragma unroll
         for (int b = 0; b < kBatch; b++) {
