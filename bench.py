@@ -9,9 +9,11 @@ library's own stream; the same launches re-reading one input are reported as `wa
 bytes per launch / average launch time against the 8 TB/s HBM peak) and a `cpu_baseline`
 object (the reference's Cpu(Reference) op sequence, restated in oracle/, timed on this host).
 
-`--workload c4s|c4g|c2|c3|c3b|c5|matmul|readout` measures the other configurations the same way, one JSON
-line each:
+`--workload c4s|c4f|c4g|c2|c3|c3b|c5|matmul|readout` measures the other configurations the same way, one
+JSON line each:
   c4s C4 with one u8 grammar mask [1,V] shared by every row (mask_ld 0);
+  c4f C4's rows under the reference's own mask form, the same grammar mask as an f32 additive
+      0 / -inf mask [256,V] (the streaming sampler);
   c4g C4's rows through the reference's own Gumbel-max sample_categorical (one u64 per logit,
       generated on the device at the stream's position; nt_hip_rl_sample_gumbel);
   c2  decode step, f32 [1,64,1,32000], no mask, tau 0.8: the fused sample + logp;
@@ -326,17 +328,25 @@ def bench_sample(nr, W, args, name):
     same launches on one input, re-read every time (cache-warm, as when the logits were just
     written by the readout), are reported beside them as `warm_cache`."""
     shared = name == "c4s"  # C4 with one grammar mask [1, V] shared by every row (mask_ld 0)
+    f32mask = name == "c4f"  # C4's grammar mask as the reference's f32 additive 0 / -inf mask
 
     def mk_w(sd):
-        return W.c2(sd) if name == "c2" else W.c4(sd, shared_mask=shared)
+        if name == "c2":
+            return W.c2(sd)
+        w = W.c4(sd, shared_mask=shared)
+        if f32mask:
+            keep = w["mask"].to_numpy()
+            w["mask_f32"] = nr.Tensor.from_numpy(np.where(keep != 0, 0.0, -np.inf).astype(np.float32))
+        return w
 
     w = mk_w(args.seed)
     rows, V = w["rows"], w["V"]
     dt = nr.NT_BF16 if w["logits"].dtype == "bf16" else nr.NT_F32
-    mk = nr.NT_MASK_U8 if w["mask"] is not None else nr.NT_MASK_NONE
+    mk = nr.NT_MASK_F32 if f32mask else (nr.NT_MASK_U8 if w["mask"] is not None else nr.NT_MASK_NONE)
+    mkey = "mask_f32" if f32mask else "mask"
     esz = 2 if dt == nr.NT_BF16 else 4
     # Algorithmic bytes per launch: every input read once, every output written once.
-    mask_row = V if (mk == nr.NT_MASK_U8 and not shared) else 0
+    mask_row = 4 * V if f32mask else (V if (mk == nr.NT_MASK_U8 and not shared) else 0)
     per_row = esz * V + mask_row + 8 + 4 + 4 + 1  # logits, mask, uniform, id, logp, status
     bytes_launch = per_row * rows + (V if shared else 0)
     copies = max(2, -(-CACHE_BYTES // bytes_launch))
@@ -353,7 +363,7 @@ def bench_sample(nr, W, args, name):
         for i in range(n_launch):
             x = pick(i)
             out.append(nr.NtRlSampleArgs(x["logits"].ptr, dt, mk, rows, V, V,
-                                         x["mask"].ptr if x["mask"] is not None else None,
+                                         x[mkey].ptr if x["mask"] is not None else None,
                                          V if (x["mask"] is not None and not shared) else 0, w["temperature"],
                                          U.ptr + 8 * rows * i,
                                          ids.ptr, logp.ptr, None, status.ptr))
@@ -384,7 +394,13 @@ def bench_sample(nr, W, args, name):
     if name == "c4":
         roof["measured_copy_gbs"] = copy_peak(nr)  # a device-to-device copy on this box, for scale
         roof["practical"] = practical_floor(nr, bytes_launch, roof.get("traffic"), ms, rows)
-    if name == "c4s":
+    if name == "c4f":
+        metric = "rows/sec + achieved HBM GB/s, fused masked sample+logprob, V=128256 bf16, f32 additive mask"
+        config = {"workload": "c4 under the reference's own mask form: bf16 logits [1,256,1,128256] ~ N(0,2^2), the "
+                              "runs grammar mask as an f32 additive 0 / -inf mask [256,V] (4 bytes a token), temperature "
+                              "0.7, fused sample + logp; launches cycle over independent input copies (1 GiB in all)",
+                  "rows": rows, "vocab": V, "parallelism": "none (1 GPU)"}
+    elif name == "c4s":
         metric = "rows/sec + achieved HBM GB/s, fused masked sample+logprob, V=128256 bf16, one shared mask"
         config = {"workload": "c4 with one u8 grammar mask [1,V] shared by the 256 rows (mask_ld 0): bf16 logits "
                               "[1,256,1,128256] ~ N(0,2^2), temperature 0.7, fused sample + logp; launches cycle over "
@@ -913,7 +929,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 20; 3 for c3/c5)")
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--workload", default="c4",
-                    choices=["c4", "c4s", "c4g", "c2", "c3", "c3b", "c5", "ops", "readout", "matmul"])
+                    choices=["c4", "c4s", "c4f", "c4g", "c2", "c3", "c3b", "c5", "ops", "readout", "matmul"])
     ap.add_argument("--kernels", default="rtc", choices=["aot", "rtc"],
                     help="how the sampler kernels are loaded: hiprtc at first use, the reference's NVRTC route "
                          "(the default; compiled by the first, untimed launch, or read from the disk cache), "
@@ -954,7 +970,7 @@ def main():
         torch.zeros(1, device="cuda:0")
     nr.set_kernel_path(args.kernels)
     nr.claim(0)
-    if args.workload in ("c4", "c4s", "c2"):
+    if args.workload in ("c4", "c4s", "c4f", "c2"):
         out = bench_sample(nr, W, args, args.workload)
     elif args.workload == "c4g":
         out = bench_gumbel(nr, W, args)
