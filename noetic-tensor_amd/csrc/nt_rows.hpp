@@ -190,6 +190,34 @@ __device__ __forceinline__ float logit(const uint32_t *x, int j) {
     else return widen16<DT>((j % 2 == 0) ? (x[j / 2] & 0xffffu) : (x[j / 2] >> 16));
 }
 
+// z[j] / tau in place for tau > 0, each quotient the correctly rounded f32 of the division. The
+// f64 product of z with rt = 1 / tau (rounded to f64) lies within 2^-52 relative of the exact
+// quotient. An exact quotient of two f32 values of magnitude at least 2^-126 lies at least 2^-49
+// relative from every boundary where f32 rounding changes (the midpoints M 2^e between
+// neighbours, M odd with 2^24 <= M < 2^25, and the overflow threshold, which is one of them:
+// reaching one would take a numerator of more than 24 significant bits). So the product rounded
+// to f32 is the division's result, zeros, infinities and NaN included. Below 2^-126 the midpoints
+// are evenly spaced and a quotient can be one exactly; a wave holding such a nonzero element
+// divides those. (The f32 division is a ten-instruction sequence; this is three.)
+template <int N>
+__device__ __forceinline__ void div_tau(float *z, float tau) {
+    const double rt = 1.0 / double(tau);
+    float q[N];
+    bool tiny = false;
+#pragma unroll
+    for (int j = 0; j < N; j++) {
+        q[j] = float(double(z[j]) * rt);
+        tiny = tiny || (fabsf(q[j]) < 0x1p-126f && z[j] != 0.0f);
+    }
+    if (__builtin_amdgcn_ballot_w64(tiny)) {
+#pragma unroll
+        for (int j = 0; j < N; j++)
+            if (fabsf(q[j]) < 0x1p-126f && z[j] != 0.0f) q[j] = z[j] / tau;
+    }
+#pragma unroll
+    for (int j = 0; j < N; j++) z[j] = q[j];
+}
+
 // The "value" of an element, the quantity the kernels take maxima and exponentials of.
 //  - no mask / u8 mask: v = x (an excluded token -> -inf); the temperature is applied through
 //    the exponent scale c = log2(e)/T, and m_z = max(x)/T is exact because correctly rounded
@@ -199,6 +227,15 @@ __device__ __forceinline__ float logit(const uint32_t *x, int j) {
 template <int DT, int MK>
 __device__ __forceinline__ void decode_words(const uint32_t *xw, const uint32_t *mw, float v[kEpl], float tau,
                                              bool tau_one) {
+    if constexpr (MK == NT_MASK_F32) {
+        float z[kEpl];
+#pragma unroll
+        for (int j = 0; j < kEpl; j++) z[j] = logit<DT>(xw, j);
+        if (!tau_one) div_tau<kEpl>(z, tau);
+#pragma unroll
+        for (int j = 0; j < kEpl; j++) v[j] = z[j] + __uint_as_float(mw[j]);
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < kEpl; j++) {
         float x = logit<DT>(xw, j);
@@ -489,6 +526,15 @@ __device__ __forceinline__ float keep_byte(uint32_t mw, float x, float ninf) {
 // Decode EPL elements (logit words + mask words) into the kernel's value space.
 template <int DT, int MK, int EPL>
 __device__ __forceinline__ void decode_e(const uint32_t *xw, const uint32_t *mw, float *v, float tau, bool tau_one) {
+    if constexpr (MK == NT_MASK_F32) {
+        float z[EPL];
+#pragma unroll
+        for (int j = 0; j < EPL; j++) z[j] = logit<DT>(xw, j);
+        if (!tau_one) div_tau<EPL>(z, tau);
+#pragma unroll
+        for (int j = 0; j < EPL; j++) v[j] = z[j] + __uint_as_float(mw[j]);
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < EPL; j++) {
         const float x = logit<DT>(xw, j);

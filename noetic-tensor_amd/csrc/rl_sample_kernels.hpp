@@ -40,10 +40,20 @@ __global__ __launch_bounds__(1024) void k_sample(SampleP p) {
         MK != NT_MASK_NONE ? __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(mrow), short(0),
                                                                Vb * MaskWords<MK>::kBytes, kBufferWord3)
                            : xres;
-    for (int c0 = wave; c0 < p.nc; c0 += nw * kBatch) {
-        Raw<DT, MK> raw[kBatch];
+    // An f32 mask on such rows goes through LDS: each wave's batch of chunks has its own slots
+    // after the per-chunk records (16-byte aligned; the launch sizes them), filled by the load
+    // unit one contiguous KiB per instruction (buffer_load ... lds), where two 16-byte loads per
+    // lane 32 bytes apart would each touch every 128-byte line half.
+    constexpr bool kMl = kBuf && MK == NT_MASK_F32;
+    constexpr int kSB = kMl ? 2 : kBatch;  // chunks per wave with loads in flight together
+    constexpr int kMB = kChunk * 4;        // f32 mask bytes per chunk
+    static_assert(!kMl || kSB == 2, "the waits below count two chunks");
+    uint8_t *const mstage = reinterpret_cast<uint8_t *>(smem) + ((p.nc * (ENT ? 3 : 2) * 4 + 15) & ~15);
+    const uint32_t mslot = uint32_t((uintptr_t)(lds_ptr_t)(mstage)) + uint32_t(wave * kSB * kMB) + uint32_t(lane * 32);
+    for (int c0 = wave; c0 < p.nc; c0 += nw * kSB) {
+        Raw<DT, MK> raw[kSB];
 #pragma unroll
-        for (int b = 0; b < kBatch; b++) {
+        for (int b = 0; b < kSB; b++) {
             const int c = c0 + b * nw;
             const int64_t e0 = int64_t(c < p.nc ? c : 0) * kChunk + lane * kEpl;
             if constexpr (kBuf) {
@@ -55,24 +65,34 @@ __global__ __launch_bounds__(1024) void k_sample(SampleP p) {
                     raw[b].m[0] = k[0];
                     raw[b].m[1] = k[1];
                 } else if constexpr (MK == NT_MASK_F32) {
+                    // (a chunk past the row reads zeros)
+                    const int mb = c < p.nc ? c * kMB : Vb * 4;
+                    uint8_t *slot = mstage + (wave * kSB + b) * kMB;
 #pragma unroll
-                    for (int q = 0; q < 2; q++) {
-                        const auto a = __builtin_amdgcn_raw_buffer_load_b128(mres, eb * 4 + 16 * q, 0, kCachePolicyNT);
-                        for (int i = 0; i < 4; i++) raw[b].m[4 * q + i] = a[i];
-                    }
+                    for (int d = 0; d < 2; d++)
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(mres, (lds_ptr_t)(slot + d * 1024), 16,
+                                                                 mb + d * 1024 + 16 * lane, 0, 0, kCachePolicyNT);
                 } else {
                     raw[b].m[0] = 0;
                 }
                 if (eb >= Vb) {
                     for (int i = 0; i < 4; i++) raw[b].x[i] = Elem<DT>::kNegInf;
                 }
+                // (each chunk's three loads stay together, in chunk order, for the waits below)
+                if constexpr (kMl) __builtin_amdgcn_sched_barrier(0);
             } else {
                 load_raw<DT, MK, AL>(raw[b], xrow, mrow, c < p.nc ? e0 : p.V, p.V);
             }
         }
 #pragma unroll
-        for (int b = 0; b < kBatch; b++) {
+        for (int b = 0; b < kSB; b++) {
             const int c = c0 + b * nw;
+            if constexpr (kMl) {
+                // chunk b's three loads are done once at most the later chunk's three are out
+                if (b == 0) wait_vmcnt<3>();
+                else wait_vmcnt<0>();
+                lds_mask_words<NT_MASK_F32, kEpl>(mslot + uint32_t(b * kMB), raw[b].m);
+            }
             if (c < p.nc) {
             float v[kEpl];
             decode<DT, MK>(raw[b], v, p.tau, tau_one);

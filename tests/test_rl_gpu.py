@@ -426,6 +426,56 @@ def test_sampler_mask_layouts_against_the_oracle(case):
     check_sample(f"{case}", z, u, ids, lp, ent, bf16=False)
 
 
+
+@pytest.mark.parametrize("case", [
+    # (dtype, V, rows, one shared mask row, temperature, entropy, NOETIC_HIP_SAMPLE_RR)
+    ("bf16", 128256, 96, False, 0.7, True, None),   # C4's vocabulary: 251 chunks, the last half full; 16 waves
+    ("f16", 40000, 72, False, 1.0, False, None),    # 79 chunks
+    ("bf16", 32776, 80, False, 0.0, False, None),   # greedy; 65 chunks, the last of 8 elements
+    ("bf16", 33280, 2048, True, 0.9, True, None),   # 2048 rows: 4 waves per row; one mask row for all
+    ("bf16", 4104, 40, False, 0.8, True, "off"),    # 9 chunks: 2 waves (the streaming kernel forced)
+    ("f16", 1032, 24, False, 1.3, True, "off"),     # 3 chunks: 1 wave
+])
+def test_streaming_sampler_f32_masks_on_16_bit_rows(case, monkeypatch):
+    """An additive f32 mask on aligned 16-bit rows longer than the register-resident kernel holds
+    (V > 32768 there) takes the streaming sampler, which stages each wave's mask words through
+    LDS, two chunks at a time. Masks mix -inf, -1e9 and finite values; rows, chunk counts and
+    wave counts cover a partial last chunk, 1, 2, 4 and 16 waves per row and a shared mask row."""
+    dtype, V, rows, shared, tau, want_ent, rr = case
+    if rr:
+        monkeypatch.setenv("NOETIC_HIP_SAMPLE_RR", rr)
+    rng = np.random.default_rng(V + rows)
+    x = rng.normal(0, 2, (rows, V)).astype(np.float32)
+    if dtype == "bf16":
+        xb = O.bf16_from_f32(x)
+        x = O.bf16_to_f32(xb)
+        xt = nr.Tensor.from_numpy(xb, "bf16")
+    else:
+        h = x.astype(np.float16)
+        x = h.astype(np.float32)
+        xt = nr.Tensor.from_numpy(h.view(np.uint16), "f16")
+    mrows = 1 if shared else rows
+    add = np.where(rng.random((mrows, V)) < 0.4, -np.inf, rng.normal(0, 0.5, (mrows, V))).astype(np.float32)
+    add[:, ::97] = -1e9
+    add[:, rng.integers(0, V)] = 0.0
+    mt = nr.Tensor.from_numpy(add)
+    u = nr.Rng(V, "streaming f32 masks").uniforms(rows)
+    out = nr.sample_logp(xt, tau, mt, None, entropy=want_ent, uniforms=nr.Tensor.from_numpy(u, "f64"))
+    ids, lp = out[0].to_numpy().ravel(), out[1].to_numpy().ravel()
+    ent = out[2].to_numpy().ravel() if want_ent else None
+    sel = np.arange(rows) if rows <= 96 else np.arange(0, rows, 64)
+    xs = x[sel]
+    am = add if shared else add[sel]
+    z = O.tempered(xs, 1.0 if tau == 0 else tau, addmask=np.broadcast_to(am, xs.shape))
+    if tau == 0.0:
+        assert np.array_equal(ids[sel], O.argmax_first(z)), f"{case}: greedy ids"
+        assert np.all(close_f32(lp[sel], O.token_logp(z, ids[sel]))), f"{case}: greedy logp"
+    else:
+        check_sample(f"{case}", z, u[sel], ids[sel], lp[sel], None if ent is None else ent[sel])
+    again = nr.sample_logp(xt, tau, mt, None, entropy=want_ent, uniforms=nr.Tensor.from_numpy(u, "f64"))
+    for a, b in zip(out, again):
+        assert a.to_numpy().tobytes() == b.to_numpy().tobytes(), f"{case}: rerun bits"
+
 def _peaked_rows(rows, V, seed, bf16):
     """N(0,1) rows with one dominant logit (+20 .. +60) placed late in the row (after every
     early reference has been set), at an index that differs per row; the tokens are the peaks,
