@@ -72,11 +72,13 @@ def test_c4_parity_and_rerun_bits_through_both_paths():
     check_sample("c4 (aot = rtc)", z, u, ids, lp, bf16=False)
 
 
-@pytest.mark.parametrize("case", ["c2_f32_entropy", "seg_bf16_16rows", "stream_unaligned_f32", "queued_shared_mask"])
+@pytest.mark.parametrize("case", ["c2_f32_entropy", "seg_bf16_16rows", "stream_unaligned_f32", "queued_shared_mask",
+                                  "stream_f32_mask_bf16"])
 def test_each_sampler_kernel_is_byte_identical_through_both_paths(case):
     """One call per kernel family: the register-resident sampler with entropy (C2), the segmented
-    sampler (16 rows of V = 128256), the streaming sampler (unaligned rows), and the queued
-    sampler's instance for a mask row shared by every row (C4's shape, 128 rows)."""
+    sampler (16 rows of V = 128256), the streaming sampler (unaligned rows, and aligned bf16 rows
+    under an f32 mask, whose words it stages through LDS), and the queued sampler's instance for a
+    mask row shared by every row (C4's shape, 128 rows)."""
     rng = np.random.default_rng(7)
     if case == "c2_f32_entropy":
         w = W.c2()
@@ -89,6 +91,13 @@ def test_each_sampler_kernel_is_byte_identical_through_both_paths(case):
     elif case == "queued_shared_mask":
         w = W.c4(seed=13, rows=128, shared_mask=True)
         rows, xt, mt, tau = w["rows"], w["logits"], w["mask"], w["temperature"]
+    elif case == "stream_f32_mask_bf16":
+        rows, V = 80, 40000
+        xt = nr.Tensor.from_numpy(O.bf16_from_f32(rng.normal(0, 2, (rows, V)).astype(np.float32)), "bf16")
+        add = np.where(rng.random((rows, V)) < 0.4, -np.inf, rng.normal(0, 0.5, (rows, V))).astype(np.float32)
+        add[:, 3] = 0.0
+        mt = nr.Tensor.from_numpy(add)
+        tau = 0.8
     else:
         rows, V = 33, 1001
         xt = nr.Tensor.from_numpy(rng.normal(0, 3, (rows, V)).astype(np.float32))
