@@ -35,6 +35,7 @@ constexpr int kWave = 64;
 constexpr int kEpl = 8;                  // elements per lane per chunk
 constexpr int kChunk = kWave * kEpl;     // 512 elements per chunk
 constexpr int kBatch = 4;                // chunks per wave with loads in flight together
+constexpr int kMaskStage = 2;            // streaming sampler, f32 mask on 16-bit rows: chunks per wave staged in LDS
 // The most a lane's 8 weights of one chunk may sum to before its exponent reference moves to the
 // chunk's maximum, where a finishing difference of two log-sums must stay small (entropy, KL):
 // the reference then trails the maximum by at most log2 32 = 5 (log2 units).

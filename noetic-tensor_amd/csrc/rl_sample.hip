@@ -409,10 +409,10 @@ int sample_entry(const NtRlSampleArgs *a, WorkspaceFn workspace, bool nofree, co
             return rtc_status() ? rtc_status() : launched(who);
         }
     }
-    // An f32 mask on aligned 16-bit rows is staged through LDS after the per-chunk records: two
-    // chunks of f32 words (4 KiB) per wave, at 16 bytes.
+    // An f32 mask on aligned 16-bit rows is staged through LDS after the per-chunk records:
+    // kMaskStage chunks of f32 words (2 KiB each) per wave, at 16 bytes.
     const size_t shs = al && a->dtype != NT_F32 && a->mask_kind == NT_MASK_F32
-                           ? ((shm + 15) & ~size_t(15)) + size_t(nw) * 2 * kChunk * sizeof(float)
+                           ? ((shm + 15) & ~size_t(15)) + size_t(nw) * kMaskStage * kChunk * sizeof(float)
                            : shm;
     rtc_status() = 0;
     if (a->dtype == NT_F32) pick_mk_sample<NT_F32>(a->mask_kind, ent, al, p, a->rows, nw * kWave, shs, s);

@@ -45,9 +45,8 @@ __global__ __launch_bounds__(1024) void k_sample(SampleP p) {
     // unit one contiguous KiB per instruction (buffer_load ... lds), where two 16-byte loads per
     // lane 32 bytes apart would each touch every 128-byte line half.
     constexpr bool kMl = kBuf && MK == NT_MASK_F32;
-    constexpr int kSB = kMl ? 2 : kBatch;  // chunks per wave with loads in flight together
-    constexpr int kMB = kChunk * 4;        // f32 mask bytes per chunk
-    static_assert(!kMl || kSB == 2, "the waits below count two chunks");
+    constexpr int kSB = kMl ? kMaskStage : kBatch;  // chunks per wave with loads in flight together
+    constexpr int kMB = kChunk * 4;                 // f32 mask bytes per chunk
     uint8_t *const mstage = reinterpret_cast<uint8_t *>(smem) + ((p.nc * (ENT ? 3 : 2) * 4 + 15) & ~15);
     const uint32_t mslot = uint32_t((uintptr_t)(lds_ptr_t)(mstage)) + uint32_t(wave * kSB * kMB) + uint32_t(lane * 32);
     for (int c0 = wave; c0 < p.nc; c0 += nw * kSB) {
@@ -88,9 +87,10 @@ __global__ __launch_bounds__(1024) void k_sample(SampleP p) {
         for (int b = 0; b < kSB; b++) {
             const int c = c0 + b * nw;
             if constexpr (kMl) {
-                // chunk b's three loads are done once at most the later chunk's three are out
-                if (b == 0) wait_vmcnt<3>();
-                else wait_vmcnt<0>();
+                // chunk b's three loads are done once at most the later chunks' three each are out
+                static_for<0, kSB>([&](auto i) {
+                    if (b == decltype(i)::value) wait_vmcnt<3 * (kSB - 1 - decltype(i)::value)>();
+                });
                 lds_mask_words<NT_MASK_F32, kEpl>(mslot + uint32_t(b * kMB), raw[b].m);
             }
             if (c < p.nc) {
