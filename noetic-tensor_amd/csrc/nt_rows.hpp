@@ -199,18 +199,25 @@ __device__ __forceinline__ float logit(const uint32_t *x, int j) {
 // reaching one would take a numerator of more than 24 significant bits). So the product rounded
 // to f32 is the division's result, zeros, infinities and NaN included. Below 2^-126 the midpoints
 // are evenly spaced and a quotient can be one exactly; a wave holding such a nonzero element
-// divides those. (The f32 division is a ten-instruction sequence; this is three.)
+// divides those. (The f32 division is a ten-instruction sequence; this is three, and a lane's
+// test for such elements is one minimum over its N quotients. A NaN can hide a small quotient
+// from that minimum; its row is refused, NaN, whatever the other values.)
 template <int N>
 __device__ __forceinline__ void div_tau(float *z, float tau) {
     const double rt = 1.0 / double(tau);
     float q[N];
-    bool tiny = false;
 #pragma unroll
-    for (int j = 0; j < N; j++) {
-        q[j] = float(double(z[j]) * rt);
-        tiny = tiny || (fabsf(q[j]) < 0x1p-126f && z[j] != 0.0f);
+    for (int j = 0; j < N; j++) q[j] = float(double(z[j]) * rt);
+    // one test per lane: the smallest magnitude of its quotients (v_min3 with |.| modifiers; a
+    // zero quotient, exact, sends the wave down the test per element as well)
+    float m = fabsf(q[0]);
+#pragma unroll
+    for (int j = 1; j < N; j += 2) {
+        float r;
+        asm volatile("v_min3_f32 %0, |%1|, |%2|, |%3|" : "=v"(r) : "v"(m), "v"(q[j]), "v"(q[j + 1 < N ? j + 1 : j]));
+        m = r;
     }
-    if (__builtin_amdgcn_ballot_w64(tiny)) {
+    if (__builtin_amdgcn_ballot_w64(m < 0x1p-126f)) {
 #pragma unroll
         for (int j = 0; j < N; j++)
             if (fabsf(q[j]) < 0x1p-126f && z[j] != 0.0f) q[j] = z[j] / tau;
